@@ -1,0 +1,258 @@
+/*
+ * velox_hip.h -- C ABI of the MI355X (gfx950) decode backend for Velox's generated LLM runners.
+ *
+ * The emitted-runner ABI of the reference is kept: the arena struct, the device-resident decode
+ * state, and the per-model `velox_<Model>_{decode,prefill}{_graph_step,}` entry points, now with a
+ * hipStream_t. Behind it every kernel is hand-written HIP for gfx950. No torch types appear here:
+ * plain pointers, sizes and hipStream_t only.
+ *
+ * Errors: the step entry points return void like the reference's (src/codegen.rs:2803-2808) and
+ * record the first launch error, readable with velox_hip_last_error(); every other entry point
+ * returns an int status (0 = success, >0 = hipError_t, <0 = VELOX_HIP_E* argument errors).
+ */
+#ifndef VELOX_HIP_H
+#define VELOX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes (negative: argument/plan errors; positive: hipError_t) ---- */
+#define VELOX_HIP_OK 0
+#define VELOX_HIP_EINVAL (-1)    /* bad argument / unsupported shape */
+#define VELOX_HIP_ENOMEM (-2)    /* plan exceeds the VRAM budget (reference diagnostic E002) */
+#define VELOX_HIP_ESHAPE (-3)    /* tensor size does not match the plan */
+#define VELOX_HIP_ENOTLOADED (-4)
+
+/* ---- quant_mode values (src/codegen.rs:1024-1028 defines 0 fp32, 1 fp16, 2 group-64 "Q4",
+ *      3/4 fp8). GGML Q4_0 is new to this backend and gets its own value. ---- */
+#define VELOX_QUANT_F32 0u
+#define VELOX_QUANT_F16 1u
+#define VELOX_QUANT_Q4_GROUP64 2u
+#define VELOX_QUANT_GGML_Q4_0 5u
+
+/* Tensor kinds for the loaders (one per HF safetensors name the reference resolves,
+ * src/runtime.rs:1273-1300). */
+enum VeloxHipTensor {
+    VELOX_T_EMBED = 1, VELOX_T_Q = 2, VELOX_T_K = 3, VELOX_T_V = 4, VELOX_T_O = 5,
+    VELOX_T_GATE = 6, VELOX_T_UP = 7, VELOX_T_DOWN = 8, VELOX_T_ATTN_NORM = 9,
+    VELOX_T_MLP_NORM = 10, VELOX_T_FINAL_NORM = 11, VELOX_T_HEAD = 12,
+    VELOX_T_BQ = 13, VELOX_T_BK = 14, VELOX_T_BV = 15
+};
+
+/* Model constants. Replaces the compile-time VELOX_MODEL_* macros of the emitted module
+ * (src/codegen.rs:993-1029) and runtime.rs TransformerConfig (src/runtime.rs:1160-1210); eps,
+ * theta and the QKV bias come from the config instead of the reference's hard-coded values. */
+typedef struct VeloxHipModelConfig {
+    char name[32];
+    uint32_t vocab_size, hidden_dim, intermediate_dim, num_layers;
+    uint32_t num_heads, num_kv_heads, head_dim, max_seq_len;
+    float rms_norm_eps, rope_theta;
+    uint32_t qkv_bias;          /* 1: q/k/v biases (Qwen) */
+    uint32_t tied_lm_head;      /* 1: LM head reads the embedding table */
+    uint32_t quant_mode;        /* VELOX_QUANT_GGML_Q4_0 */
+    uint32_t attn_splits;       /* split-K partitions over the sequence; 0 = automatic */
+    uint64_t vram_budget_bytes; /* 0 = 288 GB of HBM3E */
+} VeloxHipModelConfig;
+
+typedef struct VeloxHipModel VeloxHipModel; /* opaque: the static memory plan */
+
+/* Mirror of VeloxCudaArena (src/codegen.rs:1032-1041) plus the plan pointer. weight_arena holds
+ * the packed Q4_0 nibbles of every linear/embedding matrix, weight_scales their fp16 block scales
+ * (codes and scales are split so that both stream with 128-bit loads), norm_weight_arena the fp32
+ * norm gains, biases and the RoPE cos/sin table. */
+typedef struct VeloxHipArena {
+    const uint8_t* weight_arena;
+    uint8_t* kv_cache_pool;
+    uint8_t* activation_arena;
+    uint32_t* host_pinned_ring;
+    const uint8_t* norm_weight_arena;
+    const uint8_t* weight_scales;
+    uint32_t quant_mode;
+    uint32_t tied_lm_head;
+    const VeloxHipModel* model;
+} VeloxHipArena;
+
+/* Device-resident decode state (src/codegen.rs:1046-1050): one captured graph replays every step. */
+typedef struct VeloxDecodeState {
+    uint64_t step;
+    uint32_t token;
+    uint32_t reserved;
+} VeloxDecodeState;
+
+#define VELOX_HIP_RING_SIZE 1024u
+
+/* Built-in configurations of BASELINE.json (configs 1,2,3,5). which: "smollm_135m", "llama3_8b",
+ * "qwen2_5_7b", "qwen2_72b". max_seq_len 0 keeps the default. */
+int velox_hip_builtin_config(const char* which, uint32_t max_seq_len, VeloxHipModelConfig* out);
+
+/* ---- plan (memory_planner, src/memory_planner.rs:282-488) ---- */
+int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out);
+void velox_hip_model_destroy(VeloxHipModel* m);
+int velox_hip_model_config(const VeloxHipModel* m, VeloxHipModelConfig* out);
+int velox_hip_model_arena_bytes(const VeloxHipModel* m, uint64_t* weight_bytes, uint64_t* scale_bytes,
+                                uint64_t* norm_bytes, uint64_t* kv_bytes, uint64_t* act_bytes);
+/* HBM bytes one decode step must move at position pos (weights once + KV read/write). */
+uint64_t velox_hip_model_step_bytes(const VeloxHipModel* m, uint64_t pos);
+/* Byte offset of the fp32 logits / hidden state inside activation_arena. */
+uint64_t velox_hip_model_logits_offset(const VeloxHipModel* m);
+uint64_t velox_hip_model_hidden_offset(const VeloxHipModel* m);
+
+/* ---- arena (velox_cuda_runner.cu:417-431: cudaMalloc x3 + mapped host ring) ---- */
+int velox_hip_arena_create(const VeloxHipModel* m, VeloxHipArena* out);
+int velox_hip_arena_destroy(VeloxHipArena* a);
+
+/* ---- loaders (velox_cuda_runner.cu:154-199 stream_tensor_converted) ----
+ * q4_0: host GGML Q4_0 blocks, row-major [rows][in/32] x 18 B, for a matrix kind of `layer`.
+ * f32: host fp32 vector (norm gains, biases). Both upload and repack on `stream`. */
+int velox_hip_load_q4_0(VeloxHipArena* a, int kind, uint32_t layer, const void* blocks, uint64_t nbytes,
+                        hipStream_t stream);
+int velox_hip_load_f32(VeloxHipArena* a, int kind, uint32_t layer, const float* data, uint64_t count,
+                       hipStream_t stream);
+/* Synthesizes the whole seeded model on the device (linear weights N(0,sigma) quantized to Q4_0,
+ * norm gains 1 or N(1,norm_sigma), biases N(0,sigma)), bit-identical to the oracle's recipe. */
+int velox_hip_synthesize_model(VeloxHipArena* a, uint64_t seed, float sigma, float norm_sigma,
+                               hipStream_t stream);
+/* Fills layer `layer`'s KV cache positions [0, n_pos) with bf16 values seed-generated N(0, sigma). */
+int velox_hip_fill_kv(VeloxHipArena* a, uint32_t layer, uint32_t n_pos, uint64_t seed, float sigma,
+                      hipStream_t stream);
+
+/* ---- decode state / prompt ---- */
+/* Stages a prompt for teacher-forced prefill through the decode graph: while step+1 < n, the
+ * step's next token is prompt[step+1] instead of the argmax. */
+int velox_hip_set_prompt(VeloxHipArena* a, const uint32_t* tokens, uint32_t n, hipStream_t stream);
+int velox_hip_set_state(VeloxHipArena* a, uint64_t step, uint32_t token, hipStream_t stream);
+int velox_hip_get_state(const VeloxHipArena* a, VeloxDecodeState* out, hipStream_t stream);
+
+/* ---- the decode step (src/codegen.rs:2803-3253) ----
+ * graph_step reads (step, token) from the device state, runs embed -> L x [QKV, attention,
+ * o_proj+res, gate/up+SwiGLU, down+res] -> norm+LM head+argmax, writes ring[step & 1023] and
+ * advances the state. decode/prefill set the state first. active_mask bit 0 predicates every
+ * kernel. Capturable into a hipGraph; no allocation, no host sync. */
+void velox_hip_decode_graph_step(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
+void velox_hip_decode(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t active_mask,
+                      hipStream_t stream);
+void velox_hip_prefill_graph_step(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
+void velox_hip_prefill(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t active_mask,
+                       hipStream_t stream);
+int velox_hip_last_error(void);
+
+/* Per-model entry points with the reference's names (src/runners/tinystories_smollm.cu:1520,
+ * 2383, 2388, 3251); each checks that ctx was planned for that model. */
+void velox_SmolLM_135M_decode_graph_step_hip(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
+void velox_SmolLM_135M_decode_hip(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t active_mask,
+                                  hipStream_t stream);
+void velox_SmolLM_135M_prefill_graph_step_hip(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
+void velox_SmolLM_135M_prefill_hip(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t active_mask,
+                                   hipStream_t stream);
+void velox_Llama3_8B_decode_graph_step_hip(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
+void velox_Llama3_8B_decode_hip(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t active_mask,
+                                hipStream_t stream);
+void velox_Llama3_8B_prefill_graph_step_hip(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
+void velox_Llama3_8B_prefill_hip(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t active_mask,
+                                 hipStream_t stream);
+void velox_Qwen2_5_7B_decode_graph_step_hip(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
+void velox_Qwen2_5_7B_decode_hip(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t active_mask,
+                                 hipStream_t stream);
+void velox_Qwen2_72B_decode_graph_step_hip(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
+void velox_Qwen2_72B_decode_hip(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t active_mask,
+                                hipStream_t stream);
+
+/* ---- per-kernel entry points (device pointers; for parity tests and benchmarks) ---- */
+
+/* Q4_0 matrix in the tiled device layout. Row r, block b of an [n][k] matrix lives in lane
+ * (r % (64/s_lanes)) * s_lanes + b % s_lanes of iteration b / s_lanes of tile r / (64/s_lanes):
+ * codes uint4 [n_tiles][n_iter][64], scales fp16 [n_tiles][n_iter][64]. */
+typedef struct VeloxHipQ4Matrix {
+    void* codes;
+    void* scales;
+    uint32_t n, k;         /* rows, columns (k % 32 == 0) */
+    uint32_t s_lanes;      /* lanes per row: 4, 8, 16, 32 or 64 */
+    uint32_t n_tiles, n_iter;
+    uint32_t paired;       /* 1: tiles interleave gate/up rows for the fused SwiGLU epilogue */
+    uint32_t reserved;
+} VeloxHipQ4Matrix;
+
+/* Descriptor of a weight matrix inside an arena (kind VELOX_T_Q/K/V return the fused QKV matrix
+ * and GATE/UP the paired gate/up matrix; row0 receives the kind's first logical row). */
+int velox_hip_arena_matrix(const VeloxHipArena* a, int kind, uint32_t layer, VeloxHipQ4Matrix* out,
+                           uint32_t* row0);
+/* Device pointer of a norm gain / bias vector inside an arena and its element count. */
+int velox_hip_arena_vector(const VeloxHipArena* a, int kind, uint32_t layer, const float** out, uint64_t* count);
+
+/* Fills n_tiles/n_iter and returns the byte sizes for a matrix (s_lanes 0 = automatic). */
+int velox_hip_q4_layout(uint32_t n, uint32_t k, uint32_t s_lanes, uint32_t paired, VeloxHipQ4Matrix* m,
+                        uint64_t* code_bytes, uint64_t* scale_bytes);
+/* GGML Q4_0 blocks (device) of `rows` rows -> tiled layout rows [row0, row0+rows) (paired: pair_part
+ * 0 = gate rows, 1 = up rows). Zero padding is the caller's (the arena loaders clear it). */
+int velox_hip_q4_0_repack(const void* d_blocks, uint32_t rows, uint32_t row0, uint32_t pair_part,
+                          const VeloxHipQ4Matrix* m, hipStream_t stream);
+/* Tiled layout -> dense fp32 [n][k] (paired: logical rows gate 0..n/2-1 then up). Bit-exact d*(q-8). */
+int velox_hip_q4_0_dequant(const VeloxHipQ4Matrix* m, float* d_out, hipStream_t stream);
+/* fp32 [rows][k] -> GGML Q4_0 blocks, the GGML rounding rule restated (bit-exact with the oracle). */
+int velox_hip_q4_0_quantize(const float* d_x, uint32_t rows, uint32_t k, void* d_blocks, hipStream_t stream);
+/* Seeded N(mean, sigma) fill identical to the oracle's vxo_fill_normal. */
+int velox_hip_fill_normal(float* d_out, uint64_t n, uint64_t seed, uint64_t tag, float sigma, float mean,
+                          hipStream_t stream);
+
+/* Fused GEMV y = W x with epilogues. mode 0: y = Wx (+bias); 1: y = res + Wx; 2: paired SwiGLU
+ * y[j] = silu(g_j) * u_j; gain != NULL applies RMSNorm(x) * gain first (eps). */
+#define VELOX_GEMV_STORE 0
+#define VELOX_GEMV_RESIDUAL 1
+#define VELOX_GEMV_SWIGLU 2
+int velox_hip_gemv_q4_0(const VeloxHipQ4Matrix* m, const float* d_x, const float* d_gain, float eps,
+                        const float* d_bias, const float* d_res, float* d_y, int mode, hipStream_t stream);
+/* Fused RMSNorm + LM head + greedy argmax: logits and the winning index (lowest index on ties). */
+int velox_hip_lm_head_argmax(const VeloxHipQ4Matrix* m, const float* d_x, const float* d_gain, float eps,
+                             float* d_logits, uint32_t* d_token, hipStream_t stream);
+/* Standalone two-stage argmax over n fp32 values (strict '>' lowest-index rule). */
+int velox_hip_argmax_f32(const float* d_x, uint32_t n, uint32_t* d_out, hipStream_t stream);
+/* y = rmsnorm(x) * w (src/runtime.rs:588-601). */
+int velox_hip_rmsnorm(const float* d_x, const float* d_w, uint32_t n, float eps, float* d_y, hipStream_t stream);
+/* Decode attention for one layer at position pos: RoPE on q and the new k (table cos/sin of
+ * pos*theta^(-2j/D)), bf16 K/V append at pos, split-K online softmax with an LSE merge.
+ * qkv: fp32 [hq*d | hkv*d | hkv*d]; kv_layer: bf16 [2][hkv][s_max][d]; out: fp32 [hq*d]. */
+int velox_hip_attention_decode(const float* d_qkv, uint16_t* d_kv_layer, uint32_t hq, uint32_t hkv,
+                               uint32_t d, uint32_t s_max, uint32_t pos, float theta, uint32_t splits,
+                               float* d_out, hipStream_t stream);
+
+/* ---- runner (velox_cuda_runner.cu:327-726 flow: plan, alloc, load, capture, prefill, decode) ---- */
+typedef struct VeloxHipRunOptions {
+    const char* model;       /* builtin config name */
+    uint32_t max_seq_len;    /* 0 = prompt_len + warmup + steps + 1 */
+    uint32_t prompt_len;     /* random prompt tokens (seeded) */
+    uint32_t warmup;         /* untimed decode steps */
+    uint32_t steps;          /* timed decode steps */
+    uint64_t seed;
+    float sigma, norm_sigma;
+    uint32_t use_graph;      /* 1: hipGraph capture + replay (reference default) */
+    uint32_t num_layers;     /* 0 = config value (fewer layers for parity runs) */
+    uint32_t kernel_passes;  /* >0: afterwards time the gate/up GEMV alone over all layers this often */
+    uint32_t verbose;
+} VeloxHipRunOptions;
+
+typedef struct VeloxHipRunReport {
+    double load_ms, prefill_ms, decode_ms;  /* decode_ms over `steps` timed steps */
+    double tok_per_s;                       /* steps / decode seconds */
+    double bytes_per_step;                  /* mean algorithmic HBM bytes per timed step */
+    double hbm_gbps;
+    double wall_ms;                         /* host clock around the timed steps (synced both sides) */
+    double kernel_us;                       /* mean duration of one fused gate/up GEMV launch */
+    double kernel_bytes;                    /* algorithmic bytes of that launch */
+    uint32_t kernel_launches;               /* launches averaged over (all layers, several passes) */
+    uint32_t n_tokens;                      /* tokens written to `tokens` */
+    uint32_t first_token;
+    int status;
+} VeloxHipRunReport;
+
+/* Runs the whole flow; tokens (capacity max_tokens) receives prompt-forced and generated ids. */
+int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_tokens, VeloxHipRunReport* rep);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

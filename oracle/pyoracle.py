@@ -1,0 +1,284 @@
+"""ctypes bindings for the CPU oracle (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg import this module:
+the oracle is the checker and the timed CPU baseline, never part of the product path.
+The C sources (velox_oracle.c) cite the reference functions they restate.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "build", "libvelox_oracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libvelox_ref_smollm.so")
+
+# tensor kinds (velox_oracle.h)
+T_EMBED, T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN = 1, 2, 3, 4, 5, 6, 7, 8
+T_ATTN_NORM, T_MLP_NORM, T_FINAL_NORM, T_HEAD, T_BQ, T_BK, T_BV, T_PROMPT = 9, 10, 11, 12, 13, 14, 15, 16
+
+
+class VxoConfig(C.Structure):
+    _fields_ = [
+        ("vocab_size", C.c_uint32), ("hidden_dim", C.c_uint32), ("intermediate_dim", C.c_uint32),
+        ("num_layers", C.c_uint32), ("num_heads", C.c_uint32), ("num_kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32), ("max_seq_len", C.c_uint32), ("rms_norm_eps", C.c_float),
+        ("rope_theta", C.c_float), ("qkv_bias", C.c_uint32), ("tied_lm_head", C.c_uint32),
+        ("q4_0", C.c_uint32), ("kv_bf16", C.c_uint32),
+    ]
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        fp = C.POINTER(C.c_float)
+        u8p = C.POINTER(C.c_uint8)
+        L.vxo_mix64.restype = C.c_uint64
+        L.vxo_mix64.argtypes = [C.c_uint64]
+        L.vxo_stream.restype = C.c_uint64
+        L.vxo_stream.argtypes = [C.c_uint64, C.c_uint64]
+        L.vxo_normal.restype = C.c_float
+        L.vxo_normal.argtypes = [C.c_uint64, C.c_uint64, C.c_float]
+        L.vxo_normal_coef.restype = C.c_float
+        L.vxo_normal_coef.argtypes = [C.c_float]
+        L.vxo_uniform_u32.restype = C.c_uint32
+        L.vxo_uniform_u32.argtypes = [C.c_uint64, C.c_uint64, C.c_uint32]
+        L.vxo_fill_normal.argtypes = [fp, C.c_uint64, C.c_uint64, C.c_uint64, C.c_float, C.c_float]
+        L.vxo_tag.restype = C.c_uint64
+        L.vxo_tag.argtypes = [C.c_uint32, C.c_uint32]
+        L.vxo_f32_to_f16.restype = C.c_uint16
+        L.vxo_f32_to_f16.argtypes = [C.c_float]
+        L.vxo_f16_to_f32.restype = C.c_float
+        L.vxo_f16_to_f32.argtypes = [C.c_uint16]
+        L.vxo_f32_to_bf16.restype = C.c_uint16
+        L.vxo_f32_to_bf16.argtypes = [C.c_float]
+        L.vxo_bf16_to_f32.restype = C.c_float
+        L.vxo_bf16_to_f32.argtypes = [C.c_uint16]
+        L.vxo_q4_0_quantize_row.argtypes = [fp, C.c_uint64, u8p]
+        L.vxo_q4_0_dequant_row.argtypes = [u8p, C.c_uint64, fp]
+        L.vxo_g64_quantize.argtypes = [fp, C.c_uint64, C.POINTER(C.c_uint32), C.POINTER(C.c_uint16)]
+        L.vxo_g64_dequant.argtypes = [C.POINTER(C.c_uint32), C.POINTER(C.c_uint16), C.c_uint64, fp]
+        L.vxo_rmsnorm.argtypes = [fp, fp, fp, C.c_uint64, C.c_float]
+        L.vxo_matmul_transposed.argtypes = [fp, fp, fp, C.c_uint64, C.c_uint64]
+        L.vxo_matmul_q4_0.argtypes = [fp, fp, u8p, C.c_uint64, C.c_uint64, C.c_int]
+        L.vxo_rope_rotate_half.argtypes = [fp, C.c_uint64, C.c_uint64, C.c_uint64, C.c_float]
+        L.vxo_gqa_attention_step.argtypes = [fp, fp, fp, fp, fp, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64]
+        L.vxo_swiglu_act.argtypes = [fp, fp, C.c_uint64]
+        L.vxo_argmax.restype = C.c_uint32
+        L.vxo_argmax.argtypes = [fp, C.c_uint64]
+        L.vxo_mla_absorbed_step.argtypes = [fp, fp, fp, fp, fp, fp, fp, C.c_uint64, C.c_uint64,
+                                            C.c_uint64, C.c_uint64, C.c_float]
+        L.vxo_engine_create.restype = C.c_void_p
+        L.vxo_engine_create.argtypes = [C.POINTER(VxoConfig), C.c_uint64, C.c_float, C.c_float, C.c_uint32, C.c_int]
+        L.vxo_engine_destroy.argtypes = [C.c_void_p]
+        L.vxo_engine_forward.restype = C.c_uint32
+        L.vxo_engine_forward.argtypes = [C.c_void_p, C.c_uint32, C.c_uint64, fp]
+        L.vxo_engine_forward_layers.restype = C.c_uint32
+        L.vxo_engine_forward_layers.argtypes = [C.c_void_p, C.c_uint32, C.c_uint64, C.c_uint32, fp]
+        L.vxo_engine_reset.argtypes = [C.c_void_p]
+        L.vxo_engine_set_threads.argtypes = [C.c_void_p, C.c_int]
+        L.vxo_engine_tensor.restype = C.c_void_p
+        L.vxo_engine_tensor.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint64)]
+        L.vxo_engine_hidden.restype = fp
+        L.vxo_engine_hidden.argtypes = [C.c_void_p]
+        _lib = L
+    return _lib
+
+
+def fptr(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def u8ptr(a: np.ndarray):
+    assert a.dtype == np.uint8 and a.flags.c_contiguous
+    return a.ctypes.data_as(C.POINTER(C.c_uint8))
+
+
+# ---------------------------------------------------------------------------------------------
+# thin numpy wrappers
+# ---------------------------------------------------------------------------------------------
+def tag(layer: int, kind: int) -> int:
+    return layer * 256 + kind
+
+
+def fill_normal(n: int, seed: int, tg: int, sigma: float = 0.02, mean: float = 0.0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().vxo_fill_normal(fptr(out), n, seed, tg, sigma, mean)
+    return out
+
+
+def prompt_tokens(seed: int, n: int, vocab: int) -> np.ndarray:
+    L = lib()
+    st = L.vxo_stream(seed, tag(0, T_PROMPT))
+    return np.array([L.vxo_uniform_u32(st, i, vocab) for i in range(n)], np.uint32)
+
+
+def q4_0_quantize(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    rows, k = x.shape
+    out = np.empty((rows, (k // 32) * 18), np.uint8)
+    for r in range(rows):
+        lib().vxo_q4_0_quantize_row(fptr(x[r]), k, u8ptr(out[r]))
+    return out
+
+
+def q4_0_dequant(blocks: np.ndarray, k: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    rows = blocks.shape[0]
+    out = np.empty((rows, k), np.float32)
+    for r in range(rows):
+        lib().vxo_q4_0_dequant_row(u8ptr(blocks[r]), k, fptr(out[r]))
+    return out
+
+
+def rmsnorm(x, w, eps):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    lib().vxo_rmsnorm(fptr(out), fptr(x), fptr(w), x.size, eps)
+    return out
+
+
+def matmul_transposed(x, w):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty(w.shape[0], np.float32)
+    lib().vxo_matmul_transposed(fptr(out), fptr(x), fptr(w), w.shape[1], w.shape[0])
+    return out
+
+
+def matmul_q4_0(x, blocks, k, threads=1):
+    x = np.ascontiguousarray(x, np.float32)
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    out = np.empty(blocks.shape[0], np.float32)
+    lib().vxo_matmul_q4_0(fptr(out), fptr(x), u8ptr(blocks), k, blocks.shape[0], threads)
+    return out
+
+
+def rope(t, num_heads, head_dim, pos, theta):
+    t = np.array(t, np.float32, copy=True)
+    lib().vxo_rope_rotate_half(fptr(t), num_heads, head_dim, pos, theta)
+    return t
+
+
+def attention(q, k_layer, v_layer, n_q, n_kv, head_dim, pos):
+    q = np.ascontiguousarray(q, np.float32)
+    k_layer = np.ascontiguousarray(k_layer, np.float32)
+    v_layer = np.ascontiguousarray(v_layer, np.float32)
+    out = np.empty(n_q * head_dim, np.float32)
+    scores = np.empty(pos + 1, np.float32)
+    lib().vxo_gqa_attention_step(fptr(out), fptr(scores), fptr(q), fptr(k_layer), fptr(v_layer),
+                                 n_q, n_kv, head_dim, pos)
+    return out
+
+
+def swiglu(gate, up):
+    g = np.array(gate, np.float32, copy=True)
+    up = np.ascontiguousarray(up, np.float32)
+    lib().vxo_swiglu_act(fptr(g), fptr(up), g.size)
+    return g
+
+
+def argmax(logits):
+    logits = np.ascontiguousarray(logits, np.float32)
+    return int(lib().vxo_argmax(fptr(logits), logits.size))
+
+
+class Engine:
+    """Whole-model oracle (src/runtime.rs VeloxStaticExecutionEngine restated)."""
+
+    def __init__(self, cfg: dict, seed: int, sigma: float = 0.02, norm_sigma: float = 0.0,
+                 q4_0: bool = True, kv_bf16: bool = True, layers_to_build: int | None = None,
+                 threads: int = 1):
+        self.cfg = dict(cfg)
+        c = VxoConfig()
+        c.vocab_size = cfg["vocab_size"]
+        c.hidden_dim = cfg["hidden_dim"]
+        c.intermediate_dim = cfg["intermediate_dim"]
+        c.num_layers = cfg["num_layers"]
+        c.num_heads = cfg["num_heads"]
+        c.num_kv_heads = cfg["num_kv_heads"]
+        c.head_dim = cfg["head_dim"]
+        c.max_seq_len = cfg["max_seq_len"]
+        c.rms_norm_eps = cfg["rms_norm_eps"]
+        c.rope_theta = cfg["rope_theta"]
+        c.qkv_bias = int(cfg.get("qkv_bias", 0))
+        c.tied_lm_head = int(cfg.get("tied_lm_head", 0))
+        c.q4_0 = int(q4_0)
+        c.kv_bf16 = int(kv_bf16)
+        self._c = c
+        nl = cfg["num_layers"] if layers_to_build is None else layers_to_build
+        self.layers = min(nl, cfg["num_layers"])
+        self.h = lib().vxo_engine_create(C.byref(c), seed, sigma, norm_sigma, self.layers, threads)
+        self.logits = np.zeros(cfg["vocab_size"], np.float32)
+
+    def forward(self, token: int, pos: int, layers: int | None = None) -> int:
+        if layers is None:
+            return int(lib().vxo_engine_forward(self.h, token, pos, fptr(self.logits)))
+        return int(lib().vxo_engine_forward_layers(self.h, token, pos, layers, fptr(self.logits)))
+
+    def reset(self):
+        lib().vxo_engine_reset(self.h)
+
+    def set_threads(self, n: int):
+        lib().vxo_engine_set_threads(self.h, n)
+
+    def tensor(self, kind: int, layer: int = 0) -> np.ndarray:
+        n = C.c_uint64(0)
+        p = lib().vxo_engine_tensor(self.h, kind, layer, C.byref(n))
+        if not p:
+            raise KeyError((kind, layer))
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint8)), shape=(n.value,)).copy()
+
+    def hidden(self) -> np.ndarray:
+        p = lib().vxo_engine_hidden(self.h)
+        return np.ctypeslib.as_array(p, shape=(self.cfg["hidden_dim"],)).copy()
+
+    def close(self):
+        if self.h:
+            lib().vxo_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class RefSmolLM:
+    """The reference's emitted C99 SmolLM module compiled in place (oracle/_ref)."""
+
+    def __init__(self, seed: int, sigma: float = 0.02, norm_sigma: float = 0.0):
+        if not os.path.exists(REF_PATH):
+            raise FileNotFoundError(REF_PATH)
+        L = C.CDLL(REF_PATH)
+        L.vxr_smollm_init.restype = C.c_int
+        L.vxr_smollm_init.argtypes = [C.c_uint64, C.c_float, C.c_float]
+        L.vxr_smollm_step.restype = C.c_uint32
+        L.vxr_smollm_step.argtypes = [C.c_uint32, C.c_uint64, C.POINTER(C.c_float)]
+        L.vxr_smollm_free.argtypes = []
+        self.L = L
+        if L.vxr_smollm_init(seed, sigma, norm_sigma) != 0:
+            raise MemoryError("reference arena allocation failed")
+        self.logits = np.zeros(49152, np.float32)
+
+    def step(self, token: int, pos: int) -> int:
+        return int(self.L.vxr_smollm_step(token, pos, fptr(self.logits)))
+
+    def close(self):
+        self.L.vxr_smollm_free()

@@ -1,0 +1,121 @@
+"""CPU tests of the C ABI library: it loads, exports every declared symbol, and its planner (pure
+host code, no GPU needed) sizes the BASELINE configurations as BASELINE.md derives them."""
+import ctypes as C
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+from velox_amd import _lib as L
+from velox_amd.engine import make_config
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_library_exports_every_header_symbol(hiplib):
+    names = L.header_exports()
+    assert len(names) >= 40
+    missing = [n for n in names if not hasattr(hiplib, n)]
+    assert not missing, missing
+
+
+def _plan(cfg):
+    m = C.c_void_p()
+    rc = L.load().velox_hip_model_create(C.byref(cfg), C.byref(m))
+    return rc, m
+
+
+def test_builtin_configs_match_baseline():
+    c = L.builtin_config("llama3_8b")
+    assert (c.vocab_size, c.hidden_dim, c.intermediate_dim, c.num_layers, c.num_heads, c.num_kv_heads,
+            c.head_dim) == (128256, 4096, 14336, 32, 32, 8, 128)
+    assert c.rope_theta == 500000.0 and abs(c.rms_norm_eps - 1e-5) < 1e-12 and c.tied_lm_head == 0
+    q = L.builtin_config("qwen2_5_7b")
+    assert (q.hidden_dim, q.intermediate_dim, q.num_layers, q.num_heads, q.num_kv_heads, q.vocab_size,
+            q.qkv_bias, q.tied_lm_head) == (3584, 18944, 28, 28, 4, 152064, 1, 1)
+    s = L.builtin_config("smollm_135m")
+    assert (s.hidden_dim, s.num_layers, s.num_heads, s.num_kv_heads, s.head_dim, s.tied_lm_head) == (576, 30, 9, 3,
+                                                                                                     64, 1)
+    b = L.builtin_config("qwen2_72b")
+    assert (b.hidden_dim, b.intermediate_dim, b.num_layers, b.num_heads, b.num_kv_heads) == (8192, 29568, 80, 64, 8)
+    with pytest.raises(RuntimeError):
+        L.builtin_config("no_such_model")
+
+
+def test_step_bytes_match_baseline_llama():
+    """4,221,370,368 weight bytes + 2,304 embedding row + 1,064,960 norm bytes
+    + 131,072*(pos+1) KV read + 131,072 KV write per step."""
+    rc, m = _plan(make_config("llama3_8b", max_seq_len=385))
+    assert rc == 0
+    lib = L.load()
+    for pos in (0, 128, 383):
+        want = 4_221_370_368 + 2_304 + 1_064_960 + 131_072 * (pos + 1) + 131_072
+        assert lib.velox_hip_model_step_bytes(m, pos) == want
+    mean = np.mean([lib.velox_hip_model_step_bytes(m, p) for p in range(128, 384)])
+    assert mean == 4_222_437_632 + 131_072 * 257.5  # = 4.256 GB (BASELINE.md quotes it as "mean 4.255 GB")
+    lib.velox_hip_model_destroy(m)
+
+
+def test_arena_plan_sizes_and_budget():
+    lib = L.load()
+    rc, m = _plan(make_config("llama3_8b", max_seq_len=385))
+    assert rc == 0
+    v = [C.c_uint64() for _ in range(5)]
+    lib.velox_hip_model_arena_bytes(m, *[C.byref(x) for x in v])
+    codes, scales, norms, kv, act = [x.value for x in v]
+    # codes + scales hold exactly 18 B per 32 weights of every matrix (embedding and head included)
+    weights = (32 * (6144 * 4096 + 4096 * 4096 + 2 * 14336 * 4096 + 4096 * 14336) + 2 * 128256 * 4096)
+    assert codes == weights // 2 and scales == weights // 32 * 2
+    assert kv == 32 * 2 * 8 * 385 * 128 * 2
+    lib.velox_hip_model_destroy(m)
+    # Qwen2-72B Q4_0 with an 8448-token context fits the 288 GB budget of one MI355X
+    rc, m = _plan(make_config("qwen2_72b"))
+    assert rc == 0
+    lib.velox_hip_model_destroy(m)
+    # ... and not a 40 GB budget: reference diagnostic E002 (src/memory_planner.rs:398-420)
+    cfg = make_config("qwen2_72b")
+    cfg.vram_budget_bytes = 40 * 10 ** 9
+    rc, _ = _plan(cfg)
+    assert rc == -2
+
+
+@pytest.mark.parametrize("field,value", [("head_dim", 96), ("num_kv_heads", 5), ("hidden_dim", 4100),
+                                         ("quant_mode", 0), ("num_layers", 0)])
+def test_plan_rejects_unsupported_shapes(field, value):
+    cfg = make_config("llama3_8b", max_seq_len=64)
+    setattr(cfg, field, value)
+    rc, _ = _plan(cfg)
+    assert rc == -1
+
+
+def test_tiled_layout_choices():
+    """Lanes per row for the BASELINE shapes; padding never costs HBM bytes, only memory."""
+    lib = L.load()
+    expect = {(6144, 4096): 32, (4096, 14336): 32, (960, 576): 4, (576, 1536): 16, (4096, 3584): 32,
+              (3584, 18944): 32, (8192, 29568): 32, (1000, 64): 4}
+    for (n, k), s in expect.items():
+        m = L.Q4Matrix()
+        cb, sb = C.c_uint64(), C.c_uint64()
+        assert lib.velox_hip_q4_layout(n, k, 0, 0, C.byref(m), C.byref(cb), C.byref(sb)) == 0
+        assert m.s_lanes == s, (n, k, m.s_lanes)
+        assert m.n_iter * m.s_lanes >= k // 32 and (m.n_iter - 1) * m.s_lanes < k // 32
+        assert cb.value == m.n_tiles * m.n_iter * 64 * 16 and sb.value == m.n_tiles * m.n_iter * 64 * 2
+    m = L.Q4Matrix()
+    assert lib.velox_hip_q4_layout(10, 33, 0, 0, C.byref(m), None, None) == -1
+    assert lib.velox_hip_q4_layout(10, 64, 64, 1, C.byref(m), None, None) == -1
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=60)
+    assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_runner_rejects_unsupported_arguments():
+    runner = os.path.join(ROOT, "velox_amd", "lib", "velox_hip_runner")
+    r = subprocess.run([runner, "--weights", "x.safetensors"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 1 and "not supported" in r.stderr
+    r = subprocess.run([runner, "--bogus"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 1

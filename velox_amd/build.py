@@ -1,0 +1,66 @@
+"""Builds the gfx950 HIP library and the runner in-tree (velox_amd/lib/).
+
+    python -m velox_amd.build        # or: from velox_amd.build import build; build()
+
+hipcc cross-compiles for gfx950 without a GPU. Every HIP translation unit is built with
+packed-FP32 instruction selection disabled (-packed-fp32-ops): the hardware's v_pk_*_f32 forms
+are avoided on purpose.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+LIBDIR = os.path.join(PKG, "lib")
+LIB = os.path.join(LIBDIR, "libvelox_hip.so")
+RUNNER = os.path.join(LIBDIR, "velox_hip_runner")
+ARCH = "gfx950"
+
+HIP_SOURCES = ["vx_kernels.hip", "vx_host.cpp"]
+
+
+def _hipcc() -> str:
+    for cand in ("/opt/rocm/bin/hipcc", shutil.which("hipcc") or ""):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found: the HIP backend cannot be built")
+
+
+def common_flags() -> list[str]:
+    return [
+        f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-Wall", "-Wno-unused-function", "-Wno-unused-value",
+        f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}",
+    ]
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(LIBDIR, exist_ok=True)
+    hipcc = _hipcc()
+    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
+    tmp = LIB + ".tmp"
+    cmd = [hipcc, *common_flags(), "-shared", "-o", tmp, *srcs]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, LIB)
+    runner_src = os.path.join(CSRC, "vx_runner_main.cpp")
+    if os.path.exists(runner_src):
+        cmd = [hipcc, *common_flags(), "-o", RUNNER + ".tmp", runner_src, f"-L{LIBDIR}", "-lvelox_hip",
+               f"-Wl,-rpath,$ORIGIN"]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True)
+        os.replace(RUNNER + ".tmp", RUNNER)
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose="-v" in sys.argv)
+    print(LIB)

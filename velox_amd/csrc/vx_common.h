@@ -1,0 +1,152 @@
+// vx_common.h -- types and helpers shared by the HIP kernels (device) and the planner/runner (host).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "velox_hip.h"
+
+#define VX_HD __host__ __device__ __forceinline__
+
+// ---------------------------------------------------------------------------------------------
+// Seeded synthetic-model recipe (counter-based, identical on host and device):
+//   stream = mix64(seed ^ mix64(tag + C0)); h(i) = mix64(stream + (i+1) * golden)
+//   normal(i) = (float)(2 * sum of the eight 16-bit words of h(2i), h(2i+1) - 524280) * coef
+// An Irwin-Hall(8) approximation of N(0, sigma) computed with one exact int->float conversion and
+// one IEEE multiply, so host and device produce the same bits.
+// ---------------------------------------------------------------------------------------------
+VX_HD uint64_t vx_mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+VX_HD uint64_t vx_stream(uint64_t seed, uint64_t tag) { return vx_mix64(seed ^ vx_mix64(tag + 0x632BE59BD9B4E019ULL)); }
+VX_HD uint64_t vx_hash(uint64_t stream, uint64_t idx) { return vx_mix64(stream + (idx + 1ULL) * 0x9E3779B97F4A7C15ULL); }
+VX_HD int32_t vx_normal_int(uint64_t stream, uint64_t idx) {
+    const uint64_t a = vx_hash(stream, 2ULL * idx), b = vx_hash(stream, 2ULL * idx + 1ULL);
+    const int64_t s = (int64_t)(a & 0xFFFF) + (int64_t)((a >> 16) & 0xFFFF) + (int64_t)((a >> 32) & 0xFFFF) +
+                      (int64_t)(a >> 48) + (int64_t)(b & 0xFFFF) + (int64_t)((b >> 16) & 0xFFFF) +
+                      (int64_t)((b >> 32) & 0xFFFF) + (int64_t)(b >> 48);
+    return (int32_t)(2 * s - 524280);
+}
+VX_HD uint32_t vx_uniform_u32(uint64_t stream, uint64_t idx, uint32_t n) {
+    return (uint32_t)(((vx_hash(stream, idx) >> 32) * (uint64_t)n) >> 32);
+}
+inline float vx_normal_coef(float sigma) { return (float)((double)sigma / (131072.0 * 0.81649658092772603)); }
+VX_HD uint64_t vx_tag(uint32_t layer, uint32_t kind) { return (uint64_t)layer * 256ULL + kind; }
+#define VX_TAG_PROMPT 16u
+#define VX_TAG_KV_K 17u
+#define VX_TAG_KV_V 18u
+
+// IEEE fp32 -> fp16 bits, round to nearest even (integer form, host == device).
+VX_HD uint16_t vx_f32_to_f16_bits(float f) {
+    const uint32_t x = __builtin_bit_cast(uint32_t, f);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return (uint16_t)(sign | (ax == 0x7F800000u ? 0x7C00u : (0x7E00u | ((ax >> 13) & 0x3FFu))));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);
+    if (ax < 0x38800000u) {
+        if (ax < 0x33000000u) return (uint16_t)sign;
+        const uint32_t e = ax >> 23, mant = (ax & 0x7FFFFFu) | 0x800000u, sh = 126u - e;
+        uint32_t q = mant >> sh;
+        const uint32_t rem = mant & ((1u << sh) - 1u), half = 1u << (sh - 1u);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t h = (((ax >> 23) - 112u) << 10) | ((ax & 0x7FFFFFu) >> 13);
+    const uint32_t rem = ax & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+VX_HD float vx_f16_bits_to_f32(uint16_t h) {
+    const uint32_t sign = ((uint32_t)h & 0x8000u) << 16, e = ((uint32_t)h >> 10) & 0x1Fu;
+    uint32_t m = (uint32_t)h & 0x3FFu, x;
+    if (e == 0) {
+        if (m == 0) {
+            x = sign;
+        } else {
+            uint32_t sh = 0;
+            while (!(m & 0x400u)) { m <<= 1; sh++; }
+            x = sign | ((113u - sh) << 23) | ((m & 0x3FFu) << 13);
+        }
+    } else if (e == 31) {
+        x = sign | 0x7F800000u | (m << 13);
+    } else {
+        x = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    return __builtin_bit_cast(float, x);
+}
+VX_HD uint16_t vx_f32_to_bf16_bits(float f) {
+    uint32_t x = __builtin_bit_cast(uint32_t, f);
+    if ((x & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((x >> 16) | 0x40u);
+    x += 0x7FFFu + ((x >> 16) & 1u);
+    return (uint16_t)(x >> 16);
+}
+VX_HD float vx_bf16_bits_to_f32(uint16_t h) { return __builtin_bit_cast(float, (uint32_t)h << 16); }
+
+// ---------------------------------------------------------------------------------------------
+// Device-side views
+// ---------------------------------------------------------------------------------------------
+struct VxMat {
+    const uint4* codes;
+    const uint16_t* scales;
+    uint32_t n, k, s, n_tiles, n_iter, paired;
+};
+
+struct VxGemvArgs {
+    const uint4* codes;
+    const uint16_t* scales;
+    uint32_t n, k, n_tiles, n_iter;
+    const float* x;
+    const float* gain;
+    float eps;
+    const float* bias;
+    const float* res;
+    float* y;
+    // fused argmax (LM head)
+    float* cand_v;
+    uint32_t* cand_i;
+    uint32_t* counter;
+    VeloxDecodeState* state;
+    uint32_t* ring;
+    const uint32_t* prompt;
+    const uint32_t* prompt_len;
+    uint32_t* token_out;
+    uint64_t active_mask;
+};
+
+struct VxAttnArgs {
+    const float* qkv;
+    uint16_t* kv;            // layer base: [2][hkv][s_max][d] bf16
+    const float2* rope;      // [s_max][d/2] (cos, sin)
+    const VeloxDecodeState* state;
+    uint32_t fixed_pos;      // used when state == nullptr
+    float* part_o;           // [hq][splits][d]
+    float* part_ml;          // [hq][splits][2]
+    uint32_t* counters;      // [hkv]
+    float* out;              // [hq*d]
+    uint32_t hq, hkv, s_max, splits;
+    float scale;
+    uint64_t active_mask;
+};
+
+// Launch helpers implemented in vx_kernels.hip, used by vx_host.cpp.
+enum { VX_EPI_STORE = 0, VX_EPI_RESID = 1, VX_EPI_SWIGLU = 2, VX_EPI_ARGMAX = 3 };
+hipError_t vx_launch_gemv(const VxMat& m, const VxGemvArgs& a, int epi, uint32_t max_wgs, hipStream_t st);
+hipError_t vx_launch_attention(const VxAttnArgs& a, uint32_t d, hipStream_t st);
+hipError_t vx_launch_embed(const VxMat& m, const VeloxDecodeState* state, uint32_t fixed_token, float* h,
+                           uint64_t mask, hipStream_t st);
+hipError_t vx_launch_set_state(VeloxDecodeState* state, uint64_t step, uint32_t token, hipStream_t st);
+hipError_t vx_launch_repack(const void* blocks, uint32_t rows, uint32_t row0, uint32_t pair_part, const VxMat& m,
+                            hipStream_t st);
+hipError_t vx_launch_synth_q4(const VxMat& m, uint32_t rows, uint32_t row0, uint32_t pair_part, uint64_t stream,
+                              float coef, hipStream_t st);
+hipError_t vx_launch_fill_normal(float* out, uint64_t n, uint64_t stream, float coef, float mean, hipStream_t st);
+// Fills K/V of one layer, positions [0, n_pos): element (t, g, d) draws index (t*hkv + g)*D + d,
+// the [S][hkv*D] order of the reference's cache (src/runtime.rs:1358-1361).
+hipError_t vx_launch_fill_kv(uint16_t* layer_base, uint32_t hkv, uint32_t s_max, uint32_t d, uint32_t n_pos,
+                             uint64_t stream_k, uint64_t stream_v, float coef, hipStream_t st);
+hipError_t vx_launch_dequant(const VxMat& m, float* out, hipStream_t st);
+hipError_t vx_launch_quantize(const float* x, uint32_t rows, uint32_t k, void* blocks, hipStream_t st);
+hipError_t vx_launch_rmsnorm(const float* x, const float* w, uint32_t n, float eps, float* y, hipStream_t st);
+hipError_t vx_launch_argmax(const float* x, uint32_t n, uint32_t* out, hipStream_t st);
+uint32_t vx_gemv_max_wgs_default();

@@ -1,0 +1,949 @@
+// vx_host.cpp -- static memory plan, arena, loaders, the decode-step launcher and the runner.
+//
+// Host half of the backend. The reference splits this between the Rust planner
+// (src/memory_planner.rs:282-488), the emitted host wrapper (src/codegen.rs:2803-3253) and the
+// Windows runner (src/runners/velox_cuda_runner.cu:327-726); here it is one C++ library behind
+// the C ABI of include/velox_hip.h.
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "vx_common.h"
+
+namespace {
+
+int g_last_error = 0;
+
+inline int vx_record(hipError_t e) {
+    if (e != hipSuccess && g_last_error == 0) g_last_error = (int)e;
+    return (int)e;
+}
+
+inline uint64_t vx_align(uint64_t x, uint64_t a = 256) { return (x + a - 1) / a * a; }
+
+struct VxMatPlan {
+    uint64_t code_off = 0, scale_off = 0, code_bytes = 0, scale_bytes = 0;
+    uint32_t n = 0, k = 0, s = 0, n_tiles = 0, n_iter = 0, paired = 0;
+};
+
+struct VxLayerPlan {
+    VxMatPlan qkv, o, gate_up, down;
+    uint64_t attn_norm = 0, mlp_norm = 0, bias = 0;
+};
+
+}  // namespace
+
+struct VeloxHipModel {
+    VeloxHipModelConfig cfg;
+    std::vector<VxLayerPlan> layers;
+    VxMatPlan embed, head;
+    uint64_t final_norm = 0, rope = 0;
+    uint64_t code_bytes = 0, scale_bytes = 0, norm_bytes = 0, kv_bytes = 0, act_bytes = 0, kv_layer_bytes = 0;
+    // activation arena offsets (bytes)
+    uint64_t a_state = 0, a_plen = 0, a_argmax_counter = 0, a_counters = 0, a_token = 0, a_prompt = 0;
+    uint64_t a_h = 0, a_qkv = 0, a_attn = 0, a_act = 0, a_logits = 0, a_part_o = 0, a_part_ml = 0;
+    uint64_t a_cand_v = 0, a_cand_i = 0;
+    uint32_t splits = 1, max_wgs = 2048;
+};
+
+namespace {
+
+// Lanes per row S: the largest of {32, 16, 8, 4} whose padding of the last iteration wastes at
+// most 1/8 of the lanes, else the one wasting least. Padding costs memory, never HBM bandwidth:
+// padded blocks are not loaded.
+uint32_t vx_choose_s(uint32_t nb) {
+    const uint32_t cand[4] = {32, 16, 8, 4};
+    uint32_t best = 4;
+    double best_w = 2.0;
+    for (uint32_t s : cand) {
+        const uint32_t it = (nb + s - 1) / s;
+        const double waste = (double)(it * s - nb) / (double)(it * s);
+        if (waste <= 0.125) return s;
+        if (waste < best_w) { best_w = waste; best = s; }
+    }
+    return best;
+}
+
+void vx_mat_layout(uint32_t n, uint32_t k, uint32_t s, uint32_t paired, VxMatPlan& p) {
+    const uint32_t nb = k / 32;
+    p.n = n;
+    p.k = k;
+    p.s = s ? s : vx_choose_s(nb);
+    p.paired = paired;
+    const uint32_t R = 64 / p.s;
+    p.n_tiles = paired ? (n + R / 2 - 1) / (R / 2) : (n + R - 1) / R;
+    p.n_iter = (nb + p.s - 1) / p.s;
+    p.code_bytes = (uint64_t)p.n_tiles * p.n_iter * 64 * 16;
+    p.scale_bytes = (uint64_t)p.n_tiles * p.n_iter * 64 * 2;
+}
+
+void vx_place(VxMatPlan& p, uint64_t& code_cursor, uint64_t& scale_cursor) {
+    p.code_off = code_cursor;
+    p.scale_off = scale_cursor;
+    code_cursor = vx_align(code_cursor + p.code_bytes);
+    scale_cursor = vx_align(scale_cursor + p.scale_bytes);
+}
+
+VxMat vx_view(const VeloxHipArena* a, const VxMatPlan& p) {
+    VxMat m;
+    m.codes = (const uint4*)(a->weight_arena + p.code_off);
+    m.scales = (const uint16_t*)(a->weight_scales + p.scale_off);
+    m.n = p.n;
+    m.k = p.k;
+    m.s = p.s;
+    m.n_tiles = p.n_tiles;
+    m.n_iter = p.n_iter;
+    m.paired = p.paired;
+    return m;
+}
+
+VxMat vx_view_public(const VeloxHipQ4Matrix* q) {
+    VxMat m;
+    m.codes = (const uint4*)q->codes;
+    m.scales = (const uint16_t*)q->scales;
+    m.n = q->n;
+    m.k = q->k;
+    m.s = q->s_lanes;
+    m.n_tiles = q->n_tiles;
+    m.n_iter = q->n_iter;
+    m.paired = q->paired;
+    return m;
+}
+
+bool vx_shape_ok(const VeloxHipModelConfig& c) {
+    if (c.hidden_dim == 0 || c.num_layers == 0 || c.num_heads == 0 || c.num_kv_heads == 0) return false;
+    if (c.hidden_dim % 32 || c.intermediate_dim % 32 || c.max_seq_len == 0 || c.vocab_size == 0) return false;
+    if (c.num_heads % c.num_kv_heads) return false;
+    if (c.head_dim != 64 && c.head_dim != 128) return false;
+    const uint32_t G = c.num_heads / c.num_kv_heads;
+    if (c.head_dim == 64 && !(G == 1 || G == 2 || G == 3 || G == 4 || G == 8)) return false;
+    if (c.head_dim == 128 && !(G == 1 || G == 2 || G == 4 || G == 7 || G == 8)) return false;
+    if (((uint64_t)c.num_heads * c.head_dim) % 32) return false;
+    if (c.quant_mode != VELOX_QUANT_GGML_Q4_0) return false;
+    if (c.num_kv_heads > 64) return false;
+    if (c.hidden_dim > 32768 || c.intermediate_dim > 32768 || (uint64_t)c.num_heads * c.head_dim > 32768) return false;
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int velox_hip_last_error(void) {
+    const int e = g_last_error;
+    g_last_error = 0;
+    return e;
+}
+
+int velox_hip_builtin_config(const char* which, uint32_t max_seq_len, VeloxHipModelConfig* out) {
+    if (!which || !out) return VELOX_HIP_EINVAL;
+    VeloxHipModelConfig c;
+    std::memset(&c, 0, sizeof(c));
+    c.quant_mode = VELOX_QUANT_GGML_Q4_0;
+    if (!std::strcmp(which, "smollm_135m")) {  // examples/tinystories_smollm.vlx; src/runtime.rs:1175-1189
+        c = VeloxHipModelConfig{{0}, 49152, 576, 1536, 30, 9, 3, 64, 2048, 1e-5f, 10000.0f, 0, 1,
+                                VELOX_QUANT_GGML_Q4_0, 0, 0};
+    } else if (!std::strcmp(which, "llama3_8b")) {  // examples/llama3_8b.vlx
+        c = VeloxHipModelConfig{{0}, 128256, 4096, 14336, 32, 32, 8, 128, 8192, 1e-5f, 500000.0f, 0, 0,
+                                VELOX_QUANT_GGML_Q4_0, 0, 0};
+    } else if (!std::strcmp(which, "qwen2_5_7b")) {  // examples/qwen2_5_7b.vlx (tied head, QKV bias)
+        c = VeloxHipModelConfig{{0}, 152064, 3584, 18944, 28, 28, 4, 128, 4096, 1e-6f, 1000000.0f, 1, 1,
+                                VELOX_QUANT_GGML_Q4_0, 0, 0};
+    } else if (!std::strcmp(which, "qwen2_72b")) {  // examples/qwen2_72b.vlx
+        c = VeloxHipModelConfig{{0}, 152064, 8192, 29568, 80, 64, 8, 128, 8448, 1e-6f, 1000000.0f, 1, 0,
+                                VELOX_QUANT_GGML_Q4_0, 0, 0};
+    } else {
+        return VELOX_HIP_EINVAL;
+    }
+    std::snprintf(c.name, sizeof(c.name), "%s", which);
+    if (max_seq_len) c.max_seq_len = max_seq_len;
+    *out = c;
+    return VELOX_HIP_OK;
+}
+
+int velox_hip_q4_layout(uint32_t n, uint32_t k, uint32_t s_lanes, uint32_t paired, VeloxHipQ4Matrix* m,
+                        uint64_t* code_bytes, uint64_t* scale_bytes) {
+    if (!m || k == 0 || k % 32 || n == 0) return VELOX_HIP_EINVAL;
+    if (s_lanes && s_lanes != 4 && s_lanes != 8 && s_lanes != 16 && s_lanes != 32 && s_lanes != 64)
+        return VELOX_HIP_EINVAL;
+    if (paired && s_lanes == 64) return VELOX_HIP_EINVAL;
+    VxMatPlan p;
+    vx_mat_layout(n, k, s_lanes, paired, p);
+    m->n = n;
+    m->k = k;
+    m->s_lanes = p.s;
+    m->n_tiles = p.n_tiles;
+    m->n_iter = p.n_iter;
+    m->paired = paired;
+    m->reserved = 0;
+    if (code_bytes) *code_bytes = p.code_bytes;
+    if (scale_bytes) *scale_bytes = p.scale_bytes;
+    return VELOX_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Plan: the memory_planner's weight cursor + KV sizing + activation layout
+// (src/memory_planner.rs:282-474), re-sized for 288 GB of HBM3E on one GPU.
+// ---------------------------------------------------------------------------------------------
+int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) {
+    if (!cfg || !out) return VELOX_HIP_EINVAL;
+    if (!vx_shape_ok(*cfg)) return VELOX_HIP_EINVAL;
+    VeloxHipModel* M = new VeloxHipModel();
+    M->cfg = *cfg;
+    const VeloxHipModelConfig& c = M->cfg;
+    const uint32_t H = c.hidden_dim, F = c.intermediate_dim, D = c.head_dim;
+    const uint32_t qd = c.num_heads * D, kvd = c.num_kv_heads * D;
+    uint64_t cc = 0, sc = 0, nc = 0;
+    M->layers.resize(c.num_layers);
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        VxLayerPlan& L = M->layers[l];
+        vx_mat_layout(qd + 2 * kvd, H, 0, 0, L.qkv);
+        vx_mat_layout(H, qd, 0, 0, L.o);
+        vx_mat_layout(F, H, 0, 1, L.gate_up);
+        vx_mat_layout(H, F, 0, 0, L.down);
+        vx_place(L.qkv, cc, sc);
+        vx_place(L.o, cc, sc);
+        vx_place(L.gate_up, cc, sc);
+        vx_place(L.down, cc, sc);
+        L.attn_norm = nc;
+        nc = vx_align(nc + (uint64_t)H * 4);
+        L.mlp_norm = nc;
+        nc = vx_align(nc + (uint64_t)H * 4);
+        if (c.qkv_bias) {
+            L.bias = nc;
+            nc = vx_align(nc + (uint64_t)(qd + 2 * kvd) * 4);
+        }
+    }
+    vx_mat_layout(c.vocab_size, H, 0, 0, M->embed);
+    vx_place(M->embed, cc, sc);
+    if (c.tied_lm_head) {
+        M->head = M->embed;
+    } else {
+        vx_mat_layout(c.vocab_size, H, 0, 0, M->head);
+        vx_place(M->head, cc, sc);
+    }
+    M->final_norm = nc;
+    nc = vx_align(nc + (uint64_t)H * 4);
+    M->rope = nc;
+    nc = vx_align(nc + (uint64_t)c.max_seq_len * (D / 2) * 8);
+    M->code_bytes = cc;
+    M->scale_bytes = sc;
+    M->norm_bytes = nc;
+    M->kv_layer_bytes = vx_align((uint64_t)2 * c.num_kv_heads * c.max_seq_len * D * 2);
+    M->kv_bytes = M->kv_layer_bytes * c.num_layers;
+
+    uint32_t splits = c.attn_splits;
+    if (!splits) {
+        splits = (c.max_seq_len + 31) / 32;
+        if (splits > 64) splits = 64;
+        if (splits < 1) splits = 1;
+    }
+    M->splits = splits;
+    M->max_wgs = vx_gemv_max_wgs_default();
+
+    uint64_t ac = 0;
+    auto take = [&](uint64_t bytes) { const uint64_t o = ac; ac = vx_align(ac + bytes); return o; };
+    M->a_state = take(64);
+    M->a_plen = take(64);
+    M->a_argmax_counter = take(64);
+    M->a_counters = take(256);
+    M->a_token = take(64);
+    M->a_prompt = take((uint64_t)c.max_seq_len * 4);
+    M->a_h = take((uint64_t)H * 4);
+    M->a_qkv = take((uint64_t)(qd + 2 * kvd) * 4);
+    M->a_attn = take((uint64_t)qd * 4);
+    M->a_act = take((uint64_t)F * 4);
+    M->a_logits = take((uint64_t)c.vocab_size * 4);
+    M->a_part_o = take((uint64_t)c.num_heads * splits * D * 4);
+    M->a_part_ml = take((uint64_t)c.num_heads * splits * 2 * 4);
+    M->a_cand_v = take((uint64_t)M->max_wgs * 4);
+    M->a_cand_i = take((uint64_t)M->max_wgs * 4);
+    M->act_bytes = ac;
+
+    const uint64_t budget = c.vram_budget_bytes ? c.vram_budget_bytes : 288ULL * 1000 * 1000 * 1000;
+    const uint64_t total = M->code_bytes + M->scale_bytes + M->norm_bytes + M->kv_bytes + M->act_bytes;
+    if (total > budget) {  // reference diagnostic E002 (src/memory_planner.rs:398-420)
+        delete M;
+        return VELOX_HIP_ENOMEM;
+    }
+    *out = M;
+    return VELOX_HIP_OK;
+}
+
+void velox_hip_model_destroy(VeloxHipModel* m) { delete m; }
+
+int velox_hip_model_config(const VeloxHipModel* m, VeloxHipModelConfig* out) {
+    if (!m || !out) return VELOX_HIP_EINVAL;
+    *out = m->cfg;
+    return VELOX_HIP_OK;
+}
+
+int velox_hip_model_arena_bytes(const VeloxHipModel* m, uint64_t* weight_bytes, uint64_t* scale_bytes,
+                                uint64_t* norm_bytes, uint64_t* kv_bytes, uint64_t* act_bytes) {
+    if (!m) return VELOX_HIP_EINVAL;
+    if (weight_bytes) *weight_bytes = m->code_bytes;
+    if (scale_bytes) *scale_bytes = m->scale_bytes;
+    if (norm_bytes) *norm_bytes = m->norm_bytes;
+    if (kv_bytes) *kv_bytes = m->kv_bytes;
+    if (act_bytes) *act_bytes = m->act_bytes;
+    return VELOX_HIP_OK;
+}
+
+// Algorithmic bytes of one decode step at position pos: every linear weight once (18 B per 32
+// weights), the embedding row, the norm gains (and biases), the KV history read for positions
+// 0..pos and the new K/V written.
+uint64_t velox_hip_model_step_bytes(const VeloxHipModel* m, uint64_t pos) {
+    if (!m) return 0;
+    const VeloxHipModelConfig& c = m->cfg;
+    const uint64_t H = c.hidden_dim, F = c.intermediate_dim, D = c.head_dim;
+    const uint64_t qd = (uint64_t)c.num_heads * D, kvd = (uint64_t)c.num_kv_heads * D;
+    const uint64_t per_layer_w = (qd + 2 * kvd) * H + H * qd + 2 * F * H + H * F;
+    uint64_t bytes = (per_layer_w * c.num_layers + (uint64_t)c.vocab_size * H) / 32 * 18;
+    bytes += H / 32 * 18;                                   // embedding row
+    bytes += (2 * (uint64_t)c.num_layers + 1) * H * 4;      // norm gains
+    if (c.qkv_bias) bytes += (uint64_t)c.num_layers * (qd + 2 * kvd) * 4;
+    const uint64_t p = pos < c.max_seq_len ? pos : c.max_seq_len - 1;
+    bytes += (uint64_t)c.num_layers * 2 * kvd * 2 * (p + 1);  // KV read (bf16)
+    bytes += (uint64_t)c.num_layers * 2 * kvd * 2;            // KV write
+    return bytes;
+}
+
+uint64_t velox_hip_model_logits_offset(const VeloxHipModel* m) { return m ? m->a_logits : 0; }
+uint64_t velox_hip_model_hidden_offset(const VeloxHipModel* m) { return m ? m->a_h : 0; }
+
+// ---------------------------------------------------------------------------------------------
+// Arena
+// ---------------------------------------------------------------------------------------------
+int velox_hip_arena_create(const VeloxHipModel* m, VeloxHipArena* out) {
+    if (!m || !out) return VELOX_HIP_EINVAL;
+    std::memset(out, 0, sizeof(*out));
+    uint8_t *w = nullptr, *kv = nullptr, *act = nullptr, *nrm = nullptr;
+    uint32_t* ring = nullptr;
+    hipError_t e = hipMalloc((void**)&w, m->code_bytes + m->scale_bytes);
+    if (e == hipSuccess) e = hipMalloc((void**)&nrm, m->norm_bytes);
+    if (e == hipSuccess) e = hipMalloc((void**)&kv, m->kv_bytes);
+    if (e == hipSuccess) e = hipMalloc((void**)&act, m->act_bytes);
+    if (e == hipSuccess) e = hipHostMalloc((void**)&ring, VELOX_HIP_RING_SIZE * 4, hipHostMallocMapped);
+    if (e == hipSuccess) e = hipMemset(w, 0, m->code_bytes + m->scale_bytes);  // tile padding = 0
+    if (e == hipSuccess) e = hipMemset(nrm, 0, m->norm_bytes);
+    if (e == hipSuccess) e = hipMemset(kv, 0, m->kv_bytes);
+    if (e == hipSuccess) e = hipMemset(act, 0, m->act_bytes);  // state, counters, prompt_len = 0
+    if (e != hipSuccess) {
+        hipFree(w); hipFree(nrm); hipFree(kv); hipFree(act);
+        if (ring) hipHostFree(ring);
+        return (int)e;
+    }
+    std::memset(ring, 0, VELOX_HIP_RING_SIZE * 4);
+    // RoPE table: cos/sin of pos * theta^(-2j/D) evaluated exactly as src/runtime.rs:756-760
+    // (fp32 powf, product and sin/cos), once at startup instead of per token.
+    const VeloxHipModelConfig& c = m->cfg;
+    const uint32_t half = c.head_dim / 2;
+    std::vector<float> rope((size_t)c.max_seq_len * half * 2);
+    for (uint32_t p = 0; p < c.max_seq_len; ++p)
+        for (uint32_t j = 0; j < half; ++j) {
+            const float freq = 1.0f / powf(c.rope_theta, (float)(2 * j) / (float)c.head_dim);
+            const float angle = (float)p * freq;
+            rope[((size_t)p * half + j) * 2] = cosf(angle);
+            rope[((size_t)p * half + j) * 2 + 1] = sinf(angle);
+        }
+    e = hipMemcpy(nrm + m->rope, rope.data(), rope.size() * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return (int)e;
+    out->weight_arena = w;
+    out->weight_scales = w + m->code_bytes;
+    out->norm_weight_arena = nrm;
+    out->kv_cache_pool = kv;
+    out->activation_arena = act;
+    out->host_pinned_ring = ring;
+    out->quant_mode = c.quant_mode;
+    out->tied_lm_head = c.tied_lm_head;
+    out->model = m;
+    return VELOX_HIP_OK;
+}
+
+int velox_hip_arena_destroy(VeloxHipArena* a) {
+    if (!a) return VELOX_HIP_EINVAL;
+    hipFree((void*)a->weight_arena);
+    hipFree((void*)a->norm_weight_arena);
+    hipFree(a->kv_cache_pool);
+    hipFree(a->activation_arena);
+    if (a->host_pinned_ring) hipHostFree(a->host_pinned_ring);
+    std::memset(a, 0, sizeof(*a));
+    return VELOX_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Loaders
+// ---------------------------------------------------------------------------------------------
+namespace {
+// Target matrix, first logical row, pair part and row count of a weight kind.
+bool vx_target(const VeloxHipModel* M, int kind, uint32_t layer, const VxMatPlan** mp, uint32_t* row0,
+               uint32_t* pair, uint32_t* rows, uint32_t* cols) {
+    const VeloxHipModelConfig& c = M->cfg;
+    const uint32_t qd = c.num_heads * c.head_dim, kvd = c.num_kv_heads * c.head_dim;
+    *pair = 0;
+    *row0 = 0;
+    if (kind == VELOX_T_EMBED) { *mp = &M->embed; *rows = c.vocab_size; *cols = c.hidden_dim; return true; }
+    if (kind == VELOX_T_HEAD) {
+        if (c.tied_lm_head) return false;
+        *mp = &M->head; *rows = c.vocab_size; *cols = c.hidden_dim; return true;
+    }
+    if (layer >= c.num_layers) return false;
+    const VxLayerPlan& L = M->layers[layer];
+    switch (kind) {
+        case VELOX_T_Q: *mp = &L.qkv; *rows = qd; *cols = c.hidden_dim; return true;
+        case VELOX_T_K: *mp = &L.qkv; *row0 = qd; *rows = kvd; *cols = c.hidden_dim; return true;
+        case VELOX_T_V: *mp = &L.qkv; *row0 = qd + kvd; *rows = kvd; *cols = c.hidden_dim; return true;
+        case VELOX_T_O: *mp = &L.o; *rows = c.hidden_dim; *cols = qd; return true;
+        case VELOX_T_GATE: *mp = &L.gate_up; *rows = c.intermediate_dim; *cols = c.hidden_dim; return true;
+        case VELOX_T_UP: *mp = &L.gate_up; *pair = 1; *rows = c.intermediate_dim; *cols = c.hidden_dim; return true;
+        case VELOX_T_DOWN: *mp = &L.down; *rows = c.hidden_dim; *cols = c.intermediate_dim; return true;
+        default: return false;
+    }
+}
+
+bool vx_vec_target(const VeloxHipModel* M, int kind, uint32_t layer, uint64_t* off, uint64_t* count) {
+    const VeloxHipModelConfig& c = M->cfg;
+    const uint32_t qd = c.num_heads * c.head_dim, kvd = c.num_kv_heads * c.head_dim;
+    if (kind == VELOX_T_FINAL_NORM) { *off = M->final_norm; *count = c.hidden_dim; return true; }
+    if (layer >= c.num_layers) return false;
+    const VxLayerPlan& L = M->layers[layer];
+    switch (kind) {
+        case VELOX_T_ATTN_NORM: *off = L.attn_norm; *count = c.hidden_dim; return true;
+        case VELOX_T_MLP_NORM: *off = L.mlp_norm; *count = c.hidden_dim; return true;
+        case VELOX_T_BQ: if (!c.qkv_bias) return false; *off = L.bias; *count = qd; return true;
+        case VELOX_T_BK: if (!c.qkv_bias) return false; *off = L.bias + (uint64_t)qd * 4; *count = kvd; return true;
+        case VELOX_T_BV:
+            if (!c.qkv_bias) return false;
+            *off = L.bias + (uint64_t)(qd + kvd) * 4; *count = kvd; return true;
+        default: return false;
+    }
+}
+}  // namespace
+
+int velox_hip_arena_matrix(const VeloxHipArena* a, int kind, uint32_t layer, VeloxHipQ4Matrix* out, uint32_t* row0) {
+    if (!a || !a->model || !out) return VELOX_HIP_EINVAL;
+    const VxMatPlan* mp;
+    uint32_t r0, pair, rows, cols;
+    if (kind == VELOX_T_HEAD && a->model->cfg.tied_lm_head) kind = VELOX_T_EMBED;
+    if (!vx_target(a->model, kind, layer, &mp, &r0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
+    out->codes = (void*)(a->weight_arena + mp->code_off);
+    out->scales = (void*)(a->weight_scales + mp->scale_off);
+    out->n = mp->n;
+    out->k = mp->k;
+    out->s_lanes = mp->s;
+    out->n_tiles = mp->n_tiles;
+    out->n_iter = mp->n_iter;
+    out->paired = mp->paired;
+    out->reserved = 0;
+    if (row0) *row0 = pair ? mp->n : r0;  // paired: up rows follow the n gate rows when dequantized
+    return VELOX_HIP_OK;
+}
+
+int velox_hip_arena_vector(const VeloxHipArena* a, int kind, uint32_t layer, const float** out, uint64_t* count) {
+    if (!a || !a->model || !out) return VELOX_HIP_EINVAL;
+    uint64_t off, n;
+    if (!vx_vec_target(a->model, kind, layer, &off, &n)) return VELOX_HIP_EINVAL;
+    *out = (const float*)(a->norm_weight_arena + off);
+    if (count) *count = n;
+    return VELOX_HIP_OK;
+}
+
+int velox_hip_load_q4_0(VeloxHipArena* a, int kind, uint32_t layer, const void* blocks, uint64_t nbytes,
+                        hipStream_t stream) {
+    if (!a || !a->model || !blocks) return VELOX_HIP_EINVAL;
+    const VxMatPlan* mp;
+    uint32_t row0, pair, rows, cols;
+    if (!vx_target(a->model, kind, layer, &mp, &row0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
+    if (nbytes != (uint64_t)rows * (cols / 32) * 18) return VELOX_HIP_ESHAPE;
+    void* staging = nullptr;
+    hipError_t e = hipMalloc(&staging, nbytes);
+    if (e == hipSuccess) e = hipMemcpyAsync(staging, blocks, nbytes, hipMemcpyHostToDevice, stream);
+    if (e == hipSuccess) e = vx_launch_repack(staging, rows, row0, pair, vx_view(a, *mp), stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    hipFree(staging);
+    return (int)e;
+}
+
+int velox_hip_load_f32(VeloxHipArena* a, int kind, uint32_t layer, const float* data, uint64_t count,
+                       hipStream_t stream) {
+    if (!a || !a->model || !data) return VELOX_HIP_EINVAL;
+    uint64_t off, n;
+    if (!vx_vec_target(a->model, kind, layer, &off, &n)) return VELOX_HIP_EINVAL;
+    if (count != n) return VELOX_HIP_ESHAPE;
+    hipError_t e = hipMemcpyAsync((void*)(a->norm_weight_arena + off), data, n * 4, hipMemcpyHostToDevice, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    return (int)e;
+}
+
+int velox_hip_synthesize_model(VeloxHipArena* a, uint64_t seed, float sigma, float norm_sigma, hipStream_t st) {
+    if (!a || !a->model) return VELOX_HIP_EINVAL;
+    const VeloxHipModel* M = a->model;
+    const VeloxHipModelConfig& c = M->cfg;
+    const float coef = vx_normal_coef(sigma), ncoef = norm_sigma == 0.0f ? 0.0f : vx_normal_coef(norm_sigma);
+    hipError_t e = hipSuccess;
+    auto mat = [&](int kind, uint32_t layer) {
+        if (e != hipSuccess) return;
+        const VxMatPlan* mp;
+        uint32_t row0, pair, rows, cols;
+        if (!vx_target(M, kind, layer, &mp, &row0, &pair, &rows, &cols)) return;
+        e = vx_launch_synth_q4(vx_view(a, *mp), rows, row0, pair, vx_stream(seed, vx_tag(layer, kind)), coef, st);
+    };
+    auto vec = [&](int kind, uint32_t layer, float cf, float mean) {
+        if (e != hipSuccess) return;
+        uint64_t off, n;
+        if (!vx_vec_target(M, kind, layer, &off, &n)) return;
+        e = vx_launch_fill_normal((float*)(a->norm_weight_arena + off), n, vx_stream(seed, vx_tag(layer, kind)), cf,
+                                  mean, st);
+    };
+    mat(VELOX_T_EMBED, 0);
+    if (!c.tied_lm_head) mat(VELOX_T_HEAD, 0);
+    vec(VELOX_T_FINAL_NORM, 0, ncoef, 1.0f);
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        for (int k : {VELOX_T_Q, VELOX_T_K, VELOX_T_V, VELOX_T_O, VELOX_T_GATE, VELOX_T_UP, VELOX_T_DOWN}) mat(k, l);
+        vec(VELOX_T_ATTN_NORM, l, ncoef, 1.0f);
+        vec(VELOX_T_MLP_NORM, l, ncoef, 1.0f);
+        if (c.qkv_bias) {
+            vec(VELOX_T_BQ, l, coef, 0.0f);
+            vec(VELOX_T_BK, l, coef, 0.0f);
+            vec(VELOX_T_BV, l, coef, 0.0f);
+        }
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return (int)e;
+}
+
+int velox_hip_fill_kv(VeloxHipArena* a, uint32_t layer, uint32_t n_pos, uint64_t seed, float sigma, hipStream_t st) {
+    if (!a || !a->model) return VELOX_HIP_EINVAL;
+    const VeloxHipModelConfig& c = a->model->cfg;
+    if (layer >= c.num_layers || n_pos > c.max_seq_len) return VELOX_HIP_EINVAL;
+    uint16_t* base = (uint16_t*)(a->kv_cache_pool + a->model->kv_layer_bytes * layer);
+    hipError_t e = vx_launch_fill_kv(base, c.num_kv_heads, c.max_seq_len, c.head_dim, n_pos,
+                                     vx_stream(seed, vx_tag(layer, VX_TAG_KV_K)),
+                                     vx_stream(seed, vx_tag(layer, VX_TAG_KV_V)), vx_normal_coef(sigma), st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return (int)e;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Decode state / prompt
+// ---------------------------------------------------------------------------------------------
+int velox_hip_set_prompt(VeloxHipArena* a, const uint32_t* tokens, uint32_t n, hipStream_t st) {
+    if (!a || !a->model || (n && !tokens)) return VELOX_HIP_EINVAL;
+    if (n > a->model->cfg.max_seq_len) return VELOX_HIP_EINVAL;
+    hipError_t e = hipSuccess;
+    if (n) e = hipMemcpyAsync(a->activation_arena + a->model->a_prompt, tokens, (size_t)n * 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(a->activation_arena + a->model->a_plen, &n, 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return (int)e;
+}
+
+int velox_hip_set_state(VeloxHipArena* a, uint64_t step, uint32_t token, hipStream_t st) {
+    if (!a || !a->model) return VELOX_HIP_EINVAL;
+    return (int)vx_launch_set_state((VeloxDecodeState*)(a->activation_arena + a->model->a_state), step, token, st);
+}
+
+int velox_hip_get_state(const VeloxHipArena* a, VeloxDecodeState* out, hipStream_t st) {
+    if (!a || !a->model || !out) return VELOX_HIP_EINVAL;
+    hipError_t e = hipMemcpyAsync(out, a->activation_arena + a->model->a_state, sizeof(*out), hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return (int)e;
+}
+
+// ---------------------------------------------------------------------------------------------
+// The decode step: embed -> L x [QKV(+norm), attention, o_proj+res, gate/up(+norm)+SwiGLU,
+// down+res] -> norm + LM head + argmax (+ ring + state advance). 2 + 5L launches.
+// ---------------------------------------------------------------------------------------------
+void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st) {
+    if (!A || !A->model) { if (!g_last_error) g_last_error = VELOX_HIP_EINVAL; return; }
+    const VeloxHipModel* M = A->model;
+    const VeloxHipModelConfig& c = M->cfg;
+    uint8_t* act = A->activation_arena;
+    const float* nrm = (const float*)A->norm_weight_arena;
+    VeloxDecodeState* state = (VeloxDecodeState*)(act + M->a_state);
+    float* h = (float*)(act + M->a_h);
+    float* qkv = (float*)(act + M->a_qkv);
+    float* attn = (float*)(act + M->a_attn);
+    float* ffn = (float*)(act + M->a_act);
+    auto vecp = [&](uint64_t off) { return (const float*)((const uint8_t*)nrm + off); };
+
+    vx_record(vx_launch_embed(vx_view(A, M->embed), state, 0, h, mask, st));
+    VxAttnArgs at;
+    std::memset(&at, 0, sizeof(at));
+    at.qkv = qkv;
+    at.rope = (const float2*)vecp(M->rope);
+    at.state = state;
+    at.part_o = (float*)(act + M->a_part_o);
+    at.part_ml = (float*)(act + M->a_part_ml);
+    at.counters = (uint32_t*)(act + M->a_counters);
+    at.out = attn;
+    at.hq = c.num_heads;
+    at.hkv = c.num_kv_heads;
+    at.s_max = c.max_seq_len;
+    at.splits = M->splits;
+    at.scale = 1.0f / sqrtf((float)c.head_dim);
+    at.active_mask = mask;
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        const VxLayerPlan& L = M->layers[l];
+        VxGemvArgs g;
+        std::memset(&g, 0, sizeof(g));
+        g.active_mask = mask;
+        g.eps = c.rms_norm_eps;
+        g.x = h;
+        g.gain = vecp(L.attn_norm);
+        g.bias = c.qkv_bias ? vecp(L.bias) : nullptr;
+        g.y = qkv;
+        vx_record(vx_launch_gemv(vx_view(A, L.qkv), g, VX_EPI_STORE, M->max_wgs, st));
+
+        at.kv = (uint16_t*)(A->kv_cache_pool + M->kv_layer_bytes * l);
+        vx_record(vx_launch_attention(at, c.head_dim, st));
+
+        std::memset(&g, 0, sizeof(g));
+        g.active_mask = mask;
+        g.x = attn;
+        g.res = h;
+        g.y = h;
+        vx_record(vx_launch_gemv(vx_view(A, L.o), g, VX_EPI_RESID, M->max_wgs, st));
+
+        std::memset(&g, 0, sizeof(g));
+        g.active_mask = mask;
+        g.eps = c.rms_norm_eps;
+        g.x = h;
+        g.gain = vecp(L.mlp_norm);
+        g.y = ffn;
+        vx_record(vx_launch_gemv(vx_view(A, L.gate_up), g, VX_EPI_SWIGLU, M->max_wgs, st));
+
+        std::memset(&g, 0, sizeof(g));
+        g.active_mask = mask;
+        g.x = ffn;
+        g.res = h;
+        g.y = h;
+        vx_record(vx_launch_gemv(vx_view(A, L.down), g, VX_EPI_RESID, M->max_wgs, st));
+    }
+    VxGemvArgs g;
+    std::memset(&g, 0, sizeof(g));
+    g.active_mask = mask;
+    g.eps = c.rms_norm_eps;
+    g.x = h;
+    g.gain = vecp(M->final_norm);
+    g.y = (float*)(act + M->a_logits);
+    g.cand_v = (float*)(act + M->a_cand_v);
+    g.cand_i = (uint32_t*)(act + M->a_cand_i);
+    g.counter = (uint32_t*)(act + M->a_argmax_counter);
+    g.state = state;
+    g.ring = A->host_pinned_ring;
+    g.prompt = (const uint32_t*)(act + M->a_prompt);
+    g.prompt_len = (const uint32_t*)(act + M->a_plen);
+    g.token_out = (uint32_t*)(act + M->a_token);
+    vx_record(vx_launch_gemv(vx_view(A, M->head), g, VX_EPI_ARGMAX, M->max_wgs, st));
+}
+
+void velox_hip_decode(VeloxHipArena* A, uint32_t token_in, size_t step, uint64_t mask, hipStream_t st) {
+    if (!A || !A->model) { if (!g_last_error) g_last_error = VELOX_HIP_EINVAL; return; }
+    vx_record(vx_launch_set_state((VeloxDecodeState*)(A->activation_arena + A->model->a_state), step, token_in, st));
+    velox_hip_decode_graph_step(A, mask, st);
+}
+
+// Prefill is the same single-token step (the reference runner prefills token by token,
+// velox_cuda_runner.cu:504-506); the staged prompt forces the next token.
+void velox_hip_prefill_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st) {
+    velox_hip_decode_graph_step(A, mask, st);
+}
+void velox_hip_prefill(VeloxHipArena* A, uint32_t token_in, size_t step, uint64_t mask, hipStream_t st) {
+    velox_hip_decode(A, token_in, step, mask, st);
+}
+
+#define VX_MODEL_ENTRY(NAME, KEY)                                                                   \
+    static bool vx_is_##NAME(const VeloxHipArena* a) {                                              \
+        if (a && a->model && !std::strcmp(a->model->cfg.name, KEY)) return true;                    \
+        if (!g_last_error) g_last_error = VELOX_HIP_EINVAL;                                         \
+        return false;                                                                               \
+    }                                                                                               \
+    void velox_##NAME##_decode_graph_step_hip(VeloxHipArena* ctx, uint64_t m, hipStream_t s) {      \
+        if (vx_is_##NAME(ctx)) velox_hip_decode_graph_step(ctx, m, s);                              \
+    }                                                                                               \
+    void velox_##NAME##_decode_hip(VeloxHipArena* ctx, uint32_t t, size_t st, uint64_t m, hipStream_t s) { \
+        if (vx_is_##NAME(ctx)) velox_hip_decode(ctx, t, st, m, s);                                  \
+    }
+
+VX_MODEL_ENTRY(SmolLM_135M, "smollm_135m")
+VX_MODEL_ENTRY(Llama3_8B, "llama3_8b")
+VX_MODEL_ENTRY(Qwen2_5_7B, "qwen2_5_7b")
+VX_MODEL_ENTRY(Qwen2_72B, "qwen2_72b")
+
+void velox_SmolLM_135M_prefill_graph_step_hip(VeloxHipArena* ctx, uint64_t m, hipStream_t s) {
+    if (vx_is_SmolLM_135M(ctx)) velox_hip_prefill_graph_step(ctx, m, s);
+}
+void velox_SmolLM_135M_prefill_hip(VeloxHipArena* ctx, uint32_t t, size_t st, uint64_t m, hipStream_t s) {
+    if (vx_is_SmolLM_135M(ctx)) velox_hip_prefill(ctx, t, st, m, s);
+}
+void velox_Llama3_8B_prefill_graph_step_hip(VeloxHipArena* ctx, uint64_t m, hipStream_t s) {
+    if (vx_is_Llama3_8B(ctx)) velox_hip_prefill_graph_step(ctx, m, s);
+}
+void velox_Llama3_8B_prefill_hip(VeloxHipArena* ctx, uint32_t t, size_t st, uint64_t m, hipStream_t s) {
+    if (vx_is_Llama3_8B(ctx)) velox_hip_prefill(ctx, t, st, m, s);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Per-kernel entry points
+// ---------------------------------------------------------------------------------------------
+int velox_hip_q4_0_repack(const void* d_blocks, uint32_t rows, uint32_t row0, uint32_t pair_part,
+                          const VeloxHipQ4Matrix* m, hipStream_t st) {
+    if (!d_blocks || !m) return VELOX_HIP_EINVAL;
+    const uint32_t logical = m->n;
+    if (row0 + rows > logical || pair_part > (m->paired ? 1u : 0u)) return VELOX_HIP_EINVAL;
+    return (int)vx_launch_repack(d_blocks, rows, row0, pair_part, vx_view_public(m), st);
+}
+
+int velox_hip_q4_0_dequant(const VeloxHipQ4Matrix* m, float* d_out, hipStream_t st) {
+    if (!m || !d_out) return VELOX_HIP_EINVAL;
+    return (int)vx_launch_dequant(vx_view_public(m), d_out, st);
+}
+
+int velox_hip_q4_0_quantize(const float* d_x, uint32_t rows, uint32_t k, void* d_blocks, hipStream_t st) {
+    if (!d_x || !d_blocks || k % 32) return VELOX_HIP_EINVAL;
+    return (int)vx_launch_quantize(d_x, rows, k, d_blocks, st);
+}
+
+int velox_hip_fill_normal(float* d_out, uint64_t n, uint64_t seed, uint64_t tag, float sigma, float mean,
+                          hipStream_t st) {
+    if (!d_out) return VELOX_HIP_EINVAL;
+    return (int)vx_launch_fill_normal(d_out, n, vx_stream(seed, tag), sigma == 0.0f ? 0.0f : vx_normal_coef(sigma),
+                                      mean, st);
+}
+
+int velox_hip_gemv_q4_0(const VeloxHipQ4Matrix* m, const float* d_x, const float* d_gain, float eps,
+                        const float* d_bias, const float* d_res, float* d_y, int mode, hipStream_t st) {
+    if (!m || !d_x || !d_y || mode < 0 || mode > 2) return VELOX_HIP_EINVAL;
+    if (mode == VELOX_GEMV_RESIDUAL && !d_res) return VELOX_HIP_EINVAL;
+    if ((mode == VELOX_GEMV_SWIGLU) != (m->paired != 0)) return VELOX_HIP_EINVAL;
+    VxGemvArgs g;
+    std::memset(&g, 0, sizeof(g));
+    g.x = d_x;
+    g.gain = d_gain;
+    g.eps = eps;
+    g.bias = d_bias;
+    g.res = d_res;
+    g.y = d_y;
+    g.active_mask = 1;
+    const int epi = mode == VELOX_GEMV_STORE ? VX_EPI_STORE : mode == VELOX_GEMV_RESIDUAL ? VX_EPI_RESID : VX_EPI_SWIGLU;
+    return (int)vx_launch_gemv(vx_view_public(m), g, epi, vx_gemv_max_wgs_default(), st);
+}
+
+int velox_hip_lm_head_argmax(const VeloxHipQ4Matrix* m, const float* d_x, const float* d_gain, float eps,
+                             float* d_logits, uint32_t* d_token, hipStream_t st) {
+    if (!m || !d_x || !d_logits || !d_token || m->paired) return VELOX_HIP_EINVAL;
+    // scratch for candidates + counter, reused across calls on this device
+    static void* scratch = nullptr;
+    const uint32_t wgs = vx_gemv_max_wgs_default();
+    if (!scratch) {
+        hipError_t e = hipMalloc(&scratch, (size_t)wgs * 8 + 256);
+        if (e != hipSuccess) return (int)e;
+        e = hipMemset(scratch, 0, (size_t)wgs * 8 + 256);
+        if (e != hipSuccess) return (int)e;
+    }
+    VxGemvArgs g;
+    std::memset(&g, 0, sizeof(g));
+    g.x = d_x;
+    g.gain = d_gain;
+    g.eps = eps;
+    g.y = d_logits;
+    g.cand_v = (float*)scratch;
+    g.cand_i = (uint32_t*)((uint8_t*)scratch + (size_t)wgs * 4);
+    g.counter = (uint32_t*)((uint8_t*)scratch + (size_t)wgs * 8);
+    g.token_out = d_token;
+    g.active_mask = 1;
+    return (int)vx_launch_gemv(vx_view_public(m), g, VX_EPI_ARGMAX, wgs, st);
+}
+
+int velox_hip_argmax_f32(const float* d_x, uint32_t n, uint32_t* d_out, hipStream_t st) {
+    if (!d_x || !d_out || n == 0) return VELOX_HIP_EINVAL;
+    return (int)vx_launch_argmax(d_x, n, d_out, st);
+}
+
+int velox_hip_rmsnorm(const float* d_x, const float* d_w, uint32_t n, float eps, float* d_y, hipStream_t st) {
+    if (!d_x || !d_w || !d_y || n == 0) return VELOX_HIP_EINVAL;
+    return (int)vx_launch_rmsnorm(d_x, d_w, n, eps, d_y, st);
+}
+
+int velox_hip_attention_decode(const float* d_qkv, uint16_t* d_kv_layer, uint32_t hq, uint32_t hkv, uint32_t d,
+                               uint32_t s_max, uint32_t pos, float theta, uint32_t splits, float* d_out,
+                               hipStream_t st) {
+    if (!d_qkv || !d_kv_layer || !d_out || hkv == 0 || hkv > 64 || hq % hkv || pos >= s_max || splits == 0 ||
+        splits > 256)
+        return VELOX_HIP_EINVAL;
+    // rope row for `pos`, partials and counters: per-call scratch (test entry point)
+    const uint32_t half = d / 2;
+    std::vector<float> rope((size_t)half * 2);
+    for (uint32_t j = 0; j < half; ++j) {
+        const float freq = 1.0f / powf(theta, (float)(2 * j) / (float)d);
+        const float angle = (float)pos * freq;
+        rope[2 * j] = cosf(angle);
+        rope[2 * j + 1] = sinf(angle);
+    }
+    const size_t rope_b = vx_align((size_t)(pos + 1) * half * 8);
+    const size_t po_b = vx_align((size_t)hq * splits * d * 4), pml_b = vx_align((size_t)hq * splits * 8);
+    uint8_t* scratch = nullptr;
+    hipError_t e = hipMalloc((void**)&scratch, rope_b + po_b + pml_b + 256);
+    if (e != hipSuccess) return (int)e;
+    e = hipMemsetAsync(scratch + rope_b + po_b + pml_b, 0, 256, st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(scratch + (size_t)pos * half * 8, rope.data(), (size_t)half * 8, hipMemcpyHostToDevice, st);
+    VxAttnArgs at;
+    std::memset(&at, 0, sizeof(at));
+    at.qkv = d_qkv;
+    at.kv = d_kv_layer;
+    at.rope = (const float2*)scratch;
+    at.state = nullptr;
+    at.fixed_pos = pos;
+    at.part_o = (float*)(scratch + rope_b);
+    at.part_ml = (float*)(scratch + rope_b + po_b);
+    at.counters = (uint32_t*)(scratch + rope_b + po_b + pml_b);
+    at.out = d_out;
+    at.hq = hq;
+    at.hkv = hkv;
+    at.s_max = s_max;
+    at.splits = splits;
+    at.scale = 1.0f / sqrtf((float)d);
+    at.active_mask = 1;
+    if (e == hipSuccess) e = vx_launch_attention(at, d, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    hipFree(scratch);
+    return (int)e;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Runner: the flow of velox_cuda_runner.cu main (:327-726) -- plan, alloc, load (synthesize),
+// graph capture (:474-481), prefill (:493-512), timed decode replays (:535-563).
+// ---------------------------------------------------------------------------------------------
+int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_tokens, VeloxHipRunReport* rep) {
+    if (!opt || !rep || !opt->model || opt->prompt_len == 0) return VELOX_HIP_EINVAL;
+    std::memset(rep, 0, sizeof(*rep));
+    const uint32_t total = opt->prompt_len + opt->warmup + opt->steps;
+    VeloxHipModelConfig cfg;
+    int rc = velox_hip_builtin_config(opt->model, opt->max_seq_len ? opt->max_seq_len : total + 1, &cfg);
+    if (rc) return rc;
+    if (opt->num_layers) cfg.num_layers = opt->num_layers;
+    if (cfg.max_seq_len < total) return VELOX_HIP_EINVAL;
+    VeloxHipModel* M = nullptr;
+    rc = velox_hip_model_create(&cfg, &M);
+    if (rc) return rc;
+    VeloxHipArena A;
+    rc = velox_hip_arena_create(M, &A);
+    if (rc) { velox_hip_model_destroy(M); return rc; }
+    hipStream_t st;
+    hipStreamCreateWithFlags(&st, hipStreamNonBlocking);
+    hipEvent_t e0, e1, e2, e3;
+    hipEventCreate(&e0); hipEventCreate(&e1); hipEventCreate(&e2); hipEventCreate(&e3);
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+
+    const auto t_load = std::chrono::steady_clock::now();
+    rc = velox_hip_synthesize_model(&A, opt->seed, opt->sigma, opt->norm_sigma, st);
+    rep->load_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_load).count();
+
+    std::vector<uint32_t> prompt(opt->prompt_len);
+    const uint64_t pst = vx_stream(opt->seed, vx_tag(0, VX_TAG_PROMPT));
+    for (uint32_t i = 0; i < opt->prompt_len; ++i) prompt[i] = vx_uniform_u32(pst, i, cfg.vocab_size);
+    if (!rc) rc = velox_hip_set_prompt(&A, prompt.data(), opt->prompt_len, st);
+    if (!rc) rc = velox_hip_set_state(&A, 0, prompt[0], st);
+    velox_hip_last_error();
+    if (!rc && opt->use_graph) {
+        hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+        if (e == hipSuccess) {
+            velox_hip_decode_graph_step(&A, 1ULL, st);
+            e = hipStreamEndCapture(st, &graph);
+        }
+        if (e == hipSuccess) e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {  // fall back to eager launches (velox_cuda_runner.cu:483-486)
+            if (opt->verbose) std::fprintf(stderr, "[velox-hip] graph capture failed (%d): eager launches\n", (int)e);
+            exec = nullptr;
+            (void)hipGetLastError();
+        }
+        rc = velox_hip_last_error();
+    }
+    auto one_step = [&]() {
+        if (exec) vx_record(hipGraphLaunch(exec, st));
+        else velox_hip_decode_graph_step(&A, 1ULL, st);
+    };
+    if (!rc) {
+        hipEventRecord(e0, st);
+        for (uint32_t p = 0; p < opt->prompt_len; ++p) one_step();
+        hipEventRecord(e1, st);
+        for (uint32_t w = 0; w < opt->warmup; ++w) one_step();
+        rc = (int)hipStreamSynchronize(st);
+    }
+    if (!rc) {
+        // timed region: synchronized on both sides, device time from events on the same stream
+        const auto w0 = std::chrono::steady_clock::now();
+        hipEventRecord(e2, st);
+        for (uint32_t s = 0; s < opt->steps; ++s) one_step();
+        hipEventRecord(e3, st);
+        rc = (int)hipStreamSynchronize(st);
+        rep->wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - w0).count();
+        if (!rc) rc = velox_hip_last_error();
+    }
+    if (!rc) {
+        float ms_p = 0.f, ms_d = 0.f;
+        hipEventElapsedTime(&ms_p, e0, e1);
+        hipEventElapsedTime(&ms_d, e2, e3);
+        rep->prefill_ms = ms_p;
+        rep->decode_ms = ms_d;
+        rep->tok_per_s = opt->steps && ms_d > 0 ? opt->steps / (ms_d * 1e-3) : 0.0;
+        double bytes = 0.0;
+        const uint32_t first = opt->prompt_len + opt->warmup;
+        for (uint32_t s = 0; s < opt->steps; ++s) bytes += (double)velox_hip_model_step_bytes(M, first + s);
+        rep->bytes_per_step = opt->steps ? bytes / opt->steps : 0.0;
+        rep->hbm_gbps = rep->bytes_per_step * rep->tok_per_s / 1e9;
+        // ring[pos & 1023] holds the argmax after position pos (velox_cuda_runner.cu:541-546)
+        uint32_t n = 0;
+        const uint32_t lo = total > VELOX_HIP_RING_SIZE ? total - VELOX_HIP_RING_SIZE : 0;
+        for (uint32_t p = lo; p < total && n < max_tokens; ++p)
+            if (tokens) tokens[n++] = A.host_pinned_ring[p & (VELOX_HIP_RING_SIZE - 1)];
+        rep->n_tokens = n;
+        rep->first_token = A.host_pinned_ring[(opt->prompt_len - 1) & (VELOX_HIP_RING_SIZE - 1)];
+    }
+    if (!rc && opt->kernel_passes) {
+        // The dominant kernel alone: the fused RMSNorm + gate/up + SwiGLU GEMV of every layer in
+        // turn (each layer's weights are new to the caches), timed by events on this stream.
+        uint8_t* act = A.activation_arena;
+        VxGemvArgs g;
+        std::memset(&g, 0, sizeof(g));
+        g.active_mask = 1;
+        g.eps = cfg.rms_norm_eps;
+        g.x = (const float*)(act + M->a_h);
+        g.y = (float*)(act + M->a_act);
+        auto launch_all = [&]() {
+            for (uint32_t l = 0; l < cfg.num_layers; ++l) {
+                g.gain = (const float*)(A.norm_weight_arena + M->layers[l].mlp_norm);
+                vx_record(vx_launch_gemv(vx_view(&A, M->layers[l].gate_up), g, VX_EPI_SWIGLU, M->max_wgs, st));
+            }
+        };
+        launch_all();  // warm
+        hipEventRecord(e0, st);
+        for (uint32_t r = 0; r < opt->kernel_passes; ++r) launch_all();
+        hipEventRecord(e1, st);
+        rc = (int)hipStreamSynchronize(st);
+        if (!rc) rc = velox_hip_last_error();
+        float ms = 0.f;
+        hipEventElapsedTime(&ms, e0, e1);
+        rep->kernel_launches = opt->kernel_passes * cfg.num_layers;
+        rep->kernel_us = rep->kernel_launches ? ms * 1e3 / rep->kernel_launches : 0.0;
+        rep->kernel_bytes = (double)cfg.intermediate_dim * 2.0 * cfg.hidden_dim / 32.0 * 18.0 +
+                            (double)cfg.hidden_dim * 4.0 * 2.0 + (double)cfg.intermediate_dim * 4.0;
+    }
+    rep->status = rc;
+    if (exec) hipGraphExecDestroy(exec);
+    if (graph) hipGraphDestroy(graph);
+    hipEventDestroy(e0); hipEventDestroy(e1); hipEventDestroy(e2); hipEventDestroy(e3);
+    hipStreamDestroy(st);
+    velox_hip_arena_destroy(&A);
+    velox_hip_model_destroy(M);
+    return rc;
+}
+
+}  // extern "C"

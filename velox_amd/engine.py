@@ -1,0 +1,167 @@
+"""Host-side mirror of the reference's engine interface over the HIP decode backend.
+
+``HipDecodeEngine`` offers the call surface of ``VeloxStaticExecutionEngine``
+(src/runtime.rs:1229-1502): ``forward_step(token, pos) -> next token`` with ``logits`` filled,
+and ``generate_greedy_into(prompt, n)``; underneath, every step is one launch sequence of the
+hand-written gfx950 kernels behind include/velox_hip.h (optionally replayed as a hipGraph, as the
+reference runner does, src/runners/velox_cuda_runner.cu:471-540). Weights are the seeded synthetic
+Q4_0 model synthesized on the device.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib as L
+
+
+def make_config(model, max_seq_len: int = 0, num_layers: int = 0, attn_splits: int = 0) -> L.ModelConfig:
+    """A builtin config by name, or a dict of ModelConfig fields (custom shapes for tests)."""
+    if isinstance(model, str):
+        cfg = L.builtin_config(model, max_seq_len)
+    else:
+        cfg = L.ModelConfig()
+        d = dict(model)
+        cfg.name = d.pop("name", "custom").encode()
+        cfg.quant_mode = L.QUANT_GGML_Q4_0
+        for k, v in d.items():
+            setattr(cfg, k, v)
+        if max_seq_len:
+            cfg.max_seq_len = max_seq_len
+    if num_layers:
+        cfg.num_layers = num_layers
+    if attn_splits:
+        cfg.attn_splits = attn_splits
+    return cfg
+
+
+class HipDecodeEngine:
+    def __init__(self, model, seed: int = 0, sigma: float = 0.02, norm_sigma: float = 0.0,
+                 max_seq_len: int = 0, num_layers: int = 0, attn_splits: int = 0, synthesize: bool = True):
+        self.lib = L.load()
+        self.cfg = make_config(model, max_seq_len, num_layers, attn_splits)
+        self._model = C.c_void_p()
+        L.check(self.lib.velox_hip_model_create(C.byref(self.cfg), C.byref(self._model)), "model_create")
+        self.arena = L.Arena()
+        L.check(self.lib.velox_hip_arena_create(self._model, C.byref(self.arena)), "arena_create")
+        self.vocab = self.cfg.vocab_size
+        self.logits_off = self.lib.velox_hip_model_logits_offset(self._model)
+        self.hidden_off = self.lib.velox_hip_model_hidden_offset(self._model)
+        self.logits = np.zeros(self.vocab, np.float32)
+        self._graph = None
+        if synthesize:
+            L.check(self.lib.velox_hip_synthesize_model(C.byref(self.arena), seed, sigma, norm_sigma, None),
+                    "synthesize_model")
+
+    # -- plan ---------------------------------------------------------------------------------
+    def step_bytes(self, pos: int) -> int:
+        return int(self.lib.velox_hip_model_step_bytes(self._model, pos))
+
+    def arena_bytes(self) -> dict:
+        v = [C.c_uint64() for _ in range(5)]
+        L.check(self.lib.velox_hip_model_arena_bytes(self._model, *[C.byref(x) for x in v]))
+        return dict(zip(["weights", "scales", "norms", "kv", "activations"], [x.value for x in v]))
+
+    # -- loaders ------------------------------------------------------------------------------
+    def load_q4_0(self, kind: int, layer: int, blocks: np.ndarray) -> None:
+        blocks = np.ascontiguousarray(blocks, np.uint8)
+        L.check(self.lib.velox_hip_load_q4_0(C.byref(self.arena), kind, layer, blocks.ctypes.data, blocks.nbytes,
+                                             None), "load_q4_0")
+
+    def load_f32(self, kind: int, layer: int, data: np.ndarray) -> None:
+        data = np.ascontiguousarray(data, np.float32)
+        L.check(self.lib.velox_hip_load_f32(C.byref(self.arena), kind, layer, data.ctypes.data, data.size, None),
+                "load_f32")
+
+    def fill_kv(self, layer: int, n_pos: int, seed: int, sigma: float = 1.0) -> None:
+        L.check(self.lib.velox_hip_fill_kv(C.byref(self.arena), layer, n_pos, seed, sigma, None), "fill_kv")
+
+    # -- state --------------------------------------------------------------------------------
+    def set_prompt(self, tokens) -> None:
+        arr = (C.c_uint32 * len(tokens))(*[int(t) for t in tokens])
+        L.check(self.lib.velox_hip_set_prompt(C.byref(self.arena), arr, len(tokens), None), "set_prompt")
+
+    def set_state(self, step: int, token: int) -> None:
+        L.check(self.lib.velox_hip_set_state(C.byref(self.arena), step, token, None), "set_state")
+
+    def state(self) -> tuple[int, int]:
+        s = L.DecodeState()
+        L.check(self.lib.velox_hip_get_state(C.byref(self.arena), C.byref(s), None), "get_state")
+        return int(s.step), int(s.token)
+
+    def sync(self) -> None:
+        rc = L.hip().hipDeviceSynchronize()
+        if rc != 0:
+            raise RuntimeError(f"hipDeviceSynchronize failed: {rc}")
+        err = self.lib.velox_hip_last_error()
+        if err != 0:
+            raise RuntimeError(f"decode step launch failed: {err}")
+
+    # -- the step -----------------------------------------------------------------------------
+    def forward_step(self, token: int, pos: int) -> int:
+        """src/runtime.rs:1328-1451: one token at position pos; fills self.logits."""
+        self.lib.velox_hip_decode(C.byref(self.arena), int(token), int(pos), 1, None)
+        self.sync()
+        self.read_logits()
+        return int(self.arena.host_pinned_ring[pos & (L.RING_SIZE - 1)])
+
+    def graph_step(self) -> None:
+        """One decode step driven by the device state (no host round trip)."""
+        self.lib.velox_hip_decode_graph_step(C.byref(self.arena), 1, None)
+
+    def read_logits(self) -> np.ndarray:
+        L.memcpy_dtoh(self.logits.ctypes.data, self.arena.activation_arena + self.logits_off, self.logits.nbytes)
+        return self.logits
+
+    def read_hidden(self) -> np.ndarray:
+        h = np.empty(self.cfg.hidden_dim, np.float32)
+        L.memcpy_dtoh(h.ctypes.data, self.arena.activation_arena + self.hidden_off, h.nbytes)
+        return h
+
+    def ring(self, pos: int) -> int:
+        return int(self.arena.host_pinned_ring[pos & (L.RING_SIZE - 1)])
+
+    def generate_greedy_into(self, prompt, num_new_tokens: int) -> list[int]:
+        """src/runtime.rs:1456-1490: prefill token by token, then greedy decode."""
+        pos = 0
+        nxt = int(prompt[0])
+        for tok in prompt:
+            nxt = self.forward_step(int(tok), pos)
+            pos += 1
+        out = []
+        if num_new_tokens == 0:
+            return out
+        out.append(nxt)
+        for _ in range(1, num_new_tokens):
+            nxt = self.forward_step(nxt, pos)
+            pos += 1
+            out.append(nxt)
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "_model", None) and self._model.value:
+            self.lib.velox_hip_arena_destroy(C.byref(self.arena))
+            self.lib.velox_hip_model_destroy(self._model)
+            self._model = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def run(model: str = "llama3_8b", prompt_len: int = 128, warmup: int = 5, steps: int = 251, seed: int = 1234,
+        sigma: float = 0.02, norm_sigma: float = 0.0, use_graph: bool = True, num_layers: int = 0,
+        max_seq_len: int = 0, max_tokens: int = 1024, kernel_passes: int = 0) -> tuple[dict, list[int]]:
+    """The C++ runner flow (velox_hip_run): synthesize, capture, prefill, timed decode."""
+    lib = L.load()
+    opt = L.RunOptions(model.encode(), max_seq_len, prompt_len, warmup, steps, seed, sigma, norm_sigma,
+                       int(use_graph), num_layers, kernel_passes, 0)
+    rep = L.RunReport()
+    toks = (C.c_uint32 * max_tokens)()
+    rc = lib.velox_hip_run(C.byref(opt), toks, max_tokens, C.byref(rep))
+    L.check(rc, "velox_hip_run")
+    d = {f: getattr(rep, f) for f, _ in rep._fields_}
+    return d, [int(toks[i]) for i in range(rep.n_tokens)]
