@@ -55,7 +55,7 @@ typedef struct VeloxHipModelConfig {
     uint32_t qkv_bias;          /* 1: q/k/v biases (Qwen) */
     uint32_t tied_lm_head;      /* 1: LM head reads the embedding table */
     uint32_t quant_mode;        /* VELOX_QUANT_GGML_Q4_0 */
-    uint32_t attn_splits;       /* split-K partitions over the sequence; 0 = automatic */
+    uint32_t attn_splits;       /* split-K partitions over the sequence (<= 64); 0 = automatic */
     uint64_t vram_budget_bytes; /* 0 = 288 GB of HBM3E */
 } VeloxHipModelConfig;
 

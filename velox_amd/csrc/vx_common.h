@@ -95,7 +95,7 @@ struct VxMat {
 struct VxGemvArgs {
     const uint4* codes;
     const uint16_t* scales;
-    uint32_t n, k, n_tiles, n_iter;
+    uint32_t n, k, n_tiles, n_iter, contig;
     const float* x;
     const float* gain;
     float eps;
@@ -150,3 +150,7 @@ hipError_t vx_launch_quantize(const float* x, uint32_t rows, uint32_t k, void* b
 hipError_t vx_launch_rmsnorm(const float* x, const float* w, uint32_t n, float eps, float* y, hipStream_t st);
 hipError_t vx_launch_argmax(const float* x, uint32_t n, uint32_t* out, hipStream_t st);
 uint32_t vx_gemv_max_wgs_default();
+uint32_t vx_gemv_grid(uint32_t n_tiles, uint32_t max_wgs);
+hipError_t vx_launch_argmax_finalize(const float* cand_v, const uint32_t* cand_i, uint32_t n, VeloxDecodeState* state,
+                                     uint32_t* ring, const uint32_t* prompt, const uint32_t* prompt_len,
+                                     uint32_t* token_out, uint64_t mask, hipStream_t st);

@@ -52,17 +52,19 @@ struct VeloxHipModel {
 
 namespace {
 
-// Lanes per row S: the largest of {32, 16, 8, 4} whose padding of the last iteration wastes at
-// most 1/8 of the lanes, else the one wasting least. Padding costs memory, never HBM bandwidth:
-// padded blocks are not loaded.
+// Lanes per row S: the largest of {32, 16, 8, 4} that tiles a row's blocks exactly, else the
+// largest wasting at most 1/32 of a row, else the one wasting least. Padded blocks are zero and
+// are streamed with the rest, so waste costs bandwidth as well as memory.
 uint32_t vx_choose_s(uint32_t nb) {
     const uint32_t cand[4] = {32, 16, 8, 4};
+    for (uint32_t s : cand)
+        if (nb % s == 0) return s;
     uint32_t best = 4;
     double best_w = 2.0;
     for (uint32_t s : cand) {
         const uint32_t it = (nb + s - 1) / s;
         const double waste = (double)(it * s - nb) / (double)(it * s);
-        if (waste <= 0.125) return s;
+        if (waste <= 1.0 / 32.0) return s;
         if (waste < best_w) { best_w = waste; best = s; }
     }
     return best;
@@ -124,7 +126,7 @@ bool vx_shape_ok(const VeloxHipModelConfig& c) {
     if (c.head_dim == 128 && !(G == 1 || G == 2 || G == 4 || G == 7 || G == 8)) return false;
     if (((uint64_t)c.num_heads * c.head_dim) % 32) return false;
     if (c.quant_mode != VELOX_QUANT_GGML_Q4_0) return false;
-    if (c.num_kv_heads > 64) return false;
+    if (c.num_kv_heads > 64 || c.attn_splits > 64) return false;
     if (c.hidden_dim > 32768 || c.intermediate_dim > 32768 || (uint64_t)c.num_heads * c.head_dim > 32768) return false;
     return true;
 }
@@ -236,11 +238,12 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
     M->kv_layer_bytes = vx_align((uint64_t)2 * c.num_kv_heads * c.max_seq_len * D * 2);
     M->kv_bytes = M->kv_layer_bytes * c.num_layers;
 
+    // Split-K over the sequence only for long contexts: up to 1024 positions one workgroup per KV
+    // head covers the history without a cross-workgroup merge.
     uint32_t splits = c.attn_splits;
     if (!splits) {
-        splits = (c.max_seq_len + 31) / 32;
+        splits = c.max_seq_len <= 1024 ? 1u : (c.max_seq_len + 255) / 256;
         if (splits > 64) splits = 64;
-        if (splits < 1) splits = 1;
     }
     M->splits = splits;
     M->max_wgs = vx_gemv_max_wgs_default();
@@ -260,8 +263,8 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
     M->a_logits = take((uint64_t)c.vocab_size * 4);
     M->a_part_o = take((uint64_t)c.num_heads * splits * D * 4);
     M->a_part_ml = take((uint64_t)c.num_heads * splits * 2 * 4);
-    M->a_cand_v = take((uint64_t)M->max_wgs * 4);
-    M->a_cand_i = take((uint64_t)M->max_wgs * 4);
+    M->a_cand_v = take((uint64_t)65536 * 4);
+    M->a_cand_i = take((uint64_t)65536 * 4);
     M->act_bytes = ac;
 
     const uint64_t budget = c.vram_budget_bytes ? c.vram_budget_bytes : 288ULL * 1000 * 1000 * 1000;
@@ -633,13 +636,10 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
     g.y = (float*)(act + M->a_logits);
     g.cand_v = (float*)(act + M->a_cand_v);
     g.cand_i = (uint32_t*)(act + M->a_cand_i);
-    g.counter = (uint32_t*)(act + M->a_argmax_counter);
-    g.state = state;
-    g.ring = A->host_pinned_ring;
-    g.prompt = (const uint32_t*)(act + M->a_prompt);
-    g.prompt_len = (const uint32_t*)(act + M->a_plen);
-    g.token_out = (uint32_t*)(act + M->a_token);
     vx_record(vx_launch_gemv(vx_view(A, M->head), g, VX_EPI_ARGMAX, M->max_wgs, st));
+    vx_record(vx_launch_argmax_finalize(g.cand_v, g.cand_i, vx_gemv_grid(M->head.n_tiles, M->max_wgs), state,
+                                        A->host_pinned_ring, (const uint32_t*)(act + M->a_prompt),
+                                        (const uint32_t*)(act + M->a_plen), (uint32_t*)(act + M->a_token), mask, st));
 }
 
 void velox_hip_decode(VeloxHipArena* A, uint32_t token_in, size_t step, uint64_t mask, hipStream_t st) {
@@ -739,11 +739,11 @@ int velox_hip_lm_head_argmax(const VeloxHipQ4Matrix* m, const float* d_x, const 
     if (!m || !d_x || !d_logits || !d_token || m->paired) return VELOX_HIP_EINVAL;
     // scratch for candidates + counter, reused across calls on this device
     static void* scratch = nullptr;
-    const uint32_t wgs = vx_gemv_max_wgs_default();
+    const uint32_t wgs = vx_gemv_max_wgs_default(), cap = 65536;
     if (!scratch) {
-        hipError_t e = hipMalloc(&scratch, (size_t)wgs * 8 + 256);
+        hipError_t e = hipMalloc(&scratch, (size_t)cap * 8 + 256);
         if (e != hipSuccess) return (int)e;
-        e = hipMemset(scratch, 0, (size_t)wgs * 8 + 256);
+        e = hipMemset(scratch, 0, (size_t)cap * 8 + 256);
         if (e != hipSuccess) return (int)e;
     }
     VxGemvArgs g;
@@ -753,11 +753,13 @@ int velox_hip_lm_head_argmax(const VeloxHipQ4Matrix* m, const float* d_x, const 
     g.eps = eps;
     g.y = d_logits;
     g.cand_v = (float*)scratch;
-    g.cand_i = (uint32_t*)((uint8_t*)scratch + (size_t)wgs * 4);
-    g.counter = (uint32_t*)((uint8_t*)scratch + (size_t)wgs * 8);
-    g.token_out = d_token;
+    g.cand_i = (uint32_t*)((uint8_t*)scratch + (size_t)cap * 4);
     g.active_mask = 1;
-    return (int)vx_launch_gemv(vx_view_public(m), g, VX_EPI_ARGMAX, wgs, st);
+    hipError_t e = vx_launch_gemv(vx_view_public(m), g, VX_EPI_ARGMAX, wgs, st);
+    if (e == hipSuccess)
+        e = vx_launch_argmax_finalize(g.cand_v, g.cand_i, vx_gemv_grid(m->n_tiles, wgs), nullptr, nullptr, nullptr,
+                                      nullptr, d_token, 1, st);
+    return (int)e;
 }
 
 int velox_hip_argmax_f32(const float* d_x, uint32_t n, uint32_t* d_out, hipStream_t st) {
@@ -774,7 +776,7 @@ int velox_hip_attention_decode(const float* d_qkv, uint16_t* d_kv_layer, uint32_
                                uint32_t s_max, uint32_t pos, float theta, uint32_t splits, float* d_out,
                                hipStream_t st) {
     if (!d_qkv || !d_kv_layer || !d_out || hkv == 0 || hkv > 64 || hq % hkv || pos >= s_max || splits == 0 ||
-        splits > 256)
+        splits > 64)
         return VELOX_HIP_EINVAL;
     // rope row for `pos`, partials and counters: per-call scratch (test entry point)
     const uint32_t half = d / 2;

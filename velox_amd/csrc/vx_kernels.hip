@@ -14,6 +14,8 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+
 #include "vx_common.h"
 
 typedef _Float16 vx_h2 __attribute__((ext_vector_type(2)));
@@ -22,24 +24,45 @@ typedef uint32_t vx_u32x4 __attribute__((ext_vector_type(4)));
 namespace {
 
 constexpr int kWG = 256;  // threads per workgroup (4 wave64)
-constexpr int kU = 8;     // GEMV iterations in flight per lane (8 x 16 B)
+
 
 __device__ __forceinline__ float vx_h2f(uint32_t h) { return __half2float(__ushort_as_half((unsigned short)h)); }
 
-// 8 weights of one code dword against 8 fp16 activations (4 half2). Nibble p of the low half
-// holds element 2p, nibble p of the high half element 2p+1, so (h_p.x, h_p.y) = 1024 + q for the
-// consecutive pair (x[2p], x[2p+1]).
+// Code dword layout (8 weights): byte j holds element j in its low nibble and element j + 4 in
+// its high nibble. v_perm_b32 places two nibble bytes under the fp16 exponent byte 0x64, giving
+// half2 (1024 + q_a, 1024 + q_b) for consecutive elements, consumed by v_dot2c_f32_f16 against the
+// matching fp16 activation pair; the -1032 offset is folded into the block correction.
+__device__ __forceinline__ uint32_t vx_code_nibble(uint32_t dw, int e) { return (dw >> (8 * (e & 3) + 4 * (e >> 2))) & 15u; }
+
 __device__ __forceinline__ float vx_dot8(uint32_t q, uint4 xq, float acc) {
-    const uint32_t m = 0x000F000Fu, bias = 0x64006400u;
-    const uint32_t h0 = (q & m) | bias;
-    const uint32_t h1 = ((q >> 4) & m) | bias;
-    const uint32_t h2 = ((q >> 8) & m) | bias;
-    const uint32_t h3 = ((q >> 12) & m) | bias;
+    const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+    const uint32_t c64 = 0x64646464u;
+    const uint32_t h0 = __builtin_amdgcn_perm(c64, lo, 0x04010400u);  // elements 0, 1
+    const uint32_t h1 = __builtin_amdgcn_perm(c64, lo, 0x04030402u);  // elements 2, 3
+    const uint32_t h2 = __builtin_amdgcn_perm(c64, hi, 0x04010400u);  // elements 4, 5
+    const uint32_t h3 = __builtin_amdgcn_perm(c64, hi, 0x04030402u);  // elements 6, 7
     acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, h0), __builtin_bit_cast(vx_h2, xq.x), acc, false);
     acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, h1), __builtin_bit_cast(vx_h2, xq.y), acc, false);
     acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, h2), __builtin_bit_cast(vx_h2, xq.z), acc, false);
     acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, h3), __builtin_bit_cast(vx_h2, xq.w), acc, false);
     return acc;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float vx_dpp(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over aligned groups of S lanes (S in 2..64): DPP within 16-lane rows, a swizzle across rows.
+template <int S>
+__device__ __forceinline__ float vx_group_sum(float v) {
+    if constexpr (S >= 2) v += vx_dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    if constexpr (S >= 4) v += vx_dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    if constexpr (S >= 8) v += vx_dpp<0x141>(v);  // row_half_mirror
+    if constexpr (S >= 16) v += vx_dpp<0x140>(v); // row_mirror
+    if constexpr (S >= 32) v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+    if constexpr (S >= 64) v += __shfl_xor(v, 32);
+    return v;
 }
 
 __device__ __forceinline__ float vx_wave_sum(float v) {
@@ -59,14 +82,18 @@ __device__ __forceinline__ bool vx_better(float v, uint32_t i, float bv, uint32_
     return v > bv || (v == bv && i < bi);
 }
 
-// Block-wide sum over 256 threads; red must hold 4 floats. Result broadcast to all threads.
+// Block-wide sum over W waves; red must hold W floats. Result broadcast to all threads.
+template <int W>
 __device__ __forceinline__ float vx_block_sum(float v, float* red) {
     v = vx_wave_sum(v);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     __syncthreads();
     if (lane == 0) red[wave] = v;
     __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) t += red[w];
+    return t;
 }
 
 // Places one GGML Q4_0 block (scale bits d, 16 bytes qs: element j low nibble of qs[j],
@@ -78,11 +105,10 @@ __device__ __forceinline__ void vx_store_tiled_block(const VxMat& m, uint32_t ph
     for (int w = 0; w < 4; ++w) {
         uint32_t v = 0;
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const int e0 = 8 * w + 2 * p, e1 = e0 + 1;
-            const uint32_t q0 = e0 < 16 ? (qs[e0] & 15u) : (qs[e0 - 16] >> 4);
-            const uint32_t q1 = e1 < 16 ? (qs[e1] & 15u) : (qs[e1 - 16] >> 4);
-            v |= (q0 << (4 * p)) | (q1 << (16 + 4 * p));
+        for (int e = 0; e < 8; ++e) {
+            const int el = 8 * w + e;
+            const uint32_t q = el < 16 ? (qs[el] & 15u) : (qs[el - 16] >> 4);
+            v |= q << (8 * (e & 3) + 4 * (e >> 2));
         }
         dw[w] = v;
     }
@@ -139,29 +165,81 @@ __device__ __forceinline__ float vx_normal_value(uint64_t stream, uint64_t idx, 
 // =============================================================================================
 // Fused Q4_0 GEMV
 // =============================================================================================
-template <int S, int EPI>
-__global__ __launch_bounds__(kWG) void vx_gemv_q4_kernel(VxGemvArgs a) {
+// Each wave streams the code words of its tiles as one flat sequence of items (tile, iteration):
+// kU 16-byte loads stay in flight per lane across tile boundaries, and the first kU are issued
+// before the prologue, so that staging the activations in LDS overlaps the weight fetch. Tiles go
+// to waves round-robin over the grid (a.contig == 0) or in contiguous runs (a.contig == 1).
+// No workgroup waits on another: the LM head's argmax leaves one candidate per workgroup for
+// vx_argmax_finalize_kernel (a release fence per workgroup costs a full L2 write-back on gfx950).
+template <int S, int EPI, int W, int kU>
+__global__ __launch_bounds__(64 * W) void vx_gemv_q4_kernel(VxGemvArgs a) {
     extern __shared__ __align__(16) unsigned char vx_smem[];
     if ((a.active_mask & 1ULL) == 0ULL) return;
-    constexpr int R = 64 / S;
-    const uint32_t K = a.k, nb = K >> 5;
-    __half* xs = (__half*)vx_smem;
+    constexpr int R = 64 / S, NT = 64 * W;
+    const uint32_t K = a.k, nb = K >> 5, n_iter = a.n_iter;
+    uint4* xs4 = (uint4*)vx_smem;  // fp16 activations: 4 planes of nb 16-byte chunks
     float* corr = (float*)(vx_smem + (size_t)K * 2u);
     float* red = corr + nb;
-    const int tid = threadIdx.x;
+    // the wave index is uniform: readfirstlane lets every per-wave quantity live in SGPRs
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane / S, s = lane % S;
+    const uint32_t waves_total = gridDim.x * W, gw = blockIdx.x * W + wave;
+    uint32_t first, step, my_tiles;
+    if (a.contig) {
+        const uint32_t per = (a.n_tiles + waves_total - 1u) / waves_total;
+        first = gw * per;
+        step = 1u;
+        my_tiles = first < a.n_tiles ? min(per, a.n_tiles - first) : 0u;
+    } else {
+        first = gw;
+        step = waves_total;
+        my_tiles = first < a.n_tiles ? (a.n_tiles - 1u - first) / waves_total + 1u : 0u;
+    }
+    const uint32_t total = my_tiles * n_iter;
+
+    auto row_of = [&](uint32_t t) -> uint32_t {
+        if constexpr (EPI == VX_EPI_SWIGLU) return t * (R / 2) + (r % (R / 2));  // logical j of gate/up
+        else return t * R + r;
+    };
+    // Code words and scales through buffer descriptors: per-lane offsets are constant, the item
+    // offset is wave-uniform (scalar). Padded slots of a tile hold zero codes and zero scales, so
+    // they are loaded and contribute exactly 0 without any per-lane branch.
+    const __amdgpu_buffer_rsrc_t rc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.codes, (short)0, (int)(a.n_tiles * n_iter * 1024u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.scales, (short)0, (int)(a.n_tiles * n_iter * 128u), 0x00020000);
+    const uint32_t lane16 = (uint32_t)lane * 16u, lane2 = (uint32_t)lane * 2u;
+    vx_u32x4 buf[kU];
+    uint32_t sbuf[kU];
+    uint32_t nt = 0, ni = 0, nslot = first * n_iter;  // next item: tile index, iteration, 64-lane slot
+    auto issue = [&](int u) {
+        if (nt < my_tiles) {
+            buf[u] = __builtin_amdgcn_raw_buffer_load_b128(rc, lane16, nslot * 1024u, 2);
+            sbuf[u] = __builtin_amdgcn_raw_buffer_load_b16(rsc, lane2, nslot * 128u, 2);
+        }
+        if (++ni == n_iter) {
+            ni = 0;
+            ++nt;
+            nslot = (first + nt * step) * n_iter;
+        } else {
+            ++nslot;
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < kU; ++u) issue(u);
 
     // ---- prologue: optional RMSNorm scale (src/runtime.rs:588-601), x -> fp16 in LDS ----
     float inv_rms = 1.0f;
     if (a.gain) {
         float ss = 0.0f;
-        for (uint32_t i = (uint32_t)tid * 4u; i < K; i += kWG * 4u) {
+        for (uint32_t i = (uint32_t)tid * 4u; i < K; i += NT * 4u) {
             const float4 v = *(const float4*)(a.x + i);
             ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         }
-        ss = vx_block_sum(ss, red + 4);
+        ss = vx_block_sum<W>(ss, red);
         inv_rms = 1.0f / sqrtf(ss / (float)K + a.eps);
     }
-    for (uint32_t g = tid; g < (K >> 3); g += kWG) {
+    for (uint32_t g = tid; g < (K >> 3); g += NT) {
         float4 v0 = *(const float4*)(a.x + 8u * g);
         float4 v1 = *(const float4*)(a.x + 8u * g + 4u);
         if (a.gain) {
@@ -174,89 +252,69 @@ __global__ __launch_bounds__(kWG) void vx_gemv_q4_kernel(VxGemvArgs a) {
         }
         const __half h[8] = {__float2half(v0.x), __float2half(v0.y), __float2half(v0.z), __float2half(v0.w),
                              __float2half(v1.x), __float2half(v1.y), __float2half(v1.z), __float2half(v1.w)};
-        *(uint4*)(xs + 8u * g) = *(const uint4*)h;
-        float s = 0.0f;
+        // plane-major [w][b]: the S lanes of a row read blocks b..b+S-1 of one plane at consecutive
+        // 16-byte addresses (no LDS bank conflicts)
+        xs4[(g & 3u) * nb + (g >> 2)] = *(const uint4*)h;
+        float sum = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s += __half2float(h[e]);
+        for (int e = 0; e < 8; ++e) sum += __half2float(h[e]);
         // the four 8-element groups of one 32-block sit in four consecutive lanes
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
-        if ((g & 3u) == 0u) corr[g >> 2] = -1032.0f * s;
+        sum += __shfl_xor(sum, 1);
+        sum += __shfl_xor(sum, 2);
+        if ((g & 3u) == 0u) corr[g >> 2] = -1032.0f * sum;
     }
     __syncthreads();
 
-    // ---- main loop: wave-per-tile, lanes stream 16-byte code words ----
-    const int lane = tid & 63, wave = tid >> 6;
-    const int r = lane / S, s = lane % S;
+    // ---- stream: consume slot u, refill it with the item kU ahead, finish tiles on the fly ----
     float best_v = -INFINITY;
     uint32_t best_i = 0xFFFFFFFFu;
-    const uint32_t waves_total = gridDim.x * (kWG / 64);
-    for (uint32_t tile = blockIdx.x * (kWG / 64) + wave; tile < a.n_tiles; tile += waves_total) {
-        uint32_t row;
-        bool row_ok;
-        if constexpr (EPI == VX_EPI_SWIGLU) {
-            row = tile * (R / 2) + (r % (R / 2));  // logical j of this lane's gate/up row
-            row_ok = row < a.n;                    // a.n = F for paired matrices
-        } else {
-            row = tile * R + r;
-            row_ok = row < a.n;
-        }
-        const size_t base = (size_t)tile * a.n_iter * 64u + lane;
-        float acc = 0.0f;
-        for (uint32_t i0 = 0; i0 < a.n_iter; i0 += kU) {
-            uint4 c[kU];
-            uint32_t dsc[kU];
+    float acc = 0.0f;
+    uint32_t ct = 0, ci = 0;  // current item
+    for (uint32_t f0 = 0; f0 < total; f0 += kU) {
 #pragma unroll
-            for (int u = 0; u < kU; ++u) {
-                const uint32_t i = i0 + u, b = i * S + s;
-                if (i < a.n_iter && b < nb && row_ok) {
-                    const vx_u32x4 cv = __builtin_nontemporal_load((const vx_u32x4*)a.codes + base + (size_t)i * 64u);
-                    c[u] = make_uint4(cv.x, cv.y, cv.z, cv.w);
-                    dsc[u] = __builtin_nontemporal_load((const unsigned short*)a.scales + base + (size_t)i * 64u);
-                } else {
-                    c[u] = make_uint4(0, 0, 0, 0);
-                    dsc[u] = 0;
+        for (int u = 0; u < kU; ++u) {
+            if (f0 + u < total) {
+                // padded blocks (b >= nb, zero scale) read a valid activation chunk instead
+                const uint32_t b = min(ci * S + s, nb - 1u);
+                const vx_u32x4 c = buf[u];
+                float dot = corr[b];
+                dot = vx_dot8(c.x, xs4[b], dot);
+                dot = vx_dot8(c.y, xs4[nb + b], dot);
+                dot = vx_dot8(c.z, xs4[2u * nb + b], dot);
+                dot = vx_dot8(c.w, xs4[3u * nb + b], dot);
+                acc = fmaf(vx_h2f(sbuf[u]), dot, acc);
+                issue(u);
+                if (++ci == n_iter) {
+                    acc = vx_group_sum<S>(acc);
+                    const uint32_t row = row_of(first + ct * step);
+                    const bool row_ok = row < a.n;
+                    if constexpr (EPI == VX_EPI_STORE) {
+                        if (s == 0 && row_ok) a.y[row] = a.bias ? acc + a.bias[row] : acc;
+                    } else if constexpr (EPI == VX_EPI_RESID) {
+                        if (s == 0 && row_ok) a.y[row] = a.res[row] + acc;
+                    } else if constexpr (EPI == VX_EPI_SWIGLU) {
+                        const float up = __shfl_down(acc, 32);  // partner up row is 32 lanes above
+                        if (s == 0 && r < R / 2 && row_ok) {
+                            const float gt = acc;
+                            a.y[row] = (gt / (1.0f + expf(-gt))) * up;  // src/runtime.rs:1064-1066
+                        }
+                    } else {  // VX_EPI_ARGMAX
+                        if (s == 0 && row_ok) {
+                            a.y[row] = acc;
+                            if (vx_better(acc, row, best_v, best_i)) { best_v = acc; best_i = row; }
+                        }
+                    }
+                    acc = 0.0f;
+                    ci = 0;
+                    ++ct;
                 }
-            }
-#pragma unroll
-            for (int u = 0; u < kU; ++u) {
-                const uint32_t i = i0 + u, b = i * S + s;
-                if (i < a.n_iter && b < nb && row_ok) {
-                    const uint4* xq = (const uint4*)(xs + b * 32u);
-                    float dot = corr[b];
-                    dot = vx_dot8(c[u].x, xq[0], dot);
-                    dot = vx_dot8(c[u].y, xq[1], dot);
-                    dot = vx_dot8(c[u].z, xq[2], dot);
-                    dot = vx_dot8(c[u].w, xq[3], dot);
-                    acc = fmaf(vx_h2f(dsc[u]), dot, acc);
-                }
-            }
-        }
-#pragma unroll
-        for (int off = S / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-
-        if constexpr (EPI == VX_EPI_STORE) {
-            if (s == 0 && row_ok) a.y[row] = a.bias ? acc + a.bias[row] : acc;
-        } else if constexpr (EPI == VX_EPI_RESID) {
-            if (s == 0 && row_ok) a.y[row] = a.res[row] + acc;
-        } else if constexpr (EPI == VX_EPI_SWIGLU) {
-            const float up = __shfl_down(acc, 32);  // partner up row is 32 lanes above
-            if (s == 0 && r < R / 2 && row_ok) {
-                const float g = acc;
-                a.y[row] = (g / (1.0f + expf(-g))) * up;  // src/runtime.rs:1064-1066
-            }
-        } else {  // VX_EPI_ARGMAX
-            if (s == 0 && row_ok) {
-                a.y[row] = acc;
-                if (vx_better(acc, row, best_v, best_i)) { best_v = acc; best_i = row; }
             }
         }
     }
 
     if constexpr (EPI == VX_EPI_ARGMAX) {
-        __shared__ float s_v[4];
-        __shared__ uint32_t s_i[4];
-        __shared__ int s_last;
+        __shared__ float s_v[W];
+        __shared__ uint32_t s_i[W];
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) {
             const float ov = __shfl_xor(best_v, off);
@@ -268,71 +326,98 @@ __global__ __launch_bounds__(kWG) void vx_gemv_q4_kernel(VxGemvArgs a) {
         if (tid == 0) {
             float bv = s_v[0];
             uint32_t bi = s_i[0];
-            for (int w = 1; w < 4; ++w)
+            for (int w = 1; w < W; ++w)
                 if (vx_better(s_v[w], s_i[w], bv, bi)) { bv = s_v[w]; bi = s_i[w]; }
             a.cand_v[blockIdx.x] = bv;
             a.cand_i[blockIdx.x] = bi;
-            __threadfence();
-            const uint32_t prev = atomicAdd(a.counter, 1u);
-            s_last = (prev == gridDim.x - 1u);
         }
-        __syncthreads();
-        if (s_last) {
-            __threadfence();
-            float bv = -INFINITY;
-            uint32_t bi = 0xFFFFFFFFu;
-            for (uint32_t j = tid; j < gridDim.x; j += kWG) {
-                const float v = a.cand_v[j];
-                const uint32_t ii = a.cand_i[j];
-                if (vx_better(v, ii, bv, bi)) { bv = v; bi = ii; }
-            }
+    }
+}
+
+// Greedy token from the LM head's per-workgroup candidates (strict '>' scan semantics, lowest
+// index on ties), then the ring write and device-state advance of src/codegen.rs:1627-1677.
+__global__ __launch_bounds__(256) void vx_argmax_finalize_kernel(const float* cand_v, const uint32_t* cand_i,
+                                                                 uint32_t n, VeloxDecodeState* state, uint32_t* ring,
+                                                                 const uint32_t* prompt, const uint32_t* prompt_len,
+                                                                 uint32_t* token_out, uint64_t mask) {
+    if ((mask & 1ULL) == 0ULL) return;
+    __shared__ float s_v[4];
+    __shared__ uint32_t s_i[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (uint32_t j = tid; j < n; j += 256) {
+        const float v = cand_v[j];
+        const uint32_t ii = cand_i[j];
+        if (vx_better(v, ii, bv, bi)) { bv = v; bi = ii; }
+    }
 #pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                const float ov = __shfl_xor(bv, off);
-                const uint32_t oi = __shfl_xor(bi, off);
-                if (vx_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const uint32_t oi = __shfl_xor(bi, off);
+        if (vx_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) { s_v[wave] = bv; s_i[wave] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 4; ++w)
+            if (vx_better(s_v[w], s_i[w], s_v[0], s_i[0])) { s_v[0] = s_v[w]; s_i[0] = s_i[w]; }
+        // all-NaN or empty logits: token 0, as the reference's scan from -inf
+        const uint32_t win = s_i[0] == 0xFFFFFFFFu ? 0u : s_i[0];
+        if (token_out) *token_out = win;
+        if (state) {
+            const uint64_t step = state->step;
+            if (ring) {
+                __atomic_store_n(ring + (step & (VELOX_HIP_RING_SIZE - 1u)), win, __ATOMIC_RELAXED);
+                __threadfence_system();
             }
-            __syncthreads();
-            if (lane == 0) { s_v[wave] = bv; s_i[wave] = bi; }
-            __syncthreads();
-            if (tid == 0) {
-                for (int w = 1; w < 4; ++w)
-                    if (vx_better(s_v[w], s_i[w], s_v[0], s_i[0])) { s_v[0] = s_v[w]; s_i[0] = s_i[w]; }
-                // all-NaN or empty logits: token 0, as the reference's scan from -inf
-                const uint32_t win = s_i[0] == 0xFFFFFFFFu ? 0u : s_i[0];
-                if (a.token_out) *a.token_out = win;
-                if (a.state) {
-                    // src/codegen.rs:1666-1676: ring write, then device state advance
-                    const uint64_t step = a.state->step;
-                    if (a.ring) {
-                        __atomic_store_n(a.ring + (step & (VELOX_HIP_RING_SIZE - 1u)), win, __ATOMIC_RELAXED);
-                        __threadfence_system();
-                    }
-                    const uint32_t plen = a.prompt_len ? *a.prompt_len : 0u;
-                    const uint32_t next = (step + 1u < (uint64_t)plen) ? a.prompt[step + 1u] : win;
-                    a.state->token = next;
-                    a.state->step = step + 1u;
-                }
-                *a.counter = 0u;
-            }
+            const uint32_t plen = prompt_len ? *prompt_len : 0u;
+            const uint32_t next = (step + 1u < (uint64_t)plen) ? prompt[step + 1u] : win;
+            state->token = next;
+            state->step = step + 1u;
         }
     }
 }
 
 // =============================================================================================
-// Split-K decode attention with RoPE + KV append prologue and last-workgroup LSE merge.
+// Split-K decode attention: RoPE + bf16 KV append prologue, per-lane-group online softmax over
+// coalesced 16-byte K/V rows, LSE merge within the workgroup, then across splits by the last
+// workgroup of each KV head.
 // =============================================================================================
-template <int D, int G>
-__global__ __launch_bounds__(kWG) void vx_attn_kernel(VxAttnArgs a) {
+namespace {
+__device__ __forceinline__ float vx_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Merge softmax state (m, l, o[8]) with a partner's, all in the log2 domain.
+template <int G>
+__device__ __forceinline__ void vx_merge_state(float (&m)[G], float (&l)[G], float (&o)[G][8], int off) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        const float m2 = __shfl_xor(m[h], off), l2 = __shfl_xor(l[h], off);
+        const float mn = fmaxf(m[h], m2);
+        const float w1 = (m[h] == -INFINITY) ? 0.0f : vx_exp2(m[h] - mn);
+        const float w2 = (m2 == -INFINITY) ? 0.0f : vx_exp2(m2 - mn);
+        l[h] = l[h] * w1 + l2 * w2;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float o2 = __shfl_xor(o[h][e], off);
+            o[h][e] = o[h][e] * w1 + o2 * w2;
+        }
+        m[h] = mn;
+    }
+}
+}  // namespace
+
+template <int D, int G, int W>
+__global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     if ((a.active_mask & 1ULL) == 0ULL) return;
-    constexpr int HALF = D / 2, TG = kWG / D;
+    constexpr int HALF = D / 2, LPP = D / 8, PPW = 64 / LPP, NT = 64 * W;  // lanes per position, positions/wave step
+    constexpr int PF = 8;  // positions in flight per lane group
+    constexpr float kLog2e = 1.4426950408889634f;
     __shared__ float q_s[G * D];
-    __shared__ float kn[D], vn[D];
-    __shared__ float p_s[G][kWG];
-    __shared__ float red[G][4];
-    __shared__ float o_red[TG > 1 ? TG - 1 : 1][G * D];
-    __shared__ int s_last;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ __align__(16) uint16_t kn_s[D], vn_s[D];
+    __shared__ float w_m[W][G], w_l[W][G];
+    __shared__ float w_o[W][G * D];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t g = blockIdx.y, sp = blockIdx.x;
     const uint64_t step = a.state ? a.state->step : (uint64_t)a.fixed_pos;
     const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;  // safe_step clamp
@@ -340,164 +425,160 @@ __global__ __launch_bounds__(kWG) void vx_attn_kernel(VxAttnArgs a) {
     const uint32_t chunk = (len + a.splits - 1u) / a.splits;
     const uint32_t t0 = sp * chunk;
     const uint32_t t1 = min(len, t0 + chunk);
+    const int grp = lane / LPP, sub = lane % LPP;
+    uint16_t* Kc = a.kv + (size_t)g * a.s_max * D;
+    uint16_t* Vc = a.kv + ((size_t)a.hkv + g) * a.s_max * D;
+    const uint32_t wstep = (uint32_t)(W * PPW);
 
+    // ---- cached K/V rows (positions < pos) of the first batch, issued before the prologue ----
+    uint4 kr[PF], vr[PF];
+    auto fetch = [&](uint32_t tb) {
+#pragma unroll
+        for (int j = 0; j < PF; ++j) {
+            const uint32_t t = tb + j * wstep + (uint32_t)(wave * PPW + grp);
+            if (t < t1 && t != pos) {
+                kr[j] = *(const uint4*)(Kc + (size_t)t * D + 8 * sub);
+                vr[j] = *(const uint4*)(Vc + (size_t)t * D + 8 * sub);
+            }
+        }
+    };
+    fetch(t0);
+
+    // ---- RoPE (src/runtime.rs:745-768) on this group's q heads and the new k; bf16 K/V row ----
     const float* q = a.qkv;
     const float* k = a.qkv + (size_t)a.hq * D;
     const float* v = k + (size_t)a.hkv * D;
     const float2* rp = a.rope + (size_t)pos * HALF;
-    // rotate-half RoPE (src/runtime.rs:745-768) on this group's q heads and the new k
-    for (int p = tid; p < (G + 1) * HALF; p += kWG) {
+    for (int p = tid; p < (G + 1) * HALF; p += NT) {
         const int hh = p / HALF, j = p % HALF;
         const float* src = hh < G ? q + (size_t)(g * G + hh) * D : k + (size_t)g * D;
         const float2 o = vx_rope_pair(src[j], src[j + HALF], rp[j]);
-        const float o1 = o.x, o2 = o.y;
         if (hh < G) {
-            q_s[hh * D + j] = o1;
-            q_s[hh * D + j + HALF] = o2;
+            q_s[hh * D + j] = o.x;
+            q_s[hh * D + j + HALF] = o.y;
         } else {
-            kn[j] = vx_bf16_bits_to_f32(vx_f32_to_bf16_bits(o1));
-            kn[j + HALF] = vx_bf16_bits_to_f32(vx_f32_to_bf16_bits(o2));
+            kn_s[j] = vx_f32_to_bf16_bits(o.x);
+            kn_s[j + HALF] = vx_f32_to_bf16_bits(o.y);
         }
     }
-    for (int d = tid; d < D; d += kWG) vn[d] = vx_bf16_bits_to_f32(vx_f32_to_bf16_bits(v[(size_t)g * D + d]));
+    for (int d = tid; d < D; d += NT) vn_s[d] = vx_f32_to_bf16_bits(v[(size_t)g * D + d]);
     __syncthreads();
-
-    uint16_t* Kc = a.kv + (size_t)g * a.s_max * D;
-    uint16_t* Vc = a.kv + ((size_t)a.hkv + g) * a.s_max * D;
     if (sp == 0) {
-        for (int d = tid; d < D; d += kWG) {
-            Kc[(size_t)pos * D + d] = (uint16_t)(__builtin_bit_cast(uint32_t, kn[d]) >> 16);
-            Vc[(size_t)pos * D + d] = (uint16_t)(__builtin_bit_cast(uint32_t, vn[d]) >> 16);
+        for (int d = tid; d < D; d += NT) {
+            Kc[(size_t)pos * D + d] = kn_s[d];
+            Vc[(size_t)pos * D + d] = vn_s[d];
         }
     }
 
-    float m_run[G], l_run[G], o_acc[G];
+    // ---- scores and online softmax: lane group grp handles one position per step ----
+    const float qscale = a.scale * kLog2e;
+    float qv[G][8];
 #pragma unroll
-    for (int h = 0; h < G; ++h) { m_run[h] = -INFINITY; l_run[h] = 0.0f; o_acc[h] = 0.0f; }
-    const int pd = tid % D, ptg = tid / D;
-
-    for (uint32_t tt0 = t0; tt0 < t1; tt0 += kWG) {
-        const uint32_t t = tt0 + tid;
-        const bool valid = t < t1;
-        float sc[G];
+    for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int h = 0; h < G; ++h) sc[h] = 0.0f;
-        if (valid) {
-            if (t == pos) {
-                for (int d = 0; d < D; ++d) {
-                    const float kv = kn[d];
+        for (int e = 0; e < 8; ++e) qv[h][e] = q_s[h * D + 8 * sub + e];
+    float m[G], l[G], o[G][8];
 #pragma unroll
-                    for (int h = 0; h < G; ++h) sc[h] += q_s[h * D + d] * kv;
-                }
-            } else {
-                const uint4* krow = (const uint4*)(Kc + (size_t)t * D);
-                for (int c8 = 0; c8 < D / 8; ++c8) {
-                    const uint4 w = krow[c8];
-                    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+    for (int h = 0; h < G; ++h) {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float k0 = __builtin_bit_cast(float, wv[e] << 16);
-                        const float k1 = __builtin_bit_cast(float, wv[e] & 0xFFFF0000u);
-                        const int d = c8 * 8 + 2 * e;
+        for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
+    }
+    for (uint32_t tb = t0; tb < t1; tb += PF * wstep) {
+        if (tb != t0) fetch(tb);
 #pragma unroll
-                        for (int h = 0; h < G; ++h) {
-                            sc[h] += q_s[h * D + d] * k0;
-                            sc[h] += q_s[h * D + d + 1] * k1;
-                        }
-                    }
+        for (int j = 0; j < PF; ++j) {
+            const uint32_t t = tb + j * wstep + (uint32_t)(wave * PPW + grp);
+            const bool valid = t < t1;
+            // the new position comes from LDS (it may not have reached memory yet)
+            const uint4 kq = (t == pos) ? *(const uint4*)(kn_s + 8 * sub) : kr[j];
+            const uint4 vq = (t == pos) ? *(const uint4*)(vn_s + 8 * sub) : vr[j];
+            const uint32_t kw[4] = {kq.x, kq.y, kq.z, kq.w};
+            const uint32_t vw[4] = {vq.x, vq.y, vq.z, vq.w};
+            float kf[8], vf[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                kf[2 * e] = __builtin_bit_cast(float, kw[e] << 16);
+                kf[2 * e + 1] = __builtin_bit_cast(float, kw[e] & 0xFFFF0000u);
+                vf[2 * e] = __builtin_bit_cast(float, vw[e] << 16);
+                vf[2 * e + 1] = __builtin_bit_cast(float, vw[e] & 0xFFFF0000u);
+            }
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                float sc = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sc += qv[h][e] * kf[e];
+                sc = vx_group_sum<LPP>(sc) * qscale;
+                if (valid) {
+                    const float mn = fmaxf(m[h], sc);
+                    const float alpha = (m[h] == -INFINITY) ? 0.0f : vx_exp2(m[h] - mn);
+                    const float p = vx_exp2(sc - mn);
+                    l[h] = l[h] * alpha + p;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) o[h][e] = o[h][e] * alpha + p * vf[e];
+                    m[h] = mn;
                 }
             }
         }
-        // tile max per head
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            sc[h] = valid ? sc[h] * a.scale : -INFINITY;
-            const float wm = vx_wave_max(sc[h]);
-            if (lane == 0) red[h][wave] = wm;
-        }
-        __syncthreads();
-        float alpha[G], mnew[G];
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            const float tm = fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3]));
-            mnew[h] = fmaxf(m_run[h], tm);
-            alpha[h] = (m_run[h] == -INFINITY) ? 0.0f : expf(m_run[h] - mnew[h]);
-            const float p = valid ? expf(sc[h] - mnew[h]) : 0.0f;
-            p_s[h][tid] = p;
-            sc[h] = p;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            const float ws = vx_wave_sum(sc[h]);
-            if (lane == 0) red[h][wave] = ws;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            l_run[h] = l_run[h] * alpha[h] + ((red[h][0] + red[h][1]) + (red[h][2] + red[h][3]));
-            m_run[h] = mnew[h];
-            o_acc[h] *= alpha[h];
-        }
-        // P.V: thread (pd, ptg) accumulates column pd over the tile positions ptg, ptg+TG, ...
-        const uint32_t ntile = min((uint32_t)kWG, t1 - tt0);
-        for (uint32_t tp = ptg; tp < ntile; tp += TG) {
-            const uint32_t tt = tt0 + tp;
-            const float vv = (tt == pos) ? vn[pd] : vx_bf16_bits_to_f32(Vc[(size_t)tt * D + pd]);
-#pragma unroll
-            for (int h = 0; h < G; ++h) o_acc[h] += p_s[h][tp] * vv;
-        }
-        __syncthreads();
     }
-    // combine the TG partial column sums
-    if (TG > 1) {
-        if (ptg > 0) {
+    // ---- merge: lane groups of a wave, then the W waves ----
 #pragma unroll
-            for (int h = 0; h < G; ++h) o_red[ptg - 1][h * D + pd] = o_acc[h];
-        }
-        __syncthreads();
-        if (ptg == 0) {
-            for (int gg = 1; gg < TG; ++gg)
-#pragma unroll
-                for (int h = 0; h < G; ++h) o_acc[h] += o_red[gg - 1][h * D + pd];
-        }
-    }
-    if (ptg == 0) {
+    for (int off = LPP; off < 64; off <<= 1) vx_merge_state<G>(m, l, o, off);
+    if (grp == 0) {
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            const size_t hq_idx = (size_t)g * G + h;
-            a.part_o[(hq_idx * a.splits + sp) * D + pd] = o_acc[h];
-            if (pd == 0) {
-                a.part_ml[(hq_idx * a.splits + sp) * 2] = m_run[h];
-                a.part_ml[(hq_idx * a.splits + sp) * 2 + 1] = l_run[h];
-            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) w_o[wave][h * D + 8 * sub + e] = o[h][e];
+            if (sub == 0) { w_m[wave][h] = m[h]; w_l[wave][h] = l[h]; }
         }
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = atomicAdd(a.counters + g, 1u);
-        s_last = (prev == a.splits - 1u);
     }
     __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    for (int idx = tid; idx < G * D; idx += kWG) {
+    for (int idx = tid; idx < G * D; idx += NT) {
         const int h = idx / D, d = idx % D;
-        const size_t hq_idx = (size_t)g * G + h;
-        float M = -INFINITY;
-        for (uint32_t j = 0; j < a.splits; ++j) M = fmaxf(M, a.part_ml[(hq_idx * a.splits + j) * 2]);
-        float L = 0.0f, O = 0.0f;
-        for (uint32_t j = 0; j < a.splits; ++j) {
-            const float mj = a.part_ml[(hq_idx * a.splits + j) * 2];
-            if (mj == -INFINITY) continue;
-            const float w = expf(mj - M);
-            L += a.part_ml[(hq_idx * a.splits + j) * 2 + 1] * w;
-            O += a.part_o[(hq_idx * a.splits + j) * D + d] * w;
+        float mn = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < W; ++w) mn = fmaxf(mn, w_m[w][h]);
+        float lsum = 0.0f, osum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float wt = (w_m[w][h] == -INFINITY) ? 0.0f : vx_exp2(w_m[w][h] - mn);
+            lsum += w_l[w][h] * wt;
+            osum += w_o[w][idx] * wt;
         }
-        a.out[hq_idx * D + d] = L > 0.0f ? O / L : 0.0f;
+        const size_t hq_idx = (size_t)g * G + h;
+        if (a.splits == 1) {
+            a.out[hq_idx * D + d] = lsum > 0.0f ? osum / lsum : 0.0f;
+        } else {
+            a.part_o[(hq_idx * a.splits + sp) * D + d] = osum;
+            if (d == 0) {
+                a.part_ml[(hq_idx * a.splits + sp) * 2] = mn;
+                a.part_ml[(hq_idx * a.splits + sp) * 2 + 1] = lsum;
+            }
+        }
     }
-    if (tid == 0) a.counters[g] = 0u;
+}
+
+// LSE merge of the split partials (m, l in the log2 domain) of one q head per workgroup.
+template <int D>
+__global__ __launch_bounds__(D) void vx_attn_merge_kernel(VxAttnArgs a) {
+    if ((a.active_mask & 1ULL) == 0ULL) return;
+    __shared__ float s_w[64];
+    const int tid = threadIdx.x;
+    const size_t h = blockIdx.x;
+    if (tid < 64) {
+        const float mj = tid < (int)a.splits ? a.part_ml[(h * a.splits + tid) * 2] : -INFINITY;
+        const float lj = tid < (int)a.splits ? a.part_ml[(h * a.splits + tid) * 2 + 1] : 0.0f;
+        const float M = vx_wave_max(mj);
+        const float wj = (mj == -INFINITY) ? 0.0f : vx_exp2(mj - M);
+        const float L = vx_wave_sum(lj * wj);
+        s_w[tid] = L > 0.0f ? wj / L : 0.0f;
+    }
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll 8
+    for (uint32_t j = 0; j < a.splits; ++j) acc += s_w[j] * a.part_o[(h * a.splits + j) * D + tid];
+    a.out[h * D + tid] = acc;
 }
 
 // =============================================================================================
@@ -518,10 +599,7 @@ __global__ __launch_bounds__(kWG) void vx_embed_kernel(VxMat m, const VeloxDecod
 #pragma unroll
     for (int w = 0; w < 4; ++w)
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            h[b * 32 + 8 * w + 2 * p] = (float)((int)((dw[w] >> (4 * p)) & 15u) - 8) * d;
-            h[b * 32 + 8 * w + 2 * p + 1] = (float)((int)((dw[w] >> (16 + 4 * p)) & 15u) - 8) * d;
-        }
+        for (int e = 0; e < 8; ++e) h[b * 32 + 8 * w + e] = (float)((int)vx_code_nibble(dw[w], e) - 8) * d;
 }
 
 __global__ void vx_set_state_kernel(VeloxDecodeState* s, uint64_t step, uint32_t token) {
@@ -596,10 +674,7 @@ __global__ __launch_bounds__(kWG) void vx_dequant_kernel(VxMat m, float* out) {
 #pragma unroll
     for (int w = 0; w < 4; ++w)
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            o[8 * w + 2 * p] = (float)((int)((dw[w] >> (4 * p)) & 15u) - 8) * d;
-            o[8 * w + 2 * p + 1] = (float)((int)((dw[w] >> (16 + 4 * p)) & 15u) - 8) * d;
-        }
+        for (int e = 0; e < 8; ++e) o[8 * w + e] = (float)((int)vx_code_nibble(dw[w], e) - 8) * d;
 }
 
 __global__ __launch_bounds__(kWG) void vx_quantize_kernel(const float* x, uint32_t rows, uint32_t k, uint8_t* blocks) {
@@ -621,7 +696,7 @@ __global__ __launch_bounds__(kWG) void vx_rmsnorm_kernel(const float* x, const f
     __shared__ float red[4];
     float ss = 0.0f;
     for (uint32_t i = threadIdx.x; i < n; i += kWG) ss += x[i] * x[i];
-    ss = vx_block_sum(ss, red);
+    ss = vx_block_sum<4>(ss, red);
     const float inv = 1.0f / sqrtf(ss / (float)n + eps);
     for (uint32_t i = threadIdx.x; i < n; i += kWG) y[i] = (x[i] * inv) * w[i];
 }
@@ -653,48 +728,84 @@ __global__ __launch_bounds__(kWG) void vx_argmax_kernel(const float* x, uint32_t
 // Launch helpers
 // =============================================================================================
 namespace {
-template <int S, int EPI>
+int vx_env_int(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e ? (int)strtol(e, nullptr, 10) : dflt;
+}
+
+template <int S, int EPI, int W, int KU>
 hipError_t vx_gemv_launch_t(const VxGemvArgs& a, uint32_t max_wgs, hipStream_t st) {
     const uint32_t nb = a.k >> 5;
     const size_t lds = (size_t)a.k * 2u + (size_t)nb * 4u + 64u;
     static size_t attr_lds = 64u * 1024u;
     if (lds > attr_lds) {
-        if (hipFuncSetAttribute((const void*)vx_gemv_q4_kernel<S, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        if (hipFuncSetAttribute((const void*)vx_gemv_q4_kernel<S, EPI, W, KU>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds) != hipSuccess) {
             (void)hipGetLastError();
             return hipErrorInvalidValue;
         }
         attr_lds = lds;
     }
-    uint32_t wgs = (a.n_tiles + 3u) / 4u;
+    uint32_t wgs = (a.n_tiles + W - 1u) / W;
     if (wgs > max_wgs) wgs = max_wgs;
     if (wgs == 0) wgs = 1;
-    hipLaunchKernelGGL((vx_gemv_q4_kernel<S, EPI>), dim3(wgs), dim3(kWG), lds, st, a);
+    hipLaunchKernelGGL((vx_gemv_q4_kernel<S, EPI, W, KU>), dim3(wgs), dim3(64 * W), lds, st, a);
     return hipGetLastError();
 }
 
-template <int EPI>
+template <int EPI, int W, int KU>
 hipError_t vx_gemv_dispatch_s(uint32_t s, const VxGemvArgs& a, uint32_t max_wgs, hipStream_t st) {
     switch (s) {
-        case 4: return vx_gemv_launch_t<4, EPI>(a, max_wgs, st);
-        case 8: return vx_gemv_launch_t<8, EPI>(a, max_wgs, st);
-        case 16: return vx_gemv_launch_t<16, EPI>(a, max_wgs, st);
-        case 32: return vx_gemv_launch_t<32, EPI>(a, max_wgs, st);
+        case 4: return vx_gemv_launch_t<4, EPI, W, KU>(a, max_wgs, st);
+        case 8: return vx_gemv_launch_t<8, EPI, W, KU>(a, max_wgs, st);
+        case 16: return vx_gemv_launch_t<16, EPI, W, KU>(a, max_wgs, st);
+        case 32: return vx_gemv_launch_t<32, EPI, W, KU>(a, max_wgs, st);
         case 64:
-            if constexpr (EPI != VX_EPI_SWIGLU) return vx_gemv_launch_t<64, EPI>(a, max_wgs, st);
+            if constexpr (EPI != VX_EPI_SWIGLU) return vx_gemv_launch_t<64, EPI, W, KU>(a, max_wgs, st);
             return hipErrorInvalidValue;
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int EPI, int W>
+hipError_t vx_gemv_dispatch_u(uint32_t ku, uint32_t s, const VxGemvArgs& a, uint32_t max_wgs, hipStream_t st) {
+    switch (ku) {
+        case 4: return vx_gemv_dispatch_s<EPI, W, 4>(s, a, max_wgs, st);
+        case 8: return vx_gemv_dispatch_s<EPI, W, 8>(s, a, max_wgs, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int EPI>
+hipError_t vx_gemv_dispatch_w(uint32_t w, uint32_t s, const VxGemvArgs& a, uint32_t max_wgs, hipStream_t st) {
+    const uint32_t ku = (uint32_t)vx_env_int("VELOX_HIP_GEMV_KU", 4);
+    switch (w) {
+        case 4: return vx_gemv_dispatch_u<EPI, 4>(ku, s, a, max_wgs, st);
+        case 8: return vx_gemv_dispatch_u<EPI, 8>(ku, s, a, max_wgs, st);
         default: return hipErrorInvalidValue;
     }
 }
 
 template <int D, int G>
 hipError_t vx_attn_launch_t(const VxAttnArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((vx_attn_kernel<D, G>), dim3(a.splits, a.hkv), dim3(kWG), 0, st, a);
-    return hipGetLastError();
+    constexpr int W = 8;
+    hipLaunchKernelGGL((vx_attn_kernel<D, G, W>), dim3(a.splits, a.hkv), dim3(64 * W), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && a.splits > 1) {
+        hipLaunchKernelGGL((vx_attn_merge_kernel<D>), dim3(a.hq), dim3(D), 0, st, a);
+        e = hipGetLastError();
+    }
+    return e;
 }
+
 }  // namespace
 
-uint32_t vx_gemv_max_wgs_default() { return 2048u; }
+// Upper bound on GEMV workgroups (waves loop over the remaining tiles); VELOX_HIP_GEMV_MAX_WGS
+// overrides it for tuning sweeps.
+uint32_t vx_gemv_max_wgs_default() {
+    const int v = vx_env_int("VELOX_HIP_GEMV_MAX_WGS", 0);
+    return (v > 0 && v <= 65536) ? (uint32_t)v : 512u;
+}
 
 hipError_t vx_launch_gemv(const VxMat& m, const VxGemvArgs& a0, int epi, uint32_t max_wgs, hipStream_t st) {
     VxGemvArgs a = a0;
@@ -704,19 +815,36 @@ hipError_t vx_launch_gemv(const VxMat& m, const VxGemvArgs& a0, int epi, uint32_
     a.k = m.k;
     a.n_tiles = m.n_tiles;
     a.n_iter = m.n_iter;
+    a.contig = (uint32_t)vx_env_int("VELOX_HIP_GEMV_CONTIG", 0);
+    const uint32_t w = (uint32_t)vx_env_int("VELOX_HIP_GEMV_WAVES", 8);
     if (m.k == 0 || (m.k & 31u) != 0) return hipErrorInvalidValue;
     if ((epi == VX_EPI_SWIGLU) != (m.paired != 0)) return hipErrorInvalidValue;
     switch (epi) {
-        case VX_EPI_STORE: return vx_gemv_dispatch_s<VX_EPI_STORE>(m.s, a, max_wgs, st);
-        case VX_EPI_RESID: return vx_gemv_dispatch_s<VX_EPI_RESID>(m.s, a, max_wgs, st);
-        case VX_EPI_SWIGLU: return vx_gemv_dispatch_s<VX_EPI_SWIGLU>(m.s, a, max_wgs, st);
-        case VX_EPI_ARGMAX: return vx_gemv_dispatch_s<VX_EPI_ARGMAX>(m.s, a, max_wgs, st);
+        case VX_EPI_STORE: return vx_gemv_dispatch_w<VX_EPI_STORE>(w, m.s, a, max_wgs, st);
+        case VX_EPI_RESID: return vx_gemv_dispatch_w<VX_EPI_RESID>(w, m.s, a, max_wgs, st);
+        case VX_EPI_SWIGLU: return vx_gemv_dispatch_w<VX_EPI_SWIGLU>(w, m.s, a, max_wgs, st);
+        case VX_EPI_ARGMAX: return vx_gemv_dispatch_w<VX_EPI_ARGMAX>(w, m.s, a, max_wgs, st);
         default: return hipErrorInvalidValue;
     }
 }
 
+hipError_t vx_launch_argmax_finalize(const float* cand_v, const uint32_t* cand_i, uint32_t n, VeloxDecodeState* state,
+                                     uint32_t* ring, const uint32_t* prompt, const uint32_t* prompt_len,
+                                     uint32_t* token_out, uint64_t mask, hipStream_t st) {
+    hipLaunchKernelGGL(vx_argmax_finalize_kernel, dim3(1), dim3(256), 0, st, cand_v, cand_i, n, state, ring, prompt,
+                       prompt_len, token_out, mask);
+    return hipGetLastError();
+}
+
+uint32_t vx_gemv_grid(uint32_t n_tiles, uint32_t max_wgs) {
+    const uint32_t w = (uint32_t)vx_env_int("VELOX_HIP_GEMV_WAVES", 8);
+    uint32_t wgs = (n_tiles + w - 1u) / w;
+    if (wgs > max_wgs) wgs = max_wgs;
+    return wgs ? wgs : 1u;
+}
+
 hipError_t vx_launch_attention(const VxAttnArgs& a, uint32_t d, hipStream_t st) {
-    if (a.hkv == 0 || a.hq % a.hkv != 0 || a.splits == 0 || a.s_max == 0) return hipErrorInvalidValue;
+    if (a.hkv == 0 || a.hq % a.hkv != 0 || a.splits == 0 || a.splits > 64 || a.s_max == 0) return hipErrorInvalidValue;
     const uint32_t G = a.hq / a.hkv;
     if (d == 64) {
         switch (G) {
