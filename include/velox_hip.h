@@ -233,6 +233,8 @@ typedef struct VeloxHipRunOptions {
     uint32_t num_layers;     /* 0 = config value (fewer layers for parity runs) */
     uint32_t kernel_passes;  /* >0: afterwards time the gate/up GEMV alone over all layers this often */
     uint32_t verbose;
+    const uint32_t* prompt_tokens; /* NULL: prompt_len seeded random ids; else prompt_len explicit ids
+                                      (the runner's --tokens, src/cli.rs:655-661) */
 } VeloxHipRunOptions;
 
 typedef struct VeloxHipRunReport {

@@ -119,3 +119,9 @@ def test_runner_rejects_unsupported_arguments():
     assert r.returncode == 1 and "not supported" in r.stderr
     r = subprocess.run([runner, "--bogus"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 1
+    # argv of src/cli.rs:653-675: token lists are parsed strictly; speculative flags are refused
+    r = subprocess.run([runner, "--weights", "synthetic", "--tokens", "1,x,3"], capture_output=True, text=True,
+                       timeout=60)
+    assert r.returncode == 1 and "bad token id 'x'" in r.stderr
+    r = subprocess.run([runner, "--speculative"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 1 and "not supported" in r.stderr

@@ -93,3 +93,15 @@ def test_active_mask_predication(oracle):
     g.sync()
     assert g.state() == (0, 5)
     g.close()
+
+
+def test_run_with_explicit_prompt_tokens(oracle):
+    """velox_hip_run with explicit ids (the runner's --tokens) equals the seeded-prompt run when the
+    ids are the seeded ones, and refuses an id outside the vocabulary."""
+    seed, P = 23, 5
+    prompt = [int(t) for t in oracle.prompt_tokens(seed, P, 49152)]
+    rep_a, toks_a = run("smollm_135m", prompt_len=P, warmup=0, steps=4, seed=seed, num_layers=3, max_seq_len=16)
+    rep_b, toks_b = run("smollm_135m", prompt=prompt, warmup=0, steps=4, seed=seed, num_layers=3, max_seq_len=16)
+    assert rep_a["status"] == rep_b["status"] == 0 and toks_a == toks_b
+    with pytest.raises(RuntimeError):
+        run("smollm_135m", prompt=[1, 49152], warmup=0, steps=1, seed=seed, num_layers=1, max_seq_len=8)

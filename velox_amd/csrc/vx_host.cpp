@@ -850,7 +850,10 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
 
     std::vector<uint32_t> prompt(opt->prompt_len);
     const uint64_t pst = vx_stream(opt->seed, vx_tag(0, VX_TAG_PROMPT));
-    for (uint32_t i = 0; i < opt->prompt_len; ++i) prompt[i] = vx_uniform_u32(pst, i, cfg.vocab_size);
+    for (uint32_t i = 0; i < opt->prompt_len; ++i) {
+        prompt[i] = opt->prompt_tokens ? opt->prompt_tokens[i] : vx_uniform_u32(pst, i, cfg.vocab_size);
+        if (prompt[i] >= cfg.vocab_size && !rc) rc = VELOX_HIP_EINVAL;
+    }
     if (!rc) rc = velox_hip_set_prompt(&A, prompt.data(), opt->prompt_len, st);
     if (!rc) rc = velox_hip_set_state(&A, 0, prompt[0], st);
     velox_hip_last_error();

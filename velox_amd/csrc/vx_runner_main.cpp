@@ -3,10 +3,11 @@
 // (src/cli.rs:640-770, "[Step N] Token: id" parsing at :706-733) and the benchmark regexes
 // (benchmarks/run_sota_roofline_benchmarks.py:278-292) keep working.
 //
-//   velox_hip_runner [--model llama3_8b] [--tokens 1,2,3 | --prompt-len N] [--steps N]
-//                    [--warmup N] [--seed S] [--layers L] [--no-cuda-graph] [--verbose]
+//   velox_hip_runner [--model llama3_8b] [--weights synthetic] [--tokens 1,2,3 | --prompt-len N]
+//                    [--steps N] [--warmup N] [--seed S] [--layers L] [--no-cuda-graph] [--verbose]
 //
-// Weights are the seeded synthetic Q4_0 model (no checkpoint is available offline).
+// Weights are the seeded synthetic Q4_0 model: `--weights synthetic` (what src/cli.rs:654 passes
+// through) is accepted, a checkpoint path is refused with exit 1.
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -34,9 +35,17 @@ int main(int argc, char** argv) {
             while (p < s.size()) {
                 size_t q = s.find(',', p);
                 if (q == std::string::npos) q = s.size();
-                tokens.push_back((uint32_t)std::strtoul(s.substr(p, q - p).c_str(), nullptr, 10));
+                const std::string t = s.substr(p, q - p);
+                char* end = nullptr;
+                const unsigned long v = std::strtoul(t.c_str(), &end, 10);
+                if (t.empty() || *end != '\0' || v > 0xFFFFFFFFul) {
+                    std::fprintf(stderr, "Error: bad token id '%s' in --tokens\n", t.c_str());
+                    return 1;
+                }
+                tokens.push_back((uint32_t)v);
                 p = q + 1;
             }
+            if (tokens.empty()) { std::fprintf(stderr, "Error: --tokens is empty\n"); return 1; }
         } else if (!std::strcmp(a, "--prompt-len")) prompt_len = (uint32_t)std::atoi(next());
         else if (!std::strcmp(a, "--steps")) steps = (uint32_t)std::atoi(next());
         else if (!std::strcmp(a, "--warmup")) warmup = (uint32_t)std::atoi(next());
@@ -44,18 +53,23 @@ int main(int argc, char** argv) {
         else if (!std::strcmp(a, "--layers")) layers = (uint32_t)std::atoi(next());
         else if (!std::strcmp(a, "--no-cuda-graph") || !std::strcmp(a, "--no-graph")) graph = false;
         else if (!std::strcmp(a, "--verbose")) verbose = true;
-        else if (!std::strcmp(a, "--weights") || !std::strcmp(a, "--quantize")) {
-            std::fprintf(stderr, "Error: %s is not supported (synthetic Q4_0 weights only)\n", a);
+        else if (!std::strcmp(a, "--weights")) {
+            const char* w = next();
+            if (std::strcmp(w, "synthetic") != 0) {
+                std::fprintf(stderr, "Error: --weights %s is not supported (synthetic Q4_0 weights only)\n", w);
+                return 1;
+            }
+        } else if (!std::strcmp(a, "--quantize") || !std::strcmp(a, "--speculative") ||
+                   !std::strcmp(a, "--draft-len") || !std::strcmp(a, "--spec-ema") ||
+                   !std::strcmp(a, "--context-len")) {
+            std::fprintf(stderr, "Error: %s is not supported by this runner\n", a);
             return 1;
         } else {
             std::fprintf(stderr, "Error: unknown argument %s\n", a);
             return 1;
         }
     }
-    if (!tokens.empty()) {
-        std::fprintf(stderr, "Error: explicit --tokens are not supported by this runner build; use --prompt-len\n");
-        return 1;
-    }
+    if (!tokens.empty()) prompt_len = (uint32_t)tokens.size();
     if (steps == 0 || prompt_len == 0) { std::fprintf(stderr, "Error: --steps and --prompt-len must be > 0\n"); return 1; }
 
     VeloxHipRunOptions opt;
@@ -70,11 +84,13 @@ int main(int argc, char** argv) {
     opt.use_graph = graph ? 1 : 0;
     opt.num_layers = layers;
     opt.verbose = verbose ? 1 : 0;
+    opt.prompt_tokens = tokens.empty() ? nullptr : tokens.data();
     std::vector<uint32_t> out(prompt_len + warmup + opt.steps + 8);
     VeloxHipRunReport rep;
     const int rc = velox_hip_run(&opt, out.data(), (uint32_t)out.size(), &rep);
     if (rc != 0) {
-        std::fprintf(stderr, "HIP error detected: status %d\n", rc);
+        std::fprintf(stderr, "HIP error detected: status %d%s\n", rc,
+                     rc == VELOX_HIP_EINVAL ? " (invalid argument: token id >= vocab or unsupported shape)" : "");
         return 1;
     }
     // ring[p] = argmax after position p; generated tokens start at p = prompt_len - 1
