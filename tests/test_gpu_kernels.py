@@ -151,6 +151,29 @@ def test_gemv_norm_bias_residual(hiplib, oracle, dev):
     assert np.max(np.abs(got - tight)) < 5e-4
 
 
+@pytest.mark.parametrize("n,k", [(960, 576), (512, 4096)])
+def test_gemv_norm_fp16_staging_consistent(hiplib, oracle, dev, n, k):
+    """The RMSNorm'd activations are staged as fp16 together with each block's sum, which cancels
+    the +1024 of the unpacked codes. If the staged values and the sum came from different fp16
+    roundings of (x * inv) * g, a single element would shift its block's dot by 1024 ulp for every
+    row. Double-rounding cases occur in a few percent of random vectors, so 48 vectors hit some."""
+    blocks = _weights(oracle, n, k, 77)
+    t = TiledQ4(hiplib, dev, blocks, n, k)
+    deq = oracle.q4_0_dequant(blocks, k)
+    rng = np.random.default_rng(k)
+    dy = dev.empty(n)
+    rms = lambda a: float(np.sqrt(np.mean(np.square(a, dtype=np.float64))))
+    for _ in range(48):
+        x = (0.3 * rng.standard_normal(k)).astype(np.float32)
+        gain = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+        dx, dg = dev.put(x), dev.put(gain)
+        L.check(hiplib.velox_hip_gemv_q4_0(C.byref(t.m), dx.data_ptr(), dg.data_ptr(), 1e-5, None, None,
+                                           dy.data_ptr(), L.GEMV_STORE, None))
+        got = dev.get(dy)
+        tight = _fp64_gemv(deq, oracle.rmsnorm(x, gain, 1e-5).astype(np.float16))
+        assert rms(got - tight) < 1e-4 * rms(tight)
+
+
 @pytest.mark.parametrize("F,H", [(14336, 4096), (1536, 576), (100, 576)])
 def test_gemv_swiglu(hiplib, oracle, dev, F, H):
     rng = np.random.default_rng(F)

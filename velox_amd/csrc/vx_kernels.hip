@@ -166,16 +166,21 @@ __device__ __forceinline__ float vx_normal_value(uint64_t stream, uint64_t idx, 
 // Fused Q4_0 GEMV
 // =============================================================================================
 // Each wave streams the code words of its tiles as one flat sequence of items (tile, iteration):
-// kU 16-byte loads stay in flight per lane across tile boundaries, and the first kU are issued
-// before the prologue, so that staging the activations in LDS overlaps the weight fetch. Tiles go
-// to waves round-robin over the grid (a.contig == 0) or in contiguous runs (a.contig == 1).
+// kU 16-byte loads stay in flight per lane across tile boundaries. The activations are loaded
+// first, then the first kU weight items, so staging x in LDS overlaps the weight fetch. Every
+// load outside the last 2*kU items is issued unconditionally: vector memory completes in issue
+// order, and with no load under a branch the compiler's s_waitcnt for item u waits for that item
+// only, keeping kU items in flight instead of draining the queue once per iteration. Tiles go to
+// waves round-robin over the grid (a.contig == 0) or in contiguous runs (a.contig == 1).
 // No workgroup waits on another: the LM head's argmax leaves one candidate per workgroup for
 // vx_argmax_finalize_kernel (a release fence per workgroup costs a full L2 write-back on gfx950).
-template <int S, int EPI, int W, int kU>
-__global__ __launch_bounds__(64 * W) void vx_gemv_q4_kernel(VxGemvArgs a) {
+constexpr int kGemvWaves = 8, kGemvU = 4;
+
+template <int S, int EPI, bool NORM, int GX>
+__global__ __launch_bounds__(64 * kGemvWaves) void vx_gemv_q4_kernel(VxGemvArgs a) {
     extern __shared__ __align__(16) unsigned char vx_smem[];
     if ((a.active_mask & 1ULL) == 0ULL) return;
-    constexpr int R = 64 / S, NT = 64 * W;
+    constexpr int W = kGemvWaves, kU = kGemvU, R = 64 / S, NT = 64 * W;
     const uint32_t K = a.k, nb = K >> 5, n_iter = a.n_iter;
     uint4* xs4 = (uint4*)vx_smem;  // fp16 activations: 4 planes of nb 16-byte chunks
     float* corr = (float*)(vx_smem + (size_t)K * 2u);
@@ -201,6 +206,21 @@ __global__ __launch_bounds__(64 * W) void vx_gemv_q4_kernel(VxGemvArgs a) {
         if constexpr (EPI == VX_EPI_SWIGLU) return t * (R / 2) + (r % (R / 2));  // logical j of gate/up
         else return t * R + r;
     };
+
+    // ---- activations (and the RMSNorm gain) into registers, before any weight load ----
+    const uint32_t ng = K >> 3;  // 8-element groups; a multiple of 4
+    float4 xv[2 * GX], gv[2 * GX];
+#pragma unroll
+    for (int i = 0; i < GX; ++i) {
+        const uint32_t g = min((uint32_t)tid + (uint32_t)i * NT, ng - 1u);  // clamped: never a branch
+        xv[2 * i] = *(const float4*)(a.x + 8u * g);
+        xv[2 * i + 1] = *(const float4*)(a.x + 8u * g + 4u);
+        if constexpr (NORM) {
+            gv[2 * i] = *(const float4*)(a.gain + 8u * g);
+            gv[2 * i + 1] = *(const float4*)(a.gain + 8u * g + 4u);
+        }
+    }
+
     // Code words and scales through buffer descriptors: per-lane offsets are constant, the item
     // offset is wave-uniform (scalar). Padded slots of a tile hold zero codes and zero scales, so
     // they are loaded and contribute exactly 0 without any per-lane branch.
@@ -212,11 +232,7 @@ __global__ __launch_bounds__(64 * W) void vx_gemv_q4_kernel(VxGemvArgs a) {
     vx_u32x4 buf[kU];
     uint32_t sbuf[kU];
     uint32_t nt = 0, ni = 0, nslot = first * n_iter;  // next item: tile index, iteration, 64-lane slot
-    auto issue = [&](int u) {
-        if (nt < my_tiles) {
-            buf[u] = __builtin_amdgcn_raw_buffer_load_b128(rc, lane16, nslot * 1024u, 2);
-            sbuf[u] = __builtin_amdgcn_raw_buffer_load_b16(rsc, lane2, nslot * 128u, 2);
-        }
+    auto advance = [&]() {
         if (++ni == n_iter) {
             ni = 0;
             ++nt;
@@ -225,26 +241,42 @@ __global__ __launch_bounds__(64 * W) void vx_gemv_q4_kernel(VxGemvArgs a) {
             ++nslot;
         }
     };
+    // unconditional load of the next item; past this wave's last item it re-reads slot 0 (in
+    // bounds, cache-resident after the first wave touches it) and the value is never consumed
+    auto issue = [&](int u) {
+        const uint32_t slot = __builtin_amdgcn_readfirstlane(nt < my_tiles ? nslot : 0u);
+        buf[u] = __builtin_amdgcn_raw_buffer_load_b128(rc, lane16, slot * 1024u, 2);
+        sbuf[u] = __builtin_amdgcn_raw_buffer_load_b16(rsc, lane2, slot * 128u, 2);
+        advance();
+    };
 #pragma unroll
     for (int u = 0; u < kU; ++u) issue(u);
 
-    // ---- prologue: optional RMSNorm scale (src/runtime.rs:588-601), x -> fp16 in LDS ----
+    // ---- RMSNorm scale (src/runtime.rs:588-601) from the registers, plus groups beyond them ----
     float inv_rms = 1.0f;
-    if (a.gain) {
+    if constexpr (NORM) {
         float ss = 0.0f;
-        for (uint32_t i = (uint32_t)tid * 4u; i < K; i += NT * 4u) {
-            const float4 v = *(const float4*)(a.x + i);
-            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+#pragma unroll
+        for (int i = 0; i < GX; ++i) {
+            if ((uint32_t)tid + (uint32_t)i * NT < ng) {
+                const float4 v0 = xv[2 * i], v1 = xv[2 * i + 1];
+                ss += v0.x * v0.x + v0.y * v0.y + v0.z * v0.z + v0.w * v0.w;
+                ss += v1.x * v1.x + v1.y * v1.y + v1.z * v1.z + v1.w * v1.w;
+            }
+        }
+        for (uint32_t g = (uint32_t)tid + GX * NT; g < ng; g += NT) {
+            const float4 v0 = *(const float4*)(a.x + 8u * g);
+            const float4 v1 = *(const float4*)(a.x + 8u * g + 4u);
+            ss += v0.x * v0.x + v0.y * v0.y + v0.z * v0.z + v0.w * v0.w;
+            ss += v1.x * v1.x + v1.y * v1.y + v1.z * v1.z + v1.w * v1.w;
         }
         ss = vx_block_sum<W>(ss, red);
         inv_rms = 1.0f / sqrtf(ss / (float)K + a.eps);
     }
-    for (uint32_t g = tid; g < (K >> 3); g += NT) {
-        float4 v0 = *(const float4*)(a.x + 8u * g);
-        float4 v1 = *(const float4*)(a.x + 8u * g + 4u);
-        if (a.gain) {
-            const float4 g0 = *(const float4*)(a.gain + 8u * g);
-            const float4 g1 = *(const float4*)(a.gain + 8u * g + 4u);
+    // x -> fp16 in LDS, plane-major [w][b]: the S lanes of a row read blocks b..b+S-1 of one plane
+    // at consecutive 16-byte addresses (no LDS bank conflicts); corr[b] = -1032 * sum of block b
+    auto stage = [&](uint32_t g, float4 v0, float4 v1, float4 g0, float4 g1) {
+        if constexpr (NORM) {
             v0 = make_float4((v0.x * inv_rms) * g0.x, (v0.y * inv_rms) * g0.y, (v0.z * inv_rms) * g0.z,
                              (v0.w * inv_rms) * g0.w);
             v1 = make_float4((v1.x * inv_rms) * g1.x, (v1.y * inv_rms) * g1.y, (v1.z * inv_rms) * g1.z,
@@ -252,16 +284,36 @@ __global__ __launch_bounds__(64 * W) void vx_gemv_q4_kernel(VxGemvArgs a) {
         }
         const __half h[8] = {__float2half(v0.x), __float2half(v0.y), __float2half(v0.z), __float2half(v0.w),
                              __float2half(v1.x), __float2half(v1.y), __float2half(v1.z), __float2half(v1.w)};
-        // plane-major [w][b]: the S lanes of a row read blocks b..b+S-1 of one plane at consecutive
-        // 16-byte addresses (no LDS bank conflicts)
-        xs4[(g & 3u) * nb + (g >> 2)] = *(const uint4*)h;
-        float sum = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sum += __half2float(h[e]);
-        // the four 8-element groups of one 32-block sit in four consecutive lanes
+        const uint4 hp = *(const uint4*)h;
+        xs4[(g & 3u) * nb + (g >> 2)] = hp;
+        // corr must see exactly the fp16 values stored above. The compiler may fuse the product
+        // and the conversion (v_fma_mix, one rounding) for one use of h and not for another (two
+        // roundings), so the sum is taken from the stored bits with v_dot2 against (1, 1):
+        // a one-ulp disagreement would cost 1024 ulp in the block's dot product.
+        const vx_h2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
+        float sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, hp.x), one2, 0.0f, false);
+        sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, hp.y), one2, sum, false);
+        sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, hp.z), one2, sum, false);
+        sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, hp.w), one2, sum, false);
+        // the four 8-element groups of one 32-block sit in four consecutive lanes, which are all
+        // in range or all out of range (ng is a multiple of 4)
         sum += __shfl_xor(sum, 1);
         sum += __shfl_xor(sum, 2);
         if ((g & 3u) == 0u) corr[g >> 2] = -1032.0f * sum;
+    };
+#pragma unroll
+    for (int i = 0; i < GX; ++i) {
+        const uint32_t g = (uint32_t)tid + (uint32_t)i * NT;
+        if (g < ng) stage(g, xv[2 * i], xv[2 * i + 1], gv[2 * i], gv[2 * i + 1]);
+    }
+    for (uint32_t g = (uint32_t)tid + GX * NT; g < ng; g += NT) {
+        const float4 v0 = *(const float4*)(a.x + 8u * g), v1 = *(const float4*)(a.x + 8u * g + 4u);
+        float4 g0 = v0, g1 = v1;
+        if constexpr (NORM) {
+            g0 = *(const float4*)(a.gain + 8u * g);
+            g1 = *(const float4*)(a.gain + 8u * g + 4u);
+        }
+        stage(g, v0, v1, g0, g1);
     }
     __syncthreads();
 
@@ -270,44 +322,57 @@ __global__ __launch_bounds__(64 * W) void vx_gemv_q4_kernel(VxGemvArgs a) {
     uint32_t best_i = 0xFFFFFFFFu;
     float acc = 0.0f;
     uint32_t ct = 0, ci = 0;  // current item
-    for (uint32_t f0 = 0; f0 < total; f0 += kU) {
+    auto consume = [&](int u) {
+        // padded blocks (b >= nb, zero scale) read a valid activation chunk instead
+        const uint32_t b = min(ci * S + s, nb - 1u);
+        const vx_u32x4 c = buf[u];
+        float dot = corr[b];
+        dot = vx_dot8(c.x, xs4[b], dot);
+        dot = vx_dot8(c.y, xs4[nb + b], dot);
+        dot = vx_dot8(c.z, xs4[2u * nb + b], dot);
+        dot = vx_dot8(c.w, xs4[3u * nb + b], dot);
+        acc = fmaf(vx_h2f(sbuf[u]), dot, acc);
+        if (++ci == n_iter) {
+            acc = vx_group_sum<S>(acc);
+            const uint32_t row = row_of(first + ct * step);
+            const bool row_ok = row < a.n;
+            if constexpr (EPI == VX_EPI_STORE) {
+                if (s == 0 && row_ok) a.y[row] = a.bias ? acc + a.bias[row] : acc;
+            } else if constexpr (EPI == VX_EPI_RESID) {
+                if (s == 0 && row_ok) a.y[row] = a.res[row] + acc;
+            } else if constexpr (EPI == VX_EPI_SWIGLU) {
+                const float up = __shfl_down(acc, 32);  // partner up row is 32 lanes above
+                if (s == 0 && r < R / 2 && row_ok) {
+                    const float gt = acc;
+                    a.y[row] = (gt / (1.0f + expf(-gt))) * up;  // src/runtime.rs:1064-1066
+                }
+            } else {  // VX_EPI_ARGMAX
+                if (s == 0 && row_ok) {
+                    a.y[row] = acc;
+                    if (vx_better(acc, row, best_v, best_i)) { best_v = acc; best_i = row; }
+                }
+            }
+            acc = 0.0f;
+            ci = 0;
+            ++ct;
+        }
+    };
+    uint32_t f0 = 0;
+    // steady state: every refill is a real item of this wave
+    for (; f0 + 2u * kU <= total; f0 += kU) {
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            consume(u);
+            issue(u);
+        }
+    }
+    // the last (< 2 kU) items: refills only while items remain
+    for (; f0 < total; f0 += kU) {
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
             if (f0 + u < total) {
-                // padded blocks (b >= nb, zero scale) read a valid activation chunk instead
-                const uint32_t b = min(ci * S + s, nb - 1u);
-                const vx_u32x4 c = buf[u];
-                float dot = corr[b];
-                dot = vx_dot8(c.x, xs4[b], dot);
-                dot = vx_dot8(c.y, xs4[nb + b], dot);
-                dot = vx_dot8(c.z, xs4[2u * nb + b], dot);
-                dot = vx_dot8(c.w, xs4[3u * nb + b], dot);
-                acc = fmaf(vx_h2f(sbuf[u]), dot, acc);
-                issue(u);
-                if (++ci == n_iter) {
-                    acc = vx_group_sum<S>(acc);
-                    const uint32_t row = row_of(first + ct * step);
-                    const bool row_ok = row < a.n;
-                    if constexpr (EPI == VX_EPI_STORE) {
-                        if (s == 0 && row_ok) a.y[row] = a.bias ? acc + a.bias[row] : acc;
-                    } else if constexpr (EPI == VX_EPI_RESID) {
-                        if (s == 0 && row_ok) a.y[row] = a.res[row] + acc;
-                    } else if constexpr (EPI == VX_EPI_SWIGLU) {
-                        const float up = __shfl_down(acc, 32);  // partner up row is 32 lanes above
-                        if (s == 0 && r < R / 2 && row_ok) {
-                            const float gt = acc;
-                            a.y[row] = (gt / (1.0f + expf(-gt))) * up;  // src/runtime.rs:1064-1066
-                        }
-                    } else {  // VX_EPI_ARGMAX
-                        if (s == 0 && row_ok) {
-                            a.y[row] = acc;
-                            if (vx_better(acc, row, best_v, best_i)) { best_v = acc; best_i = row; }
-                        }
-                    }
-                    acc = 0.0f;
-                    ci = 0;
-                    ++ct;
-                }
+                consume(u);
+                if (f0 + u + kU < total) issue(u);
             }
         }
     }
@@ -733,14 +798,15 @@ int vx_env_int(const char* name, int dflt) {
     return e ? (int)strtol(e, nullptr, 10) : dflt;
 }
 
-template <int S, int EPI, int W, int KU>
+template <int S, int EPI, bool NORM, int GX>
 hipError_t vx_gemv_launch_t(const VxGemvArgs& a, uint32_t max_wgs, hipStream_t st) {
+    constexpr int W = kGemvWaves;
     const uint32_t nb = a.k >> 5;
     const size_t lds = (size_t)a.k * 2u + (size_t)nb * 4u + 64u;
     static size_t attr_lds = 64u * 1024u;
     if (lds > attr_lds) {
-        if (hipFuncSetAttribute((const void*)vx_gemv_q4_kernel<S, EPI, W, KU>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds) != hipSuccess) {
+        if (hipFuncSetAttribute((const void*)vx_gemv_q4_kernel<S, EPI, NORM, GX>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
             (void)hipGetLastError();
             return hipErrorInvalidValue;
         }
@@ -749,40 +815,41 @@ hipError_t vx_gemv_launch_t(const VxGemvArgs& a, uint32_t max_wgs, hipStream_t s
     uint32_t wgs = (a.n_tiles + W - 1u) / W;
     if (wgs > max_wgs) wgs = max_wgs;
     if (wgs == 0) wgs = 1;
-    hipLaunchKernelGGL((vx_gemv_q4_kernel<S, EPI, W, KU>), dim3(wgs), dim3(64 * W), lds, st, a);
+    hipLaunchKernelGGL((vx_gemv_q4_kernel<S, EPI, NORM, GX>), dim3(wgs), dim3(64 * W), lds, st, a);
     return hipGetLastError();
 }
 
-template <int EPI, int W, int KU>
+// x register groups per thread: ceil(K / 8 / threads) rounded up to 1, 2 or 4 (larger K loops)
+template <int S, int EPI, bool NORM>
+hipError_t vx_gemv_dispatch_gx(const VxGemvArgs& a, uint32_t max_wgs, hipStream_t st) {
+    const uint32_t per = ((a.k >> 3) + 64u * kGemvWaves - 1u) / (64u * kGemvWaves);
+    if (per <= 1u) return vx_gemv_launch_t<S, EPI, NORM, 1>(a, max_wgs, st);
+    if (per <= 2u) return vx_gemv_launch_t<S, EPI, NORM, 2>(a, max_wgs, st);
+    return vx_gemv_launch_t<S, EPI, NORM, 4>(a, max_wgs, st);
+}
+
+template <int EPI, bool NORM>
 hipError_t vx_gemv_dispatch_s(uint32_t s, const VxGemvArgs& a, uint32_t max_wgs, hipStream_t st) {
     switch (s) {
-        case 4: return vx_gemv_launch_t<4, EPI, W, KU>(a, max_wgs, st);
-        case 8: return vx_gemv_launch_t<8, EPI, W, KU>(a, max_wgs, st);
-        case 16: return vx_gemv_launch_t<16, EPI, W, KU>(a, max_wgs, st);
-        case 32: return vx_gemv_launch_t<32, EPI, W, KU>(a, max_wgs, st);
+        case 4: return vx_gemv_dispatch_gx<4, EPI, NORM>(a, max_wgs, st);
+        case 8: return vx_gemv_dispatch_gx<8, EPI, NORM>(a, max_wgs, st);
+        case 16: return vx_gemv_dispatch_gx<16, EPI, NORM>(a, max_wgs, st);
+        case 32: return vx_gemv_dispatch_gx<32, EPI, NORM>(a, max_wgs, st);
         case 64:
-            if constexpr (EPI != VX_EPI_SWIGLU) return vx_gemv_launch_t<64, EPI, W, KU>(a, max_wgs, st);
+            if constexpr (EPI != VX_EPI_SWIGLU) return vx_gemv_dispatch_gx<64, EPI, NORM>(a, max_wgs, st);
             return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }
 
-template <int EPI, int W>
-hipError_t vx_gemv_dispatch_u(uint32_t ku, uint32_t s, const VxGemvArgs& a, uint32_t max_wgs, hipStream_t st) {
-    switch (ku) {
-        case 4: return vx_gemv_dispatch_s<EPI, W, 4>(s, a, max_wgs, st);
-        case 8: return vx_gemv_dispatch_s<EPI, W, 8>(s, a, max_wgs, st);
-        default: return hipErrorInvalidValue;
-    }
-}
-
 template <int EPI>
-hipError_t vx_gemv_dispatch_w(uint32_t w, uint32_t s, const VxGemvArgs& a, uint32_t max_wgs, hipStream_t st) {
-    const uint32_t ku = (uint32_t)vx_env_int("VELOX_HIP_GEMV_KU", 4);
-    switch (w) {
-        case 4: return vx_gemv_dispatch_u<EPI, 4>(ku, s, a, max_wgs, st);
-        case 8: return vx_gemv_dispatch_u<EPI, 8>(ku, s, a, max_wgs, st);
-        default: return hipErrorInvalidValue;
+hipError_t vx_gemv_dispatch_norm(uint32_t s, const VxGemvArgs& a, uint32_t max_wgs, hipStream_t st) {
+    if constexpr (EPI == VX_EPI_RESID) {
+        if (a.gain) return hipErrorInvalidValue;  // the residual epilogue takes raw activations
+        return vx_gemv_dispatch_s<EPI, false>(s, a, max_wgs, st);
+    } else {
+        return a.gain ? vx_gemv_dispatch_s<EPI, true>(s, a, max_wgs, st)
+                      : vx_gemv_dispatch_s<EPI, false>(s, a, max_wgs, st);
     }
 }
 
@@ -816,14 +883,13 @@ hipError_t vx_launch_gemv(const VxMat& m, const VxGemvArgs& a0, int epi, uint32_
     a.n_tiles = m.n_tiles;
     a.n_iter = m.n_iter;
     a.contig = (uint32_t)vx_env_int("VELOX_HIP_GEMV_CONTIG", 0);
-    const uint32_t w = (uint32_t)vx_env_int("VELOX_HIP_GEMV_WAVES", 8);
     if (m.k == 0 || (m.k & 31u) != 0) return hipErrorInvalidValue;
     if ((epi == VX_EPI_SWIGLU) != (m.paired != 0)) return hipErrorInvalidValue;
     switch (epi) {
-        case VX_EPI_STORE: return vx_gemv_dispatch_w<VX_EPI_STORE>(w, m.s, a, max_wgs, st);
-        case VX_EPI_RESID: return vx_gemv_dispatch_w<VX_EPI_RESID>(w, m.s, a, max_wgs, st);
-        case VX_EPI_SWIGLU: return vx_gemv_dispatch_w<VX_EPI_SWIGLU>(w, m.s, a, max_wgs, st);
-        case VX_EPI_ARGMAX: return vx_gemv_dispatch_w<VX_EPI_ARGMAX>(w, m.s, a, max_wgs, st);
+        case VX_EPI_STORE: return vx_gemv_dispatch_norm<VX_EPI_STORE>(m.s, a, max_wgs, st);
+        case VX_EPI_RESID: return vx_gemv_dispatch_norm<VX_EPI_RESID>(m.s, a, max_wgs, st);
+        case VX_EPI_SWIGLU: return vx_gemv_dispatch_norm<VX_EPI_SWIGLU>(m.s, a, max_wgs, st);
+        case VX_EPI_ARGMAX: return vx_gemv_dispatch_norm<VX_EPI_ARGMAX>(m.s, a, max_wgs, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -837,8 +903,7 @@ hipError_t vx_launch_argmax_finalize(const float* cand_v, const uint32_t* cand_i
 }
 
 uint32_t vx_gemv_grid(uint32_t n_tiles, uint32_t max_wgs) {
-    const uint32_t w = (uint32_t)vx_env_int("VELOX_HIP_GEMV_WAVES", 8);
-    uint32_t wgs = (n_tiles + w - 1u) / w;
+    uint32_t wgs = (n_tiles + kGemvWaves - 1u) / kGemvWaves;
     if (wgs > max_wgs) wgs = max_wgs;
     return wgs ? wgs : 1u;
 }
