@@ -23,12 +23,12 @@ QWEN7 = dict(vocab_size=152064, hidden_dim=3584, intermediate_dim=18944, num_lay
              head_dim=128, rms_norm_eps=1e-6, rope_theta=1000000.0, qkv_bias=1, tied_lm_head=1)
 
 
-def _compare(oracle, name, cfg, layers, max_seq, n_steps, seed, norm_sigma, threads=8):
+def _compare(oracle, name, cfg, layers, max_seq, n_steps, seed, norm_sigma, threads=8, attn_splits=0):
     ocfg = dict(cfg, num_layers=layers, max_seq_len=max_seq)
     ref = oracle.Engine(ocfg, seed=seed, sigma=0.02, norm_sigma=norm_sigma, q4_0=True, kv_bf16=True,
                         threads=threads)
     gpu = HipDecodeEngine(name, seed=seed, sigma=0.02, norm_sigma=norm_sigma, max_seq_len=max_seq,
-                          num_layers=layers)
+                          num_layers=layers, attn_splits=attn_splits)
     toks = list(oracle.prompt_tokens(seed, n_steps, cfg["vocab_size"]))
     worst = 0.0
     for pos, tok in enumerate(toks):
@@ -57,6 +57,13 @@ def test_decode_llama_shapes_2_layers_vs_oracle(oracle):
 
 def test_decode_qwen_bias_tied_2_layers_vs_oracle(oracle):
     _compare(oracle, "qwen2_5_7b", QWEN7, 2, 24, 3, seed=13, norm_sigma=0.1, threads=16)
+
+
+@pytest.mark.parametrize("splits", [2, 8, 3])
+def test_decode_split_k_attention_vs_oracle(oracle, splits):
+    """Split-K attention over the sequence: 2 and 8 splits are merged in the o_proj GEMV prologue,
+    3 splits by the separate LSE merge kernel; 20 positions leave some splits empty early on."""
+    _compare(oracle, "smollm_135m", SMOLLM, 4, 24, 20, seed=17, norm_sigma=0.1, attn_splits=splits)
 
 
 def test_graph_replay_matches_eager(oracle):

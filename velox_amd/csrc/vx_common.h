@@ -112,6 +112,11 @@ struct VxGemvArgs {
     const uint32_t* prompt_len;
     uint32_t* token_out;
     uint64_t active_mask;
+    // x from split-K attention partials instead of `x` (o_proj): x[h*d + e] is the LSE merge of
+    // part_o[h][s][e] with (m, l) = part_ml[h][s] over att_splits splits
+    const float* part_o;
+    const float* part_ml;
+    uint32_t att_splits, att_d;
 };
 
 struct VxAttnArgs {
@@ -127,6 +132,7 @@ struct VxAttnArgs {
     uint32_t hq, hkv, s_max, splits;
     float scale;
     uint64_t active_mask;
+    uint32_t partials_only;  // 1: always write (m, l, o) partials; the consumer merges them
 };
 
 // Launch helpers implemented in vx_kernels.hip, used by vx_host.cpp.

@@ -26,6 +26,8 @@ namespace {
 constexpr int kWG = 256;  // threads per workgroup (4 wave64)
 
 
+// 2^x on the transcendental unit (the softmax works in the log2 domain)
+__device__ __forceinline__ float vx_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float vx_h2f(uint32_t h) { return __half2float(__ushort_as_half((unsigned short)h)); }
 
 // Code dword layout (8 weights): byte j holds element j in its low nibble and element j + 4 in
@@ -176,7 +178,7 @@ __device__ __forceinline__ float vx_normal_value(uint64_t stream, uint64_t idx, 
 // vx_argmax_finalize_kernel (a release fence per workgroup costs a full L2 write-back on gfx950).
 constexpr int kGemvWaves = 8, kGemvU = 4;
 
-template <int S, int EPI, bool NORM, int GX>
+template <int S, int EPI, bool NORM, int GX, int SPL>
 __global__ __launch_bounds__(64 * kGemvWaves) void vx_gemv_q4_kernel(VxGemvArgs a) {
     extern __shared__ __align__(16) unsigned char vx_smem[];
     if ((a.active_mask & 1ULL) == 0ULL) return;
@@ -210,11 +212,25 @@ __global__ __launch_bounds__(64 * kGemvWaves) void vx_gemv_q4_kernel(VxGemvArgs 
     // ---- activations (and the RMSNorm gain) into registers, before any weight load ----
     const uint32_t ng = K >> 3;  // 8-element groups; a multiple of 4
     float4 xv[2 * GX], gv[2 * GX];
+    // SPL > 0: the activations are SPL split-K attention partials per head, merged below
+    float2 pml[SPL > 0 ? GX : 1][SPL > 0 ? SPL : 1];
+    float4 po[SPL > 0 ? GX : 1][SPL > 0 ? SPL : 1][2];
 #pragma unroll
     for (int i = 0; i < GX; ++i) {
         const uint32_t g = min((uint32_t)tid + (uint32_t)i * NT, ng - 1u);  // clamped: never a branch
-        xv[2 * i] = *(const float4*)(a.x + 8u * g);
-        xv[2 * i + 1] = *(const float4*)(a.x + 8u * g + 4u);
+        if constexpr (SPL == 0) {
+            xv[2 * i] = *(const float4*)(a.x + 8u * g);
+            xv[2 * i + 1] = *(const float4*)(a.x + 8u * g + 4u);
+        } else {
+            const uint32_t h = (8u * g) / a.att_d, e0 = 8u * g - h * a.att_d;
+#pragma unroll
+            for (int sp = 0; sp < SPL; ++sp) {
+                const size_t hs = (size_t)h * SPL + (uint32_t)sp;
+                pml[i][sp] = *(const float2*)(a.part_ml + hs * 2u);
+                po[i][sp][0] = *(const float4*)(a.part_o + hs * a.att_d + e0);
+                po[i][sp][1] = *(const float4*)(a.part_o + hs * a.att_d + e0 + 4u);
+            }
+        }
         if constexpr (NORM) {
             gv[2 * i] = *(const float4*)(a.gain + 8u * g);
             gv[2 * i + 1] = *(const float4*)(a.gain + 8u * g + 4u);
@@ -251,6 +267,36 @@ __global__ __launch_bounds__(64 * kGemvWaves) void vx_gemv_q4_kernel(VxGemvArgs 
     };
 #pragma unroll
     for (int u = 0; u < kU; ++u) issue(u);
+
+    if constexpr (SPL > 0) {
+        // LSE merge of the splits (m, l in the log2 domain; an empty split has m = -inf, l = 0):
+        // x = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s, the merge of
+        // tests/empirical_challenge_phase2/test2_split_k_flashdecoding_parity.cu:23-125
+#pragma unroll
+        for (int i = 0; i < GX; ++i) {
+            float M = -INFINITY;
+#pragma unroll
+            for (int sp = 0; sp < SPL; ++sp) M = fmaxf(M, pml[i][sp].x);
+            float L = 0.0f, w[SPL];
+#pragma unroll
+            for (int sp = 0; sp < SPL; ++sp) {
+                w[sp] = pml[i][sp].x == -INFINITY ? 0.0f : vx_exp2(pml[i][sp].x - M);
+                L += w[sp] * pml[i][sp].y;
+            }
+            const float invl = L > 0.0f ? 1.0f / L : 0.0f;
+            float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+#pragma unroll
+            for (int sp = 0; sp < SPL; ++sp) {
+                const float ws = w[sp] * invl;
+                x0.x += ws * po[i][sp][0].x; x0.y += ws * po[i][sp][0].y;
+                x0.z += ws * po[i][sp][0].z; x0.w += ws * po[i][sp][0].w;
+                x1.x += ws * po[i][sp][1].x; x1.y += ws * po[i][sp][1].y;
+                x1.z += ws * po[i][sp][1].z; x1.w += ws * po[i][sp][1].w;
+            }
+            xv[2 * i] = x0;
+            xv[2 * i + 1] = x1;
+        }
+    }
 
     // ---- RMSNorm scale (src/runtime.rs:588-601) from the registers, plus groups beyond them ----
     float inv_rms = 1.0f;
@@ -450,7 +496,6 @@ __global__ __launch_bounds__(256) void vx_argmax_finalize_kernel(const float* ca
 // workgroup of each KV head.
 // =============================================================================================
 namespace {
-__device__ __forceinline__ float vx_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Merge softmax state (m, l, o[8]) with a partner's, all in the log2 domain.
 template <int G>
@@ -495,38 +540,60 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     uint16_t* Vc = a.kv + ((size_t)a.hkv + g) * a.s_max * D;
     const uint32_t wstep = (uint32_t)(W * PPW);
 
-    // ---- cached K/V rows (positions < pos) of the first batch, issued before the prologue ----
-    uint4 kr[PF], vr[PF];
-    auto fetch = [&](uint32_t tb) {
-#pragma unroll
-        for (int j = 0; j < PF; ++j) {
-            const uint32_t t = tb + j * wstep + (uint32_t)(wave * PPW + grp);
-            if (t < t1 && t != pos) {
-                kr[j] = *(const uint4*)(Kc + (size_t)t * D + 8 * sub);
-                vr[j] = *(const uint4*)(Vc + (size_t)t * D + 8 * sub);
-            }
-        }
-    };
-    fetch(t0);
-
-    // ---- RoPE (src/runtime.rs:745-768) on this group's q heads and the new k; bf16 K/V row ----
+    // ---- q, the new k/v and the RoPE row into registers first: vector memory returns in issue
+    // order, so they arrive before the cold K/V rows fetched right after them ----
     const float* q = a.qkv;
     const float* k = a.qkv + (size_t)a.hq * D;
     const float* v = k + (size_t)a.hkv * D;
     const float2* rp = a.rope + (size_t)pos * HALF;
-    for (int p = tid; p < (G + 1) * HALF; p += NT) {
+    constexpr int NP = (G + 1) * HALF, RP = (NP + NT - 1) / NT;  // RoPE pairs, pairs per thread
+    float r1[RP], r2[RP];
+    float2 rcs[RP];
+#pragma unroll
+    for (int i = 0; i < RP; ++i) {
+        const int p = min(tid + i * NT, NP - 1);  // clamped: never a branch
         const int hh = p / HALF, j = p % HALF;
         const float* src = hh < G ? q + (size_t)(g * G + hh) * D : k + (size_t)g * D;
-        const float2 o = vx_rope_pair(src[j], src[j + HALF], rp[j]);
-        if (hh < G) {
-            q_s[hh * D + j] = o.x;
-            q_s[hh * D + j + HALF] = o.y;
-        } else {
-            kn_s[j] = vx_f32_to_bf16_bits(o.x);
-            kn_s[j + HALF] = vx_f32_to_bf16_bits(o.y);
+        r1[i] = src[j];
+        r2[i] = src[j + HALF];
+        rcs[i] = rp[j];
+    }
+    const float vnew = v[(size_t)g * D + min(tid, D - 1)];
+    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the K/V fetch
+
+    // ---- cached K/V rows (positions < pos) of the first batch. Loads are unconditional (a
+    // position past this split's range reads row min(t, pos), which is in the cache; the value is
+    // never used, and row pos itself is taken from LDS) so no load sits under a branch ----
+    uint4 kr[PF], vr[PF];
+    auto fetch = [&](uint32_t tb) {
+#pragma unroll
+        for (int j = 0; j < PF; ++j) {
+            const uint32_t t = min(tb + j * wstep + (uint32_t)(wave * PPW + grp), pos);
+            kr[j] = *(const uint4*)(Kc + (size_t)t * D + 8 * sub);
+            vr[j] = *(const uint4*)(Vc + (size_t)t * D + 8 * sub);
+        }
+    };
+    fetch(t0);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- RoPE (src/runtime.rs:745-768) on this group's q heads and the new k; bf16 K/V row.
+    // Computed unconditionally (clamped pairs) so the loads above are not sunk into the branch ----
+#pragma unroll
+    for (int i = 0; i < RP; ++i) {
+        const int p = tid + i * NT;
+        const float2 o = vx_rope_pair(r1[i], r2[i], rcs[i]);
+        if (p < NP) {
+            const int hh = p / HALF, j = p % HALF;
+            if (hh < G) {
+                q_s[hh * D + j] = o.x;
+                q_s[hh * D + j + HALF] = o.y;
+            } else {
+                kn_s[j] = vx_f32_to_bf16_bits(o.x);
+                kn_s[j + HALF] = vx_f32_to_bf16_bits(o.y);
+            }
         }
     }
-    for (int d = tid; d < D; d += NT) vn_s[d] = vx_f32_to_bf16_bits(v[(size_t)g * D + d]);
+    if (tid < D) vn_s[tid] = vx_f32_to_bf16_bits(vnew);
     __syncthreads();
     if (sp == 0) {
         for (int d = tid; d < D; d += NT) {
@@ -554,6 +621,7 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
         if (tb != t0) fetch(tb);
 #pragma unroll
         for (int j = 0; j < PF; ++j) {
+            if (tb + j * wstep >= t1) break;  // no position of this step is in range (uniform)
             const uint32_t t = tb + j * wstep + (uint32_t)(wave * PPW + grp);
             const bool valid = t < t1;
             // the new position comes from LDS (it may not have reached memory yet)
@@ -612,7 +680,7 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
             osum += w_o[w][idx] * wt;
         }
         const size_t hq_idx = (size_t)g * G + h;
-        if (a.splits == 1) {
+        if (a.splits == 1 && !a.partials_only) {
             a.out[hq_idx * D + d] = lsum > 0.0f ? osum / lsum : 0.0f;
         } else {
             a.part_o[(hq_idx * a.splits + sp) * D + d] = osum;
@@ -798,45 +866,57 @@ int vx_env_int(const char* name, int dflt) {
     return e ? (int)strtol(e, nullptr, 10) : dflt;
 }
 
-template <int S, int EPI, bool NORM, int GX>
+// Workgroups for n_tiles wave tiles: every wave gets ceil(n_tiles / waves) tiles for the largest
+// allowed grid, and the grid shrinks to the fewest waves that still need no more than that, so
+// the tile count per wave is as even as the shape allows (e.g. 14336 tiles -> 448 x 8 waves x 4).
+uint32_t vx_balanced_wgs(uint32_t n_tiles, uint32_t max_wgs) {
+    if (n_tiles == 0 || max_wgs == 0) return 1u;
+    const uint32_t max_waves = max_wgs * (uint32_t)kGemvWaves;
+    const uint32_t per_wave = (n_tiles + max_waves - 1u) / max_waves;
+    const uint32_t waves = (n_tiles + per_wave - 1u) / per_wave;
+    const uint32_t wgs = (waves + kGemvWaves - 1u) / kGemvWaves;
+    return wgs < 1u ? 1u : (wgs > max_wgs ? max_wgs : wgs);
+}
+
+template <int S, int EPI, bool NORM, int GX, int SPL>
 hipError_t vx_gemv_launch_t(const VxGemvArgs& a, uint32_t max_wgs, hipStream_t st) {
     constexpr int W = kGemvWaves;
     const uint32_t nb = a.k >> 5;
     const size_t lds = (size_t)a.k * 2u + (size_t)nb * 4u + 64u;
     static size_t attr_lds = 64u * 1024u;
     if (lds > attr_lds) {
-        if (hipFuncSetAttribute((const void*)vx_gemv_q4_kernel<S, EPI, NORM, GX>,
+        if (hipFuncSetAttribute((const void*)vx_gemv_q4_kernel<S, EPI, NORM, GX, SPL>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
             (void)hipGetLastError();
             return hipErrorInvalidValue;
         }
         attr_lds = lds;
     }
-    uint32_t wgs = (a.n_tiles + W - 1u) / W;
-    if (wgs > max_wgs) wgs = max_wgs;
-    if (wgs == 0) wgs = 1;
-    hipLaunchKernelGGL((vx_gemv_q4_kernel<S, EPI, NORM, GX>), dim3(wgs), dim3(64 * W), lds, st, a);
+    const uint32_t wgs = vx_balanced_wgs(a.n_tiles, max_wgs);
+    hipLaunchKernelGGL((vx_gemv_q4_kernel<S, EPI, NORM, GX, SPL>), dim3(wgs), dim3(64 * W), lds, st, a);
     return hipGetLastError();
 }
 
-// x register groups per thread: ceil(K / 8 / threads) rounded up to 1, 2 or 4 (larger K loops)
-template <int S, int EPI, bool NORM>
+// x register groups per thread: ceil(K / 8 / threads) rounded up to 1, 2 or 4 (larger K loops;
+// merged attention partials must fit the registers)
+template <int S, int EPI, bool NORM, int SPL>
 hipError_t vx_gemv_dispatch_gx(const VxGemvArgs& a, uint32_t max_wgs, hipStream_t st) {
     const uint32_t per = ((a.k >> 3) + 64u * kGemvWaves - 1u) / (64u * kGemvWaves);
-    if (per <= 1u) return vx_gemv_launch_t<S, EPI, NORM, 1>(a, max_wgs, st);
-    if (per <= 2u) return vx_gemv_launch_t<S, EPI, NORM, 2>(a, max_wgs, st);
-    return vx_gemv_launch_t<S, EPI, NORM, 4>(a, max_wgs, st);
+    if (per <= 1u) return vx_gemv_launch_t<S, EPI, NORM, 1, SPL>(a, max_wgs, st);
+    if (per <= 2u) return vx_gemv_launch_t<S, EPI, NORM, 2, SPL>(a, max_wgs, st);
+    if (SPL > 0 && per > 4u) return hipErrorInvalidValue;
+    return vx_gemv_launch_t<S, EPI, NORM, 4, SPL>(a, max_wgs, st);
 }
 
-template <int EPI, bool NORM>
+template <int EPI, bool NORM, int SPL>
 hipError_t vx_gemv_dispatch_s(uint32_t s, const VxGemvArgs& a, uint32_t max_wgs, hipStream_t st) {
     switch (s) {
-        case 4: return vx_gemv_dispatch_gx<4, EPI, NORM>(a, max_wgs, st);
-        case 8: return vx_gemv_dispatch_gx<8, EPI, NORM>(a, max_wgs, st);
-        case 16: return vx_gemv_dispatch_gx<16, EPI, NORM>(a, max_wgs, st);
-        case 32: return vx_gemv_dispatch_gx<32, EPI, NORM>(a, max_wgs, st);
+        case 4: return vx_gemv_dispatch_gx<4, EPI, NORM, SPL>(a, max_wgs, st);
+        case 8: return vx_gemv_dispatch_gx<8, EPI, NORM, SPL>(a, max_wgs, st);
+        case 16: return vx_gemv_dispatch_gx<16, EPI, NORM, SPL>(a, max_wgs, st);
+        case 32: return vx_gemv_dispatch_gx<32, EPI, NORM, SPL>(a, max_wgs, st);
         case 64:
-            if constexpr (EPI != VX_EPI_SWIGLU) return vx_gemv_dispatch_gx<64, EPI, NORM>(a, max_wgs, st);
+            if constexpr (EPI != VX_EPI_SWIGLU) return vx_gemv_dispatch_gx<64, EPI, NORM, SPL>(a, max_wgs, st);
             return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
@@ -846,10 +926,20 @@ template <int EPI>
 hipError_t vx_gemv_dispatch_norm(uint32_t s, const VxGemvArgs& a, uint32_t max_wgs, hipStream_t st) {
     if constexpr (EPI == VX_EPI_RESID) {
         if (a.gain) return hipErrorInvalidValue;  // the residual epilogue takes raw activations
-        return vx_gemv_dispatch_s<EPI, false>(s, a, max_wgs, st);
+        if (!a.part_o) return vx_gemv_dispatch_s<EPI, false, 0>(s, a, max_wgs, st);
+        // o_proj over split-K attention partials: 8-element groups must not straddle heads
+        if (!a.part_ml || a.att_d == 0 || (a.att_d & 7u) || a.k % a.att_d) return hipErrorInvalidValue;
+        switch (a.att_splits) {
+            case 1: return vx_gemv_dispatch_s<EPI, false, 1>(s, a, max_wgs, st);
+            case 2: return vx_gemv_dispatch_s<EPI, false, 2>(s, a, max_wgs, st);
+            case 4: return vx_gemv_dispatch_s<EPI, false, 4>(s, a, max_wgs, st);
+            case 8: return vx_gemv_dispatch_s<EPI, false, 8>(s, a, max_wgs, st);
+            default: return hipErrorInvalidValue;
+        }
     } else {
-        return a.gain ? vx_gemv_dispatch_s<EPI, true>(s, a, max_wgs, st)
-                      : vx_gemv_dispatch_s<EPI, false>(s, a, max_wgs, st);
+        if (a.part_o) return hipErrorInvalidValue;
+        return a.gain ? vx_gemv_dispatch_s<EPI, true, 0>(s, a, max_wgs, st)
+                      : vx_gemv_dispatch_s<EPI, false, 0>(s, a, max_wgs, st);
     }
 }
 
@@ -858,7 +948,7 @@ hipError_t vx_attn_launch_t(const VxAttnArgs& a, hipStream_t st) {
     constexpr int W = 8;
     hipLaunchKernelGGL((vx_attn_kernel<D, G, W>), dim3(a.splits, a.hkv), dim3(64 * W), 0, st, a);
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && a.splits > 1) {
+    if (e == hipSuccess && a.splits > 1 && !a.partials_only) {
         hipLaunchKernelGGL((vx_attn_merge_kernel<D>), dim3(a.hq), dim3(D), 0, st, a);
         e = hipGetLastError();
     }
@@ -902,11 +992,7 @@ hipError_t vx_launch_argmax_finalize(const float* cand_v, const uint32_t* cand_i
     return hipGetLastError();
 }
 
-uint32_t vx_gemv_grid(uint32_t n_tiles, uint32_t max_wgs) {
-    uint32_t wgs = (n_tiles + kGemvWaves - 1u) / kGemvWaves;
-    if (wgs > max_wgs) wgs = max_wgs;
-    return wgs ? wgs : 1u;
-}
+uint32_t vx_gemv_grid(uint32_t n_tiles, uint32_t max_wgs) { return vx_balanced_wgs(n_tiles, max_wgs); }
 
 hipError_t vx_launch_attention(const VxAttnArgs& a, uint32_t d, hipStream_t st) {
     if (a.hkv == 0 || a.hq % a.hkv != 0 || a.splits == 0 || a.splits > 64 || a.s_max == 0) return hipErrorInvalidValue;
