@@ -29,6 +29,21 @@ sys.path.insert(0, ROOT)
 METRIC = "decode tok/s + achieved HBM GB/s (% of ~8 TB/s), Llama-3-8B Q4 bs=1, 1 GPU"
 HBM_PEAK_GBPS = 8000.0
 PROMPT_LEN = 128
+# HBM bytes per launch of the dominant kernel, measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+# and scaled by a copy kernel of known size; the file records the commands and the raw counters.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gate_up_gemv_hbm_traffic.md")
+
+
+def measured_traffic() -> int | None:
+    """`traffic_bytes_per_launch = N` from the committed counter summary, if present."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch ="):
+                    return int(line.split("=", 1)[1].strip().split()[0])
+    except OSError:
+        return None
+    return None
 
 
 def cpu_baseline(seed: int) -> dict:
@@ -78,6 +93,9 @@ def main() -> int:
     ap.add_argument("--kernel-passes", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--prompt-len", type=int, default=PROMPT_LEN)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="afterwards run a device-to-device copy of MIB MiB (byte-counter yardstick)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures the single-GPU decode step only; --gpus {args.gpus} is not supported "
@@ -88,13 +106,16 @@ def main() -> int:
     from velox_amd.engine import run
 
     L.load()
-    print(f"[bench] llama3_8b Q4_0 decode: prompt {PROMPT_LEN}, warmup {args.warmup}, steps {args.steps}",
+    plen = args.prompt_len
+    print(f"[bench] llama3_8b Q4_0 decode: prompt {plen}, warmup {args.warmup}, steps {args.steps}",
           file=sys.stderr, flush=True)
-    rep, toks = run("llama3_8b", prompt_len=PROMPT_LEN, warmup=args.warmup, steps=args.steps, seed=args.seed,
+    rep, toks = run("llama3_8b", prompt_len=plen, warmup=args.warmup, steps=args.steps, seed=args.seed,
                     use_graph=not args.no_graph, kernel_passes=args.kernel_passes)
     print(f"[bench] decode done: {rep['tok_per_s']:.1f} tok/s, {rep['hbm_gbps']:.0f} GB/s; gate/up kernel "
           f"{rep['kernel_us']:.2f} us", file=sys.stderr, flush=True)
 
+    if args.copy_calibration > 0:
+        L.device_copy_calibration(args.copy_calibration << 20)
     kernel_gbps = rep["kernel_bytes"] / (rep["kernel_us"] * 1e-6) / 1e9 if rep["kernel_us"] > 0 else 0.0
     out = {
         "metric": METRIC,
@@ -112,8 +133,8 @@ def main() -> int:
         "config": {
             "workload": "llama3_8b_q4_0_decode_bs1",
             "batch": 1,
-            "prompt_tokens": PROMPT_LEN,
-            "timed_positions": [PROMPT_LEN + args.warmup, PROMPT_LEN + args.warmup + args.steps - 1],
+            "prompt_tokens": plen,
+            "timed_positions": [plen + args.warmup, plen + args.warmup + args.steps - 1],
             "hipgraph": not args.no_graph,
         },
         "hbm_gbps": round(rep["hbm_gbps"], 1),
@@ -128,11 +149,11 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "avg_us": round(rep["kernel_us"], 3),
             "bytes_per_launch": int(rep["kernel_bytes"]),
         },
-        "first_tokens": toks[PROMPT_LEN - 1:PROMPT_LEN + 7],
+        "first_tokens": toks[plen - 1:plen + 7],
     }
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline (oracle, bounded sample)...", file=sys.stderr, flush=True)

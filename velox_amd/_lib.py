@@ -183,3 +183,30 @@ def memcpy_htod(dst_dev_ptr: int, src_host_ptr: int, nbytes: int) -> None:
     rc = hip().hipMemcpy(dst_dev_ptr, src_host_ptr, nbytes, 1)
     if rc != 0:
         raise RuntimeError(f"hipMemcpy HtoD failed: {rc}")
+
+
+def device_copy_calibration(nbytes: int, reps: int = 3) -> None:
+    """hipMemcpy device->device of `nbytes`, `reps` times: a plain copy kernel of known size
+    (reads and writes nbytes per dispatch), the yardstick for the HBM byte counters under
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE."""
+    h = hip()
+    h.hipMalloc.restype = C.c_int
+    h.hipMalloc.argtypes = [C.POINTER(_P), C.c_size_t]
+    h.hipFree.restype = C.c_int
+    h.hipFree.argtypes = [_P]
+    h.hipMemset.restype = C.c_int
+    h.hipMemset.argtypes = [_P, C.c_int, C.c_size_t]
+    src, dst = _P(), _P()
+    if h.hipMalloc(C.byref(src), nbytes) or h.hipMalloc(C.byref(dst), nbytes):
+        raise RuntimeError("hipMalloc failed")
+    try:
+        if h.hipMemset(src, 1, nbytes):
+            raise RuntimeError("hipMemset failed")
+        for _ in range(reps):
+            if h.hipMemcpy(dst, src, nbytes, 3):
+                raise RuntimeError("hipMemcpy DtoD failed")
+        if h.hipDeviceSynchronize():
+            raise RuntimeError("hipDeviceSynchronize failed")
+    finally:
+        h.hipFree(src)
+        h.hipFree(dst)
