@@ -491,57 +491,58 @@ __global__ __launch_bounds__(256) void vx_argmax_finalize_kernel(const float* ca
 }
 
 // =============================================================================================
-// Split-K decode attention: RoPE + bf16 KV append prologue, per-lane-group online softmax over
-// coalesced 16-byte K/V rows, LSE merge within the workgroup, then across splits by the last
-// workgroup of each KV head.
+// Split-K decode attention with LDS-staged K/V tiles
 // =============================================================================================
-namespace {
 
-// Merge softmax state (m, l, o[8]) with a partner's, all in the log2 domain.
-template <int G>
-__device__ __forceinline__ void vx_merge_state(float (&m)[G], float (&l)[G], float (&o)[G][8], int off) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        const float m2 = __shfl_xor(m[h], off), l2 = __shfl_xor(l[h], off);
-        const float mn = fmaxf(m[h], m2);
-        const float w1 = (m[h] == -INFINITY) ? 0.0f : vx_exp2(m[h] - mn);
-        const float w2 = (m2 == -INFINITY) ? 0.0f : vx_exp2(m2 - mn);
-        l[h] = l[h] * w1 + l2 * w2;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float o2 = __shfl_xor(o[h][e], off);
-            o[h][e] = o[h][e] * w1 + o2 * w2;
-        }
-        m[h] = mn;
-    }
+// Decode attention for one (split, kv head): RoPE of q and the new k (src/runtime.rs:745-768),
+// bf16 KV append, then softmax(q K^T / sqrt(D)) V over this split's positions
+// (src/runtime.rs:772-831) in tiles of kAttnTile positions staged in LDS:
+//   1. the tile's K and V rows are loaded with unconditional 16-byte loads (clamped rows) right
+//      behind q/k/v and the RoPE row, so one memory round trip brings everything;
+//   2. scores: a lane group of D/8 lanes per position, 8 dimensions per lane, DPP group sum;
+//   3. per head (one wave each), the tile's max, 2^(s - m) and sum, with the running (m, l) of the
+//      online softmax in the log2 domain;
+//   4. P V: one thread per (head, dimension) output, accumulating across tiles.
+// The result is the split's (m, l, o) partial (o unnormalized), merged by the o_proj GEMV or by
+// vx_attn_merge_kernel, or with one split and no consumer merge, the normalized output.
+constexpr int kAttnTile = 128;
+
+template <int D, int G, int W>
+constexpr size_t vx_attn_lds_bytes() {
+    return (size_t)2 * kAttnTile * D * 2 + (size_t)G * D * 4 + (size_t)G * kAttnTile * 4 + (size_t)2 * D * 2 +
+           (size_t)G * 4 * 4;
 }
-}  // namespace
 
 template <int D, int G, int W>
 __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     if ((a.active_mask & 1ULL) == 0ULL) return;
-    constexpr int HALF = D / 2, LPP = D / 8, PPW = 64 / LPP, NT = 64 * W;  // lanes per position, positions/wave step
-    constexpr int PF = 8;  // positions in flight per lane group
+    constexpr int HALF = D / 2, LPP = D / 8, NT = 64 * W, T = kAttnTile;
+    constexpr int NGRP = NT / LPP;                         // positions per score pass
+    constexpr int CPR = D / 8;                             // 16-byte chunks per K (or V) row
+    constexpr int NLD = (2 * T * CPR + NT - 1) / NT;       // tile chunks per thread
+    constexpr int OPT = (G * D + NT - 1) / NT;             // P V outputs per thread
     constexpr float kLog2e = 1.4426950408889634f;
-    __shared__ float q_s[G * D];
-    __shared__ __align__(16) uint16_t kn_s[D], vn_s[D];
-    __shared__ float w_m[W][G], w_l[W][G];
-    __shared__ float w_o[W][G * D];
+    static_assert(W >= G, "one wave per head for the softmax statistics");
+    extern __shared__ __align__(16) unsigned char vx_smem[];
+    uint16_t* k_s = (uint16_t*)vx_smem;                    // [T][D] bf16
+    uint16_t* v_s = k_s + T * D;                           // [T][D] bf16
+    float* q_s = (float*)(v_s + T * D);                    // [G][D], pre-scaled
+    float* p_s = q_s + G * D;                              // [G][T] scores, then probabilities
+    uint16_t* kn_s = (uint16_t*)(p_s + G * T);             // new position's k (RoPE'd), v
+    uint16_t* vn_s = kn_s + D;
+    float* st_s = (float*)(vn_s + D);                      // [G][4]: m, l, alpha
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t g = blockIdx.y, sp = blockIdx.x;
     const uint64_t step = a.state ? a.state->step : (uint64_t)a.fixed_pos;
     const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;  // safe_step clamp
     const uint32_t len = pos + 1u;
     const uint32_t chunk = (len + a.splits - 1u) / a.splits;
-    const uint32_t t0 = sp * chunk;
+    const uint32_t t0 = min(sp * chunk, len);
     const uint32_t t1 = min(len, t0 + chunk);
-    const int grp = lane / LPP, sub = lane % LPP;
     uint16_t* Kc = a.kv + (size_t)g * a.s_max * D;
     uint16_t* Vc = a.kv + ((size_t)a.hkv + g) * a.s_max * D;
-    const uint32_t wstep = (uint32_t)(W * PPW);
 
-    // ---- q, the new k/v and the RoPE row into registers first: vector memory returns in issue
-    // order, so they arrive before the cold K/V rows fetched right after them ----
+    // ---- q, the new k/v and the RoPE row into registers (clamped: no load under a branch) ----
     const float* q = a.qkv;
     const float* k = a.qkv + (size_t)a.hq * D;
     const float* v = k + (size_t)a.hkv * D;
@@ -551,7 +552,7 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     float2 rcs[RP];
 #pragma unroll
     for (int i = 0; i < RP; ++i) {
-        const int p = min(tid + i * NT, NP - 1);  // clamped: never a branch
+        const int p = min(tid + i * NT, NP - 1);
         const int hh = p / HALF, j = p % HALF;
         const float* src = hh < G ? q + (size_t)(g * G + hh) * D : k + (size_t)g * D;
         r1[i] = src[j];
@@ -559,25 +560,25 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
         rcs[i] = rp[j];
     }
     const float vnew = v[(size_t)g * D + min(tid, D - 1)];
-    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the K/V fetch
+    __builtin_amdgcn_sched_barrier(0);  // these loads go out ahead of the K/V tile
 
-    // ---- cached K/V rows (positions < pos) of the first batch. Loads are unconditional (a
-    // position past this split's range reads row min(t, pos), which is in the cache; the value is
-    // never used, and row pos itself is taken from LDS) so no load sits under a branch ----
-    uint4 kr[PF], vr[PF];
-    auto fetch = [&](uint32_t tb) {
+    // ---- K/V rows of a tile [tb, tb + T) into registers (rows past the split read row
+    // min(t, pos): in the cache, never used) ----
+    uint4 kv[NLD];
+    auto load_tile = [&](uint32_t tb) {
 #pragma unroll
-        for (int j = 0; j < PF; ++j) {
-            const uint32_t t = min(tb + j * wstep + (uint32_t)(wave * PPW + grp), pos);
-            kr[j] = *(const uint4*)(Kc + (size_t)t * D + 8 * sub);
-            vr[j] = *(const uint4*)(Vc + (size_t)t * D + 8 * sub);
+        for (int j = 0; j < NLD; ++j) {
+            const int i = min(tid + j * NT, 2 * T * CPR - 1);
+            const int part = i / (T * CPR), r = (i % (T * CPR)) / CPR, c = i % CPR;
+            const uint32_t t = min(tb + (uint32_t)r, pos);
+            kv[j] = *(const uint4*)((part ? Vc : Kc) + (size_t)t * D + 8 * c);
         }
     };
-    fetch(t0);
+    load_tile(t0);
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- RoPE (src/runtime.rs:745-768) on this group's q heads and the new k; bf16 K/V row.
-    // Computed unconditionally (clamped pairs) so the loads above are not sunk into the branch ----
+    // ---- RoPE on this group's q heads and the new k; bf16 K/V row ----
+    const float qscale = a.scale * kLog2e;  // scores in the log2 domain
 #pragma unroll
     for (int i = 0; i < RP; ++i) {
         const int p = tid + i * NT;
@@ -585,8 +586,8 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
         if (p < NP) {
             const int hh = p / HALF, j = p % HALF;
             if (hh < G) {
-                q_s[hh * D + j] = o.x;
-                q_s[hh * D + j + HALF] = o.y;
+                q_s[hh * D + j] = o.x * qscale;
+                q_s[hh * D + j + HALF] = o.y * qscale;
             } else {
                 kn_s[j] = vx_f32_to_bf16_bits(o.x);
                 kn_s[j + HALF] = vx_f32_to_bf16_bits(o.y);
@@ -594,6 +595,10 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
         }
     }
     if (tid < D) vn_s[tid] = vx_f32_to_bf16_bits(vnew);
+    if (tid < G) {
+        st_s[tid * 4 + 0] = -INFINITY;  // running m
+        st_s[tid * 4 + 1] = 0.0f;       // running l
+    }
     __syncthreads();
     if (sp == 0) {
         for (int d = tid; d < D; d += NT) {
@@ -601,92 +606,118 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
             Vc[(size_t)pos * D + d] = vn_s[d];
         }
     }
-
-    // ---- scores and online softmax: lane group grp handles one position per step ----
-    const float qscale = a.scale * kLog2e;
+    const int grp = tid / LPP, sub = tid % LPP;
     float qv[G][8];
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
         for (int e = 0; e < 8; ++e) qv[h][e] = q_s[h * D + 8 * sub + e];
-    float m[G], l[G], o[G][8];
+    float acc[OPT];
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-        m[h] = -INFINITY;
-        l[h] = 0.0f;
+    for (int i = 0; i < OPT; ++i) acc[i] = 0.0f;
+
+    for (uint32_t tb = t0; tb < t1; tb += T) {
+        if (tb != t0) load_tile(tb);
+        const int tt = (int)min((uint32_t)T, t1 - tb);  // positions in this tile
+        // stage the tile; the current position comes from the RoPE'd k / new v (the cache write
+        // above may not have landed)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
-    }
-    for (uint32_t tb = t0; tb < t1; tb += PF * wstep) {
-        if (tb != t0) fetch(tb);
-#pragma unroll
-        for (int j = 0; j < PF; ++j) {
-            if (tb + j * wstep >= t1) break;  // no position of this step is in range (uniform)
-            const uint32_t t = tb + j * wstep + (uint32_t)(wave * PPW + grp);
-            const bool valid = t < t1;
-            // the new position comes from LDS (it may not have reached memory yet)
-            const uint4 kq = (t == pos) ? *(const uint4*)(kn_s + 8 * sub) : kr[j];
-            const uint4 vq = (t == pos) ? *(const uint4*)(vn_s + 8 * sub) : vr[j];
+        for (int j = 0; j < NLD; ++j) {
+            const int i = tid + j * NT;
+            if (i < 2 * T * CPR) {
+                const int part = i / (T * CPR), r = (i % (T * CPR)) / CPR, c = i % CPR;
+                uint4 val = kv[j];
+                if (tb + (uint32_t)r == pos) val = *(const uint4*)((part ? vn_s : kn_s) + 8 * c);
+                *(uint4*)((part ? v_s : k_s) + r * D + 8 * c) = val;
+            }
+        }
+        __syncthreads();
+        // scores s[h][r] = q_h . k_r (q pre-scaled)
+        for (int r = grp; r < tt; r += NGRP) {
+            const uint4 kq = *(const uint4*)(k_s + r * D + 8 * sub);
             const uint32_t kw[4] = {kq.x, kq.y, kq.z, kq.w};
-            const uint32_t vw[4] = {vq.x, vq.y, vq.z, vq.w};
-            float kf[8], vf[8];
+            float kf[8];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 kf[2 * e] = __builtin_bit_cast(float, kw[e] << 16);
                 kf[2 * e + 1] = __builtin_bit_cast(float, kw[e] & 0xFFFF0000u);
-                vf[2 * e] = __builtin_bit_cast(float, vw[e] << 16);
-                vf[2 * e + 1] = __builtin_bit_cast(float, vw[e] & 0xFFFF0000u);
             }
 #pragma unroll
             for (int h = 0; h < G; ++h) {
                 float sc = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) sc += qv[h][e] * kf[e];
-                sc = vx_group_sum<LPP>(sc) * qscale;
-                if (valid) {
-                    const float mn = fmaxf(m[h], sc);
-                    const float alpha = (m[h] == -INFINITY) ? 0.0f : vx_exp2(m[h] - mn);
-                    const float p = vx_exp2(sc - mn);
-                    l[h] = l[h] * alpha + p;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) o[h][e] = o[h][e] * alpha + p * vf[e];
-                    m[h] = mn;
-                }
+                sc = vx_group_sum<LPP>(sc);
+                if (sub == 0) p_s[h * T + r] = sc;
             }
         }
-    }
-    // ---- merge: lane groups of a wave, then the W waves ----
+        __syncthreads();
+        // per head: tile max, probabilities, running (m, l) and the rescale factor alpha
+        if (wave < G) {
+            const int h = wave;
+            float sv[T / 64];
+            float mt = -INFINITY;
 #pragma unroll
-    for (int off = LPP; off < 64; off <<= 1) vx_merge_state<G>(m, l, o, off);
-    if (grp == 0) {
+            for (int i = 0; i < T / 64; ++i) {
+                sv[i] = lane + 64 * i < tt ? p_s[h * T + lane + 64 * i] : -INFINITY;
+                mt = fmaxf(mt, sv[i]);
+            }
+            mt = vx_wave_max(mt);
+            const float m_old = st_s[h * 4 + 0];
+            const float m_new = fmaxf(m_old, mt);
+            float lt = 0.0f;
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) w_o[wave][h * D + 8 * sub + e] = o[h][e];
-            if (sub == 0) { w_m[wave][h] = m[h]; w_l[wave][h] = l[h]; }
+            for (int i = 0; i < T / 64; ++i) {
+                const float pr = sv[i] == -INFINITY ? 0.0f : vx_exp2(sv[i] - m_new);
+                p_s[h * T + lane + 64 * i] = pr;
+                lt += pr;
+            }
+            lt = vx_wave_sum(lt);
+            if (lane == 0) {
+                const float alpha = m_old == -INFINITY ? 0.0f : vx_exp2(m_old - m_new);
+                st_s[h * 4 + 0] = m_new;
+                st_s[h * 4 + 1] = st_s[h * 4 + 1] * alpha + lt;
+                st_s[h * 4 + 2] = alpha;
+            }
         }
-    }
-    __syncthreads();
-    for (int idx = tid; idx < G * D; idx += NT) {
-        const int h = idx / D, d = idx % D;
-        float mn = -INFINITY;
+        __syncthreads();
+        // P V: thread -> (head, dimension)
 #pragma unroll
-        for (int w = 0; w < W; ++w) mn = fmaxf(mn, w_m[w][h]);
-        float lsum = 0.0f, osum = 0.0f;
-#pragma unroll
-        for (int w = 0; w < W; ++w) {
-            const float wt = (w_m[w][h] == -INFINITY) ? 0.0f : vx_exp2(w_m[w][h] - mn);
-            lsum += w_l[w][h] * wt;
-            osum += w_o[w][idx] * wt;
+        for (int i = 0; i < OPT; ++i) {
+            const int idx = tid + i * NT;
+            if (idx < G * D) {
+                const int h = idx / D, d = idx % D;
+                float o = acc[i] * st_s[h * 4 + 2];
+                const float* ph = p_s + h * T;
+                for (int r = 0; r < tt; r += 4) {
+                    const float4 pr = *(const float4*)(ph + r);  // rows >= tt hold p = 0
+                    o += pr.x * __builtin_bit_cast(float, (uint32_t)v_s[(r + 0) * D + d] << 16);
+                    o += pr.y * __builtin_bit_cast(float, (uint32_t)v_s[(r + 1) * D + d] << 16);
+                    o += pr.z * __builtin_bit_cast(float, (uint32_t)v_s[(r + 2) * D + d] << 16);
+                    o += pr.w * __builtin_bit_cast(float, (uint32_t)v_s[(r + 3) * D + d] << 16);
+                }
+                acc[i] = o;
+            }
         }
-        const size_t hq_idx = (size_t)g * G + h;
-        if (a.splits == 1 && !a.partials_only) {
-            a.out[hq_idx * D + d] = lsum > 0.0f ? osum / lsum : 0.0f;
-        } else {
-            a.part_o[(hq_idx * a.splits + sp) * D + d] = osum;
-            if (d == 0) {
-                a.part_ml[(hq_idx * a.splits + sp) * 2] = mn;
-                a.part_ml[(hq_idx * a.splits + sp) * 2 + 1] = lsum;
+        __syncthreads();  // the next tile overwrites k_s, v_s and p_s
+    }
+
+    // ---- this split's partial (or the normalized output) ----
+#pragma unroll
+    for (int i = 0; i < OPT; ++i) {
+        const int idx = tid + i * NT;
+        if (idx < G * D) {
+            const int h = idx / D, d = idx % D;
+            const size_t hq_idx = (size_t)g * G + h;
+            const float m_h = st_s[h * 4 + 0], l_h = st_s[h * 4 + 1];
+            if (a.splits == 1 && !a.partials_only) {
+                a.out[hq_idx * D + d] = l_h > 0.0f ? acc[i] / l_h : 0.0f;
+            } else {
+                a.part_o[(hq_idx * a.splits + sp) * D + d] = acc[i];
+                if (d == 0) {
+                    a.part_ml[(hq_idx * a.splits + sp) * 2] = m_h;
+                    a.part_ml[(hq_idx * a.splits + sp) * 2 + 1] = l_h;
+                }
             }
         }
     }
@@ -946,7 +977,17 @@ hipError_t vx_gemv_dispatch_norm(uint32_t s, const VxGemvArgs& a, uint32_t max_w
 template <int D, int G>
 hipError_t vx_attn_launch_t(const VxAttnArgs& a, hipStream_t st) {
     constexpr int W = 8;
-    hipLaunchKernelGGL((vx_attn_kernel<D, G, W>), dim3(a.splits, a.hkv), dim3(64 * W), 0, st, a);
+    constexpr size_t lds = vx_attn_lds_bytes<D, G, W>();
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void*)vx_attn_kernel<D, G, W>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds) != hipSuccess) {
+            (void)hipGetLastError();
+            return hipErrorInvalidValue;
+        }
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((vx_attn_kernel<D, G, W>), dim3(a.splits, a.hkv), dim3(64 * W), lds, st, a);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && a.splits > 1 && !a.partials_only) {
         hipLaunchKernelGGL((vx_attn_merge_kernel<D>), dim3(a.hq), dim3(D), 0, st, a);
