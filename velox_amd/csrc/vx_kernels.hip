@@ -192,7 +192,15 @@ __global__ __launch_bounds__(64 * kGemvWaves) void vx_gemv_q4_kernel(VxGemvArgs 
     const int r = lane / S, s = lane % S;
     const uint32_t waves_total = gridDim.x * W, gw = blockIdx.x * W + wave;
     uint32_t first, step, my_tiles;
-    if (a.contig) {
+    if (a.contig == 2u) {
+        // workgroup blocks: workgroup b owns tiles [b n / grid, (b + 1) n / grid), dealt to its W
+        // waves round-robin, so every workgroup (every CU) streams the same number of tiles
+        const uint32_t b0 = (uint32_t)(((uint64_t)blockIdx.x * a.n_tiles) / gridDim.x);
+        const uint32_t b1 = (uint32_t)(((uint64_t)(blockIdx.x + 1u) * a.n_tiles) / gridDim.x);
+        first = b0 + (uint32_t)wave;
+        step = (uint32_t)W;
+        my_tiles = first < b1 ? (b1 - 1u - first) / (uint32_t)W + 1u : 0u;
+    } else if (a.contig) {
         const uint32_t per = (a.n_tiles + waves_total - 1u) / waves_total;
         first = gw * per;
         step = 1u;
@@ -897,11 +905,26 @@ int vx_env_int(const char* name, int dflt) {
     return e ? (int)strtol(e, nullptr, 10) : dflt;
 }
 
-// Workgroups for n_tiles wave tiles: every wave gets ceil(n_tiles / waves) tiles for the largest
-// allowed grid, and the grid shrinks to the fewest waves that still need no more than that, so
-// the tile count per wave is as even as the shape allows (e.g. 14336 tiles -> 448 x 8 waves x 4).
-uint32_t vx_balanced_wgs(uint32_t n_tiles, uint32_t max_wgs) {
+// GEMV grid for n_tiles wave tiles. The tile schedule (VELOX_HIP_GEMV_SCHED, for tuning):
+//   3 (default) workgroup blocks: min(ceil(n_tiles / W), 512, max_wgs) workgroups, each owning an
+//     equal contiguous block of tiles dealt to its waves round-robin, so every CU streams the
+//     same share however the workgroups are placed;
+//   2 the same over <= 256 workgroups;
+//   1 tiles round-robin over all waves, min(ceil(n_tiles / W), max_wgs) workgroups;
+//   0 round-robin on the fewest waves that keep the largest per-wave tile count.
+// Llama-3-8B decode: 714 / 708 / 708 / 700 tok/s for 3 / 2 / 1 / 0.
+uint32_t vx_gemv_wgs(uint32_t n_tiles, uint32_t max_wgs) {
     if (n_tiles == 0 || max_wgs == 0) return 1u;
+    const int sched = vx_env_int("VELOX_HIP_GEMV_SCHED", 3);
+    if (sched == 1) {  // round-robin, plain cap
+        const uint32_t w = (n_tiles + kGemvWaves - 1u) / kGemvWaves;
+        return w > max_wgs ? max_wgs : (w ? w : 1u);
+    }
+    if (sched == 2 || sched == 3) {  // workgroup blocks over <= 256 (2) or <= 512 (3) workgroups
+        const uint32_t cap = min(sched == 2 ? 256u : 512u, max_wgs);
+        const uint32_t w = (n_tiles + kGemvWaves - 1u) / kGemvWaves;
+        return w > cap ? cap : (w ? w : 1u);
+    }
     const uint32_t max_waves = max_wgs * (uint32_t)kGemvWaves;
     const uint32_t per_wave = (n_tiles + max_waves - 1u) / max_waves;
     const uint32_t waves = (n_tiles + per_wave - 1u) / per_wave;
@@ -923,7 +946,7 @@ hipError_t vx_gemv_launch_t(const VxGemvArgs& a, uint32_t max_wgs, hipStream_t s
         }
         attr_lds = lds;
     }
-    const uint32_t wgs = vx_balanced_wgs(a.n_tiles, max_wgs);
+    const uint32_t wgs = vx_gemv_wgs(a.n_tiles, max_wgs);
     hipLaunchKernelGGL((vx_gemv_q4_kernel<S, EPI, NORM, GX, SPL>), dim3(wgs), dim3(64 * W), lds, st, a);
     return hipGetLastError();
 }
@@ -1014,6 +1037,10 @@ hipError_t vx_launch_gemv(const VxMat& m, const VxGemvArgs& a0, int epi, uint32_
     a.n_tiles = m.n_tiles;
     a.n_iter = m.n_iter;
     a.contig = (uint32_t)vx_env_int("VELOX_HIP_GEMV_CONTIG", 0);
+    {
+        const int sched = vx_env_int("VELOX_HIP_GEMV_SCHED", 3);
+        if (sched == 2 || sched == 3) a.contig = 2u;
+    }
     if (m.k == 0 || (m.k & 31u) != 0) return hipErrorInvalidValue;
     if ((epi == VX_EPI_SWIGLU) != (m.paired != 0)) return hipErrorInvalidValue;
     switch (epi) {
@@ -1033,7 +1060,7 @@ hipError_t vx_launch_argmax_finalize(const float* cand_v, const uint32_t* cand_i
     return hipGetLastError();
 }
 
-uint32_t vx_gemv_grid(uint32_t n_tiles, uint32_t max_wgs) { return vx_balanced_wgs(n_tiles, max_wgs); }
+uint32_t vx_gemv_grid(uint32_t n_tiles, uint32_t max_wgs) { return vx_gemv_wgs(n_tiles, max_wgs); }
 
 hipError_t vx_launch_attention(const VxAttnArgs& a, uint32_t d, hipStream_t st) {
     if (a.hkv == 0 || a.hq % a.hkv != 0 || a.splits == 0 || a.splits > 64 || a.s_max == 0) return hipErrorInvalidValue;
