@@ -112,3 +112,25 @@ def test_run_with_explicit_prompt_tokens(oracle):
     assert rep_a["status"] == rep_b["status"] == 0 and toks_a == toks_b
     with pytest.raises(RuntimeError):
         run("smollm_135m", prompt=[1, 49152], warmup=0, steps=1, seed=seed, num_layers=1, max_seq_len=8)
+
+
+def test_runner_binary_stdout_contract(oracle):
+    """velox_hip_runner as src/cli.rs:640-770 spawns it: --weights/--tokens/--steps/--verbose, one
+    "[Step N] Token: id" line per generated token (parsed at src/cli.rs:706-733) and the report
+    block; the tokens equal the library's own greedy decode of the same prompt."""
+    import os
+    import re
+    import subprocess
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    runner = os.path.join(root, "velox_amd", "lib", "velox_hip_runner")
+    prompt = [int(t) for t in oracle.prompt_tokens(31, 5, 49152)]
+    r = subprocess.run([runner, "--model", "smollm_135m", "--weights", "synthetic", "--tokens",
+                        ",".join(map(str, prompt)), "--steps", "6", "--seed", "31", "--verbose"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    steps = re.findall(r"^\[Step (\d+)\] Token: (\d+)$", r.stdout, re.M)
+    assert [int(s) for s, _ in steps] == list(range(6))
+    assert re.search(r"Decode Latency \(\d+ tok\): [\d.]+ ms \([\d.]+ tok/s", r.stdout)
+    _, toks = run("smollm_135m", prompt=prompt, warmup=0, steps=5, seed=31)
+    assert [int(t) for _, t in steps] == toks[len(prompt) - 1:len(prompt) - 1 + 6]
