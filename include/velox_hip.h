@@ -235,6 +235,10 @@ typedef struct VeloxHipRunOptions {
     uint32_t verbose;
     const uint32_t* prompt_tokens; /* NULL: prompt_len seeded random ids; else prompt_len explicit ids
                                       (the runner's --tokens, src/cli.rs:655-661) */
+    uint32_t context_len;    /* >0: positions [0, context_len) of every layer's KV cache hold a seeded
+                                N(0,1) bf16 context (velox_hip_fill_kv) and decoding starts at
+                                position context_len with the first prompt token
+                                (src/runners/velox_cuda_runner_k2.cu:1789 --context-len) */
 } VeloxHipRunOptions;
 
 typedef struct VeloxHipRunReport {

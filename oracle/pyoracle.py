@@ -94,6 +94,10 @@ def lib() -> C.CDLL:
         L.vxo_engine_tensor.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint64)]
         L.vxo_engine_hidden.restype = fp
         L.vxo_engine_hidden.argtypes = [C.c_void_p]
+        L.vxo_engine_k_cache.restype = fp
+        L.vxo_engine_k_cache.argtypes = [C.c_void_p]
+        L.vxo_engine_v_cache.restype = fp
+        L.vxo_engine_v_cache.argtypes = [C.c_void_p]
         _lib = L
     return _lib
 
@@ -247,6 +251,17 @@ class Engine:
     def hidden(self) -> np.ndarray:
         p = lib().vxo_engine_hidden(self.h)
         return np.ctypeslib.as_array(p, shape=(self.cfg["hidden_dim"],)).copy()
+
+    def kv_cache(self, layer: int) -> tuple[np.ndarray, np.ndarray]:
+        """Writable views of layer `layer`'s K and V caches, [max_seq_len][num_kv_heads * head_dim]
+        fp32 (src/runtime.rs:1328-1451 keeps them per layer, position-major)."""
+        kvd = self.cfg["num_kv_heads"] * self.cfg["head_dim"]
+        n = self.cfg["max_seq_len"] * kvd
+        views = []
+        for fn in (lib().vxo_engine_k_cache, lib().vxo_engine_v_cache):
+            base = np.ctypeslib.as_array(fn(self.h), shape=(self.cfg["num_layers"] * n,))
+            views.append(base[layer * n:(layer + 1) * n].reshape(self.cfg["max_seq_len"], kvd))
+        return views[0], views[1]
 
     def close(self):
         if self.h:

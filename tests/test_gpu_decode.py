@@ -134,3 +134,37 @@ def test_runner_binary_stdout_contract(oracle):
     assert re.search(r"Decode Latency \(\d+ tok\): [\d.]+ ms \([\d.]+ tok/s", r.stdout)
     _, toks = run("smollm_135m", prompt=prompt, warmup=0, steps=5, seed=31)
     assert [int(t) for _, t in steps] == toks[len(prompt) - 1:len(prompt) - 1 + 6]
+
+
+LONG = dict(vocab_size=4096, hidden_dim=8192, intermediate_dim=2048, num_heads=64, num_kv_heads=8, head_dim=128,
+            rms_norm_eps=1e-6, rope_theta=1000000.0, qkv_bias=1, tied_lm_head=0)
+
+
+@pytest.mark.parametrize("splits", [0, 8])
+def test_decode_long_context_vs_oracle(oracle, splits):
+    """Qwen2-72B attention shape (64 q / 8 kv heads, D 128, hidden 8192, QKV bias) after a seeded
+    2048-position context already in the KV cache (the BASELINE long-context setup): automatic
+    256-position splits with the merge kernel, and 8 splits merged in the o_proj prologue."""
+    ctx, max_seq, seed = 2048, 2064, 41
+    gpu = HipDecodeEngine(dict(LONG, num_layers=1), seed=seed, norm_sigma=0.1, max_seq_len=max_seq,
+                          attn_splits=splits)
+    gpu.fill_kv(0, ctx, seed=9, sigma=1.0)
+    kvd = LONG["num_kv_heads"] * LONG["head_dim"]
+    raw = np.zeros(2 * kvd * max_seq, np.uint16)
+    L.memcpy_dtoh(raw.ctypes.data, gpu.arena.kv_cache_pool, raw.nbytes)
+    kv = (raw.astype(np.uint32) << 16).view(np.float32).reshape(2, LONG["num_kv_heads"], max_seq, LONG["head_dim"])
+    ref = oracle.Engine(dict(LONG, num_layers=1, max_seq_len=max_seq), seed=seed, sigma=0.02, norm_sigma=0.1,
+                        q4_0=True, kv_bf16=True, threads=16)
+    kr, vr = ref.kv_cache(0)
+    kr[:ctx] = kv[0, :, :ctx, :].transpose(1, 0, 2).reshape(ctx, kvd)
+    vr[:ctx] = kv[1, :, :ctx, :].transpose(1, 0, 2).reshape(ctx, kvd)
+    for i, tok in enumerate(oracle.prompt_tokens(seed, 3, LONG["vocab_size"])):
+        pos = ctx + i
+        t_ref = ref.forward(int(tok), pos)
+        t_gpu = gpu.forward_step(int(tok), pos)
+        d = float(np.max(np.abs(gpu.logits - ref.logits)))
+        print(f"[long ctx splits={splits}] pos={pos} gpu={t_gpu} ref={t_ref} maxabs={d:.3e}", flush=True)
+        assert t_gpu == oracle.argmax(gpu.logits)
+        assert d < LOGIT_TOL, (pos, d)
+    gpu.close()
+    ref.close()

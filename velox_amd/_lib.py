@@ -64,6 +64,7 @@ class RunOptions(C.Structure):
         ("warmup", C.c_uint32), ("steps", C.c_uint32), ("seed", C.c_uint64), ("sigma", C.c_float),
         ("norm_sigma", C.c_float), ("use_graph", C.c_uint32), ("num_layers", C.c_uint32),
         ("kernel_passes", C.c_uint32), ("verbose", C.c_uint32), ("prompt_tokens", C.POINTER(C.c_uint32)),
+        ("context_len", C.c_uint32),
     ]
 
 

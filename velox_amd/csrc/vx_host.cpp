@@ -848,8 +848,10 @@ int velox_hip_attention_decode(const float* d_qkv, uint16_t* d_kv_layer, uint32_
 // ---------------------------------------------------------------------------------------------
 int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_tokens, VeloxHipRunReport* rep) {
     if (!opt || !rep || !opt->model || opt->prompt_len == 0) return VELOX_HIP_EINVAL;
+    if (opt->context_len && opt->prompt_len != 1) return VELOX_HIP_EINVAL;  // context + one seed token
     std::memset(rep, 0, sizeof(*rep));
-    const uint32_t total = opt->prompt_len + opt->warmup + opt->steps;
+    const uint32_t base = opt->context_len;  // first decoded position
+    const uint32_t total = base + opt->prompt_len + opt->warmup + opt->steps;
     VeloxHipModelConfig cfg;
     int rc = velox_hip_builtin_config(opt->model, opt->max_seq_len ? opt->max_seq_len : total + 1, &cfg);
     if (rc) return rc;
@@ -878,8 +880,10 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
         prompt[i] = opt->prompt_tokens ? opt->prompt_tokens[i] : vx_uniform_u32(pst, i, cfg.vocab_size);
         if (prompt[i] >= cfg.vocab_size && !rc) rc = VELOX_HIP_EINVAL;
     }
+    for (uint32_t l = 0; l < cfg.num_layers && !rc && base; ++l)
+        rc = velox_hip_fill_kv(&A, l, base, opt->seed, 1.0f, st);
     if (!rc) rc = velox_hip_set_prompt(&A, prompt.data(), opt->prompt_len, st);
-    if (!rc) rc = velox_hip_set_state(&A, 0, prompt[0], st);
+    if (!rc) rc = velox_hip_set_state(&A, base, prompt[0], st);
     velox_hip_last_error();
     if (!rc && opt->use_graph) {
         hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
@@ -924,17 +928,18 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
         rep->decode_ms = ms_d;
         rep->tok_per_s = opt->steps && ms_d > 0 ? opt->steps / (ms_d * 1e-3) : 0.0;
         double bytes = 0.0;
-        const uint32_t first = opt->prompt_len + opt->warmup;
+        const uint32_t first = base + opt->prompt_len + opt->warmup;
         for (uint32_t s = 0; s < opt->steps; ++s) bytes += (double)velox_hip_model_step_bytes(M, first + s);
         rep->bytes_per_step = opt->steps ? bytes / opt->steps : 0.0;
         rep->hbm_gbps = rep->bytes_per_step * rep->tok_per_s / 1e9;
         // ring[pos & 1023] holds the argmax after position pos (velox_cuda_runner.cu:541-546)
         uint32_t n = 0;
-        const uint32_t lo = total > VELOX_HIP_RING_SIZE ? total - VELOX_HIP_RING_SIZE : 0;
+        uint32_t lo = total > VELOX_HIP_RING_SIZE ? total - VELOX_HIP_RING_SIZE : 0;
+        if (lo < base) lo = base;
         for (uint32_t p = lo; p < total && n < max_tokens; ++p)
             if (tokens) tokens[n++] = A.host_pinned_ring[p & (VELOX_HIP_RING_SIZE - 1)];
         rep->n_tokens = n;
-        rep->first_token = A.host_pinned_ring[(opt->prompt_len - 1) & (VELOX_HIP_RING_SIZE - 1)];
+        rep->first_token = A.host_pinned_ring[(base + opt->prompt_len - 1) & (VELOX_HIP_RING_SIZE - 1)];
     }
     if (!rc && opt->kernel_passes) {
         // The dominant kernel alone: the fused RMSNorm + gate/up + SwiGLU GEMV of every layer in

@@ -4,7 +4,8 @@
 // (benchmarks/run_sota_roofline_benchmarks.py:278-292) keep working.
 //
 //   velox_hip_runner [--model llama3_8b] [--weights synthetic] [--tokens 1,2,3 | --prompt-len N]
-//                    [--steps N] [--warmup N] [--seed S] [--layers L] [--no-cuda-graph] [--verbose]
+//                    [--context-len N] [--steps N] [--warmup N] [--seed S] [--layers L]
+//                    [--no-cuda-graph] [--verbose]
 //
 // Weights are the seeded synthetic Q4_0 model: `--weights synthetic` (what src/cli.rs:654 passes
 // through) is accepted, a checkpoint path is refused with exit 1.
@@ -19,7 +20,7 @@
 int main(int argc, char** argv) {
     std::string model = "llama3_8b";
     std::vector<uint32_t> tokens;
-    uint32_t prompt_len = 128, steps = 32, warmup = 0, layers = 0;
+    uint32_t prompt_len = 128, steps = 32, warmup = 0, layers = 0, context_len = 0;
     uint64_t seed = 1234;
     bool graph = true, verbose = false;
     for (int i = 1; i < argc; ++i) {
@@ -59,9 +60,10 @@ int main(int argc, char** argv) {
                 std::fprintf(stderr, "Error: --weights %s is not supported (synthetic Q4_0 weights only)\n", w);
                 return 1;
             }
+        } else if (!std::strcmp(a, "--context-len")) {
+            context_len = (uint32_t)std::atoi(next());
         } else if (!std::strcmp(a, "--quantize") || !std::strcmp(a, "--speculative") ||
-                   !std::strcmp(a, "--draft-len") || !std::strcmp(a, "--spec-ema") ||
-                   !std::strcmp(a, "--context-len")) {
+                   !std::strcmp(a, "--draft-len") || !std::strcmp(a, "--spec-ema")) {
             std::fprintf(stderr, "Error: %s is not supported by this runner\n", a);
             return 1;
         } else {
@@ -70,6 +72,13 @@ int main(int argc, char** argv) {
         }
     }
     if (!tokens.empty()) prompt_len = (uint32_t)tokens.size();
+    if (context_len && prompt_len != 1) {
+        if (!tokens.empty()) {
+            std::fprintf(stderr, "Error: --context-len continues from one token; pass a single --tokens id\n");
+            return 1;
+        }
+        prompt_len = 1;
+    }
     if (steps == 0 || prompt_len == 0) { std::fprintf(stderr, "Error: --steps and --prompt-len must be > 0\n"); return 1; }
 
     VeloxHipRunOptions opt;
@@ -85,6 +94,7 @@ int main(int argc, char** argv) {
     opt.num_layers = layers;
     opt.verbose = verbose ? 1 : 0;
     opt.prompt_tokens = tokens.empty() ? nullptr : tokens.data();
+    opt.context_len = context_len;
     std::vector<uint32_t> out(prompt_len + warmup + opt.steps + 8);
     VeloxHipRunReport rep;
     const int rc = velox_hip_run(&opt, out.data(), (uint32_t)out.size(), &rep);
