@@ -211,6 +211,13 @@ int velox_hip_lm_head_argmax(const VeloxHipQ4Matrix* m, const float* d_x, const 
                              float* d_logits, uint32_t* d_token, hipStream_t stream);
 /* Standalone two-stage argmax over n fp32 values (strict '>' lowest-index rule). */
 int velox_hip_argmax_f32(const float* d_x, uint32_t n, uint32_t* d_out, hipStream_t stream);
+/* Batched GEMM of `batch` <= 32 sequences (src/runners/velox_cuda_runner_k2.cu:553-997, batched
+ * Q4 kernels), on MFMA: d_x16 is [batch][ldx] fp16. mode VELOX_GEMV_STORE: y[m][n] = W x_m (+ bias);
+ * VELOX_GEMV_RESIDUAL: y[m][n] += W x_m; VELOX_GEMV_SWIGLU (paired layout): d_out16[m][j] =
+ * fp16(silu(gate) * up). Row strides ldx, ldy, ldo in elements. */
+int velox_hip_gemm_q4_0_batch(const VeloxHipQ4Matrix* m, const uint16_t* d_x16, uint32_t batch, uint32_t ldx,
+                              const float* d_bias, float* d_y, uint32_t ldy, uint16_t* d_out16, uint32_t ldo,
+                              int mode, hipStream_t stream);
 /* y = rmsnorm(x) * w (src/runtime.rs:588-601). */
 int velox_hip_rmsnorm(const float* d_x, const float* d_w, uint32_t n, float eps, float* d_y, hipStream_t stream);
 /* Decode attention for one layer at position pos: RoPE on q and the new k (table cos/sin of

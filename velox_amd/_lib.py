@@ -15,6 +15,7 @@ HEADER = os.path.join(ROOT, "include", "velox_hip.h")
 
 QUANT_GGML_Q4_0 = 5
 GEMV_STORE, GEMV_RESIDUAL, GEMV_SWIGLU = 0, 1, 2
+EINVAL, ENOMEM, ESHAPE, ENOTLOADED = -1, -2, -3, -4
 T_EMBED, T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN = 1, 2, 3, 4, 5, 6, 7, 8
 T_ATTN_NORM, T_MLP_NORM, T_FINAL_NORM, T_HEAD, T_BQ, T_BK, T_BV = 9, 10, 11, 12, 13, 14, 15
 RING_SIZE = 1024
@@ -120,6 +121,7 @@ _SIGS = {
     "velox_hip_q4_0_quantize": (_I, [_P, _U32, _U32, _P, _P]),
     "velox_hip_fill_normal": (_I, [_P, _U64, _U64, _U64, _F, _F, _P]),
     "velox_hip_gemv_q4_0": (_I, [C.POINTER(Q4Matrix), _P, _P, _F, _P, _P, _P, _I, _P]),
+    "velox_hip_gemm_q4_0_batch": (_I, [C.POINTER(Q4Matrix), _P, _U32, _U32, _P, _P, _U32, _P, _U32, _I, _P]),
     "velox_hip_lm_head_argmax": (_I, [C.POINTER(Q4Matrix), _P, _P, _F, _P, _P, _P]),
     "velox_hip_argmax_f32": (_I, [_P, _U32, _P, _P]),
     "velox_hip_rmsnorm": (_I, [_P, _P, _U32, _F, _P, _P]),

@@ -135,10 +135,31 @@ struct VxAttnArgs {
     uint32_t partials_only;  // 1: always write (m, l, o) partials; the consumer merges them
 };
 
+// Batched (B <= 32 sequences) Q4_0 GEMM: Y[m][n] = sum_k X[m][k] W[n][k] for fp16 activations
+// X (row stride ldx elements), through MFMA, with the same epilogues as the GEMV.
+struct VxBGemmArgs {
+    const uint4* codes;
+    const uint16_t* scales;
+    uint32_t n, k, n_tiles, n_iter, batch;
+    const uint16_t* x16;   // [batch][ldx] fp16
+    uint32_t ldx;
+    const float* bias;     // STORE: + bias[n]
+    float* y;              // STORE / ARGMAX: y[m][n] = ...; RESID: y[m][n] += ...   (row stride ldy)
+    uint32_t ldy;
+    uint16_t* out16;       // SWIGLU: out16[m][j] = fp16(silu(gate) * up)          (row stride ldo)
+    uint32_t ldo;
+    float* cand_v;         // ARGMAX: per (m, workgroup) candidates, [batch][gridDim.x]
+    uint32_t* cand_i;
+    uint64_t active_mask;
+};
+
 // Launch helpers implemented in vx_kernels.hip, used by vx_host.cpp.
 enum { VX_EPI_STORE = 0, VX_EPI_RESID = 1, VX_EPI_SWIGLU = 2, VX_EPI_ARGMAX = 3 };
 hipError_t vx_launch_gemv(const VxMat& m, const VxGemvArgs& a, int epi, uint32_t max_wgs, hipStream_t st);
 hipError_t vx_launch_attention(const VxAttnArgs& a, uint32_t d, hipStream_t st);
+// vx_batch.hip
+hipError_t vx_launch_bgemm(const VxMat& m, const VxBGemmArgs& a, int epi, hipStream_t st);
+uint32_t vx_bgemm_grid(uint32_t n_tiles, uint32_t s);
 hipError_t vx_launch_embed(const VxMat& m, const VeloxDecodeState* state, uint32_t fixed_token, float* h,
                            uint64_t mask, hipStream_t st);
 hipError_t vx_launch_set_state(VeloxDecodeState* state, uint64_t step, uint32_t token, hipStream_t st);

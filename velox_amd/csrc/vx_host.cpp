@@ -758,6 +758,27 @@ int velox_hip_gemv_q4_0(const VeloxHipQ4Matrix* m, const float* d_x, const float
     return (int)vx_launch_gemv(vx_view_public(m), g, epi, vx_gemv_max_wgs_default(), st);
 }
 
+int velox_hip_gemm_q4_0_batch(const VeloxHipQ4Matrix* m, const uint16_t* d_x16, uint32_t batch, uint32_t ldx,
+                              const float* d_bias, float* d_y, uint32_t ldy, uint16_t* d_out16, uint32_t ldo,
+                              int mode, hipStream_t st) {
+    if (!m || !d_x16 || batch == 0 || batch > 32 || ldx < m->k || mode < 0 || mode > 2) return VELOX_HIP_EINVAL;
+    if ((mode == VELOX_GEMV_SWIGLU) != (m->paired != 0)) return VELOX_HIP_EINVAL;
+    if (mode == VELOX_GEMV_SWIGLU ? (!d_out16 || ldo < m->n) : (!d_y || ldy < m->n)) return VELOX_HIP_EINVAL;
+    VxBGemmArgs g;
+    std::memset(&g, 0, sizeof(g));
+    g.batch = batch;
+    g.x16 = d_x16;
+    g.ldx = ldx;
+    g.bias = d_bias;
+    g.y = d_y;
+    g.ldy = ldy;
+    g.out16 = d_out16;
+    g.ldo = ldo;
+    g.active_mask = 1;
+    const int epi = mode == VELOX_GEMV_STORE ? VX_EPI_STORE : mode == VELOX_GEMV_RESIDUAL ? VX_EPI_RESID : VX_EPI_SWIGLU;
+    return (int)vx_launch_bgemm(vx_view_public(m), g, epi, st);
+}
+
 int velox_hip_lm_head_argmax(const VeloxHipQ4Matrix* m, const float* d_x, const float* d_gain, float eps,
                              float* d_logits, uint32_t* d_token, hipStream_t st) {
     if (!m || !d_x || !d_logits || !d_token || m->paired) return VELOX_HIP_EINVAL;
