@@ -98,6 +98,8 @@ def main() -> int:
                     help="builtin configuration (the headline metric is llama3_8b)")
     ap.add_argument("--context-len", type=int, default=0,
                     help="start from a seeded context of N positions already in the KV cache (prompt = 1 token)")
+    ap.add_argument("--batch", type=int, default=1,
+                    help="decode B <= 32 independent sequences per step (batched MFMA GEMMs); value = all tokens/s")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="afterwards run a device-to-device copy of MIB MiB (byte-counter yardstick)")
     args = ap.parse_args()
@@ -116,17 +118,18 @@ def main() -> int:
     print(f"[bench] {args.model} Q4_0 decode: context {ctx}, prompt {plen}, warmup {args.warmup}, steps {args.steps}",
           file=sys.stderr, flush=True)
     rep, toks = run(args.model, prompt_len=plen, warmup=args.warmup, steps=args.steps, seed=args.seed,
-                    use_graph=not args.no_graph, kernel_passes=args.kernel_passes, context_len=ctx)
+                    use_graph=not args.no_graph, kernel_passes=args.kernel_passes, context_len=ctx,
+                    batch=args.batch)
     print(f"[bench] decode done: {rep['tok_per_s']:.1f} tok/s, {rep['hbm_gbps']:.0f} GB/s; gate/up kernel "
           f"{rep['kernel_us']:.2f} us", file=sys.stderr, flush=True)
 
     if args.copy_calibration > 0:
         L.device_copy_calibration(args.copy_calibration << 20)
     kernel_gbps = rep["kernel_bytes"] / (rep["kernel_us"] * 1e-6) / 1e9 if rep["kernel_us"] > 0 else 0.0
-    headline = args.model == "llama3_8b" and ctx == 0
-    workload = f"{args.model}_q4_0_decode_bs1" + (f"_ctx{ctx}" if ctx else "")
+    headline = args.model == "llama3_8b" and ctx == 0 and args.batch == 1
+    workload = f"{args.model}_q4_0_decode_bs{args.batch}" + (f"_ctx{ctx}" if ctx else "")
     out = {
-        "metric": METRIC if headline else f"decode tok/s + achieved HBM GB/s, {args.model} Q4_0 bs=1"
+        "metric": METRIC if headline else f"decode tok/s + achieved HBM GB/s, {args.model} Q4_0 bs={args.batch}"
                   + (f" ctx {ctx}" if ctx else "") + ", 1 GPU",
         "value": round(rep["tok_per_s"], 2),
         "unit": "tok/s",
@@ -141,7 +144,7 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": workload,
-            "batch": 1,
+            "batch": args.batch,
             "context_tokens": ctx,
             "prompt_tokens": plen,
             "timed_positions": [ctx + plen + args.warmup, ctx + plen + args.warmup + args.steps - 1],
@@ -153,8 +156,10 @@ def main() -> int:
         "wall_ms": round(rep["wall_ms"], 3),
         "prefill_ms": round(rep["prefill_ms"], 3),
         "roofline": {
-            "kernel": f"vx_gemv_q4_kernel<S,SWIGLU> (RMSNorm + gate/up Q4_0 GEMV + SwiGLU), "
-                      f"{cfg.intermediate_dim}x2 x {cfg.hidden_dim}",
+            "kernel": (f"vx_gemv_q4_kernel<S,SWIGLU> (RMSNorm + gate/up Q4_0 GEMV + SwiGLU), "
+                       f"{cfg.intermediate_dim}x2 x {cfg.hidden_dim}") if args.batch == 1 else
+                      (f"vx_bgemm_q4_kernel<S,SWIGLU,MT> (gate/up Q4_0 MFMA GEMM + SwiGLU, {args.batch} sequences), "
+                       f"{cfg.intermediate_dim}x2 x {cfg.hidden_dim}"),
             "bound": "hbm",
             "achieved": round(kernel_gbps, 1),
             "peak": HBM_PEAK_GBPS,

@@ -57,6 +57,9 @@ typedef struct VeloxHipModelConfig {
     uint32_t quant_mode;        /* VELOX_QUANT_GGML_Q4_0 */
     uint32_t attn_splits;       /* split-K partitions over the sequence (<= 64); 0 = automatic */
     uint64_t vram_budget_bytes; /* 0 = 288 GB of HBM3E */
+    uint32_t max_batch;         /* sequences of the batched decode step (<= 32; 0 or 1 = single);
+                                   sizes the KV pool like B_MAX in src/memory_planner.rs:282-488 */
+    uint32_t reserved;
 } VeloxHipModelConfig;
 
 typedef struct VeloxHipModel VeloxHipModel; /* opaque: the static memory plan */
@@ -164,6 +167,25 @@ void velox_Qwen2_72B_decode_hip(VeloxHipArena* ctx, uint32_t token_in, size_t st
 
 /* ---- per-kernel entry points (device pointers; for parity tests and benchmarks) ---- */
 
+/* ---- batched decode of independent sequences (src/runners/velox_cuda_runner_k2.cu:553-1088 batched
+ *      kernels; arena planned with max_batch > 1, src/memory_planner.rs:282-488 B_MAX) ----
+ * Sequence b owns KV caches, a decode state, a prompt for teacher forcing and ring
+ * host_pinned_ring[b * VELOX_HIP_RING_SIZE ...]; its logits are at logits_offset + b * vocab * 4 of
+ * the activation arena and its hidden state at hidden_offset + b * hidden_dim * 4. */
+int velox_hip_model_batch_layout(const VeloxHipModel* m, uint32_t* max_batch, uint64_t* logits_offset,
+                                 uint64_t* hidden_offset);
+/* Algorithmic HBM bytes of one batched step with every sequence at position pos. */
+uint64_t velox_hip_model_batch_step_bytes(const VeloxHipModel* m, uint32_t batch, uint64_t pos);
+int velox_hip_batch_set_prompt(VeloxHipArena* a, uint32_t seq, const uint32_t* tokens, uint32_t n, hipStream_t stream);
+int velox_hip_batch_set_state(VeloxHipArena* a, uint32_t seq, uint64_t step, uint32_t token, hipStream_t stream);
+int velox_hip_batch_get_state(const VeloxHipArena* a, uint32_t seq, VeloxDecodeState* out, hipStream_t stream);
+/* Seeded N(0, sigma) bf16 context of sequence seq (seq 0: the same values as velox_hip_fill_kv). */
+int velox_hip_fill_kv_seq(VeloxHipArena* a, uint32_t layer, uint32_t seq, uint32_t n_pos, uint64_t seed, float sigma,
+                          hipStream_t stream);
+/* One decode step of sequences 0 .. batch-1 (batch <= max_batch), each at its own state; capturable
+ * like velox_hip_decode_graph_step. Weights are read once per step for all sequences (MFMA GEMMs). */
+void velox_hip_decode_batch_graph_step(VeloxHipArena* ctx, uint32_t batch, uint64_t active_mask, hipStream_t stream);
+
 /* Q4_0 matrix in the tiled device layout. Row r, block b of an [n][k] matrix lives in lane
  * (r % (64/s_lanes)) * s_lanes + b % s_lanes of iteration b / s_lanes of tile r / (64/s_lanes):
  * codes uint4 [n_tiles][n_iter][64], scales fp16 [n_tiles][n_iter][64]. */
@@ -246,6 +268,8 @@ typedef struct VeloxHipRunOptions {
                                 N(0,1) bf16 context (velox_hip_fill_kv) and decoding starts at
                                 position context_len with the first prompt token
                                 (src/runners/velox_cuda_runner_k2.cu:1789 --context-len) */
+    uint32_t batch;          /* >1: decode `batch` independent sequences per step (own seeded prompt and
+                                context each); tokens/report cover sequence 0, tok_per_s all of them */
 } VeloxHipRunOptions;
 
 typedef struct VeloxHipRunReport {

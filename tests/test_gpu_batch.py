@@ -79,3 +79,73 @@ def test_gemm_batch_rejects_bad_arguments(hiplib, oracle, dev):
     for batch, ldx in ((0, 576), (33, 576), (4, 500)):
         assert hiplib.velox_hip_gemm_q4_0_batch(C.byref(t.m), dx.data_ptr(), batch, ldx, None, dy.data_ptr(), 64,
                                                 None, 0, L.GEMV_STORE, None) == L.EINVAL
+
+
+# ---- the batched decode step against one oracle replay per sequence -------------------------
+from velox_amd.engine import HipBatchEngine, run  # noqa: E402
+
+LOGIT_TOL = 2e-2
+SMOLLM = dict(vocab_size=49152, hidden_dim=576, intermediate_dim=1536, num_heads=9, num_kv_heads=3, head_dim=64,
+              rms_norm_eps=1e-5, rope_theta=10000.0, qkv_bias=0, tied_lm_head=1)
+QWEN_SMALL_VOCAB = dict(vocab_size=4096, hidden_dim=3584, intermediate_dim=18944, num_heads=28, num_kv_heads=4,
+                        head_dim=128, rms_norm_eps=1e-6, rope_theta=1000000.0, qkv_bias=1, tied_lm_head=1)
+GOLDEN = 0x9E3779B97F4A7C15
+
+
+def _batch_vs_oracle(oracle, model, cfg, layers, batch, n_steps, max_seq, seed, starts):
+    gpu = HipBatchEngine(model, max_batch=batch, seed=seed, norm_sigma=0.1, max_seq_len=max_seq, num_layers=layers)
+    V = cfg["vocab_size"]
+    prompts = [[int(t) for t in oracle.prompt_tokens(seed + 100 + b, max_seq, V)] for b in range(batch)]
+    for b in range(batch):
+        gpu.set_prompt_seq(b, prompts[b])
+        gpu.set_state_seq(b, starts[b], prompts[b][starts[b]])
+    got = [[] for _ in range(batch)]
+    for _ in range(n_steps):
+        gpu.batch_step(batch)
+        gpu.sync()
+        for b in range(batch):
+            got[b].append(gpu.logits_seq(b))
+    ref = oracle.Engine(dict(cfg, num_layers=layers, max_seq_len=max_seq), seed=seed, sigma=0.02, norm_sigma=0.1,
+                        q4_0=True, kv_bf16=True, threads=16)
+    worst = 0.0
+    for b in range(batch):
+        ref.reset()  # positions before starts[b] hold zero K/V in both caches
+        for t in range(n_steps):
+            pos = starts[b] + t
+            ref.forward(prompts[b][pos], pos)
+            d = float(np.max(np.abs(got[b][t] - ref.logits)))
+            worst = max(worst, d)
+            assert gpu.ring_seq(b, pos) == oracle.argmax(got[b][t]), (b, pos)
+            assert d < LOGIT_TOL, (b, pos, d)
+        assert gpu.state_seq(b) == (starts[b] + n_steps, prompts[b][starts[b] + n_steps])
+    print(f"[{model} batch {batch}] worst logits maxabs {worst:.3e}", flush=True)
+    gpu.close()
+    ref.close()
+
+
+@pytest.mark.parametrize("batch", [3, 17])
+def test_batch_decode_smollm_vs_oracle(oracle, batch):
+    _batch_vs_oracle(oracle, "smollm_135m", SMOLLM, 4, batch, 5, 16, seed=51, starts=[b % 3 for b in range(batch)])
+
+
+def test_batch_decode_qwen_bias_32_vs_oracle(oracle):
+    _batch_vs_oracle(oracle, QWEN_SMALL_VOCAB, QWEN_SMALL_VOCAB, 1, 32, 2, 8, seed=52, starts=[0] * 32)
+
+
+def test_batch_run_graph_matches_eager(oracle):
+    """velox_hip_run with batch > 1 (hipGraph of the batched step) produces sequence 0's tokens of an
+    eager batched decode of the same seeded prompts."""
+    seed, B, P, n = 61, 4, 5, 4
+    rep, toks = run("smollm_135m", prompt_len=P, warmup=0, steps=n - 1, seed=seed, num_layers=3, batch=B,
+                    max_seq_len=16)
+    assert rep["status"] == 0 and rep["tok_per_s"] > 0
+    gpu = HipBatchEngine("smollm_135m", max_batch=B, seed=seed, max_seq_len=16, num_layers=3)
+    for b in range(B):
+        pr = [int(t) for t in oracle.prompt_tokens((seed + b * GOLDEN) % (1 << 64), P, 49152)]
+        gpu.set_prompt_seq(b, pr)
+        gpu.set_state_seq(b, 0, pr[0])
+    for _ in range(P + n - 1):
+        gpu.batch_step(B)
+    gpu.sync()
+    assert [gpu.ring_seq(0, p) for p in range(P + n - 1)] == toks[:P + n - 1]
+    gpu.close()

@@ -25,6 +25,8 @@ namespace {
 typedef _Float16 vx_h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 vx_bh2 __attribute__((ext_vector_type(2)));
 typedef float vx_f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t vx_bu4 __attribute__((ext_vector_type(4)));  // a plain vector (HIP's uint4 is a union
+                                                               // struct that arrays keep on the stack)
 
 constexpr int kBWaves = 4, kBThreads = 64 * kBWaves;
 
@@ -53,17 +55,20 @@ __device__ __forceinline__ vx_h8 vx_unpack8(uint32_t q) {
 
 template <int S, int MT>
 constexpr size_t vx_bgemm_lds() {
-    return (size_t)S * 64 * 16 + (size_t)S * 64 * 2 + (size_t)MT * 16 * S * 32 * 2;
+    return (size_t)S * 64 * 16 + (size_t)S * 64 * 2 + (size_t)MT * 16 * (S * 4 + 1) * 16;
 }
 
 template <int S, int EPI, int MT>
 __global__ __launch_bounds__(kBThreads) void vx_bgemm_q4_kernel(VxBGemmArgs a) {
     if ((a.active_mask & 1ULL) == 0ULL) return;
     constexpr int R = 64 / S, TPW = S, XC = S * 4;  // rows per tile, tiles per workgroup, x chunks per row
+    constexpr int XP = XC + 1;                      // padded activation row: rows 4 banks apart
     extern __shared__ __align__(16) unsigned char vx_smem[];
-    uint4* c_s = (uint4*)vx_smem;                     // [TPW][64] code words of this item
-    uint16_t* s_s = (uint16_t*)(c_s + TPW * 64);      // [TPW][64] their scales
-    uint4* x_s = (uint4*)(s_s + TPW * 64);            // [MT * 16][XC] fp16 activations (8 per chunk)
+    // code words and scales of this item, transposed to [wave][block j][row 0..15]: the 16 lanes
+    // that read one dword column of a block read 16 consecutive words (no bank conflicts)
+    vx_bu4* c_s = (vx_bu4*)vx_smem;
+    uint16_t* s_s = (uint16_t*)(c_s + TPW * 64);
+    vx_bu4* x_s = (vx_bu4*)(s_s + TPW * 64);          // [MT * 16][XP] fp16 activations (8 per chunk)
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t t0 = blockIdx.x * (uint32_t)TPW, n_iter = a.n_iter;
     const int nl = 16 * wave + (lane & 15), g = lane >> 4;  // this lane's weight row in the workgroup
@@ -72,35 +77,67 @@ __global__ __launch_bounds__(kBThreads) void vx_bgemm_q4_kernel(VxBGemmArgs a) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = vx_f4{0.f, 0.f, 0.f, 0.f};
 
+    // Operands of one item in registers: the next item's loads are issued before the current one
+    // is computed from LDS, so HBM latency overlaps the MFMA work. Loads are unconditional (tiles
+    // past the matrix re-read its last tile, sequences past the batch the last sequence, elements
+    // past K the last chunk); those rows and columns never reach an output, and padded blocks have
+    // zero scales.
+    constexpr int NC = S / 4, NX = MT * S / 4;  // 16-byte code words and activation chunks per thread
+    vx_bu4 cr[NC], xr[NX];
+    uint16_t sr[NC];
+    const uint32_t t_last = a.n_tiles - 1u, m_last = a.batch - 1u, e_last = a.k - 8u;
+    // loads of item `it` into the prefetch registers (a macro keeps the arrays in registers: the
+    // same loop behind a lambda called from two places was left on the stack)
+#define VX_BGEMM_LOAD(it_)                                                                          \
+    do {                                                                                            \
+        _Pragma("unroll") for (int u = 0; u < NC; ++u) {                                            \
+            const int i = tid + u * kBThreads;                                                      \
+            const uint32_t t = min(t0 + (uint32_t)(i >> 6), t_last);                                \
+            const size_t slot = ((size_t)t * n_iter + (it_)) * 64u + (uint32_t)(i & 63);            \
+            cr[u] = ((const vx_bu4*)a.codes)[slot];                                                 \
+            sr[u] = a.scales[slot];                                                                 \
+        }                                                                                           \
+        _Pragma("unroll") for (int u = 0; u < NX; ++u) {                                            \
+            const int i = tid + u * kBThreads;                                                      \
+            const uint32_t m = min((uint32_t)(i / XC), m_last);                                     \
+            const uint32_t e = min((it_) * (uint32_t)(S * 32) + (uint32_t)(i % XC) * 8u, e_last);   \
+            xr[u] = *(const vx_bu4*)(a.x16 + (size_t)m * a.ldx + e);                                \
+        }                                                                                           \
+    } while (0)
+    VX_BGEMM_LOAD(0u);
     for (uint32_t it = 0; it < n_iter; ++it) {
         __syncthreads();  // the previous item's operands are consumed
-        for (int i = tid; i < TPW * 64; i += kBThreads) {
-            const uint32_t t = t0 + (uint32_t)(i >> 6);
-            const size_t slot = ((size_t)t * n_iter + it) * 64u + (uint32_t)(i & 63);
-            c_s[i] = t < a.n_tiles ? a.codes[slot] : make_uint4(0u, 0u, 0u, 0u);
-            s_s[i] = t < a.n_tiles ? a.scales[slot] : (uint16_t)0;
+#pragma unroll
+        for (int u = 0; u < NC; ++u) {
+            // word i = (tile i / 64, layout lane i % 64 = (row r, block s)) -> (wave, s, row in wave)
+            const int i = tid + u * kBThreads;
+            const int row = (i >> 6) * R + (i & 63) / S, blk = (i & 63) % S;
+            const int o = ((row >> 4) * S + blk) * 16 + (row & 15);
+            c_s[o] = cr[u];
+            s_s[o] = sr[u];
         }
-        for (int i = tid; i < MT * 16 * XC; i += kBThreads) {
-            const int m = i / XC, ch = i % XC;
-            const uint32_t e = it * (uint32_t)(S * 32) + (uint32_t)ch * 8u;
-            x_s[i] = ((uint32_t)m < a.batch && e < a.k) ? *(const uint4*)(a.x16 + (size_t)m * a.ldx + e)
-                                                        : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int u = 0; u < NX; ++u) {
+            const int i = tid + u * kBThreads;
+            x_s[(i / XC) * XP + i % XC] = xr[u];
         }
         __syncthreads();
+        if (it + 1u < n_iter) VX_BGEMM_LOAD(it + 1u);
 #pragma unroll 4
         for (int j = 0; j < S; ++j) {
-            const int wi = tl * 64 + r * S + j;  // layout lane (r, block j) of tile tl
+            const int wi = (wave * S + j) * 16 + (lane & 15);  // this lane's row, block j
             const uint32_t q = ((const uint32_t*)(c_s + wi))[g];
             const float d = vx_bh2f(s_s[wi]);
             const vx_h8 bw = vx_unpack8(q);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                const vx_h8 ax = __builtin_bit_cast(vx_h8, x_s[(mt * 16 + (lane & 15)) * XC + j * 4 + g]);
+                const vx_h8 ax = __builtin_bit_cast(vx_h8, x_s[(mt * 16 + (lane & 15)) * XP + j * 4 + g]);
                 const vx_f4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, bw, vx_f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                 acc[mt] += d * c;
             }
         }
     }
+#undef VX_BGEMM_LOAD
 
     // ---- epilogues: lane holds acc[mt][i] for sequence m = 16 mt + 4 g + i of weight row nl ----
     const uint32_t t = t0 + (uint32_t)tl;
@@ -225,4 +262,174 @@ hipError_t vx_launch_bgemm(const VxMat& m, const VxBGemmArgs& a0, int epi, hipSt
         case VX_EPI_ARGMAX: return vx_bgemm_dispatch_mt<VX_EPI_ARGMAX>(m.s, a, st);
         default: return hipErrorInvalidValue;
     }
+}
+
+// =============================================================================================
+// The rest of a batched decode step: one grid row (or workgroup) per sequence
+// =============================================================================================
+namespace {
+
+__device__ __forceinline__ uint32_t vx_bnibble(uint32_t dw, int e) { return (dw >> (8 * (e & 3) + 4 * (e >> 2))) & 15u; }
+
+template <int W>
+__device__ __forceinline__ float vx_bblock_sum(float v, float* red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) t += red[w];
+    return t;
+}
+
+}  // namespace
+
+// h[b] = embedding row of states[b].token, dequantized (src/codegen.rs:2381-2410 per sequence).
+__global__ __launch_bounds__(256) void vx_bembed_kernel(VxMat m, const VeloxDecodeState* states, float* h,
+                                                        uint32_t ldh, uint64_t mask) {
+    if ((mask & 1ULL) == 0ULL) return;
+    const uint32_t b = blockIdx.y, token = states[b].token;
+    const uint32_t blk = blockIdx.x * 256u + threadIdx.x, nb = m.k >> 5;
+    if (blk >= nb || token >= m.n) return;  // src/codegen.rs:2386-2390 guard
+    const uint32_t R = 64u / m.s;
+    const size_t off = ((size_t)(token / R) * m.n_iter + blk / m.s) * 64u + (token % R) * m.s + blk % m.s;
+    const uint4 c = m.codes[off];
+    const float d = vx_bh2f(m.scales[off]);
+    const uint32_t dw[4] = {c.x, c.y, c.z, c.w};
+    float* o = h + (size_t)b * ldh + (size_t)blk * 32u;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[8 * w + e] = (float)((int)vx_bnibble(dw[w], e) - 8) * d;
+}
+
+// x16[b] = fp16((h[b] / rms(h[b])) * g): the RMSNorm of src/runtime.rs:588-601 per sequence, written
+// as the fp16 operand of the batched GEMM (the product is rounded to fp32 first, as in the GEMV).
+__global__ __launch_bounds__(256) void vx_bnorm_kernel(const float* h, uint32_t ldh, const float* g, uint32_t k,
+                                                       float eps, uint16_t* x16, uint32_t ldx, uint64_t mask) {
+    if ((mask & 1ULL) == 0ULL) return;
+    __shared__ float red[4];
+    const float* x = h + (size_t)blockIdx.x * ldh;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < k; i += 256u) ss += x[i] * x[i];
+    ss = vx_bblock_sum<4>(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)k + eps);
+    uint16_t* o = x16 + (size_t)blockIdx.x * ldx;
+    for (uint32_t i = threadIdx.x; i < k; i += 256u) {
+#pragma clang fp contract(off)
+        const float v = (x[i] * inv) * g[i];
+        o[i] = __half_as_ushort(__float2half(v));
+    }
+}
+
+// LSE merge of one sequence's split partials of one q head (m, l in the log2 domain), written as
+// the fp16 operand of the o_proj GEMM.
+template <int D>
+__global__ __launch_bounds__(D) void vx_bmerge_kernel(const float* part_o, const float* part_ml, uint32_t hq,
+                                                      uint32_t splits, uint16_t* x16, uint32_t ldx, uint64_t mask) {
+    if ((mask & 1ULL) == 0ULL) return;
+    __shared__ float s_w[64];
+    const int tid = threadIdx.x;
+    const size_t h = blockIdx.x, b = blockIdx.y;
+    const float* po = part_o + (b * hq + h) * splits * D;
+    const float* pml = part_ml + (b * hq + h) * splits * 2u;
+    if (tid < 64) {
+        const float mj = tid < (int)splits ? pml[tid * 2] : -INFINITY;
+        const float lj = tid < (int)splits ? pml[tid * 2 + 1] : 0.0f;
+        float M = mj;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+        const float wj = mj == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mj - M);
+        float Ls = lj * wj;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) Ls += __shfl_xor(Ls, off);
+        s_w[tid] = Ls > 0.0f ? wj / Ls : 0.0f;
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    for (uint32_t j = 0; j < splits; ++j) acc += s_w[j] * po[j * D + tid];
+    x16[b * ldx + h * D + tid] = __half_as_ushort(__float2half(acc));
+}
+
+// Per sequence: the argmax over the LM head's workgroup candidates (lowest index on ties), the
+// ring entry ring_b[step & 1023], and the state advance with teacher forcing while step + 1 <
+// plen_b (src/runtime.rs:1078-1088; src/codegen.rs:1590-1677 per sequence).
+__global__ __launch_bounds__(256) void vx_bfinalize_kernel(const float* cand_v, const uint32_t* cand_i, uint32_t n,
+                                                           VeloxDecodeState* states, uint32_t* rings,
+                                                           const uint32_t* prompts, const uint32_t* plens,
+                                                           uint32_t prompt_stride, uint64_t mask) {
+    if ((mask & 1ULL) == 0ULL) return;
+    __shared__ float s_v[4];
+    __shared__ uint32_t s_i[4];
+    const uint32_t b = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (uint32_t j = tid; j < n; j += 256) {
+        const float v = cand_v[(size_t)b * n + j];
+        const uint32_t ii = cand_i[(size_t)b * n + j];
+        if (vx_bbetter(v, ii, bv, bi)) { bv = v; bi = ii; }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const uint32_t oi = __shfl_xor(bi, off);
+        if (vx_bbetter(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) { s_v[wave] = bv; s_i[wave] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 4; ++w)
+            if (vx_bbetter(s_v[w], s_i[w], s_v[0], s_i[0])) { s_v[0] = s_v[w]; s_i[0] = s_i[w]; }
+        const uint32_t win = s_i[0] == 0xFFFFFFFFu ? 0u : s_i[0];
+        VeloxDecodeState* st = states + b;
+        const uint64_t step = st->step;
+        if (rings) {
+            __atomic_store_n(rings + (size_t)b * VELOX_HIP_RING_SIZE + (step & (VELOX_HIP_RING_SIZE - 1u)), win,
+                             __ATOMIC_RELAXED);
+            __threadfence_system();
+        }
+        const uint32_t plen = plens ? plens[b] : 0u;
+        const uint32_t next = (step + 1u < (uint64_t)plen) ? prompts[(size_t)b * prompt_stride + step + 1u] : win;
+        st->token = next;
+        st->step = step + 1u;
+    }
+}
+
+hipError_t vx_launch_bembed(const VxMat& m, const VeloxDecodeState* states, uint32_t batch, float* h, uint32_t ldh,
+                            uint64_t mask, hipStream_t st) {
+    const uint32_t nb = m.k >> 5;
+    hipLaunchKernelGGL(vx_bembed_kernel, dim3((nb + 255u) / 256u, batch), dim3(256), 0, st, m, states, h, ldh, mask);
+    return hipGetLastError();
+}
+
+hipError_t vx_launch_bnorm(const float* h, uint32_t ldh, const float* g, uint32_t k, float eps, uint16_t* x16,
+                           uint32_t ldx, uint32_t batch, uint64_t mask, hipStream_t st) {
+    hipLaunchKernelGGL(vx_bnorm_kernel, dim3(batch), dim3(256), 0, st, h, ldh, g, k, eps, x16, ldx, mask);
+    return hipGetLastError();
+}
+
+hipError_t vx_launch_bmerge(const float* part_o, const float* part_ml, uint32_t hq, uint32_t d, uint32_t splits,
+                            uint16_t* x16, uint32_t ldx, uint32_t batch, uint64_t mask, hipStream_t st) {
+    if (splits == 0 || splits > 64) return hipErrorInvalidValue;
+    if (d == 64)
+        hipLaunchKernelGGL((vx_bmerge_kernel<64>), dim3(hq, batch), dim3(64), 0, st, part_o, part_ml, hq, splits, x16,
+                           ldx, mask);
+    else if (d == 128)
+        hipLaunchKernelGGL((vx_bmerge_kernel<128>), dim3(hq, batch), dim3(128), 0, st, part_o, part_ml, hq, splits,
+                           x16, ldx, mask);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t vx_launch_bfinalize(const float* cand_v, const uint32_t* cand_i, uint32_t n, VeloxDecodeState* states,
+                               uint32_t* rings, const uint32_t* prompts, const uint32_t* plens, uint32_t prompt_stride,
+                               uint32_t batch, uint64_t mask, hipStream_t st) {
+    hipLaunchKernelGGL(vx_bfinalize_kernel, dim3(batch), dim3(256), 0, st, cand_v, cand_i, n, states, rings, prompts,
+                       plens, prompt_stride, mask);
+    return hipGetLastError();
 }

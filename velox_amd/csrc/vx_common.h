@@ -133,6 +133,11 @@ struct VxAttnArgs {
     float scale;
     uint64_t active_mask;
     uint32_t partials_only;  // 1: always write (m, l, o) partials; the consumer merges them
+    // batched decode: sequence b = blockIdx.z uses state[b], kv + b * kv_bstride (elements),
+    // qkv + b * qkv_bstride, and partials offset by b * hq * splits * (d or 2)
+    uint32_t batch;
+    uint64_t kv_bstride;
+    uint32_t qkv_bstride;
 };
 
 // Batched (B <= 32 sequences) Q4_0 GEMM: Y[m][n] = sum_k X[m][k] W[n][k] for fp16 activations
@@ -160,6 +165,15 @@ hipError_t vx_launch_attention(const VxAttnArgs& a, uint32_t d, hipStream_t st);
 // vx_batch.hip
 hipError_t vx_launch_bgemm(const VxMat& m, const VxBGemmArgs& a, int epi, hipStream_t st);
 uint32_t vx_bgemm_grid(uint32_t n_tiles, uint32_t s);
+hipError_t vx_launch_bembed(const VxMat& m, const VeloxDecodeState* states, uint32_t batch, float* h, uint32_t ldh,
+                            uint64_t mask, hipStream_t st);
+hipError_t vx_launch_bnorm(const float* h, uint32_t ldh, const float* g, uint32_t k, float eps, uint16_t* x16,
+                           uint32_t ldx, uint32_t batch, uint64_t mask, hipStream_t st);
+hipError_t vx_launch_bmerge(const float* part_o, const float* part_ml, uint32_t hq, uint32_t d, uint32_t splits,
+                            uint16_t* x16, uint32_t ldx, uint32_t batch, uint64_t mask, hipStream_t st);
+hipError_t vx_launch_bfinalize(const float* cand_v, const uint32_t* cand_i, uint32_t n, VeloxDecodeState* states,
+                               uint32_t* rings, const uint32_t* prompts, const uint32_t* plens, uint32_t prompt_stride,
+                               uint32_t batch, uint64_t mask, hipStream_t st);
 hipError_t vx_launch_embed(const VxMat& m, const VeloxDecodeState* state, uint32_t fixed_token, float* h,
                            uint64_t mask, hipStream_t st);
 hipError_t vx_launch_set_state(VeloxDecodeState* state, uint64_t step, uint32_t token, hipStream_t st);

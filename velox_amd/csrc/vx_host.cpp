@@ -50,6 +50,11 @@ struct VeloxHipModel {
     uint64_t a_cand_v = 0, a_cand_i = 0;
     uint32_t splits = 1, max_wgs = 2048;
     bool fused_merge = false;  // o_proj merges the attention partials
+    // batched decode (max_batch > 1): per-sequence states, prompts, fp32 residuals, two fp16 GEMM
+    // operands, q/k/v, attention partials, logits and LM-head candidates, sequence-major
+    uint32_t batch = 1, xw = 0, head_bwgs = 0;
+    uint64_t a_bstate = 0, a_bplen = 0, a_bprompt = 0, a_bh = 0, a_bxa = 0, a_bxb = 0, a_bqkv = 0;
+    uint64_t a_bpart_o = 0, a_bpart_ml = 0, a_blogits = 0, a_bcand_v = 0, a_bcand_i = 0;
 };
 
 namespace {
@@ -105,6 +110,12 @@ VxMat vx_view(const VeloxHipArena* a, const VxMatPlan& p) {
     return m;
 }
 
+// KV cache of (layer, sequence): [layer][sequence][K | V][kv head][position][dim] bf16
+uint16_t* vx_kv(const VeloxHipArena* a, uint32_t layer, uint32_t seq) {
+    const VeloxHipModel* M = a->model;
+    return (uint16_t*)(a->kv_cache_pool + M->kv_layer_bytes * ((uint64_t)layer * M->batch + seq));
+}
+
 VxMat vx_view_public(const VeloxHipQ4Matrix* q) {
     VxMat m;
     m.codes = (const uint4*)q->codes;
@@ -128,7 +139,7 @@ bool vx_shape_ok(const VeloxHipModelConfig& c) {
     if (c.head_dim == 128 && !(G == 1 || G == 2 || G == 4 || G == 7 || G == 8)) return false;
     if (((uint64_t)c.num_heads * c.head_dim) % 32) return false;
     if (c.quant_mode != VELOX_QUANT_GGML_Q4_0) return false;
-    if (c.num_kv_heads > 64 || c.attn_splits > 64) return false;
+    if (c.num_kv_heads > 64 || c.attn_splits > 64 || c.max_batch > 32) return false;
     if (c.hidden_dim > 32768 || c.intermediate_dim > 32768 || (uint64_t)c.num_heads * c.head_dim > 32768) return false;
     return true;
 }
@@ -237,8 +248,9 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
     M->code_bytes = cc;
     M->scale_bytes = sc;
     M->norm_bytes = nc;
+    M->batch = c.max_batch > 1 ? c.max_batch : 1u;
     M->kv_layer_bytes = vx_align((uint64_t)2 * c.num_kv_heads * c.max_seq_len * D * 2);
-    M->kv_bytes = M->kv_layer_bytes * c.num_layers;
+    M->kv_bytes = M->kv_layer_bytes * c.num_layers * M->batch;  // [layer][sequence]
 
     // Split-K over the sequence: up to 1024 positions, a power of two <= 8 splits of ~128
     // positions whose (m, l, o) partials the o_proj GEMV merges in its prologue (no extra launch);
@@ -282,6 +294,25 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
     M->a_part_ml = take((uint64_t)c.num_heads * splits * 2 * 4);
     M->a_cand_v = take((uint64_t)65536 * 4);
     M->a_cand_i = take((uint64_t)65536 * 4);
+    if (M->batch > 1) {
+        const uint64_t B = M->batch;
+        uint32_t xw = H > qd ? H : qd;
+        if (F > xw) xw = F;
+        M->xw = (xw + 7u) & ~7u;
+        M->head_bwgs = vx_bgemm_grid(M->head.n_tiles, M->head.s);
+        M->a_bstate = take(B * sizeof(VeloxDecodeState));
+        M->a_bplen = take(B * 4);
+        M->a_bprompt = take(B * c.max_seq_len * 4);
+        M->a_bh = take(B * H * 4);
+        M->a_bxa = take(B * M->xw * 2);
+        M->a_bxb = take(B * M->xw * 2);
+        M->a_bqkv = take(B * (qd + 2 * kvd) * 4);
+        M->a_bpart_o = take(B * c.num_heads * splits * D * 4);
+        M->a_bpart_ml = take(B * c.num_heads * splits * 2 * 4);
+        M->a_blogits = take(B * c.vocab_size * 4);
+        M->a_bcand_v = take(B * M->head_bwgs * 4);
+        M->a_bcand_i = take(B * M->head_bwgs * 4);
+    }
     M->act_bytes = ac;
 
     const uint64_t budget = c.vram_budget_bytes ? c.vram_budget_bytes : 288ULL * 1000 * 1000 * 1000;
@@ -347,7 +378,9 @@ int velox_hip_arena_create(const VeloxHipModel* m, VeloxHipArena* out) {
     if (e == hipSuccess) e = hipMalloc((void**)&nrm, m->norm_bytes);
     if (e == hipSuccess) e = hipMalloc((void**)&kv, m->kv_bytes);
     if (e == hipSuccess) e = hipMalloc((void**)&act, m->act_bytes);
-    if (e == hipSuccess) e = hipHostMalloc((void**)&ring, VELOX_HIP_RING_SIZE * 4, hipHostMallocMapped);
+    // one ring of VELOX_HIP_RING_SIZE tokens per sequence (sequence 0 is the single-sequence ring)
+    const size_t ring_bytes = (size_t)VELOX_HIP_RING_SIZE * 4u * m->batch;
+    if (e == hipSuccess) e = hipHostMalloc((void**)&ring, ring_bytes, hipHostMallocMapped);
     if (e == hipSuccess) e = hipMemset(w, 0, m->code_bytes + m->scale_bytes);  // tile padding = 0
     if (e == hipSuccess) e = hipMemset(nrm, 0, m->norm_bytes);
     if (e == hipSuccess) e = hipMemset(kv, 0, m->kv_bytes);
@@ -357,7 +390,7 @@ int velox_hip_arena_create(const VeloxHipModel* m, VeloxHipArena* out) {
         if (ring) hipHostFree(ring);
         return (int)e;
     }
-    std::memset(ring, 0, VELOX_HIP_RING_SIZE * 4);
+    std::memset(ring, 0, ring_bytes);
     // RoPE table: cos/sin of pos * theta^(-2j/D) evaluated exactly as src/runtime.rs:756-760
     // (fp32 powf, product and sin/cos), once at startup instead of per token.
     const VeloxHipModelConfig& c = m->cfg;
@@ -540,7 +573,7 @@ int velox_hip_fill_kv(VeloxHipArena* a, uint32_t layer, uint32_t n_pos, uint64_t
     if (!a || !a->model) return VELOX_HIP_EINVAL;
     const VeloxHipModelConfig& c = a->model->cfg;
     if (layer >= c.num_layers || n_pos > c.max_seq_len) return VELOX_HIP_EINVAL;
-    uint16_t* base = (uint16_t*)(a->kv_cache_pool + a->model->kv_layer_bytes * layer);
+    uint16_t* base = vx_kv(a, layer, 0);
     hipError_t e = vx_launch_fill_kv(base, c.num_kv_heads, c.max_seq_len, c.head_dim, n_pos,
                                      vx_stream(seed, vx_tag(layer, VX_TAG_KV_K)),
                                      vx_stream(seed, vx_tag(layer, VX_TAG_KV_V)), vx_normal_coef(sigma), st);
@@ -572,6 +605,166 @@ int velox_hip_get_state(const VeloxHipArena* a, VeloxDecodeState* out, hipStream
     hipError_t e = hipMemcpyAsync(out, a->activation_arena + a->model->a_state, sizeof(*out), hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     return (int)e;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Batched decode of independent sequences (arena planned with max_batch > 1)
+// ---------------------------------------------------------------------------------------------
+int velox_hip_batch_set_prompt(VeloxHipArena* a, uint32_t seq, const uint32_t* tokens, uint32_t n, hipStream_t st) {
+    if (!a || !a->model || a->model->batch < 2 || seq >= a->model->batch || (n && !tokens)) return VELOX_HIP_EINVAL;
+    const VeloxHipModel* M = a->model;
+    if (n > M->cfg.max_seq_len) return VELOX_HIP_EINVAL;
+    hipError_t e = hipSuccess;
+    if (n)
+        e = hipMemcpyAsync(a->activation_arena + M->a_bprompt + (size_t)seq * M->cfg.max_seq_len * 4, tokens,
+                           (size_t)n * 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(a->activation_arena + M->a_bplen + (size_t)seq * 4, &n, 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return (int)e;
+}
+
+int velox_hip_batch_set_state(VeloxHipArena* a, uint32_t seq, uint64_t step, uint32_t token, hipStream_t st) {
+    if (!a || !a->model || a->model->batch < 2 || seq >= a->model->batch) return VELOX_HIP_EINVAL;
+    VeloxDecodeState* s = (VeloxDecodeState*)(a->activation_arena + a->model->a_bstate) + seq;
+    return (int)vx_launch_set_state(s, step, token, st);
+}
+
+int velox_hip_batch_get_state(const VeloxHipArena* a, uint32_t seq, VeloxDecodeState* out, hipStream_t st) {
+    if (!a || !a->model || a->model->batch < 2 || seq >= a->model->batch || !out) return VELOX_HIP_EINVAL;
+    hipError_t e = hipMemcpyAsync(out, a->activation_arena + a->model->a_bstate + (size_t)seq * sizeof(*out),
+                                  sizeof(*out), hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return (int)e;
+}
+
+int velox_hip_fill_kv_seq(VeloxHipArena* a, uint32_t layer, uint32_t seq, uint32_t n_pos, uint64_t seed, float sigma,
+                          hipStream_t st) {
+    if (!a || !a->model || seq >= a->model->batch) return VELOX_HIP_EINVAL;
+    const VeloxHipModelConfig& c = a->model->cfg;
+    if (layer >= c.num_layers || n_pos > c.max_seq_len) return VELOX_HIP_EINVAL;
+    // sequence 0 is velox_hip_fill_kv's context; others draw from streams of a sequence-tagged seed
+    const uint64_t sseed = seed + (uint64_t)seq * 0x9E3779B97F4A7C15ULL;
+    hipError_t e = vx_launch_fill_kv(vx_kv(a, layer, seq), c.num_kv_heads, c.max_seq_len, c.head_dim, n_pos,
+                                     vx_stream(sseed, vx_tag(layer, VX_TAG_KV_K)),
+                                     vx_stream(sseed, vx_tag(layer, VX_TAG_KV_V)), vx_normal_coef(sigma), st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return (int)e;
+}
+
+int velox_hip_model_batch_layout(const VeloxHipModel* m, uint32_t* max_batch, uint64_t* logits_offset,
+                                 uint64_t* hidden_offset) {
+    if (!m) return VELOX_HIP_EINVAL;
+    if (max_batch) *max_batch = m->batch;
+    if (logits_offset) *logits_offset = m->a_blogits;
+    if (hidden_offset) *hidden_offset = m->a_bh;
+    return VELOX_HIP_OK;
+}
+
+uint64_t velox_hip_model_batch_step_bytes(const VeloxHipModel* m, uint32_t batch, uint64_t pos) {
+    if (!m || batch == 0) return 0;
+    const VeloxHipModelConfig& c = m->cfg;
+    const uint64_t kvd = (uint64_t)c.num_kv_heads * c.head_dim;
+    const uint64_t p = pos < c.max_seq_len ? pos : c.max_seq_len - 1;
+    // weights and norms once; per further sequence its embedding row and its own KV read + write
+    const uint64_t per_seq = (uint64_t)c.hidden_dim / 32 * 18 + (uint64_t)c.num_layers * 2 * kvd * 2 * (p + 2);
+    return velox_hip_model_step_bytes(m, pos) + (uint64_t)(batch - 1) * per_seq;
+}
+
+// One decode step of sequences 0 .. batch-1, each at its own state (step, token): the weights are
+// read once per step for all of them. Launches: embed, L x [norm, QKV, attention, merge, o_proj +
+// residual, norm, gate/up + SwiGLU, down + residual], norm, LM head, argmax per sequence.
+void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_t mask, hipStream_t st) {
+    if (!A || !A->model || A->model->batch < 2 || batch == 0 || batch > A->model->batch) {
+        if (!g_last_error) g_last_error = VELOX_HIP_EINVAL;
+        return;
+    }
+    const VeloxHipModel* M = A->model;
+    const VeloxHipModelConfig& c = M->cfg;
+    uint8_t* act = A->activation_arena;
+    const uint32_t H = c.hidden_dim, D = c.head_dim, qd = c.num_heads * D, kvd = c.num_kv_heads * D;
+    const float* nrm = (const float*)A->norm_weight_arena;
+    auto vecp = [&](uint64_t off) { return (const float*)((const uint8_t*)nrm + off); };
+    VeloxDecodeState* states = (VeloxDecodeState*)(act + M->a_bstate);
+    float* h = (float*)(act + M->a_bh);
+    uint16_t* xa = (uint16_t*)(act + M->a_bxa);
+    uint16_t* xb = (uint16_t*)(act + M->a_bxb);
+    float* qkv = (float*)(act + M->a_bqkv);
+
+    vx_record(vx_launch_bembed(vx_view(A, M->embed), states, batch, h, H, mask, st));
+    VxAttnArgs at;
+    std::memset(&at, 0, sizeof(at));
+    at.qkv = qkv;
+    at.rope = (const float2*)vecp(M->rope);
+    at.state = states;
+    at.part_o = (float*)(act + M->a_bpart_o);
+    at.part_ml = (float*)(act + M->a_bpart_ml);
+    at.hq = c.num_heads;
+    at.hkv = c.num_kv_heads;
+    at.s_max = c.max_seq_len;
+    at.splits = M->splits;
+    at.scale = 1.0f / sqrtf((float)D);
+    at.active_mask = mask;
+    at.partials_only = 1;
+    at.batch = batch;
+    at.kv_bstride = M->kv_layer_bytes / 2;  // consecutive sequences of one layer
+    at.qkv_bstride = qd + 2 * kvd;
+    VxBGemmArgs g;
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        const VxLayerPlan& L = M->layers[l];
+        vx_record(vx_launch_bnorm(h, H, vecp(L.attn_norm), H, c.rms_norm_eps, xa, M->xw, batch, mask, st));
+        std::memset(&g, 0, sizeof(g));
+        g.batch = batch;
+        g.active_mask = mask;
+        g.x16 = xa;
+        g.ldx = M->xw;
+        g.bias = c.qkv_bias ? vecp(L.bias) : nullptr;
+        g.y = qkv;
+        g.ldy = qd + 2 * kvd;
+        vx_record(vx_launch_bgemm(vx_view(A, L.qkv), g, VX_EPI_STORE, st));
+        at.kv = vx_kv(A, l, 0);
+        vx_record(vx_launch_attention(at, D, st));
+        vx_record(vx_launch_bmerge(at.part_o, at.part_ml, c.num_heads, D, M->splits, xa, M->xw, batch, mask, st));
+        std::memset(&g, 0, sizeof(g));
+        g.batch = batch;
+        g.active_mask = mask;
+        g.x16 = xa;
+        g.ldx = M->xw;
+        g.y = h;
+        g.ldy = H;
+        vx_record(vx_launch_bgemm(vx_view(A, L.o), g, VX_EPI_RESID, st));
+        vx_record(vx_launch_bnorm(h, H, vecp(L.mlp_norm), H, c.rms_norm_eps, xa, M->xw, batch, mask, st));
+        std::memset(&g, 0, sizeof(g));
+        g.batch = batch;
+        g.active_mask = mask;
+        g.x16 = xa;
+        g.ldx = M->xw;
+        g.out16 = xb;
+        g.ldo = M->xw;
+        vx_record(vx_launch_bgemm(vx_view(A, L.gate_up), g, VX_EPI_SWIGLU, st));
+        std::memset(&g, 0, sizeof(g));
+        g.batch = batch;
+        g.active_mask = mask;
+        g.x16 = xb;
+        g.ldx = M->xw;
+        g.y = h;
+        g.ldy = H;
+        vx_record(vx_launch_bgemm(vx_view(A, L.down), g, VX_EPI_RESID, st));
+    }
+    vx_record(vx_launch_bnorm(h, H, vecp(M->final_norm), H, c.rms_norm_eps, xa, M->xw, batch, mask, st));
+    std::memset(&g, 0, sizeof(g));
+    g.batch = batch;
+    g.active_mask = mask;
+    g.x16 = xa;
+    g.ldx = M->xw;
+    g.y = (float*)(act + M->a_blogits);
+    g.ldy = c.vocab_size;
+    g.cand_v = (float*)(act + M->a_bcand_v);
+    g.cand_i = (uint32_t*)(act + M->a_bcand_i);
+    vx_record(vx_launch_bgemm(vx_view(A, M->head), g, VX_EPI_ARGMAX, st));
+    vx_record(vx_launch_bfinalize(g.cand_v, g.cand_i, M->head_bwgs, states, A->host_pinned_ring,
+                                  (const uint32_t*)(act + M->a_bprompt), (const uint32_t*)(act + M->a_bplen),
+                                  c.max_seq_len, batch, mask, st));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -620,7 +813,7 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
         g.y = qkv;
         vx_record(vx_launch_gemv(vx_view(A, L.qkv), g, VX_EPI_STORE, M->max_wgs, st));
 
-        at.kv = (uint16_t*)(A->kv_cache_pool + M->kv_layer_bytes * l);
+        at.kv = vx_kv(A, l, 0);
         vx_record(vx_launch_attention(at, c.head_dim, st));
 
         std::memset(&g, 0, sizeof(g));
@@ -877,6 +1070,9 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
     int rc = velox_hip_builtin_config(opt->model, opt->max_seq_len ? opt->max_seq_len : total + 1, &cfg);
     if (rc) return rc;
     if (opt->num_layers) cfg.num_layers = opt->num_layers;
+    const uint32_t B = opt->batch > 1 ? opt->batch : 1u;
+    if (B > 32 || (B > 1 && opt->prompt_tokens)) return VELOX_HIP_EINVAL;
+    if (B > 1) cfg.max_batch = B;
     if (cfg.max_seq_len < total) return VELOX_HIP_EINVAL;
     VeloxHipModel* M = nullptr;
     rc = velox_hip_model_create(&cfg, &M);
@@ -895,21 +1091,38 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
     rc = velox_hip_synthesize_model(&A, opt->seed, opt->sigma, opt->norm_sigma, st);
     rep->load_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_load).count();
 
-    std::vector<uint32_t> prompt(opt->prompt_len);
-    const uint64_t pst = vx_stream(opt->seed, vx_tag(0, VX_TAG_PROMPT));
-    for (uint32_t i = 0; i < opt->prompt_len; ++i) {
-        prompt[i] = opt->prompt_tokens ? opt->prompt_tokens[i] : vx_uniform_u32(pst, i, cfg.vocab_size);
-        if (prompt[i] >= cfg.vocab_size && !rc) rc = VELOX_HIP_EINVAL;
+    // sequence b's prompt: seeded ids (sequence 0: the single-sequence prompt) or explicit ones
+    std::vector<uint32_t> prompt((size_t)opt->prompt_len * B);
+    for (uint32_t b = 0; b < B; ++b) {
+        const uint64_t pst = vx_stream(opt->seed + (uint64_t)b * 0x9E3779B97F4A7C15ULL, vx_tag(0, VX_TAG_PROMPT));
+        for (uint32_t i = 0; i < opt->prompt_len; ++i) {
+            uint32_t& t = prompt[(size_t)b * opt->prompt_len + i];
+            t = opt->prompt_tokens ? opt->prompt_tokens[i] : vx_uniform_u32(pst, i, cfg.vocab_size);
+            if (t >= cfg.vocab_size && !rc) rc = VELOX_HIP_EINVAL;
+        }
     }
     for (uint32_t l = 0; l < cfg.num_layers && !rc && base; ++l)
-        rc = velox_hip_fill_kv(&A, l, base, opt->seed, 1.0f, st);
-    if (!rc) rc = velox_hip_set_prompt(&A, prompt.data(), opt->prompt_len, st);
-    if (!rc) rc = velox_hip_set_state(&A, base, prompt[0], st);
+        for (uint32_t b = 0; b < B && !rc; ++b)
+            rc = B > 1 ? velox_hip_fill_kv_seq(&A, l, b, base, opt->seed, 1.0f, st)
+                       : velox_hip_fill_kv(&A, l, base, opt->seed, 1.0f, st);
+    if (B > 1) {
+        for (uint32_t b = 0; b < B && !rc; ++b) {
+            rc = velox_hip_batch_set_prompt(&A, b, prompt.data() + (size_t)b * opt->prompt_len, opt->prompt_len, st);
+            if (!rc) rc = velox_hip_batch_set_state(&A, b, base, prompt[(size_t)b * opt->prompt_len], st);
+        }
+    } else {
+        if (!rc) rc = velox_hip_set_prompt(&A, prompt.data(), opt->prompt_len, st);
+        if (!rc) rc = velox_hip_set_state(&A, base, prompt[0], st);
+    }
     velox_hip_last_error();
+    auto launch_step = [&]() {
+        if (B > 1) velox_hip_decode_batch_graph_step(&A, B, 1ULL, st);
+        else velox_hip_decode_graph_step(&A, 1ULL, st);
+    };
     if (!rc && opt->use_graph) {
         hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
         if (e == hipSuccess) {
-            velox_hip_decode_graph_step(&A, 1ULL, st);
+            launch_step();
             e = hipStreamEndCapture(st, &graph);
         }
         if (e == hipSuccess) e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
@@ -922,7 +1135,7 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
     }
     auto one_step = [&]() {
         if (exec) vx_record(hipGraphLaunch(exec, st));
-        else velox_hip_decode_graph_step(&A, 1ULL, st);
+        else launch_step();
     };
     if (!rc) {
         hipEventRecord(e0, st);
@@ -947,12 +1160,14 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
         hipEventElapsedTime(&ms_d, e2, e3);
         rep->prefill_ms = ms_p;
         rep->decode_ms = ms_d;
-        rep->tok_per_s = opt->steps && ms_d > 0 ? opt->steps / (ms_d * 1e-3) : 0.0;
+        rep->tok_per_s = opt->steps && ms_d > 0 ? (double)B * opt->steps / (ms_d * 1e-3) : 0.0;
         double bytes = 0.0;
         const uint32_t first = base + opt->prompt_len + opt->warmup;
-        for (uint32_t s = 0; s < opt->steps; ++s) bytes += (double)velox_hip_model_step_bytes(M, first + s);
+        for (uint32_t s = 0; s < opt->steps; ++s)
+            bytes += (double)(B > 1 ? velox_hip_model_batch_step_bytes(M, B, first + s)
+                                    : velox_hip_model_step_bytes(M, first + s));
         rep->bytes_per_step = opt->steps ? bytes / opt->steps : 0.0;
-        rep->hbm_gbps = rep->bytes_per_step * rep->tok_per_s / 1e9;
+        rep->hbm_gbps = rep->bytes_per_step * rep->tok_per_s / B / 1e9;
         // ring[pos & 1023] holds the argmax after position pos (velox_cuda_runner.cu:541-546)
         uint32_t n = 0;
         uint32_t lo = total > VELOX_HIP_RING_SIZE ? total - VELOX_HIP_RING_SIZE : 0;
@@ -972,10 +1187,23 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
         g.eps = cfg.rms_norm_eps;
         g.x = (const float*)(act + M->a_h);
         g.y = (float*)(act + M->a_act);
+        // batched: the MFMA GEMM of the gate/up + SwiGLU over all B sequences' fp16 activations
+        VxBGemmArgs bg;
+        std::memset(&bg, 0, sizeof(bg));
+        bg.batch = B;
+        bg.active_mask = 1;
+        bg.x16 = (const uint16_t*)(act + M->a_bxa);
+        bg.ldx = M->xw;
+        bg.out16 = (uint16_t*)(act + M->a_bxb);
+        bg.ldo = M->xw;
         auto launch_all = [&]() {
             for (uint32_t l = 0; l < cfg.num_layers; ++l) {
-                g.gain = (const float*)(A.norm_weight_arena + M->layers[l].mlp_norm);
-                vx_record(vx_launch_gemv(vx_view(&A, M->layers[l].gate_up), g, VX_EPI_SWIGLU, M->max_wgs, st));
+                if (B > 1) {
+                    vx_record(vx_launch_bgemm(vx_view(&A, M->layers[l].gate_up), bg, VX_EPI_SWIGLU, st));
+                } else {
+                    g.gain = (const float*)(A.norm_weight_arena + M->layers[l].mlp_norm);
+                    vx_record(vx_launch_gemv(vx_view(&A, M->layers[l].gate_up), g, VX_EPI_SWIGLU, M->max_wgs, st));
+                }
             }
         };
         launch_all();  // warm
@@ -989,7 +1217,8 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
         rep->kernel_launches = opt->kernel_passes * cfg.num_layers;
         rep->kernel_us = rep->kernel_launches ? ms * 1e3 / rep->kernel_launches : 0.0;
         rep->kernel_bytes = (double)cfg.intermediate_dim * 2.0 * cfg.hidden_dim / 32.0 * 18.0 +
-                            (double)cfg.hidden_dim * 4.0 * 2.0 + (double)cfg.intermediate_dim * 4.0;
+                            (B > 1 ? (double)B * (cfg.hidden_dim * 2.0 + cfg.intermediate_dim * 2.0)
+                                   : (double)cfg.hidden_dim * 4.0 * 2.0 + (double)cfg.intermediate_dim * 4.0);
     }
     rep->status = rc;
     if (exec) hipGraphExecDestroy(exec);

@@ -540,19 +540,20 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     uint16_t* vn_s = kn_s + D;
     float* st_s = (float*)(vn_s + D);                      // [G][4]: m, l, alpha
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t g = blockIdx.y, sp = blockIdx.x;
-    const uint64_t step = a.state ? a.state->step : (uint64_t)a.fixed_pos;
+    const uint32_t g = blockIdx.y, sp = blockIdx.x, bq = blockIdx.z;  // bq: sequence of a batch
+    const uint64_t step = a.state ? a.state[bq].step : (uint64_t)a.fixed_pos;
     const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;  // safe_step clamp
     const uint32_t len = pos + 1u;
     const uint32_t chunk = (len + a.splits - 1u) / a.splits;
     const uint32_t t0 = min(sp * chunk, len);
     const uint32_t t1 = min(len, t0 + chunk);
-    uint16_t* Kc = a.kv + (size_t)g * a.s_max * D;
-    uint16_t* Vc = a.kv + ((size_t)a.hkv + g) * a.s_max * D;
+    uint16_t* kvb = a.kv + (size_t)bq * a.kv_bstride;
+    uint16_t* Kc = kvb + (size_t)g * a.s_max * D;
+    uint16_t* Vc = kvb + ((size_t)a.hkv + g) * a.s_max * D;
 
     // ---- q, the new k/v and the RoPE row into registers (clamped: no load under a branch) ----
-    const float* q = a.qkv;
-    const float* k = a.qkv + (size_t)a.hq * D;
+    const float* q = a.qkv + (size_t)bq * a.qkv_bstride;
+    const float* k = q + (size_t)a.hq * D;
     const float* v = k + (size_t)a.hkv * D;
     const float2* rp = a.rope + (size_t)pos * HALF;
     constexpr int NP = (G + 1) * HALF, RP = (NP + NT - 1) / NT;  // RoPE pairs, pairs per thread
@@ -716,7 +717,7 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
         const int idx = tid + i * NT;
         if (idx < G * D) {
             const int h = idx / D, d = idx % D;
-            const size_t hq_idx = (size_t)g * G + h;
+            const size_t hq_idx = (size_t)bq * a.hq + (size_t)g * G + h;  // (sequence, q head)
             const float m_h = st_s[h * 4 + 0], l_h = st_s[h * 4 + 1];
             if (a.splits == 1 && !a.partials_only) {
                 a.out[hq_idx * D + d] = l_h > 0.0f ? acc[i] / l_h : 0.0f;
@@ -1010,9 +1011,11 @@ hipError_t vx_attn_launch_t(const VxAttnArgs& a, hipStream_t st) {
         }
         attr_set = true;
     }
-    hipLaunchKernelGGL((vx_attn_kernel<D, G, W>), dim3(a.splits, a.hkv), dim3(64 * W), lds, st, a);
+    hipLaunchKernelGGL((vx_attn_kernel<D, G, W>), dim3(a.splits, a.hkv, a.batch ? a.batch : 1u), dim3(64 * W), lds,
+                       st, a);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && a.splits > 1 && !a.partials_only) {
+        if (a.batch > 1) return hipErrorInvalidValue;  // batched steps merge with vx_bmerge_kernel
         hipLaunchKernelGGL((vx_attn_merge_kernel<D>), dim3(a.hq), dim3(D), 0, st, a);
         e = hipGetLastError();
     }

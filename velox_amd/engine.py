@@ -16,7 +16,8 @@ import numpy as np
 from . import _lib as L
 
 
-def make_config(model, max_seq_len: int = 0, num_layers: int = 0, attn_splits: int = 0) -> L.ModelConfig:
+def make_config(model, max_seq_len: int = 0, num_layers: int = 0, attn_splits: int = 0,
+                max_batch: int = 0) -> L.ModelConfig:
     """A builtin config by name, or a dict of ModelConfig fields (custom shapes for tests)."""
     if isinstance(model, str):
         cfg = L.builtin_config(model, max_seq_len)
@@ -33,14 +34,17 @@ def make_config(model, max_seq_len: int = 0, num_layers: int = 0, attn_splits: i
         cfg.num_layers = num_layers
     if attn_splits:
         cfg.attn_splits = attn_splits
+    if max_batch:
+        cfg.max_batch = max_batch
     return cfg
 
 
 class HipDecodeEngine:
     def __init__(self, model, seed: int = 0, sigma: float = 0.02, norm_sigma: float = 0.0,
-                 max_seq_len: int = 0, num_layers: int = 0, attn_splits: int = 0, synthesize: bool = True):
+                 max_seq_len: int = 0, num_layers: int = 0, attn_splits: int = 0, synthesize: bool = True,
+                 max_batch: int = 0):
         self.lib = L.load()
-        self.cfg = make_config(model, max_seq_len, num_layers, attn_splits)
+        self.cfg = make_config(model, max_seq_len, num_layers, attn_splits, max_batch)
         self._model = C.c_void_p()
         L.check(self.lib.velox_hip_model_create(C.byref(self.cfg), C.byref(self._model)), "model_create")
         self.arena = L.Arena()
@@ -152,10 +156,52 @@ class HipDecodeEngine:
             pass
 
 
+class HipBatchEngine(HipDecodeEngine):
+    """Batched decode of up to 32 independent sequences (src/runners/velox_cuda_runner_k2.cu:
+    553-1088 batched kernels): each sequence keeps its own KV cache, decode state, prompt and ring;
+    one step advances all of them, reading the weights once (MFMA GEMMs)."""
+
+    def __init__(self, model, max_batch: int, **kw):
+        super().__init__(model, max_batch=max_batch, **kw)
+        mb, lo, ho = C.c_uint32(), C.c_uint64(), C.c_uint64()
+        L.check(self.lib.velox_hip_model_batch_layout(self._model, C.byref(mb), C.byref(lo), C.byref(ho)))
+        self.max_batch, self.blogits_off, self.bhidden_off = mb.value, lo.value, ho.value
+
+    def fill_kv_seq(self, layer: int, seq: int, n_pos: int, seed: int, sigma: float = 1.0) -> None:
+        L.check(self.lib.velox_hip_fill_kv_seq(C.byref(self.arena), layer, seq, n_pos, seed, sigma, None))
+
+    def set_prompt_seq(self, seq: int, tokens) -> None:
+        arr = (C.c_uint32 * max(1, len(tokens)))(*[int(t) for t in tokens])
+        L.check(self.lib.velox_hip_batch_set_prompt(C.byref(self.arena), seq, arr, len(tokens), None))
+
+    def set_state_seq(self, seq: int, step: int, token: int) -> None:
+        L.check(self.lib.velox_hip_batch_set_state(C.byref(self.arena), seq, step, token, None))
+
+    def state_seq(self, seq: int) -> tuple[int, int]:
+        s = L.DecodeState()
+        L.check(self.lib.velox_hip_batch_get_state(C.byref(self.arena), seq, C.byref(s), None))
+        return int(s.step), int(s.token)
+
+    def batch_step(self, batch: int) -> None:
+        self.lib.velox_hip_decode_batch_graph_step(C.byref(self.arena), batch, 1, None)
+
+    def logits_seq(self, seq: int) -> np.ndarray:
+        out = np.empty(self.vocab, np.float32)
+        L.memcpy_dtoh(out.ctypes.data, self.arena.activation_arena + self.blogits_off + seq * self.vocab * 4,
+                      out.nbytes)
+        return out
+
+    def ring_seq(self, seq: int, pos: int) -> int:
+        return int(self.arena.host_pinned_ring[seq * L.RING_SIZE + (pos & (L.RING_SIZE - 1))])
+
+    def step_bytes_batch(self, batch: int, pos: int) -> int:
+        return int(self.lib.velox_hip_model_batch_step_bytes(self._model, batch, pos))
+
+
 def run(model: str = "llama3_8b", prompt_len: int = 128, warmup: int = 5, steps: int = 251, seed: int = 1234,
         sigma: float = 0.02, norm_sigma: float = 0.0, use_graph: bool = True, num_layers: int = 0,
         max_seq_len: int = 0, max_tokens: int = 1024, kernel_passes: int = 0,
-        prompt: list[int] | None = None, context_len: int = 0) -> tuple[dict, list[int]]:
+        prompt: list[int] | None = None, context_len: int = 0, batch: int = 1) -> tuple[dict, list[int]]:
     """The C++ runner flow (velox_hip_run): synthesize, capture, prefill, timed decode. `prompt`
     replaces the seeded random prompt of `prompt_len` ids; `context_len` > 0 starts from a seeded
     context of that many positions already in the KV cache (then prompt_len must be 1). Returned
@@ -166,7 +212,7 @@ def run(model: str = "llama3_8b", prompt_len: int = 128, warmup: int = 5, steps:
         prompt_len = len(prompt)
         ptoks = (C.c_uint32 * prompt_len)(*prompt)
     opt = L.RunOptions(model.encode(), max_seq_len, prompt_len, warmup, steps, seed, sigma, norm_sigma,
-                       int(use_graph), num_layers, kernel_passes, 0, ptoks, context_len)
+                       int(use_graph), num_layers, kernel_passes, 0, ptoks, context_len, batch)
     rep = L.RunReport()
     toks = (C.c_uint32 * max_tokens)()
     rc = lib.velox_hip_run(C.byref(opt), toks, max_tokens, C.byref(rep))
