@@ -29,6 +29,7 @@ typedef uint32_t vx_bu4 __attribute__((ext_vector_type(4)));  // a plain vector 
                                                                // struct that arrays keep on the stack)
 
 constexpr int kBWaves = 4, kBThreads = 64 * kBWaves;
+constexpr uint32_t kBNormMaxParts = 8;  // K splits of a RESID GEMM that one batched RMSNorm folds in
 
 __device__ __forceinline__ float vx_bh2f(uint32_t h) { return __half2float(__ushort_as_half((unsigned short)h)); }
 
@@ -71,6 +72,8 @@ __global__ __launch_bounds__(kBThreads) void vx_bgemm_q4_kernel(VxBGemmArgs a) {
     vx_bu4* x_s = (vx_bu4*)(s_s + TPW * 64);          // [MT * 16][XP] fp16 activations (8 per chunk)
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t t0 = blockIdx.x * (uint32_t)TPW, n_iter = a.n_iter;
+    // this workgroup's items: all of them, or the blockIdx.y-th of gridDim.y equal K ranges
+    const uint32_t it_begin = blockIdx.y * n_iter / gridDim.y, it_end = (blockIdx.y + 1u) * n_iter / gridDim.y;
     const int nl = 16 * wave + (lane & 15), g = lane >> 4;  // this lane's weight row in the workgroup
     const int tl = nl / R, r = nl % R;
     vx_f4 acc[MT];
@@ -104,8 +107,8 @@ __global__ __launch_bounds__(kBThreads) void vx_bgemm_q4_kernel(VxBGemmArgs a) {
             xr[u] = *(const vx_bu4*)(a.x16 + (size_t)m * a.ldx + e);                                \
         }                                                                                           \
     } while (0)
-    VX_BGEMM_LOAD(0u);
-    for (uint32_t it = 0; it < n_iter; ++it) {
+    VX_BGEMM_LOAD(it_begin);
+    for (uint32_t it = it_begin; it < it_end; ++it) {
         __syncthreads();  // the previous item's operands are consumed
 #pragma unroll
         for (int u = 0; u < NC; ++u) {
@@ -122,7 +125,7 @@ __global__ __launch_bounds__(kBThreads) void vx_bgemm_q4_kernel(VxBGemmArgs a) {
             x_s[(i / XC) * XP + i % XC] = xr[u];
         }
         __syncthreads();
-        if (it + 1u < n_iter) VX_BGEMM_LOAD(it + 1u);
+        if (it + 1u < it_end) VX_BGEMM_LOAD(it + 1u);
 #pragma unroll 4
         for (int j = 0; j < S; ++j) {
             const int wi = (wave * S + j) * 16 + (lane & 15);  // this lane's row, block j
@@ -168,8 +171,10 @@ __global__ __launch_bounds__(kBThreads) void vx_bgemm_q4_kernel(VxBGemmArgs a) {
                 if (!ok || m >= a.batch) continue;
                 float* yp = a.y + (size_t)m * a.ldy + n;
                 if constexpr (EPI == VX_EPI_STORE) *yp = a.bias ? acc[mt][i] + a.bias[n] : acc[mt][i];
-                else if constexpr (EPI == VX_EPI_RESID) *yp += acc[mt][i];
-                else *yp = acc[mt][i];
+                else if constexpr (EPI == VX_EPI_RESID) {
+                    if (gridDim.y > 1u) a.part[blockIdx.y * a.pstride + (size_t)m * a.ldy + n] = acc[mt][i];
+                    else *yp += acc[mt][i];
+                } else *yp = acc[mt][i];
             }
         if constexpr (EPI == VX_EPI_ARGMAX) {
             // per sequence: the best (value, lowest index) of this workgroup's 64 rows
@@ -219,7 +224,8 @@ hipError_t vx_bgemm_launch_t(const VxBGemmArgs& a, hipStream_t st) {
         }
         attr_set = true;
     }
-    hipLaunchKernelGGL((vx_bgemm_q4_kernel<S, EPI, MT>), dim3(vx_bgemm_grid(a.n_tiles, S)), dim3(kBThreads), lds, st, a);
+    hipLaunchKernelGGL((vx_bgemm_q4_kernel<S, EPI, MT>), dim3(vx_bgemm_grid(a.n_tiles, S), a.ksplit > 1u ? a.ksplit : 1u),
+                       dim3(kBThreads), lds, st, a);
     return hipGetLastError();
 }
 
@@ -255,6 +261,9 @@ hipError_t vx_launch_bgemm(const VxMat& m, const VxBGemmArgs& a0, int epi, hipSt
     a.n_iter = m.n_iter;
     if (m.k == 0 || (m.k & 31u) || (a.ldx & 7u) || !a.x16) return hipErrorInvalidValue;
     if ((epi == VX_EPI_SWIGLU) != (m.paired != 0)) return hipErrorInvalidValue;
+    if (a.ksplit > 1u && (epi != VX_EPI_RESID || !a.part || a.ksplit > m.n_iter || a.ksplit > kBNormMaxParts ||
+                          a.pstride < (uint64_t)a.batch * a.ldy))
+        return hipErrorInvalidValue;
     switch (epi) {
         case VX_EPI_STORE: return vx_bgemm_dispatch_mt<VX_EPI_STORE>(m.s, a, st);
         case VX_EPI_RESID: return vx_bgemm_dispatch_mt<VX_EPI_RESID>(m.s, a, st);
@@ -308,20 +317,69 @@ __global__ __launch_bounds__(256) void vx_bembed_kernel(VxMat m, const VeloxDeco
 
 // x16[b] = fp16((h[b] / rms(h[b])) * g): the RMSNorm of src/runtime.rs:588-601 per sequence, written
 // as the fp16 operand of the batched GEMM (the product is rounded to fp32 first, as in the GEMV).
-__global__ __launch_bounds__(256) void vx_bnorm_kernel(const float* h, uint32_t ldh, const float* g, uint32_t k,
-                                                       float eps, uint16_t* x16, uint32_t ldx, uint64_t mask) {
+// With parts, h[b] first takes the K-split partial sums of the RESID GEMM before it, added in split
+// order and written back. One workgroup of 1024 threads per sequence holds the row in registers
+// (NV float4 per thread), so every load of the row and of its partials is issued at once.
+template <int NV>
+__global__ __launch_bounds__(1024) void vx_bnorm_kernel(float* h, uint32_t ldh, const float* parts, uint32_t nparts,
+                                                        uint64_t pstride, const float* g, uint32_t k, float eps,
+                                                        uint16_t* x16, uint32_t ldx, uint64_t mask) {
     if ((mask & 1ULL) == 0ULL) return;
-    __shared__ float red[4];
-    const float* x = h + (size_t)blockIdx.x * ldh;
+    __shared__ float red[16];
+    const uint32_t b = blockIdx.x, k4 = k >> 2;
+    float4* x = (float4*)(h + (size_t)b * ldh);
+    float4 v[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t i = min(threadIdx.x + 1024u * j, k4 - 1u);
+        v[j] = x[i];
+    }
+    if (parts) {
+        // every partial of every element loaded before the first add (split index clamped; the
+        // adds past nparts are skipped)
+        float4 p[kBNormMaxParts][NV];
+#pragma unroll
+        for (uint32_t s = 0; s < kBNormMaxParts; ++s)
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const uint32_t i = min(threadIdx.x + 1024u * j, k4 - 1u);
+                p[s][j] = ((const float4*)(parts + min(s, nparts - 1u) * pstride + (size_t)b * ldh))[i];
+            }
+#pragma unroll
+        for (uint32_t s = 0; s < kBNormMaxParts; ++s)
+            if (s < nparts)
+#pragma unroll
+                for (int j = 0; j < NV; ++j) {
+                    v[j].x += p[s][j].x;
+                    v[j].y += p[s][j].y;
+                    v[j].z += p[s][j].z;
+                    v[j].w += p[s][j].w;
+                }
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            if (threadIdx.x + 1024u * j < k4) x[threadIdx.x + 1024u * j] = v[j];
+    }
     float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < k; i += 256u) ss += x[i] * x[i];
-    ss = vx_bblock_sum<4>(ss, red);
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+        if (threadIdx.x + 1024u * j < k4) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+    ss = vx_bblock_sum<16>(ss, red);
     const float inv = 1.0f / sqrtf(ss / (float)k + eps);
-    uint16_t* o = x16 + (size_t)blockIdx.x * ldx;
-    for (uint32_t i = threadIdx.x; i < k; i += 256u) {
+    const float4* g4 = (const float4*)g;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t i = threadIdx.x + 1024u * j;
+        if (i >= k4) continue;
+        const float4 gg = g4[i];
+        uint16_t o[4];
+        {
 #pragma clang fp contract(off)
-        const float v = (x[i] * inv) * g[i];
-        o[i] = __half_as_ushort(__float2half(v));
+            o[0] = __half_as_ushort(__float2half((v[j].x * inv) * gg.x));
+            o[1] = __half_as_ushort(__float2half((v[j].y * inv) * gg.y));
+            o[2] = __half_as_ushort(__float2half((v[j].z * inv) * gg.z));
+            o[3] = __half_as_ushort(__float2half((v[j].w * inv) * gg.w));
+        }
+        *(uint2*)(x16 + (size_t)b * ldx + 4u * i) = make_uint2(o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16));
     }
 }
 
@@ -406,9 +464,20 @@ hipError_t vx_launch_bembed(const VxMat& m, const VeloxDecodeState* states, uint
     return hipGetLastError();
 }
 
-hipError_t vx_launch_bnorm(const float* h, uint32_t ldh, const float* g, uint32_t k, float eps, uint16_t* x16,
-                           uint32_t ldx, uint32_t batch, uint64_t mask, hipStream_t st) {
-    hipLaunchKernelGGL(vx_bnorm_kernel, dim3(batch), dim3(256), 0, st, h, ldh, g, k, eps, x16, ldx, mask);
+hipError_t vx_launch_bnorm(float* h, uint32_t ldh, const float* parts, uint32_t nparts, uint64_t pstride, const float* g,
+                           uint32_t k, float eps, uint16_t* x16, uint32_t ldx, uint32_t batch, uint64_t mask,
+                           hipStream_t st) {
+    // float4 rows: k, ldh, ldx and pstride multiples of 4 (16-byte h and parts rows, 8-byte x16 rows)
+    if (k == 0 || (k & 3u) || (ldh & 3u) || (ldx & 3u) || ldh < k || ldx < k) return hipErrorInvalidValue;
+    if (parts && (nparts == 0 || nparts > kBNormMaxParts || (pstride & 3u))) return hipErrorInvalidValue;
+    if (!parts) nparts = 0;
+    const dim3 grid(batch), block(1024);
+    if (k <= 4096u)
+        hipLaunchKernelGGL((vx_bnorm_kernel<1>), grid, block, 0, st, h, ldh, parts, nparts, pstride, g, k, eps, x16, ldx, mask);
+    else if (k <= 8192u)
+        hipLaunchKernelGGL((vx_bnorm_kernel<2>), grid, block, 0, st, h, ldh, parts, nparts, pstride, g, k, eps, x16, ldx, mask);
+    else  // rows past 8192 would need more than 64 registers of partials per thread
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

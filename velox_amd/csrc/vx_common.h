@@ -156,6 +156,12 @@ struct VxBGemmArgs {
     float* cand_v;         // ARGMAX: per (m, workgroup) candidates, [batch][gridDim.x]
     uint32_t* cand_i;
     uint64_t active_mask;
+    // RESID split over K: ksplit > 1 workgroup rows each cover n_iter / ksplit items and store
+    // their sums to part[ks * pstride + m * ldy + n] instead of adding to y; the next batched
+    // RMSNorm adds the ksplit partials to y in split order (vx_launch_bnorm's parts)
+    uint32_t ksplit;
+    float* part;
+    uint64_t pstride;
 };
 
 // Launch helpers implemented in vx_kernels.hip, used by vx_host.cpp.
@@ -167,8 +173,10 @@ hipError_t vx_launch_bgemm(const VxMat& m, const VxBGemmArgs& a, int epi, hipStr
 uint32_t vx_bgemm_grid(uint32_t n_tiles, uint32_t s);
 hipError_t vx_launch_bembed(const VxMat& m, const VeloxDecodeState* states, uint32_t batch, float* h, uint32_t ldh,
                             uint64_t mask, hipStream_t st);
-hipError_t vx_launch_bnorm(const float* h, uint32_t ldh, const float* g, uint32_t k, float eps, uint16_t* x16,
-                           uint32_t ldx, uint32_t batch, uint64_t mask, hipStream_t st);
+// parts != nullptr: h[b] += sum over s < nparts of parts[s * pstride + b * ldh] first (written back)
+hipError_t vx_launch_bnorm(float* h, uint32_t ldh, const float* parts, uint32_t nparts, uint64_t pstride, const float* g,
+                           uint32_t k, float eps, uint16_t* x16, uint32_t ldx, uint32_t batch, uint64_t mask,
+                           hipStream_t st);
 hipError_t vx_launch_bmerge(const float* part_o, const float* part_ml, uint32_t hq, uint32_t d, uint32_t splits,
                             uint16_t* x16, uint32_t ldx, uint32_t batch, uint64_t mask, hipStream_t st);
 hipError_t vx_launch_bfinalize(const float* cand_v, const uint32_t* cand_i, uint32_t n, VeloxDecodeState* states,

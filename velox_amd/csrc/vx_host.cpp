@@ -36,6 +36,21 @@ struct VxLayerPlan {
     uint64_t attn_norm = 0, mlp_norm = 0, bias = 0;
 };
 
+// K splits of a batched residual GEMM: enough workgroup rows over its 64-row groups to give
+// about 512 workgroups (the GEMMs of hidden-sized outputs have only hidden / 64 row groups), at
+// most 8 (the partials the batched RMSNorm folds in) and at most one item per split.
+uint32_t vx_bgemm_ksplit(const VxMatPlan& m) {
+    uint32_t ks = 0;
+    if (const char* env = std::getenv("VELOX_HIP_BGEMM_KSPLIT")) ks = (uint32_t)std::strtoul(env, nullptr, 10);  // tuning
+    if (ks == 0) {
+        const uint32_t wgs = vx_bgemm_grid(m.n_tiles, m.s);
+        ks = (512u + wgs - 1u) / wgs;
+    }
+    if (ks > 8u) ks = 8u;
+    if (ks > m.n_iter) ks = m.n_iter;
+    return ks ? ks : 1u;
+}
+
 }  // namespace
 
 struct VeloxHipModel {
@@ -55,6 +70,9 @@ struct VeloxHipModel {
     uint32_t batch = 1, xw = 0, head_bwgs = 0;
     uint64_t a_bstate = 0, a_bplen = 0, a_bprompt = 0, a_bh = 0, a_bxa = 0, a_bxb = 0, a_bqkv = 0;
     uint64_t a_bpart_o = 0, a_bpart_ml = 0, a_blogits = 0, a_bcand_v = 0, a_bcand_i = 0;
+    // K-split partials of the residual GEMMs (o_proj, down): [ksplit][batch][hidden]
+    uint64_t a_bpart_r = 0;
+    uint32_t ksplit_o = 1, ksplit_down = 1;
 };
 
 namespace {
@@ -140,6 +158,8 @@ bool vx_shape_ok(const VeloxHipModelConfig& c) {
     if (((uint64_t)c.num_heads * c.head_dim) % 32) return false;
     if (c.quant_mode != VELOX_QUANT_GGML_Q4_0) return false;
     if (c.num_kv_heads > 64 || c.attn_splits > 64 || c.max_batch > 32) return false;
+    // batched RMSNorm: float4 rows of at most 8192
+    if (c.max_batch > 1 && ((c.hidden_dim & 3u) || c.hidden_dim > 8192)) return false;
     if (c.hidden_dim > 32768 || c.intermediate_dim > 32768 || (uint64_t)c.num_heads * c.head_dim > 32768) return false;
     return true;
 }
@@ -312,6 +332,9 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
         M->a_blogits = take(B * c.vocab_size * 4);
         M->a_bcand_v = take(B * M->head_bwgs * 4);
         M->a_bcand_i = take(B * M->head_bwgs * 4);
+        M->a_bpart_r = take(8 * B * H * 4);
+        M->ksplit_o = vx_bgemm_ksplit(M->layers[0].o);
+        M->ksplit_down = vx_bgemm_ksplit(M->layers[0].down);
     }
     M->act_bytes = ac;
 
@@ -690,6 +713,8 @@ void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_
     uint16_t* xa = (uint16_t*)(act + M->a_bxa);
     uint16_t* xb = (uint16_t*)(act + M->a_bxb);
     float* qkv = (float*)(act + M->a_bqkv);
+    float* part_r = (float*)(act + M->a_bpart_r);
+    const uint64_t pstride = (uint64_t)M->batch * H;
 
     vx_record(vx_launch_bembed(vx_view(A, M->embed), states, batch, h, H, mask, st));
     VxAttnArgs at;
@@ -712,7 +737,9 @@ void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_
     VxBGemmArgs g;
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         const VxLayerPlan& L = M->layers[l];
-        vx_record(vx_launch_bnorm(h, H, vecp(L.attn_norm), H, c.rms_norm_eps, xa, M->xw, batch, mask, st));
+        // the previous layer's down projection left its K-split partials (none before layer 0)
+        vx_record(vx_launch_bnorm(h, H, l && M->ksplit_down > 1 ? part_r : nullptr, M->ksplit_down, pstride, vecp(L.attn_norm), H,
+                                  c.rms_norm_eps, xa, M->xw, batch, mask, st));
         std::memset(&g, 0, sizeof(g));
         g.batch = batch;
         g.active_mask = mask;
@@ -732,8 +759,12 @@ void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_
         g.ldx = M->xw;
         g.y = h;
         g.ldy = H;
+        g.ksplit = M->ksplit_o;
+        g.part = part_r;
+        g.pstride = pstride;
         vx_record(vx_launch_bgemm(vx_view(A, L.o), g, VX_EPI_RESID, st));
-        vx_record(vx_launch_bnorm(h, H, vecp(L.mlp_norm), H, c.rms_norm_eps, xa, M->xw, batch, mask, st));
+        vx_record(vx_launch_bnorm(h, H, M->ksplit_o > 1 ? part_r : nullptr, M->ksplit_o, pstride, vecp(L.mlp_norm), H,
+                                  c.rms_norm_eps, xa, M->xw, batch, mask, st));
         std::memset(&g, 0, sizeof(g));
         g.batch = batch;
         g.active_mask = mask;
@@ -749,9 +780,13 @@ void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_
         g.ldx = M->xw;
         g.y = h;
         g.ldy = H;
+        g.ksplit = M->ksplit_down;
+        g.part = part_r;
+        g.pstride = pstride;
         vx_record(vx_launch_bgemm(vx_view(A, L.down), g, VX_EPI_RESID, st));
     }
-    vx_record(vx_launch_bnorm(h, H, vecp(M->final_norm), H, c.rms_norm_eps, xa, M->xw, batch, mask, st));
+    vx_record(vx_launch_bnorm(h, H, M->ksplit_down > 1 ? part_r : nullptr, M->ksplit_down, pstride, vecp(M->final_norm),
+                              H, c.rms_norm_eps, xa, M->xw, batch, mask, st));
     std::memset(&g, 0, sizeof(g));
     g.batch = batch;
     g.active_mask = mask;
