@@ -11,6 +11,8 @@ import pytest
 from velox_amd import _lib as L
 from velox_amd.engine import HipDecodeEngine, run
 
+from test_gpu_kernels import kv_from_device
+
 pytestmark = pytest.mark.gpu
 
 LOGIT_TOL = 2e-2
@@ -150,9 +152,10 @@ def test_decode_long_context_vs_oracle(oracle, splits):
                           attn_splits=splits)
     gpu.fill_kv(0, ctx, seed=9, sigma=1.0)
     kvd = LONG["num_kv_heads"] * LONG["head_dim"]
-    raw = np.zeros(2 * kvd * max_seq, np.uint16)
+    cap = (max_seq + 31) // 32 * 32
+    raw = np.zeros(2 * kvd * cap, np.uint16)
     L.memcpy_dtoh(raw.ctypes.data, gpu.arena.kv_cache_pool, raw.nbytes)
-    kv = (raw.astype(np.uint32) << 16).view(np.float32).reshape(2, LONG["num_kv_heads"], max_seq, LONG["head_dim"])
+    kv = (kv_from_device(raw, LONG["num_kv_heads"], max_seq, LONG["head_dim"]).astype(np.uint32) << 16).view(np.float32)
     ref = oracle.Engine(dict(LONG, num_layers=1, max_seq_len=max_seq), seed=seed, sigma=0.02, norm_sigma=0.1,
                         q4_0=True, kv_bf16=True, threads=16)
     kr, vr = ref.kv_cache(0)

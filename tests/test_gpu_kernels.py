@@ -254,6 +254,42 @@ def _from_bf16(u16):
     return (u16.astype(np.uint32) << 16).view(np.float32)
 
 
+def kv_slot(r):
+    """Slot of position r (0..31) inside a V block: slot 8j + 4 half + i holds position 16 half + 4j + i."""
+    r = np.asarray(r)
+    return 8 * ((r % 16) // 4) + 4 * (r // 16) + r % 4
+
+
+def kv_to_device(cache):
+    """[2][hkv][s][D] (K, V) -> the device layer layout: K [hkv][s_cap][D], V [hkv][s_cap/32][D][32]."""
+    _, hkv, s, d = cache.shape
+    cap = (s + 31) // 32 * 32
+    k = np.zeros((hkv, cap, d), cache.dtype)
+    k[:, :s] = cache[0]
+    v = np.zeros((hkv, cap, d), cache.dtype)
+    v[:, :s] = cache[1]
+    vb = np.zeros((hkv, cap // 32, d, 32), cache.dtype)
+    r = np.arange(32)
+    vb[:, :, :, kv_slot(r)] = v.reshape(hkv, cap // 32, 32, d).transpose(0, 1, 3, 2)
+    return np.concatenate([k.ravel(), vb.ravel()])
+
+
+def kv_from_device(flat, hkv, s, d):
+    """Inverse of kv_to_device: the device layer layout -> [2][hkv][s][D]."""
+    cap = (s + 31) // 32 * 32
+    k = flat[:hkv * cap * d].reshape(hkv, cap, d)
+    vb = flat[hkv * cap * d:2 * hkv * cap * d].reshape(hkv, cap // 32, d, 32)
+    v = vb[:, :, :, kv_slot(np.arange(32))].transpose(0, 1, 3, 2).reshape(hkv, cap, d)
+    return np.stack([k[:, :s], v[:, :s]])
+
+
+def test_kv_layout_roundtrip():
+    """The V block slot order is a permutation of 0..31, and the layout helpers invert each other."""
+    assert sorted(kv_slot(np.arange(32)).tolist()) == list(range(32))
+    c = np.arange(2 * 3 * 40 * 8, dtype=np.uint16).reshape(2, 3, 40, 8)
+    assert np.array_equal(kv_from_device(kv_to_device(c), 3, 40, 8), c)
+
+
 @pytest.mark.parametrize("hq,hkv,D,pos,smax,splits", [
     (32, 8, 128, 0, 64, 4), (32, 8, 128, 383, 512, 13), (9, 3, 64, 37, 64, 2), (28, 4, 128, 1000, 2048, 64),
     (64, 8, 128, 300, 512, 1), (8, 8, 64, 5, 16, 16)])
@@ -262,11 +298,11 @@ def test_attention_decode(hiplib, oracle, dev, hq, hkv, D, pos, smax, splits):
     theta = 500000.0
     qkv = rng.standard_normal((hq + 2 * hkv) * D).astype(np.float32)
     cache = _bf16(rng.standard_normal((2, hkv, smax, D)).astype(np.float32))
-    dq, dkv, dout = dev.put(qkv), dev.put(cache.view(np.int16)), dev.empty(hq * D)
+    dq, dkv, dout = dev.put(qkv), dev.put(kv_to_device(cache).view(np.int16)), dev.empty(hq * D)
     L.check(hiplib.velox_hip_attention_decode(dq.data_ptr(), dkv.data_ptr(), hq, hkv, D, smax, pos, theta, splits,
                                               dout.data_ptr(), None))
     got = dev.get(dout)
-    new_cache = dev.get(dkv).view(np.uint16).reshape(2, hkv, smax, D)
+    new_cache = kv_from_device(dev.get(dkv).view(np.uint16), hkv, smax, D)
     # oracle: rope q and k (src/runtime.rs:745-768), bf16 K/V, two-pass softmax attention
     q = oracle.rope(qkv[:hq * D], hq, D, pos, theta)
     k_new = oracle.rope(qkv[hq * D:(hq + hkv) * D], hkv, D, pos, theta)

@@ -121,7 +121,7 @@ struct VxGemvArgs {
 
 struct VxAttnArgs {
     const float* qkv;
-    uint16_t* kv;            // layer base: [2][hkv][s_max][d] bf16
+    uint16_t* kv;            // layer base, bf16: K [hkv][s_cap][d], then V [hkv][s_cap / 32][d][32] (vx_vslot)
     const float2* rope;      // [s_max][d/2] (cos, sin)
     const VeloxDecodeState* state;
     uint32_t fixed_pos;      // used when state == nullptr
@@ -130,6 +130,7 @@ struct VxAttnArgs {
     uint32_t* counters;      // [hkv]
     float* out;              // [hq*d]
     uint32_t hq, hkv, s_max, splits;
+    uint32_t s_cap;          // KV plane capacity in positions: s_max rounded up to 32
     float scale;
     uint64_t active_mask;
     uint32_t partials_only;  // 1: always write (m, l, o) partials; the consumer merges them
@@ -192,7 +193,7 @@ hipError_t vx_launch_synth_q4(const VxMat& m, uint32_t rows, uint32_t row0, uint
 hipError_t vx_launch_fill_normal(float* out, uint64_t n, uint64_t stream, float coef, float mean, hipStream_t st);
 // Fills K/V of one layer, positions [0, n_pos): element (t, g, d) draws index (t*hkv + g)*D + d,
 // the [S][hkv*D] order of the reference's cache (src/runtime.rs:1358-1361).
-hipError_t vx_launch_fill_kv(uint16_t* layer_base, uint32_t hkv, uint32_t s_max, uint32_t d, uint32_t n_pos,
+hipError_t vx_launch_fill_kv(uint16_t* layer_base, uint32_t hkv, uint32_t s_cap, uint32_t d, uint32_t n_pos,
                              uint64_t stream_k, uint64_t stream_v, float coef, hipStream_t st);
 hipError_t vx_launch_dequant(const VxMat& m, float* out, hipStream_t st);
 hipError_t vx_launch_quantize(const float* x, uint32_t rows, uint32_t k, void* blocks, hipStream_t st);

@@ -63,7 +63,7 @@ struct VeloxHipModel {
     uint64_t a_state = 0, a_plen = 0, a_argmax_counter = 0, a_counters = 0, a_token = 0, a_prompt = 0;
     uint64_t a_h = 0, a_qkv = 0, a_attn = 0, a_act = 0, a_logits = 0, a_part_o = 0, a_part_ml = 0;
     uint64_t a_cand_v = 0, a_cand_i = 0;
-    uint32_t splits = 1, max_wgs = 2048;
+    uint32_t splits = 1, max_wgs = 2048, s_cap = 0;
     bool fused_merge = false;  // o_proj merges the attention partials
     // batched decode (max_batch > 1): per-sequence states, prompts, fp32 residuals, two fp16 GEMM
     // operands, q/k/v, attention partials, logits and LM-head candidates, sequence-major
@@ -269,7 +269,8 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
     M->scale_bytes = sc;
     M->norm_bytes = nc;
     M->batch = c.max_batch > 1 ? c.max_batch : 1u;
-    M->kv_layer_bytes = vx_align((uint64_t)2 * c.num_kv_heads * c.max_seq_len * D * 2);
+    M->s_cap = (c.max_seq_len + 31u) & ~31u;  // V planes hold blocks of 32 positions
+    M->kv_layer_bytes = vx_align((uint64_t)2 * c.num_kv_heads * M->s_cap * D * 2);
     M->kv_bytes = M->kv_layer_bytes * c.num_layers * M->batch;  // [layer][sequence]
 
     // Split-K over the sequence: up to 1024 positions, a power of two <= 8 splits of ~128
@@ -597,7 +598,7 @@ int velox_hip_fill_kv(VeloxHipArena* a, uint32_t layer, uint32_t n_pos, uint64_t
     const VeloxHipModelConfig& c = a->model->cfg;
     if (layer >= c.num_layers || n_pos > c.max_seq_len) return VELOX_HIP_EINVAL;
     uint16_t* base = vx_kv(a, layer, 0);
-    hipError_t e = vx_launch_fill_kv(base, c.num_kv_heads, c.max_seq_len, c.head_dim, n_pos,
+    hipError_t e = vx_launch_fill_kv(base, c.num_kv_heads, a->model->s_cap, c.head_dim, n_pos,
                                      vx_stream(seed, vx_tag(layer, VX_TAG_KV_K)),
                                      vx_stream(seed, vx_tag(layer, VX_TAG_KV_V)), vx_normal_coef(sigma), st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
@@ -668,7 +669,7 @@ int velox_hip_fill_kv_seq(VeloxHipArena* a, uint32_t layer, uint32_t seq, uint32
     if (layer >= c.num_layers || n_pos > c.max_seq_len) return VELOX_HIP_EINVAL;
     // sequence 0 is velox_hip_fill_kv's context; others draw from streams of a sequence-tagged seed
     const uint64_t sseed = seed + (uint64_t)seq * 0x9E3779B97F4A7C15ULL;
-    hipError_t e = vx_launch_fill_kv(vx_kv(a, layer, seq), c.num_kv_heads, c.max_seq_len, c.head_dim, n_pos,
+    hipError_t e = vx_launch_fill_kv(vx_kv(a, layer, seq), c.num_kv_heads, a->model->s_cap, c.head_dim, n_pos,
                                      vx_stream(sseed, vx_tag(layer, VX_TAG_KV_K)),
                                      vx_stream(sseed, vx_tag(layer, VX_TAG_KV_V)), vx_normal_coef(sigma), st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
@@ -727,6 +728,7 @@ void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_
     at.hq = c.num_heads;
     at.hkv = c.num_kv_heads;
     at.s_max = c.max_seq_len;
+    at.s_cap = M->s_cap;
     at.splits = M->splits;
     at.scale = 1.0f / sqrtf((float)D);
     at.active_mask = mask;
@@ -832,6 +834,7 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
     at.hq = c.num_heads;
     at.hkv = c.num_kv_heads;
     at.s_max = c.max_seq_len;
+    at.s_cap = M->s_cap;
     at.splits = M->splits;
     at.scale = 1.0f / sqrtf((float)c.head_dim);
     at.active_mask = mask;
@@ -1082,6 +1085,7 @@ int velox_hip_attention_decode(const float* d_qkv, uint16_t* d_kv_layer, uint32_
     at.hq = hq;
     at.hkv = hkv;
     at.s_max = s_max;
+    at.s_cap = (s_max + 31u) & ~31u;
     at.splits = splits;
     at.scale = 1.0f / sqrtf((float)d);
     at.active_mask = 1;

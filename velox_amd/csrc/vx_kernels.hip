@@ -499,66 +499,99 @@ __global__ __launch_bounds__(256) void vx_argmax_finalize_kernel(const float* ca
 }
 
 // =============================================================================================
-// Split-K decode attention with LDS-staged K/V tiles
+// Split-K decode attention on MFMA
 // =============================================================================================
 
-// Decode attention for one (split, kv head): RoPE of q and the new k (src/runtime.rs:745-768),
-// bf16 KV append, then softmax(q K^T / sqrt(D)) V over this split's positions
-// (src/runtime.rs:772-831) in tiles of kAttnTile positions staged in LDS:
-//   1. the tile's K and V rows are loaded with unconditional 16-byte loads (clamped rows) right
-//      behind q/k/v and the RoPE row, so one memory round trip brings everything;
-//   2. scores: a lane group of D/8 lanes per position, 8 dimensions per lane, DPP group sum;
-//   3. per head (one wave each), the tile's max, 2^(s - m) and sum, with the running (m, l) of the
-//      online softmax in the log2 domain;
-//   4. P V: one thread per (head, dimension) output, accumulating across tiles.
-// The result is the split's (m, l, o) partial (o unnormalized), merged by the o_proj GEMV or by
-// vx_attn_merge_kernel, or with one split and no consumer merge, the normalized output.
-constexpr int kAttnTile = 128;
+// KV cache of one layer (and sequence), bf16: the K plane [hkv][s_cap][D] row-major, and the V
+// plane [hkv][s_cap / 32][D][32]: per block of 32 positions, dimension-major, the 32 positions of
+// one dimension in the slot order vx_vslot gives. s_cap is the position capacity rounded up to 32.
+// Slot of position r (0..31) of a V block: the P.V MFMA's lane group j supplies, as its 8
+// K-elements, positions 4j..4j+3 and 16+4j..16+4j+3 -- the scores that the K.Q^T MFMA leaves in
+// lane group j for the block's two 16-position halves -- so slot 8j + 4 half + i holds position
+// 16 half + 4j + i, and one 16-byte load gives a lane its 8 values.
+__device__ __forceinline__ uint32_t vx_vslot(uint32_t r) { return 8u * ((r & 15u) >> 2) + 4u * (r >> 4) + (r & 3u); }
+
+typedef __bf16 vx_bf8 __attribute__((ext_vector_type(8)));
+typedef float vx_af4 __attribute__((ext_vector_type(4)));
+typedef uint32_t vx_au4 __attribute__((ext_vector_type(4)));
+
+// 8 fp32 values as the sum of NS bf16 vectors, each the truncation of what the previous ones leave
+// (exact differences): NS = 3 represents every fp32 exactly, NS = 2 to 2^-16 relative.
+template <int NS>
+__device__ __forceinline__ void vx_split_bf16(const float (&x)[8], vx_bf8 (&out)[NS]) {
+    float r[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = x[e];
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+        vx_au4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t a = __float_as_uint(r[2 * e]) & 0xFFFF0000u, b = __float_as_uint(r[2 * e + 1]) & 0xFFFF0000u;
+            w[e] = (a >> 16) | b;
+            r[2 * e] -= __uint_as_float(a);
+            r[2 * e + 1] -= __uint_as_float(b);
+        }
+        out[t] = __builtin_bit_cast(vx_bf8, w);
+    }
+}
+
+// Decode attention for one (split, kv head, sequence): RoPE of q and the new k
+// (src/runtime.rs:745-768), bf16 KV append, then softmax(q K^T / sqrt(D)) V over the positions
+// (src/runtime.rs:772-831). Split sp owns positions [sp * chunk, (sp + 1) * chunk) of the capacity
+// (chunk a multiple of 32 fixed by s_max and the split count, so the first K/V loads need no
+// state); its waves take the 32-position chunks below the current position in turn, on
+// v_mfma_f32_16x16x32_bf16:
+//   scores S^T[pos][head] = K Q^T: A = K rows straight from HBM (16 positions x 32 dimensions per
+//     instruction, one 16-byte load per lane), B = the G q heads (rows past G zero) as three bf16
+//     terms whose sum is the fp32 q, so every product and sum is fp32;
+//   online softmax per head in the log2 domain (q pre-scaled by log2(e) / sqrt(D)); each lane
+//     holds 8 positions of one head, the chunk maximum takes two lane exchanges;
+//   O[head][dim] += P V: A = the probabilities where the scores left them (two bf16 terms), B =
+//     the V block (one 16-byte load per lane and 16 dimensions).
+// The current position is never read from the cache (the append may not have landed): the split
+// that owns it adds q . k_new and v_new from the RoPE'd registers as one more softmax term when it
+// merges its waves' (m, l, O) into the split's partial (o unnormalized). The o_proj GEMV or
+// vx_attn_merge_kernel merges the partials; with one split and no consumer merge, the output is
+// normalized here.
+template <int D, int G>
+constexpr int vx_attn_hrows() { return G <= 4 ? 4 : 8; }  // head rows of the per-wave O in LDS
 
 template <int D, int G, int W>
 constexpr size_t vx_attn_lds_bytes() {
-    return (size_t)2 * kAttnTile * D * 2 + (size_t)G * D * 4 + (size_t)G * kAttnTile * 4 + (size_t)2 * D * 2 +
-           (size_t)G * 4 * 4;
+    return (size_t)3 * 16 * (D + 8) * 2 + (size_t)2 * D * 2 + (size_t)W * 16 * 2 * 4 + 16 * 4 +
+           (size_t)W * vx_attn_hrows<D, G>() * D * 4;
 }
 
 template <int D, int G, int W>
 __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     if ((a.active_mask & 1ULL) == 0ULL) return;
-    constexpr int HALF = D / 2, LPP = D / 8, NT = 64 * W, T = kAttnTile;
-    constexpr int NGRP = NT / LPP;                         // positions per score pass
-    constexpr int CPR = D / 8;                             // 16-byte chunks per K (or V) row
-    constexpr int NLD = (2 * T * CPR + NT - 1) / NT;       // tile chunks per thread
-    constexpr int OPT = (G * D + NT - 1) / NT;             // P V outputs per thread
+    constexpr int HALF = D / 2, NT = 64 * W, NC = D / 32, NB = D / 16, HR = vx_attn_hrows<D, G>();
+    constexpr int QP = D + 8;  // padded q row: the 16 rows one operand read touches sit 4 banks apart
     constexpr float kLog2e = 1.4426950408889634f;
-    static_assert(W >= G, "one wave per head for the softmax statistics");
+    static_assert(G >= 1 && G <= 8, "q heads of a group: MFMA columns 0..G-1, O rows 4 grp + i < 8");
     extern __shared__ __align__(16) unsigned char vx_smem[];
-    uint16_t* k_s = (uint16_t*)vx_smem;                    // [T][D] bf16
-    uint16_t* v_s = k_s + T * D;                           // [T][D] bf16
-    float* q_s = (float*)(v_s + T * D);                    // [G][D], pre-scaled
-    float* p_s = q_s + G * D;                              // [G][T] scores, then probabilities
-    uint16_t* kn_s = (uint16_t*)(p_s + G * T);             // new position's k (RoPE'd), v
+    uint16_t* qt_s = (uint16_t*)vx_smem;                   // [3][16][QP] bf16 terms of the pre-scaled q
+    uint16_t* kn_s = qt_s + 3 * 16 * QP;                   // new position's k (RoPE'd), v
     uint16_t* vn_s = kn_s + D;
-    float* st_s = (float*)(vn_s + D);                      // [G][4]: m, l, alpha
+    float* ml_s = (float*)(vn_s + D);                      // [W][2][16]: per wave m, l of each head
+    float* sn_s = ml_s + W * 32;                           // [16]: q_h . k_new of the new position
+    float* o_s = sn_s + 16;                                // [W][HR][D]: per wave O
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, grp = lane >> 4;            // MFMA column (head / dimension), K group
     const uint32_t g = blockIdx.y, sp = blockIdx.x, bq = blockIdx.z;  // bq: sequence of a batch
-    const uint64_t step = a.state ? a.state[bq].step : (uint64_t)a.fixed_pos;
-    const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;  // safe_step clamp
-    const uint32_t len = pos + 1u;
-    const uint32_t chunk = (len + a.splits - 1u) / a.splits;
-    const uint32_t t0 = min(sp * chunk, len);
-    const uint32_t t1 = min(len, t0 + chunk);
+    const uint32_t chunk = ((a.s_max + a.splits - 1u) / a.splits + 31u) & ~31u;
+    const uint32_t t0 = sp * chunk;
     uint16_t* kvb = a.kv + (size_t)bq * a.kv_bstride;
-    uint16_t* Kc = kvb + (size_t)g * a.s_max * D;
-    uint16_t* Vc = kvb + ((size_t)a.hkv + g) * a.s_max * D;
+    uint16_t* Kc = kvb + (size_t)g * a.s_cap * D;
+    uint16_t* Vc = kvb + ((size_t)a.hkv + g) * a.s_cap * D;
 
-    // ---- q, the new k/v and the RoPE row into registers (clamped: no load under a branch) ----
+    // ---- q, the new k/v into registers (clamped: no load under a branch) ----
     const float* q = a.qkv + (size_t)bq * a.qkv_bstride;
     const float* k = q + (size_t)a.hq * D;
     const float* v = k + (size_t)a.hkv * D;
-    const float2* rp = a.rope + (size_t)pos * HALF;
     constexpr int NP = (G + 1) * HALF, RP = (NP + NT - 1) / NT;  // RoPE pairs, pairs per thread
     float r1[RP], r2[RP];
-    float2 rcs[RP];
 #pragma unroll
     for (int i = 0; i < RP; ++i) {
         const int p = min(tid + i * NT, NP - 1);
@@ -566,28 +599,45 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
         const float* src = hh < G ? q + (size_t)(g * G + hh) * D : k + (size_t)g * D;
         r1[i] = src[j];
         r2[i] = src[j + HALF];
-        rcs[i] = rp[j];
     }
     const float vnew = v[(size_t)g * D + min(tid, D - 1)];
-    __builtin_amdgcn_sched_barrier(0);  // these loads go out ahead of the K/V tile
 
-    // ---- K/V rows of a tile [tb, tb + T) into registers (rows past the split read row
-    // min(t, pos): in the cache, never used) ----
-    uint4 kv[NLD];
-    auto load_tile = [&](uint32_t tb) {
+    // ---- one 32-position chunk into registers: K rows cb + 16 b + col, dimensions 32 c + 8 grp;
+    // V block cb / 32, dimensions 16 nb + col (clamped to the capacity; positions at or past the
+    // current one are masked) ----
+    vx_bf8 kf[2][NC], vf[NB];
+    auto load_chunk = [&](uint32_t cb) {
 #pragma unroll
-        for (int j = 0; j < NLD; ++j) {
-            const int i = min(tid + j * NT, 2 * T * CPR - 1);
-            const int part = i / (T * CPR), r = (i % (T * CPR)) / CPR, c = i % CPR;
-            const uint32_t t = min(tb + (uint32_t)r, pos);
-            kv[j] = *(const uint4*)((part ? Vc : Kc) + (size_t)t * D + 8 * c);
+        for (int b = 0; b < 2; ++b) {
+            const uint32_t row = min(cb + 16u * b + (uint32_t)col, a.s_cap - 1u);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) kf[b][c] = *(const vx_bf8*)(Kc + (size_t)row * D + 32 * c + 8 * grp);
         }
+        const uint16_t* vb = Vc + (size_t)(min(cb, a.s_cap - 32u) >> 5) * D * 32;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) vf[nb] = *(const vx_bf8*)(vb + (16 * nb + col) * 32 + 8 * grp);
     };
-    load_tile(t0);
+    uint32_t ci = (uint32_t)wave;
+    load_chunk(t0 + 32u * min(ci, chunk / 32u - 1u));
+    // q/k/v and the first chunk go out before the state is read: scalar loads complete out of
+    // order, so a state load issued earlier would hold these behind its s_waitcnt lgkmcnt(0)
     __builtin_amdgcn_sched_barrier(0);
+    const uint64_t step = a.state ? a.state[bq].step : (uint64_t)a.fixed_pos;
+    const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;  // safe_step clamp
+    const uint32_t t1 = min(pos, t0 + chunk);                 // cached positions [t0, t1)
+    const uint32_t n_chunks = t1 > t0 ? (t1 - t0 + 31u) >> 5 : 0u;
+    const bool has_new = t0 <= pos && pos < t0 + chunk;       // this split owns the new position
+    const float2* rp = a.rope + (size_t)pos * HALF;
+    float2 rcs[RP];
+#pragma unroll
+    for (int i = 0; i < RP; ++i) rcs[i] = rp[min(tid + i * NT, NP - 1) % HALF];
 
     // ---- RoPE on this group's q heads and the new k; bf16 K/V row ----
     const float qscale = a.scale * kLog2e;  // scores in the log2 domain
+    for (int i = tid; i < 3 * (16 - G) * QP / 2; i += NT) {  // q rows G..15 of every term: zero
+        const int t = i / ((16 - G) * QP / 2), r = i % ((16 - G) * QP / 2);
+        ((uint32_t*)(qt_s + (t * 16 + G) * QP))[r] = 0u;
+    }
 #pragma unroll
     for (int i = 0; i < RP; ++i) {
         const int p = tid + i * NT;
@@ -595,8 +645,16 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
         if (p < NP) {
             const int hh = p / HALF, j = p % HALF;
             if (hh < G) {
-                q_s[hh * D + j] = o.x * qscale;
-                q_s[hh * D + j + HALF] = o.y * qscale;
+                // the pre-scaled q as three bf16 terms (truncations of the exact remainders)
+                float x0 = o.x * qscale, x1 = o.y * qscale;
+#pragma unroll
+                for (int t = 0; t < 3; ++t) {
+                    const uint32_t b0 = __float_as_uint(x0) & 0xFFFF0000u, b1 = __float_as_uint(x1) & 0xFFFF0000u;
+                    qt_s[(t * 16 + hh) * QP + j] = (uint16_t)(b0 >> 16);
+                    qt_s[(t * 16 + hh) * QP + j + HALF] = (uint16_t)(b1 >> 16);
+                    x0 -= __uint_as_float(b0);
+                    x1 -= __uint_as_float(b1);
+                }
             } else {
                 kn_s[j] = vx_f32_to_bf16_bits(o.x);
                 kn_s[j + HALF] = vx_f32_to_bf16_bits(o.y);
@@ -604,129 +662,132 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
         }
     }
     if (tid < D) vn_s[tid] = vx_f32_to_bf16_bits(vnew);
-    if (tid < G) {
-        st_s[tid * 4 + 0] = -INFINITY;  // running m
-        st_s[tid * 4 + 1] = 0.0f;       // running l
-    }
     __syncthreads();
     if (sp == 0) {
+        const uint16_t* vblk = Vc + (size_t)(pos >> 5) * D * 32 + vx_vslot(pos & 31u);
         for (int d = tid; d < D; d += NT) {
             Kc[(size_t)pos * D + d] = kn_s[d];
-            Vc[(size_t)pos * D + d] = vn_s[d];
+            ((uint16_t*)vblk)[d * 32] = vn_s[d];
         }
     }
-    const int grp = tid / LPP, sub = tid % LPP;
-    float qv[G][8];
+    if (has_new && wave == W - 1) {
+        // q_h . k_new for the new position (q = the sum of its three exact terms)
+        for (int h = 0; h < G; ++h) {
+            float sn = 0.0f;
 #pragma unroll
-    for (int h = 0; h < G; ++h)
+            for (int d = lane; d < D; d += 64) {
+                float qv = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qv[h][e] = q_s[h * D + 8 * sub + e];
-    float acc[OPT];
+                for (int t = 0; t < 3; ++t) qv += __uint_as_float((uint32_t)qt_s[(t * 16 + h) * QP + d] << 16);
+                sn += qv * __uint_as_float((uint32_t)kn_s[d] << 16);
+            }
+            sn = vx_wave_sum(sn);
+            if (lane == 0) sn_s[h] = sn;
+        }
+    }
+    // q operand: head col (rows past G are zero), dimensions 32 c + 8 grp .. + 7, three bf16 terms
+    vx_bf8 qop[NC][3];
 #pragma unroll
-    for (int i = 0; i < OPT; ++i) acc[i] = 0.0f;
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int t = 0; t < 3; ++t) qop[c][t] = *(const vx_bf8*)(qt_s + (t * 16 + col) * QP + 32 * c + 8 * grp);
 
-    for (uint32_t tb = t0; tb < t1; tb += T) {
-        if (tb != t0) load_tile(tb);
-        const int tt = (int)min((uint32_t)T, t1 - tb);  // positions in this tile
-        // stage the tile; the current position comes from the RoPE'd k / new v (the cache write
-        // above may not have landed)
+    float m_run = -INFINITY, l_run = 0.0f;  // head col: running max, this lane's share of the sum
+    vx_af4 o_acc[NB];
 #pragma unroll
-        for (int j = 0; j < NLD; ++j) {
-            const int i = tid + j * NT;
-            if (i < 2 * T * CPR) {
-                const int part = i / (T * CPR), r = (i % (T * CPR)) / CPR, c = i % CPR;
-                uint4 val = kv[j];
-                if (tb + (uint32_t)r == pos) val = *(const uint4*)((part ? vn_s : kn_s) + 8 * c);
-                *(uint4*)((part ? v_s : k_s) + r * D + 8 * c) = val;
-            }
+    for (int nb = 0; nb < NB; ++nb) o_acc[nb] = vx_af4{0.f, 0.f, 0.f, 0.f};
+
+    for (; ci < n_chunks; ci += W) {
+        const uint32_t cb = t0 + 32u * ci;
+        // scores: sc[b][i] = S[position cb + 16 b + 4 grp + i][head col]
+        vx_af4 sc[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            sc[b] = vx_af4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int t = 0; t < 3; ++t) sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[b][c], qop[c][t], sc[b], 0, 0, 0);
         }
-        __syncthreads();
-        // scores s[h][r] = q_h . k_r (q pre-scaled)
-        for (int r = grp; r < tt; r += NGRP) {
-            const uint4 kq = *(const uint4*)(k_s + r * D + 8 * sub);
-            const uint32_t kw[4] = {kq.x, kq.y, kq.z, kq.w};
-            float kf[8];
+        float pr[8];
+        float mx = -INFINITY;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                kf[2 * e] = __builtin_bit_cast(float, kw[e] << 16);
-                kf[2 * e + 1] = __builtin_bit_cast(float, kw[e] & 0xFFFF0000u);
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t p = cb + 16u * b + 4u * grp + i;
+                pr[4 * b + i] = p < t1 ? sc[b][i] : -INFINITY;
+                mx = fmaxf(mx, pr[4 * b + i]);
             }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = m_run == -INFINITY ? 0.0f : vx_exp2(m_run - m_new);
+        float lt = 0.0f;
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
-                float sc = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) sc += qv[h][e] * kf[e];
-                sc = vx_group_sum<LPP>(sc);
-                if (sub == 0) p_s[h * T + r] = sc;
-            }
+        for (int e = 0; e < 8; ++e) {
+            pr[e] = pr[e] == -INFINITY ? 0.0f : vx_exp2(pr[e] - m_new);
+            lt += pr[e];
         }
-        __syncthreads();
-        // per head: tile max, probabilities, running (m, l) and the rescale factor alpha
-        if (wave < G) {
-            const int h = wave;
-            float sv[T / 64];
-            float mt = -INFINITY;
+        l_run = l_run * alpha + lt;
+        m_run = m_new;
+        // rescale O: o_acc[nb][i] belongs to head 4 grp + i, whose alpha lane (4 grp + i) holds
 #pragma unroll
-            for (int i = 0; i < T / 64; ++i) {
-                sv[i] = lane + 64 * i < tt ? p_s[h * T + lane + 64 * i] : -INFINITY;
-                mt = fmaxf(mt, sv[i]);
-            }
-            mt = vx_wave_max(mt);
-            const float m_old = st_s[h * 4 + 0];
-            const float m_new = fmaxf(m_old, mt);
-            float lt = 0.0f;
+        for (int i = 0; i < 4; ++i) {
+            const float ai = __shfl(alpha, 4 * grp + i);
 #pragma unroll
-            for (int i = 0; i < T / 64; ++i) {
-                const float pr = sv[i] == -INFINITY ? 0.0f : vx_exp2(sv[i] - m_new);
-                p_s[h * T + lane + 64 * i] = pr;
-                lt += pr;
-            }
-            lt = vx_wave_sum(lt);
-            if (lane == 0) {
-                const float alpha = m_old == -INFINITY ? 0.0f : vx_exp2(m_old - m_new);
-                st_s[h * 4 + 0] = m_new;
-                st_s[h * 4 + 1] = st_s[h * 4 + 1] * alpha + lt;
-                st_s[h * 4 + 2] = alpha;
-            }
+            for (int nb = 0; nb < NB; ++nb) o_acc[nb][i] *= ai;
         }
-        __syncthreads();
-        // P V: thread -> (head, dimension)
+        vx_bf8 pop[2];
+        vx_split_bf16<2>(pr, pop);
 #pragma unroll
-        for (int i = 0; i < OPT; ++i) {
-            const int idx = tid + i * NT;
-            if (idx < G * D) {
-                const int h = idx / D, d = idx % D;
-                float o = acc[i] * st_s[h * 4 + 2];
-                const float* ph = p_s + h * T;
-                for (int r = 0; r < tt; r += 4) {
-                    const float4 pr = *(const float4*)(ph + r);  // rows >= tt hold p = 0
-                    o += pr.x * __builtin_bit_cast(float, (uint32_t)v_s[(r + 0) * D + d] << 16);
-                    o += pr.y * __builtin_bit_cast(float, (uint32_t)v_s[(r + 1) * D + d] << 16);
-                    o += pr.z * __builtin_bit_cast(float, (uint32_t)v_s[(r + 2) * D + d] << 16);
-                    o += pr.w * __builtin_bit_cast(float, (uint32_t)v_s[(r + 3) * D + d] << 16);
-                }
-                acc[i] = o;
-            }
-        }
-        __syncthreads();  // the next tile overwrites k_s, v_s and p_s
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) o_acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop[t], vf[nb], o_acc[nb], 0, 0, 0);
+        if (ci + W < n_chunks) load_chunk(t0 + 32u * (ci + W));
     }
 
-    // ---- this split's partial (or the normalized output) ----
+    // ---- merge the waves (and the new position): per head the max m, weights 2^(m_w - m) ----
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    if (lane < 16) {
+        ml_s[wave * 32 + lane] = m_run;
+        ml_s[wave * 32 + 16 + lane] = l_run;
+    }
+    if (grp < HR / 4) {
 #pragma unroll
-    for (int i = 0; i < OPT; ++i) {
-        const int idx = tid + i * NT;
-        if (idx < G * D) {
-            const int h = idx / D, d = idx % D;
-            const size_t hq_idx = (size_t)bq * a.hq + (size_t)g * G + h;  // (sequence, q head)
-            const float m_h = st_s[h * 4 + 0], l_h = st_s[h * 4 + 1];
-            if (a.splits == 1 && !a.partials_only) {
-                a.out[hq_idx * D + d] = l_h > 0.0f ? acc[i] / l_h : 0.0f;
-            } else {
-                a.part_o[(hq_idx * a.splits + sp) * D + d] = acc[i];
-                if (d == 0) {
-                    a.part_ml[(hq_idx * a.splits + sp) * 2] = m_h;
-                    a.part_ml[(hq_idx * a.splits + sp) * 2 + 1] = l_h;
-                }
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o_s[(wave * HR + 4 * grp + i) * D + 16 * nb + col] = o_acc[nb][i];
+    }
+    __syncthreads();
+    for (int idx = tid; idx < G * D; idx += NT) {
+        const int h = idx / D, d = idx % D;
+        const float sn = has_new ? sn_s[h] : -INFINITY;
+        float M = sn;
+#pragma unroll
+        for (int w = 0; w < W; ++w) M = fmaxf(M, ml_s[w * 32 + h]);
+        float o = 0.0f, l = 0.0f;
+        if (has_new) {
+            const float wt = vx_exp2(sn - M);
+            o = wt * __uint_as_float((uint32_t)vn_s[d] << 16);
+            l = wt;
+        }
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float mw = ml_s[w * 32 + h];
+            const float wt = mw == -INFINITY ? 0.0f : vx_exp2(mw - M);
+            o += wt * o_s[(w * HR + h) * D + d];
+            l += wt * ml_s[w * 32 + 16 + h];
+        }
+        const size_t hq_idx = (size_t)bq * a.hq + (size_t)g * G + h;  // (sequence, q head)
+        if (a.splits == 1 && !a.partials_only) {
+            a.out[hq_idx * D + d] = l > 0.0f ? o / l : 0.0f;
+        } else {
+            a.part_o[(hq_idx * a.splits + sp) * D + d] = o;
+            if (d == 0) {
+                a.part_ml[(hq_idx * a.splits + sp) * 2] = M;
+                a.part_ml[(hq_idx * a.splits + sp) * 2 + 1] = l;
             }
         }
     }
@@ -816,7 +877,7 @@ __global__ __launch_bounds__(kWG) void vx_fill_normal_kernel(float* out, uint64_
         out[i] = vx_normal_value(stream, i, coef, mean);
 }
 
-__global__ __launch_bounds__(kWG) void vx_fill_kv_kernel(uint16_t* base, uint32_t hkv, uint32_t s_max, uint32_t d,
+__global__ __launch_bounds__(kWG) void vx_fill_kv_kernel(uint16_t* base, uint32_t hkv, uint32_t s_cap, uint32_t d,
                                                          uint32_t n_pos, uint64_t stream_k, uint64_t stream_v,
                                                          float coef) {
     const uint64_t per_plane = (uint64_t)hkv * n_pos * d, n = 2 * per_plane;
@@ -827,7 +888,9 @@ __global__ __launch_bounds__(kWG) void vx_fill_kv_kernel(uint16_t* base, uint32_
         const uint32_t t = (uint32_t)((r / d) % n_pos), dd = (uint32_t)(r % d);
         const uint64_t ref_idx = ((uint64_t)t * hkv + g) * d + dd;
         const float v = vx_normal_value(kv ? stream_v : stream_k, ref_idx, coef, 0.0f);
-        base[(((uint64_t)kv * hkv + g) * s_max + t) * d + dd] = vx_f32_to_bf16_bits(v);
+        const uint64_t plane = ((uint64_t)kv * hkv + g) * s_cap * d;
+        const uint64_t off = kv ? ((uint64_t)(t >> 5) * d + dd) * 32u + vx_vslot(t & 31u) : (uint64_t)t * d + dd;
+        base[plane + off] = vx_f32_to_bf16_bits(v);
     }
 }
 
@@ -1066,7 +1129,9 @@ hipError_t vx_launch_argmax_finalize(const float* cand_v, const uint32_t* cand_i
 uint32_t vx_gemv_grid(uint32_t n_tiles, uint32_t max_wgs) { return vx_gemv_wgs(n_tiles, max_wgs); }
 
 hipError_t vx_launch_attention(const VxAttnArgs& a, uint32_t d, hipStream_t st) {
-    if (a.hkv == 0 || a.hq % a.hkv != 0 || a.splits == 0 || a.splits > 64 || a.s_max == 0) return hipErrorInvalidValue;
+    if (a.hkv == 0 || a.hq % a.hkv != 0 || a.splits == 0 || a.splits > 64 || a.s_max == 0 || (a.s_cap & 31u) ||
+        a.s_cap < a.s_max)
+        return hipErrorInvalidValue;
     const uint32_t G = a.hq / a.hkv;
     if (d == 64) {
         switch (G) {
@@ -1130,13 +1195,13 @@ hipError_t vx_launch_fill_normal(float* out, uint64_t n, uint64_t stream, float 
     return hipGetLastError();
 }
 
-hipError_t vx_launch_fill_kv(uint16_t* layer_base, uint32_t hkv, uint32_t s_max, uint32_t d, uint32_t n_pos,
+hipError_t vx_launch_fill_kv(uint16_t* layer_base, uint32_t hkv, uint32_t s_cap, uint32_t d, uint32_t n_pos,
                              uint64_t stream_k, uint64_t stream_v, float coef, hipStream_t st) {
     const uint64_t n = 2ULL * hkv * n_pos * d;
     if (n == 0) return hipSuccess;
     const size_t g = (n + kWG - 1) / kWG;
     hipLaunchKernelGGL(vx_fill_kv_kernel, dim3((unsigned)(g < 65536 ? g : 65536)), dim3(kWG), 0, st, layer_base, hkv,
-                       s_max, d, n_pos, stream_k, stream_v, coef);
+                       s_cap, d, n_pos, stream_k, stream_v, coef);
     return hipGetLastError();
 }
 
