@@ -289,6 +289,85 @@ typedef struct VeloxHipRunReport {
 /* Runs the whole flow; tokens (capacity max_tokens) receives prompt-forced and generated ids. */
 int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_tokens, VeloxHipRunReport* rep);
 
+/* ---- Absorbed multi-head latent attention layer (DeepSeek-V3 form) ----
+ * Replaces the reference's MLA step: the emitted velox_cuda_fused_mla_absorbed_attn
+ * (src/codegen.rs:2001-2109, launched 1x256 at :2993) and the CPU mla_absorbed_step_f32
+ * (src/runtime.rs:845-1044) with its absorbed weights (MlaAbsorptionPass, src/optimizer.rs:138-184).
+ * Per head h: q_abs_h = W_uk[h]^T q_nope_h; s_ht = softmax_scale * (q_abs_h . c_t + rope(q_rope_h) .
+ * kr_t); ctx_h = softmax_t(s) . c_t; o_h = W_uv[h] ctx_h; hidden += W_o [o_h]. q = W_qb rmsnorm(W_qa x)
+ * (q_lora_rank > 0) or W_qb x; [c_t | kr_t] = [rmsnorm(c) | rope(kr)] of W_kva x, appended to the
+ * bf16 latent cache. With num_heads 1, no q LoRA, no rope part, kv_norm 0 and identity W_kvb this
+ * is the reference's simplified step. Weights are fp8 e4m3fn with fp32 scales per 128x128 block. */
+typedef struct VeloxHipMlaConfig {
+    uint32_t hidden_dim, num_heads, q_lora_rank, kv_lora_rank, qk_nope_dim, qk_rope_dim, v_head_dim;
+    uint32_t num_layers, max_seq_len, max_batch; /* max_batch <= 32 */
+    uint32_t kv_norm;                            /* 1: RMSNorm on the latent (kv_a_layernorm) */
+    uint32_t attn_splits;                        /* 0: planner's choice */
+    float rms_norm_eps, rope_theta, softmax_scale; /* softmax_scale 0: 1/sqrt(qk_nope_dim + qk_rope_dim) */
+    uint32_t reserved;
+    uint64_t vram_budget_bytes;                  /* 0: 288e9 */
+} VeloxHipMlaConfig;
+
+typedef struct VeloxHipMla VeloxHipMla;
+
+/* weight kinds: fp8 matrices (row-major [rows][cols] as in the checkpoint) and fp32 gains */
+enum {
+    VELOX_MLA_Q_A = 1,       /* [q_lora_rank][hidden_dim] */
+    VELOX_MLA_Q_B = 2,       /* [num_heads * (nope + rope)][q_lora_rank or hidden_dim] */
+    VELOX_MLA_KV_A = 3,      /* [kv_lora_rank + rope][hidden_dim] */
+    VELOX_MLA_KV_B = 4,      /* [num_heads * (nope + v)][kv_lora_rank]: per head its nope k rows, then v rows */
+    VELOX_MLA_O = 5,         /* [hidden_dim][num_heads * v] */
+    VELOX_MLA_NORM = 6,      /* [hidden_dim] */
+    VELOX_MLA_Q_A_NORM = 7,  /* [q_lora_rank] */
+    VELOX_MLA_KV_A_NORM = 8  /* [kv_lora_rank] */
+};
+
+typedef struct VeloxHipMlaBuffers {
+    float* hidden;           /* [max_batch][hidden_dim] fp32: input and output of a layer step */
+    uint16_t* latent_cache;  /* bf16 [num_layers][max_batch][s_cap][kv_lora_rank + rope] */
+    VeloxDecodeState* states;/* [max_batch]: step = the sequence's position */
+    uint32_t s_cap, splits;
+    uint64_t weight_bytes, cache_bytes, act_bytes;
+} VeloxHipMlaBuffers;
+
+/* "deepseek_v3_mla": hidden 7168, 128 heads, q LoRA 1536, kv LoRA 512, nope 128 + rope 64, v 128. */
+int velox_hip_mla_builtin_config(const char* which, uint32_t max_seq_len, uint32_t max_batch,
+                                 VeloxHipMlaConfig* out);
+int velox_hip_mla_create(const VeloxHipMlaConfig* cfg, VeloxHipMla** out);  /* plan + one hipMalloc */
+void velox_hip_mla_destroy(VeloxHipMla* m);
+int velox_hip_mla_buffers(const VeloxHipMla* m, VeloxHipMlaBuffers* out);
+/* fp8 matrix of `kind` for `layer`: codes [rows][cols], scales [ceil(rows/128)][ceil(cols/128)]. */
+int velox_hip_mla_load_fp8(VeloxHipMla* m, int kind, uint32_t layer, const uint8_t* codes, const float* scales,
+                           hipStream_t stream);
+int velox_hip_mla_load_f32(VeloxHipMla* m, int kind, uint32_t layer, const float* data, uint64_t count,
+                           hipStream_t stream);
+/* Every weight seeded N(0, sigma) and quantized on the device (the oracle's vxo_fp8_synth_matrix);
+ * gains 1 (norm_sigma 0) or N(1, norm_sigma). */
+int velox_hip_mla_synthesize(VeloxHipMla* m, uint64_t seed, float sigma, float norm_sigma, hipStream_t stream);
+/* Latent rows [0, n_pos) of sequence `seq` in `layer` := bf16 of seeded N(0, sigma). */
+int velox_hip_mla_fill_cache(VeloxHipMla* m, uint32_t layer, uint32_t seq, uint32_t n_pos, uint64_t seed,
+                             float sigma, hipStream_t stream);
+int velox_hip_mla_set_position(VeloxHipMla* m, uint32_t seq, uint64_t pos, hipStream_t stream);
+/* hidden[b] += MLA(hidden[b]) for b < batch at each sequence's position; appends the latent row.
+ * Capturable; errors through velox_hip_last_error(). */
+void velox_hip_mla_layer_step(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t active_mask,
+                              hipStream_t stream);
+/* Algorithmic HBM bytes of one layer step (weights + scales + latent rows 0..pos + activations). */
+double velox_hip_mla_step_bytes(const VeloxHipMla* m, uint32_t batch, uint64_t pos);
+
+typedef struct VeloxHipMlaRunReport {
+    double us_per_layer;     /* mean device time of one layer step (hipGraph replays) */
+    double bytes_per_layer, hbm_gbps;
+    double attn_us;          /* mean attention-kernel time (event-timed passes) */
+    double attn_bytes;       /* its algorithmic bytes (latent rows read) */
+    double wall_ms;
+    int status;
+} VeloxHipMlaRunReport;
+/* Synthesize `which`, seed a context_len-position latent context per sequence, time `steps` layer
+ * steps of `batch` sequences at position context_len after `warmup` untimed ones. */
+int velox_hip_mla_run(const char* which, uint32_t batch, uint32_t context_len, uint32_t warmup, uint32_t steps,
+                      uint64_t seed, VeloxHipMlaRunReport* rep);
+
 #ifdef __cplusplus
 }
 #endif

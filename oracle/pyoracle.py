@@ -31,6 +31,17 @@ class VxoConfig(C.Structure):
     ]
 
 
+class VxoMlaConfig(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("hidden", "n_heads", "q_lora", "kv_lora", "d_nope", "d_rope", "d_v",
+                                          "kv_norm", "max_seq")] + \
+               [(n, C.c_float) for n in ("eps", "rope_theta", "scale")]
+
+
+class VxoMlaWeights(C.Structure):
+    _fields_ = [(n, C.POINTER(C.c_float)) for n in ("norm", "q_a", "q_a_norm", "q_b", "kv_a", "kv_a_norm", "kv_b",
+                                                    "o")]
+
+
 def build() -> None:
     subprocess.run(["make", "-s", "-C", HERE], check=True)
 
@@ -81,6 +92,15 @@ def lib() -> C.CDLL:
         L.vxo_argmax.argtypes = [fp, C.c_uint64]
         L.vxo_mla_absorbed_step.argtypes = [fp, fp, fp, fp, fp, fp, fp, C.c_uint64, C.c_uint64,
                                             C.c_uint64, C.c_uint64, C.c_float]
+        L.vxo_f32_to_e4m3.restype = C.c_uint8
+        L.vxo_f32_to_e4m3.argtypes = [C.c_float]
+        L.vxo_e4m3_to_f32.restype = C.c_float
+        L.vxo_e4m3_to_f32.argtypes = [C.c_uint8]
+        L.vxo_fp8_quantize.argtypes = [fp, C.c_uint64, C.c_uint64, u8p, fp]
+        L.vxo_fp8_dequant.argtypes = [u8p, fp, C.c_uint64, C.c_uint64, fp]
+        L.vxo_fp8_synth_matrix.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, C.c_float, u8p, fp, fp]
+        L.vxo_mla_layer_step.argtypes = [C.POINTER(VxoMlaConfig), C.POINTER(VxoMlaWeights), fp, C.c_int, fp, fp,
+                                         C.c_uint64]
         L.vxo_engine_create.restype = C.c_void_p
         L.vxo_engine_create.argtypes = [C.POINTER(VxoConfig), C.c_uint64, C.c_float, C.c_float, C.c_uint32, C.c_int]
         L.vxo_engine_destroy.argtypes = [C.c_void_p]
@@ -297,3 +317,84 @@ class RefSmolLM:
 
     def close(self):
         self.L.vxr_smollm_free()
+
+
+# ---- fp8 e4m3fn block format and the absorbed MLA layer ----
+MLA_TAGS = dict(norm=32, q_a=33, q_a_norm=34, q_b=35, kv_a=36, kv_a_norm=37, kv_b=38, o=39, hidden=40, cache=41)
+
+
+def e4m3_encode(x: np.ndarray) -> np.ndarray:
+    L = lib()
+    return np.array([L.vxo_f32_to_e4m3(float(v)) for v in np.asarray(x, np.float32).ravel()], np.uint8)
+
+
+def e4m3_decode(b: np.ndarray) -> np.ndarray:
+    L = lib()
+    return np.array([L.vxo_e4m3_to_f32(int(v)) for v in np.asarray(b, np.uint8).ravel()], np.float32)
+
+
+def fp8_quantize(w: np.ndarray):
+    """w [rows][cols] fp32 -> (codes uint8 [rows][cols], scales [ceil(rows/128)][ceil(cols/128)])."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    codes = np.zeros((rows, cols), np.uint8)
+    scales = np.zeros(((rows + 127) // 128, (cols + 127) // 128), np.float32)
+    lib().vxo_fp8_quantize(fptr(w), rows, cols, u8ptr(codes), fptr(scales))
+    return codes, scales
+
+
+def fp8_dequant(codes: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    codes = np.ascontiguousarray(codes, np.uint8)
+    rows, cols = codes.shape
+    out = np.zeros((rows, cols), np.float32)
+    lib().vxo_fp8_dequant(u8ptr(codes), fptr(np.ascontiguousarray(scales, np.float32)), rows, cols, fptr(out))
+    return out
+
+
+def fp8_synth_matrix(seed: int, tg: int, rows: int, cols: int, sigma: float):
+    """Seeded N(0, sigma) matrix as fp8 blocks: (codes, scales, dequantized fp32)."""
+    codes = np.zeros((rows, cols), np.uint8)
+    scales = np.zeros(((rows + 127) // 128, (cols + 127) // 128), np.float32)
+    deq = np.zeros((rows, cols), np.float32)
+    lib().vxo_fp8_synth_matrix(seed, tg, rows, cols, sigma, u8ptr(codes), fptr(scales), fptr(deq))
+    return codes, scales, deq
+
+
+def mla_config(hidden, n_heads, q_lora, kv_lora, d_nope, d_rope, d_v, kv_norm=1, max_seq=64, eps=1e-6,
+               rope_theta=10000.0, scale=None) -> VxoMlaConfig:
+    if scale is None:
+        scale = 1.0 / np.sqrt(np.float32(d_nope + d_rope))
+    return VxoMlaConfig(hidden, n_heads, q_lora, kv_lora, d_nope, d_rope, d_v, kv_norm, max_seq, eps, rope_theta,
+                        float(scale))
+
+
+def mla_layer_step(cfg: VxoMlaConfig, w: dict, cache: np.ndarray, h: np.ndarray, pos: int,
+                   cache_bf16: bool = True) -> np.ndarray:
+    """One absorbed-MLA decode step (vxo_mla_layer_step); cache [max_seq][kv_lora + d_rope] is updated."""
+    keep = {k: np.ascontiguousarray(v, np.float32) for k, v in w.items() if v is not None}
+    nul = C.POINTER(C.c_float)()
+    ws = VxoMlaWeights(*[fptr(keep[n]) if n in keep else nul for n in
+                         ("norm", "q_a", "q_a_norm", "q_b", "kv_a", "kv_a_norm", "kv_b", "o")])
+    h = np.ascontiguousarray(h, np.float32)
+    out = np.zeros_like(h)
+    assert cache.dtype == np.float32 and cache.flags.c_contiguous
+    lib().vxo_mla_layer_step(C.byref(cfg), C.byref(ws), fptr(cache), int(cache_bf16), fptr(h), fptr(out), pos)
+    return out
+
+
+def mla_synth_weights(cfg: VxoMlaConfig, seed: int, sigma: float = 0.02, norm_sigma: float = 0.0, layer: int = 0):
+    """The seeded fp8 MLA layer (device synthesizer's recipe): dequantized fp32 weights by name."""
+    H, nh, ql, lr = cfg.hidden, cfg.n_heads, cfg.q_lora, cfg.kv_lora
+    dq, R = cfg.d_nope + cfg.d_rope, cfg.kv_lora + cfg.d_rope
+    t = lambda k: tag(layer, MLA_TAGS[k])
+    w = {}
+    w["q_a"] = fp8_synth_matrix(seed, t("q_a"), ql, H, sigma)[2] if ql else None
+    w["q_b"] = fp8_synth_matrix(seed, t("q_b"), nh * dq, ql if ql else H, sigma)[2]
+    w["kv_a"] = fp8_synth_matrix(seed, t("kv_a"), R, H, sigma)[2]
+    w["kv_b"] = fp8_synth_matrix(seed, t("kv_b"), nh * (cfg.d_nope + cfg.d_v), lr, sigma)[2]
+    w["o"] = fp8_synth_matrix(seed, t("o"), H, nh * cfg.d_v, sigma)[2]
+    vec = lambda k, n: (fill_normal(n, seed, t(k), norm_sigma, 1.0) if norm_sigma else np.ones(n, np.float32))
+    w["norm"] = vec("norm", H)
+    w["q_a_norm"] = vec("q_a_norm", ql) if ql else None
+    w["kv_a_norm"] = vec("kv_a_norm", lr) if cfg.kv_norm else None
+    return w

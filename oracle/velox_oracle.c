@@ -419,6 +419,178 @@ void vxo_mla_absorbed_step(float* dst_hidden, const float* input_hidden, const f
 }
 
 /* ------------------------------------------------------------------------------------------ */
+/* fp8 e4m3fn (OCP) with 128x128 block scales: BASELINE config 4's weight format (DeepSeek-V3),  */
+/* not in the reference. Integer round-to-nearest-even so the device quantizer matches bit for  */
+/* bit.                                                                                         */
+/* ------------------------------------------------------------------------------------------ */
+static inline uint32_t vxo_fbits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+uint8_t vxo_f32_to_e4m3(float f) {
+    const uint32_t u = vxo_fbits(f);
+    const uint8_t sign = (uint8_t)((u >> 24) & 0x80u);
+    const uint32_t a = u & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return sign | 0x7Fu;  /* NaN */
+    if (a >= 0x43E00000u) return sign | 0x7Eu; /* |f| >= 448: saturate */
+    const int e = (int)(a >> 23) - 127;
+    if (e < -6) {
+        /* subnormal range: q = rne(|f| * 2^9), q <= 8 (8 is the smallest normal, code 0x08) */
+        if (a < 0x00800000u) return sign;      /* fp32 subnormals round to 0 */
+        const uint32_t mant = (a & 0x7FFFFFu) | 0x800000u;
+        const int shift = 14 - e;              /* |f| * 2^9 = mant * 2^(e - 14) */
+        if (shift > 25) return sign;
+        uint32_t q = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1u))) ++q;
+        return sign | (uint8_t)q;
+    }
+    uint32_t m = (a & 0x7FFFFFu) >> 20, ex = (uint32_t)(e + 7);
+    const uint32_t rem = a & 0xFFFFFu, half = 0x80000u;
+    if (rem > half || (rem == half && (m & 1u))) ++m;
+    if (m == 8u) { m = 0u; ++ex; }
+    if (ex > 15u || (ex == 15u && m == 7u)) return sign | 0x7Eu;
+    return sign | (uint8_t)((ex << 3) | m);
+}
+
+float vxo_e4m3_to_f32(uint8_t b) {
+    const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+    if (e == 15u && m == 7u) return NAN;
+    const float v = e ? ldexpf(1.0f + (float)m / 8.0f, (int)e - 7) : ldexpf((float)m / 8.0f, -6);
+    return (b & 0x80u) ? -v : v;
+}
+
+void vxo_fp8_quantize(const float* w, uint64_t rows, uint64_t cols, uint8_t* codes, float* scales) {
+    const uint64_t rb = (rows + 127) / 128, cb = (cols + 127) / 128;
+    for (uint64_t i = 0; i < rb; ++i)
+        for (uint64_t j = 0; j < cb; ++j) {
+            float amax = 0.0f;
+            for (uint64_t r = i * 128; r < rows && r < i * 128 + 128; ++r)
+                for (uint64_t c = j * 128; c < cols && c < j * 128 + 128; ++c) {
+                    const float v = fabsf(w[r * cols + c]);
+                    if (v > amax) amax = v;
+                }
+            const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
+            scales[i * cb + j] = s;
+            for (uint64_t r = i * 128; r < rows && r < i * 128 + 128; ++r)
+                for (uint64_t c = j * 128; c < cols && c < j * 128 + 128; ++c)
+                    codes[r * cols + c] = vxo_f32_to_e4m3(w[r * cols + c] / s);
+        }
+}
+
+void vxo_fp8_dequant(const uint8_t* codes, const float* scales, uint64_t rows, uint64_t cols, float* out) {
+    const uint64_t cb = (cols + 127) / 128;
+    for (uint64_t r = 0; r < rows; ++r)
+        for (uint64_t c = 0; c < cols; ++c)
+            out[r * cols + c] = vxo_e4m3_to_f32(codes[r * cols + c]) * scales[(r / 128) * cb + c / 128];
+}
+
+void vxo_fp8_synth_matrix(uint64_t seed, uint64_t tag, uint64_t rows, uint64_t cols, float sigma, uint8_t* codes,
+                          float* scales, float* dequant) {
+    const uint64_t st = vxo_stream(seed, tag);
+    const float coef = vxo_normal_coef(sigma);
+    float* w = (float*)malloc(rows * cols * sizeof(float));
+    for (uint64_t i = 0; i < rows * cols; ++i) w[i] = vxo_normal(st, i, coef);
+    const uint64_t ns = ((rows + 127) / 128) * ((cols + 127) / 128);
+    uint8_t* cd = codes ? codes : (uint8_t*)malloc(rows * cols);
+    float* sc = scales ? scales : (float*)malloc(ns * sizeof(float));
+    vxo_fp8_quantize(w, rows, cols, cd, sc);
+    if (dequant) vxo_fp8_dequant(cd, sc, rows, cols, dequant);
+    if (!codes) free(cd);
+    if (!scales) free(sc);
+    free(w);
+}
+
+/* DeepSeek-V3 absorbed MLA decode step. The attention loop is the reference's online softmax
+ * (src/runtime.rs:995-1028) per head; the projections use the reference's matmul
+ * (src/runtime.rs:702-740); RoPE is the reference's rotate-half (src/runtime.rs:745-768) over the
+ * d_rope dimensions. */
+void vxo_mla_layer_step(const VxoMlaConfig* c, const VxoMlaWeights* w, float* cache, int cache_bf16,
+                        const float* h, float* h_out, uint64_t pos) {
+    const uint64_t H = c->hidden, nh = c->n_heads, dn = c->d_nope, dr = c->d_rope, dv = c->d_v;
+    const uint64_t lr = c->kv_lora, R = lr + dr, dq = dn + dr, kvb_rows = dn + dv;
+    float* x = (float*)malloc(H * sizeof(float));
+    float* q = (float*)malloc(nh * dq * sizeof(float));
+    float* ckr = (float*)malloc(R * sizeof(float));
+    float* o = (float*)malloc(nh * dv * sizeof(float));
+    float* out = (float*)malloc(H * sizeof(float));
+    vxo_rmsnorm(x, h, w->norm, H, c->eps);
+    if (c->q_lora) {
+        float* ql = (float*)malloc(c->q_lora * sizeof(float));
+        float* qn = (float*)malloc(c->q_lora * sizeof(float));
+        vxo_matmul_transposed(ql, x, w->q_a, H, c->q_lora);
+        vxo_rmsnorm(qn, ql, w->q_a_norm, c->q_lora, c->eps);
+        vxo_matmul_transposed(q, qn, w->q_b, c->q_lora, nh * dq);
+        free(ql); free(qn);
+    } else {
+        vxo_matmul_transposed(q, x, w->q_b, H, nh * dq);
+    }
+    vxo_matmul_transposed(ckr, x, w->kv_a, H, R);
+    float* row = cache + pos * R;
+    if (c->kv_norm) vxo_rmsnorm(row, ckr, w->kv_a_norm, lr, c->eps);
+    else memcpy(row, ckr, lr * sizeof(float));
+    if (dr) {
+        memcpy(row + lr, ckr + lr, dr * sizeof(float));
+        vxo_rope_rotate_half(row + lr, 1, dr, pos, c->rope_theta);
+    }
+    if (cache_bf16)
+        for (uint64_t i = 0; i < R; ++i) row[i] = vxo_bf16_to_f32(vxo_f32_to_bf16(row[i]));
+    /* heads are independent; each is computed in order by one thread */
+#if defined(_OPENMP)
+#pragma omp parallel
+#endif
+    {
+    float* qabs = (float*)malloc(lr * sizeof(float));
+    float* qr = (float*)malloc((dr ? dr : 1) * sizeof(float));
+    float* ctx = (float*)malloc(lr * sizeof(float));
+#if defined(_OPENMP)
+#pragma omp for schedule(static)
+#endif
+    for (long hl = 0; hl < (long)nh; ++hl) {
+        const uint64_t hh = (uint64_t)hl;
+        const float* qn = q + hh * dq;
+        const float* wk = w->kv_b + hh * kvb_rows * lr;  /* W_uk[hh]: dn rows of lr */
+        const float* wv = wk + dn * lr;                  /* W_uv[hh]: dv rows of lr */
+        for (uint64_t cc = 0; cc < lr; ++cc) {
+            float acc = 0.0f;
+            for (uint64_t i = 0; i < dn; ++i) acc += qn[i] * wk[i * lr + cc];
+            qabs[cc] = acc;
+        }
+        if (dr) {
+            memcpy(qr, qn + dn, dr * sizeof(float));
+            vxo_rope_rotate_half(qr, 1, dr, pos, c->rope_theta);
+        }
+        float m = -INFINITY, l = 0.0f;
+        for (uint64_t cc = 0; cc < lr; ++cc) ctx[cc] = 0.0f;
+        for (uint64_t t = 0; t <= pos; ++t) {
+            const float* kv = cache + t * R;
+            float dot = 0.0f;
+            for (uint64_t cc = 0; cc < lr; ++cc) dot += qabs[cc] * kv[cc];
+            for (uint64_t j = 0; j < dr; ++j) dot += qr[j] * kv[lr + j];
+            const float s = dot * c->scale;
+            const float nm = s > m ? s : m;
+            const float alpha = (m == -INFINITY) ? 0.0f : expf(m - nm);
+            const float beta = expf(s - nm);
+            l = l * alpha + beta;
+            m = nm;
+            for (uint64_t cc = 0; cc < lr; ++cc) ctx[cc] = ctx[cc] * alpha + beta * kv[cc];
+        }
+        if (l > 0.0f) {
+            const float inv_l = 1.0f / l;
+            for (uint64_t cc = 0; cc < lr; ++cc) ctx[cc] *= inv_l;
+        }
+        for (uint64_t j = 0; j < dv; ++j) {
+            float acc = 0.0f;
+            for (uint64_t cc = 0; cc < lr; ++cc) acc += wv[j * lr + cc] * ctx[cc];
+            o[hh * dv + j] = acc;
+        }
+    }
+    free(qabs); free(qr); free(ctx);
+    }
+    vxo_matmul_transposed(out, o, w->o, nh * dv, H);
+    for (uint64_t i = 0; i < H; ++i) h_out[i] = h[i] + out[i];
+    free(x); free(q); free(ckr); free(o); free(out);
+}
+
+/* ------------------------------------------------------------------------------------------ */
 /* Engine: src/runtime.rs:1229-1451 (VeloxStaticExecutionEngine::forward_step) with the        */
 /* BASELINE extensions (config-driven eps/theta, Q4_0 weights, bf16 KV rounding, QKV bias,     */
 /* tied head).                                                                                 */

@@ -32,7 +32,10 @@ enum {
     VXO_T_EMBED = 1, VXO_T_Q = 2, VXO_T_K = 3, VXO_T_V = 4, VXO_T_O = 5, VXO_T_GATE = 6,
     VXO_T_UP = 7, VXO_T_DOWN = 8, VXO_T_ATTN_NORM = 9, VXO_T_MLP_NORM = 10,
     VXO_T_FINAL_NORM = 11, VXO_T_HEAD = 12, VXO_T_BQ = 13, VXO_T_BK = 14, VXO_T_BV = 15,
-    VXO_T_PROMPT = 16
+    VXO_T_PROMPT = 16,
+    /* MLA layer tensors */
+    VXO_T_MLA_NORM = 32, VXO_T_MLA_QA = 33, VXO_T_MLA_QA_NORM = 34, VXO_T_MLA_QB = 35, VXO_T_MLA_KVA = 36,
+    VXO_T_MLA_KVA_NORM = 37, VXO_T_MLA_KVB = 38, VXO_T_MLA_O = 39, VXO_T_MLA_HIDDEN = 40, VXO_T_MLA_CACHE = 41
 };
 uint64_t vxo_tag(uint32_t layer, uint32_t kind);
 
@@ -67,6 +70,40 @@ void vxo_mla_absorbed_step(float* dst_hidden, const float* input_hidden, const f
                            const float* w_dkv, const float* w_abs_q, const float* w_abs_o,
                            float* kv_latent_pool, uint64_t hidden_dim, uint64_t latent_dim,
                            uint64_t max_seq_len, uint64_t step, float eps);
+
+/* ---- fp8 e4m3fn (OCP) with 128x128 block scales (not in the reference: BASELINE config 4's
+ * DeepSeek-V3 weight format). scale = amax / 448 per block; code = e4m3(w / scale), round to
+ * nearest even, saturating at +-448. Scales are [ceil(rows/128)][ceil(cols/128)] floats. ---- */
+uint8_t vxo_f32_to_e4m3(float f);
+float vxo_e4m3_to_f32(uint8_t b);
+void vxo_fp8_quantize(const float* w, uint64_t rows, uint64_t cols, uint8_t* codes, float* scales);
+void vxo_fp8_dequant(const uint8_t* codes, const float* scales, uint64_t rows, uint64_t cols, float* out);
+
+/* ---- absorbed multi-head latent attention layer (DeepSeek-V3 form of src/runtime.rs:845-1044) ----
+ * h_out = h + W_o concat_h(W_uv[h] ctx_h), ctx_h = softmax_t(s_ht) . c_t over t <= pos, with
+ * s_ht = scale * (q_abs_h . c_t + rope(q_rope_h) . kr_t), q_abs_h = W_uk[h]^T q_nope_h,
+ * q = W_qb rmsnorm(W_qa x) (q_lora > 0) or W_qb x (q_lora == 0), x = rmsnorm(h),
+ * [c_t | kr_t] = [rmsnorm(c) (kv_norm) | rope(kr)] of W_kva x, written to cache row pos.
+ * W_kvb rows: head h's d_nope k rows (W_uk[h]) then its d_v v rows (W_uv[h]).
+ * With n_heads 1, q_lora 0, d_rope 0, kv_norm 0, d_nope = d_v = kv_lora and W_kvb = [I; I] this
+ * is the reference's simplified step (vxo_mla_absorbed_step). */
+typedef struct VxoMlaConfig {
+    uint32_t hidden, n_heads, q_lora, kv_lora, d_nope, d_rope, d_v, kv_norm, max_seq;
+    float eps, rope_theta, scale;
+} VxoMlaConfig;
+
+typedef struct VxoMlaWeights {
+    const float *norm, *q_a, *q_a_norm, *q_b, *kv_a, *kv_a_norm, *kv_b, *o;  /* fp32 row-major [out][in] */
+} VxoMlaWeights;
+
+/* cache: [max_seq][kv_lora + d_rope]; cache_bf16: round the written row to bf16 (the device cache). */
+void vxo_mla_layer_step(const VxoMlaConfig* c, const VxoMlaWeights* w, float* cache, int cache_bf16,
+                        const float* h, float* h_out, uint64_t pos);
+
+/* Seeded N(0, sigma) matrix (index r * cols + col of stream(seed, tag)) quantized to fp8 blocks;
+ * codes [rows][cols], scales as above, dequant [rows][cols] fp32 (any output may be NULL). */
+void vxo_fp8_synth_matrix(uint64_t seed, uint64_t tag, uint64_t rows, uint64_t cols, float sigma, uint8_t* codes,
+                          float* scales, float* dequant);
 
 /* ---- whole-model engine (src/runtime.rs:1160-1490) ---- */
 typedef struct VxoConfig {

@@ -68,7 +68,8 @@ def test_arena_plan_sizes_and_budget():
     # codes + scales hold exactly 18 B per 32 weights of every matrix (embedding and head included)
     weights = (32 * (6144 * 4096 + 4096 * 4096 + 2 * 14336 * 4096 + 4096 * 14336) + 2 * 128256 * 4096)
     assert codes == weights // 2 and scales == weights // 32 * 2
-    assert kv == 32 * 2 * 8 * 385 * 128 * 2
+    # bf16 K and V of every layer; the position capacity rounds up to whole 32-position V blocks
+    assert kv == 32 * 2 * 8 * 416 * 128 * 2
     lib.velox_hip_model_destroy(m)
     # Qwen2-72B Q4_0 with an 8448-token context fits the 288 GB budget of one MI355X
     rc, m = _plan(make_config("qwen2_72b"))

@@ -79,6 +79,28 @@ class RunReport(C.Structure):
     ]
 
 
+class MlaConfig(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("hidden_dim", "num_heads", "q_lora_rank", "kv_lora_rank", "qk_nope_dim",
+                                          "qk_rope_dim", "v_head_dim", "num_layers", "max_seq_len", "max_batch",
+                                          "kv_norm", "attn_splits")] + \
+               [("rms_norm_eps", C.c_float), ("rope_theta", C.c_float), ("softmax_scale", C.c_float),
+                ("reserved", C.c_uint32), ("vram_budget_bytes", C.c_uint64)]
+
+
+class MlaBuffers(C.Structure):
+    _fields_ = [("hidden", C.c_void_p), ("latent_cache", C.c_void_p), ("states", C.c_void_p), ("s_cap", C.c_uint32),
+                ("splits", C.c_uint32), ("weight_bytes", C.c_uint64), ("cache_bytes", C.c_uint64),
+                ("act_bytes", C.c_uint64)]
+
+
+class MlaRunReport(C.Structure):
+    _fields_ = [(n, C.c_double) for n in ("us_per_layer", "bytes_per_layer", "hbm_gbps", "attn_us", "attn_bytes",
+                                          "wall_ms")] + [("status", C.c_int)]
+
+
+MLA_Q_A, MLA_Q_B, MLA_KV_A, MLA_KV_B, MLA_O, MLA_NORM, MLA_Q_A_NORM, MLA_KV_A_NORM = range(1, 9)
+
+
 def header_exports(path: str = HEADER) -> list[str]:
     """Names of every function declared in include/velox_hip.h."""
     text = open(path).read()
@@ -135,6 +157,18 @@ _SIGS = {
     "velox_hip_rmsnorm": (_I, [_P, _P, _U32, _F, _P, _P]),
     "velox_hip_attention_decode": (_I, [_P, _P, _U32, _U32, _U32, _U32, _U32, _F, _U32, _P, _P]),
     "velox_hip_run": (_I, [C.POINTER(RunOptions), C.POINTER(_U32), _U32, C.POINTER(RunReport)]),
+    "velox_hip_mla_builtin_config": (_I, [C.c_char_p, _U32, _U32, C.POINTER(MlaConfig)]),
+    "velox_hip_mla_create": (_I, [C.POINTER(MlaConfig), C.POINTER(_P)]),
+    "velox_hip_mla_destroy": (None, [_P]),
+    "velox_hip_mla_buffers": (_I, [_P, C.POINTER(MlaBuffers)]),
+    "velox_hip_mla_load_fp8": (_I, [_P, _I, _U32, _P, _P, _P]),
+    "velox_hip_mla_load_f32": (_I, [_P, _I, _U32, _P, _U64, _P]),
+    "velox_hip_mla_synthesize": (_I, [_P, _U64, _F, _F, _P]),
+    "velox_hip_mla_fill_cache": (_I, [_P, _U32, _U32, _U32, _U64, _F, _P]),
+    "velox_hip_mla_set_position": (_I, [_P, _U32, _U64, _P]),
+    "velox_hip_mla_layer_step": (None, [_P, _U32, _U32, _U64, _P]),
+    "velox_hip_mla_step_bytes": (C.c_double, [_P, _U32, _U64]),
+    "velox_hip_mla_run": (_I, [C.c_char_p, _U32, _U32, _U32, _U32, _U64, C.POINTER(MlaRunReport)]),
 }
 
 

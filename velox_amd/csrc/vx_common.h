@@ -165,6 +165,30 @@ struct VxBGemmArgs {
     uint64_t pstride;
 };
 
+// fp8 (e4m3fn) block-scaled GEMM of up to 32 rows of activations, on MFMA (vx_mla.hip). Weights
+// in 16-row x 64-column tiles of 1 KiB: lane l of tile (rt, kt) holds row 16 rt + l % 16, columns
+// 64 kt + 16 (l / 16) .. + 15; scales per (16-row tile, 128-column block). grid (ceil(n_rt / 4),
+// ksplit, groups): group g uses codes + g * w_gstride (16-byte units), scales + g * s_gstride,
+// x + g * x_gstride, y + g * y_gstride (elements); ksplit > 1 stores split ks at y + ks * pstride.
+struct VxF8GemmArgs {
+    const uint4* codes;
+    const float* scales;
+    uint32_t n_rt, n_kt, n_kb, batch;
+    const void* x;          // [batch][ldx] fp16 (x_f32 == 0) or fp32
+    uint32_t ldx, x_f32;
+    float* y;               // [batch][ldy]
+    uint32_t ldy, ksplit;
+    uint64_t w_gstride, s_gstride, x_gstride, y_gstride, pstride;
+    uint64_t active_mask;
+};
+
+// vx_mla.hip launchers (absorbed MLA layer), used by vx_mla_host.cpp.
+struct VxF8Dest;
+struct VxMlaPrepArgs;
+struct VxMlaAttnArgs;
+hipError_t vx_launch_f8gemm(const VxF8GemmArgs& a, uint32_t groups, hipStream_t st);
+int vx_record_error(hipError_t e);  // vx_host.cpp: the first error of a step, read by velox_hip_last_error
+
 // Launch helpers implemented in vx_kernels.hip, used by vx_host.cpp.
 enum { VX_EPI_STORE = 0, VX_EPI_RESID = 1, VX_EPI_SWIGLU = 2, VX_EPI_ARGMAX = 3 };
 hipError_t vx_launch_gemv(const VxMat& m, const VxGemvArgs& a, int epi, uint32_t max_wgs, hipStream_t st);

@@ -26,6 +26,13 @@ inline int vx_record(hipError_t e) {
 
 inline uint64_t vx_align(uint64_t x, uint64_t a = 256) { return (x + a - 1) / a * a; }
 
+}  // namespace
+
+// First-error recording shared with the other host translation units.
+int vx_record_error(hipError_t e) { return vx_record(e); }
+
+namespace {
+
 struct VxMatPlan {
     uint64_t code_off = 0, scale_off = 0, code_bytes = 0, scale_bytes = 0;
     uint32_t n = 0, k = 0, s = 0, n_tiles = 0, n_iter = 0, paired = 0;

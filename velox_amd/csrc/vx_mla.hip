@@ -1,0 +1,610 @@
+// vx_mla.hip -- the DeepSeek-V3 absorbed multi-head latent attention layer on gfx950: fp8 (e4m3fn,
+// 128x128 block scales) projection weights and a bf16 latent KV cache, for 1..32 sequences.
+//
+// The reference's MLA (src/runtime.rs:845-1044, emitted as velox_cuda_fused_mla_absorbed_attn,
+// src/codegen.rs:2001-2109) is a single-latent-head simplification; this is the full form of the
+// same absorbed computation: per head h,
+//   q_abs_h = W_uk[h]^T q_nope_h,  s_ht = scale (q_abs_h . c_t + rope(q_rope_h) . kr_t),
+//   ctx_h = softmax_t(s_ht) . c_t,  o_h = W_uv[h] ctx_h,  h_out = h + W_o [o_1 .. o_H].
+// One layer step is 9 launches: RMSNorm -> GEMM [W_qa; W_kva] (split over K) -> prep (q / latent
+// RMSNorms, RoPE of the new k_rope, latent append) -> GEMM W_qb -> grouped GEMM W_uk^T (absorption)
+// -> attention (split over positions) -> merge -> grouped GEMM W_uv -> GEMM W_o (split over K) ->
+// residual. Every GEMM is the same fp8 kernel: weights converted exactly to fp16 in registers
+// (v_cvt_scalef32_pk_f16_fp8), activations fp16, v_mfma_f32_16x16x32_f16, block scales on the
+// fp32 partial sums.
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "vx_common.h"
+#include "vx_mla.h"
+
+namespace {
+
+typedef _Float16 vm_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 vm_h2 __attribute__((ext_vector_type(2)));
+typedef float vm_f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t vm_u4 __attribute__((ext_vector_type(4)));
+
+constexpr int kFWaves = 4, kFDepth = 4;  // fp8 GEMM: waves per workgroup, k-tiles in flight per wave
+
+// f32 -> e4m3fn, round to nearest even, saturating at +-448: the integer steps of the oracle's
+// vxo_f32_to_e4m3, so device-synthesized codes equal the host's bit for bit.
+__device__ uint8_t vm_f32_to_e4m3(float f) {
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t sign = (u >> 24) & 0x80u, a = u & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return (uint8_t)(sign | 0x7Fu);
+    if (a >= 0x43E00000u) return (uint8_t)(sign | 0x7Eu);
+    const int e = (int)(a >> 23) - 127;
+    if (e < -6) {
+        if (a < 0x00800000u) return (uint8_t)sign;
+        const uint32_t mant = (a & 0x7FFFFFu) | 0x800000u;
+        const int shift = 14 - e;
+        if (shift > 25) return (uint8_t)sign;
+        uint32_t q = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1u))) ++q;
+        return (uint8_t)(sign | q);
+    }
+    uint32_t m = (a & 0x7FFFFFu) >> 20, ex = (uint32_t)(e + 7);
+    const uint32_t rem = a & 0xFFFFFu, half = 0x80000u;
+    if (rem > half || (rem == half && (m & 1u))) ++m;
+    if (m == 8u) { m = 0u; ++ex; }
+    if (ex > 15u || (ex == 15u && m == 7u)) return (uint8_t)(sign | 0x7Eu);
+    return (uint8_t)(sign | (ex << 3) | m);
+}
+
+// Eight fp8 codes (bytes of two dwords, in order) -> eight fp16, exactly.
+__device__ __forceinline__ vm_h8 vm_fp8x8(uint32_t a, uint32_t b) {
+    const vm_h2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(a, 1.0f, false);
+    const vm_h2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(a, 1.0f, true);
+    const vm_h2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(b, 1.0f, false);
+    const vm_h2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(b, 1.0f, true);
+    vm_h8 r;
+    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+    return r;
+}
+
+__device__ __forceinline__ vm_h8 vm_f32x8_to_h8(float4 lo, float4 hi) {
+    vm_h8 r;
+    r[0] = (_Float16)lo.x; r[1] = (_Float16)lo.y; r[2] = (_Float16)lo.z; r[3] = (_Float16)lo.w;
+    r[4] = (_Float16)hi.x; r[5] = (_Float16)hi.y; r[6] = (_Float16)hi.z; r[7] = (_Float16)hi.w;
+    return r;
+}
+
+__device__ __forceinline__ float vm_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// The seeded N(0, sigma) value of the oracle's vxo_normal: an exact integer times coef.
+__device__ __forceinline__ float vm_normal(uint64_t stream, uint64_t idx, float coef) {
+#pragma clang fp contract(off)
+    return (float)vx_normal_int(stream, idx) * coef;
+}
+
+template <int NT>
+__device__ __forceinline__ float vm_block_sum(float v, float* red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) t += red[w];
+    return t;
+}
+
+// Rotate-half RoPE pair (src/runtime.rs:761-764), unfused.
+__device__ __forceinline__ float2 vm_rope_pair(float x1, float x2, float2 cs) {
+#pragma clang fp contract(off)
+    return make_float2(x1 * cs.x - x2 * cs.y, x2 * cs.x + x1 * cs.y);
+}
+
+// Slot of position r (0..31) in a transposed 32-position V block: the P.V MFMA's lane group j
+// supplies positions 4j..4j+3 and 16+4j..16+4j+3 (where the score MFMA left them), so slot
+// 8j + 4 half + i holds position 16 half + 4j + i.
+__device__ __forceinline__ uint32_t vm_vslot(uint32_t r) { return 8u * ((r & 15u) >> 2) + 4u * (r >> 4) + (r & 3u); }
+
+}  // namespace
+
+// =============================================================================================
+// fp8 block-scaled GEMM: y[m][n] = sum_k x[m][k] W[n][k]
+// =============================================================================================
+// Each wave owns one 16-row tile over its split's k-tiles and keeps kFDepth tiles of weights and
+// activations in flight: tile kt's 16 bytes per lane are exactly the B operands of two MFMAs
+// (k-elements 16 grp + 0..7 and + 8..15 of row col), the activations of sequence col the matching
+// A operands. Per k-tile: two MFMAs into a fresh accumulator, then acc += block scale * it.
+template <int MT, bool XF32>
+__global__ __launch_bounds__(64 * kFWaves) void vx_f8gemm_kernel(VxF8GemmArgs a) {
+    if ((a.active_mask & 1ULL) == 0ULL) return;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, grp = lane >> 4;
+    const uint32_t g = blockIdx.z, ks = blockIdx.y;
+    const uint32_t rt_raw = blockIdx.x * kFWaves + (uint32_t)wave;
+    const uint32_t rt = min(rt_raw, a.n_rt - 1u);
+    const uint32_t kt0 = ks * a.n_kt / gridDim.y, kt1 = (ks + 1u) * a.n_kt / gridDim.y;
+    const uint4* W = a.codes + g * a.w_gstride + (size_t)rt * a.n_kt * 64u + lane;
+    const float* S = a.scales + g * a.s_gstride + (size_t)rt * a.n_kb;
+    const uint32_t m_last = a.batch - 1u;
+    size_t xoff[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+        xoff[mt] = g * a.x_gstride + (size_t)min((uint32_t)(16 * mt + col), m_last) * a.ldx + 16u * grp;
+    constexpr int XW = XF32 ? 4 : 2;  // 16-byte activation loads per lane and k-tile
+    uint4 wr[kFDepth];
+    uint4 xr[kFDepth][MT][XW];
+    auto issue = [&](int u, uint32_t kt) {
+        wr[u] = W[(size_t)kt * 64u];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            if constexpr (XF32) {
+                const uint4* xp = (const uint4*)((const float*)a.x + xoff[mt] + (size_t)kt * 64u);
+#pragma unroll
+                for (int w = 0; w < XW; ++w) xr[u][mt][w] = xp[w];
+            } else {
+                const uint4* xp = (const uint4*)((const uint16_t*)a.x + xoff[mt] + (size_t)kt * 64u);
+#pragma unroll
+                for (int w = 0; w < XW; ++w) xr[u][mt][w] = xp[w];
+            }
+        }
+    };
+    vm_f4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = vm_f4{0.f, 0.f, 0.f, 0.f};
+    const uint32_t kt_last = kt1 > kt0 ? kt1 - 1u : kt0;
+#pragma unroll
+    for (int u = 0; u < kFDepth; ++u) issue(u, min(kt0 + (uint32_t)u, kt_last));
+    for (uint32_t base = kt0; base < kt1; base += kFDepth) {
+#pragma unroll
+        for (int u = 0; u < kFDepth; ++u) {
+            const uint32_t kt = base + (uint32_t)u;
+            if (kt < kt1) {
+                const float s = S[kt >> 1];
+                const vm_h8 w0 = vm_fp8x8(wr[u].x, wr[u].y), w1 = vm_fp8x8(wr[u].z, wr[u].w);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    vm_h8 x0, x1;
+                    if constexpr (XF32) {
+                        x0 = vm_f32x8_to_h8(__builtin_bit_cast(float4, xr[u][mt][0]), __builtin_bit_cast(float4, xr[u][mt][1]));
+                        x1 = vm_f32x8_to_h8(__builtin_bit_cast(float4, xr[u][mt][2]), __builtin_bit_cast(float4, xr[u][mt][3]));
+                    } else {
+                        x0 = __builtin_bit_cast(vm_h8, xr[u][mt][0]);
+                        x1 = __builtin_bit_cast(vm_h8, xr[u][mt][1]);
+                    }
+                    vm_f4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, w0, vm_f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, w1, c, 0, 0, 0);
+                    acc[mt] += s * c;
+                }
+            }
+            issue(u, min(kt + (uint32_t)kFDepth, kt_last));
+        }
+    }
+    if (rt_raw >= a.n_rt) return;
+    float* y = a.y + g * a.y_gstride + (gridDim.y > 1u ? ks * a.pstride : 0u) + 16u * rt + col;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t m = (uint32_t)(16 * mt + 4 * grp + i);
+            if (m < a.batch) y[(size_t)m * a.ldy] = acc[mt][i];
+        }
+}
+
+hipError_t vx_launch_f8gemm(const VxF8GemmArgs& a, uint32_t groups, hipStream_t st) {
+    if (a.n_rt == 0 || a.n_kt == 0 || a.batch == 0 || a.batch > 32 || a.ksplit == 0 || a.ksplit > a.n_kt ||
+        groups == 0 || (a.ldx & 7u) || a.n_kb != (a.n_kt + 1u) / 2u)
+        return hipErrorInvalidValue;
+    if (a.ksplit > 1u && a.pstride < (uint64_t)a.batch * a.ldy) return hipErrorInvalidValue;
+    const dim3 grid((a.n_rt + kFWaves - 1) / kFWaves, a.ksplit, groups), block(64 * kFWaves);
+    if (a.batch <= 16) {
+        if (a.x_f32) hipLaunchKernelGGL((vx_f8gemm_kernel<1, true>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((vx_f8gemm_kernel<1, false>), grid, block, 0, st, a);
+    } else {
+        if (a.x_f32) hipLaunchKernelGGL((vx_f8gemm_kernel<2, true>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((vx_f8gemm_kernel<2, false>), grid, block, 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+// =============================================================================================
+// Weight synthesis / repack into the tiled fp8 layout
+// =============================================================================================
+// Source element of destination (g, r, k): the maps of VxF8Dest.
+__device__ __forceinline__ void vm_dest_src(const VxF8Dest& d, uint32_t g, uint32_t r, uint32_t k, uint32_t& sr,
+                                            uint32_t& sc) {
+    if (d.map == VX_MAP_UKT) { sr = g * (d.dn + d.dv) + k; sc = r; }
+    else if (d.map == VX_MAP_UV) { sr = g * (d.dn + d.dv) + d.dn + r; sc = k; }
+    else { sr = d.row_off + r; sc = k; }
+}
+
+// Block scales of a synthesized source matrix: amax / 448 per 128x128 block (vxo_fp8_quantize).
+__global__ __launch_bounds__(256) void vx_f8_synth_scales_kernel(float* scales, uint32_t rows, uint32_t cols,
+                                                                 uint64_t stream, float coef) {
+    __shared__ float red[4];
+    const uint32_t cbn = (cols + 127u) / 128u, rb = blockIdx.x / cbn, cb = blockIdx.x % cbn;
+    float amax = 0.0f;
+    for (uint32_t i = threadIdx.x; i < 128u * 128u; i += 256u) {
+        const uint32_t r = rb * 128u + i / 128u, c = cb * 128u + i % 128u;
+        if (r < rows && c < cols) amax = fmaxf(amax, fabsf(vm_normal(stream, (uint64_t)r * cols + c, coef)));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        scales[blockIdx.x] = m > 0.0f ? m / 448.0f : 1.0f;
+    }
+}
+
+// One 16-byte lane word of the destination per thread: 16 codes of row r, columns 16 j .. + 15.
+__global__ __launch_bounds__(256) void vx_f8_pack_kernel(VxF8Dest d) {
+    const uint64_t words_per_g = (uint64_t)(d.rows / 16u) * d.n_kt * 64u;
+    const uint64_t idx = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (idx >= words_per_g * d.groups) return;
+    const uint32_t g = (uint32_t)(idx / words_per_g);
+    const uint64_t w = idx % words_per_g;
+    const uint32_t lane = (uint32_t)(w % 64u), tile = (uint32_t)(w / 64u);
+    const uint32_t rt = tile / d.n_kt, kt = tile % d.n_kt;
+    const uint32_t r = rt * 16u + lane % 16u, k0 = kt * 64u + 16u * (lane / 16u);
+    const uint32_t scbn = (d.src_cols + 127u) / 128u;
+    uint32_t b[4] = {0u, 0u, 0u, 0u};
+    for (int e = 0; e < 16; ++e) {
+        const uint32_t k = k0 + (uint32_t)e;
+        if (k >= d.cols) continue;
+        uint32_t sr, sc;
+        vm_dest_src(d, g, r, k, sr, sc);
+        uint32_t code;
+        if (d.src_codes) {
+            code = d.src_codes[(size_t)sr * d.src_cols + sc];
+        } else {
+            code = vm_f32_to_e4m3(vm_normal(d.stream, (uint64_t)sr * d.src_cols + sc, d.coef) /
+                                  d.src_scales[(sr / 128u) * scbn + sc / 128u]);
+        }
+        b[e >> 2] |= code << (8 * (e & 3));
+    }
+    d.codes[g * d.w_gstride + ((size_t)(d.row_tile0 + rt) * d.n_kt + kt) * 64u + lane] = make_uint4(b[0], b[1], b[2], b[3]);
+    if (lane == 0 && (kt & 1u) == 0u) {
+        // the scale of (row tile, 128-column block): the source block of its first element
+        uint32_t sr, sc;
+        vm_dest_src(d, g, rt * 16u, kt * 64u, sr, sc);
+        d.scales[g * d.s_gstride + (size_t)(d.row_tile0 + rt) * d.n_kb + kt / 2u] = d.src_scales[(sr / 128u) * scbn + sc / 128u];
+    }
+}
+
+hipError_t vx_launch_f8_synth_scales(float* scales, uint32_t rows, uint32_t cols, uint64_t stream, float coef,
+                                     hipStream_t st) {
+    const uint32_t n = ((rows + 127u) / 128u) * ((cols + 127u) / 128u);
+    hipLaunchKernelGGL(vx_f8_synth_scales_kernel, dim3(n), dim3(256), 0, st, scales, rows, cols, stream, coef);
+    return hipGetLastError();
+}
+
+hipError_t vx_launch_f8_pack(const VxF8Dest& d, hipStream_t st) {
+    if ((d.rows & 15u) || d.cols != d.n_kt * 64u) return hipErrorInvalidValue;
+    const uint64_t n = (uint64_t)(d.rows / 16u) * d.n_kt * 64u * d.groups;
+    hipLaunchKernelGGL(vx_f8_pack_kernel, dim3((unsigned)((n + 255u) / 256u)), dim3(256), 0, st, d);
+    return hipGetLastError();
+}
+
+// =============================================================================================
+// Layer-step kernels
+// =============================================================================================
+
+// Per sequence (one workgroup): sum the K-split partials; q latent RMSNorm -> fp16 (or q -> fp32);
+// latent RMSNorm and RoPE of k_rope -> bf16 cache row pos (src/runtime.rs:588-601, 745-768).
+__global__ __launch_bounds__(256) void vx_mla_prep_kernel(VxMlaPrepArgs a) {
+    if ((a.active_mask & 1ULL) == 0ULL) return;
+    extern __shared__ __align__(16) unsigned char vm_smem[];
+    float* qs = (float*)vm_smem;                  // [q_lora]
+    float* cs = qs + (a.q_lora ? a.q_lora : 1u);  // [lr + dr]
+    __shared__ float red[4];
+    const uint32_t b = blockIdx.x, tid = threadIdx.x;
+    const uint64_t step = a.states[b].step;
+    const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;
+    const float* pb = a.parts + (size_t)b * a.na;
+    for (uint32_t i = tid; i < a.na; i += 256u) {
+        float v = 0.0f;
+        for (uint32_t s = 0; s < a.nparts; ++s) v += pb[s * a.pstride + i];
+        if (i < a.q_part) {
+            if (a.q_lora) qs[i] = v;
+            else a.q32[(size_t)b * a.q_part + i] = v;
+        } else {
+            cs[i - a.q_part] = v;
+        }
+    }
+    __syncthreads();
+    if (a.q_lora) {
+        float ss = 0.0f;
+        for (uint32_t i = tid; i < a.q_lora; i += 256u) ss += qs[i] * qs[i];
+        ss = vm_block_sum<256>(ss, red);
+        const float inv = 1.0f / sqrtf(ss / (float)a.q_lora + a.eps);
+        for (uint32_t i = tid; i < a.q_lora; i += 256u) {
+#pragma clang fp contract(off)
+            const float v = (qs[i] * inv) * a.g_qa[i];
+            a.q16[(size_t)b * a.ldq16 + i] = __half_as_ushort(__float2half(v));
+        }
+    }
+    uint16_t* row = a.cache + (size_t)b * a.cache_bstride + (size_t)pos * (a.lr + a.dr);
+    float inv = 1.0f;
+    if (a.kv_norm) {
+        float ss = 0.0f;
+        for (uint32_t i = tid; i < a.lr; i += 256u) ss += cs[i] * cs[i];
+        ss = vm_block_sum<256>(ss, red);
+        inv = 1.0f / sqrtf(ss / (float)a.lr + a.eps);
+    }
+    for (uint32_t i = tid; i < a.lr; i += 256u) {
+#pragma clang fp contract(off)
+        const float v = a.kv_norm ? (cs[i] * inv) * a.g_kva[i] : cs[i];
+        row[i] = vx_f32_to_bf16_bits(v);
+    }
+    const uint32_t half = a.dr / 2u;
+    for (uint32_t j = tid; j < half; j += 256u) {
+        const float2 o = vm_rope_pair(cs[a.lr + j], cs[a.lr + j + half], a.rope[(size_t)pos * half + j]);
+        row[a.lr + j] = vx_f32_to_bf16_bits(o.x);
+        row[a.lr + j + half] = vx_f32_to_bf16_bits(o.y);
+    }
+}
+
+
+template <int LR, int DR, int W>
+constexpr size_t vx_mla_attn_lds() {
+    return (size_t)32 * (LR + DR + 8) * 2 + (size_t)LR * 40 * 2;
+}
+
+// Absorbed MLA attention of one (split, sequence, group of 16 W heads). The split's positions go
+// through LDS in chunks of 32: the bf16 latent rows are converted to fp16 once, as rows for the
+// scores and dimension-major for P.V. Each wave owns 16 heads: scores S^T[pos][head] = [c | kr] .
+// [q_abs | rope(q_rope)] on v_mfma_f32_16x16x32_f16 (the q operands stay in registers), a log2-
+// domain online softmax per head, O[head][latent] += P c on MFMA. Writes the split's (m, l, o).
+template <int LR, int DR, int W>
+__global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a) {
+    if ((a.active_mask & 1ULL) == 0ULL) return;
+    constexpr int R = LR + DR, NCK = R / 32, NB = LR / 16, KP = R + 8, VP = 40, NT = 64 * W;
+    constexpr int NLD = (4 * R + NT - 1) / NT;  // 16-byte loads per thread per chunk (32 rows)
+    extern __shared__ __align__(16) unsigned char vm_smem[];
+    _Float16* k_s = (_Float16*)vm_smem;        // [32][KP]: rows [c | kr]
+    _Float16* v_s = k_s + 32 * KP;             // [LR][VP]: latent dims, slots vm_vslot(position)
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, grp = lane >> 4;
+    const uint32_t sp = blockIdx.x, b = blockIdx.y;
+    const uint32_t head = (blockIdx.z * W + (uint32_t)wave) * 16u + (uint32_t)col;
+    const uint64_t step = a.states[b].step;
+    const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;
+    const uint32_t len = pos + 1u;
+    const uint32_t chunk = ((a.s_max + a.splits - 1u) / a.splits + 31u) & ~31u;
+    const uint32_t t0 = sp * chunk, t1 = min(len, t0 + chunk);
+    const uint32_t n_chunks = t1 > t0 ? (t1 - t0 + 31u) >> 5 : 0u;
+    const uint16_t* cb_base = a.cache + (size_t)b * a.cache_bstride;
+
+    // ---- the chunk's rows into registers (rows clamped to pos: past t1 they are masked) ----
+    uint4 kr[NLD];
+    auto load_chunk = [&](uint32_t cb) {
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+            const int i = min(tid + j * NT, 4 * R - 1);
+            const uint32_t r = (uint32_t)i / (R / 8), c8 = (uint32_t)i % (R / 8);
+            kr[j] = *(const uint4*)(cb_base + (size_t)min(cb + r, pos) * R + 8u * c8);
+        }
+    };
+    load_chunk(t0 < len ? t0 : pos & ~31u);
+
+    // ---- q operands of head col: latent dims scaled, the RoPE part rotated, as fp16 ----
+    vm_h8 qop[NCK];
+    {
+        const float* qa = a.qabs + ((size_t)b * a.nh + head) * LR;
+        const float* qr = a.q32 + (size_t)b * a.nh * a.dq + (size_t)head * a.dq + a.dn;
+        const float2* rp = a.rope + (size_t)pos * (DR / 2);
+#pragma unroll
+        for (int c = 0; c < NCK; ++c) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int d = 32 * c + 8 * grp + e;
+                float v;
+                if (d < LR) {
+                    v = qa[d];
+                } else {
+                    const int r = d - LR, h2 = DR / 2;
+                    const float2 o = vm_rope_pair(qr[r % h2], qr[r % h2 + h2], rp[r % h2]);
+                    v = r < h2 ? o.x : o.y;
+                }
+                qop[c][e] = (_Float16)(v * a.qscale);
+            }
+        }
+    }
+
+    float m_run = -INFINITY, l_run = 0.0f;
+    vm_f4 o_acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) o_acc[nb] = vm_f4{0.f, 0.f, 0.f, 0.f};
+
+    for (uint32_t ci = 0; ci < n_chunks; ++ci) {
+        const uint32_t cb = t0 + 32u * ci;
+        __syncthreads();  // the previous chunk is consumed
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+            const int i = tid + j * NT;
+            if (i < 4 * R) {
+                const uint32_t r = (uint32_t)i / (R / 8), c8 = (uint32_t)i % (R / 8);
+                const uint32_t w4[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
+                vm_h8 h;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    h[2 * e] = (_Float16)__uint_as_float(w4[e] << 16);
+                    h[2 * e + 1] = (_Float16)__uint_as_float(w4[e] & 0xFFFF0000u);
+                }
+                *(vm_h8*)(k_s + r * KP + 8 * c8) = h;
+                if (8u * c8 < (uint32_t)LR) {
+                    const uint32_t sl = vm_vslot(r);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v_s[(8 * c8 + e) * VP + sl] = h[e];
+                }
+            }
+        }
+        __syncthreads();
+        if (ci + 1u < n_chunks) load_chunk(cb + 32u);
+        // scores: sc[bb][i] = S[position cb + 16 bb + 4 grp + i][head col]
+        vm_f4 sc[2];
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb) {
+            sc[bb] = vm_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < NCK; ++c) {
+                const vm_h8 kop = *(const vm_h8*)(k_s + (16 * bb + col) * KP + 32 * c + 8 * grp);
+                sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[c], sc[bb], 0, 0, 0);
+            }
+        }
+        float pr[8];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t p = cb + 16u * bb + 4u * grp + i;
+                pr[4 * bb + i] = p < t1 ? sc[bb][i] : -INFINITY;
+                mx = fmaxf(mx, pr[4 * bb + i]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = m_run == -INFINITY ? 0.0f : vm_exp2(m_run - m_new);
+        float lt = 0.0f;
+        vm_h8 pop;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float p = pr[e] == -INFINITY ? 0.0f : vm_exp2(pr[e] - m_new);
+            lt += p;
+            pop[e] = (_Float16)p;
+        }
+        l_run = l_run * alpha + lt;
+        m_run = m_new;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float ai = __shfl(alpha, 4 * grp + i);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) o_acc[nb][i] *= ai;
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const vm_h8 vop = *(const vm_h8*)(v_s + (16 * nb + col) * VP + 8 * grp);
+            o_acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, vop, o_acc[nb], 0, 0, 0);
+        }
+    }
+
+    // ---- the split's partial: o_acc[nb][i] is head 4 grp + i of the wave, latent dim 16 nb + col ----
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    const uint32_t hbase = (blockIdx.z * W + (uint32_t)wave) * 16u;
+    const size_t bh = (size_t)b * a.nh;
+    if (lane < 16) {
+        a.part_ml[((bh + hbase + lane) * a.splits + sp) * 2] = m_run;
+        a.part_ml[((bh + hbase + lane) * a.splits + sp) * 2 + 1] = l_run;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float* po = a.part_o + ((bh + hbase + 4u * grp + i) * a.splits + sp) * LR + col;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) po[16 * nb] = o_acc[nb][i];
+    }
+}
+
+// LSE merge of the split partials of one (head, sequence) -> ctx[b][h][LR] fp32.
+__global__ __launch_bounds__(256) void vx_mla_merge_kernel(const float* part_o, const float* part_ml, uint32_t nh,
+                                                           uint32_t splits, uint32_t lr, float* ctx, uint64_t mask) {
+    if ((mask & 1ULL) == 0ULL) return;
+    __shared__ float s_w[64];
+    const size_t bh = (size_t)blockIdx.y * nh + blockIdx.x;
+    const float* pml = part_ml + bh * splits * 2u;
+    if (threadIdx.x < 64) {
+        const int j = threadIdx.x;
+        const float mj = j < (int)splits ? pml[2 * j] : -INFINITY;
+        const float lj = j < (int)splits ? pml[2 * j + 1] : 0.0f;
+        float M = mj;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+        const float wj = mj == -INFINITY ? 0.0f : vm_exp2(mj - M);
+        float Ls = lj * wj;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) Ls += __shfl_xor(Ls, off);
+        s_w[j] = Ls > 0.0f ? wj / Ls : 0.0f;
+    }
+    __syncthreads();
+    const float* po = part_o + bh * splits * lr;
+    for (uint32_t d = threadIdx.x; d < lr; d += 256u) {
+        float acc = 0.0f;
+        for (uint32_t j = 0; j < splits; ++j) acc += s_w[j] * po[(size_t)j * lr + d];
+        ctx[bh * lr + d] = acc;
+    }
+}
+
+// h[b] += the K-split partials of W_o, in split order.
+__global__ __launch_bounds__(256) void vx_mla_resid_kernel(float* h, const float* parts, uint32_t nparts,
+                                                           uint64_t pstride, uint32_t n, uint64_t mask) {
+    if ((mask & 1ULL) == 0ULL) return;
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x, b = blockIdx.y;
+    if (i >= n) return;
+    float v = h[(size_t)b * n + i];
+    for (uint32_t s = 0; s < nparts; ++s) v += parts[s * pstride + (size_t)b * n + i];
+    h[(size_t)b * n + i] = v;
+}
+
+hipError_t vx_launch_mla_prep(const VxMlaPrepArgs& a, uint32_t batch, hipStream_t st) {
+    const size_t lds = ((size_t)(a.q_lora ? a.q_lora : 1u) + a.lr + a.dr) * 4;
+    if (lds > 60000 || a.na != a.q_part + a.lr + a.dr || (a.dr & 1u)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(vx_mla_prep_kernel, dim3(batch), dim3(256), lds, st, a);
+    return hipGetLastError();
+}
+
+template <int LR, int DR, int W>
+hipError_t vx_mla_attn_launch_t(const VxMlaAttnArgs& a, uint32_t batch, hipStream_t st) {
+    constexpr size_t lds = vx_mla_attn_lds<LR, DR, W>();
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void*)vx_mla_attn_kernel<LR, DR, W>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds) != hipSuccess) {
+            (void)hipGetLastError();
+            return hipErrorInvalidValue;
+        }
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((vx_mla_attn_kernel<LR, DR, W>), dim3(a.splits, batch, a.nh / (16u * W)), dim3(64 * W), lds, st,
+                       a);
+    return hipGetLastError();
+}
+
+hipError_t vx_launch_mla_attn(const VxMlaAttnArgs& a, uint32_t lr, uint32_t dr, uint32_t batch, hipStream_t st) {
+    if (a.splits == 0 || a.splits > 64 || (a.s_cap & 31u) || a.s_cap < a.s_max || a.nh % 16u || dr != 64u)
+        return hipErrorInvalidValue;
+    if (lr == 512 && a.nh % 64u == 0) return vx_mla_attn_launch_t<512, 64, 4>(a, batch, st);
+    if (lr == 128 && a.nh % 16u == 0) return vx_mla_attn_launch_t<128, 64, 1>(a, batch, st);
+    return hipErrorInvalidValue;
+}
+
+hipError_t vx_launch_mla_merge(const float* part_o, const float* part_ml, uint32_t nh, uint32_t splits, uint32_t lr,
+                               float* ctx, uint32_t batch, uint64_t mask, hipStream_t st) {
+    if (splits == 0 || splits > 64) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(vx_mla_merge_kernel, dim3(nh, batch), dim3(256), 0, st, part_o, part_ml, nh, splits, lr, ctx,
+                       mask);
+    return hipGetLastError();
+}
+
+hipError_t vx_launch_mla_resid(float* h, const float* parts, uint32_t nparts, uint64_t pstride, uint32_t n,
+                               uint32_t batch, uint64_t mask, hipStream_t st) {
+    hipLaunchKernelGGL(vx_mla_resid_kernel, dim3((n + 255u) / 256u, batch), dim3(256), 0, st, h, parts, nparts, pstride,
+                       n, mask);
+    return hipGetLastError();
+}
+
+// Latent rows [0, n_pos) of one sequence := bf16 of seeded N(0, sigma): element (t, d) draws index
+// t * row + d of the stream (the tests' numpy fill of the same stream, rounded to bf16).
+__global__ __launch_bounds__(256) void vx_mla_fill_cache_kernel(uint16_t* dst, uint64_t n, uint64_t stream, float coef) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256u)
+        dst[i] = vx_f32_to_bf16_bits(vm_normal(stream, i, coef));
+}
+
+hipError_t vx_launch_mla_fill_cache(uint16_t* dst, uint64_t n, uint64_t stream, float coef, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    const uint64_t g = (n + 255u) / 256u;
+    hipLaunchKernelGGL(vx_mla_fill_cache_kernel, dim3((unsigned)(g < 65536u ? g : 65536u)), dim3(256), 0, st, dst, n,
+                       stream, coef);
+    return hipGetLastError();
+}

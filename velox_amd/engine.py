@@ -219,3 +219,95 @@ def run(model: str = "llama3_8b", prompt_len: int = 128, warmup: int = 5, steps:
     L.check(rc, "velox_hip_run")
     d = {f: getattr(rep, f) for f, _ in rep._fields_}
     return d, [int(toks[i]) for i in range(rep.n_tokens)]
+
+
+class MlaEngine:
+    """The absorbed multi-head latent attention layer behind the C ABI: the
+    full form of the reference's ``mla_absorbed_step_f32`` (src/runtime.rs:845-1044), for up to
+    32 sequences, with fp8 block-scaled weights and a bf16 latent cache on the device."""
+
+    def __init__(self, cfg: dict | str = "deepseek_v3_mla", max_seq_len: int = 64, max_batch: int = 1,
+                 num_layers: int = 1, seed: int = 1, sigma: float = 0.02, norm_sigma: float = 0.0,
+                 attn_splits: int = 0, synthesize: bool = True):
+        self.lib = L.load()
+        c = L.MlaConfig()
+        if isinstance(cfg, str):
+            L.check(self.lib.velox_hip_mla_builtin_config(cfg.encode(), max_seq_len, max_batch, C.byref(c)), cfg)
+        else:
+            for k, v in cfg.items():
+                setattr(c, k, v)
+            c.max_seq_len, c.max_batch = max_seq_len, max_batch
+            if not c.rms_norm_eps:
+                c.rms_norm_eps = 1e-6
+            if not c.rope_theta:
+                c.rope_theta = 10000.0
+        c.num_layers = num_layers
+        c.attn_splits = attn_splits
+        self.cfg = c
+        self._m = C.c_void_p()
+        L.check(self.lib.velox_hip_mla_create(C.byref(c), C.byref(self._m)), "mla_create")
+        self.buf = L.MlaBuffers()
+        L.check(self.lib.velox_hip_mla_buffers(self._m, C.byref(self.buf)), "mla_buffers")
+        self.R = c.kv_lora_rank + c.qk_rope_dim
+        if synthesize:
+            L.check(self.lib.velox_hip_mla_synthesize(self._m, seed, sigma, norm_sigma, None), "mla_synthesize")
+
+    def fill_cache(self, layer: int, seq: int, n_pos: int, seed: int, sigma: float = 1.0) -> None:
+        L.check(self.lib.velox_hip_mla_fill_cache(self._m, layer, seq, n_pos, seed, sigma, None), "mla_fill_cache")
+
+    def set_position(self, seq: int, pos: int) -> None:
+        L.check(self.lib.velox_hip_mla_set_position(self._m, seq, pos, None), "mla_set_position")
+
+    def set_hidden(self, h: np.ndarray) -> None:
+        h = np.ascontiguousarray(h, np.float32)
+        L.memcpy_htod(self.buf.hidden, h.ctypes.data, h.nbytes)
+
+    def hidden(self, batch: int) -> np.ndarray:
+        out = np.zeros((batch, self.cfg.hidden_dim), np.float32)
+        L.memcpy_dtoh(out.ctypes.data, self.buf.hidden, out.nbytes)
+        return out
+
+    def cache(self, layer: int, seq: int, n_pos: int) -> np.ndarray:
+        """Latent rows [0, n_pos) of one sequence as fp32 (from the bf16 cache)."""
+        raw = np.zeros((n_pos, self.R), np.uint16)
+        off = ((layer * self.cfg.max_batch + seq) * self.buf.s_cap) * self.R * 2
+        L.memcpy_dtoh(raw.ctypes.data, self.buf.latent_cache + off, raw.nbytes)
+        return (raw.astype(np.uint32) << 16).view(np.float32)
+
+    def load_fp8(self, kind: int, layer: int, codes: np.ndarray, scales: np.ndarray) -> None:
+        codes = np.ascontiguousarray(codes, np.uint8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        L.check(self.lib.velox_hip_mla_load_fp8(self._m, kind, layer, codes.ctypes.data, scales.ctypes.data, None),
+                "mla_load_fp8")
+
+    def load_f32(self, kind: int, layer: int, data: np.ndarray) -> None:
+        data = np.ascontiguousarray(data, np.float32)
+        L.check(self.lib.velox_hip_mla_load_f32(self._m, kind, layer, data.ctypes.data, data.size, None), "mla_load_f32")
+
+    def step(self, layer: int = 0, batch: int = 1) -> None:
+        self.lib.velox_hip_mla_layer_step(self._m, layer, batch, 1, None)
+        L.check(L.hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
+        L.check(self.lib.velox_hip_last_error(), "mla_layer_step")
+
+    def step_bytes(self, batch: int, pos: int) -> float:
+        return float(self.lib.velox_hip_mla_step_bytes(self._m, batch, pos))
+
+    def close(self) -> None:
+        if self._m:
+            self.lib.velox_hip_mla_destroy(self._m)
+            self._m = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def mla_run(which: str = "deepseek_v3_mla", batch: int = 1, context_len: int = 4096, warmup: int = 5,
+            steps: int = 50, seed: int = 1234) -> dict:
+    """velox_hip_mla_run: synthesize, seed the latent context, time graph-replayed layer steps."""
+    rep = L.MlaRunReport()
+    L.check(L.load().velox_hip_mla_run(which.encode(), batch, context_len, warmup, steps, seed, C.byref(rep)),
+            "velox_hip_mla_run")
+    return {f: getattr(rep, f) for f, _ in rep._fields_}
