@@ -187,6 +187,7 @@ struct VxF8Dest;
 struct VxMlaPrepArgs;
 struct VxMlaAttnArgs;
 hipError_t vx_launch_f8gemm(const VxF8GemmArgs& a, uint32_t groups, hipStream_t st);
+uint32_t vx_f8gemm_rows_per_wave(uint32_t batch);  // 16-row tiles per wave of the fp8 GEMM
 int vx_record_error(hipError_t e);  // vx_host.cpp: the first error of a step, read by velox_hip_last_error
 
 // Launch helpers implemented in vx_kernels.hip, used by vx_host.cpp.

@@ -16,6 +16,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "vx_common.h"
 #include "vx_mla.h"
 
@@ -100,41 +102,43 @@ __device__ __forceinline__ float2 vm_rope_pair(float x1, float x2, float2 cs) {
     return make_float2(x1 * cs.x - x2 * cs.y, x2 * cs.x + x1 * cs.y);
 }
 
-// Slot of position r (0..31) in a transposed 32-position V block: the P.V MFMA's lane group j
-// supplies positions 4j..4j+3 and 16+4j..16+4j+3 (where the score MFMA left them), so slot
-// 8j + 4 half + i holds position 16 half + 4j + i.
-__device__ __forceinline__ uint32_t vm_vslot(uint32_t r) { return 8u * ((r & 15u) >> 2) + 4u * (r >> 4) + (r & 3u); }
-
 }  // namespace
 
 // =============================================================================================
 // fp8 block-scaled GEMM: y[m][n] = sum_k x[m][k] W[n][k]
 // =============================================================================================
-// Each wave owns one 16-row tile over its split's k-tiles and keeps kFDepth tiles of weights and
+// Each wave owns MR 16-row tiles over its split's k-tiles and keeps kFDepth k-tiles of weights and
 // activations in flight: tile kt's 16 bytes per lane are exactly the B operands of two MFMAs
 // (k-elements 16 grp + 0..7 and + 8..15 of row col), the activations of sequence col the matching
-// A operands. Per k-tile: two MFMAs into a fresh accumulator, then acc += block scale * it.
-template <int MT, bool XF32>
+// A operands, shared by the MR tiles. Per k-tile: two MFMAs into a fresh accumulator, then
+// acc += block scale * it.
+template <int MT, int MR, bool XF32>
 __global__ __launch_bounds__(64 * kFWaves) void vx_f8gemm_kernel(VxF8GemmArgs a) {
     if ((a.active_mask & 1ULL) == 0ULL) return;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, grp = lane >> 4;
     const uint32_t g = blockIdx.z, ks = blockIdx.y;
-    const uint32_t rt_raw = blockIdx.x * kFWaves + (uint32_t)wave;
-    const uint32_t rt = min(rt_raw, a.n_rt - 1u);
+    const uint32_t rt0 = (blockIdx.x * kFWaves + (uint32_t)wave) * MR;
     const uint32_t kt0 = ks * a.n_kt / gridDim.y, kt1 = (ks + 1u) * a.n_kt / gridDim.y;
-    const uint4* W = a.codes + g * a.w_gstride + (size_t)rt * a.n_kt * 64u + lane;
-    const float* S = a.scales + g * a.s_gstride + (size_t)rt * a.n_kb;
+    const uint4* W[MR];
+    const float* S[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+        const uint32_t rt = min(rt0 + (uint32_t)r, a.n_rt - 1u);
+        W[r] = a.codes + g * a.w_gstride + (size_t)rt * a.n_kt * 64u + lane;
+        S[r] = a.scales + g * a.s_gstride + (size_t)rt * a.n_kb;
+    }
     const uint32_t m_last = a.batch - 1u;
     size_t xoff[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
         xoff[mt] = g * a.x_gstride + (size_t)min((uint32_t)(16 * mt + col), m_last) * a.ldx + 16u * grp;
     constexpr int XW = XF32 ? 4 : 2;  // 16-byte activation loads per lane and k-tile
-    uint4 wr[kFDepth];
+    uint4 wr[kFDepth][MR];
     uint4 xr[kFDepth][MT][XW];
     auto issue = [&](int u, uint32_t kt) {
-        wr[u] = W[(size_t)kt * 64u];
+#pragma unroll
+        for (int r = 0; r < MR; ++r) wr[u][r] = W[r][(size_t)kt * 64u];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             if constexpr (XF32) {
@@ -148,9 +152,11 @@ __global__ __launch_bounds__(64 * kFWaves) void vx_f8gemm_kernel(VxF8GemmArgs a)
             }
         }
     };
-    vm_f4 acc[MT];
+    vm_f4 acc[MR][MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = vm_f4{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[r][mt] = vm_f4{0.f, 0.f, 0.f, 0.f};
     const uint32_t kt_last = kt1 > kt0 ? kt1 - 1u : kt0;
 #pragma unroll
     for (int u = 0; u < kFDepth; ++u) issue(u, min(kt0 + (uint32_t)u, kt_last));
@@ -159,49 +165,73 @@ __global__ __launch_bounds__(64 * kFWaves) void vx_f8gemm_kernel(VxF8GemmArgs a)
         for (int u = 0; u < kFDepth; ++u) {
             const uint32_t kt = base + (uint32_t)u;
             if (kt < kt1) {
-                const float s = S[kt >> 1];
-                const vm_h8 w0 = vm_fp8x8(wr[u].x, wr[u].y), w1 = vm_fp8x8(wr[u].z, wr[u].w);
+                vm_h8 x0[MT], x1[MT];
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
-                    vm_h8 x0, x1;
                     if constexpr (XF32) {
-                        x0 = vm_f32x8_to_h8(__builtin_bit_cast(float4, xr[u][mt][0]), __builtin_bit_cast(float4, xr[u][mt][1]));
-                        x1 = vm_f32x8_to_h8(__builtin_bit_cast(float4, xr[u][mt][2]), __builtin_bit_cast(float4, xr[u][mt][3]));
+                        x0[mt] = vm_f32x8_to_h8(__builtin_bit_cast(float4, xr[u][mt][0]), __builtin_bit_cast(float4, xr[u][mt][1]));
+                        x1[mt] = vm_f32x8_to_h8(__builtin_bit_cast(float4, xr[u][mt][2]), __builtin_bit_cast(float4, xr[u][mt][3]));
                     } else {
-                        x0 = __builtin_bit_cast(vm_h8, xr[u][mt][0]);
-                        x1 = __builtin_bit_cast(vm_h8, xr[u][mt][1]);
+                        x0[mt] = __builtin_bit_cast(vm_h8, xr[u][mt][0]);
+                        x1[mt] = __builtin_bit_cast(vm_h8, xr[u][mt][1]);
                     }
-                    vm_f4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, w0, vm_f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, w1, c, 0, 0, 0);
-                    acc[mt] += s * c;
+                }
+#pragma unroll
+                for (int r = 0; r < MR; ++r) {
+                    const float s = S[r][kt >> 1];
+                    const vm_h8 w0 = vm_fp8x8(wr[u][r].x, wr[u][r].y), w1 = vm_fp8x8(wr[u][r].z, wr[u][r].w);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        vm_f4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0[mt], w0, vm_f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1[mt], w1, c, 0, 0, 0);
+                        acc[r][mt] += s * c;
+                    }
                 }
             }
             issue(u, min(kt + (uint32_t)kFDepth, kt_last));
         }
     }
-    if (rt_raw >= a.n_rt) return;
-    float* y = a.y + g * a.y_gstride + (gridDim.y > 1u ? ks * a.pstride : 0u) + 16u * rt + col;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int r = 0; r < MR; ++r) {
+        const uint32_t rt = rt0 + (uint32_t)r;
+        if (rt >= a.n_rt) continue;
+        float* y = a.y + g * a.y_gstride + (gridDim.y > 1u ? ks * a.pstride : 0u) + 16u * rt + col;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t m = (uint32_t)(16 * mt + 4 * grp + i);
-            if (m < a.batch) y[(size_t)m * a.ldy] = acc[mt][i];
-        }
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t m = (uint32_t)(16 * mt + 4 * grp + i);
+                if (m < a.batch) y[(size_t)m * a.ldy] = acc[r][mt][i];
+            }
+    }
 }
+
+namespace {
+
+template <int MT, int MR>
+void vx_f8gemm_launch_t(const VxF8GemmArgs& a, uint32_t groups, hipStream_t st) {
+    const uint32_t tiles_per_wg = kFWaves * MR;
+    const dim3 grid((a.n_rt + tiles_per_wg - 1) / tiles_per_wg, a.ksplit, groups), block(64 * kFWaves);
+    if (a.x_f32) hipLaunchKernelGGL((vx_f8gemm_kernel<MT, MR, true>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((vx_f8gemm_kernel<MT, MR, false>), grid, block, 0, st, a);
+}
+
+}  // namespace
+
+// Row tiles per wave: 4 once the activation fragments of >= 8 sequences outweigh the weights.
+uint32_t vx_f8gemm_rows_per_wave(uint32_t batch) { return batch >= 8 ? 4u : 1u; }
 
 hipError_t vx_launch_f8gemm(const VxF8GemmArgs& a, uint32_t groups, hipStream_t st) {
     if (a.n_rt == 0 || a.n_kt == 0 || a.batch == 0 || a.batch > 32 || a.ksplit == 0 || a.ksplit > a.n_kt ||
         groups == 0 || (a.ldx & 7u) || a.n_kb != (a.n_kt + 1u) / 2u)
         return hipErrorInvalidValue;
     if (a.ksplit > 1u && a.pstride < (uint64_t)a.batch * a.ldy) return hipErrorInvalidValue;
-    const dim3 grid((a.n_rt + kFWaves - 1) / kFWaves, a.ksplit, groups), block(64 * kFWaves);
+    const bool mr4 = vx_f8gemm_rows_per_wave(a.batch) == 4u;
     if (a.batch <= 16) {
-        if (a.x_f32) hipLaunchKernelGGL((vx_f8gemm_kernel<1, true>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((vx_f8gemm_kernel<1, false>), grid, block, 0, st, a);
+        if (mr4) vx_f8gemm_launch_t<1, 4>(a, groups, st);
+        else vx_f8gemm_launch_t<1, 1>(a, groups, st);
     } else {
-        if (a.x_f32) hipLaunchKernelGGL((vx_f8gemm_kernel<2, true>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((vx_f8gemm_kernel<2, false>), grid, block, 0, st, a);
+        vx_f8gemm_launch_t<2, 4>(a, groups, st);
     }
     return hipGetLastError();
 }
@@ -290,21 +320,29 @@ hipError_t vx_launch_f8_pack(const VxF8Dest& d, hipStream_t st) {
 // Layer-step kernels
 // =============================================================================================
 
-// Per sequence (one workgroup): sum the K-split partials; q latent RMSNorm -> fp16 (or q -> fp32);
-// latent RMSNorm and RoPE of k_rope -> bf16 cache row pos (src/runtime.rs:588-601, 745-768).
-__global__ __launch_bounds__(256) void vx_mla_prep_kernel(VxMlaPrepArgs a) {
+// Per sequence (one workgroup): sum the K-split partials (all of an element's partials loaded at
+// once); q latent RMSNorm -> fp16 (or q -> fp32); latent RMSNorm and RoPE of k_rope -> bf16 cache
+// row pos (src/runtime.rs:588-601, 745-768).
+constexpr uint32_t kMlaMaxParts = 16;
+
+__global__ __launch_bounds__(1024) void vx_mla_prep_kernel(VxMlaPrepArgs a) {
     if ((a.active_mask & 1ULL) == 0ULL) return;
     extern __shared__ __align__(16) unsigned char vm_smem[];
     float* qs = (float*)vm_smem;                  // [q_lora]
     float* cs = qs + (a.q_lora ? a.q_lora : 1u);  // [lr + dr]
-    __shared__ float red[4];
+    __shared__ float red[16];
     const uint32_t b = blockIdx.x, tid = threadIdx.x;
     const uint64_t step = a.states[b].step;
     const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;
     const float* pb = a.parts + (size_t)b * a.na;
-    for (uint32_t i = tid; i < a.na; i += 256u) {
+    for (uint32_t i = tid; i < a.na; i += 1024u) {
+        float p[kMlaMaxParts];
+#pragma unroll
+        for (uint32_t s = 0; s < kMlaMaxParts; ++s) p[s] = pb[min(s, a.nparts - 1u) * a.pstride + i];
         float v = 0.0f;
-        for (uint32_t s = 0; s < a.nparts; ++s) v += pb[s * a.pstride + i];
+#pragma unroll
+        for (uint32_t s = 0; s < kMlaMaxParts; ++s)
+            if (s < a.nparts) v += p[s];
         if (i < a.q_part) {
             if (a.q_lora) qs[i] = v;
             else a.q32[(size_t)b * a.q_part + i] = v;
@@ -315,10 +353,10 @@ __global__ __launch_bounds__(256) void vx_mla_prep_kernel(VxMlaPrepArgs a) {
     __syncthreads();
     if (a.q_lora) {
         float ss = 0.0f;
-        for (uint32_t i = tid; i < a.q_lora; i += 256u) ss += qs[i] * qs[i];
-        ss = vm_block_sum<256>(ss, red);
+        for (uint32_t i = tid; i < a.q_lora; i += 1024u) ss += qs[i] * qs[i];
+        ss = vm_block_sum<1024>(ss, red);
         const float inv = 1.0f / sqrtf(ss / (float)a.q_lora + a.eps);
-        for (uint32_t i = tid; i < a.q_lora; i += 256u) {
+        for (uint32_t i = tid; i < a.q_lora; i += 1024u) {
 #pragma clang fp contract(off)
             const float v = (qs[i] * inv) * a.g_qa[i];
             a.q16[(size_t)b * a.ldq16 + i] = __half_as_ushort(__float2half(v));
@@ -328,23 +366,22 @@ __global__ __launch_bounds__(256) void vx_mla_prep_kernel(VxMlaPrepArgs a) {
     float inv = 1.0f;
     if (a.kv_norm) {
         float ss = 0.0f;
-        for (uint32_t i = tid; i < a.lr; i += 256u) ss += cs[i] * cs[i];
-        ss = vm_block_sum<256>(ss, red);
+        for (uint32_t i = tid; i < a.lr; i += 1024u) ss += cs[i] * cs[i];
+        ss = vm_block_sum<1024>(ss, red);
         inv = 1.0f / sqrtf(ss / (float)a.lr + a.eps);
     }
-    for (uint32_t i = tid; i < a.lr; i += 256u) {
+    for (uint32_t i = tid; i < a.lr; i += 1024u) {
 #pragma clang fp contract(off)
         const float v = a.kv_norm ? (cs[i] * inv) * a.g_kva[i] : cs[i];
         row[i] = vx_f32_to_bf16_bits(v);
     }
     const uint32_t half = a.dr / 2u;
-    for (uint32_t j = tid; j < half; j += 256u) {
+    for (uint32_t j = tid; j < half; j += 1024u) {
         const float2 o = vm_rope_pair(cs[a.lr + j], cs[a.lr + j + half], a.rope[(size_t)pos * half + j]);
         row[a.lr + j] = vx_f32_to_bf16_bits(o.x);
         row[a.lr + j + half] = vx_f32_to_bf16_bits(o.y);
     }
 }
-
 
 template <int LR, int DR, int W>
 constexpr size_t vx_mla_attn_lds() {
@@ -360,10 +397,9 @@ template <int LR, int DR, int W>
 __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a) {
     if ((a.active_mask & 1ULL) == 0ULL) return;
     constexpr int R = LR + DR, NCK = R / 32, NB = LR / 16, KP = R + 8, VP = 40, NT = 64 * W;
-    constexpr int NLD = (4 * R + NT - 1) / NT;  // 16-byte loads per thread per chunk (32 rows)
     extern __shared__ __align__(16) unsigned char vm_smem[];
     _Float16* k_s = (_Float16*)vm_smem;        // [32][KP]: rows [c | kr]
-    _Float16* v_s = k_s + 32 * KP;             // [LR][VP]: latent dims, slots vm_vslot(position)
+    _Float16* v_s = k_s + 32 * KP;             // [LR][VP]: latent dims; slot 8j + e holds vrow(j, e)
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, grp = lane >> 4;
     const uint32_t sp = blockIdx.x, b = blockIdx.y;
@@ -376,17 +412,33 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
     const uint32_t n_chunks = t1 > t0 ? (t1 - t0 + 31u) >> 5 : 0u;
     const uint16_t* cb_base = a.cache + (size_t)b * a.cache_bstride;
 
-    // ---- the chunk's rows into registers (rows clamped to pos: past t1 they are masked) ----
-    uint4 kr[NLD];
-    auto load_chunk = [&](uint32_t cb) {
+    // ---- the chunk's rows into registers (rows clamped to pos: past t1 they are masked). Latent
+    // units: slot group j (positions 4j..4j+3 and 16+4j..16+4j+3) x 8 dimensions, 8 row loads each;
+    // RoPE units: one row x 8 dimensions. j is the fastest index, so the transposed 16-byte stores
+    // of neighbouring lanes land 64 bytes apart in LDS ----
+    constexpr int NVU = (4 * (LR / 8) + NT - 1) / NT, NRU = (32 * (DR / 8) + NT - 1) / NT;
+    // two register sets: chunk i + 2 is loaded while chunk i is computed
+    uint4 kv[2][NVU][8], kq[2][NRU];
+    auto vrow = [](int j, int e) { return (uint32_t)(e < 4 ? 4 * j + e : 16 + 4 * j + (e - 4)); };
+    auto load_chunk = [&](auto SET, uint32_t cb) {
+        constexpr int S = decltype(SET)::value;
 #pragma unroll
-        for (int j = 0; j < NLD; ++j) {
-            const int i = min(tid + j * NT, 4 * R - 1);
-            const uint32_t r = (uint32_t)i / (R / 8), c8 = (uint32_t)i % (R / 8);
-            kr[j] = *(const uint4*)(cb_base + (size_t)min(cb + r, pos) * R + 8u * c8);
+        for (int u = 0; u < NVU; ++u) {
+            const int un = min(tid + u * NT, 4 * (LR / 8) - 1), j = un & 3, db = un >> 2;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                kv[S][u][e] = *(const uint4*)(cb_base + (size_t)min(cb + vrow(j, e), pos) * R + 8 * db);
+        }
+#pragma unroll
+        for (int u = 0; u < NRU; ++u) {
+            const int un = min(tid + u * NT, 32 * (DR / 8) - 1), r = un / (DR / 8), db = LR / 8 + un % (DR / 8);
+            kq[S][u] = *(const uint4*)(cb_base + (size_t)min(cb + (uint32_t)r, pos) * R + 8 * db);
         }
     };
-    load_chunk(t0 < len ? t0 : pos & ~31u);
+    using Set0 = std::integral_constant<int, 0>;
+    using Set1 = std::integral_constant<int, 1>;
+    load_chunk(Set0{}, t0 < len ? t0 : pos & ~31u);
+    load_chunk(Set1{}, t0 + 32u < len ? t0 + 32u : pos & ~31u);
 
     // ---- q operands of head col: latent dims scaled, the RoPE part rotated, as fp16 ----
     vm_h8 qop[NCK];
@@ -417,31 +469,50 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) o_acc[nb] = vm_f4{0.f, 0.f, 0.f, 0.f};
 
-    for (uint32_t ci = 0; ci < n_chunks; ++ci) {
+    auto chunk_step = [&](auto SET, uint32_t ci) {
+        constexpr int S = decltype(SET)::value;
         const uint32_t cb = t0 + 32u * ci;
         __syncthreads();  // the previous chunk is consumed
+        auto to_h8 = [](const uint4& q) {
+            const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+            vm_h8 h;
 #pragma unroll
-        for (int j = 0; j < NLD; ++j) {
-            const int i = tid + j * NT;
-            if (i < 4 * R) {
-                const uint32_t r = (uint32_t)i / (R / 8), c8 = (uint32_t)i % (R / 8);
-                const uint32_t w4[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
-                vm_h8 h;
+            for (int e = 0; e < 4; ++e) {
+                h[2 * e] = (_Float16)__uint_as_float(w4[e] << 16);
+                h[2 * e + 1] = (_Float16)__uint_as_float(w4[e] & 0xFFFF0000u);
+            }
+            return h;
+        };
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    h[2 * e] = (_Float16)__uint_as_float(w4[e] << 16);
-                    h[2 * e + 1] = (_Float16)__uint_as_float(w4[e] & 0xFFFF0000u);
+        for (int u = 0; u < NVU; ++u) {
+            const int un = tid + u * NT;
+            if (un < 4 * (LR / 8)) {
+                const int j = un & 3, db = un >> 2;
+                vm_h8 hv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    hv[e] = to_h8(kv[S][u][e]);
+                    *(vm_h8*)(k_s + vrow(j, e) * KP + 8 * db) = hv[e];
                 }
-                *(vm_h8*)(k_s + r * KP + 8 * c8) = h;
-                if (8u * c8 < (uint32_t)LR) {
-                    const uint32_t sl = vm_vslot(r);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) v_s[(8 * c8 + e) * VP + sl] = h[e];
+                for (int d = 0; d < 8; ++d) {
+                    vm_h8 t;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) t[e] = hv[e][d];
+                    *(vm_h8*)(v_s + (8 * db + d) * VP + 8 * j) = t;
                 }
             }
         }
+#pragma unroll
+        for (int u = 0; u < NRU; ++u) {
+            const int un = tid + u * NT;
+            if (un < 32 * (DR / 8)) {
+                const int r = un / (DR / 8), db = LR / 8 + un % (DR / 8);
+                *(vm_h8*)(k_s + r * KP + 8 * db) = to_h8(kq[S][u]);
+            }
+        }
         __syncthreads();
-        if (ci + 1u < n_chunks) load_chunk(cb + 32u);
+        if (ci + 2u < n_chunks) load_chunk(SET, cb + 64u);
         // scores: sc[bb][i] = S[position cb + 16 bb + 4 grp + i][head col]
         vm_f4 sc[2];
 #pragma unroll
@@ -488,6 +559,10 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
             const vm_h8 vop = *(const vm_h8*)(v_s + (16 * nb + col) * VP + 8 * grp);
             o_acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, vop, o_acc[nb], 0, 0, 0);
         }
+    };
+    for (uint32_t ci = 0; ci < n_chunks; ci += 2u) {
+        chunk_step(Set0{}, ci);
+        if (ci + 1u < n_chunks) chunk_step(Set1{}, ci + 1u);
     }
 
     // ---- the split's partial: o_acc[nb][i] is head 4 grp + i of the wave, latent dim 16 nb + col ----
@@ -549,8 +624,9 @@ __global__ __launch_bounds__(256) void vx_mla_resid_kernel(float* h, const float
 
 hipError_t vx_launch_mla_prep(const VxMlaPrepArgs& a, uint32_t batch, hipStream_t st) {
     const size_t lds = ((size_t)(a.q_lora ? a.q_lora : 1u) + a.lr + a.dr) * 4;
-    if (lds > 60000 || a.na != a.q_part + a.lr + a.dr || (a.dr & 1u)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(vx_mla_prep_kernel, dim3(batch), dim3(256), lds, st, a);
+    if (lds > 60000 || a.na != a.q_part + a.lr + a.dr || (a.dr & 1u) || a.nparts == 0 || a.nparts > kMlaMaxParts)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(vx_mla_prep_kernel, dim3(batch), dim3(1024), lds, st, a);
     return hipGetLastError();
 }
 

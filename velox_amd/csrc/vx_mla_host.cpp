@@ -235,9 +235,11 @@ int velox_hip_mla_create(const VeloxHipMlaConfig* cfg, VeloxHipMla** out) {
     m->cache_bytes = vm_align(m->cache_layer_bytes * c.num_layers);
 
     // split counts: ~512 workgroups for the two skinny GEMMs; attention ~256 workgroups with at
-    // least 256 positions per split
-    const uint32_t wg_a = (m->na / 16 + 3) / 4, wg_o = (m->H / 16 + 3) / 4;
+    // least 64 positions per split
+    const uint32_t tpw = 4 * vx_f8gemm_rows_per_wave(m->B);  // row tiles per GEMM workgroup
+    const uint32_t wg_a = (m->na / 16 + tpw - 1) / tpw, wg_o = (m->H / 16 + tpw - 1) / tpw;
     m->ks_a = (512 + wg_a - 1) / wg_a;
+    if (m->ks_a > 16) m->ks_a = 16;  // the prep kernel folds at most 16 partials
     if (m->ks_a > m->H / 64) m->ks_a = m->H / 64;
     m->ks_o = (512 + wg_o - 1) / wg_o;
     if (m->ks_o > m->nh * m->dv / 64) m->ks_o = m->nh * m->dv / 64;
@@ -248,7 +250,7 @@ int velox_hip_mla_create(const VeloxHipMlaConfig* cfg, VeloxHipMla** out) {
     if (!splits) {
         const uint32_t hg = m->lr == 512 ? m->nh / 64 : m->nh / 16;
         splits = (256 + m->B * hg - 1) / (m->B * hg);
-        const uint32_t by_len = (c.max_seq_len + 255) / 256;
+        const uint32_t by_len = (c.max_seq_len + 63) / 64;  // at least two 32-position chunks per split
         if (splits > by_len) splits = by_len;
     }
     if (splits < 1) splits = 1;
