@@ -84,6 +84,54 @@ def cpu_baseline(seed: int) -> dict:
     }
 
 
+def bench_mla(args) -> int:
+    """one DeepSeek-V3 absorbed-MLA layer (fp8 e4m3 weights with 128x128 block
+    scales, bf16 latent cache of `context_len` seeded positions per sequence), timed as hipGraph
+    replays of the layer step; value = device microseconds per layer (lower is better)."""
+    from velox_amd.engine import mla_run
+
+    ctx = args.context_len or 4096
+    print(f"[bench] deepseek_v3_mla layer: batch {args.batch}, context {ctx}, warmup {args.warmup}, "
+          f"steps {args.steps}", file=sys.stderr, flush=True)
+    r = mla_run(batch=args.batch, context_len=ctx, warmup=args.warmup, steps=args.steps, seed=args.seed)
+    attn_gbps = r["attn_bytes"] / (r["attn_us"] * 1e3) if r["attn_us"] > 0 else 0.0
+    print(f"[bench] mla done: {r['us_per_layer']:.2f} us/layer, {r['hbm_gbps']:.0f} GB/s; attention "
+          f"{r['attn_us']:.2f} us", file=sys.stderr, flush=True)
+    out = {
+        "metric": f"MLA layer us + achieved HBM GB/s, DeepSeek-V3 MLA fp8 bs={args.batch} ctx {ctx}, 1 GPU",
+        "value": round(r["us_per_layer"], 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["us_per_layer"] / 1e3, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8 e4m3 x f16 -> f32 (bf16 latent cache)",
+        "data": "synthetic",
+        "config": {"workload": f"deepseek_v3_mla_fp8_layer_bs{args.batch}_ctx{ctx}", "batch": args.batch,
+                   "context_tokens": ctx, "hipgraph": True},
+        "hbm_gbps": round(r["hbm_gbps"], 1),
+        "hbm_frac": round(r["hbm_gbps"] / HBM_PEAK_GBPS, 4),
+        "bytes_per_step": int(r["bytes_per_layer"]),
+        "wall_ms": round(r["wall_ms"], 3),
+        "roofline": {
+            "kernel": "vx_mla_attn_kernel<512,64,4> (absorbed MLA attention over the bf16 latent cache, MFMA)",
+            "bound": "hbm",
+            "achieved": round(attn_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "avg_us": round(r["attn_us"], 3),
+            "bytes_per_launch": int(r["attn_bytes"]),
+        },
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -94,8 +142,10 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--prompt-len", type=int, default=PROMPT_LEN)
-    ap.add_argument("--model", default="llama3_8b", choices=["llama3_8b", "qwen2_5_7b", "qwen2_72b", "smollm_135m"],
-                    help="builtin configuration (the headline metric is llama3_8b)")
+    ap.add_argument("--model", default="llama3_8b",
+                    choices=["llama3_8b", "qwen2_5_7b", "qwen2_72b", "smollm_135m", "deepseek_v3_mla"],
+                    help="builtin configuration (the headline metric is llama3_8b; deepseek_v3_mla times one "
+                         "absorbed-MLA layer with fp8 weights, BASELINE config 4)")
     ap.add_argument("--context-len", type=int, default=0,
                     help="start from a seeded context of N positions already in the KV cache (prompt = 1 token)")
     ap.add_argument("--batch", type=int, default=1,
@@ -112,6 +162,8 @@ def main() -> int:
     from velox_amd.engine import run
 
     L.load()
+    if args.model == "deepseek_v3_mla":
+        return bench_mla(args)
     plen = 1 if args.context_len else args.prompt_len
     ctx = args.context_len
     cfg = L.builtin_config(args.model)
