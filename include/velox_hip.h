@@ -270,6 +270,8 @@ typedef struct VeloxHipRunOptions {
                                 (src/runners/velox_cuda_runner_k2.cu:1789 --context-len) */
     uint32_t batch;          /* >1: decode `batch` independent sequences per step (own seeded prompt and
                                 context each); tokens/report cover sequence 0, tok_per_s all of them */
+    const char* weights_path;/* NULL: synthetic weights of `model`; else a GGUF Q4_0 checkpoint whose
+                                metadata defines the model (the runner's --weights file.gguf) */
 } VeloxHipRunOptions;
 
 typedef struct VeloxHipRunReport {
@@ -288,6 +290,23 @@ typedef struct VeloxHipRunReport {
 
 /* Runs the whole flow; tokens (capacity max_tokens) receives prompt-forced and generated ids. */
 int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_tokens, VeloxHipRunReport* rep);
+
+/* ---- GGUF checkpoints (GGML's container, read by the reference's K2 runner,
+ * src/runners/velox_cuda_runner_k2.cu:48-196; llama.cpp tensor names as at :1918-1963) ----
+ * Memory-maps the file and parses header, metadata and tensor directory (bounds checked).
+ * velox_hip_gguf_config derives the model from the {arch}.* metadata (vocab from token_embd,
+ * QKV bias from blk.0.attn_q.bias, tied head when output.weight is absent); velox_hip_gguf_load
+ * loads every Q4_0 matrix and fp32/fp16 vector into an arena planned with that config. For arch
+ * "llama" the q/k rows (and biases) return from llama.cpp's pairwise order to rotate-half order. */
+typedef struct VeloxHipGguf VeloxHipGguf;
+int velox_hip_gguf_open(const char* path, VeloxHipGguf** out);
+void velox_hip_gguf_close(VeloxHipGguf* g);
+uint64_t velox_hip_gguf_tensor_count(const VeloxHipGguf* g);
+/* dims: 4 entries, GGML order (dims[0] is the contiguous one); nbytes 0 for unknown types */
+int velox_hip_gguf_tensor_info(const VeloxHipGguf* g, uint64_t i, char* name, uint32_t name_cap, uint32_t* type,
+                               uint32_t* n_dims, uint64_t* dims, uint64_t* nbytes);
+int velox_hip_gguf_config(const VeloxHipGguf* g, uint32_t max_seq_len, VeloxHipModelConfig* out);
+int velox_hip_gguf_load(VeloxHipArena* arena, const VeloxHipGguf* g, hipStream_t stream);
 
 /* ---- Absorbed multi-head latent attention layer (DeepSeek-V3 form) ----
  * Replaces the reference's MLA step: the emitted velox_cuda_fused_mla_absorbed_attn

@@ -66,7 +66,7 @@ class RunOptions(C.Structure):
         ("warmup", C.c_uint32), ("steps", C.c_uint32), ("seed", C.c_uint64), ("sigma", C.c_float),
         ("norm_sigma", C.c_float), ("use_graph", C.c_uint32), ("num_layers", C.c_uint32),
         ("kernel_passes", C.c_uint32), ("verbose", C.c_uint32), ("prompt_tokens", C.POINTER(C.c_uint32)),
-        ("context_len", C.c_uint32), ("batch", C.c_uint32),
+        ("context_len", C.c_uint32), ("batch", C.c_uint32), ("weights_path", C.c_char_p),
     ]
 
 
@@ -157,6 +157,13 @@ _SIGS = {
     "velox_hip_rmsnorm": (_I, [_P, _P, _U32, _F, _P, _P]),
     "velox_hip_attention_decode": (_I, [_P, _P, _U32, _U32, _U32, _U32, _U32, _F, _U32, _P, _P]),
     "velox_hip_run": (_I, [C.POINTER(RunOptions), C.POINTER(_U32), _U32, C.POINTER(RunReport)]),
+    "velox_hip_gguf_open": (_I, [C.c_char_p, C.POINTER(_P)]),
+    "velox_hip_gguf_close": (None, [_P]),
+    "velox_hip_gguf_tensor_count": (_U64, [_P]),
+    "velox_hip_gguf_tensor_info": (_I, [_P, _U64, C.c_char_p, _U32, C.POINTER(_U32), C.POINTER(_U32),
+                                        C.POINTER(_U64), C.POINTER(_U64)]),
+    "velox_hip_gguf_config": (_I, [_P, _U32, C.POINTER(ModelConfig)]),
+    "velox_hip_gguf_load": (_I, [C.POINTER(Arena), _P, _P]),
     "velox_hip_mla_builtin_config": (_I, [C.c_char_p, _U32, _U32, C.POINTER(MlaConfig)]),
     "velox_hip_mla_create": (_I, [C.POINTER(MlaConfig), C.POINTER(_P)]),
     "velox_hip_mla_destroy": (None, [_P]),

@@ -1107,15 +1107,25 @@ int velox_hip_attention_decode(const float* d_qkv, uint16_t* d_kv_layer, uint32_
 // graph capture (:474-481), prefill (:493-512), timed decode replays (:535-563).
 // ---------------------------------------------------------------------------------------------
 int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_tokens, VeloxHipRunReport* rep) {
-    if (!opt || !rep || !opt->model || opt->prompt_len == 0) return VELOX_HIP_EINVAL;
+    if (!opt || !rep || (!opt->model && !opt->weights_path) || opt->prompt_len == 0) return VELOX_HIP_EINVAL;
     if (opt->context_len && opt->prompt_len != 1) return VELOX_HIP_EINVAL;  // context + one seed token
     std::memset(rep, 0, sizeof(*rep));
     const uint32_t base = opt->context_len;  // first decoded position
     const uint32_t total = base + opt->prompt_len + opt->warmup + opt->steps;
     VeloxHipModelConfig cfg;
-    int rc = velox_hip_builtin_config(opt->model, opt->max_seq_len ? opt->max_seq_len : total + 1, &cfg);
-    if (rc) return rc;
-    if (opt->num_layers) cfg.num_layers = opt->num_layers;
+    VeloxHipGguf* gguf = nullptr;
+    int rc;
+    if (opt->weights_path) {
+        rc = velox_hip_gguf_open(opt->weights_path, &gguf);
+        if (!rc) rc = velox_hip_gguf_config(gguf, opt->max_seq_len ? opt->max_seq_len : total + 1, &cfg);
+        if (rc) { velox_hip_gguf_close(gguf); return rc; }
+    } else {
+        rc = velox_hip_builtin_config(opt->model, opt->max_seq_len ? opt->max_seq_len : total + 1, &cfg);
+        if (rc) return rc;
+    }
+    // the arena's model stays alive until the end of the run; the file is closed once loaded
+    struct GgufCloser { VeloxHipGguf*& g; ~GgufCloser() { velox_hip_gguf_close(g); } } gguf_closer{gguf};
+    if (opt->num_layers && !gguf) cfg.num_layers = opt->num_layers;
     const uint32_t B = opt->batch > 1 ? opt->batch : 1u;
     if (B > 32 || (B > 1 && opt->prompt_tokens)) return VELOX_HIP_EINVAL;
     if (B > 1) cfg.max_batch = B;
@@ -1134,7 +1144,7 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
     hipGraphExec_t exec = nullptr;
 
     const auto t_load = std::chrono::steady_clock::now();
-    rc = velox_hip_synthesize_model(&A, opt->seed, opt->sigma, opt->norm_sigma, st);
+    rc = gguf ? velox_hip_gguf_load(&A, gguf, st) : velox_hip_synthesize_model(&A, opt->seed, opt->sigma, opt->norm_sigma, st);
     rep->load_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_load).count();
 
     // sequence b's prompt: seeded ids (sequence 0: the single-sequence prompt) or explicit ones

@@ -3,12 +3,13 @@
 // (src/cli.rs:640-770, "[Step N] Token: id" parsing at :706-733) and the benchmark regexes
 // (benchmarks/run_sota_roofline_benchmarks.py:278-292) keep working.
 //
-//   velox_hip_runner [--model llama3_8b] [--weights synthetic] [--tokens 1,2,3 | --prompt-len N]
+//   velox_hip_runner [--model llama3_8b] [--weights synthetic|FILE.gguf] [--tokens 1,2,3 | --prompt-len N]
 //                    [--context-len N] [--steps N] [--warmup N] [--seed S] [--layers L]
 //                    [--no-cuda-graph] [--verbose]
 //
-// Weights are the seeded synthetic Q4_0 model: `--weights synthetic` (what src/cli.rs:654 passes
-// through) is accepted, a checkpoint path is refused with exit 1.
+// Weights are the seeded synthetic Q4_0 model (`--weights synthetic`, what src/cli.rs:654 passes
+// through) or a GGUF Q4_0 checkpoint (`--weights FILE.gguf`, whose metadata then defines the model,
+// as the K2 runner's --weights does); other checkpoint formats are refused with exit 1.
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -18,7 +19,7 @@
 #include "velox_hip.h"
 
 int main(int argc, char** argv) {
-    std::string model = "llama3_8b";
+    std::string model = "llama3_8b", weights;
     std::vector<uint32_t> tokens;
     uint32_t prompt_len = 128, steps = 32, warmup = 0, layers = 0, context_len = 0;
     uint64_t seed = 1234;
@@ -56,8 +57,11 @@ int main(int argc, char** argv) {
         else if (!std::strcmp(a, "--verbose")) verbose = true;
         else if (!std::strcmp(a, "--weights")) {
             const char* w = next();
-            if (std::strcmp(w, "synthetic") != 0) {
-                std::fprintf(stderr, "Error: --weights %s is not supported (synthetic Q4_0 weights only)\n", w);
+            const size_t n = std::strlen(w);
+            if (n > 5 && !std::strcmp(w + n - 5, ".gguf")) {
+                weights = w;
+            } else if (std::strcmp(w, "synthetic") != 0) {
+                std::fprintf(stderr, "Error: --weights %s is not supported (synthetic or a .gguf Q4_0 file)\n", w);
                 return 1;
             }
         } else if (!std::strcmp(a, "--context-len")) {
@@ -95,6 +99,7 @@ int main(int argc, char** argv) {
     opt.verbose = verbose ? 1 : 0;
     opt.prompt_tokens = tokens.empty() ? nullptr : tokens.data();
     opt.context_len = context_len;
+    opt.weights_path = weights.empty() ? nullptr : weights.c_str();
     std::vector<uint32_t> out(prompt_len + warmup + opt.steps + 8);
     VeloxHipRunReport rep;
     const int rc = velox_hip_run(&opt, out.data(), (uint32_t)out.size(), &rep);
@@ -110,8 +115,13 @@ int main(int argc, char** argv) {
     std::printf("================================================================================\n");
     std::printf("VELOX MI355X HIP RUNTIME EXECUTION REPORT\n");
     std::printf("================================================================================\n");
-    std::printf("Model                  : %s (synthetic Q4_0, seed %llu)\n", model.c_str(), (unsigned long long)seed);
-    std::printf("Weight Synthesis       : %.2f ms\n", rep.load_ms);
+    if (weights.empty()) {
+        std::printf("Model                  : %s (synthetic Q4_0, seed %llu)\n", model.c_str(), (unsigned long long)seed);
+        std::printf("Weight Synthesis       : %.2f ms\n", rep.load_ms);
+    } else {
+        std::printf("Model                  : %s (GGUF Q4_0)\n", weights.c_str());
+        std::printf("Weight Load            : %.2f ms\n", rep.load_ms);
+    }
     std::printf("TTFT (Prefill Latency) : %.3f ms\n", rep.prefill_ms);
     std::printf("Decode Latency (%u tok): %.3f ms (%.2f tok/s, %.3f ms/tok)\n", opt.steps, rep.decode_ms, rep.tok_per_s,
                 rep.decode_ms / opt.steps);

@@ -16,10 +16,26 @@ import numpy as np
 from . import _lib as L
 
 
+def gguf_config(path: str, max_seq_len: int = 0) -> L.ModelConfig:
+    """The model configuration a GGUF checkpoint's metadata defines (velox_hip_gguf_config)."""
+    lib = L.load()
+    g = C.c_void_p()
+    L.check(lib.velox_hip_gguf_open(path.encode(), C.byref(g)), "gguf_open")
+    try:
+        cfg = L.ModelConfig()
+        L.check(lib.velox_hip_gguf_config(g, max_seq_len, C.byref(cfg)), "gguf_config")
+    finally:
+        lib.velox_hip_gguf_close(g)
+    return cfg
+
+
 def make_config(model, max_seq_len: int = 0, num_layers: int = 0, attn_splits: int = 0,
                 max_batch: int = 0) -> L.ModelConfig:
-    """A builtin config by name, or a dict of ModelConfig fields (custom shapes for tests)."""
-    if isinstance(model, str):
+    """A builtin config by name, a GGUF file (path ending in .gguf), or a dict of ModelConfig
+    fields (custom shapes for tests)."""
+    if isinstance(model, str) and model.endswith(".gguf"):
+        cfg = gguf_config(model, max_seq_len)
+    elif isinstance(model, str):
         cfg = L.builtin_config(model, max_seq_len)
     else:
         cfg = L.ModelConfig()
@@ -54,7 +70,14 @@ class HipDecodeEngine:
         self.hidden_off = self.lib.velox_hip_model_hidden_offset(self._model)
         self.logits = np.zeros(self.vocab, np.float32)
         self._graph = None
-        if synthesize:
+        if isinstance(model, str) and model.endswith(".gguf"):
+            g = C.c_void_p()
+            L.check(self.lib.velox_hip_gguf_open(model.encode(), C.byref(g)), "gguf_open")
+            try:
+                L.check(self.lib.velox_hip_gguf_load(C.byref(self.arena), g, None), "gguf_load")
+            finally:
+                self.lib.velox_hip_gguf_close(g)
+        elif synthesize:
             L.check(self.lib.velox_hip_synthesize_model(C.byref(self.arena), seed, sigma, norm_sigma, None),
                     "synthesize_model")
 
