@@ -59,7 +59,8 @@ typedef struct VeloxHipModelConfig {
     uint64_t vram_budget_bytes; /* 0 = 288 GB of HBM3E */
     uint32_t max_batch;         /* sequences of the batched decode step (<= 32; 0 or 1 = single);
                                    sizes the KV pool like B_MAX in src/memory_planner.rs:282-488 */
-    uint32_t reserved;
+    uint32_t prefill_chunk;     /* >1: positions of one prompt that velox_hip_prefill_batch runs as the
+                                   rows of one batched step (<= 32); 0 or 1 = token-by-token only */
 } VeloxHipModelConfig;
 
 typedef struct VeloxHipModel VeloxHipModel; /* opaque: the static memory plan */
@@ -186,6 +187,20 @@ int velox_hip_fill_kv_seq(VeloxHipArena* a, uint32_t layer, uint32_t seq, uint32
  * like velox_hip_decode_graph_step. Weights are read once per step for all sequences (MFMA GEMMs). */
 void velox_hip_decode_batch_graph_step(VeloxHipArena* ctx, uint32_t batch, uint64_t active_mask, hipStream_t stream);
 
+/* ---- batched prefill (replaces the token-by-token prefill loop of velox_cuda_runner.cu:493-512
+ *      for a prompt staged with velox_hip_set_prompt; the runtime form of the DSL's chunked_prefill
+ *      scope and its chunk_size, src/ast.rs:632-654; arena planned with prefill_chunk > 1) ----
+ * Positions [pos0, pos0 + n_tokens) of the staged prompt run in chunks of up to prefill_chunk
+ * positions, each chunk as the rows of one batched step (the weights are read once per chunk):
+ * every row's K/V row goes into the single-sequence KV cache, then each row attends over
+ * [0, its position]. Afterwards the decode state is {pos0 + n_tokens, the next prompt token, or
+ * the last row's argmax past the prompt} -- what n_tokens token-by-token prefill steps leave --,
+ * ring[p % VELOX_HIP_RING_SIZE] holds each position's argmax and the last chunk's logits are at
+ * the batch layout's logits_offset (row r = position of the chunk's r-th row). Positions must lie
+ * inside the staged prompt and below max_seq_len. Returns the first launch error. */
+int velox_hip_prefill_batch(VeloxHipArena* ctx, uint64_t pos0, uint32_t n_tokens, uint64_t active_mask,
+                            hipStream_t stream);
+
 /* Q4_0 matrix in the tiled device layout. Row r, block b of an [n][k] matrix lives in lane
  * (r % (64/s_lanes)) * s_lanes + b % s_lanes of iteration b / s_lanes of tile r / (64/s_lanes):
  * codes uint4 [n_tiles][n_iter][64], scales fp16 [n_tiles][n_iter][64]. */
@@ -272,6 +287,9 @@ typedef struct VeloxHipRunOptions {
                                 context each); tokens/report cover sequence 0, tok_per_s all of them */
     const char* weights_path;/* NULL: synthetic weights of `model`; else a GGUF Q4_0 checkpoint whose
                                 metadata defines the model (the runner's --weights file.gguf) */
+    uint32_t prefill_chunk;  /* >1 (single sequence, no context_len): the prompt runs through
+                                velox_hip_prefill_batch in chunks of this many positions (<= 32)
+                                instead of one decode step each */
 } VeloxHipRunOptions;
 
 typedef struct VeloxHipRunReport {

@@ -30,7 +30,7 @@ class ModelConfig(C.Structure):
         ("rms_norm_eps", C.c_float), ("rope_theta", C.c_float),
         ("qkv_bias", C.c_uint32), ("tied_lm_head", C.c_uint32), ("quant_mode", C.c_uint32),
         ("attn_splits", C.c_uint32), ("vram_budget_bytes", C.c_uint64),
-        ("max_batch", C.c_uint32), ("reserved", C.c_uint32),
+        ("max_batch", C.c_uint32), ("prefill_chunk", C.c_uint32),
     ]
 
     def as_dict(self) -> dict:
@@ -67,6 +67,7 @@ class RunOptions(C.Structure):
         ("norm_sigma", C.c_float), ("use_graph", C.c_uint32), ("num_layers", C.c_uint32),
         ("kernel_passes", C.c_uint32), ("verbose", C.c_uint32), ("prompt_tokens", C.POINTER(C.c_uint32)),
         ("context_len", C.c_uint32), ("batch", C.c_uint32), ("weights_path", C.c_char_p),
+        ("prefill_chunk", C.c_uint32),
     ]
 
 
@@ -140,6 +141,7 @@ _SIGS = {
     "velox_hip_batch_get_state": (_I, [C.POINTER(Arena), _U32, C.POINTER(DecodeState), _P]),
     "velox_hip_fill_kv_seq": (_I, [C.POINTER(Arena), _U32, _U32, _U32, _U64, _F, _P]),
     "velox_hip_decode_batch_graph_step": (None, [C.POINTER(Arena), _U32, _U64, _P]),
+    "velox_hip_prefill_batch": (_I, [C.POINTER(Arena), _U64, _U32, _U64, _P]),
     "velox_hip_decode": (None, [C.POINTER(Arena), _U32, C.c_size_t, _U64, _P]),
     "velox_hip_prefill_graph_step": (None, [C.POINTER(Arena), _U64, _P]),
     "velox_hip_prefill": (None, [C.POINTER(Arena), _U32, C.c_size_t, _U64, _P]),

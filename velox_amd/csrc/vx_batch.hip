@@ -457,6 +457,117 @@ __global__ __launch_bounds__(256) void vx_bfinalize_kernel(const float* cand_v, 
     }
 }
 
+// ---- batched prefill: the rows of a chunk are consecutive positions of one sequence ----
+
+// Row r of the chunk: position p0 + r, input token prompt[p0 + r].
+__global__ __launch_bounds__(64) void vx_prefill_rows_kernel(VeloxDecodeState* rows, uint32_t n_rows, uint64_t p0,
+                                                             const uint32_t* prompt, uint64_t mask) {
+    if ((mask & 1ULL) == 0ULL) return;
+    for (uint32_t r = threadIdx.x; r < n_rows; r += 64u) {
+        rows[r].step = p0 + r;
+        rows[r].token = prompt[p0 + r];
+    }
+}
+
+// K/V of every row into the one sequence's cache before the chunk's attention reads them: RoPE of
+// k at the row's position (src/runtime.rs:745-768), bf16 K row and V slot.
+__global__ __launch_bounds__(64) void vx_kv_append_rows_kernel(const float* qkv, uint32_t ldq, uint32_t hq,
+                                                               uint32_t hkv, uint32_t d, const VeloxDecodeState* rows,
+                                                               const float2* rope, uint32_t s_max, uint32_t s_cap,
+                                                               uint16_t* kv, uint64_t mask) {
+    if ((mask & 1ULL) == 0ULL) return;
+    const uint32_t g = blockIdx.x, r = blockIdx.y, half = d / 2u;
+    const uint64_t step = rows[r].step;
+    const uint32_t pos = step < (uint64_t)s_max ? (uint32_t)step : s_max - 1u;
+    const float* k = qkv + (size_t)r * ldq + (size_t)hq * d + (size_t)g * d;
+    const float* v = qkv + (size_t)r * ldq + (size_t)(hq + hkv) * d + (size_t)g * d;
+    uint16_t* Kc = kv + (size_t)g * s_cap * d;
+    uint16_t* Vc = kv + ((size_t)hkv + g) * s_cap * d;
+    for (uint32_t j = threadIdx.x; j < half; j += 64u) {
+        const float2 cs = rope[(size_t)pos * half + j];
+        const float x1 = k[j], x2 = k[j + half];
+        float o1, o2;
+        {
+#pragma clang fp contract(off)
+            o1 = x1 * cs.x - x2 * cs.y;
+            o2 = x2 * cs.x + x1 * cs.y;
+        }
+        Kc[(size_t)pos * d + j] = vx_f32_to_bf16_bits(o1);
+        Kc[(size_t)pos * d + j + half] = vx_f32_to_bf16_bits(o2);
+    }
+    uint16_t* vb = Vc + (size_t)(pos >> 5) * d * 32u + vx_vslot(pos & 31u);
+    for (uint32_t i = threadIdx.x; i < d; i += 64u) vb[(size_t)i * 32u] = vx_f32_to_bf16_bits(v[i]);
+}
+
+// Per row: the argmax over the LM head's candidates into the ring at the row's position; the last
+// row sets the sequence's state: position p0 + n_rows, the next prompt token while inside the
+// prompt, else the argmax (the token-by-token prefill's teacher forcing, src/runtime.rs:1078-1088).
+__global__ __launch_bounds__(256) void vx_prefill_finalize_kernel(const float* cand_v, const uint32_t* cand_i,
+                                                                  uint32_t n, const VeloxDecodeState* rows,
+                                                                  uint32_t n_rows, uint32_t* ring,
+                                                                  VeloxDecodeState* state, const uint32_t* prompt,
+                                                                  const uint32_t* plen, uint64_t mask) {
+    if ((mask & 1ULL) == 0ULL) return;
+    __shared__ float s_v[4];
+    __shared__ uint32_t s_i[4];
+    const uint32_t r = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (uint32_t j = tid; j < n; j += 256) {
+        const float v = cand_v[(size_t)r * n + j];
+        const uint32_t ii = cand_i[(size_t)r * n + j];
+        if (vx_bbetter(v, ii, bv, bi)) { bv = v; bi = ii; }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const uint32_t oi = __shfl_xor(bi, off);
+        if (vx_bbetter(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) { s_v[wave] = bv; s_i[wave] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 4; ++w)
+            if (vx_bbetter(s_v[w], s_i[w], s_v[0], s_i[0])) { s_v[0] = s_v[w]; s_i[0] = s_i[w]; }
+        const uint32_t win = s_i[0] == 0xFFFFFFFFu ? 0u : s_i[0];
+        const uint64_t step = rows[r].step;
+        if (ring) {
+            __atomic_store_n(ring + (step & (VELOX_HIP_RING_SIZE - 1u)), win, __ATOMIC_RELAXED);
+            __threadfence_system();
+        }
+        if (r + 1u == n_rows) {
+            const uint32_t p = plen ? plen[0] : 0u;
+            state->token = (step + 1u < (uint64_t)p) ? prompt[step + 1u] : win;
+            state->step = step + 1u;
+        }
+    }
+}
+
+hipError_t vx_launch_prefill_rows(VeloxDecodeState* rows, uint32_t n_rows, uint64_t p0, const uint32_t* prompt,
+                                  uint64_t mask, hipStream_t st) {
+    hipLaunchKernelGGL(vx_prefill_rows_kernel, dim3(1), dim3(64), 0, st, rows, n_rows, p0, prompt, mask);
+    return hipGetLastError();
+}
+
+hipError_t vx_launch_kv_append_rows(const float* qkv, uint32_t ldq, uint32_t hq, uint32_t hkv, uint32_t d,
+                                    const VeloxDecodeState* rows, uint32_t n_rows, const float2* rope, uint32_t s_max,
+                                    uint32_t s_cap, uint16_t* kv, uint64_t mask, hipStream_t st) {
+    if ((s_cap & 31u) || s_cap < s_max || (d & 1u)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(vx_kv_append_rows_kernel, dim3(hkv, n_rows), dim3(64), 0, st, qkv, ldq, hq, hkv, d, rows, rope,
+                       s_max, s_cap, kv, mask);
+    return hipGetLastError();
+}
+
+hipError_t vx_launch_prefill_finalize(const float* cand_v, const uint32_t* cand_i, uint32_t n,
+                                      const VeloxDecodeState* rows, uint32_t n_rows, uint32_t* ring,
+                                      VeloxDecodeState* state, const uint32_t* prompt, const uint32_t* plen,
+                                      uint64_t mask, hipStream_t st) {
+    hipLaunchKernelGGL(vx_prefill_finalize_kernel, dim3(n_rows), dim3(256), 0, st, cand_v, cand_i, n, rows, n_rows,
+                       ring, state, prompt, plen, mask);
+    return hipGetLastError();
+}
+
 hipError_t vx_launch_bembed(const VxMat& m, const VeloxDecodeState* states, uint32_t batch, float* h, uint32_t ldh,
                             uint64_t mask, hipStream_t st) {
     const uint32_t nb = m.k >> 5;

@@ -83,6 +83,11 @@ VX_HD uint16_t vx_f32_to_bf16_bits(float f) {
 }
 VX_HD float vx_bf16_bits_to_f32(uint16_t h) { return __builtin_bit_cast(float, (uint32_t)h << 16); }
 
+// V cache blocks hold 32 positions dimension-major; slot of position r (0..31) of a block: the P.V
+// MFMA's lane group j supplies, as its 8 K-elements, positions 4j..4j+3 and 16+4j..16+4j+3 (where
+// the K.Q^T MFMA leaves the scores), so slot 8j + 4 half + i holds position 16 half + 4j + i.
+VX_HD uint32_t vx_vslot(uint32_t r) { return 8u * ((r & 15u) >> 2) + 4u * (r >> 4) + (r & 3u); }
+
 // ---------------------------------------------------------------------------------------------
 // Device-side views
 // ---------------------------------------------------------------------------------------------
@@ -131,6 +136,8 @@ struct VxAttnArgs {
     float* out;              // [hq*d]
     uint32_t hq, hkv, s_max, splits;
     uint32_t s_cap;          // KV plane capacity in positions: s_max rounded up to 32
+    uint32_t prefill;        // 1: the rows are positions of one sequence whose K/V rows (its own
+                             // included) are already in the cache: attend over [0, pos], no append
     float scale;
     uint64_t active_mask;
     uint32_t partials_only;  // 1: always write (m, l, o) partials; the consumer merges them
@@ -197,6 +204,16 @@ hipError_t vx_launch_attention(const VxAttnArgs& a, uint32_t d, hipStream_t st);
 // vx_batch.hip
 hipError_t vx_launch_bgemm(const VxMat& m, const VxBGemmArgs& a, int epi, hipStream_t st);
 uint32_t vx_bgemm_grid(uint32_t n_tiles, uint32_t s);
+// Batched prefill (vx_batch.hip): row r of a chunk is position p0 + r of the one sequence.
+hipError_t vx_launch_prefill_rows(VeloxDecodeState* rows, uint32_t n_rows, uint64_t p0, const uint32_t* prompt,
+                                  uint64_t mask, hipStream_t st);
+hipError_t vx_launch_kv_append_rows(const float* qkv, uint32_t ldq, uint32_t hq, uint32_t hkv, uint32_t d,
+                                    const VeloxDecodeState* rows, uint32_t n_rows, const float2* rope, uint32_t s_max,
+                                    uint32_t s_cap, uint16_t* kv, uint64_t mask, hipStream_t st);
+hipError_t vx_launch_prefill_finalize(const float* cand_v, const uint32_t* cand_i, uint32_t n,
+                                      const VeloxDecodeState* rows, uint32_t n_rows, uint32_t* ring,
+                                      VeloxDecodeState* state, const uint32_t* prompt, const uint32_t* plen,
+                                      uint64_t mask, hipStream_t st);
 hipError_t vx_launch_bembed(const VxMat& m, const VeloxDecodeState* states, uint32_t batch, float* h, uint32_t ldh,
                             uint64_t mask, hipStream_t st);
 // parts != nullptr: h[b] += sum over s < nparts of parts[s * pstride + b * ldh] first (written back)

@@ -75,6 +75,9 @@ struct VeloxHipModel {
     // batched decode (max_batch > 1): per-sequence states, prompts, fp32 residuals, two fp16 GEMM
     // operands, q/k/v, attention partials, logits and LM-head candidates, sequence-major
     uint32_t batch = 1, xw = 0, head_bwgs = 0;
+    // rows of the batched region: max(batch, prefill_chunk) (sequences, or positions of a prompt)
+    uint32_t rows = 1;
+    uint64_t a_prows = 0;  // prefill: the chunk's rows {position, token}
     uint64_t a_bstate = 0, a_bplen = 0, a_bprompt = 0, a_bh = 0, a_bxa = 0, a_bxb = 0, a_bqkv = 0;
     uint64_t a_bpart_o = 0, a_bpart_ml = 0, a_blogits = 0, a_bcand_v = 0, a_bcand_i = 0;
     // K-split partials of the residual GEMMs (o_proj, down): [ksplit][batch][hidden]
@@ -164,9 +167,9 @@ bool vx_shape_ok(const VeloxHipModelConfig& c) {
     if (c.head_dim == 128 && !(G == 1 || G == 2 || G == 4 || G == 7 || G == 8)) return false;
     if (((uint64_t)c.num_heads * c.head_dim) % 32) return false;
     if (c.quant_mode != VELOX_QUANT_GGML_Q4_0) return false;
-    if (c.num_kv_heads > 64 || c.attn_splits > 64 || c.max_batch > 32) return false;
+    if (c.num_kv_heads > 64 || c.attn_splits > 64 || c.max_batch > 32 || c.prefill_chunk > 32) return false;
     // batched RMSNorm: float4 rows of at most 8192
-    if (c.max_batch > 1 && ((c.hidden_dim & 3u) || c.hidden_dim > 8192)) return false;
+    if ((c.max_batch > 1 || c.prefill_chunk > 1) && ((c.hidden_dim & 3u) || c.hidden_dim > 8192)) return false;
     if (c.hidden_dim > 32768 || c.intermediate_dim > 32768 || (uint64_t)c.num_heads * c.head_dim > 32768) return false;
     return true;
 }
@@ -322,15 +325,18 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
     M->a_part_ml = take((uint64_t)c.num_heads * splits * 2 * 4);
     M->a_cand_v = take((uint64_t)65536 * 4);
     M->a_cand_i = take((uint64_t)65536 * 4);
-    if (M->batch > 1) {
-        const uint64_t B = M->batch;
+    M->rows = M->batch;
+    if (c.prefill_chunk > M->rows) M->rows = c.prefill_chunk;
+    if (M->rows > 1) {
+        const uint64_t B = M->rows;
         uint32_t xw = H > qd ? H : qd;
         if (F > xw) xw = F;
         M->xw = (xw + 7u) & ~7u;
         M->head_bwgs = vx_bgemm_grid(M->head.n_tiles, M->head.s);
-        M->a_bstate = take(B * sizeof(VeloxDecodeState));
-        M->a_bplen = take(B * 4);
-        M->a_bprompt = take(B * c.max_seq_len * 4);
+        const uint64_t S = M->batch;  // per-sequence state, prompt length and prompt
+        M->a_bstate = take(S * sizeof(VeloxDecodeState));
+        M->a_bplen = take(S * 4);
+        M->a_bprompt = take(S * c.max_seq_len * 4);
         M->a_bh = take(B * H * 4);
         M->a_bxa = take(B * M->xw * 2);
         M->a_bxb = take(B * M->xw * 2);
@@ -341,6 +347,7 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
         M->a_bcand_v = take(B * M->head_bwgs * 4);
         M->a_bcand_i = take(B * M->head_bwgs * 4);
         M->a_bpart_r = take(8 * B * H * 4);
+        M->a_prows = take(B * sizeof(VeloxDecodeState));
         M->ksplit_o = vx_bgemm_ksplit(M->layers[0].o);
         M->ksplit_down = vx_bgemm_ksplit(M->layers[0].down);
     }
@@ -702,34 +709,36 @@ uint64_t velox_hip_model_batch_step_bytes(const VeloxHipModel* m, uint32_t batch
     return velox_hip_model_step_bytes(m, pos) + (uint64_t)(batch - 1) * per_seq;
 }
 
-// One decode step of sequences 0 .. batch-1, each at its own state (step, token): the weights are
-// read once per step for all of them. Launches: embed, L x [norm, QKV, attention, merge, o_proj +
-// residual, norm, gate/up + SwiGLU, down + residual], norm, LM head, argmax per sequence.
-void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_t mask, hipStream_t st) {
-    if (!A || !A->model || A->model->batch < 2 || batch == 0 || batch > A->model->batch) {
-        if (!g_last_error) g_last_error = VELOX_HIP_EINVAL;
-        return;
-    }
+namespace {
+
+// One forward over rows 0 .. n-1 of the batched region through the LM head's argmax candidates;
+// rows[r] holds row r's position and input token. Decode: row b is sequence b with its own KV
+// cache, which the attention kernel appends the new position to. Prefill: the rows are
+// consecutive positions of sequence 0, whose K/V rows all go into its cache before the attention,
+// which then attends over [0, position] of every row. Launches: embed, L x [norm, QKV, (prefill:
+// K/V rows,) attention, merge, o_proj + residual, norm, gate/up + SwiGLU, down + residual], norm,
+// LM head.
+void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n, uint64_t mask, bool prefill,
+                     hipStream_t st) {
     const VeloxHipModel* M = A->model;
     const VeloxHipModelConfig& c = M->cfg;
     uint8_t* act = A->activation_arena;
     const uint32_t H = c.hidden_dim, D = c.head_dim, qd = c.num_heads * D, kvd = c.num_kv_heads * D;
     const float* nrm = (const float*)A->norm_weight_arena;
     auto vecp = [&](uint64_t off) { return (const float*)((const uint8_t*)nrm + off); };
-    VeloxDecodeState* states = (VeloxDecodeState*)(act + M->a_bstate);
     float* h = (float*)(act + M->a_bh);
     uint16_t* xa = (uint16_t*)(act + M->a_bxa);
     uint16_t* xb = (uint16_t*)(act + M->a_bxb);
     float* qkv = (float*)(act + M->a_bqkv);
     float* part_r = (float*)(act + M->a_bpart_r);
-    const uint64_t pstride = (uint64_t)M->batch * H;
+    const uint64_t pstride = (uint64_t)M->rows * H;
 
-    vx_record(vx_launch_bembed(vx_view(A, M->embed), states, batch, h, H, mask, st));
+    vx_record(vx_launch_bembed(vx_view(A, M->embed), rows, n, h, H, mask, st));
     VxAttnArgs at;
     std::memset(&at, 0, sizeof(at));
     at.qkv = qkv;
     at.rope = (const float2*)vecp(M->rope);
-    at.state = states;
+    at.state = rows;
     at.part_o = (float*)(act + M->a_bpart_o);
     at.part_ml = (float*)(act + M->a_bpart_ml);
     at.hq = c.num_heads;
@@ -740,17 +749,19 @@ void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_
     at.scale = 1.0f / sqrtf((float)D);
     at.active_mask = mask;
     at.partials_only = 1;
-    at.batch = batch;
-    at.kv_bstride = M->kv_layer_bytes / 2;  // consecutive sequences of one layer
+    at.batch = n;
+    at.prefill = prefill ? 1u : 0u;
+    // decode: consecutive sequences of one layer; prefill: every row reads sequence 0's cache
+    at.kv_bstride = prefill ? 0 : M->kv_layer_bytes / 2;
     at.qkv_bstride = qd + 2 * kvd;
     VxBGemmArgs g;
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         const VxLayerPlan& L = M->layers[l];
         // the previous layer's down projection left its K-split partials (none before layer 0)
-        vx_record(vx_launch_bnorm(h, H, l && M->ksplit_down > 1 ? part_r : nullptr, M->ksplit_down, pstride, vecp(L.attn_norm), H,
-                                  c.rms_norm_eps, xa, M->xw, batch, mask, st));
+        vx_record(vx_launch_bnorm(h, H, l && M->ksplit_down > 1 ? part_r : nullptr, M->ksplit_down, pstride,
+                                  vecp(L.attn_norm), H, c.rms_norm_eps, xa, M->xw, n, mask, st));
         std::memset(&g, 0, sizeof(g));
-        g.batch = batch;
+        g.batch = n;
         g.active_mask = mask;
         g.x16 = xa;
         g.ldx = M->xw;
@@ -759,10 +770,13 @@ void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_
         g.ldy = qd + 2 * kvd;
         vx_record(vx_launch_bgemm(vx_view(A, L.qkv), g, VX_EPI_STORE, st));
         at.kv = vx_kv(A, l, 0);
+        if (prefill)
+            vx_record(vx_launch_kv_append_rows(qkv, qd + 2 * kvd, c.num_heads, c.num_kv_heads, D, rows, n, at.rope,
+                                               c.max_seq_len, M->s_cap, at.kv, mask, st));
         vx_record(vx_launch_attention(at, D, st));
-        vx_record(vx_launch_bmerge(at.part_o, at.part_ml, c.num_heads, D, M->splits, xa, M->xw, batch, mask, st));
+        vx_record(vx_launch_bmerge(at.part_o, at.part_ml, c.num_heads, D, M->splits, xa, M->xw, n, mask, st));
         std::memset(&g, 0, sizeof(g));
-        g.batch = batch;
+        g.batch = n;
         g.active_mask = mask;
         g.x16 = xa;
         g.ldx = M->xw;
@@ -773,9 +787,9 @@ void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_
         g.pstride = pstride;
         vx_record(vx_launch_bgemm(vx_view(A, L.o), g, VX_EPI_RESID, st));
         vx_record(vx_launch_bnorm(h, H, M->ksplit_o > 1 ? part_r : nullptr, M->ksplit_o, pstride, vecp(L.mlp_norm), H,
-                                  c.rms_norm_eps, xa, M->xw, batch, mask, st));
+                                  c.rms_norm_eps, xa, M->xw, n, mask, st));
         std::memset(&g, 0, sizeof(g));
-        g.batch = batch;
+        g.batch = n;
         g.active_mask = mask;
         g.x16 = xa;
         g.ldx = M->xw;
@@ -783,7 +797,7 @@ void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_
         g.ldo = M->xw;
         vx_record(vx_launch_bgemm(vx_view(A, L.gate_up), g, VX_EPI_SWIGLU, st));
         std::memset(&g, 0, sizeof(g));
-        g.batch = batch;
+        g.batch = n;
         g.active_mask = mask;
         g.x16 = xb;
         g.ldx = M->xw;
@@ -794,10 +808,10 @@ void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_
         g.pstride = pstride;
         vx_record(vx_launch_bgemm(vx_view(A, L.down), g, VX_EPI_RESID, st));
     }
-    vx_record(vx_launch_bnorm(h, H, M->ksplit_down > 1 ? part_r : nullptr, M->ksplit_down, pstride, vecp(M->final_norm),
-                              H, c.rms_norm_eps, xa, M->xw, batch, mask, st));
+    vx_record(vx_launch_bnorm(h, H, M->ksplit_down > 1 ? part_r : nullptr, M->ksplit_down, pstride,
+                              vecp(M->final_norm), H, c.rms_norm_eps, xa, M->xw, n, mask, st));
     std::memset(&g, 0, sizeof(g));
-    g.batch = batch;
+    g.batch = n;
     g.active_mask = mask;
     g.x16 = xa;
     g.ldx = M->xw;
@@ -806,9 +820,52 @@ void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_
     g.cand_v = (float*)(act + M->a_bcand_v);
     g.cand_i = (uint32_t*)(act + M->a_bcand_i);
     vx_record(vx_launch_bgemm(vx_view(A, M->head), g, VX_EPI_ARGMAX, st));
-    vx_record(vx_launch_bfinalize(g.cand_v, g.cand_i, M->head_bwgs, states, A->host_pinned_ring,
-                                  (const uint32_t*)(act + M->a_bprompt), (const uint32_t*)(act + M->a_bplen),
-                                  c.max_seq_len, batch, mask, st));
+}
+
+}  // namespace
+
+// One decode step of sequences 0 .. batch-1, each at its own state (step, token): the weights are
+// read once per step for all of them; then the argmax of every sequence.
+void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_t mask, hipStream_t st) {
+    if (!A || !A->model || A->model->batch < 2 || batch == 0 || batch > A->model->batch) {
+        if (!g_last_error) g_last_error = VELOX_HIP_EINVAL;
+        return;
+    }
+    const VeloxHipModel* M = A->model;
+    uint8_t* act = A->activation_arena;
+    VeloxDecodeState* states = (VeloxDecodeState*)(act + M->a_bstate);
+    vx_rows_forward(A, states, batch, mask, false, st);
+    vx_record(vx_launch_bfinalize((const float*)(act + M->a_bcand_v), (const uint32_t*)(act + M->a_bcand_i),
+                                  M->head_bwgs, states, A->host_pinned_ring, (const uint32_t*)(act + M->a_bprompt),
+                                  (const uint32_t*)(act + M->a_bplen), M->cfg.max_seq_len, batch, mask, st));
+}
+
+// Prompt positions [pos0, pos0 + n_tokens) of sequence 0 in chunks of up to prefill_chunk rows.
+int velox_hip_prefill_batch(VeloxHipArena* A, uint64_t pos0, uint32_t n_tokens, uint64_t mask, hipStream_t st) {
+    if (!A || !A->model) return VELOX_HIP_EINVAL;
+    const VeloxHipModel* M = A->model;
+    const uint32_t chunk = M->cfg.prefill_chunk;
+    if (chunk < 2 || n_tokens == 0 || pos0 + n_tokens > M->cfg.max_seq_len) return VELOX_HIP_EINVAL;
+    uint8_t* act = A->activation_arena;
+    VeloxDecodeState* rows = (VeloxDecodeState*)(act + M->a_prows);
+    const uint32_t* prompt = (const uint32_t*)(act + M->a_prompt);
+    const int before = g_last_error;
+    for (uint32_t done = 0; done < n_tokens;) {
+        const uint32_t n = n_tokens - done < chunk ? n_tokens - done : chunk;
+        vx_record(vx_launch_prefill_rows(rows, n, pos0 + done, prompt, mask, st));
+        vx_rows_forward(A, rows, n, mask, true, st);
+        vx_record(vx_launch_prefill_finalize((const float*)(act + M->a_bcand_v), (const uint32_t*)(act + M->a_bcand_i),
+                                             M->head_bwgs, rows, n, A->host_pinned_ring,
+                                             (VeloxDecodeState*)(act + M->a_state), prompt,
+                                             (const uint32_t*)(act + M->a_plen), mask, st));
+        done += n;
+    }
+    if (!before && g_last_error) {
+        const int e = g_last_error;
+        g_last_error = 0;
+        return e;
+    }
+    return VELOX_HIP_OK;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1129,6 +1186,10 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
     const uint32_t B = opt->batch > 1 ? opt->batch : 1u;
     if (B > 32 || (B > 1 && opt->prompt_tokens)) return VELOX_HIP_EINVAL;
     if (B > 1) cfg.max_batch = B;
+    const bool batched_prefill = opt->prefill_chunk > 1;
+    // (the batched prefill reads its tokens from the staged prompt at their positions: no context)
+    if (batched_prefill && (B > 1 || opt->prefill_chunk > 32 || base)) return VELOX_HIP_EINVAL;
+    if (batched_prefill) cfg.prefill_chunk = opt->prefill_chunk;
     if (cfg.max_seq_len < total) return VELOX_HIP_EINVAL;
     VeloxHipModel* M = nullptr;
     rc = velox_hip_model_create(&cfg, &M);
@@ -1195,10 +1256,13 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
     };
     if (!rc) {
         hipEventRecord(e0, st);
-        for (uint32_t p = 0; p < opt->prompt_len; ++p) one_step();
+        if (batched_prefill) rc = velox_hip_prefill_batch(&A, base, opt->prompt_len, 1ULL, st);
+        else
+            for (uint32_t p = 0; p < opt->prompt_len; ++p) one_step();
         hipEventRecord(e1, st);
-        for (uint32_t w = 0; w < opt->warmup; ++w) one_step();
-        rc = (int)hipStreamSynchronize(st);
+        for (uint32_t w = 0; w < opt->warmup && !rc; ++w) one_step();
+        const int e = (int)hipStreamSynchronize(st);
+        if (!rc) rc = e;
     }
     if (!rc) {
         // timed region: synchronized on both sides, device time from events on the same stream

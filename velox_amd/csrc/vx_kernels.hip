@@ -504,12 +504,8 @@ __global__ __launch_bounds__(256) void vx_argmax_finalize_kernel(const float* ca
 
 // KV cache of one layer (and sequence), bf16: the K plane [hkv][s_cap][D] row-major, and the V
 // plane [hkv][s_cap / 32][D][32]: per block of 32 positions, dimension-major, the 32 positions of
-// one dimension in the slot order vx_vslot gives. s_cap is the position capacity rounded up to 32.
-// Slot of position r (0..31) of a V block: the P.V MFMA's lane group j supplies, as its 8
-// K-elements, positions 4j..4j+3 and 16+4j..16+4j+3 -- the scores that the K.Q^T MFMA leaves in
-// lane group j for the block's two 16-position halves -- so slot 8j + 4 half + i holds position
-// 16 half + 4j + i, and one 16-byte load gives a lane its 8 values.
-__device__ __forceinline__ uint32_t vx_vslot(uint32_t r) { return 8u * ((r & 15u) >> 2) + 4u * (r >> 4) + (r & 3u); }
+// one dimension in the slot order vx_vslot (vx_common.h) gives, so one 16-byte load gives a P.V
+// lane its 8 values. s_cap is the position capacity rounded up to 32.
 
 typedef __bf16 vx_bf8 __attribute__((ext_vector_type(8)));
 typedef float vx_af4 __attribute__((ext_vector_type(4)));
@@ -624,9 +620,10 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     const uint64_t step = a.state ? a.state[bq].step : (uint64_t)a.fixed_pos;
     const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;  // safe_step clamp
-    const uint32_t t1 = min(pos, t0 + chunk);                 // cached positions [t0, t1)
+    // cached positions [t0, t1): below pos, or up to pos when a prefill chunk appended its rows
+    const uint32_t t1 = min(a.prefill ? pos + 1u : pos, t0 + chunk);
     const uint32_t n_chunks = t1 > t0 ? (t1 - t0 + 31u) >> 5 : 0u;
-    const bool has_new = t0 <= pos && pos < t0 + chunk;       // this split owns the new position
+    const bool has_new = !a.prefill && t0 <= pos && pos < t0 + chunk;  // this split folds in the new position
     const float2* rp = a.rope + (size_t)pos * HALF;
     float2 rcs[RP];
 #pragma unroll
@@ -663,7 +660,7 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     }
     if (tid < D) vn_s[tid] = vx_f32_to_bf16_bits(vnew);
     __syncthreads();
-    if (sp == 0) {
+    if (sp == 0 && !a.prefill) {
         const uint16_t* vblk = Vc + (size_t)(pos >> 5) * D * 32 + vx_vslot(pos & 31u);
         for (int d = tid; d < D; d += NT) {
             Kc[(size_t)pos * D + d] = kn_s[d];

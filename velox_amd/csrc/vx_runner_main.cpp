@@ -5,7 +5,10 @@
 //
 //   velox_hip_runner [--model llama3_8b] [--weights synthetic|FILE.gguf] [--tokens 1,2,3 | --prompt-len N]
 //                    [--context-len N] [--steps N] [--warmup N] [--seed S] [--layers L]
-//                    [--no-cuda-graph] [--verbose]
+//                    [--prefill-chunk N] [--no-cuda-graph] [--verbose]
+//
+// --prefill-chunk N (2..32) prefills the prompt N positions per batched step (one weight pass per
+// chunk) instead of the reference's one decode step per prompt token; TTFT reports either.
 //
 // Weights are the seeded synthetic Q4_0 model (`--weights synthetic`, what src/cli.rs:654 passes
 // through) or a GGUF Q4_0 checkpoint (`--weights FILE.gguf`, whose metadata then defines the model,
@@ -21,7 +24,7 @@
 int main(int argc, char** argv) {
     std::string model = "llama3_8b", weights;
     std::vector<uint32_t> tokens;
-    uint32_t prompt_len = 128, steps = 32, warmup = 0, layers = 0, context_len = 0;
+    uint32_t prompt_len = 128, steps = 32, warmup = 0, layers = 0, context_len = 0, prefill_chunk = 0;
     uint64_t seed = 1234;
     bool graph = true, verbose = false;
     for (int i = 1; i < argc; ++i) {
@@ -53,6 +56,13 @@ int main(int argc, char** argv) {
         else if (!std::strcmp(a, "--warmup")) warmup = (uint32_t)std::atoi(next());
         else if (!std::strcmp(a, "--seed")) seed = std::strtoull(next(), nullptr, 10);
         else if (!std::strcmp(a, "--layers")) layers = (uint32_t)std::atoi(next());
+        else if (!std::strcmp(a, "--prefill-chunk")) {
+            prefill_chunk = (uint32_t)std::atoi(next());
+            if (prefill_chunk < 2 || prefill_chunk > 32) {
+                std::fprintf(stderr, "Error: --prefill-chunk takes 2..32 positions\n");
+                return 1;
+            }
+        }
         else if (!std::strcmp(a, "--no-cuda-graph") || !std::strcmp(a, "--no-graph")) graph = false;
         else if (!std::strcmp(a, "--verbose")) verbose = true;
         else if (!std::strcmp(a, "--weights")) {
@@ -100,6 +110,7 @@ int main(int argc, char** argv) {
     opt.prompt_tokens = tokens.empty() ? nullptr : tokens.data();
     opt.context_len = context_len;
     opt.weights_path = weights.empty() ? nullptr : weights.c_str();
+    opt.prefill_chunk = context_len ? 0 : prefill_chunk;
     std::vector<uint32_t> out(prompt_len + warmup + opt.steps + 8);
     VeloxHipRunReport rep;
     const int rc = velox_hip_run(&opt, out.data(), (uint32_t)out.size(), &rep);
@@ -122,7 +133,8 @@ int main(int argc, char** argv) {
         std::printf("Model                  : %s (GGUF Q4_0)\n", weights.c_str());
         std::printf("Weight Load            : %.2f ms\n", rep.load_ms);
     }
-    std::printf("TTFT (Prefill Latency) : %.3f ms\n", rep.prefill_ms);
+    std::printf("TTFT (Prefill Latency) : %.3f ms (%u prompt tokens, %s)\n", rep.prefill_ms, prompt_len,
+                opt.prefill_chunk ? "batched prefill" : "token by token");
     std::printf("Decode Latency (%u tok): %.3f ms (%.2f tok/s, %.3f ms/tok)\n", opt.steps, rep.decode_ms, rep.tok_per_s,
                 rep.decode_ms / opt.steps);
     std::printf("Achieved HBM Bandwidth : %.1f GB/s (%.2f%% of 8000 GB/s)\n", rep.hbm_gbps, rep.hbm_gbps / 80.0);

@@ -30,7 +30,7 @@ def gguf_config(path: str, max_seq_len: int = 0) -> L.ModelConfig:
 
 
 def make_config(model, max_seq_len: int = 0, num_layers: int = 0, attn_splits: int = 0,
-                max_batch: int = 0) -> L.ModelConfig:
+                max_batch: int = 0, prefill_chunk: int = 0) -> L.ModelConfig:
     """A builtin config by name, a GGUF file (path ending in .gguf), or a dict of ModelConfig
     fields (custom shapes for tests)."""
     if isinstance(model, str) and model.endswith(".gguf"):
@@ -52,15 +52,17 @@ def make_config(model, max_seq_len: int = 0, num_layers: int = 0, attn_splits: i
         cfg.attn_splits = attn_splits
     if max_batch:
         cfg.max_batch = max_batch
+    if prefill_chunk:
+        cfg.prefill_chunk = prefill_chunk
     return cfg
 
 
 class HipDecodeEngine:
     def __init__(self, model, seed: int = 0, sigma: float = 0.02, norm_sigma: float = 0.0,
                  max_seq_len: int = 0, num_layers: int = 0, attn_splits: int = 0, synthesize: bool = True,
-                 max_batch: int = 0):
+                 max_batch: int = 0, prefill_chunk: int = 0):
         self.lib = L.load()
-        self.cfg = make_config(model, max_seq_len, num_layers, attn_splits, max_batch)
+        self.cfg = make_config(model, max_seq_len, num_layers, attn_splits, max_batch, prefill_chunk)
         self._model = C.c_void_p()
         L.check(self.lib.velox_hip_model_create(C.byref(self.cfg), C.byref(self._model)), "model_create")
         self.arena = L.Arena()
@@ -132,6 +134,22 @@ class HipDecodeEngine:
         self.sync()
         self.read_logits()
         return int(self.arena.host_pinned_ring[pos & (L.RING_SIZE - 1)])
+
+    def prefill_batch(self, pos0: int, n_tokens: int) -> None:
+        """Positions [pos0, pos0 + n_tokens) of the staged prompt as batched chunks of
+        cfg.prefill_chunk rows (the token-by-token prefill of velox_cuda_runner.cu:493-512 in one
+        weight pass per chunk); leaves the state where that many prefill steps would."""
+        L.check(self.lib.velox_hip_prefill_batch(C.byref(self.arena), int(pos0), int(n_tokens), 1, None),
+                "prefill_batch")
+        self.sync()
+
+    def chunk_logits(self, n_rows: int) -> np.ndarray:
+        """The last prefill chunk's logits, one row per position."""
+        lo = C.c_uint64()
+        L.check(self.lib.velox_hip_model_batch_layout(self._model, None, C.byref(lo), None))
+        out = np.empty((n_rows, self.vocab), np.float32)
+        L.memcpy_dtoh(out.ctypes.data, self.arena.activation_arena + lo.value, out.nbytes)
+        return out
 
     def graph_step(self) -> None:
         """One decode step driven by the device state (no host round trip)."""
@@ -224,18 +242,21 @@ class HipBatchEngine(HipDecodeEngine):
 def run(model: str = "llama3_8b", prompt_len: int = 128, warmup: int = 5, steps: int = 251, seed: int = 1234,
         sigma: float = 0.02, norm_sigma: float = 0.0, use_graph: bool = True, num_layers: int = 0,
         max_seq_len: int = 0, max_tokens: int = 1024, kernel_passes: int = 0,
-        prompt: list[int] | None = None, context_len: int = 0, batch: int = 1) -> tuple[dict, list[int]]:
+        prompt: list[int] | None = None, context_len: int = 0, batch: int = 1,
+        prefill_chunk: int = 0) -> tuple[dict, list[int]]:
     """The C++ runner flow (velox_hip_run): synthesize, capture, prefill, timed decode. `prompt`
     replaces the seeded random prompt of `prompt_len` ids; `context_len` > 0 starts from a seeded
     context of that many positions already in the KV cache (then prompt_len must be 1). Returned
-    tokens are ring entries, ring[p] = argmax after position p, for the last positions run."""
+    tokens are ring entries, ring[p] = argmax after position p, for the last positions run.
+    `prefill_chunk` > 1 prefills the prompt as batched chunks of that many positions."""
     lib = L.load()
     ptoks = None
     if prompt is not None:
         prompt_len = len(prompt)
         ptoks = (C.c_uint32 * prompt_len)(*prompt)
     opt = L.RunOptions(model.encode(), max_seq_len, prompt_len, warmup, steps, seed, sigma, norm_sigma,
-                       int(use_graph), num_layers, kernel_passes, 0, ptoks, context_len, batch)
+                       int(use_graph), num_layers, kernel_passes, 0, ptoks, context_len, batch, None,
+                       prefill_chunk)
     rep = L.RunReport()
     toks = (C.c_uint32 * max_tokens)()
     rc = lib.velox_hip_run(C.byref(opt), toks, max_tokens, C.byref(rep))
