@@ -188,8 +188,10 @@ int velox_hip_fill_kv_seq(VeloxHipArena* a, uint32_t layer, uint32_t seq, uint32
 void velox_hip_decode_batch_graph_step(VeloxHipArena* ctx, uint32_t batch, uint64_t active_mask, hipStream_t stream);
 
 /* ---- batched prefill (replaces the token-by-token prefill loop of velox_cuda_runner.cu:493-512
- *      for a prompt staged with velox_hip_set_prompt; the runtime form of the DSL's chunked_prefill
- *      scope and its chunk_size, src/ast.rs:632-654; arena planned with prefill_chunk > 1) ----
+ *      and the K2 runner's velox_batched_prefill_q4, velox_cuda_runner_k2.cu:1614-1711, which takes
+ *      at most 16 tokens in one pass and falls back to sequential decode beyond; the runtime form of
+ *      the DSL's chunked_prefill scope and its chunk_size, src/ast.rs:632-654; arena planned with
+ *      prefill_chunk > 1) ----
  * Positions [pos0, pos0 + n_tokens) of the staged prompt run in chunks of up to prefill_chunk
  * positions, each chunk as the rows of one batched step (the weights are read once per chunk):
  * every row's K/V row goes into the single-sequence KV cache, then each row attends over
@@ -255,6 +257,23 @@ int velox_hip_argmax_f32(const float* d_x, uint32_t n, uint32_t* d_out, hipStrea
 int velox_hip_gemm_q4_0_batch(const VeloxHipQ4Matrix* m, const uint16_t* d_x16, uint32_t batch, uint32_t ldx,
                               const float* d_bias, float* d_y, uint32_t ldy, uint16_t* d_out16, uint32_t ldo,
                               int mode, hipStream_t stream);
+/* The batched GEMM's MFMA operand layout ("M-layout"), a second copy of a tiled matrix that arenas
+ * planned for more than one batched row keep for every matrix: 16-row tiles (paired: gate tile u at
+ * 2u, up tile u at 2u + 1) x groups of four blocks; per (tile, group) 64 words of 16 bytes, lane l
+ * holding dword l / 16 (elements 8(l/16) .. +7) of blocks 4j .. 4j+3 of row l % 16; fp16 scales
+ * [tile][group][row][4]. _bytes gives the sizes, _mlayout builds the copy from the tiled matrix. */
+int velox_hip_q4_mlayout_bytes(const VeloxHipQ4Matrix* m, uint64_t* code_bytes, uint64_t* scale_bytes);
+int velox_hip_q4_mlayout(const VeloxHipQ4Matrix* m, void* d_codes, void* d_scales, hipStream_t stream);
+/* velox_hip_gemm_q4_0_batch over an M-layout copy (the batched decode and prefill steps' GEMM).
+ * Activations: element k of row m at d_x16[m * ldx + (k / 32) * xbs + k % 32] -- row-major with
+ * xbs = 32 (0 means 32), or block-major [k / 32][rows][32] with ldx = 32, xbs = 32 * rows, the layout
+ * the batched steps use (one operand load is 1 KiB contiguous); d_out16 (SWIGLU) likewise with
+ * (ldo, obs). ksplit 1..8 splits K over workgroup rows (STORE and RESIDUAL), the partials going
+ * through d_part [ksplit][batch][ldy] and summed in split order (+ bias for STORE) into y. */
+int velox_hip_gemm_q4_0_batch_m(const VeloxHipQ4Matrix* m, const void* d_mcodes, const void* d_mscales,
+                                const uint16_t* d_x16, uint32_t batch, uint32_t ldx, uint32_t xbs, const float* d_bias,
+                                float* d_y, uint32_t ldy, uint16_t* d_out16, uint32_t ldo, uint32_t obs, int mode,
+                                uint32_t ksplit, float* d_part, hipStream_t stream);
 /* y = rmsnorm(x) * w (src/runtime.rs:588-601). */
 int velox_hip_rmsnorm(const float* d_x, const float* d_w, uint32_t n, float eps, float* d_y, hipStream_t stream);
 /* Decode attention for one layer at position pos: RoPE on q and the new k (table cos/sin of

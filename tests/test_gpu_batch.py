@@ -149,3 +149,163 @@ def test_batch_run_graph_matches_eager(oracle):
     gpu.sync()
     assert [gpu.ring_seq(0, p) for p in range(P + n - 1)] == toks[:P + n - 1]
     gpu.close()
+
+
+# ---- the batched GEMM over the MFMA-layout copy (the batched decode and prefill steps' GEMM) -------
+def _tiled_dwords(blocks: np.ndarray, k: int) -> tuple[np.ndarray, np.ndarray]:
+    """GGML Q4_0 blocks [n][k/32][18] -> per block the tiled layout's 4 code dwords (dword w: elements
+    8w..8w+7, element e at bits 8 (e % 4) + 4 (e // 4)) and the fp16 scale bits."""
+    n = blocks.shape[0] if blocks.ndim == 3 else blocks.size // (k // 32 * 18)
+    b = blocks.reshape(n, k // 32, 18)
+    d = b[:, :, 0].astype(np.uint16) | (b[:, :, 1].astype(np.uint16) << 8)
+    qs = b[:, :, 2:].astype(np.uint32)
+    q = np.concatenate([qs & 15, qs >> 4], axis=2)  # element el of the block
+    dw = np.zeros((n, k // 32, 4), np.uint32)
+    for w in range(4):
+        for e in range(8):
+            dw[:, :, w] |= q[:, :, 8 * w + e] << (8 * (e % 4) + 4 * (e // 4))
+    return dw, d
+
+
+def mlayout_reference(blocks, n, k, up_blocks=None):
+    """The M-layout restated: codes [tiles][groups][64][4] uint32, scales [tiles][groups][16][4] uint16."""
+    parts = [blocks] if up_blocks is None else [blocks, up_blocks]
+    nb = k // 32
+    ng = (nb + 3) // 4
+    t16 = (n + 15) // 16
+    tiles = t16 * len(parts)
+    codes = np.zeros((tiles, ng, 64, 4), np.uint32)
+    scales = np.zeros((tiles, ng, 16, 4), np.uint16)
+    for pi, blk in enumerate(parts):
+        dw, d = _tiled_dwords(blk, k)
+        for t in range(t16):
+            T = t * len(parts) + pi
+            for rho in range(16):
+                r = 16 * t + rho
+                if r >= n:
+                    continue
+                for j in range(ng):
+                    for bb in range(4):
+                        blkid = 4 * j + bb
+                        if blkid >= nb:
+                            continue
+                        scales[T, j, rho, bb] = d[r, blkid]
+                        for g in range(4):
+                            codes[T, j, rho + 16 * g, bb] = dw[r, blkid, g]
+    return codes, scales
+
+
+class MQ4:
+    """The M-layout copy of a TiledQ4 matrix."""
+
+    def __init__(self, hiplib, dev, t: TiledQ4):
+        cb, sb = C.c_uint64(), C.c_uint64()
+        L.check(hiplib.velox_hip_q4_mlayout_bytes(C.byref(t.m), C.byref(cb), C.byref(sb)))
+        self.codes = dev.empty(cb.value, np.uint8)
+        self.scales = dev.empty(sb.value, np.uint8)
+        L.check(hiplib.velox_hip_q4_mlayout(C.byref(t.m), self.codes.data_ptr(), self.scales.data_ptr(), None))
+
+
+@pytest.mark.parametrize("n,k,paired", [(100, 576, False), (40, 576, True), (33, 4096, False), (24, 3584, True)])
+def test_mlayout_matches_restatement(hiplib, oracle, dev, n, k, paired):
+    g = _weights(oracle, n, k, 31)
+    u = _weights(oracle, n, k, 32) if paired else None
+    t = TiledQ4(hiplib, dev, g, n, k, up_blocks=u)
+    mq = MQ4(hiplib, dev, t)
+    codes, scales = mlayout_reference(g, n, k, u)
+    assert np.array_equal(dev.get(mq.codes).view(np.uint32), codes.ravel())
+    assert np.array_equal(dev.get(mq.scales).view(np.uint16), scales.ravel())
+
+
+def _block_major(x: np.ndarray, k: int) -> np.ndarray:
+    """[rows][>= k] fp16 -> [k / 32][rows][32] (ldx 32, xbs 32 * rows)."""
+    rows = x.shape[0]
+    return np.ascontiguousarray(x[:, :k].reshape(rows, k // 32, 32).transpose(1, 0, 2))
+
+
+@pytest.mark.parametrize("n,k,batch,ks,bm", [(4608, 3584, 8, 1, 1), (4608, 3584, 32, 4, 1), (960, 576, 5, 1, 0),
+                                             (123, 4096, 17, 3, 1), (4096, 14336, 32, 8, 0), (64, 4096, 1, 2, 1),
+                                             (200, 1536, 16, 1, 0)])
+def test_gemm_m_store_and_residual(hiplib, oracle, dev, n, k, batch, ks, bm):
+    """Row-major (bm 0) and block-major (bm 1) activations; 1..8 K splits."""
+    rng = np.random.default_rng(n + k + batch + ks)
+    blocks = _weights(oracle, n, k, 600 + batch)
+    t = TiledQ4(hiplib, dev, blocks, n, k)
+    mq = MQ4(hiplib, dev, t)
+    deq = oracle.q4_0_dequant(blocks, k).astype(np.float64)
+    ldx, ldy = k + 8, n + 3
+    x = _x16(rng, batch, k, ldx)
+    bias = (0.1 * rng.standard_normal(n)).astype(np.float32)
+    if bm:
+        dx, ldx, xbs = dev.put(_block_major(x, k).view(np.int16)), 32, 32 * batch
+    else:
+        dx, xbs = dev.put(x.view(np.int16)), 32
+    db = dev.put(bias)
+    part = dev.empty(ks * batch * ldy)
+    scale = max(1.0, np.sqrt(k / 4096))
+    dy = dev.put(np.full((batch, ldy), 7.0, np.float32))
+    L.check(hiplib.velox_hip_gemm_q4_0_batch_m(C.byref(t.m), mq.codes.data_ptr(), mq.scales.data_ptr(), dx.data_ptr(),
+                                               batch, ldx, xbs, db.data_ptr(), dy.data_ptr(), ldy, None, 0, 0,
+                                               L.GEMV_STORE, ks, part.data_ptr(), None))
+    got = dev.get(dy).reshape(batch, ldy)
+    want = x[:, :k].astype(np.float64) @ deq.T + bias
+    assert rms(got[:, :n] - want) < 1e-5 * rms(want) * scale
+    assert np.all(got[:, n:] == 7.0)
+    y0 = rng.standard_normal((batch, ldy)).astype(np.float32)
+    dy = dev.put(y0)
+    L.check(hiplib.velox_hip_gemm_q4_0_batch_m(C.byref(t.m), mq.codes.data_ptr(), mq.scales.data_ptr(), dx.data_ptr(),
+                                               batch, ldx, xbs, None, dy.data_ptr(), ldy, None, 0, 0, L.GEMV_RESIDUAL,
+                                               ks, part.data_ptr(), None))
+    got = dev.get(dy).reshape(batch, ldy)
+    want = y0[:, :n].astype(np.float64) + x[:, :k].astype(np.float64) @ deq.T
+    assert rms(got[:, :n] - want) < 1e-5 * rms(want - y0[:, :n]) * scale
+    assert np.array_equal(got[:, n:], y0[:, n:])
+
+
+@pytest.mark.parametrize("F,H,batch,bm", [(1536, 576, 3, 0), (2048, 3584, 32, 1), (100, 576, 9, 0), (18944, 3584, 20, 1),
+                                          (96, 576, 16, 1)])
+def test_gemm_m_swiglu(hiplib, oracle, dev, F, H, batch, bm):
+    rng = np.random.default_rng(F + batch + 1)
+    g = _weights(oracle, F, H, 41)
+    u = _weights(oracle, F, H, 42)
+    t = TiledQ4(hiplib, dev, g, F, H, up_blocks=u)
+    mq = MQ4(hiplib, dev, t)
+    x = _x16(rng, batch, H, H)
+    Fp = (F + 31) // 32 * 32  # block-major output rows cover whole blocks
+    if bm:
+        dx, ldx, xbs = dev.put(_block_major(x, H).view(np.int16)), 32, 32 * batch
+        dout, ldo, obs = dev.empty(batch * Fp, np.uint16), 32, 32 * batch
+    else:
+        dx, ldx, xbs = dev.put(x.view(np.int16)), H, 32
+        dout, ldo, obs = dev.empty(batch * F, np.uint16), F, 32
+    L.check(hiplib.velox_hip_gemm_q4_0_batch_m(C.byref(t.m), mq.codes.data_ptr(), mq.scales.data_ptr(), dx.data_ptr(),
+                                               batch, ldx, xbs, None, None, 0, dout.data_ptr(), ldo, obs,
+                                               L.GEMV_SWIGLU, 1, None, None))
+    raw = dev.get(dout).view(np.float16)
+    if bm:
+        raw = raw.reshape(Fp // 32, batch, 32).transpose(1, 0, 2).reshape(batch, Fp)[:, :F]
+    got = raw.reshape(batch, F).astype(np.float64)
+    xx = x.astype(np.float64)
+    gg = xx @ oracle.q4_0_dequant(g, H).astype(np.float64).T
+    uu = xx @ oracle.q4_0_dequant(u, H).astype(np.float64).T
+    want = gg / (1.0 + np.exp(-gg)) * uu
+    assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-3)) < 2e-3
+    assert rms(got - want) < 5e-4 * rms(want)
+
+
+def test_gemm_m_rejects_bad_arguments(hiplib, oracle, dev):
+    blocks = _weights(oracle, 64, 576, 9)
+    t = TiledQ4(hiplib, dev, blocks, 64, 576)
+    mq = MQ4(hiplib, dev, t)
+    dx, dy, part = dev.empty(33 * 576, np.uint16), dev.empty(33 * 64), dev.empty(9 * 33 * 64)
+    cases = [(0, 576, 1, part), (33, 576, 1, part), (4, 500, 1, part), (4, 576, 9, part), (4, 576, 2, None),
+             (4, 576, 6, part)]  # 576 = 18 blocks = 5 groups: at most 5 splits
+    for batch, ldx, ks, p in cases:
+        assert hiplib.velox_hip_gemm_q4_0_batch_m(C.byref(t.m), mq.codes.data_ptr(), mq.scales.data_ptr(),
+                                                  dx.data_ptr(), batch, ldx, 32, None, dy.data_ptr(), 64, None, 0, 0,
+                                                  L.GEMV_STORE, ks, p.data_ptr() if p is not None else None,
+                                                  None) == L.EINVAL, (batch, ldx, ks)
+    # block-major rows must fit inside a block: xbs >= batch * ldx
+    assert hiplib.velox_hip_gemm_q4_0_batch_m(C.byref(t.m), mq.codes.data_ptr(), mq.scales.data_ptr(), dx.data_ptr(),
+                                              8, 32, 32 * 7, None, dy.data_ptr(), 64, None, 0, 0, L.GEMV_STORE, 1,
+                                              None, None) == L.EINVAL

@@ -154,6 +154,10 @@ _SIGS = {
     "velox_hip_fill_normal": (_I, [_P, _U64, _U64, _U64, _F, _F, _P]),
     "velox_hip_gemv_q4_0": (_I, [C.POINTER(Q4Matrix), _P, _P, _F, _P, _P, _P, _I, _P]),
     "velox_hip_gemm_q4_0_batch": (_I, [C.POINTER(Q4Matrix), _P, _U32, _U32, _P, _P, _U32, _P, _U32, _I, _P]),
+    "velox_hip_q4_mlayout_bytes": (_I, [C.POINTER(Q4Matrix), C.POINTER(_U64), C.POINTER(_U64)]),
+    "velox_hip_q4_mlayout": (_I, [C.POINTER(Q4Matrix), _P, _P, _P]),
+    "velox_hip_gemm_q4_0_batch_m": (_I, [C.POINTER(Q4Matrix), _P, _P, _P, _U32, _U32, _U32, _P, _P, _U32, _P, _U32,
+                                         _U32, _I, _U32, _P, _P]),
     "velox_hip_lm_head_argmax": (_I, [C.POINTER(Q4Matrix), _P, _P, _F, _P, _P, _P]),
     "velox_hip_argmax_f32": (_I, [_P, _U32, _P, _P]),
     "velox_hip_rmsnorm": (_I, [_P, _P, _U32, _F, _P, _P]),

@@ -104,7 +104,7 @@ __global__ __launch_bounds__(kBThreads) void vx_bgemm_q4_kernel(VxBGemmArgs a) {
             const int i = tid + u * kBThreads;                                                      \
             const uint32_t m = min((uint32_t)(i / XC), m_last);                                     \
             const uint32_t e = min((it_) * (uint32_t)(S * 32) + (uint32_t)(i % XC) * 8u, e_last);   \
-            xr[u] = *(const vx_bu4*)(a.x16 + (size_t)m * a.ldx + e);                                \
+            xr[u] = *(const vx_bu4*)(a.x16 + (size_t)m * a.ldx + (size_t)(e >> 5) * a.xbs + (e & 31u)); \
         }                                                                                           \
     } while (0)
     VX_BGEMM_LOAD(it_begin);
@@ -157,7 +157,8 @@ __global__ __launch_bounds__(kBThreads) void vx_bgemm_q4_kernel(VxBGemmArgs a) {
                 const uint32_t m = (uint32_t)(16 * mt + 4 * g + i);
                 if (r < R / 2 && ok && m < a.batch) {
                     const float gt = acc[mt][i];
-                    a.out16[(size_t)m * a.ldo + j] = __half_as_ushort(__float2half((gt / (1.0f + expf(-gt))) * up));
+                    a.out16[(size_t)m * a.ldo + (size_t)(j >> 5) * a.obs + (j & 31u)] =
+                        __half_as_ushort(__float2half((gt / (1.0f + expf(-gt))) * up));
                 }
             }
     } else {
@@ -259,7 +260,9 @@ hipError_t vx_launch_bgemm(const VxMat& m, const VxBGemmArgs& a0, int epi, hipSt
     a.k = m.k;
     a.n_tiles = m.n_tiles;
     a.n_iter = m.n_iter;
-    if (m.k == 0 || (m.k & 31u) || (a.ldx & 7u) || !a.x16) return hipErrorInvalidValue;
+    if (m.k == 0 || (m.k & 31u) || (a.ldx & 7u) || (a.xbs & 7u) || !a.x16 || !vx_x_layout_ok(m.k, a.ldx, a.xbs, a.batch))
+        return hipErrorInvalidValue;
+    if (epi == VX_EPI_SWIGLU && !vx_x_layout_ok(m.n, a.ldo, a.obs, a.batch)) return hipErrorInvalidValue;
     if ((epi == VX_EPI_SWIGLU) != (m.paired != 0)) return hipErrorInvalidValue;
     if (a.ksplit > 1u && (epi != VX_EPI_RESID || !a.part || a.ksplit > m.n_iter || a.ksplit > kBNormMaxParts ||
                           a.pstride < (uint64_t)a.batch * a.ldy))
@@ -323,7 +326,7 @@ __global__ __launch_bounds__(256) void vx_bembed_kernel(VxMat m, const VeloxDeco
 template <int NV>
 __global__ __launch_bounds__(1024) void vx_bnorm_kernel(float* h, uint32_t ldh, const float* parts, uint32_t nparts,
                                                         uint64_t pstride, const float* g, uint32_t k, float eps,
-                                                        uint16_t* x16, uint32_t ldx, uint64_t mask) {
+                                                        uint16_t* x16, uint32_t ldx, uint32_t xbs, uint64_t mask) {
     if ((mask & 1ULL) == 0ULL) return;
     __shared__ float red[16];
     const uint32_t b = blockIdx.x, k4 = k >> 2;
@@ -379,7 +382,8 @@ __global__ __launch_bounds__(1024) void vx_bnorm_kernel(float* h, uint32_t ldh, 
             o[2] = __half_as_ushort(__float2half((v[j].z * inv) * gg.z));
             o[3] = __half_as_ushort(__float2half((v[j].w * inv) * gg.w));
         }
-        *(uint2*)(x16 + (size_t)b * ldx + 4u * i) = make_uint2(o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16));
+        *(uint2*)(x16 + (size_t)b * ldx + (size_t)(i >> 3) * xbs + 4u * (i & 7u)) =
+            make_uint2(o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16));
     }
 }
 
@@ -387,7 +391,8 @@ __global__ __launch_bounds__(1024) void vx_bnorm_kernel(float* h, uint32_t ldh, 
 // the fp16 operand of the o_proj GEMM.
 template <int D>
 __global__ __launch_bounds__(D) void vx_bmerge_kernel(const float* part_o, const float* part_ml, uint32_t hq,
-                                                      uint32_t splits, uint16_t* x16, uint32_t ldx, uint64_t mask) {
+                                                      uint32_t splits, uint16_t* x16, uint32_t ldx, uint32_t xbs,
+                                                      uint64_t mask) {
     if ((mask & 1ULL) == 0ULL) return;
     __shared__ float s_w[64];
     const int tid = threadIdx.x;
@@ -409,7 +414,8 @@ __global__ __launch_bounds__(D) void vx_bmerge_kernel(const float* part_o, const
     __syncthreads();
     float acc = 0.0f;
     for (uint32_t j = 0; j < splits; ++j) acc += s_w[j] * po[j * D + tid];
-    x16[b * ldx + h * D + tid] = __half_as_ushort(__float2half(acc));
+    const size_t e = h * D + tid;
+    x16[b * ldx + (e >> 5) * xbs + (e & 31u)] = __half_as_ushort(__float2half(acc));
 }
 
 // Per sequence: the argmax over the LM head's workgroup candidates (lowest index on ties), the
@@ -575,32 +581,42 @@ hipError_t vx_launch_bembed(const VxMat& m, const VeloxDecodeState* states, uint
     return hipGetLastError();
 }
 
+// Activation operand layout check: row-major (xbs 32, rows ldx >= k apart) or block-major (rows
+// ldx >= 32 apart inside blocks of xbs >= batch * ldx elements), with 8-byte aligned 4-element runs.
+bool vx_x_layout_ok(uint32_t k, uint32_t ldx, uint32_t xbs, uint32_t batch) {
+    if ((ldx & 3u) || (xbs & 3u) || xbs < 32u) return false;
+    if (batch <= 1u) return true;  // one row: any row stride
+    return xbs == 32u ? ldx >= k : (ldx >= 32u && (uint64_t)xbs >= (uint64_t)batch * ldx);
+}
+
 hipError_t vx_launch_bnorm(float* h, uint32_t ldh, const float* parts, uint32_t nparts, uint64_t pstride, const float* g,
-                           uint32_t k, float eps, uint16_t* x16, uint32_t ldx, uint32_t batch, uint64_t mask,
-                           hipStream_t st) {
-    // float4 rows: k, ldh, ldx and pstride multiples of 4 (16-byte h and parts rows, 8-byte x16 rows)
-    if (k == 0 || (k & 3u) || (ldh & 3u) || (ldx & 3u) || ldh < k || ldx < k) return hipErrorInvalidValue;
+                           uint32_t k, float eps, uint16_t* x16, uint32_t ldx, uint32_t xbs, uint32_t batch,
+                           uint64_t mask, hipStream_t st) {
+    // float4 rows: k, ldh and pstride multiples of 4 (16-byte h and parts rows, 8-byte x16 runs)
+    if (k == 0 || (k & 3u) || (ldh & 3u) || ldh < k || !vx_x_layout_ok(k, ldx, xbs, batch)) return hipErrorInvalidValue;
     if (parts && (nparts == 0 || nparts > kBNormMaxParts || (pstride & 3u))) return hipErrorInvalidValue;
     if (!parts) nparts = 0;
     const dim3 grid(batch), block(1024);
     if (k <= 4096u)
-        hipLaunchKernelGGL((vx_bnorm_kernel<1>), grid, block, 0, st, h, ldh, parts, nparts, pstride, g, k, eps, x16, ldx, mask);
+        hipLaunchKernelGGL((vx_bnorm_kernel<1>), grid, block, 0, st, h, ldh, parts, nparts, pstride, g, k, eps, x16, ldx,
+                           xbs, mask);
     else if (k <= 8192u)
-        hipLaunchKernelGGL((vx_bnorm_kernel<2>), grid, block, 0, st, h, ldh, parts, nparts, pstride, g, k, eps, x16, ldx, mask);
+        hipLaunchKernelGGL((vx_bnorm_kernel<2>), grid, block, 0, st, h, ldh, parts, nparts, pstride, g, k, eps, x16, ldx,
+                           xbs, mask);
     else  // rows past 8192 would need more than 64 registers of partials per thread
         return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
 hipError_t vx_launch_bmerge(const float* part_o, const float* part_ml, uint32_t hq, uint32_t d, uint32_t splits,
-                            uint16_t* x16, uint32_t ldx, uint32_t batch, uint64_t mask, hipStream_t st) {
-    if (splits == 0 || splits > 64) return hipErrorInvalidValue;
+                            uint16_t* x16, uint32_t ldx, uint32_t xbs, uint32_t batch, uint64_t mask, hipStream_t st) {
+    if (splits == 0 || splits > 64 || !vx_x_layout_ok(hq * d, ldx, xbs, batch)) return hipErrorInvalidValue;
     if (d == 64)
         hipLaunchKernelGGL((vx_bmerge_kernel<64>), dim3(hq, batch), dim3(64), 0, st, part_o, part_ml, hq, splits, x16,
-                           ldx, mask);
+                           ldx, xbs, mask);
     else if (d == 128)
         hipLaunchKernelGGL((vx_bmerge_kernel<128>), dim3(hq, batch), dim3(128), 0, st, part_o, part_ml, hq, splits,
-                           x16, ldx, mask);
+                           x16, ldx, xbs, mask);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

@@ -154,13 +154,15 @@ struct VxBGemmArgs {
     const uint4* codes;
     const uint16_t* scales;
     uint32_t n, k, n_tiles, n_iter, batch;
-    const uint16_t* x16;   // [batch][ldx] fp16
-    uint32_t ldx;
+    // fp16 activations: element k of row m at x16[m * ldx + (k / 32) * xbs + k % 32] -- row-major
+    // with xbs = 32, or block-major ([k / 32][rows][32]) with ldx = 32 and xbs = 32 * rows
+    const uint16_t* x16;
+    uint32_t ldx, xbs;
     const float* bias;     // STORE: + bias[n]
     float* y;              // STORE / ARGMAX: y[m][n] = ...; RESID: y[m][n] += ...   (row stride ldy)
     uint32_t ldy;
-    uint16_t* out16;       // SWIGLU: out16[m][j] = fp16(silu(gate) * up)          (row stride ldo)
-    uint32_t ldo;
+    uint16_t* out16;       // SWIGLU: out16[m * ldo + (j / 32) * obs + j % 32] = fp16(silu(gate) * up)
+    uint32_t ldo, obs;
     float* cand_v;         // ARGMAX: per (m, workgroup) candidates, [batch][gridDim.x]
     uint32_t* cand_i;
     uint64_t active_mask;
@@ -171,6 +173,27 @@ struct VxBGemmArgs {
     float* part;
     uint64_t pstride;
 };
+
+// A Q4_0 matrix in the MFMA operand layout of the batched GEMM (vx_mgemm.hip), a second copy of a
+// tiled matrix: 16-row tiles (paired: gate tile u at 2u, up tile u at 2u + 1) x groups of 4 blocks;
+// per (tile, group) 64 16-byte words, lane l = row (l % 16), dword l / 16 of blocks 4j .. 4j+3;
+// fp16 scales [tile][group][row][4].
+struct VxMMat {
+    const uint4* codes;
+    const uint2* scales;
+    uint32_t n, k, n_tiles, n_grp, paired;
+};
+void vx_mmat_shape(uint32_t n, uint32_t k, uint32_t paired, VxMMat& m);  // fills n, k, paired, n_tiles, n_grp
+uint64_t vx_mmat_code_bytes(const VxMMat& m);
+uint64_t vx_mmat_scale_bytes(const VxMMat& m);
+uint32_t vx_mgemm_grid(uint32_t n_tiles);  // workgroups of one grid row (also the ARGMAX candidate count)
+hipError_t vx_launch_mlayout(const VxMat& src, const VxMMat& dst, hipStream_t st);
+// Same arguments and epilogues as vx_launch_bgemm (codes/scales/n/k from `w`); ksplit > 1 is also
+// allowed for STORE, whose partials vx_launch_msum then sums (+ bias) into y.
+hipError_t vx_launch_mgemm(const VxMMat& w, const VxBGemmArgs& a, int epi, hipStream_t st);
+hipError_t vx_launch_msum(const float* part, uint32_t nparts, uint64_t pstride, const float* bias, float* y,
+                          uint32_t n, uint32_t ldy, uint32_t batch, uint32_t accumulate, uint64_t mask,
+                          hipStream_t st);
 
 // fp8 (e4m3fn) block-scaled GEMM of up to 32 rows of activations, on MFMA (vx_mla.hip). Weights
 // in 16-row x 64-column tiles of 1 KiB: lane l of tile (rt, kt) holds row 16 rt + l % 16, columns
@@ -218,10 +241,11 @@ hipError_t vx_launch_bembed(const VxMat& m, const VeloxDecodeState* states, uint
                             uint64_t mask, hipStream_t st);
 // parts != nullptr: h[b] += sum over s < nparts of parts[s * pstride + b * ldh] first (written back)
 hipError_t vx_launch_bnorm(float* h, uint32_t ldh, const float* parts, uint32_t nparts, uint64_t pstride, const float* g,
-                           uint32_t k, float eps, uint16_t* x16, uint32_t ldx, uint32_t batch, uint64_t mask,
-                           hipStream_t st);
+                           uint32_t k, float eps, uint16_t* x16, uint32_t ldx, uint32_t xbs, uint32_t batch,
+                           uint64_t mask, hipStream_t st);
+bool vx_x_layout_ok(uint32_t k, uint32_t ldx, uint32_t xbs, uint32_t batch);  // activation operand layout check
 hipError_t vx_launch_bmerge(const float* part_o, const float* part_ml, uint32_t hq, uint32_t d, uint32_t splits,
-                            uint16_t* x16, uint32_t ldx, uint32_t batch, uint64_t mask, hipStream_t st);
+                            uint16_t* x16, uint32_t ldx, uint32_t xbs, uint32_t batch, uint64_t mask, hipStream_t st);
 hipError_t vx_launch_bfinalize(const float* cand_v, const uint32_t* cand_i, uint32_t n, VeloxDecodeState* states,
                                uint32_t* rings, const uint32_t* prompts, const uint32_t* plens, uint32_t prompt_stride,
                                uint32_t batch, uint64_t mask, hipStream_t st);

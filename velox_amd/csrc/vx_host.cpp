@@ -36,6 +36,10 @@ namespace {
 struct VxMatPlan {
     uint64_t code_off = 0, scale_off = 0, code_bytes = 0, scale_bytes = 0;
     uint32_t n = 0, k = 0, s = 0, n_tiles = 0, n_iter = 0, paired = 0;
+    // second copy in the MFMA operand layout of the batched GEMM (arenas planned for more than one row)
+    bool has_m = false;
+    uint64_t mcode_off = 0, mscale_off = 0;
+    uint32_t m_tiles = 0, m_grp = 0;
 };
 
 struct VxLayerPlan {
@@ -55,6 +59,21 @@ uint32_t vx_bgemm_ksplit(const VxMatPlan& m) {
     }
     if (ks > 8u) ks = 8u;
     if (ks > m.n_iter) ks = m.n_iter;
+    return ks ? ks : 1u;
+}
+
+// K splits of a batched GEMM over the MFMA layout: enough grid rows for about 1024 workgroups (two
+// 16-row tiles each, its 4 waves splitting K again), at most 8 (the partials a batched RMSNorm or
+// the partial sum folds in) and at most one group of 4 blocks per split.
+uint32_t vx_mgemm_ksplit(const VxMatPlan& m) {
+    uint32_t ks = 0;
+    if (const char* env = std::getenv("VELOX_HIP_MGEMM_KSPLIT")) ks = (uint32_t)std::strtoul(env, nullptr, 10);  // tuning
+    if (ks == 0) {
+        const uint32_t wgs = vx_mgemm_grid(m.m_tiles);
+        ks = (1024u + wgs - 1u) / wgs;
+    }
+    if (ks > 8u) ks = 8u;
+    if (ks > m.m_grp) ks = m.m_grp;
     return ks ? ks : 1u;
 }
 
@@ -82,7 +101,12 @@ struct VeloxHipModel {
     uint64_t a_bpart_o = 0, a_bpart_ml = 0, a_blogits = 0, a_bcand_v = 0, a_bcand_i = 0;
     // K-split partials of the residual GEMMs (o_proj, down): [ksplit][batch][hidden]
     uint64_t a_bpart_r = 0;
-    uint32_t ksplit_o = 1, ksplit_down = 1;
+    uint32_t ksplit_o = 1, ksplit_down = 1, ksplit_qkv = 1;
+    bool mgemm = false;  // batched GEMMs over the MFMA-layout copies (else the LDS-staged tiled GEMM)
+    // fp16 activation operands: element k of row m at m * x_ld + (k / 32) * x_bs + k % 32 -- block-major
+    // [k / 32][16-row-padded rows][32] for the MFMA-layout GEMM (one operand load = 1 KiB contiguous),
+    // row-major [rows][xw] for the tiled GEMM
+    uint32_t x_ld = 0, x_bs = 32;
 };
 
 namespace {
@@ -125,6 +149,18 @@ void vx_place(VxMatPlan& p, uint64_t& code_cursor, uint64_t& scale_cursor) {
     scale_cursor = vx_align(scale_cursor + p.scale_bytes);
 }
 
+void vx_place_m(VxMatPlan& p, uint64_t& code_cursor, uint64_t& scale_cursor) {
+    VxMMat m;
+    vx_mmat_shape(p.n, p.k, p.paired, m);
+    p.has_m = true;
+    p.m_tiles = m.n_tiles;
+    p.m_grp = m.n_grp;
+    p.mcode_off = code_cursor;
+    p.mscale_off = scale_cursor;
+    code_cursor = vx_align(code_cursor + vx_mmat_code_bytes(m));
+    scale_cursor = vx_align(scale_cursor + vx_mmat_scale_bytes(m));
+}
+
 VxMat vx_view(const VeloxHipArena* a, const VxMatPlan& p) {
     VxMat m;
     m.codes = (const uint4*)(a->weight_arena + p.code_off);
@@ -136,6 +172,24 @@ VxMat vx_view(const VeloxHipArena* a, const VxMatPlan& p) {
     m.n_iter = p.n_iter;
     m.paired = p.paired;
     return m;
+}
+
+VxMMat vx_mview(const VeloxHipArena* a, const VxMatPlan& p) {
+    VxMMat m;
+    m.codes = (const uint4*)(a->weight_arena + p.mcode_off);
+    m.scales = (const uint2*)(a->weight_scales + p.mscale_off);
+    m.n = p.n;
+    m.k = p.k;
+    m.n_tiles = p.m_tiles;
+    m.n_grp = p.m_grp;
+    m.paired = p.paired;
+    return m;
+}
+
+// Rebuilds a matrix's MFMA-layout copy from its tiled layout (after a load or synthesis).
+hipError_t vx_build_m(const VeloxHipArena* a, const VxMatPlan& p, hipStream_t st) {
+    if (!p.has_m) return hipSuccess;
+    return vx_launch_mlayout(vx_view(a, p), vx_mview(a, p), st);
 }
 
 // KV cache of (layer, sequence): [layer][sequence][K | V][kv head][position][dim] bf16
@@ -271,6 +325,18 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
         vx_mat_layout(c.vocab_size, H, 0, 0, M->head);
         vx_place(M->head, cc, sc);
     }
+    // batched rows (sequences of a batched step, or positions of a prefill chunk): every matrix
+    // the batched GEMMs read gets its MFMA-layout copy
+    const uint32_t brows = c.max_batch > c.prefill_chunk ? c.max_batch : c.prefill_chunk;
+    if (brows > 1) {
+        for (VxLayerPlan& L : M->layers) {
+            vx_place_m(L.qkv, cc, sc);
+            vx_place_m(L.o, cc, sc);
+            vx_place_m(L.gate_up, cc, sc);
+            vx_place_m(L.down, cc, sc);
+        }
+        vx_place_m(M->head, cc, sc);  // (a tied head: its copy is made from the embedding table)
+    }
     M->final_norm = nc;
     nc = vx_align(nc + (uint64_t)H * 4);
     M->rope = nc;
@@ -332,24 +398,36 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
         uint32_t xw = H > qd ? H : qd;
         if (F > xw) xw = F;
         M->xw = (xw + 7u) & ~7u;
-        M->head_bwgs = vx_bgemm_grid(M->head.n_tiles, M->head.s);
+        const char* tiled = std::getenv("VELOX_HIP_BGEMM_TILED");  // A/B switch: the LDS-staged tiled GEMM
+        M->mgemm = M->head.has_m && !(tiled && tiled[0] == '1');
+        M->head_bwgs = M->mgemm ? vx_mgemm_grid(M->head.m_tiles) : vx_bgemm_grid(M->head.n_tiles, M->head.s);
         const uint64_t S = M->batch;  // per-sequence state, prompt length and prompt
         M->a_bstate = take(S * sizeof(VeloxDecodeState));
         M->a_bplen = take(S * 4);
         M->a_bprompt = take(S * c.max_seq_len * 4);
         M->a_bh = take(B * H * 4);
-        M->a_bxa = take(B * M->xw * 2);
-        M->a_bxb = take(B * M->xw * 2);
+        const uint64_t R16 = (B + 15u) / 16u * 16u;
+        M->x_ld = M->mgemm ? 32u : M->xw;
+        M->x_bs = M->mgemm ? (uint32_t)(32u * R16) : 32u;
+        M->a_bxa = take(R16 * M->xw * 2);
+        M->a_bxb = take(R16 * M->xw * 2);
         M->a_bqkv = take(B * (qd + 2 * kvd) * 4);
         M->a_bpart_o = take(B * c.num_heads * splits * D * 4);
         M->a_bpart_ml = take(B * c.num_heads * splits * 2 * 4);
         M->a_blogits = take(B * c.vocab_size * 4);
         M->a_bcand_v = take(B * M->head_bwgs * 4);
         M->a_bcand_i = take(B * M->head_bwgs * 4);
-        M->a_bpart_r = take(8 * B * H * 4);
+        // K-split partials: [8][rows][max(hidden, q/k/v width)]
+        M->a_bpart_r = take(8 * B * (H > qd + 2 * kvd ? H : qd + 2 * kvd) * 4);
         M->a_prows = take(B * sizeof(VeloxDecodeState));
-        M->ksplit_o = vx_bgemm_ksplit(M->layers[0].o);
-        M->ksplit_down = vx_bgemm_ksplit(M->layers[0].down);
+        if (M->mgemm) {
+            M->ksplit_qkv = vx_mgemm_ksplit(M->layers[0].qkv);
+            M->ksplit_o = vx_mgemm_ksplit(M->layers[0].o);
+            M->ksplit_down = vx_mgemm_ksplit(M->layers[0].down);
+        } else {
+            M->ksplit_o = vx_bgemm_ksplit(M->layers[0].o);
+            M->ksplit_down = vx_bgemm_ksplit(M->layers[0].down);
+        }
     }
     M->act_bytes = ac;
 
@@ -554,6 +632,8 @@ int velox_hip_load_q4_0(VeloxHipArena* a, int kind, uint32_t layer, const void* 
     hipError_t e = hipMalloc(&staging, nbytes);
     if (e == hipSuccess) e = hipMemcpyAsync(staging, blocks, nbytes, hipMemcpyHostToDevice, stream);
     if (e == hipSuccess) e = vx_launch_repack(staging, rows, row0, pair, vx_view(a, *mp), stream);
+    if (e == hipSuccess) e = vx_build_m(a, *mp, stream);
+    if (e == hipSuccess && kind == VELOX_T_EMBED && a->model->cfg.tied_lm_head) e = vx_build_m(a, a->model->head, stream);
     if (e == hipSuccess) e = hipStreamSynchronize(stream);
     hipFree(staging);
     return (int)e;
@@ -603,6 +683,10 @@ int velox_hip_synthesize_model(VeloxHipArena* a, uint64_t seed, float sigma, flo
             vec(VELOX_T_BV, l, coef, 0.0f);
         }
     }
+    for (const VxLayerPlan& L : M->layers)
+        for (const VxMatPlan* p : {&L.qkv, &L.o, &L.gate_up, &L.down})
+            if (e == hipSuccess) e = vx_build_m(a, *p, st);
+    if (e == hipSuccess) e = vx_build_m(a, M->head, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     return (int)e;
 }
@@ -732,6 +816,9 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
     float* qkv = (float*)(act + M->a_bqkv);
     float* part_r = (float*)(act + M->a_bpart_r);
     const uint64_t pstride = (uint64_t)M->rows * H;
+    auto gemm = [&](const VxMatPlan& p, const VxBGemmArgs& ga, int epi) {
+        return M->mgemm ? vx_launch_mgemm(vx_mview(A, p), ga, epi, st) : vx_launch_bgemm(vx_view(A, p), ga, epi, st);
+    };
 
     vx_record(vx_launch_bembed(vx_view(A, M->embed), rows, n, h, H, mask, st));
     VxAttnArgs at;
@@ -759,67 +846,80 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
         const VxLayerPlan& L = M->layers[l];
         // the previous layer's down projection left its K-split partials (none before layer 0)
         vx_record(vx_launch_bnorm(h, H, l && M->ksplit_down > 1 ? part_r : nullptr, M->ksplit_down, pstride,
-                                  vecp(L.attn_norm), H, c.rms_norm_eps, xa, M->xw, n, mask, st));
+                                  vecp(L.attn_norm), H, c.rms_norm_eps, xa, M->x_ld, M->x_bs, n, mask, st));
         std::memset(&g, 0, sizeof(g));
         g.batch = n;
         g.active_mask = mask;
         g.x16 = xa;
-        g.ldx = M->xw;
+        g.ldx = M->x_ld;
+        g.xbs = M->x_bs;
         g.bias = c.qkv_bias ? vecp(L.bias) : nullptr;
         g.y = qkv;
         g.ldy = qd + 2 * kvd;
-        vx_record(vx_launch_bgemm(vx_view(A, L.qkv), g, VX_EPI_STORE, st));
+        if (M->mgemm && M->ksplit_qkv > 1) {  // K-split partials, then their sum + bias
+            g.ksplit = M->ksplit_qkv;
+            g.part = part_r;
+            g.pstride = (uint64_t)M->rows * g.ldy;
+        }
+        vx_record(gemm(L.qkv, g, VX_EPI_STORE));
+        if (g.ksplit > 1)
+            vx_record(vx_launch_msum(part_r, g.ksplit, g.pstride, g.bias, qkv, g.ldy, g.ldy, n, 0, mask, st));
         at.kv = vx_kv(A, l, 0);
         if (prefill)
             vx_record(vx_launch_kv_append_rows(qkv, qd + 2 * kvd, c.num_heads, c.num_kv_heads, D, rows, n, at.rope,
                                                c.max_seq_len, M->s_cap, at.kv, mask, st));
         vx_record(vx_launch_attention(at, D, st));
-        vx_record(vx_launch_bmerge(at.part_o, at.part_ml, c.num_heads, D, M->splits, xa, M->xw, n, mask, st));
+        vx_record(vx_launch_bmerge(at.part_o, at.part_ml, c.num_heads, D, M->splits, xa, M->x_ld, M->x_bs, n, mask, st));
         std::memset(&g, 0, sizeof(g));
         g.batch = n;
         g.active_mask = mask;
         g.x16 = xa;
-        g.ldx = M->xw;
+        g.ldx = M->x_ld;
+        g.xbs = M->x_bs;
         g.y = h;
         g.ldy = H;
         g.ksplit = M->ksplit_o;
         g.part = part_r;
         g.pstride = pstride;
-        vx_record(vx_launch_bgemm(vx_view(A, L.o), g, VX_EPI_RESID, st));
+        vx_record(gemm(L.o, g, VX_EPI_RESID));
         vx_record(vx_launch_bnorm(h, H, M->ksplit_o > 1 ? part_r : nullptr, M->ksplit_o, pstride, vecp(L.mlp_norm), H,
-                                  c.rms_norm_eps, xa, M->xw, n, mask, st));
+                                  c.rms_norm_eps, xa, M->x_ld, M->x_bs, n, mask, st));
         std::memset(&g, 0, sizeof(g));
         g.batch = n;
         g.active_mask = mask;
         g.x16 = xa;
-        g.ldx = M->xw;
+        g.ldx = M->x_ld;
+        g.xbs = M->x_bs;
         g.out16 = xb;
-        g.ldo = M->xw;
-        vx_record(vx_launch_bgemm(vx_view(A, L.gate_up), g, VX_EPI_SWIGLU, st));
+        g.ldo = M->x_ld;
+        g.obs = M->x_bs;
+        vx_record(gemm(L.gate_up, g, VX_EPI_SWIGLU));
         std::memset(&g, 0, sizeof(g));
         g.batch = n;
         g.active_mask = mask;
         g.x16 = xb;
-        g.ldx = M->xw;
+        g.ldx = M->x_ld;
+        g.xbs = M->x_bs;
         g.y = h;
         g.ldy = H;
         g.ksplit = M->ksplit_down;
         g.part = part_r;
         g.pstride = pstride;
-        vx_record(vx_launch_bgemm(vx_view(A, L.down), g, VX_EPI_RESID, st));
+        vx_record(gemm(L.down, g, VX_EPI_RESID));
     }
     vx_record(vx_launch_bnorm(h, H, M->ksplit_down > 1 ? part_r : nullptr, M->ksplit_down, pstride,
-                              vecp(M->final_norm), H, c.rms_norm_eps, xa, M->xw, n, mask, st));
+                              vecp(M->final_norm), H, c.rms_norm_eps, xa, M->x_ld, M->x_bs, n, mask, st));
     std::memset(&g, 0, sizeof(g));
     g.batch = n;
     g.active_mask = mask;
     g.x16 = xa;
-    g.ldx = M->xw;
+    g.ldx = M->x_ld;
+        g.xbs = M->x_bs;
     g.y = (float*)(act + M->a_blogits);
     g.ldy = c.vocab_size;
     g.cand_v = (float*)(act + M->a_bcand_v);
     g.cand_i = (uint32_t*)(act + M->a_bcand_i);
-    vx_record(vx_launch_bgemm(vx_view(A, M->head), g, VX_EPI_ARGMAX, st));
+    vx_record(gemm(M->head, g, VX_EPI_ARGMAX));
 }
 
 }  // namespace
@@ -1064,14 +1164,80 @@ int velox_hip_gemm_q4_0_batch(const VeloxHipQ4Matrix* m, const uint16_t* d_x16, 
     g.batch = batch;
     g.x16 = d_x16;
     g.ldx = ldx;
+    g.xbs = 32;
     g.bias = d_bias;
     g.y = d_y;
     g.ldy = ldy;
     g.out16 = d_out16;
     g.ldo = ldo;
+    g.obs = 32;
     g.active_mask = 1;
     const int epi = mode == VELOX_GEMV_STORE ? VX_EPI_STORE : mode == VELOX_GEMV_RESIDUAL ? VX_EPI_RESID : VX_EPI_SWIGLU;
     return (int)vx_launch_bgemm(vx_view_public(m), g, epi, st);
+}
+
+namespace {
+bool vx_mmat_public(const VeloxHipQ4Matrix* m, const void* codes, const void* scales, VxMMat& out) {
+    if (!m || m->k == 0 || (m->k & 31u) || m->n == 0) return false;
+    vx_mmat_shape(m->n, m->k, m->paired, out);
+    out.codes = (const uint4*)codes;
+    out.scales = (const uint2*)scales;
+    return true;
+}
+}  // namespace
+
+int velox_hip_q4_mlayout_bytes(const VeloxHipQ4Matrix* m, uint64_t* code_bytes, uint64_t* scale_bytes) {
+    VxMMat mm;
+    if (!vx_mmat_public(m, nullptr, nullptr, mm)) return VELOX_HIP_EINVAL;
+    if (code_bytes) *code_bytes = vx_mmat_code_bytes(mm);
+    if (scale_bytes) *scale_bytes = vx_mmat_scale_bytes(mm);
+    return VELOX_HIP_OK;
+}
+
+int velox_hip_q4_mlayout(const VeloxHipQ4Matrix* m, void* d_codes, void* d_scales, hipStream_t st) {
+    VxMMat mm;
+    if (!d_codes || !d_scales || !vx_mmat_public(m, d_codes, d_scales, mm)) return VELOX_HIP_EINVAL;
+    return (int)vx_launch_mlayout(vx_view_public(m), mm, st);
+}
+
+int velox_hip_gemm_q4_0_batch_m(const VeloxHipQ4Matrix* m, const void* d_mcodes, const void* d_mscales,
+                                const uint16_t* d_x16, uint32_t batch, uint32_t ldx, uint32_t xbs, const float* d_bias,
+                                float* d_y, uint32_t ldy, uint16_t* d_out16, uint32_t ldo, uint32_t obs, int mode,
+                                uint32_t ksplit, float* d_part, hipStream_t st) {
+    VxMMat mm;
+    if (!d_mcodes || !d_mscales || !vx_mmat_public(m, d_mcodes, d_mscales, mm)) return VELOX_HIP_EINVAL;
+    if (xbs == 0) xbs = 32;
+    if (obs == 0) obs = 32;
+    if (!d_x16 || batch == 0 || batch > 32 || (ldx & 7u) || (xbs & 7u) || !vx_x_layout_ok(m->k, ldx, xbs, batch) ||
+        mode < 0 || mode > 2)
+        return VELOX_HIP_EINVAL;
+    if ((mode == VELOX_GEMV_SWIGLU) != (m->paired != 0)) return VELOX_HIP_EINVAL;
+    if (mode == VELOX_GEMV_SWIGLU ? (!d_out16 || !vx_x_layout_ok(m->n, ldo, obs, batch)) : (!d_y || ldy < m->n))
+        return VELOX_HIP_EINVAL;
+    if (ksplit == 0 || ksplit > 8 || ksplit > mm.n_grp || (ksplit > 1 && (mode == VELOX_GEMV_SWIGLU || !d_part)))
+        return VELOX_HIP_EINVAL;
+    VxBGemmArgs g;
+    std::memset(&g, 0, sizeof(g));
+    g.batch = batch;
+    g.x16 = d_x16;
+    g.ldx = ldx;
+    g.xbs = xbs;
+    g.bias = d_bias;
+    g.y = d_y;
+    g.ldy = ldy;
+    g.out16 = d_out16;
+    g.ldo = ldo;
+    g.obs = obs;
+    g.active_mask = 1;
+    g.ksplit = ksplit;
+    g.part = d_part;
+    g.pstride = (uint64_t)batch * ldy;
+    const int epi = mode == VELOX_GEMV_STORE ? VX_EPI_STORE : mode == VELOX_GEMV_RESIDUAL ? VX_EPI_RESID : VX_EPI_SWIGLU;
+    hipError_t e = vx_launch_mgemm(mm, g, epi, st);
+    if (e == hipSuccess && ksplit > 1)
+        e = vx_launch_msum(d_part, ksplit, g.pstride, epi == VX_EPI_STORE ? d_bias : nullptr, d_y, m->n, ldy, batch,
+                           epi == VX_EPI_RESID ? 1u : 0u, 1ULL, st);
+    return (int)e;
 }
 
 int velox_hip_lm_head_argmax(const VeloxHipQ4Matrix* m, const float* d_x, const float* d_gain, float eps,
@@ -1313,13 +1479,17 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
         bg.batch = B;
         bg.active_mask = 1;
         bg.x16 = (const uint16_t*)(act + M->a_bxa);
-        bg.ldx = M->xw;
+        bg.ldx = M->x_ld;
+        bg.xbs = M->x_bs;
         bg.out16 = (uint16_t*)(act + M->a_bxb);
-        bg.ldo = M->xw;
+        bg.ldo = M->x_ld;
+        bg.obs = M->x_bs;
         auto launch_all = [&]() {
             for (uint32_t l = 0; l < cfg.num_layers; ++l) {
                 if (B > 1) {
-                    vx_record(vx_launch_bgemm(vx_view(&A, M->layers[l].gate_up), bg, VX_EPI_SWIGLU, st));
+                    const VxMatPlan& gu = M->layers[l].gate_up;
+                    vx_record(M->mgemm ? vx_launch_mgemm(vx_mview(&A, gu), bg, VX_EPI_SWIGLU, st)
+                                       : vx_launch_bgemm(vx_view(&A, gu), bg, VX_EPI_SWIGLU, st));
                 } else {
                     g.gain = (const float*)(A.norm_weight_arena + M->layers[l].mlp_norm);
                     vx_record(vx_launch_gemv(vx_view(&A, M->layers[l].gate_up), g, VX_EPI_SWIGLU, M->max_wgs, st));

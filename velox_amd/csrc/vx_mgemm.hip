@@ -1,0 +1,400 @@
+// vx_mgemm.hip -- the Q4_0 GEMM of the batched decode and prefill steps on gfx950 (MFMA), over a
+// second copy of every matrix in the MFMA operand layout ("M-layout").
+//
+// M-layout of an [n][k] Q4_0 matrix: 16-row tiles (paired gate/up matrices: gate tile u at 2u,
+// the matching up tile at 2u + 1) and groups of four 32-element blocks (k padded to 128 with
+// zero-scale blocks). Per (tile, group) 64 words of 16 bytes: lane l holds, for row 16 t + l % 16,
+// dword g = l / 16 -- elements 8g .. 8g+7, in the tiled layout's nibble order -- of each of the
+// blocks 4j .. 4j+3, i.e. the B operand of one v_mfma_f32_16x16x32_f16 per block. Scales: fp16
+// [tile][group][row][4 blocks]. One 16-byte load per lane per group feeds four MFMAs, straight from
+// HBM into registers: no LDS staging and no barriers (the tiled decode layout, made for the
+// GEMV's per-row lane streams, needed an LDS transposition per item and held one workgroup per CU).
+//
+// Per wave: NT tiles x MT groups of 16 activation rows over a range of groups (split-K across grid
+// rows). Block b of group j: c = mfma(x[m][32b + 8g .. +7], unpack(dword), 0); acc += d_b * c. The
+// products are exact (fp16 activations times integers -8..7), the block scale is applied in fp32
+// and the sums are fp32, as in the single-sequence GEMV and the tiled batched GEMM.
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include <cstdlib>
+
+#include "vx_common.h"
+
+namespace {
+
+typedef _Float16 vx_mh8 __attribute__((ext_vector_type(8)));
+typedef _Float16 vx_mh2 __attribute__((ext_vector_type(2)));
+typedef float vx_mf4 __attribute__((ext_vector_type(4)));
+typedef uint32_t vx_mu4 __attribute__((ext_vector_type(4)));
+typedef uint32_t vx_mu2 __attribute__((ext_vector_type(2)));
+
+constexpr int kMWaves = 4, kMThreads = 64 * kMWaves;
+
+__device__ __forceinline__ float vx_mh2f(uint32_t h) { return __half2float(__ushort_as_half((unsigned short)h)); }
+
+__device__ __forceinline__ bool vx_mbetter(float v, uint32_t i, float bv, uint32_t bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+// One code dword (byte e: element e low nibble, element e + 4 high nibble) -> the 8 values q - 8 as
+// fp16 in element order (1024 + q under the 0x64 exponent byte, minus 1032: exact).
+__device__ __forceinline__ vx_mh8 vx_munpack8(uint32_t q) {
+    const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu, c64 = 0x64646464u;
+    const vx_mh2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const vx_mh2 p0 = __builtin_bit_cast(vx_mh2, __builtin_amdgcn_perm(c64, lo, 0x04010400u)) + off;
+    const vx_mh2 p1 = __builtin_bit_cast(vx_mh2, __builtin_amdgcn_perm(c64, lo, 0x04030402u)) + off;
+    const vx_mh2 p2 = __builtin_bit_cast(vx_mh2, __builtin_amdgcn_perm(c64, hi, 0x04010400u)) + off;
+    const vx_mh2 p3 = __builtin_bit_cast(vx_mh2, __builtin_amdgcn_perm(c64, hi, 0x04030402u)) + off;
+    vx_mh8 r;
+    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+    return r;
+}
+
+// ---- M-layout copy of a tiled matrix: one thread per (tile, group, lane) ----
+__global__ __launch_bounds__(256) void vx_mlayout_kernel(VxMat src, VxMMat dst) {
+    const size_t idx = (size_t)blockIdx.x * 256u + threadIdx.x;
+    const size_t total = (size_t)dst.n_tiles * dst.n_grp * 64u;
+    if (idx >= total) return;
+    const uint32_t lane = (uint32_t)(idx & 63u), j = (uint32_t)((idx >> 6) % dst.n_grp);
+    const uint32_t t = (uint32_t)((idx >> 6) / dst.n_grp);
+    const uint32_t rho = lane & 15u, g = lane >> 4;
+    uint32_t row, part = 0;
+    if (dst.paired) {
+        row = 16u * (t >> 1) + rho;
+        part = t & 1u;
+    } else {
+        row = 16u * t + rho;
+    }
+    const uint32_t nb = src.k >> 5, R = 64u / src.s;
+    uint32_t out[4];
+    uint16_t sc[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const uint32_t blk = 4u * j + (uint32_t)b;
+        out[b] = 0u;
+        sc[b] = 0u;
+        if (row < dst.n && blk < nb) {
+            uint32_t phys = row;
+            if (src.paired) {
+                const uint32_t half = R / 2u;
+                phys = (row / half) * (2u * half) + part * half + (row % half);
+            }
+            const size_t off = ((size_t)(phys / R) * src.n_iter + blk / src.s) * 64u + (phys % R) * src.s + blk % src.s;
+            const uint4 c = src.codes[off];
+            out[b] = g == 0 ? c.x : g == 1 ? c.y : g == 2 ? c.z : c.w;
+            sc[b] = src.scales[off];
+        }
+    }
+    ((uint4*)dst.codes)[idx] = make_uint4(out[0], out[1], out[2], out[3]);
+    if (g == 0) {
+        uint2 s;
+        s.x = (uint32_t)sc[0] | ((uint32_t)sc[1] << 16);
+        s.y = (uint32_t)sc[2] | ((uint32_t)sc[3] << 16);
+        ((uint2*)dst.scales)[((size_t)t * dst.n_grp + j) * 16u + rho] = s;
+    }
+}
+
+// ---- split-K partial sums (+ bias) of a STORE GEMM: y[m][n] = sum_s part[s][m][n] + bias[n] ----
+// (accumulate: y[m][n] += the sum instead, the RESID form)
+__global__ __launch_bounds__(256) void vx_msum_kernel(const float* part, uint32_t nparts, uint64_t pstride,
+                                                      const float* bias, float* y, uint32_t n, uint32_t ldy,
+                                                      uint32_t accumulate, uint64_t mask) {
+    if ((mask & 1ULL) == 0ULL) return;
+    const uint32_t m = blockIdx.y, c = blockIdx.x * 256u + threadIdx.x;
+    if (c >= n) return;
+    // every part's load in flight at once (clamped to a loaded part), then the sum in split order
+    float v[8];
+#pragma unroll
+    for (uint32_t p = 0; p < 8; ++p) v[p] = part[min(p, nparts - 1u) * pstride + (size_t)m * ldy + c];
+    float s = 0.0f;
+#pragma unroll
+    for (uint32_t p = 0; p < 8; ++p)
+        if (p < nparts) s += v[p];
+    if (bias) s += bias[c];
+    float* yp = y + (size_t)m * ldy + c;
+    *yp = accumulate ? *yp + s : s;
+}
+
+}  // namespace
+
+// ---- the GEMM ----
+// A workgroup's 4 waves share its NT tiles and split its K range: wave w takes groups j0 + w,
+// j0 + w + 4, ... (adjacent 1 KiB words of a tile in flight together), then the partial sums meet
+// in LDS in wave order and wave 0 runs the epilogue.
+template <int EPI, int MT, int NT, int PD>
+__global__ __launch_bounds__(kMThreads) void vx_mgemm_kernel(VxMMat w, VxBGemmArgs a) {
+    if ((a.active_mask & 1ULL) == 0ULL) return;
+    static_assert(EPI != VX_EPI_SWIGLU || NT % 2 == 0, "paired tiles come in (gate, up) pairs");
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int row = lane & 15, g = lane >> 4;
+    const uint32_t T0 = blockIdx.x * (uint32_t)NT;
+    const uint32_t ng = w.n_grp;
+    const uint32_t j0 = blockIdx.y * ng / gridDim.y, j1 = (blockIdx.y + 1u) * ng / gridDim.y;
+
+    // tiles past the matrix re-read its last tile, activation rows past the batch the last row,
+    // padded blocks (zero scales) the last real block: every load is in bounds and unconditional
+    const vx_mu4* cp[NT];
+    const vx_mu2* sp[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t t = min(T0 + (uint32_t)nt, w.n_tiles - 1u);
+        cp[nt] = (const vx_mu4*)w.codes + (size_t)t * ng * 64u + lane;
+        sp[nt] = (const vx_mu2*)w.scales + (size_t)t * ng * 16u + row;
+    }
+    const uint16_t* xp[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+        xp[mt] = a.x16 + (size_t)min((uint32_t)(16 * mt + row), a.batch - 1u) * a.ldx + 8 * g;
+    const uint32_t xbs = a.xbs;
+    const uint32_t b_last = (w.k >> 5) - 1u;
+
+    vx_mf4 acc[NT][MT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = vx_mf4{0.f, 0.f, 0.f, 0.f};
+
+    const uint32_t jw = j0 + (uint32_t)wave;  // this wave's first group; then every kMWaves-th
+    if (jw < j1) {
+        vx_mu4 cw[PD][NT];
+        vx_mu2 sw[PD][NT];
+        vx_mh8 xa[2][MT][4];
+        // group i of this wave: jw + kMWaves i, clamped to its last group (in bounds, L2-resident)
+        const uint32_t jlast = jw + (j1 - 1u - jw) / kMWaves * kMWaves;
+#define VX_MG_LOADW(p_, jj_)                                                                      \
+    do {                                                                                          \
+        const uint32_t jc_ = min((jj_), jlast);                                                   \
+        _Pragma("unroll") for (int nt = 0; nt < NT; ++nt) {                                       \
+            cw[p_][nt] = cp[nt][(size_t)jc_ * 64u];                                               \
+            sw[p_][nt] = sp[nt][(size_t)jc_ * 16u];                                               \
+        }                                                                                         \
+    } while (0)
+#define VX_MG_LOADX(s_, jj_)                                                                      \
+    do {                                                                                          \
+        const uint32_t jc_ = min((jj_), jlast);                                                   \
+        _Pragma("unroll") for (int b = 0; b < 4; ++b) {                                           \
+            const uint32_t blk_ = min(4u * jc_ + (uint32_t)b, b_last);                            \
+            _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                     \
+                xa[s_][mt][b] = *(const vx_mh8*)(xp[mt] + (size_t)blk_ * xbs);                    \
+        }                                                                                         \
+    } while (0)
+#pragma unroll
+        for (int p = 0; p < PD; ++p) VX_MG_LOADW(p, jw + (uint32_t)(kMWaves * p));
+        VX_MG_LOADX(0, jw);
+        for (uint32_t j = jw; j <= jlast; j += (uint32_t)(kMWaves * PD)) {
+#pragma unroll
+            for (int p = 0; p < PD; ++p) {
+                // loads stay outside the branch (clamped, in bounds), so the compiler's waits at the
+                // join do not drain the groups in flight
+                const uint32_t jj = j + (uint32_t)(kMWaves * p);
+                const int cur = p & 1;
+                VX_MG_LOADX(cur ^ 1, jj + (uint32_t)kMWaves);
+                if (jj <= jlast) {
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+#pragma unroll
+                        for (int nt = 0; nt < NT; ++nt) {
+                            const vx_mh8 wb = vx_munpack8(cw[p][nt][b]);
+                            const uint32_t sv = b < 2 ? sw[p][nt].x : sw[p][nt].y;
+                            const float d = vx_mh2f((sv >> (16 * (b & 1))) & 0xFFFFu);
+#pragma unroll
+                            for (int mt = 0; mt < MT; ++mt) {
+                                const vx_mf4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[cur][mt][b], wb,
+                                                                                        vx_mf4{0.f, 0.f, 0.f, 0.f}, 0,
+                                                                                        0, 0);
+                                acc[nt][mt] += d * c;
+                            }
+                        }
+                }
+                VX_MG_LOADW(p, jj + (uint32_t)(kMWaves * PD));
+            }
+            // PD odd: the x buffer parity alternates across outer iterations
+            if constexpr (PD & 1) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) xa[0][mt][b] = xa[1][mt][b];
+            }
+        }
+#undef VX_MG_LOADW
+#undef VX_MG_LOADX
+    }
+
+    // ---- the 4 waves' partial sums, added in wave order (deterministic) ----
+    __shared__ vx_mf4 red_s[kMWaves - 1][NT * MT][64];
+    if (wave > 0) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) red_s[wave - 1][nt * MT + mt][lane] = acc[nt][mt];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int wv = 0; wv < kMWaves - 1; ++wv)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[nt][mt] += red_s[wv][nt * MT + mt][lane];
+
+    // ---- epilogues (wave 0): lane holds acc[nt][mt][i] for activation row m = 16 mt + 4 g + i of
+    // tile T0 + nt's row 16 t + row ----
+    if constexpr (EPI == VX_EPI_SWIGLU) {
+#pragma unroll
+        for (int u = 0; u < NT / 2; ++u) {
+            const uint32_t t = T0 + 2u * (uint32_t)u;  // gate tile; t + 1 its up tile
+            const uint32_t jrow = 16u * (t >> 1) + (uint32_t)row;
+            if (t >= w.n_tiles || jrow >= w.n) continue;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t m = (uint32_t)(16 * mt + 4 * g + i);
+                    if (m >= a.batch) continue;
+                    const float gt = acc[2 * u][mt][i], up = acc[2 * u + 1][mt][i];
+                    a.out16[(size_t)m * a.ldo + (size_t)(jrow >> 5) * a.obs + (jrow & 31u)] =
+                        __half_as_ushort(__float2half((gt / (1.0f + expf(-gt))) * up));
+                }
+        }
+    } else if constexpr (EPI == VX_EPI_ARGMAX) {
+        // per activation row: logits, then the best (value, lowest index) of this workgroup's rows
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t m = (uint32_t)(16 * mt + 4 * g + i);
+                float bv = -INFINITY;
+                uint32_t bi = 0xFFFFFFFFu;
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const uint32_t t = T0 + (uint32_t)nt, n = 16u * t + (uint32_t)row;
+                    if (t < w.n_tiles && n < w.n) {
+                        if (m < a.batch) a.y[(size_t)m * a.ldy + n] = acc[nt][mt][i];
+                        if (vx_mbetter(acc[nt][mt][i], n, bv, bi)) { bv = acc[nt][mt][i]; bi = n; }
+                    }
+                }
+#pragma unroll
+                for (int off = 1; off < 16; off <<= 1) {
+                    const float ov = __shfl_xor(bv, off);
+                    const uint32_t oi = __shfl_xor(bi, off);
+                    if (vx_mbetter(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+                }
+                if (row == 0 && m < a.batch) {
+                    a.cand_v[(size_t)m * gridDim.x + blockIdx.x] = bv;
+                    a.cand_i[(size_t)m * gridDim.x + blockIdx.x] = bi;
+                }
+            }
+    } else {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const uint32_t t = T0 + (uint32_t)nt, n = 16u * t + (uint32_t)row;
+            if (t >= w.n_tiles || n >= w.n) continue;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t m = (uint32_t)(16 * mt + 4 * g + i);
+                    if (m >= a.batch) continue;
+                    const float v = acc[nt][mt][i];
+                    if (gridDim.y > 1u) {
+                        a.part[blockIdx.y * a.pstride + (size_t)m * a.ldy + n] = v;
+                    } else {
+                        float* yp = a.y + (size_t)m * a.ldy + n;
+                        if constexpr (EPI == VX_EPI_STORE) *yp = a.bias ? v + a.bias[n] : v;
+                        else *yp += v;
+                    }
+                }
+        }
+    }
+}
+
+namespace {
+
+constexpr int kMNT = 2;  // tiles per wave (a gate/up pair for SWIGLU)
+
+int vx_mgemm_pd() {
+    static int pd = 0;
+    if (!pd) {
+        const char* env = std::getenv("VELOX_HIP_MGEMM_PD");  // tuning: weight groups in flight per wave
+        pd = env ? std::atoi(env) : 1;  // measured: 1 beats 2 and 4 (fewer registers, more waves)
+        if (pd != 1 && pd != 2 && pd != 4) pd = 1;
+    }
+    return pd;
+}
+
+template <int EPI, int MT, int PD>
+hipError_t vx_mgemm_launch_t(const VxMMat& w, const VxBGemmArgs& a, hipStream_t st) {
+    const dim3 grid(vx_mgemm_grid(w.n_tiles), a.ksplit > 1u ? a.ksplit : 1u);
+    hipLaunchKernelGGL((vx_mgemm_kernel<EPI, MT, kMNT, PD>), grid, dim3(kMThreads), 0, st, w, a);
+    return hipGetLastError();
+}
+
+template <int EPI, int MT>
+hipError_t vx_mgemm_dispatch_pd(const VxMMat& w, const VxBGemmArgs& a, hipStream_t st) {
+    switch (vx_mgemm_pd()) {
+        case 2: return vx_mgemm_launch_t<EPI, MT, 2>(w, a, st);
+        case 4: return vx_mgemm_launch_t<EPI, MT, 4>(w, a, st);
+        default: return vx_mgemm_launch_t<EPI, MT, 1>(w, a, st);
+    }
+}
+
+template <int EPI>
+hipError_t vx_mgemm_dispatch_mt(const VxMMat& w, const VxBGemmArgs& a, hipStream_t st) {
+    if (a.batch == 0 || a.batch > 32) return hipErrorInvalidValue;
+    return a.batch <= 16 ? vx_mgemm_dispatch_pd<EPI, 1>(w, a, st) : vx_mgemm_dispatch_pd<EPI, 2>(w, a, st);
+}
+
+}  // namespace
+
+uint32_t vx_mgemm_grid(uint32_t n_tiles) { return (n_tiles + kMNT - 1u) / kMNT; }
+
+void vx_mmat_shape(uint32_t n, uint32_t k, uint32_t paired, VxMMat& m) {
+    m.n = n;
+    m.k = k;
+    m.paired = paired;
+    const uint32_t t = (n + 15u) / 16u;
+    m.n_tiles = paired ? 2u * t : t;
+    m.n_grp = (k / 32u + 3u) / 4u;
+}
+
+uint64_t vx_mmat_code_bytes(const VxMMat& m) { return (uint64_t)m.n_tiles * m.n_grp * 64u * 16u; }
+uint64_t vx_mmat_scale_bytes(const VxMMat& m) { return (uint64_t)m.n_tiles * m.n_grp * 16u * 8u; }
+
+hipError_t vx_launch_mlayout(const VxMat& src, const VxMMat& dst, hipStream_t st) {
+    if (src.n != dst.n || src.k != dst.k || src.paired != dst.paired || (src.k & 31u)) return hipErrorInvalidValue;
+    const size_t total = (size_t)dst.n_tiles * dst.n_grp * 64u;
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(vx_mlayout_kernel, dim3((unsigned)((total + 255u) / 256u)), dim3(256), 0, st, src, dst);
+    return hipGetLastError();
+}
+
+hipError_t vx_launch_mgemm(const VxMMat& w, const VxBGemmArgs& a, int epi, hipStream_t st) {
+    if (w.k == 0 || (w.k & 31u) || (a.ldx & 7u) || (a.xbs & 7u) || !a.x16 || !vx_x_layout_ok(w.k, a.ldx, a.xbs, a.batch))
+        return hipErrorInvalidValue;
+    if (epi == VX_EPI_SWIGLU && !vx_x_layout_ok(w.n, a.ldo, a.obs, a.batch)) return hipErrorInvalidValue;
+    if ((epi == VX_EPI_SWIGLU) != (w.paired != 0)) return hipErrorInvalidValue;
+    if (a.ksplit > 1u && ((epi != VX_EPI_RESID && epi != VX_EPI_STORE) || !a.part || a.ksplit > w.n_grp ||
+                          a.ksplit > 8u || a.pstride < (uint64_t)a.batch * a.ldy))
+        return hipErrorInvalidValue;
+    switch (epi) {
+        case VX_EPI_STORE: return vx_mgemm_dispatch_mt<VX_EPI_STORE>(w, a, st);
+        case VX_EPI_RESID: return vx_mgemm_dispatch_mt<VX_EPI_RESID>(w, a, st);
+        case VX_EPI_SWIGLU: return vx_mgemm_dispatch_mt<VX_EPI_SWIGLU>(w, a, st);
+        case VX_EPI_ARGMAX: return vx_mgemm_dispatch_mt<VX_EPI_ARGMAX>(w, a, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t vx_launch_msum(const float* part, uint32_t nparts, uint64_t pstride, const float* bias, float* y,
+                          uint32_t n, uint32_t ldy, uint32_t batch, uint32_t accumulate, uint64_t mask,
+                          hipStream_t st) {
+    if (nparts == 0 || nparts > 8 || batch == 0 || ldy < n || pstride < (uint64_t)batch * ldy)
+        return hipErrorInvalidValue;
+    const uint32_t gx = (n + 255u) / 256u;
+    hipLaunchKernelGGL(vx_msum_kernel, dim3(gx ? gx : 1u, batch), dim3(256), 0, st, part, nparts, pstride, bias, y, n,
+                       ldy, accumulate, mask);
+    return hipGetLastError();
+}

@@ -456,7 +456,7 @@ void velox_hip_mla_layer_step(VeloxHipMla* m, uint32_t layer, uint32_t batch, ui
     };
     // 1. x = rmsnorm(h) as fp16
     vx_record_error(vx_launch_bnorm(h, m->H, nullptr, 0, 0, (const float*)((const uint8_t*)norms + L.norm), m->H,
-                                    c.rms_norm_eps, x16, m->ldx16, batch, mask, st));
+                                    c.rms_norm_eps, x16, m->ldx16, 32u, batch, mask, st));
     // 2. [W_qa; W_kva] x, split over K
     float* parts_a = vm_act(m, m->a_parts_a);
     const uint64_t pstride_a = (uint64_t)m->B * m->na;
