@@ -260,8 +260,9 @@ int velox_hip_gemm_q4_0_batch(const VeloxHipQ4Matrix* m, const uint16_t* d_x16, 
 /* The batched GEMM's MFMA operand layout ("M-layout"), a second copy of a tiled matrix that arenas
  * planned for more than one batched row keep for every matrix: 16-row tiles (paired: gate tile u at
  * 2u, up tile u at 2u + 1) x groups of four blocks; per (tile, group) 64 words of 16 bytes, lane l
- * holding dword l / 16 (elements 8(l/16) .. +7) of blocks 4j .. 4j+3 of row l % 16; fp16 scales
- * [tile][group][row][4]. _bytes gives the sizes, _mlayout builds the copy from the tiled matrix. */
+ * holding dword l / 16 (elements 8(l/16) .. +7, element e at bit 16 (e & 1) + 4 (e >> 1)) of blocks
+ * 4j .. 4j+3 of row l % 16; fp16 scales [tile][group][row][4]. _bytes gives the sizes, _mlayout
+ * builds the copy from the tiled matrix. */
 int velox_hip_q4_mlayout_bytes(const VeloxHipQ4Matrix* m, uint64_t* code_bytes, uint64_t* scale_bytes);
 int velox_hip_q4_mlayout(const VeloxHipQ4Matrix* m, void* d_codes, void* d_scales, hipStream_t stream);
 /* velox_hip_gemm_q4_0_batch over an M-layout copy (the batched decode and prefill steps' GEMM).

@@ -167,6 +167,15 @@ def _tiled_dwords(blocks: np.ndarray, k: int) -> tuple[np.ndarray, np.ndarray]:
     return dw, d
 
 
+def _m_order(dw: np.ndarray) -> np.ndarray:
+    """Tiled dword nibble order (element e at bit 8 (e % 4) + 4 (e // 4)) -> the M-layout's (bit
+    16 (e % 2) + 4 (e // 2))."""
+    out = np.zeros_like(dw)
+    for e in range(8):
+        out |= ((dw >> (8 * (e % 4) + 4 * (e // 4))) & 15) << (16 * (e % 2) + 4 * (e // 2))
+    return out
+
+
 def mlayout_reference(blocks, n, k, up_blocks=None):
     """The M-layout restated: codes [tiles][groups][64][4] uint32, scales [tiles][groups][16][4] uint16."""
     parts = [blocks] if up_blocks is None else [blocks, up_blocks]
@@ -178,6 +187,7 @@ def mlayout_reference(blocks, n, k, up_blocks=None):
     scales = np.zeros((tiles, ng, 16, 4), np.uint16)
     for pi, blk in enumerate(parts):
         dw, d = _tiled_dwords(blk, k)
+        dw = _m_order(dw)
         for t in range(t16):
             T = t * len(parts) + pi
             for rho in range(16):

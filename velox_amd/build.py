@@ -8,10 +8,12 @@ are avoided on purpose.
 """
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
@@ -40,15 +42,34 @@ def common_flags() -> list[str]:
     ]
 
 
+# Per-file code generation flags. The batched GEMM keeps MFMA results in VGPRs: its scale FMA reads
+# every MFMA result, and the AGPR form cost four v_accvgpr_read per MFMA (a quarter of its loop).
+FILE_FLAGS = {"vx_mgemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(LIBDIR, exist_ok=True)
     hipcc = _hipcc()
-    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
     tmp = LIB + ".tmp"
-    cmd = [hipcc, *common_flags(), "-shared", "-o", tmp, *srcs]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    subprocess.run(cmd, check=True)
+    with tempfile.TemporaryDirectory(prefix="velox_hip_build_") as objdir:
+        cmds, objs = [], []
+        for s in HIP_SOURCES:
+            obj = os.path.join(objdir, s + ".o")
+            objs.append(obj)
+            cmds.append([hipcc, *common_flags(), *FILE_FLAGS.get(s, []), "-c", "-o", obj, os.path.join(CSRC, s)])
+        with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(cmds))) as pool:
+            for cmd in cmds:
+                if verbose:
+                    print(" ".join(cmd), flush=True)
+            for r in pool.map(lambda c: subprocess.run(c, capture_output=True, text=True), cmds):
+                if r.stderr:
+                    sys.stderr.write(r.stderr)
+                if r.returncode != 0:
+                    raise subprocess.CalledProcessError(r.returncode, r.args, r.stdout, r.stderr)
+        cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
     runner_src = os.path.join(CSRC, "vx_runner_main.cpp")
     if os.path.exists(runner_src):

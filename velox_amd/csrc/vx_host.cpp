@@ -832,7 +832,13 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
     at.hkv = c.num_kv_heads;
     at.s_max = c.max_seq_len;
     at.s_cap = M->s_cap;
-    at.splits = M->splits;
+    // splits for about 256 attention workgroups over the rows' (row, kv head) pairs (measured at
+    // Qwen2.5-7B ctx 2048: B = 32 best at 2, B = 8 at 8), at most the planned count the partial
+    // buffers hold
+    uint32_t bsplits = (256u + n * c.num_kv_heads / 2u) / (n * c.num_kv_heads);
+    if (const char* env = std::getenv("VELOX_HIP_BATCH_ATTN_SPLITS")) bsplits = (uint32_t)std::strtoul(env, nullptr, 10);
+    bsplits = bsplits < 1u ? 1u : bsplits > M->splits ? M->splits : bsplits;
+    at.splits = bsplits;
     at.scale = 1.0f / sqrtf((float)D);
     at.active_mask = mask;
     at.partials_only = 1;
@@ -869,7 +875,7 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
             vx_record(vx_launch_kv_append_rows(qkv, qd + 2 * kvd, c.num_heads, c.num_kv_heads, D, rows, n, at.rope,
                                                c.max_seq_len, M->s_cap, at.kv, mask, st));
         vx_record(vx_launch_attention(at, D, st));
-        vx_record(vx_launch_bmerge(at.part_o, at.part_ml, c.num_heads, D, M->splits, xa, M->x_ld, M->x_bs, n, mask, st));
+        vx_record(vx_launch_bmerge(at.part_o, at.part_ml, c.num_heads, D, bsplits, xa, M->x_ld, M->x_bs, n, mask, st));
         std::memset(&g, 0, sizeof(g));
         g.batch = n;
         g.active_mask = mask;

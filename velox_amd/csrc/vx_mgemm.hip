@@ -4,8 +4,8 @@
 // M-layout of an [n][k] Q4_0 matrix: 16-row tiles (paired gate/up matrices: gate tile u at 2u,
 // the matching up tile at 2u + 1) and groups of four 32-element blocks (k padded to 128 with
 // zero-scale blocks). Per (tile, group) 64 words of 16 bytes: lane l holds, for row 16 t + l % 16,
-// dword g = l / 16 -- elements 8g .. 8g+7, in the tiled layout's nibble order -- of each of the
-// blocks 4j .. 4j+3, i.e. the B operand of one v_mfma_f32_16x16x32_f16 per block. Scales: fp16
+// dword g = l / 16 -- elements 8g .. 8g+7, element e at bit 16 (e & 1) + 4 (e >> 1) -- of each of
+// the blocks 4j .. 4j+3, i.e. the B operand of one v_mfma_f32_16x16x32_f16 per block. Scales: fp16
 // [tile][group][row][4 blocks]. One 16-byte load per lane per group feeds four MFMAs, straight from
 // HBM into registers: no LDS staging and no barriers (the tiled decode layout, made for the
 // GEMV's per-row lane streams, needed an LDS transposition per item and held one workgroup per CU).
@@ -17,8 +17,6 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
-
-#include <cstdlib>
 
 #include "vx_common.h"
 
@@ -38,19 +36,40 @@ __device__ __forceinline__ bool vx_mbetter(float v, uint32_t i, float bv, uint32
     return v > bv || (v == bv && i < bi);
 }
 
-// One code dword (byte e: element e low nibble, element e + 4 high nibble) -> the 8 values q - 8 as
-// fp16 in element order (1024 + q under the 0x64 exponent byte, minus 1032: exact).
-__device__ __forceinline__ vx_mh8 vx_munpack8(uint32_t q) {
-    const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu, c64 = 0x64646464u;
+// One M-layout code dword -> the 8 values q - 8 as fp16 in element order. Element e sits at bit
+// 16 (e & 1) + 4 (e >> 1), so each half of the dword holds one element of each pair: under the
+// 0x6400 exponent (1024 + q in the mantissa), masks 0x000F000F / 0x00F000F0 of q and of q >> 8 give
+// the pairs (e0, e1), (e2, e3) scaled by 16, (e4, e5), (e6, e7) scaled by 16; -1032, or x / 16 - 72
+// for the scaled ones, leaves q - 8 exactly (9 instructions per dword).
+// (a & m) | e in one VOP3 instruction: GFX9 reads at most one scalar or constant operand per VALU
+// instruction, so the compiler splits the two-constant form into v_and + v_or; here the mask comes
+// from an SGPR and the exponent pattern from a VGPR.
+__device__ __forceinline__ uint32_t vx_and_or(uint32_t a, uint32_t m, uint32_t e) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(e));
+    return r;
+}
+
+__device__ __forceinline__ vx_mh8 vx_munpack8(uint32_t q, uint32_t e) {
+    const uint32_t q8 = q >> 8;
     const vx_mh2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-    const vx_mh2 p0 = __builtin_bit_cast(vx_mh2, __builtin_amdgcn_perm(c64, lo, 0x04010400u)) + off;
-    const vx_mh2 p1 = __builtin_bit_cast(vx_mh2, __builtin_amdgcn_perm(c64, lo, 0x04030402u)) + off;
-    const vx_mh2 p2 = __builtin_bit_cast(vx_mh2, __builtin_amdgcn_perm(c64, hi, 0x04010400u)) + off;
-    const vx_mh2 p3 = __builtin_bit_cast(vx_mh2, __builtin_amdgcn_perm(c64, hi, 0x04030402u)) + off;
+    const vx_mh2 sc = {(_Float16)0.0625f, (_Float16)0.0625f}, off16 = {(_Float16)-72.0f, (_Float16)-72.0f};
+    const vx_mh2 p0 = __builtin_bit_cast(vx_mh2, vx_and_or(q, 0x000F000Fu, e)) + off;
+    const vx_mh2 p1 = __builtin_bit_cast(vx_mh2, vx_and_or(q, 0x00F000F0u, e)) * sc + off16;
+    const vx_mh2 p2 = __builtin_bit_cast(vx_mh2, vx_and_or(q8, 0x000F000Fu, e)) + off;
+    const vx_mh2 p3 = __builtin_bit_cast(vx_mh2, vx_and_or(q8, 0x00F000F0u, e)) * sc + off16;
     vx_mh8 r;
     r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
     r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
     return r;
+}
+
+// Tiled-layout dword (element e at bit 8 (e & 3) + 4 (e >> 2)) -> M-layout dword order.
+__device__ __forceinline__ uint32_t vx_mreorder(uint32_t t) {
+    uint32_t o = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o |= ((t >> (8 * (e & 3) + 4 * (e >> 2))) & 15u) << (16 * (e & 1) + 4 * (e >> 1));
+    return o;
 }
 
 // ---- M-layout copy of a tiled matrix: one thread per (tile, group, lane) ----
@@ -84,7 +103,7 @@ __global__ __launch_bounds__(256) void vx_mlayout_kernel(VxMat src, VxMMat dst) 
             }
             const size_t off = ((size_t)(phys / R) * src.n_iter + blk / src.s) * 64u + (phys % R) * src.s + blk % src.s;
             const uint4 c = src.codes[off];
-            out[b] = g == 0 ? c.x : g == 1 ? c.y : g == 2 ? c.z : c.w;
+            out[b] = vx_mreorder(g == 0 ? c.x : g == 1 ? c.y : g == 2 ? c.z : c.w);
             sc[b] = src.scales[off];
         }
     }
@@ -124,7 +143,7 @@ __global__ __launch_bounds__(256) void vx_msum_kernel(const float* part, uint32_
 // A workgroup's 4 waves share its NT tiles and split its K range: wave w takes groups j0 + w,
 // j0 + w + 4, ... (adjacent 1 KiB words of a tile in flight together), then the partial sums meet
 // in LDS in wave order and wave 0 runs the epilogue.
-template <int EPI, int MT, int NT, int PD>
+template <int EPI, int MT, int NT>
 __global__ __launch_bounds__(kMThreads) void vx_mgemm_kernel(VxMMat w, VxBGemmArgs a) {
     if ((a.active_mask & 1ULL) == 0ULL) return;
     static_assert(EPI != VX_EPI_SWIGLU || NT % 2 == 0, "paired tiles come in (gate, up) pairs");
@@ -158,69 +177,55 @@ __global__ __launch_bounds__(kMThreads) void vx_mgemm_kernel(VxMMat w, VxBGemmAr
         for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = vx_mf4{0.f, 0.f, 0.f, 0.f};
 
     const uint32_t jw = j0 + (uint32_t)wave;  // this wave's first group; then every kMWaves-th
-    if (jw < j1) {
-        vx_mu4 cw[PD][NT];
-        vx_mu2 sw[PD][NT];
-        vx_mh8 xa[2][MT][4];
-        // group i of this wave: jw + kMWaves i, clamped to its last group (in bounds, L2-resident)
-        const uint32_t jlast = jw + (j1 - 1u - jw) / kMWaves * kMWaves;
-#define VX_MG_LOADW(p_, jj_)                                                                      \
+    const uint32_t ngw = jw < j1 ? (j1 - jw + (uint32_t)kMWaves - 1u) / (uint32_t)kMWaves : 0u;
+    if (ngw) {
+        // Two operand sets ping-pong over pairs of groups: each set's loads are issued before the
+        // other set's MFMAs, and the loop body has no branch, so the compiler's waits keep the
+        // other set in flight (a branch around the MFMAs made it drain every load per iteration).
+        const uint32_t jlast = jw + (ngw - 1u) * (uint32_t)kMWaves;
+        const uint32_t e6400 = __builtin_amdgcn_readfirstlane(0x64006400u) + (uint32_t)lane * 0u;  // held in a VGPR
+        vx_mu4 cwA[NT], cwB[NT];
+        vx_mu2 swA[NT], swB[NT];
+        vx_mh8 xaA[MT][4], xaB[MT][4];
+#define VX_MG_LOAD(cw_, sw_, xa_, jj_)                                                            \
     do {                                                                                          \
         const uint32_t jc_ = min((jj_), jlast);                                                   \
         _Pragma("unroll") for (int nt = 0; nt < NT; ++nt) {                                       \
-            cw[p_][nt] = cp[nt][(size_t)jc_ * 64u];                                               \
-            sw[p_][nt] = sp[nt][(size_t)jc_ * 16u];                                               \
+            cw_[nt] = cp[nt][(size_t)jc_ * 64u];                                                  \
+            sw_[nt] = sp[nt][(size_t)jc_ * 16u];                                                  \
         }                                                                                         \
-    } while (0)
-#define VX_MG_LOADX(s_, jj_)                                                                      \
-    do {                                                                                          \
-        const uint32_t jc_ = min((jj_), jlast);                                                   \
         _Pragma("unroll") for (int b = 0; b < 4; ++b) {                                           \
             const uint32_t blk_ = min(4u * jc_ + (uint32_t)b, b_last);                            \
             _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                     \
-                xa[s_][mt][b] = *(const vx_mh8*)(xp[mt] + (size_t)blk_ * xbs);                    \
+                xa_[mt][b] = *(const vx_mh8*)(xp[mt] + (size_t)blk_ * xbs);                       \
         }                                                                                         \
     } while (0)
-#pragma unroll
-        for (int p = 0; p < PD; ++p) VX_MG_LOADW(p, jw + (uint32_t)(kMWaves * p));
-        VX_MG_LOADX(0, jw);
-        for (uint32_t j = jw; j <= jlast; j += (uint32_t)(kMWaves * PD)) {
-#pragma unroll
-            for (int p = 0; p < PD; ++p) {
-                // loads stay outside the branch (clamped, in bounds), so the compiler's waits at the
-                // join do not drain the groups in flight
-                const uint32_t jj = j + (uint32_t)(kMWaves * p);
-                const int cur = p & 1;
-                VX_MG_LOADX(cur ^ 1, jj + (uint32_t)kMWaves);
-                if (jj <= jlast) {
-#pragma unroll
-                    for (int b = 0; b < 4; ++b)
-#pragma unroll
-                        for (int nt = 0; nt < NT; ++nt) {
-                            const vx_mh8 wb = vx_munpack8(cw[p][nt][b]);
-                            const uint32_t sv = b < 2 ? sw[p][nt].x : sw[p][nt].y;
-                            const float d = vx_mh2f((sv >> (16 * (b & 1))) & 0xFFFFu);
-#pragma unroll
-                            for (int mt = 0; mt < MT; ++mt) {
-                                const vx_mf4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[cur][mt][b], wb,
-                                                                                        vx_mf4{0.f, 0.f, 0.f, 0.f}, 0,
-                                                                                        0, 0);
-                                acc[nt][mt] += d * c;
-                            }
-                        }
-                }
-                VX_MG_LOADW(p, jj + (uint32_t)(kMWaves * PD));
-            }
-            // PD odd: the x buffer parity alternates across outer iterations
-            if constexpr (PD & 1) {
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) xa[0][mt][b] = xa[1][mt][b];
-            }
+#define VX_MG_COMPUTE(cw_, sw_, xa_)                                                              \
+    do {                                                                                          \
+        _Pragma("unroll") for (int b = 0; b < 4; ++b)                                             \
+        _Pragma("unroll") for (int nt = 0; nt < NT; ++nt) {                                       \
+            const vx_mh8 wb = vx_munpack8(cw_[nt][b], e6400);                                     \
+            const vx_mh2 sh = __builtin_bit_cast(vx_mh2, b < 2 ? sw_[nt].x : sw_[nt].y);          \
+            const float d = (float)sh[b & 1];                                                     \
+            _Pragma("unroll") for (int mt = 0; mt < MT; ++mt) {                                   \
+                const vx_mf4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa_[mt][b], wb,           \
+                                                                        vx_mf4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0); \
+                acc[nt][mt] += d * c;                                                             \
+            }                                                                                     \
+        }                                                                                         \
+    } while (0)
+        VX_MG_LOAD(cwA, swA, xaA, jw);
+        uint32_t i = 0;
+        for (; i + 2u <= ngw; i += 2u) {
+            const uint32_t jj = jw + i * (uint32_t)kMWaves;
+            VX_MG_LOAD(cwB, swB, xaB, jj + (uint32_t)kMWaves);
+            VX_MG_COMPUTE(cwA, swA, xaA);
+            VX_MG_LOAD(cwA, swA, xaA, jj + 2u * (uint32_t)kMWaves);  // past the last group: clamped
+            VX_MG_COMPUTE(cwB, swB, xaB);
         }
-#undef VX_MG_LOADW
-#undef VX_MG_LOADX
+        if (i < ngw) VX_MG_COMPUTE(cwA, swA, xaA);  // odd count: set A holds the last group
+#undef VX_MG_LOAD
+#undef VX_MG_COMPUTE
     }
 
     // ---- the 4 waves' partial sums, added in wave order (deterministic) ----
@@ -315,36 +320,17 @@ namespace {
 
 constexpr int kMNT = 2;  // tiles per wave (a gate/up pair for SWIGLU)
 
-int vx_mgemm_pd() {
-    static int pd = 0;
-    if (!pd) {
-        const char* env = std::getenv("VELOX_HIP_MGEMM_PD");  // tuning: weight groups in flight per wave
-        pd = env ? std::atoi(env) : 1;  // measured: 1 beats 2 and 4 (fewer registers, more waves)
-        if (pd != 1 && pd != 2 && pd != 4) pd = 1;
-    }
-    return pd;
-}
-
-template <int EPI, int MT, int PD>
+template <int EPI, int MT>
 hipError_t vx_mgemm_launch_t(const VxMMat& w, const VxBGemmArgs& a, hipStream_t st) {
     const dim3 grid(vx_mgemm_grid(w.n_tiles), a.ksplit > 1u ? a.ksplit : 1u);
-    hipLaunchKernelGGL((vx_mgemm_kernel<EPI, MT, kMNT, PD>), grid, dim3(kMThreads), 0, st, w, a);
+    hipLaunchKernelGGL((vx_mgemm_kernel<EPI, MT, kMNT>), grid, dim3(kMThreads), 0, st, w, a);
     return hipGetLastError();
-}
-
-template <int EPI, int MT>
-hipError_t vx_mgemm_dispatch_pd(const VxMMat& w, const VxBGemmArgs& a, hipStream_t st) {
-    switch (vx_mgemm_pd()) {
-        case 2: return vx_mgemm_launch_t<EPI, MT, 2>(w, a, st);
-        case 4: return vx_mgemm_launch_t<EPI, MT, 4>(w, a, st);
-        default: return vx_mgemm_launch_t<EPI, MT, 1>(w, a, st);
-    }
 }
 
 template <int EPI>
 hipError_t vx_mgemm_dispatch_mt(const VxMMat& w, const VxBGemmArgs& a, hipStream_t st) {
     if (a.batch == 0 || a.batch > 32) return hipErrorInvalidValue;
-    return a.batch <= 16 ? vx_mgemm_dispatch_pd<EPI, 1>(w, a, st) : vx_mgemm_dispatch_pd<EPI, 2>(w, a, st);
+    return a.batch <= 16 ? vx_mgemm_launch_t<EPI, 1>(w, a, st) : vx_mgemm_launch_t<EPI, 2>(w, a, st);
 }
 
 }  // namespace
