@@ -42,9 +42,11 @@ def common_flags() -> list[str]:
     ]
 
 
-# Per-file code generation flags. The batched GEMM keeps MFMA results in VGPRs: its scale FMA reads
-# every MFMA result, and the AGPR form cost four v_accvgpr_read per MFMA (a quarter of its loop).
-FILE_FLAGS = {"vx_mgemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-file code generation flags. The batched Q4_0 GEMM and the fp8 GEMMs of the MLA layer keep MFMA
+# results in VGPRs: their scale FMAs read every MFMA result, and the AGPR form cost four
+# v_accvgpr_read per MFMA (a quarter of the Q4_0 GEMM's loop, a fifth of the fp8 GEMM's).
+_VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+FILE_FLAGS = {"vx_mgemm.hip": _VGPR_MFMA, "vx_mla.hip": _VGPR_MFMA}
 
 
 def build(verbose: bool = False) -> str:

@@ -477,7 +477,8 @@ __global__ __launch_bounds__(64) void vx_prefill_rows_kernel(VeloxDecodeState* r
 
 // K/V of every row into the one sequence's cache before the chunk's attention reads them: RoPE of
 // k at the row's position (src/runtime.rs:745-768), bf16 K row and V slot.
-__global__ __launch_bounds__(64) void vx_kv_append_rows_kernel(const float* qkv, uint32_t ldq, uint32_t hq,
+__global__ __launch_bounds__(64) void vx_kv_append_rows_kernel(const float* qkv, uint32_t ldq, uint32_t nparts,
+                                                               uint64_t pstride, const float* bias, uint32_t hq,
                                                                uint32_t hkv, uint32_t d, const VeloxDecodeState* rows,
                                                                const float2* rope, uint32_t s_max, uint32_t s_cap,
                                                                uint16_t* kv, uint64_t mask) {
@@ -485,13 +486,20 @@ __global__ __launch_bounds__(64) void vx_kv_append_rows_kernel(const float* qkv,
     const uint32_t g = blockIdx.x, r = blockIdx.y, half = d / 2u;
     const uint64_t step = rows[r].step;
     const uint32_t pos = step < (uint64_t)s_max ? (uint32_t)step : s_max - 1u;
-    const float* k = qkv + (size_t)r * ldq + (size_t)hq * d + (size_t)g * d;
-    const float* v = qkv + (size_t)r * ldq + (size_t)(hq + hkv) * d + (size_t)g * d;
+    const uint32_t kc = (hq + g) * d, vc = (hq + hkv + g) * d;  // columns of this group's k and v
+    const float* row = qkv + (size_t)r * ldq;
+    // element c of the row: the value, or its K-split partials summed in split order (+ bias)
+    auto at = [&](uint32_t c) {
+        if (nparts == 0) return row[c];
+        float acc = 0.0f;
+        for (uint32_t p = 0; p < nparts; ++p) acc += row[p * pstride + c];
+        return bias ? acc + bias[c] : acc;
+    };
     uint16_t* Kc = kv + (size_t)g * s_cap * d;
     uint16_t* Vc = kv + ((size_t)hkv + g) * s_cap * d;
     for (uint32_t j = threadIdx.x; j < half; j += 64u) {
         const float2 cs = rope[(size_t)pos * half + j];
-        const float x1 = k[j], x2 = k[j + half];
+        const float x1 = at(kc + j), x2 = at(kc + j + half);
         float o1, o2;
         {
 #pragma clang fp contract(off)
@@ -502,7 +510,7 @@ __global__ __launch_bounds__(64) void vx_kv_append_rows_kernel(const float* qkv,
         Kc[(size_t)pos * d + j + half] = vx_f32_to_bf16_bits(o2);
     }
     uint16_t* vb = Vc + (size_t)(pos >> 5) * d * 32u + vx_vslot(pos & 31u);
-    for (uint32_t i = threadIdx.x; i < d; i += 64u) vb[(size_t)i * 32u] = vx_f32_to_bf16_bits(v[i]);
+    for (uint32_t i = threadIdx.x; i < d; i += 64u) vb[(size_t)i * 32u] = vx_f32_to_bf16_bits(at(vc + i));
 }
 
 // Per row: the argmax over the LM head's candidates into the ring at the row's position; the last
@@ -556,12 +564,13 @@ hipError_t vx_launch_prefill_rows(VeloxDecodeState* rows, uint32_t n_rows, uint6
     return hipGetLastError();
 }
 
-hipError_t vx_launch_kv_append_rows(const float* qkv, uint32_t ldq, uint32_t hq, uint32_t hkv, uint32_t d,
+hipError_t vx_launch_kv_append_rows(const float* qkv, uint32_t ldq, uint32_t nparts, uint64_t pstride,
+                                    const float* bias, uint32_t hq, uint32_t hkv, uint32_t d,
                                     const VeloxDecodeState* rows, uint32_t n_rows, const float2* rope, uint32_t s_max,
                                     uint32_t s_cap, uint16_t* kv, uint64_t mask, hipStream_t st) {
-    if ((s_cap & 31u) || s_cap < s_max || (d & 1u)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(vx_kv_append_rows_kernel, dim3(hkv, n_rows), dim3(64), 0, st, qkv, ldq, hq, hkv, d, rows, rope,
-                       s_max, s_cap, kv, mask);
+    if ((s_cap & 31u) || s_cap < s_max || (d & 1u) || nparts > 8) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(vx_kv_append_rows_kernel, dim3(hkv, n_rows), dim3(64), 0, st, qkv, ldq, nparts, pstride, bias,
+                       hq, hkv, d, rows, rope, s_max, s_cap, kv, mask);
     return hipGetLastError();
 }
 

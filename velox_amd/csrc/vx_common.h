@@ -146,6 +146,13 @@ struct VxAttnArgs {
     uint32_t batch;
     uint64_t kv_bstride;
     uint32_t qkv_bstride;
+    // q/k/v as the K-split partials of the batched QKV GEMM (qkv_nparts > 0): element c of row b is
+    // sum_{p < qkv_nparts} qkv_part[p * qkv_pstride + b * qkv_bstride + c] (+ qkv_bias[c]), summed in
+    // split order as the partial-sum kernel would; qkv is then unused
+    const float* qkv_part;
+    const float* qkv_bias;
+    uint64_t qkv_pstride;
+    uint32_t qkv_nparts;
 };
 
 // Batched (B <= 32 sequences) Q4_0 GEMM: Y[m][n] = sum_k X[m][k] W[n][k] for fp16 activations
@@ -230,7 +237,9 @@ uint32_t vx_bgemm_grid(uint32_t n_tiles, uint32_t s);
 // Batched prefill (vx_batch.hip): row r of a chunk is position p0 + r of the one sequence.
 hipError_t vx_launch_prefill_rows(VeloxDecodeState* rows, uint32_t n_rows, uint64_t p0, const uint32_t* prompt,
                                   uint64_t mask, hipStream_t st);
-hipError_t vx_launch_kv_append_rows(const float* qkv, uint32_t ldq, uint32_t hq, uint32_t hkv, uint32_t d,
+// qkv rows ldq apart; nparts > 0: qkv holds nparts K-split partials pstride apart (+ bias), summed here
+hipError_t vx_launch_kv_append_rows(const float* qkv, uint32_t ldq, uint32_t nparts, uint64_t pstride,
+                                    const float* bias, uint32_t hq, uint32_t hkv, uint32_t d,
                                     const VeloxDecodeState* rows, uint32_t n_rows, const float2* rope, uint32_t s_max,
                                     uint32_t s_cap, uint16_t* kv, uint64_t mask, hipStream_t st);
 hipError_t vx_launch_prefill_finalize(const float* cand_v, const uint32_t* cand_i, uint32_t n,

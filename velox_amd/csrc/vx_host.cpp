@@ -868,11 +868,15 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
             g.pstride = (uint64_t)M->rows * g.ldy;
         }
         vx_record(gemm(L.qkv, g, VX_EPI_STORE));
-        if (g.ksplit > 1)
-            vx_record(vx_launch_msum(part_r, g.ksplit, g.pstride, g.bias, qkv, g.ldy, g.ldy, n, 0, mask, st));
+        // QKV split over K: the K/V-row and attention kernels sum the partials (+ bias) themselves
+        at.qkv_nparts = g.ksplit > 1 ? g.ksplit : 0u;
+        at.qkv_part = part_r;
+        at.qkv_pstride = g.pstride;
+        at.qkv_bias = g.bias;
         at.kv = vx_kv(A, l, 0);
         if (prefill)
-            vx_record(vx_launch_kv_append_rows(qkv, qd + 2 * kvd, c.num_heads, c.num_kv_heads, D, rows, n, at.rope,
+            vx_record(vx_launch_kv_append_rows(at.qkv_nparts ? part_r : qkv, qd + 2 * kvd, at.qkv_nparts, g.pstride,
+                                               g.bias, c.num_heads, c.num_kv_heads, D, rows, n, at.rope,
                                                c.max_seq_len, M->s_cap, at.kv, mask, st));
         vx_record(vx_launch_attention(at, D, st));
         vx_record(vx_launch_bmerge(at.part_o, at.part_ml, c.num_heads, D, bsplits, xa, M->x_ld, M->x_bs, n, mask, st));

@@ -559,7 +559,7 @@ constexpr size_t vx_attn_lds_bytes() {
            (size_t)W * vx_attn_hrows<D, G>() * D * 4;
 }
 
-template <int D, int G, int W>
+template <int D, int G, int W, bool PS>
 __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     if ((a.active_mask & 1ULL) == 0ULL) return;
     constexpr int HALF = D / 2, NT = 64 * W, NC = D / 32, NB = D / 16, HR = vx_attn_hrows<D, G>();
@@ -583,20 +583,47 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     uint16_t* Vc = kvb + ((size_t)a.hkv + g) * a.s_cap * D;
 
     // ---- q, the new k/v into registers (clamped: no load under a branch) ----
-    const float* q = a.qkv + (size_t)bq * a.qkv_bstride;
-    const float* k = q + (size_t)a.hq * D;
-    const float* v = k + (size_t)a.hkv * D;
     constexpr int NP = (G + 1) * HALF, RP = (NP + NT - 1) / NT;  // RoPE pairs, pairs per thread
-    float r1[RP], r2[RP];
+    float r1[RP], r2[RP], vnew;
+    if constexpr (!PS) {
+        const float* q = a.qkv + (size_t)bq * a.qkv_bstride;
+        const float* k = q + (size_t)a.hq * D;
+        const float* v = k + (size_t)a.hkv * D;
 #pragma unroll
-    for (int i = 0; i < RP; ++i) {
-        const int p = min(tid + i * NT, NP - 1);
-        const int hh = p / HALF, j = p % HALF;
-        const float* src = hh < G ? q + (size_t)(g * G + hh) * D : k + (size_t)g * D;
-        r1[i] = src[j];
-        r2[i] = src[j + HALF];
+        for (int i = 0; i < RP; ++i) {
+            const int p = min(tid + i * NT, NP - 1);
+            const int hh = p / HALF, j = p % HALF;
+            const float* src = hh < G ? q + (size_t)(g * G + hh) * D : k + (size_t)g * D;
+            r1[i] = src[j];
+            r2[i] = src[j + HALF];
+        }
+        vnew = v[(size_t)g * D + min(tid, D - 1)];
+    } else {
+        const uint32_t vcol = (a.hq + a.hkv + g) * (uint32_t)D + (uint32_t)min(tid, D - 1);
+        // K-split partials of the batched QKV GEMM: every partial of an element loaded before the
+        // adds, summed in split order, then the bias
+        const float* base = a.qkv_part + (size_t)bq * a.qkv_bstride;
+        const uint32_t np = a.qkv_nparts;
+        auto qkv_at = [&](uint32_t c) {
+            float t[8];
+#pragma unroll
+            for (uint32_t s = 0; s < 8; ++s) t[s] = base[min(s, np - 1u) * a.qkv_pstride + c];
+            float acc = 0.0f;
+#pragma unroll
+            for (uint32_t s = 0; s < 8; ++s)
+                if (s < np) acc += t[s];
+            return a.qkv_bias ? acc + a.qkv_bias[c] : acc;
+        };
+#pragma unroll
+        for (int i = 0; i < RP; ++i) {
+            const int p = min(tid + i * NT, NP - 1);
+            const int hh = p / HALF, j = p % HALF;
+            const uint32_t c0 = (hh < G ? (g * G + hh) : (a.hq + g)) * (uint32_t)D + (uint32_t)j;
+            r1[i] = qkv_at(c0);
+            r2[i] = qkv_at(c0 + HALF);
+        }
+        vnew = qkv_at(vcol);
     }
-    const float vnew = v[(size_t)g * D + min(tid, D - 1)];
 
     // ---- one 32-position chunk into registers: K rows cb + 16 b + col, dimensions 32 c + 8 grp;
     // V block cb / 32, dimensions 16 nb + col (clamped to the capacity; positions at or past the
@@ -1058,21 +1085,29 @@ hipError_t vx_gemv_dispatch_norm(uint32_t s, const VxGemvArgs& a, uint32_t max_w
     }
 }
 
-template <int D, int G>
-hipError_t vx_attn_launch_t(const VxAttnArgs& a, hipStream_t st) {
+template <int D, int G, bool PS>
+hipError_t vx_attn_launch_ps(const VxAttnArgs& a, hipStream_t st) {
     constexpr int W = 8;
     constexpr size_t lds = vx_attn_lds_bytes<D, G, W>();
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)vx_attn_kernel<D, G, W>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        if (hipFuncSetAttribute((const void*)vx_attn_kernel<D, G, W, PS>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds) != hipSuccess) {
             (void)hipGetLastError();
             return hipErrorInvalidValue;
         }
         attr_set = true;
     }
-    hipLaunchKernelGGL((vx_attn_kernel<D, G, W>), dim3(a.splits, a.hkv, a.batch ? a.batch : 1u), dim3(64 * W), lds,
+    hipLaunchKernelGGL((vx_attn_kernel<D, G, W, PS>), dim3(a.splits, a.hkv, a.batch ? a.batch : 1u), dim3(64 * W), lds,
                        st, a);
+    return hipGetLastError();
+}
+
+template <int D, int G>
+hipError_t vx_attn_launch_t(const VxAttnArgs& a, hipStream_t st) {
+    if (a.qkv_nparts > 8 || (a.qkv_nparts && (!a.qkv_part || a.partials_only == 0))) return hipErrorInvalidValue;
+    hipError_t e0 = a.qkv_nparts ? vx_attn_launch_ps<D, G, true>(a, st) : vx_attn_launch_ps<D, G, false>(a, st);
+    if (e0 != hipSuccess) return e0;
     hipError_t e = hipGetLastError();
     if (e == hipSuccess && a.splits > 1 && !a.partials_only) {
         if (a.batch > 1) return hipErrorInvalidValue;  // batched steps merge with vx_bmerge_kernel
