@@ -331,11 +331,13 @@ __global__ __launch_bounds__(1024) void vx_mla_prep_kernel(VxMlaPrepArgs a) {
     float* qs = (float*)vm_smem;                  // [q_lora]
     float* cs = qs + (a.q_lora ? a.q_lora : 1u);  // [lr + dr]
     __shared__ float red[16];
-    const uint32_t b = blockIdx.x, tid = threadIdx.x;
+    // grid (batch, 2): workgroup y = 0 takes the q outputs, y = 1 the latent and rope outputs
+    const uint32_t b = blockIdx.x, tid = threadIdx.x, part = blockIdx.y;
     const uint64_t step = a.states[b].step;
     const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;
     const float* pb = a.parts + (size_t)b * a.na;
-    for (uint32_t i = tid; i < a.na; i += 1024u) {
+    const uint32_t i_lo = part ? a.q_part : 0u, i_hi = part ? a.na : a.q_part;
+    for (uint32_t i = i_lo + tid; i < i_hi; i += 1024u) {
         float p[kMlaMaxParts];
 #pragma unroll
         for (uint32_t s = 0; s < kMlaMaxParts; ++s) p[s] = pb[min(s, a.nparts - 1u) * a.pstride + i];
@@ -351,16 +353,19 @@ __global__ __launch_bounds__(1024) void vx_mla_prep_kernel(VxMlaPrepArgs a) {
         }
     }
     __syncthreads();
-    if (a.q_lora) {
-        float ss = 0.0f;
-        for (uint32_t i = tid; i < a.q_lora; i += 1024u) ss += qs[i] * qs[i];
-        ss = vm_block_sum<1024>(ss, red);
-        const float inv = 1.0f / sqrtf(ss / (float)a.q_lora + a.eps);
-        for (uint32_t i = tid; i < a.q_lora; i += 1024u) {
+    if (part == 0) {
+        if (a.q_lora) {
+            float ss = 0.0f;
+            for (uint32_t i = tid; i < a.q_lora; i += 1024u) ss += qs[i] * qs[i];
+            ss = vm_block_sum<1024>(ss, red);
+            const float inv = 1.0f / sqrtf(ss / (float)a.q_lora + a.eps);
+            for (uint32_t i = tid; i < a.q_lora; i += 1024u) {
 #pragma clang fp contract(off)
-            const float v = (qs[i] * inv) * a.g_qa[i];
-            a.q16[(size_t)b * a.ldq16 + i] = __half_as_ushort(__float2half(v));
+                const float v = (qs[i] * inv) * a.g_qa[i];
+                a.q16[(size_t)b * a.ldq16 + i] = __half_as_ushort(__float2half(v));
+            }
         }
+        return;
     }
     uint16_t* row = a.cache + (size_t)b * a.cache_bstride + (size_t)pos * (a.lr + a.dr);
     float inv = 1.0f;
@@ -582,8 +587,10 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
     }
 }
 
-// LSE merge of the split partials of one (head, sequence) -> ctx[b][h][LR] fp32.
-__global__ __launch_bounds__(256) void vx_mla_merge_kernel(const float* part_o, const float* part_ml, uint32_t nh,
+// LSE merge of the split partials of one (head, sequence) -> ctx[b][h][LR] fp32. A workgroup covers
+// 128 latent dimensions of its (head, sequence) (grid z), one per thread, with 8 splits' loads in
+// flight ahead of their adds (the adds stay in split order).
+__global__ __launch_bounds__(128) void vx_mla_merge_kernel(const float* part_o, const float* part_ml, uint32_t nh,
                                                            uint32_t splits, uint32_t lr, float* ctx, uint64_t mask) {
     if ((mask & 1ULL) == 0ULL) return;
     __shared__ float s_w[64];
@@ -604,11 +611,18 @@ __global__ __launch_bounds__(256) void vx_mla_merge_kernel(const float* part_o, 
     }
     __syncthreads();
     const float* po = part_o + bh * splits * lr;
-    for (uint32_t d = threadIdx.x; d < lr; d += 256u) {
-        float acc = 0.0f;
-        for (uint32_t j = 0; j < splits; ++j) acc += s_w[j] * po[(size_t)j * lr + d];
-        ctx[bh * lr + d] = acc;
+    const uint32_t d = blockIdx.z * 128u + threadIdx.x;
+    if (d >= lr) return;
+    float acc = 0.0f;
+    for (uint32_t j0 = 0; j0 < splits; j0 += 8u) {
+        float v[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) v[u] = po[(size_t)min(j0 + u, splits - 1u) * lr + d];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u)
+            if (j0 + u < splits) acc += s_w[j0 + u] * v[u];
     }
+    ctx[bh * lr + d] = acc;
 }
 
 // h[b] += the K-split partials of W_o, in split order.
@@ -626,7 +640,7 @@ hipError_t vx_launch_mla_prep(const VxMlaPrepArgs& a, uint32_t batch, hipStream_
     const size_t lds = ((size_t)(a.q_lora ? a.q_lora : 1u) + a.lr + a.dr) * 4;
     if (lds > 60000 || a.na != a.q_part + a.lr + a.dr || (a.dr & 1u) || a.nparts == 0 || a.nparts > kMlaMaxParts)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(vx_mla_prep_kernel, dim3(batch), dim3(1024), lds, st, a);
+    hipLaunchKernelGGL(vx_mla_prep_kernel, dim3(batch, 2), dim3(1024), lds, st, a);
     return hipGetLastError();
 }
 
@@ -657,9 +671,9 @@ hipError_t vx_launch_mla_attn(const VxMlaAttnArgs& a, uint32_t lr, uint32_t dr, 
 
 hipError_t vx_launch_mla_merge(const float* part_o, const float* part_ml, uint32_t nh, uint32_t splits, uint32_t lr,
                                float* ctx, uint32_t batch, uint64_t mask, hipStream_t st) {
-    if (splits == 0 || splits > 64) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(vx_mla_merge_kernel, dim3(nh, batch), dim3(256), 0, st, part_o, part_ml, nh, splits, lr, ctx,
-                       mask);
+    if (splits == 0 || splits > 64 || lr == 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(vx_mla_merge_kernel, dim3(nh, batch, (lr + 127u) / 128u), dim3(128), 0, st, part_o, part_ml, nh,
+                       splits, lr, ctx, mask);
     return hipGetLastError();
 }
 
