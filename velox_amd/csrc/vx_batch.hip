@@ -488,11 +488,17 @@ __global__ __launch_bounds__(64) void vx_kv_append_rows_kernel(const float* qkv,
     const uint32_t pos = step < (uint64_t)s_max ? (uint32_t)step : s_max - 1u;
     const uint32_t kc = (hq + g) * d, vc = (hq + hkv + g) * d;  // columns of this group's k and v
     const float* row = qkv + (size_t)r * ldq;
-    // element c of the row: the value, or its K-split partials summed in split order (+ bias)
+    // element c of the row: the value, or its K-split partials summed in split order (+ bias), every
+    // partial's load issued before the first add
     auto at = [&](uint32_t c) {
         if (nparts == 0) return row[c];
+        float t[8];
+#pragma unroll
+        for (uint32_t p = 0; p < 8; ++p) t[p] = row[min(p, nparts - 1u) * pstride + c];
         float acc = 0.0f;
-        for (uint32_t p = 0; p < nparts; ++p) acc += row[p * pstride + c];
+#pragma unroll
+        for (uint32_t p = 0; p < 8; ++p)
+            if (p < nparts) acc += t[p];
         return bias ? acc + bias[c] : acc;
     };
     uint16_t* Kc = kv + (size_t)g * s_cap * d;
