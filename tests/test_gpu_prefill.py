@@ -123,6 +123,12 @@ def test_prefill_llama_gqa_vs_oracle(oracle):
     _prefill_vs_oracle(oracle, LLAMA_SMALL_VOCAB, 2, 24, 50, [(0, 50)], 64, seed=75, decode_steps=2)
 
 
+def test_prefill_64_and_48_row_chunks_vs_oracle(oracle):
+    """Chunks of 64 rows (four MFMA row tiles) and of 48 (three), Llama-shaped and SmolLM layers."""
+    _prefill_vs_oracle(oracle, LLAMA_SMALL_VOCAB, 2, 64, 100, [(0, 100)], 128, seed=79, decode_steps=2)
+    _prefill_vs_oracle(oracle, SMOLLM, 2, 48, 60, [(0, 60)], 64, seed=80, decode_steps=1)
+
+
 def test_prefill_chunking_invariance(oracle):
     """The same prompt in chunks of 32 and of 7 (and, for layer 0, token by token): each row's
     arithmetic does not depend on the chunk it is in, up to fp32 accumulation order, so the final
@@ -183,7 +189,7 @@ def test_prefill_rejects_bad_arguments():
     b.close()
     c = L.ModelConfig()
     L.check(lib.velox_hip_builtin_config(b"smollm_135m", 32, C.byref(c)))
-    c.prefill_chunk = 33
+    c.prefill_chunk = 65
     m = C.c_void_p()
     assert lib.velox_hip_model_create(C.byref(c), C.byref(m)) == L.EINVAL
 

@@ -329,8 +329,11 @@ hipError_t vx_mgemm_launch_t(const VxMMat& w, const VxBGemmArgs& a, hipStream_t 
 
 template <int EPI>
 hipError_t vx_mgemm_dispatch_mt(const VxMMat& w, const VxBGemmArgs& a, hipStream_t st) {
-    if (a.batch == 0 || a.batch > 32) return hipErrorInvalidValue;
-    return a.batch <= 16 ? vx_mgemm_launch_t<EPI, 1>(w, a, st) : vx_mgemm_launch_t<EPI, 2>(w, a, st);
+    if (a.batch == 0 || a.batch > 64) return hipErrorInvalidValue;
+    if (a.batch <= 16) return vx_mgemm_launch_t<EPI, 1>(w, a, st);
+    if (a.batch <= 32) return vx_mgemm_launch_t<EPI, 2>(w, a, st);
+    if (a.batch <= 48) return vx_mgemm_launch_t<EPI, 3>(w, a, st);
+    return vx_mgemm_launch_t<EPI, 4>(w, a, st);
 }
 
 }  // namespace

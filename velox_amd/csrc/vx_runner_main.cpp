@@ -7,7 +7,7 @@
 //                    [--context-len N] [--steps N] [--warmup N] [--seed S] [--layers L]
 //                    [--prefill-chunk N] [--no-cuda-graph] [--verbose]
 //
-// --prefill-chunk N (2..32) prefills the prompt N positions per batched step (one weight pass per
+// --prefill-chunk N (2..64) prefills the prompt N positions per batched step (one weight pass per
 // chunk) instead of the reference's one decode step per prompt token; TTFT reports either.
 //
 // Weights are the seeded synthetic Q4_0 model (`--weights synthetic`, what src/cli.rs:654 passes
@@ -58,8 +58,8 @@ int main(int argc, char** argv) {
         else if (!std::strcmp(a, "--layers")) layers = (uint32_t)std::atoi(next());
         else if (!std::strcmp(a, "--prefill-chunk")) {
             prefill_chunk = (uint32_t)std::atoi(next());
-            if (prefill_chunk < 2 || prefill_chunk > 32) {
-                std::fprintf(stderr, "Error: --prefill-chunk takes 2..32 positions\n");
+            if (prefill_chunk < 2 || prefill_chunk > 64) {
+                std::fprintf(stderr, "Error: --prefill-chunk takes 2..64 positions\n");
                 return 1;
             }
         }
