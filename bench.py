@@ -152,6 +152,9 @@ def main() -> int:
                     help="decode B <= 32 independent sequences per step (batched MFMA GEMMs); value = all tokens/s")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="afterwards run a device-to-device copy of MIB MiB (byte-counter yardstick)")
+    ap.add_argument("--prefill-chunk", type=int, default=64,
+                    help="beside the headline, time the prompt's batched prefill in chunks of N positions "
+                         "(velox_hip_prefill_batch; 0 skips it)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures the single-GPU decode step only; --gpus {args.gpus} is not supported "
@@ -175,10 +178,22 @@ def main() -> int:
     print(f"[bench] decode done: {rep['tok_per_s']:.1f} tok/s, {rep['hbm_gbps']:.0f} GB/s; gate/up kernel "
           f"{rep['kernel_us']:.2f} us", file=sys.stderr, flush=True)
 
+    headline = args.model == "llama3_8b" and ctx == 0 and args.batch == 1
+    prefill = None
+    if headline and args.prefill_chunk > 1:
+        # time to first token with the batched prefill, same prompt, against the token-by-token
+        # prefill of the run above (the reference runner's flow)
+        rep_p, toks_p = run(args.model, prompt_len=plen, warmup=0, steps=1, seed=args.seed,
+                            use_graph=not args.no_graph, prefill_chunk=args.prefill_chunk)
+        prefill = {"prompt_tokens": plen, "chunk": args.prefill_chunk,
+                   "token_by_token_ms": round(rep["prefill_ms"], 3), "batched_ms": round(rep_p["prefill_ms"], 3),
+                   "first_token_equal": toks_p[plen - 1] == toks[plen - 1]}
+        print(f"[bench] batched prefill: {rep_p['prefill_ms']:.2f} ms vs {rep['prefill_ms']:.2f} ms token by token",
+              file=sys.stderr, flush=True)
+
     if args.copy_calibration > 0:
         L.device_copy_calibration(args.copy_calibration << 20)
     kernel_gbps = rep["kernel_bytes"] / (rep["kernel_us"] * 1e-6) / 1e9 if rep["kernel_us"] > 0 else 0.0
-    headline = args.model == "llama3_8b" and ctx == 0 and args.batch == 1
     workload = f"{args.model}_q4_0_decode_bs{args.batch}" + (f"_ctx{ctx}" if ctx else "")
     out = {
         "metric": METRIC if headline else f"decode tok/s + achieved HBM GB/s, {args.model} Q4_0 bs={args.batch}"
@@ -223,6 +238,8 @@ def main() -> int:
         },
         "first_tokens": toks[plen - 1:plen + 7],  # ring entries from position ctx on
     }
+    if prefill:
+        out["prefill"] = prefill
     if not args.no_cpu_baseline and headline:
         print("[bench] cpu baseline (oracle, bounded sample)...", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(args.seed)
