@@ -83,6 +83,13 @@ def test_mla_deepseek_shape_vs_oracle(oracle):
     _check_layer(oracle, "deepseek_v3_mla", batch=2, ctxs=[37, 100], steps=1, max_seq=160, norm_sigma=0.0)
 
 
+def test_mla_deepseek_shape_batched_vs_oracle(oracle):
+    """17 sequences: two 16-row activation tiles per GEMM wave, and GEMM waves over 4, 2 or 1 row tiles
+    (the launcher takes fewer row tiles per wave where 4 would leave fewer than 256 workgroups)."""
+    _check_layer(oracle, "deepseek_v3_mla", batch=17, ctxs=[1 + 9 * i for i in range(17)], steps=1, max_seq=160,
+                 norm_sigma=0.0)
+
+
 def test_mla_synthesized_weights_equal_loaded_codes(oracle):
     """The device quantizer and tile maps: loading the oracle's fp8 codes and block scales through the
     checkpoint entry point gives bit-identical layer outputs to the device-synthesized weights."""

@@ -214,6 +214,7 @@ struct VxF8GemmArgs {
     const void* x;          // [batch][ldx] fp16 (x_f32 == 0) or fp32
     uint32_t ldx, x_f32;
     float* y;               // [batch][ldy]
+    uint16_t* y16;          // != nullptr (ksplit 1): fp16 output [batch][ldy] in place of y
     uint32_t ldy, ksplit;
     uint64_t w_gstride, s_gstride, x_gstride, y_gstride, pstride;
     uint64_t active_mask;

@@ -195,6 +195,17 @@ __global__ __launch_bounds__(64 * kFWaves) void vx_f8gemm_kernel(VxF8GemmArgs a)
     for (int r = 0; r < MR; ++r) {
         const uint32_t rt = rt0 + (uint32_t)r;
         if (rt >= a.n_rt) continue;
+        if (a.y16) {  // fp16 for a following GEMM: the rounding its fp32 activation loads would apply
+            uint16_t* y = a.y16 + g * a.y_gstride + 16u * rt + col;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t m = (uint32_t)(16 * mt + 4 * grp + i);
+                    if (m < a.batch) y[(size_t)m * a.ldy] = __builtin_bit_cast(uint16_t, (_Float16)acc[r][mt][i]);
+                }
+            continue;
+        }
         float* y = a.y + g * a.y_gstride + (gridDim.y > 1u ? ks * a.pstride : 0u) + 16u * rt + col;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
@@ -226,12 +237,20 @@ hipError_t vx_launch_f8gemm(const VxF8GemmArgs& a, uint32_t groups, hipStream_t 
         groups == 0 || (a.ldx & 7u) || a.n_kb != (a.n_kt + 1u) / 2u)
         return hipErrorInvalidValue;
     if (a.ksplit > 1u && a.pstride < (uint64_t)a.batch * a.ldy) return hipErrorInvalidValue;
-    const bool mr4 = vx_f8gemm_rows_per_wave(a.batch) == 4u;
+    if ((a.y16 != nullptr) == (a.y != nullptr) || (a.y16 && a.ksplit != 1u)) return hipErrorInvalidValue;
+    // fewer row tiles per wave while the grid would leave CUs idle (< 256 workgroups): a wave's row
+    // tiles only share its activation loads, the per-row arithmetic is the same
+    uint32_t mr = vx_f8gemm_rows_per_wave(a.batch);
+    auto wgs = [&](uint32_t r) { return (a.n_rt + kFWaves * r - 1u) / (kFWaves * r) * a.ksplit * groups; };
+    while (mr > 1u && wgs(mr) < 256u) mr >>= 1;
     if (a.batch <= 16) {
-        if (mr4) vx_f8gemm_launch_t<1, 4>(a, groups, st);
+        if (mr == 4u) vx_f8gemm_launch_t<1, 4>(a, groups, st);
+        else if (mr == 2u) vx_f8gemm_launch_t<1, 2>(a, groups, st);
         else vx_f8gemm_launch_t<1, 1>(a, groups, st);
     } else {
-        vx_f8gemm_launch_t<2, 4>(a, groups, st);
+        if (mr == 4u) vx_f8gemm_launch_t<2, 4>(a, groups, st);
+        else if (mr == 2u) vx_f8gemm_launch_t<2, 2>(a, groups, st);
+        else vx_f8gemm_launch_t<2, 1>(a, groups, st);
     }
     return hipGetLastError();
 }

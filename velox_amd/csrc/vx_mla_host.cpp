@@ -431,7 +431,7 @@ void velox_hip_mla_layer_step(VeloxHipMla* m, uint32_t layer, uint32_t batch, ui
     uint16_t* x16 = (uint16_t*)vm_act(m, m->a_x16);
     uint16_t* cache = (uint16_t*)(m->base + m->o_cache + m->cache_layer_bytes * layer);
     auto gemm = [&](const VmF8Plan& p, const void* x, uint32_t ldx, uint64_t x_gstride, uint32_t x_f32, float* y,
-                    uint32_t ldy, uint64_t y_gstride, uint32_t ksplit, uint64_t pstride) {
+                    uint32_t ldy, uint64_t y_gstride, uint32_t ksplit, uint64_t pstride, uint16_t* y16 = nullptr) {
         VxF8GemmArgs g;
         std::memset(&g, 0, sizeof(g));
         g.codes = codes + p.code_off / 16;
@@ -443,7 +443,8 @@ void velox_hip_mla_layer_step(VeloxHipMla* m, uint32_t layer, uint32_t batch, ui
         g.x = x;
         g.ldx = ldx;
         g.x_f32 = x_f32;
-        g.y = y;
+        g.y = y16 ? nullptr : y;
+        g.y16 = y16;
         g.ldy = ldy;
         g.ksplit = ksplit;
         g.w_gstride = p.w_gstride;
@@ -521,11 +522,12 @@ void velox_hip_mla_layer_step(VeloxHipMla* m, uint32_t layer, uint32_t batch, ui
     }
     vx_record_error(vx_launch_mla_merge(po, pml, m->nh, m->splits, m->lr, ctx, batch, mask, st));
     // 8. o_h = W_uv[h] ctx_h; 9. W_o [o_h], split over K; 10. residual
-    float* oh = vm_act(m, m->a_oh);
-    gemm(L.uv, ctx, m->nh * m->lr, m->lr, 1, oh, m->nh * m->dv, m->dv, 1, 0);
+    // o_h goes to W_o as fp16, the rounding the GEMM applies to fp32 activations: half the bytes
+    uint16_t* oh16 = (uint16_t*)vm_act(m, m->a_oh);
+    gemm(L.uv, ctx, m->nh * m->lr, m->lr, 1, nullptr, m->nh * m->dv, m->dv, 1, 0, oh16);
     float* parts_o = vm_act(m, m->a_parts_o);
     const uint64_t pstride_o = (uint64_t)m->B * m->H;
-    gemm(L.o, oh, m->nh * m->dv, 0, 1, parts_o, m->H, 0, m->ks_o, pstride_o);
+    gemm(L.o, oh16, m->nh * m->dv, 0, 0, parts_o, m->H, 0, m->ks_o, pstride_o);
     vx_record_error(vx_launch_mla_resid(h, parts_o, m->ks_o, pstride_o, m->H, batch, mask, st));
 }
 
