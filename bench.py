@@ -93,6 +93,8 @@ def bench_mla(args) -> int:
     ctx = args.context_len or 4096
     print(f"[bench] deepseek_v3_mla layer: batch {args.batch}, context {ctx}, warmup {args.warmup}, "
           f"steps {args.steps}", file=sys.stderr, flush=True)
+    if args.no_graph:
+        return bench_mla_eager(args, ctx)
     r = mla_run(batch=args.batch, context_len=ctx, warmup=args.warmup, steps=args.steps, seed=args.seed)
     attn_gbps = r["attn_bytes"] / (r["attn_us"] * 1e3) if r["attn_us"] > 0 else 0.0
     print(f"[bench] mla done: {r['us_per_layer']:.2f} us/layer, {r['hbm_gbps']:.0f} GB/s; attention "
@@ -129,6 +131,36 @@ def bench_mla(args) -> int:
         },
     }
     print(json.dumps(out), flush=True)
+    return 0
+
+
+def bench_mla_eager(args, ctx: int) -> int:
+    """The same layer step launched eagerly (one synchronized step per call), for per-kernel traces:
+    rocprofv3's kernel trace of replayed hipGraphs is not usable here. Its wall time includes host
+    launch and synchronization, so it is reported beside, never as, the graph figure."""
+    import numpy as np
+
+    from velox_amd.engine import MlaEngine
+
+    n = args.warmup + args.steps
+    e = MlaEngine("deepseek_v3_mla", max_seq_len=ctx + n + 1, max_batch=args.batch, seed=args.seed)
+    for b in range(args.batch):
+        e.fill_cache(0, b, ctx, seed=args.seed + b)
+        e.set_position(b, ctx)
+    e.set_hidden(np.random.default_rng(args.seed).standard_normal((args.batch, e.cfg.hidden_dim)).astype(np.float32))
+    for _ in range(args.warmup):
+        e.step(0, args.batch)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        e.step(0, args.batch)
+    wall_us = (time.perf_counter() - t0) * 1e6 / max(args.steps, 1)
+    e.close()
+    print(f"[bench] mla eager: {args.steps} synchronized steps, {wall_us:.1f} us wall each", file=sys.stderr, flush=True)
+    print(json.dumps({"metric": f"MLA layer eager wall us, DeepSeek-V3 MLA fp8 bs={args.batch} ctx {ctx}, 1 GPU",
+                      "value": round(wall_us, 3), "unit": "us/layer (eager, host-synchronized)", "n_gpus": 1,
+                      "steps": args.steps, "warmup": args.warmup, "higher_is_better": False, "data": "synthetic",
+                      "config": {"workload": f"deepseek_v3_mla_fp8_layer_bs{args.batch}_ctx{ctx}", "hipgraph": False}}),
+          flush=True)
     return 0
 
 

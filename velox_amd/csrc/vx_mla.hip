@@ -409,7 +409,7 @@ __global__ __launch_bounds__(1024) void vx_mla_prep_kernel(VxMlaPrepArgs a) {
 
 template <int LR, int DR, int W>
 constexpr size_t vx_mla_attn_lds() {
-    return (size_t)32 * (LR + DR + 8) * 2 + (size_t)LR * 40 * 2;
+    return (size_t)32 * (LR + DR + 8) * 2 + (size_t)LR * 40 * 2 + (size_t)(LR / 8) * 32;
 }
 
 // Absorbed MLA attention of one (split, sequence, group of 16 W heads). The split's positions go
@@ -423,7 +423,7 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
     constexpr int R = LR + DR, NCK = R / 32, NB = LR / 16, KP = R + 8, VP = 40, NT = 64 * W;
     extern __shared__ __align__(16) unsigned char vm_smem[];
     _Float16* k_s = (_Float16*)vm_smem;        // [32][KP]: rows [c | kr]
-    _Float16* v_s = k_s + 32 * KP;             // [LR][VP]: latent dims; slot 8j + e holds vrow(j, e)
+    _Float16* v_s = k_s + 32 * KP;             // latent dim r at voff(r); slot 8j + e holds vrow(j, e)
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, grp = lane >> 4;
     const uint32_t sp = blockIdx.x, b = blockIdx.y;
@@ -438,17 +438,23 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
 
     // ---- the chunk's rows into registers (rows clamped to pos: past t1 they are masked). Latent
     // units: slot group j (positions 4j..4j+3 and 16+4j..16+4j+3) x 8 dimensions, 8 row loads each;
-    // RoPE units: one row x 8 dimensions. j is the fastest index, so the transposed 16-byte stores
-    // of neighbouring lanes land 64 bytes apart in LDS ----
+    // RoPE units: one row x 8 dimensions (the unit -> (j, db) map is below) ----
     constexpr int NVU = (4 * (LR / 8) + NT - 1) / NT, NRU = (32 * (DR / 8) + NT - 1) / NT;
     // two register sets: chunk i + 2 is loaded while chunk i is computed
     uint4 kv[2][NVU][8], kq[2][NRU];
     auto vrow = [](int j, int e) { return (uint32_t)(e < 4 ? 4 * j + e : 16 + 4 * j + (e - 4)); };
+    // unit un -> (slot group j, 8-dimension block db): 8 consecutive lanes take 2 slot groups x 4
+    // blocks, so their 16-byte stores into k_s hit 8 different 16-byte bank groups; voff shifts
+    // every 8 latent rows by 32 more bytes, which does the same for the transposed stores into v_s
+    // and keeps the P.V operand reads (16 consecutive rows) conflict-free
+    auto unit_j = [](int un) { return (un & 1) | (((un >> 3) & 1) << 1); };
+    auto unit_db = [](int un) { return ((un >> 1) & 3) | ((un >> 4) << 2); };
+    auto voff = [](int r) { return r * VP + 16 * (r >> 3); };
     auto load_chunk = [&](auto SET, uint32_t cb) {
         constexpr int S = decltype(SET)::value;
 #pragma unroll
         for (int u = 0; u < NVU; ++u) {
-            const int un = min(tid + u * NT, 4 * (LR / 8) - 1), j = un & 3, db = un >> 2;
+            const int un = min(tid + u * NT, 4 * (LR / 8) - 1), j = unit_j(un), db = unit_db(un);
 #pragma unroll
             for (int e = 0; e < 8; ++e)
                 kv[S][u][e] = *(const uint4*)(cb_base + (size_t)min(cb + vrow(j, e), pos) * R + 8 * db);
@@ -511,7 +517,7 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
         for (int u = 0; u < NVU; ++u) {
             const int un = tid + u * NT;
             if (un < 4 * (LR / 8)) {
-                const int j = un & 3, db = un >> 2;
+                const int j = unit_j(un), db = unit_db(un);
                 vm_h8 hv[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
@@ -523,7 +529,7 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
                     vm_h8 t;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) t[e] = hv[e][d];
-                    *(vm_h8*)(v_s + (8 * db + d) * VP + 8 * j) = t;
+                    *(vm_h8*)(v_s + voff(8 * db + d) + 8 * j) = t;
                 }
             }
         }
@@ -580,7 +586,7 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
         }
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            const vm_h8 vop = *(const vm_h8*)(v_s + (16 * nb + col) * VP + 8 * grp);
+            const vm_h8 vop = *(const vm_h8*)(v_s + voff(16 * nb + col) + 8 * grp);
             o_acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, vop, o_acc[nb], 0, 0, 0);
         }
     };
