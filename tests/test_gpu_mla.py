@@ -90,6 +90,13 @@ def test_mla_deepseek_shape_batched_vs_oracle(oracle):
                  norm_sigma=0.0)
 
 
+def test_mla_deepseek_shape_many_splits_vs_oracle(oracle):
+    """16 sequences x 8 position splits x 2 head groups = 256 attention workgroups (the config-4 B=16
+    grid), every split non-empty, merged over 8 splits."""
+    _check_layer(oracle, "deepseek_v3_mla", batch=16, ctxs=[200 + 19 * i for i in range(16)], steps=1,
+                 max_seq=520, norm_sigma=0.0)
+
+
 def test_mla_synthesized_weights_equal_loaded_codes(oracle):
     """The device quantizer and tile maps: loading the oracle's fp8 codes and block scales through the
     checkpoint entry point gives bit-identical layer outputs to the device-synthesized weights."""

@@ -613,7 +613,7 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
 }
 
 // LSE merge of the split partials of one (head, sequence) -> ctx[b][h][LR] fp32. A workgroup covers
-// 128 latent dimensions of its (head, sequence) (grid z), one per thread, with 8 splits' loads in
+// 128 latent dimensions of its (head, sequence) (grid z), one per thread, with 32 splits' loads in
 // flight ahead of their adds (the adds stay in split order).
 __global__ __launch_bounds__(128) void vx_mla_merge_kernel(const float* part_o, const float* part_ml, uint32_t nh,
                                                            uint32_t splits, uint32_t lr, float* ctx, uint64_t mask) {
@@ -639,12 +639,12 @@ __global__ __launch_bounds__(128) void vx_mla_merge_kernel(const float* part_o, 
     const uint32_t d = blockIdx.z * 128u + threadIdx.x;
     if (d >= lr) return;
     float acc = 0.0f;
-    for (uint32_t j0 = 0; j0 < splits; j0 += 8u) {
-        float v[8];
+    for (uint32_t j0 = 0; j0 < splits; j0 += 32u) {
+        float v[32];
 #pragma unroll
-        for (uint32_t u = 0; u < 8; ++u) v[u] = po[(size_t)min(j0 + u, splits - 1u) * lr + d];
+        for (uint32_t u = 0; u < 32; ++u) v[u] = po[(size_t)min(j0 + u, splits - 1u) * lr + d];
 #pragma unroll
-        for (uint32_t u = 0; u < 8; ++u)
+        for (uint32_t u = 0; u < 32; ++u)
             if (j0 + u < splits) acc += s_w[j0 + u] * v[u];
     }
     ctx[bh * lr + d] = acc;
