@@ -349,10 +349,10 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
     M->kv_layer_bytes = vx_align((uint64_t)2 * c.num_kv_heads * M->s_cap * D * 2);
     M->kv_bytes = M->kv_layer_bytes * c.num_layers * M->batch;  // [layer][sequence]
 
-    // Split-K over the sequence: up to 1024 positions, a power of two <= 8 splits of ~128
+    // Split-K over the sequence: up to 1024 positions, a power of two (2, 4) of up to 256
     // positions whose (m, l, o) partials the o_proj GEMV merges in its prologue (no extra launch);
     // longer contexts use 256-position splits and the merge kernel. (Llama-3-8B at 385 positions,
-    // measured: 1 split 634 tok/s, 2: 667, 4: 682, 8: 671.)
+    // MFMA attention, measured: 1 split 702.6 tok/s, 2: 712.7, 4: 707.4, 8: 690.3.)
     uint32_t splits = c.attn_splits;
     if (!splits) {
         const char* env = std::getenv("VELOX_HIP_ATTN_SPLITS");  // tuning override
@@ -361,8 +361,8 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
     }
     if (!splits) {
         if (c.max_seq_len <= 1024) {
-            const uint32_t want = (c.max_seq_len + 127) / 128;
-            splits = 1;
+            const uint32_t want = (c.max_seq_len + 255) / 256;
+            splits = 2;
             while (splits < want) splits <<= 1;
         } else {
             splits = (c.max_seq_len + 255) / 256;
