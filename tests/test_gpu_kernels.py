@@ -50,7 +50,9 @@ def _fp64_gemv(deq: np.ndarray, x16: np.ndarray) -> np.ndarray:
     return deq.astype(np.float64) @ x16.astype(np.float64)
 
 
-@pytest.mark.parametrize("n,k,s", [(96, 576, 0), (64, 576, 8), (130, 4096, 0), (48, 14336, 0), (200, 1536, 16)])
+# (64, 29568): 32 lanes per row over 924 blocks, 4 zero-padded blocks per row
+@pytest.mark.parametrize("n,k,s", [(96, 576, 0), (64, 576, 8), (130, 4096, 0), (48, 14336, 0), (200, 1536, 16),
+                                   (64, 29568, 0)])
 def test_repack_dequant_bitexact(hiplib, oracle, dev, n, k, s):
     blocks = _weights(oracle, n, k, 100 + n)
     t = TiledQ4(hiplib, dev, blocks, n, k, s)
@@ -127,8 +129,10 @@ def _gemv_case(hiplib, oracle, dev, n, k, mode, norm, bias, s=0):
     return got, want, tight
 
 
+# (256, 18944) and (128, 29568): the Qwen down-projection widths, 32 lanes per row with 16 and 4
+# zero-padded blocks per row
 @pytest.mark.parametrize("n,k,s", [(4096, 4096, 0), (1024, 14336, 0), (960, 576, 0), (1536, 576, 8), (576, 1536, 0),
-                                   (123, 4096, 16), (64, 4096, 4)])
+                                   (123, 4096, 16), (64, 4096, 4), (256, 18944, 0), (128, 29568, 0)])
 def test_gemv_store(hiplib, oracle, dev, n, k, s):
     got, want, tight = _gemv_case(hiplib, oracle, dev, n, k, L.GEMV_STORE, False, False, s)
     # The kernel's one approximation is fp16 activations (rms relative error ~2.8e-4, pinned below
