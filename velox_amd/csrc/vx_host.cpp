@@ -366,6 +366,12 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
             while (splits < want) splits <<= 1;
         } else {
             splits = (c.max_seq_len + 255) / 256;
+            // one round of workgroups: the D = 128 kernel holds one 8-wave workgroup per CU, so
+            // splits x KV heads above 256 runs a second round (Qwen2-72B at 8216 positions: 33 x 8
+            // workgroups span 13.2 us, 32 x 8 span 8.2 us); take 256 / KV heads longer splits while
+            // no wave gets more than two 32-position chunks (splits of up to 512 positions)
+            const uint32_t one_round = 256u / c.num_kv_heads, min_splits = (c.max_seq_len + 511) / 512;
+            if (splits * c.num_kv_heads > 256u && one_round >= min_splits) splits = one_round;
             if (splits > 64) splits = 64;
         }
     }
