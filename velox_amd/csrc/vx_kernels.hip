@@ -582,8 +582,27 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     uint16_t* Kc = kvb + (size_t)g * a.s_cap * D;
     uint16_t* Vc = kvb + ((size_t)a.hkv + g) * a.s_cap * D;
 
-    // ---- q, the new k/v into registers (clamped: no load under a branch) ----
     constexpr int NP = (G + 1) * HALF, RP = (NP + NT - 1) / NT;  // RoPE pairs, pairs per thread
+    // ---- the decode position first, as a vector load, then the RoPE row it selects; vector loads
+    // return in order, so both arrive ahead of the q/k/v and K/V chunk loads issued after them (a
+    // scalar state load issued after those waited behind every workgroup's whole burst: ~4 us at 256
+    // workgroups) ----
+    uint64_t step = (uint64_t)a.fixed_pos;
+    if (a.state) step = __hip_atomic_load((uint64_t*)&a.state[bq].step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    step = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(step >> 32)) << 32) |
+           (uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)step);
+    const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;  // safe_step clamp
+    // cached positions [t0, t1): below pos, or up to pos when a prefill chunk appended its rows
+    const uint32_t t1 = min(a.prefill ? pos + 1u : pos, t0 + chunk);
+    const uint32_t n_chunks = t1 > t0 ? (t1 - t0 + 31u) >> 5 : 0u;
+    const bool has_new = !a.prefill && t0 <= pos && pos < t0 + chunk;  // this split folds in the new position
+    const float2* rp = a.rope + (size_t)pos * HALF;
+    float2 rcs[RP];
+#pragma unroll
+    for (int i = 0; i < RP; ++i) rcs[i] = rp[min(tid + i * NT, NP - 1) % HALF];
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- q, the new k/v into registers (clamped: no load under a branch) ----
     float r1[RP], r2[RP], vnew;
     if constexpr (!PS) {
         const float* q = a.qkv + (size_t)bq * a.qkv_bstride;
@@ -642,19 +661,6 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     };
     uint32_t ci = (uint32_t)wave;
     load_chunk(t0 + 32u * min(ci, chunk / 32u - 1u));
-    // q/k/v and the first chunk go out before the state is read: scalar loads complete out of
-    // order, so a state load issued earlier would hold these behind its s_waitcnt lgkmcnt(0)
-    __builtin_amdgcn_sched_barrier(0);
-    const uint64_t step = a.state ? a.state[bq].step : (uint64_t)a.fixed_pos;
-    const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;  // safe_step clamp
-    // cached positions [t0, t1): below pos, or up to pos when a prefill chunk appended its rows
-    const uint32_t t1 = min(a.prefill ? pos + 1u : pos, t0 + chunk);
-    const uint32_t n_chunks = t1 > t0 ? (t1 - t0 + 31u) >> 5 : 0u;
-    const bool has_new = !a.prefill && t0 <= pos && pos < t0 + chunk;  // this split folds in the new position
-    const float2* rp = a.rope + (size_t)pos * HALF;
-    float2 rcs[RP];
-#pragma unroll
-    for (int i = 0; i < RP; ++i) rcs[i] = rp[min(tid + i * NT, NP - 1) % HALF];
 
     // ---- RoPE on this group's q heads and the new k; bf16 K/V row ----
     const float qscale = a.scale * kLog2e;  // scores in the log2 domain
