@@ -97,6 +97,8 @@ int velox_hip_builtin_config(const char* which, uint32_t max_seq_len, VeloxHipMo
 /* ---- plan (memory_planner, src/memory_planner.rs:282-488) ---- */
 int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out);
 void velox_hip_model_destroy(VeloxHipModel* m);
+/* The planned configuration: the input, with attn_splits = the split count the planner chose when
+ * the input left it 0. */
 int velox_hip_model_config(const VeloxHipModel* m, VeloxHipModelConfig* out);
 int velox_hip_model_arena_bytes(const VeloxHipModel* m, uint64_t* weight_bytes, uint64_t* scale_bytes,
                                 uint64_t* norm_bytes, uint64_t* kv_bytes, uint64_t* act_bytes);

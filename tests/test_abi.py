@@ -91,6 +91,31 @@ def test_plan_rejects_unsupported_shapes(field, value):
     assert rc == -1
 
 
+def test_attention_split_choices():
+    """The planner's split-K count over the sequence: up to 1024 positions a power of two >= 2 of
+    up to 256 positions (merged in the o_proj prologue); beyond, 256-position splits, or 256 / KV
+    heads longer ones when splits x KV heads would exceed 256 workgroups (two rounds of the
+    one-workgroup-per-CU attention kernel), as long as no split exceeds 512 positions."""
+    lib = L.load()
+    cases = [("llama3_8b", 130, 2), ("llama3_8b", 385, 2), ("llama3_8b", 512, 2), ("llama3_8b", 513, 4),
+             ("llama3_8b", 1024, 4), ("qwen2_5_7b", 2080, 9), ("qwen2_72b", 8216, 32), ("qwen2_72b", 8192, 32),
+             ("llama3_8b", 20000, 64)]
+    for name, max_seq, want in cases:
+        cfg = L.builtin_config(name, max_seq)
+        rc, m = _plan(cfg)
+        assert rc == 0, (name, max_seq, rc)
+        out = L.ModelConfig()
+        assert lib.velox_hip_model_config(m, C.byref(out)) == 0
+        lib.velox_hip_model_destroy(m)
+        assert out.attn_splits == want, (name, max_seq, out.attn_splits)
+    cfg = L.builtin_config("llama3_8b", 385)
+    cfg.attn_splits = 3  # an explicit count is kept
+    rc, m = _plan(cfg)
+    out = L.ModelConfig()
+    assert rc == 0 and lib.velox_hip_model_config(m, C.byref(out)) == 0 and out.attn_splits == 3
+    lib.velox_hip_model_destroy(m)
+
+
 def test_tiled_layout_choices():
     """Lanes per row for the BASELINE shapes: the largest S padding a row by at most 1/32 of its
     blocks (padded blocks are streamed, so padding costs bandwidth), else the least padding."""

@@ -376,6 +376,7 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
         }
     }
     M->splits = splits;
+    M->cfg.attn_splits = splits;  // reported by velox_hip_model_config
     const uint32_t o_groups_per_thread = (qd / 8 + 511) / 512;
     M->fused_merge = (splits == 1 || splits == 2 || splits == 4 || splits == 8) && o_groups_per_thread <= 4;
     M->max_wgs = vx_gemv_max_wgs_default();
