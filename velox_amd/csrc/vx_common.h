@@ -153,6 +153,7 @@ struct VxAttnArgs {
     const float* qkv_bias;
     uint64_t qkv_pstride;
     uint32_t qkv_nparts;
+    uint32_t max_len;        // > 0: no row attends past this many positions (a prefill chunk's end); 0 unknown
 };
 
 // Batched (B <= 32 sequences) Q4_0 GEMM: Y[m][n] = sum_k X[m][k] W[n][k] for fp16 activations

@@ -814,7 +814,7 @@ namespace {
 // K/V rows,) attention, merge, o_proj + residual, norm, gate/up + SwiGLU, down + residual], norm,
 // LM head.
 void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n, uint64_t mask, bool prefill,
-                     hipStream_t st) {
+                     uint32_t max_len, hipStream_t st) {
     const VeloxHipModel* M = A->model;
     const VeloxHipModelConfig& c = M->cfg;
     uint8_t* act = A->activation_arena;
@@ -855,6 +855,7 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
     at.partials_only = 1;
     at.batch = n;
     at.prefill = prefill ? 1u : 0u;
+    at.max_len = max_len;
     // decode: consecutive sequences of one layer; prefill: every row reads sequence 0's cache
     at.kv_bstride = prefill ? 0 : M->kv_layer_bytes / 2;
     at.qkv_bstride = qd + 2 * kvd;
@@ -955,7 +956,7 @@ void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_
     const VeloxHipModel* M = A->model;
     uint8_t* act = A->activation_arena;
     VeloxDecodeState* states = (VeloxDecodeState*)(act + M->a_bstate);
-    vx_rows_forward(A, states, batch, mask, false, st);
+    vx_rows_forward(A, states, batch, mask, false, 0u, st);
     vx_record(vx_launch_bfinalize((const float*)(act + M->a_bcand_v), (const uint32_t*)(act + M->a_bcand_i),
                                   M->head_bwgs, states, A->host_pinned_ring, (const uint32_t*)(act + M->a_bprompt),
                                   (const uint32_t*)(act + M->a_bplen), M->cfg.max_seq_len, batch, mask, st));
@@ -974,7 +975,7 @@ int velox_hip_prefill_batch(VeloxHipArena* A, uint64_t pos0, uint32_t n_tokens, 
     for (uint32_t done = 0; done < n_tokens;) {
         const uint32_t n = n_tokens - done < chunk ? n_tokens - done : chunk;
         vx_record(vx_launch_prefill_rows(rows, n, pos0 + done, prompt, mask, st));
-        vx_rows_forward(A, rows, n, mask, true, st);
+        vx_rows_forward(A, rows, n, mask, true, (uint32_t)(pos0 + done + n), st);
         vx_record(vx_launch_prefill_finalize((const float*)(act + M->a_bcand_v), (const uint32_t*)(act + M->a_bcand_i),
                                              M->head_bwgs, rows, n, A->host_pinned_ring,
                                              (VeloxDecodeState*)(act + M->a_state), prompt,

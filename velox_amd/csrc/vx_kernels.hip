@@ -1091,9 +1091,8 @@ hipError_t vx_gemv_dispatch_norm(uint32_t s, const VxGemvArgs& a, uint32_t max_w
     }
 }
 
-template <int D, int G, bool PS>
-hipError_t vx_attn_launch_ps(const VxAttnArgs& a, hipStream_t st) {
-    constexpr int W = 8;
+template <int D, int G, bool PS, int W>
+hipError_t vx_attn_launch_w(const VxAttnArgs& a, hipStream_t st) {
     constexpr size_t lds = vx_attn_lds_bytes<D, G, W>();
     static bool attr_set = false;
     if (!attr_set) {
@@ -1107,6 +1106,20 @@ hipError_t vx_attn_launch_ps(const VxAttnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((vx_attn_kernel<D, G, W, PS>), dim3(a.splits, a.hkv, a.batch ? a.batch : 1u), dim3(64 * W), lds,
                        st, a);
     return hipGetLastError();
+}
+
+template <int D, int G, bool PS>
+hipError_t vx_attn_launch_ps(const VxAttnArgs& a, hipStream_t st) {
+    if constexpr (PS) {
+        // 4 waves, two workgroups per CU, where 8-wave workgroups (one per CU) would need a second
+        // round and 4 waves still take every 32-position chunk a split can attend in one pass (the
+        // prefill chunks of short prompts: 64 rows x 8 KV heads = 512 workgroups, <= 128 positions)
+        const uint32_t chunk = ((a.s_max + a.splits - 1u) / a.splits + 31u) & ~31u;
+        const uint32_t span = a.max_len ? min(a.max_len, chunk) : chunk;
+        const uint64_t wgs = (uint64_t)a.splits * a.hkv * (a.batch ? a.batch : 1u);
+        if (wgs > 256u && span <= 4u * 32u) return vx_attn_launch_w<D, G, PS, 4>(a, st);
+    }
+    return vx_attn_launch_w<D, G, PS, 8>(a, st);
 }
 
 template <int D, int G>
