@@ -7,7 +7,7 @@ One step = one decode step (one token) of the hipGraph-captured HIP decode path:
 down+residual], RMSNorm+LM head+argmax. Weights are random N(0, 0.02) quantized to Q4_0 on the
 device (synthetic; no checkpoint), the prompt is 128 seeded random token ids (prefilled through the
 same graph, untimed), then W untimed and K timed greedy decode steps: the default W=5, K=251 covers
-the 256 decode steps of BASELINE config 2 (positions 128..383). Inputs are resident in HBM before
+the 256 decode steps of benchmark configuration 2 (positions 128..383). Inputs are resident in HBM before
 the timed region; the region is synchronized on both sides and timed with HIP events on the
 graph's stream (host clock reported beside it).
 
@@ -85,7 +85,7 @@ def cpu_baseline(seed: int) -> dict:
 
 
 def bench_mla(args) -> int:
-    """one DeepSeek-V3 absorbed-MLA layer (fp8 e4m3 weights with 128x128 block
+    """Benchmark configuration 4: one DeepSeek-V3 absorbed-MLA layer (fp8 e4m3 weights with 128x128 block
     scales, bf16 latent cache of `context_len` seeded positions per sequence), timed as hipGraph
     replays of the layer step; value = device microseconds per layer (lower is better)."""
     from velox_amd.engine import mla_run
@@ -177,7 +177,7 @@ def main() -> int:
     ap.add_argument("--model", default="llama3_8b",
                     choices=["llama3_8b", "qwen2_5_7b", "qwen2_72b", "smollm_135m", "deepseek_v3_mla"],
                     help="builtin configuration (the headline metric is llama3_8b; deepseek_v3_mla times one "
-                         "absorbed-MLA layer with fp8 weights, BASELINE config 4)")
+                         "absorbed-MLA layer with fp8 weights, benchmark configuration 4)")
     ap.add_argument("--context-len", type=int, default=0,
                     help="start from a seeded context of N positions already in the KV cache (prompt = 1 token)")
     ap.add_argument("--batch", type=int, default=1,

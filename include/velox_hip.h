@@ -90,7 +90,7 @@ typedef struct VeloxDecodeState {
 
 #define VELOX_HIP_RING_SIZE 1024u
 
-/* Built-in configurations of BASELINE.json (configs 1,2,3,5). which: "smollm_135m", "llama3_8b",
+/* Built-in benchmark configurations (1, 2, 3, 5). which: "smollm_135m", "llama3_8b",
  * "qwen2_5_7b", "qwen2_72b". max_seq_len 0 keeps the default. */
 int velox_hip_builtin_config(const char* which, uint32_t max_seq_len, VeloxHipModelConfig* out);
 
@@ -349,7 +349,7 @@ int velox_hip_gguf_tensor_info(const VeloxHipGguf* g, uint64_t i, char* name, ui
 int velox_hip_gguf_config(const VeloxHipGguf* g, uint32_t max_seq_len, VeloxHipModelConfig* out);
 int velox_hip_gguf_load(VeloxHipArena* arena, const VeloxHipGguf* g, hipStream_t stream);
 
-/* ---- Absorbed multi-head latent attention layer (DeepSeek-V3 form) ----
+/* ---- Absorbed multi-head latent attention layer (benchmark configuration 4, DeepSeek-V3 form) ----
  * Replaces the reference's MLA step: the emitted velox_cuda_fused_mla_absorbed_attn
  * (src/codegen.rs:2001-2109, launched 1x256 at :2993) and the CPU mla_absorbed_step_f32
  * (src/runtime.rs:845-1044) with its absorbed weights (MlaAbsorptionPass, src/optimizer.rs:138-184).

@@ -319,7 +319,7 @@ class RefSmolLM:
         self.L.vxr_smollm_free()
 
 
-# ---- fp8 e4m3fn block format and the absorbed MLA layer ----
+# ---- fp8 e4m3fn block format and the absorbed MLA layer (benchmark configuration 4) ----
 MLA_TAGS = dict(norm=32, q_a=33, q_a_norm=34, q_b=35, kv_a=36, kv_a_norm=37, kv_b=38, o=39, hidden=40, cache=41)
 
 

@@ -419,7 +419,7 @@ void vxo_mla_absorbed_step(float* dst_hidden, const float* input_hidden, const f
 }
 
 /* ------------------------------------------------------------------------------------------ */
-/* fp8 e4m3fn (OCP) with 128x128 block scales: BASELINE config 4's weight format (DeepSeek-V3),  */
+/* fp8 e4m3fn (OCP) with 128x128 block scales: benchmark configuration 4's weight format (DeepSeek-V3),  */
 /* not in the reference. Integer round-to-nearest-even so the device quantizer matches bit for  */
 /* bit.                                                                                         */
 /* ------------------------------------------------------------------------------------------ */
@@ -592,7 +592,7 @@ void vxo_mla_layer_step(const VxoMlaConfig* c, const VxoMlaWeights* w, float* ca
 
 /* ------------------------------------------------------------------------------------------ */
 /* Engine: src/runtime.rs:1229-1451 (VeloxStaticExecutionEngine::forward_step) with the        */
-/* BASELINE extensions (config-driven eps/theta, Q4_0 weights, bf16 KV rounding, QKV bias,     */
+/* Benchmark extensions (config-driven eps/theta, Q4_0 weights, bf16 KV rounding, QKV bias,     */
 /* tied head).                                                                                 */
 /* ------------------------------------------------------------------------------------------ */
 typedef struct {

@@ -33,7 +33,7 @@ enum {
     VXO_T_UP = 7, VXO_T_DOWN = 8, VXO_T_ATTN_NORM = 9, VXO_T_MLP_NORM = 10,
     VXO_T_FINAL_NORM = 11, VXO_T_HEAD = 12, VXO_T_BQ = 13, VXO_T_BK = 14, VXO_T_BV = 15,
     VXO_T_PROMPT = 16,
-    /* MLA layer tensors */
+    /* MLA layer tensors (benchmark configuration 4) */
     VXO_T_MLA_NORM = 32, VXO_T_MLA_QA = 33, VXO_T_MLA_QA_NORM = 34, VXO_T_MLA_QB = 35, VXO_T_MLA_KVA = 36,
     VXO_T_MLA_KVA_NORM = 37, VXO_T_MLA_KVB = 38, VXO_T_MLA_O = 39, VXO_T_MLA_HIDDEN = 40, VXO_T_MLA_CACHE = 41
 };
@@ -71,7 +71,7 @@ void vxo_mla_absorbed_step(float* dst_hidden, const float* input_hidden, const f
                            float* kv_latent_pool, uint64_t hidden_dim, uint64_t latent_dim,
                            uint64_t max_seq_len, uint64_t step, float eps);
 
-/* ---- fp8 e4m3fn (OCP) with 128x128 block scales (not in the reference: BASELINE config 4's
+/* ---- fp8 e4m3fn (OCP) with 128x128 block scales (not in the reference: benchmark configuration 4's
  * DeepSeek-V3 weight format). scale = amax / 448 per block; code = e4m3(w / scale), round to
  * nearest even, saturating at +-448. Scales are [ceil(rows/128)][ceil(cols/128)] floats. ---- */
 uint8_t vxo_f32_to_e4m3(float f);
@@ -118,7 +118,7 @@ typedef struct VxoConfig {
 
 typedef struct VxoEngine VxoEngine;
 
-/* Synthesizes the seeded model of the BASELINE recipe: linear weights N(0, sigma) (quantized to
+/* Synthesizes the seeded model of the benchmark recipe: linear weights N(0, sigma) (quantized to
  * Q4_0 when cfg->q4_0), norm gains 1.0 (norm_sigma == 0) or N(1, norm_sigma), biases N(0, sigma).
  * layers_to_build < num_layers builds only the first layers (bounded CPU samples). */
 VxoEngine* vxo_engine_create(const VxoConfig* cfg, uint64_t seed, float sigma, float norm_sigma,

@@ -1,5 +1,5 @@
 """CPU tests of the C ABI library: it loads, exports every declared symbol, and its planner (pure
-host code, no GPU needed) sizes the BASELINE configurations as BASELINE.md derives them."""
+host code, no GPU needed) sizes the benchmark configurations by their published shapes."""
 import ctypes as C
 import os
 import subprocess
@@ -45,8 +45,8 @@ def test_builtin_configs_match_baseline():
 
 
 def test_step_bytes_match_baseline_llama():
-    """4,221,370,368 weight bytes + 2,304 embedding row + 1,064,960 norm bytes
-    + 131,072*(pos+1) KV read + 131,072 KV write per step."""
+    """Llama-3-8B Q4_0 algorithmic bytes per decode step: 4,221,370,368 weight bytes + 2,304
+    embedding row + 1,064,960 norm bytes + 131,072*(pos+1) KV read + 131,072 KV write."""
     rc, m = _plan(make_config("llama3_8b", max_seq_len=385))
     assert rc == 0
     lib = L.load()
@@ -54,7 +54,7 @@ def test_step_bytes_match_baseline_llama():
         want = 4_221_370_368 + 2_304 + 1_064_960 + 131_072 * (pos + 1) + 131_072
         assert lib.velox_hip_model_step_bytes(m, pos) == want
     mean = np.mean([lib.velox_hip_model_step_bytes(m, p) for p in range(128, 384)])
-    assert mean == 4_222_437_632 + 131_072 * 257.5  # = 4.256 GB (BASELINE.md quotes it as "mean 4.255 GB")
+    assert mean == 4_222_437_632 + 131_072 * 257.5  # = 4.256 GB over positions 128..383
     lib.velox_hip_model_destroy(m)
 
 
@@ -117,7 +117,7 @@ def test_attention_split_choices():
 
 
 def test_tiled_layout_choices():
-    """Lanes per row for the BASELINE shapes: the largest S padding a row by at most 1/32 of its
+    """Lanes per row for the benchmark shapes: the largest S padding a row by at most 1/32 of its
     blocks (padded blocks are streamed, so padding costs bandwidth), else the least padding."""
     lib = L.load()
     expect = {(6144, 4096): 32, (4096, 14336): 32, (960, 576): 4, (576, 1536): 16,

@@ -1,5 +1,5 @@
 """Batched decode of independent sequences (src/runners/velox_cuda_runner_k2.cu:553-997 batched
-Q4 kernels): the MFMA GEMM against fp64 with exactly its fp16 activations, and
+Q4 kernels; benchmark configuration 3): the MFMA GEMM against fp64 with exactly its fp16 activations, and
 the batched decode step against one oracle engine per sequence."""
 import ctypes as C
 

@@ -1,8 +1,8 @@
 """End-to-end decode parity: the HIP decode step (C ABI, eager and hipGraph) vs the CPU oracle.
 
-Teacher forcing (SURVEY hard parts): both paths consume the same token sequence, so one argmax
+Teacher forcing: both paths consume the same token sequence, so one argmax
 flip on a near-tie cannot desynchronise the comparison. Bars: logits max-abs <= 2e-2 against
-the oracle with bf16 KV (the BASELINE bf16 bar; activations enter each GEMV as fp16), and the
+the oracle with bf16 KV (the bf16 parity bar; activations enter each GEMV as fp16), and the
 GPU argmax equal to the exact argmax of the GPU's own logits.
 """
 import numpy as np
@@ -145,7 +145,7 @@ LONG = dict(vocab_size=4096, hidden_dim=8192, intermediate_dim=2048, num_heads=6
 @pytest.mark.parametrize("splits", [0, 8])
 def test_decode_long_context_vs_oracle(oracle, splits):
     """Qwen2-72B attention shape (64 q / 8 kv heads, D 128, hidden 8192, QKV bias) after a seeded
-    2048-position context already in the KV cache (the BASELINE long-context setup): automatic
+    2048-position context already in the KV cache (the benchmark long-context setup): automatic
     256-position splits with the merge kernel, and 8 splits merged in the o_proj prologue."""
     ctx, max_seq, seed = 2048, 2064, 41
     gpu = HipDecodeEngine(dict(LONG, num_layers=1), seed=seed, norm_sigma=0.1, max_seq_len=max_seq,

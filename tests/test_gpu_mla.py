@@ -1,4 +1,4 @@
-"""The absorbed MLA layer on the GPU (the full form of src/runtime.rs:845-1044)
+"""The absorbed MLA layer on the GPU (benchmark configuration 4; the full form of src/runtime.rs:845-1044)
 against the oracle's vxo_mla_layer_step on the same seeded fp8 weights and latent context.
 
 Tolerance: the device computes every projection with fp16 activations against exactly converted

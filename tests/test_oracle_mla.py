@@ -1,4 +1,4 @@
-"""CPU pins of the oracle's fp8 e4m3fn block format and absorbed MLA layer.
+"""CPU pins of the oracle's fp8 e4m3fn block format and absorbed MLA layer (benchmark configuration 4).
 
 The reference's MLA (src/runtime.rs:845-1044) is a simplified single-latent-head form; config 4 asks
 for the DeepSeek-V3 form (128 heads, q LoRA, a RoPE part, fp8 weights with 128x128 block scales).

@@ -3,7 +3,7 @@
 //
 // The reference's MLA (src/runtime.rs:845-1044, emitted as velox_cuda_fused_mla_absorbed_attn,
 // src/codegen.rs:2001-2109) is a single-latent-head simplification; this is the full form of the
-// same absorbed computation: per head h,
+// same absorbed computation (benchmark configuration 4): per head h,
 //   q_abs_h = W_uk[h]^T q_nope_h,  s_ht = scale (q_abs_h . c_t + rope(q_rope_h) . kr_t),
 //   ctx_h = softmax_t(s_ht) . c_t,  o_h = W_uv[h] ctx_h,  h_out = h + W_o [o_1 .. o_H].
 // One layer step is 9 launches: RMSNorm -> GEMM [W_qa; W_kva] (split over K) -> prep (q / latent

@@ -1,5 +1,5 @@
 // vx_mla_host.cpp -- plan, arena, weight synthesis/loading and the layer step of the absorbed MLA
-// layer. The reference runs its simplified MLA as one 256-thread kernel per layer
+// layer (benchmark configuration 4). The reference runs its simplified MLA as one 256-thread kernel per layer
 // (src/codegen.rs:2001-2109, launch at :2993) over fp32 weights the optimizer pre-absorbed
 // (src/optimizer.rs:138-184); here the DeepSeek-V3 form streams fp8 weights through MFMA GEMMs and
 // keeps the latent cache in bf16, sized for one GPU's 288 GB.

@@ -266,7 +266,7 @@ def run(model: str = "llama3_8b", prompt_len: int = 128, warmup: int = 5, steps:
 
 
 class MlaEngine:
-    """The absorbed multi-head latent attention layer behind the C ABI: the
+    """The absorbed multi-head latent attention layer (benchmark configuration 4) behind the C ABI: the
     full form of the reference's ``mla_absorbed_step_f32`` (src/runtime.rs:845-1044), for up to
     32 sequences, with fp8 block-scaled weights and a bf16 latent cache on the device."""
 
