@@ -129,6 +129,31 @@ def test_prefill_64_and_48_row_chunks_vs_oracle(oracle):
     _prefill_vs_oracle(oracle, SMOLLM, 2, 48, 60, [(0, 60)], 64, seed=80, decode_steps=1)
 
 
+def test_prefill_four_and_eight_wave_attention_agree(oracle):
+    """Llama-3-8B layer shapes (8 KV heads), a 100-token prompt: 64-row chunks run the prefill
+    attention on 4-wave workgroups (64 x 8 = 512 workgroups, rows attending <= 128 positions), 16-row
+    chunks on 8-wave ones (128 workgroups). Each row's attention differs only in how its 32-position
+    chunks are dealt to waves, so the logits and the K/V rows agree to fp32 accumulation order."""
+    seed, P = 81, 100
+    prompt = [int(t) for t in oracle.prompt_tokens(seed, P, LLAMA_SMALL_VOCAB["vocab_size"])]
+    outs = []
+    for chunk in (64, 16):
+        b = HipDecodeEngine(LLAMA_SMALL_VOCAB, seed=seed, norm_sigma=0.1, max_seq_len=128, num_layers=2,
+                            prefill_chunk=chunk)
+        b.set_prompt(prompt)
+        b.prefill_batch(0, P)
+        outs.append((b.chunk_logits(P % chunk)[-1], b.state(), _device_kv(b, 1, P)))
+        b.close()
+    (la, sa, ka), (lb, sb, kb) = outs
+    assert sa == sb and sa[0] == P
+    d = float(np.max(np.abs(la - lb)))
+    print(f"[prefill 4/8-wave attention] logits maxabs {d:.3e} of {np.max(np.abs(la)):.3e}", flush=True)
+    assert d < 1e-3 * max(1.0, float(np.max(np.abs(la))))
+    # layer 1's K/V rows come from layer 0's attention output: the fp32 differences can move a
+    # bf16 rounding by an ulp or two (2^-9 at values near 0.12), far below a wrong row's error
+    assert np.all(np.abs(ka - kb) <= 2 ** -7 * np.abs(kb) + 1e-3 * np.max(np.abs(kb)))
+
+
 def test_prefill_chunking_invariance(oracle):
     """The same prompt in chunks of 32 and of 7 (and, for layer 0, token by token): each row's
     arithmetic does not depend on the chunk it is in, up to fp32 accumulation order, so the final
