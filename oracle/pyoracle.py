@@ -268,6 +268,14 @@ class Engine:
             raise KeyError((kind, layer))
         return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint8)), shape=(n.value,)).copy()
 
+    def tensor_view(self, kind: int, layer: int = 0) -> np.ndarray:
+        """Writable uint8 view of a tensor's storage (tests plant closed-form weights through it)."""
+        n = C.c_uint64(0)
+        p = lib().vxo_engine_tensor(self.h, kind, layer, C.byref(n))
+        if not p:
+            raise KeyError((kind, layer))
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint8)), shape=(n.value,))
+
     def hidden(self) -> np.ndarray:
         p = lib().vxo_engine_hidden(self.h)
         return np.ctypeslib.as_array(p, shape=(self.cfg["hidden_dim"],)).copy()

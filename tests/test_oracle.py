@@ -278,3 +278,89 @@ def test_q4_0_engine_matches_dequantized_fp32_engine(oracle):
     assert np.array_equal(oracle.matmul_q4_0(x, blocks, 576), oracle.matmul_transposed(x, w))
     assert np.array_equal(oracle.matmul_q4_0(x, blocks, 576, threads=4), oracle.matmul_transposed(x, w))
     q.close()
+
+
+# ---- QKV bias and theta-dependent RoPE (the Qwen and Llama-3 configurations) -------------------------
+def _rope64(v: np.ndarray, pos: int, theta: float) -> np.ndarray:
+    """Rotate-half RoPE of one head in float64: pair (j, j + D/2) turns by pos * theta^(-2j/D)."""
+    d = v.shape[0]
+    j = np.arange(d // 2, dtype=np.float64)
+    ang = pos * theta ** (-2.0 * j / d)
+    x1, x2 = v[:d // 2].astype(np.float64), v[d // 2:].astype(np.float64)
+    return np.concatenate([x1 * np.cos(ang) - x2 * np.sin(ang), x2 * np.cos(ang) + x1 * np.sin(ang)])
+
+
+@pytest.mark.parametrize("theta", [500000.0, 1000000.0])
+def test_rope_theta_closed_form_all_pairs(oracle, theta):
+    """Every pair j of a D = 128 head at positions up to 8191 against float64 cos/sin of
+    pos * theta^(-2j/D). The bound is what fp32 rounding of the angle allows (a few ulp of pos *
+    freq); a wrong exponent (-j/D, D/2), a swapped pair or a wrong theta misses by orders more."""
+    rng = np.random.default_rng(8)
+    d = 128
+    for pos in (1, 7, 300, 4095, 8191):
+        v = rng.standard_normal(d).astype(np.float32)
+        got = oracle.rope(v, 1, d, pos, theta).astype(np.float64)
+        want = _rope64(v, pos, theta)
+        tol = (8.0 * pos * 2.0 ** -24 + 1e-6) * np.abs(v).max() * 2
+        assert np.max(np.abs(got - want)) <= tol, (pos, np.max(np.abs(got - want)), tol)
+    # pair j = 1 at pos 1 turns by exactly theta^(-2/D): two thetas must give two different rotations
+    e = np.zeros(d, np.float32)
+    e[1] = 1.0
+    r = oracle.rope(e, 1, d, 1, theta)
+    assert abs(float(r[1]) - np.cos(theta ** (-2.0 / d))) < 1e-6
+    assert abs(float(r[1 + d // 2]) - np.sin(theta ** (-2.0 / d))) < 1e-6
+
+
+def test_qkv_bias_added_before_rope_closed_form(oracle):
+    """Qwen's q/k/v biases (HF semantics: q = W_q x + b_q, then RoPE; the reference drops the bias,
+    src/runtime.rs:1368-1370). One layer with W_q = W_k = 0, O = identity and a zero FFN, so that
+    at position p: the K cache slot is rope(b_k, p), the V slot W_v rmsnorm(x) + b_v, and the
+    hidden state minus the embedding row is softmax_t(rope(b_q, p) . rope(b_k, t) / sqrt(D)) v_t
+    per head, all computed here in float64. Bias after RoPE (K slot b_k), a dropped bias (K slot
+    0) or a q bias missing from the scores each fail."""
+    H, hq, hkv, d, theta = 64, 4, 2, 16, 1000000.0
+    cfg = dict(vocab_size=16, hidden_dim=H, intermediate_dim=32, num_layers=1, num_heads=hq, num_kv_heads=hkv,
+               head_dim=d, max_seq_len=8, rms_norm_eps=1e-5, rope_theta=theta, qkv_bias=1, tied_lm_head=1)
+    eng = oracle.Engine(cfg, seed=21, q4_0=False, kv_bf16=False, threads=1)
+    f32 = lambda kind: eng.tensor_view(kind, 0).view(np.float32)  # noqa: E731
+    rng = np.random.default_rng(9)
+    f32(oracle.T_Q)[:] = 0.0
+    f32(oracle.T_K)[:] = 0.0
+    wv = rng.standard_normal((hkv * d, H)).astype(np.float32) * np.float32(0.5)
+    f32(oracle.T_V)[:] = wv.ravel()
+    f32(oracle.T_O)[:] = np.eye(H, hq * d, dtype=np.float32).ravel()
+    for k in (oracle.T_GATE, oracle.T_UP, oracle.T_DOWN):
+        f32(k)[:] = 0.0
+    bq = rng.standard_normal(hq * d).astype(np.float32)
+    bk = rng.standard_normal(hkv * d).astype(np.float32)
+    bv = rng.standard_normal(hkv * d).astype(np.float32)
+    f32(oracle.T_BQ)[:] = bq
+    f32(oracle.T_BK)[:] = bk
+    f32(oracle.T_BV)[:] = bv
+    embed = f32(oracle.T_EMBED).reshape(16, H).astype(np.float64)
+    gain = f32(oracle.T_ATTN_NORM).astype(np.float64)
+    kc, vc = eng.kv_cache(0)
+    vs = []
+    for pos, tok in enumerate((3, 11, 5, 7)):
+        eng.forward(tok, pos)
+        x = embed[tok]
+        xn = x / np.sqrt(np.mean(x * x) + 1e-5) * gain
+        want_k = np.concatenate([_rope64(bk[g * d:(g + 1) * d], pos, theta) for g in range(hkv)])
+        want_v = wv.astype(np.float64) @ xn + bv
+        vs.append(want_v)
+        np.testing.assert_allclose(kc[pos], want_k, rtol=0, atol=2e-5)
+        np.testing.assert_allclose(vc[pos], want_v, rtol=0, atol=2e-5)
+        attn = eng.hidden().astype(np.float64) - x
+        for h in range(hq):
+            g = h // (hq // hkv)
+            q = _rope64(bq[h * d:(h + 1) * d], pos, theta)
+            s = np.array([q @ _rope64(bk[g * d:(g + 1) * d], t, theta) for t in range(pos + 1)]) / np.sqrt(d)
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            want_o = sum(p[t] * vs[t][g * d:(g + 1) * d] for t in range(pos + 1))
+            np.testing.assert_allclose(attn[h * d:(h + 1) * d], want_o, rtol=0, atol=5e-5)
+        if pos == 0:  # one position: every head of a group returns its V row
+            for h in range(hq):
+                g = h // (hq // hkv)
+                np.testing.assert_allclose(attn[h * d:(h + 1) * d], want_v[g * d:(g + 1) * d], atol=5e-5)
+    eng.close()
