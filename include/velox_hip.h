@@ -247,9 +247,19 @@ int velox_hip_fill_normal(float* d_out, uint64_t n, uint64_t seed, uint64_t tag,
 #define VELOX_GEMV_SWIGLU 2
 int velox_hip_gemv_q4_0(const VeloxHipQ4Matrix* m, const float* d_x, const float* d_gain, float eps,
                         const float* d_bias, const float* d_res, float* d_y, int mode, hipStream_t stream);
-/* Fused RMSNorm + LM head + greedy argmax: logits and the winning index (lowest index on ties). */
+/* Fused RMSNorm + LM head + greedy argmax: logits and the winning index (lowest index on ties).
+ * Allocates its candidate buffer per call and returns after synchronizing the stream. */
 int velox_hip_lm_head_argmax(const VeloxHipQ4Matrix* m, const float* d_x, const float* d_gain, float eps,
                              float* d_logits, uint32_t* d_token, hipStream_t stream);
+/* velox_hip_lm_head_argmax for callers that cannot allocate device memory (code under hipGraph
+ * capture, serving loops, harnesses that forbid hipMalloc). No counterpart in the reference: its
+ * emitted step never allocates because the runner sizes every buffer up front. Same arguments and
+ * results as velox_hip_lm_head_argmax, but the per-workgroup candidates live in a fixed device
+ * array of the library (512 candidates, 4 KiB per GPU, held until the process ends; EINVAL if a
+ * matrix needed more), so the call allocates nothing and does not synchronize. Calls that overlap
+ * on one GPU (concurrent streams or threads) share that array and race. */
+int velox_hip_lm_head_argmax_noalloc(const VeloxHipQ4Matrix* m, const float* d_x, const float* d_gain, float eps,
+                                     float* d_logits, uint32_t* d_token, hipStream_t stream);
 /* Standalone two-stage argmax over n fp32 values (strict '>' lowest-index rule). */
 int velox_hip_argmax_f32(const float* d_x, uint32_t n, uint32_t* d_out, hipStream_t stream);
 /* Batched GEMM of `batch` <= 32 sequences (src/runners/velox_cuda_runner_k2.cu:553-997, batched

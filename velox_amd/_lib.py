@@ -159,6 +159,7 @@ _SIGS = {
     "velox_hip_gemm_q4_0_batch_m": (_I, [C.POINTER(Q4Matrix), _P, _P, _P, _U32, _U32, _U32, _P, _P, _U32, _P, _U32,
                                          _U32, _I, _U32, _P, _P]),
     "velox_hip_lm_head_argmax": (_I, [C.POINTER(Q4Matrix), _P, _P, _F, _P, _P, _P]),
+    "velox_hip_lm_head_argmax_noalloc": (_I, [C.POINTER(Q4Matrix), _P, _P, _F, _P, _P, _P]),
     "velox_hip_argmax_f32": (_I, [_P, _U32, _P, _P]),
     "velox_hip_rmsnorm": (_I, [_P, _P, _U32, _F, _P, _P]),
     "velox_hip_attention_decode": (_I, [_P, _P, _U32, _U32, _U32, _U32, _U32, _F, _U32, _P, _P]),

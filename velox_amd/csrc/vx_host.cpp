@@ -1265,28 +1265,27 @@ int velox_hip_gemm_q4_0_batch_m(const VeloxHipQ4Matrix* m, const void* d_mcodes,
 int velox_hip_lm_head_argmax(const VeloxHipQ4Matrix* m, const float* d_x, const float* d_gain, float eps,
                              float* d_logits, uint32_t* d_token, hipStream_t st) {
     if (!m || !d_x || !d_logits || !d_token || m->paired) return VELOX_HIP_EINVAL;
-    // scratch for candidates + counter, reused across calls on this device
-    static void* scratch = nullptr;
-    const uint32_t wgs = vx_gemv_max_wgs_default(), cap = 65536;
-    if (!scratch) {
-        hipError_t e = hipMalloc(&scratch, (size_t)cap * 8 + 256);
-        if (e != hipSuccess) return (int)e;
-        e = hipMemset(scratch, 0, (size_t)cap * 8 + 256);
-        if (e != hipSuccess) return (int)e;
-    }
+    // per-call candidate buffer (one (value, index) per GEMV workgroup), released once the call's
+    // work has finished: this entry point returns after a stream synchronization
+    const uint32_t wgs = vx_gemv_max_wgs_default(), n = vx_gemv_grid(m->n_tiles, wgs);
+    void* cand = nullptr;
+    hipError_t e = hipMalloc(&cand, (size_t)n * 8u);
+    if (e != hipSuccess) return (int)e;
     VxGemvArgs g;
     std::memset(&g, 0, sizeof(g));
     g.x = d_x;
     g.gain = d_gain;
     g.eps = eps;
     g.y = d_logits;
-    g.cand_v = (float*)scratch;
-    g.cand_i = (uint32_t*)((uint8_t*)scratch + (size_t)cap * 4);
+    g.cand_v = (float*)cand;
+    g.cand_i = (uint32_t*)((uint8_t*)cand + (size_t)n * 4u);
     g.active_mask = 1;
-    hipError_t e = vx_launch_gemv(vx_view_public(m), g, VX_EPI_ARGMAX, wgs, st);
+    e = vx_launch_gemv(vx_view_public(m), g, VX_EPI_ARGMAX, wgs, st);
     if (e == hipSuccess)
-        e = vx_launch_argmax_finalize(g.cand_v, g.cand_i, vx_gemv_grid(m->n_tiles, wgs), nullptr, nullptr, nullptr,
-                                      nullptr, d_token, 1, st);
+        e = vx_launch_argmax_finalize(g.cand_v, g.cand_i, n, nullptr, nullptr, nullptr, nullptr, d_token, 1, st);
+    const hipError_t es = hipStreamSynchronize(st);
+    if (e == hipSuccess) e = es;
+    hipFree(cand);
     return (int)e;
 }
 
