@@ -65,10 +65,13 @@ typedef struct VeloxHipModelConfig {
 
 typedef struct VeloxHipModel VeloxHipModel; /* opaque: the static memory plan */
 
-/* Mirror of VeloxCudaArena (src/codegen.rs:1032-1041) plus the plan pointer. weight_arena holds
- * the packed Q4_0 nibbles of every linear/embedding matrix, weight_scales their fp16 block scales
- * (codes and scales are split so that both stream with 128-bit loads), norm_weight_arena the fp32
- * norm gains, biases and the RoPE cos/sin table. */
+/* Layout-identical to VeloxCudaArena (src/codegen.rs:1032-1041): the same eight fields in the same
+ * order, so emitted code and runners that fill the struct themselves (velox_cuda_runner.cu:417-431)
+ * work unchanged. weight_arena holds the packed Q4_0 nibbles of every linear/embedding matrix,
+ * weight_scales their fp16 block scales (codes and scales are split so that both stream with
+ * 128-bit loads), norm_weight_arena the fp32 norm gains, biases and the RoPE cos/sin table. The
+ * plan an arena belongs to is not a field: the library records it against weight_arena when the
+ * arena is created (velox_hip_arena_create) or bound (velox_hip_arena_bind). */
 typedef struct VeloxHipArena {
     const uint8_t* weight_arena;
     uint8_t* kv_cache_pool;
@@ -78,7 +81,6 @@ typedef struct VeloxHipArena {
     const uint8_t* weight_scales;
     uint32_t quant_mode;
     uint32_t tied_lm_head;
-    const VeloxHipModel* model;
 } VeloxHipArena;
 
 /* Device-resident decode state (src/codegen.rs:1046-1050): one captured graph replays every step. */
@@ -90,8 +92,33 @@ typedef struct VeloxDecodeState {
 
 #define VELOX_HIP_RING_SIZE 1024u
 
-/* Built-in benchmark configurations (1, 2, 3, 5). which: "smollm_135m", "llama3_8b",
- * "qwen2_5_7b", "qwen2_72b". max_seq_len 0 keeps the default. */
+/* ---- .vlx model sources (the reference's DSL; `velox build model.vlx`, src/cli.rs:1214-1388) ----
+ * The model the decode step runs is read from the source's `model Name< const ... >` header
+ * (VOCAB, HIDDEN_DIM, INTERMEDIATE_DIM, NUM_LAYERS, NUM_HEADS, NUM_KV_HEADS, HEAD_DIM, S_MAX, B_MAX,
+ * ROPE_THETA), its weight declarations (b_q/b_k/b_v: QKV bias; no w_head/w_lm_head: tied head) and
+ * its first rmsnorm eps; theta and eps fall back on the reference's name rules
+ * (src/codegen.rs:962-975, src/ir.rs:549-553). The `target hardware` block gives the planner's
+ * budget: floor(vram_capacity * safety_factor) less the driver reserve (src/memory_planner.rs:372-
+ * 488) -> vram_budget_bytes (0 without a target block: the default 288 GB). max_seq_len 0 takes
+ * S_MAX. The config's max_batch and prefill_chunk stay 0: B_MAX is reported in the target info and
+ * the caller chooses the batched rows. quant_mode is GGML Q4_0, this backend's weight format.
+ * EINVAL for a malformed source, a missing dimension, or an MLA model (LATENT_KV_DIM), which
+ * velox_hip_vlx_mla_config reads. _load reads a file (ENOTLOADED if it cannot be read). */
+typedef struct VeloxHipVlxTarget {
+    char device[64];
+    uint64_t vram_capacity_bytes;
+    double safety_factor;
+    uint64_t safe_budget_bytes;     /* floor(vram_capacity * safety_factor) */
+    uint64_t system_reserve_bytes;  /* driver + stream ring reserve */
+    uint32_t b_max, s_max;          /* the model header's B_MAX and S_MAX (0 if absent) */
+} VeloxHipVlxTarget;
+int velox_hip_vlx_config(const char* source, uint32_t max_seq_len, VeloxHipModelConfig* out,
+                         VeloxHipVlxTarget* target);
+int velox_hip_vlx_load(const char* path, uint32_t max_seq_len, VeloxHipModelConfig* out, VeloxHipVlxTarget* target);
+
+/* Built-in benchmark configurations (1, 2, 3, 5), each declared as a .vlx source targeting one
+ * MI355X and read by velox_hip_vlx_config. which: "smollm_135m", "llama3_8b", "qwen2_5_7b",
+ * "qwen2_72b" (also the config's name). max_seq_len 0 keeps the source's S_MAX. */
 int velox_hip_builtin_config(const char* which, uint32_t max_seq_len, VeloxHipModelConfig* out);
 
 /* ---- plan (memory_planner, src/memory_planner.rs:282-488) ---- */
@@ -108,9 +135,21 @@ uint64_t velox_hip_model_step_bytes(const VeloxHipModel* m, uint64_t pos);
 uint64_t velox_hip_model_logits_offset(const VeloxHipModel* m);
 uint64_t velox_hip_model_hidden_offset(const VeloxHipModel* m);
 
-/* ---- arena (velox_cuda_runner.cu:417-431: cudaMalloc x3 + mapped host ring) ---- */
+/* ---- arena (velox_cuda_runner.cu:417-431: cudaMalloc x3 + mapped host ring) ----
+ * create: one hipMalloc holding every device region (256-byte aligned) plus the mapped host ring,
+ * initialized (zeroed, RoPE table) and recorded against its weight_arena.
+ * bind: the reference runner's pattern -- the caller allocated the buffers itself, each at least
+ * the size velox_hip_model_arena_bytes gives (weights, scales, norms, KV pool, activations; a
+ * mapped ring of VELOX_HIP_RING_SIZE * max(1, max_batch) entries), and filled the eight fields with
+ * quant_mode and tied_lm_head equal to the plan's. bind initializes those buffers as create does
+ * and records the plan; EINVAL for a missing buffer, mismatching flags or a weight_arena already
+ * recorded.
+ * destroy: forgets the arena; frees the buffers only if create allocated them.
+ * model: the plan an arena was created or bound with (NULL for an unknown arena). */
 int velox_hip_arena_create(const VeloxHipModel* m, VeloxHipArena* out);
+int velox_hip_arena_bind(const VeloxHipModel* m, VeloxHipArena* a);
 int velox_hip_arena_destroy(VeloxHipArena* a);
+const VeloxHipModel* velox_hip_arena_model(const VeloxHipArena* a);
 
 /* ---- loaders (velox_cuda_runner.cu:154-199 stream_tensor_converted) ----
  * q4_0: host GGML Q4_0 blocks, row-major [rows][in/32] x 18 B, for a matrix kind of `layer`.
@@ -167,6 +206,12 @@ void velox_Qwen2_5_7B_decode_hip(VeloxHipArena* ctx, uint32_t token_in, size_t s
 void velox_Qwen2_72B_decode_graph_step_hip(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
 void velox_Qwen2_72B_decode_hip(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t active_mask,
                                 hipStream_t stream);
+void velox_Qwen2_5_7B_prefill_graph_step_hip(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
+void velox_Qwen2_5_7B_prefill_hip(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t active_mask,
+                                  hipStream_t stream);
+void velox_Qwen2_72B_prefill_graph_step_hip(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
+void velox_Qwen2_72B_prefill_hip(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t active_mask,
+                                 hipStream_t stream);
 
 /* ---- per-kernel entry points (device pointers; for parity tests and benchmarks) ---- */
 
@@ -201,7 +246,8 @@ void velox_hip_decode_batch_graph_step(VeloxHipArena* ctx, uint32_t batch, uint6
  * the last row's argmax past the prompt} -- what n_tokens token-by-token prefill steps leave --,
  * ring[p % VELOX_HIP_RING_SIZE] holds each position's argmax and the last chunk's logits are at
  * the batch layout's logits_offset (row r = position of the chunk's r-th row). Positions must lie
- * inside the staged prompt and below max_seq_len. Returns the first launch error. */
+ * inside the prompt last staged with velox_hip_set_prompt and below max_seq_len (else EINVAL).
+ * Returns this call's first launch error (an earlier unread error stays for velox_hip_last_error). */
 int velox_hip_prefill_batch(VeloxHipArena* ctx, uint64_t pos0, uint32_t n_tokens, uint64_t active_mask,
                             hipStream_t stream);
 
@@ -292,14 +338,18 @@ int velox_hip_gemm_q4_0_batch_m(const VeloxHipQ4Matrix* m, const void* d_mcodes,
 int velox_hip_rmsnorm(const float* d_x, const float* d_w, uint32_t n, float eps, float* d_y, hipStream_t stream);
 /* Decode attention for one layer at position pos: RoPE on q and the new k (table cos/sin of
  * pos*theta^(-2j/D)), bf16 K/V append at pos, split-K online softmax with an LSE merge.
- * qkv: fp32 [hq*d | hkv*d | hkv*d]; kv_layer: bf16 [2][hkv][s_max][d]; out: fp32 [hq*d]. */
+ * qkv: fp32 [hq*d | hkv*d | hkv*d]; out: fp32 [hq*d]. kv_layer: bf16, s_cap = s_max rounded up to
+ * a multiple of 32 positions; the K plane [hkv][s_cap][d] row-major, then the V plane
+ * [hkv][s_cap/32][d][32]: per block of 32 positions, dimension-major, position r (0..31) of a block
+ * in slot 8*((r%16)/4) + 4*(r/16) + r%4 (the order the P.V MFMA consumes). The arenas' KV pools use
+ * this layout per layer (and sequence). */
 int velox_hip_attention_decode(const float* d_qkv, uint16_t* d_kv_layer, uint32_t hq, uint32_t hkv,
                                uint32_t d, uint32_t s_max, uint32_t pos, float theta, uint32_t splits,
                                float* d_out, hipStream_t stream);
 
 /* ---- runner (velox_cuda_runner.cu:327-726 flow: plan, alloc, load, capture, prefill, decode) ---- */
 typedef struct VeloxHipRunOptions {
-    const char* model;       /* builtin config name */
+    const char* model;       /* builtin config name (unless model_file or weights_path is given) */
     uint32_t max_seq_len;    /* 0 = prompt_len + warmup + steps + 1 */
     uint32_t prompt_len;     /* random prompt tokens (seeded) */
     uint32_t warmup;         /* untimed decode steps */
@@ -323,6 +373,8 @@ typedef struct VeloxHipRunOptions {
     uint32_t prefill_chunk;  /* >1 (single sequence, no context_len): the prompt runs through
                                 velox_hip_prefill_batch in chunks of this many positions (<= 64)
                                 instead of one decode step each */
+    const char* model_file;  /* non-NULL: the model is read from this .vlx source (velox_hip_vlx_load),
+                                its target block setting the VRAM budget; `model` is then ignored */
 } VeloxHipRunOptions;
 
 typedef struct VeloxHipRunReport {
@@ -335,11 +387,15 @@ typedef struct VeloxHipRunReport {
     double kernel_bytes;                    /* algorithmic bytes of that launch */
     uint32_t kernel_launches;               /* launches averaged over (all layers, several passes) */
     uint32_t n_tokens;                      /* tokens written to `tokens` */
-    uint32_t first_token;
+    uint32_t first_token;                   /* the argmax after the last prompt position */
     int status;
+    uint32_t first_position;                /* position whose argmax is tokens[0] (the first decoded
+                                               position: context_len) */
 } VeloxHipRunReport;
 
-/* Runs the whole flow; tokens (capacity max_tokens) receives prompt-forced and generated ids. */
+/* Runs the whole flow; tokens (capacity max_tokens) receives, from position first_position on, the
+ * argmax after every position (prompt-forced positions included), drained from the 1024-entry ring
+ * at least once per 1024 positions. */
 int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_tokens, VeloxHipRunReport* rep);
 
 /* ---- GGUF checkpoints (GGML's container, read by the reference's K2 runner,
@@ -366,8 +422,10 @@ int velox_hip_gguf_load(VeloxHipArena* arena, const VeloxHipGguf* g, hipStream_t
  * Per head h: q_abs_h = W_uk[h]^T q_nope_h; s_ht = softmax_scale * (q_abs_h . c_t + rope(q_rope_h) .
  * kr_t); ctx_h = softmax_t(s) . c_t; o_h = W_uv[h] ctx_h; hidden += W_o [o_h]. q = W_qb rmsnorm(W_qa x)
  * (q_lora_rank > 0) or W_qb x; [c_t | kr_t] = [rmsnorm(c) | rope(kr)] of W_kva x, appended to the
- * bf16 latent cache. With num_heads 1, no q LoRA, no rope part, kv_norm 0 and identity W_kvb this
- * is the reference's simplified step. Weights are fp8 e4m3fn with fp32 scales per 128x128 block. */
+ * bf16 latent cache. Weights are fp8 e4m3fn with fp32 scales per 128x128 block. The device step
+ * takes num_heads a multiple of 16 and a 64-wide rope part; the reduction to the reference's
+ * simplified single-head step (one head, no q LoRA, no rope part, kv_norm 0, identity W_kvb) holds
+ * in the CPU oracle only, which is how the DeepSeek-V3 form is tied to the reference. */
 typedef struct VeloxHipMlaConfig {
     uint32_t hidden_dim, num_heads, q_lora_rank, kv_lora_rank, qk_nope_dim, qk_rope_dim, v_head_dim;
     uint32_t num_layers, max_seq_len, max_batch; /* max_batch <= 32 */
@@ -379,6 +437,12 @@ typedef struct VeloxHipMlaConfig {
 } VeloxHipMlaConfig;
 
 typedef struct VeloxHipMla VeloxHipMla;
+
+/* An MLA model's .vlx source (LATENT_KV_DIM, Q_LATENT_DIM, ROPE_DIM, HEAD_DIM as nope and v width,
+ * as examples/deepseek_v3_mla.vlx declares them) -> the MLA layer configuration; budget as
+ * velox_hip_vlx_config. max_seq_len / max_batch 0 take S_MAX / B_MAX (at most 32). */
+int velox_hip_vlx_mla_config(const char* source, uint32_t max_seq_len, uint32_t max_batch, VeloxHipMlaConfig* out,
+                             VeloxHipVlxTarget* target);
 
 /* weight kinds: fp8 matrices (row-major [rows][cols] as in the checkpoint) and fp32 gains */
 enum {

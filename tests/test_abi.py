@@ -152,3 +152,18 @@ def test_runner_rejects_unsupported_arguments():
     assert r.returncode == 1 and "bad token id 'x'" in r.stderr
     r = subprocess.run([runner, "--speculative"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 1 and "not supported" in r.stderr
+
+
+def test_arena_struct_is_the_reference_layout():
+    """VeloxHipArena is VeloxCudaArena (src/codegen.rs:1032-1041): six pointers then quant_mode and
+    tied_lm_head, nothing after them, in the header and in the Python mirror."""
+    import re
+
+    want = ["weight_arena", "kv_cache_pool", "activation_arena", "host_pinned_ring", "norm_weight_arena",
+            "weight_scales", "quant_mode", "tied_lm_head"]
+    assert [f for f, _ in L.Arena._fields_] == want
+    assert C.sizeof(L.Arena) == 6 * 8 + 2 * 4
+    assert [getattr(L.Arena, f).offset for f in want] == [0, 8, 16, 24, 32, 40, 48, 52]
+    hdr = open(L.HEADER).read()
+    body = re.search(r"typedef struct VeloxHipArena \{(.*?)\} VeloxHipArena;", hdr, re.S).group(1)
+    assert re.findall(r"(\w+);", body) == want

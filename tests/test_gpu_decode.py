@@ -171,3 +171,121 @@ def test_decode_long_context_vs_oracle(oracle, splits):
         assert d < LOGIT_TOL, (pos, d)
     gpu.close()
     ref.close()
+
+
+def test_caller_allocated_arena_bind(hiplib):
+    """The reference runner's allocation pattern (velox_cuda_runner.cu:417-431): the caller allocates
+    every buffer itself, fills the eight VeloxCudaArena fields and binds the plan. Decoding through
+    the model-named entry point on that arena equals decoding on an arena the library created, bit
+    for bit; a second bind of the same buffers and mismatching flags are refused."""
+    import ctypes as C
+
+    h = L.hip()
+    h.hipMalloc.restype = C.c_int
+    h.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+    h.hipHostMalloc.restype = C.c_int
+    h.hipHostMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t, C.c_uint]
+    h.hipFree.argtypes = [C.c_void_p]
+    h.hipHostFree.argtypes = [C.c_void_p]
+    seed = 41
+    ref = HipDecodeEngine("smollm_135m", seed=seed, max_seq_len=16, num_layers=2, norm_sigma=0.1)
+    sizes = ref.arena_bytes()
+    bufs = {}
+    for k in ("weights", "scales", "norms", "kv", "activations"):
+        p = C.c_void_p()
+        assert h.hipMalloc(C.byref(p), sizes[k]) == 0
+        bufs[k] = p.value
+    ring = C.c_void_p()
+    assert h.hipHostMalloc(C.byref(ring), L.RING_SIZE * 4, 0x2) == 0  # mapped
+    a = L.Arena()
+    a.weight_arena, a.weight_scales, a.norm_weight_arena = bufs["weights"], bufs["scales"], bufs["norms"]
+    a.kv_cache_pool, a.activation_arena = bufs["kv"], bufs["activations"]
+    a.host_pinned_ring = C.cast(ring, C.POINTER(C.c_uint32))
+    a.quant_mode, a.tied_lm_head = L.QUANT_GGML_Q4_0, 0  # SmolLM's head is tied: refused
+    assert hiplib.velox_hip_arena_bind(ref._model, C.byref(a)) == L.EINVAL
+    a.tied_lm_head = 1
+    L.check(hiplib.velox_hip_arena_bind(ref._model, C.byref(a)), "arena_bind")
+    assert hiplib.velox_hip_arena_model(C.byref(a)) == ref._model.value
+    assert hiplib.velox_hip_arena_bind(ref._model, C.byref(a)) == L.EINVAL  # already bound
+    L.check(hiplib.velox_hip_synthesize_model(C.byref(a), seed, 0.02, 0.1, None), "synthesize")
+    logits_off = hiplib.velox_hip_model_logits_offset(ref._model)
+    V = ref.cfg.vocab_size
+    tok = 17
+    for pos in range(4):
+        want = ref.forward_step(tok, pos)
+        hiplib.velox_SmolLM_135M_decode_hip(C.byref(a), tok, pos, 1, None)
+        assert h.hipDeviceSynchronize() == 0 and hiplib.velox_hip_last_error() == 0
+        got = np.empty(V, np.float32)
+        L.memcpy_dtoh(got.ctypes.data, bufs["activations"] + logits_off, got.nbytes)
+        assert np.array_equal(got.view(np.uint32), ref.logits.view(np.uint32))
+        assert C.cast(ring, C.POINTER(C.c_uint32))[pos] == want
+        tok = want
+    L.check(hiplib.velox_hip_arena_destroy(C.byref(a)), "destroy")  # forgets it, frees nothing
+    assert hiplib.velox_hip_arena_model(C.byref(a)) is None
+    for p in bufs.values():
+        assert h.hipFree(p) == 0
+    assert h.hipHostFree(ring) == 0
+    ref.close()
+
+
+def test_run_drains_the_ring_past_1024_positions(oracle):
+    """velox_hip_run over more positions than the 1024-entry ring (ADVICE: tokens were read only
+    at the end, shifted once positions wrapped): every position's token is the engine's own greedy
+    decode of the same prompt, from position 0 on."""
+    seed, P, steps = 29, 6, 1100
+    prompt = [int(t) for t in oracle.prompt_tokens(seed, P, 49152)]
+    rep, toks = run("smollm_135m", prompt=prompt, warmup=3, steps=steps, seed=seed, num_layers=1,
+                    max_seq_len=P + 3 + steps + 1, max_tokens=2048)
+    assert rep["status"] == 0 and rep["first_position"] == 0 and rep["n_tokens"] == P + 3 + steps
+    eng = HipDecodeEngine("smollm_135m", seed=seed, max_seq_len=P + 3 + steps + 1, num_layers=1)
+    want = eng.generate_greedy_into(prompt, 3 + steps + 1)
+    eng.close()
+    assert rep["first_token"] == want[0]
+    assert toks[P - 1:] == want[:len(toks) - (P - 1)]
+
+
+SMOLLM_VLX = """
+target hardware { device: "amd_mi355x"; vram_capacity: 8 * GiB; safety_factor: 0.95; }
+model SmolLM_135M<const B_MAX: usize = 1, const S_MAX: usize = 64, const VOCAB: usize = 49152,
+    const HIDDEN_DIM: usize = 576, const INTERMEDIATE_DIM: usize = 1536, const NUM_LAYERS: usize = 30,
+    const NUM_HEADS: usize = 9, const NUM_KV_HEADS: usize = 3, const HEAD_DIM: usize = 64> {
+    @vram_immutable weight w_embed: Tensor<[VOCAB, HIDDEN_DIM], f32> = safetensors("m.safetensors", "e");
+    scope decode<const B: usize>(t: Tensor<[B, 1], u32>, step: usize) -> Tensor<[B, 1], u32> {
+        let x = rmsnorm(h, w_attn_norm[l], eps = 1e-5);
+    }
+}
+"""
+
+
+def test_run_from_a_vlx_model_source(oracle, tmp_path):
+    """`velox build model.vlx` flow: the runner reads the model from its .vlx source
+    (velox_hip_run's model_file, the runner binary's --model-file) and decodes exactly what the
+    builtin configuration with the same shapes decodes; the named entry points accept the
+    source's model name."""
+    import os
+    import re
+    import subprocess
+
+    path = tmp_path / "smollm.vlx"
+    path.write_text(SMOLLM_VLX)
+    seed, P = 37, 4
+    prompt = [int(t) for t in oracle.prompt_tokens(seed, P, 49152)]
+    _, want = run("smollm_135m", prompt=prompt, warmup=0, steps=5, seed=seed, num_layers=2, max_seq_len=32)
+    rep, got = run("", prompt=prompt, warmup=0, steps=5, seed=seed, num_layers=2, max_seq_len=32,
+                   model_file=str(path))
+    assert rep["status"] == 0 and got == want
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    runner = os.path.join(root, "velox_amd", "lib", "velox_hip_runner")
+    r = subprocess.run([runner, "--model-file", str(path), "--tokens", ",".join(map(str, prompt)), "--steps", "4",
+                        "--seed", str(seed), "--layers", "2"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    steps = [int(t) for t in re.findall(r"^\[Step \d+\] Token: (\d+)$", r.stdout, re.M)]
+    _, want4 = run("smollm_135m", prompt=prompt, warmup=0, steps=3, seed=seed, num_layers=2)
+    assert steps == want4[P - 1:P - 1 + 4]
+    eng = HipDecodeEngine(str(path), seed=seed, max_seq_len=16, num_layers=2)
+    assert eng.cfg.name.decode() == "SmolLM_135M"
+    import ctypes as C
+
+    eng.lib.velox_SmolLM_135M_decode_hip(C.byref(eng.arena), prompt[0], 0, 1, None)
+    eng.sync()  # raises if the named entry point refused the arena
+    eng.close()

@@ -238,3 +238,15 @@ def test_run_with_batched_prefill_matches_engine(oracle):
     gpu.close()
     with pytest.raises(RuntimeError):
         run("smollm_135m", prompt_len=1, warmup=0, steps=2, context_len=8, num_layers=1, prefill_chunk=8)
+
+
+def test_prefill_rejects_positions_past_the_staged_prompt():
+    """Every row reads its token from the staged prompt: positions past it are refused (EINVAL)
+    instead of reading stale prompt memory."""
+    lib = L.load()
+    b = HipDecodeEngine(SMOLLM, max_seq_len=32, num_layers=1, prefill_chunk=8)
+    b.set_prompt([1, 2, 3, 4])
+    assert lib.velox_hip_prefill_batch(C.byref(b.arena), 0, 6, 1, None) == L.EINVAL
+    assert lib.velox_hip_prefill_batch(C.byref(b.arena), 3, 2, 1, None) == L.EINVAL
+    b.prefill_batch(0, 4)
+    b.close()

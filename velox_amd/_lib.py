@@ -44,7 +44,6 @@ class Arena(C.Structure):
         ("weight_arena", C.c_void_p), ("kv_cache_pool", C.c_void_p), ("activation_arena", C.c_void_p),
         ("host_pinned_ring", C.POINTER(C.c_uint32)), ("norm_weight_arena", C.c_void_p),
         ("weight_scales", C.c_void_p), ("quant_mode", C.c_uint32), ("tied_lm_head", C.c_uint32),
-        ("model", C.c_void_p),
     ]
 
 
@@ -67,7 +66,7 @@ class RunOptions(C.Structure):
         ("norm_sigma", C.c_float), ("use_graph", C.c_uint32), ("num_layers", C.c_uint32),
         ("kernel_passes", C.c_uint32), ("verbose", C.c_uint32), ("prompt_tokens", C.POINTER(C.c_uint32)),
         ("context_len", C.c_uint32), ("batch", C.c_uint32), ("weights_path", C.c_char_p),
-        ("prefill_chunk", C.c_uint32),
+        ("prefill_chunk", C.c_uint32), ("model_file", C.c_char_p),
     ]
 
 
@@ -77,7 +76,14 @@ class RunReport(C.Structure):
         ("tok_per_s", C.c_double), ("bytes_per_step", C.c_double), ("hbm_gbps", C.c_double),
         ("wall_ms", C.c_double), ("kernel_us", C.c_double), ("kernel_bytes", C.c_double),
         ("kernel_launches", C.c_uint32), ("n_tokens", C.c_uint32), ("first_token", C.c_uint32), ("status", C.c_int),
+        ("first_position", C.c_uint32),
     ]
+
+
+class VlxTarget(C.Structure):
+    _fields_ = [("device", C.c_char * 64), ("vram_capacity_bytes", C.c_uint64), ("safety_factor", C.c_double),
+                ("safe_budget_bytes", C.c_uint64), ("system_reserve_bytes", C.c_uint64), ("b_max", C.c_uint32),
+                ("s_max", C.c_uint32)]
 
 
 class MlaConfig(C.Structure):
@@ -117,6 +123,8 @@ _U32, _U64, _F, _I = C.c_uint32, C.c_uint64, C.c_float, C.c_int
 _SIGS = {
     "velox_hip_last_error": (_I, []),
     "velox_hip_builtin_config": (_I, [C.c_char_p, _U32, C.POINTER(ModelConfig)]),
+    "velox_hip_vlx_config": (_I, [C.c_char_p, _U32, C.POINTER(ModelConfig), C.POINTER(VlxTarget)]),
+    "velox_hip_vlx_load": (_I, [C.c_char_p, _U32, C.POINTER(ModelConfig), C.POINTER(VlxTarget)]),
     "velox_hip_model_create": (_I, [C.POINTER(ModelConfig), C.POINTER(_P)]),
     "velox_hip_model_destroy": (None, [_P]),
     "velox_hip_model_config": (_I, [_P, C.POINTER(ModelConfig)]),
@@ -126,6 +134,8 @@ _SIGS = {
     "velox_hip_model_hidden_offset": (_U64, [_P]),
     "velox_hip_arena_create": (_I, [_P, C.POINTER(Arena)]),
     "velox_hip_arena_destroy": (_I, [C.POINTER(Arena)]),
+    "velox_hip_arena_bind": (_I, [_P, C.POINTER(Arena)]),
+    "velox_hip_arena_model": (_P, [C.POINTER(Arena)]),
     "velox_hip_load_q4_0": (_I, [C.POINTER(Arena), _I, _U32, _P, _U64, _P]),
     "velox_hip_load_f32": (_I, [C.POINTER(Arena), _I, _U32, _P, _U64, _P]),
     "velox_hip_synthesize_model": (_I, [C.POINTER(Arena), _U64, _F, _F, _P]),
@@ -172,6 +182,7 @@ _SIGS = {
     "velox_hip_gguf_config": (_I, [_P, _U32, C.POINTER(ModelConfig)]),
     "velox_hip_gguf_load": (_I, [C.POINTER(Arena), _P, _P]),
     "velox_hip_mla_builtin_config": (_I, [C.c_char_p, _U32, _U32, C.POINTER(MlaConfig)]),
+    "velox_hip_vlx_mla_config": (_I, [C.c_char_p, _U32, _U32, C.POINTER(MlaConfig), C.POINTER(VlxTarget)]),
     "velox_hip_mla_create": (_I, [C.POINTER(MlaConfig), C.POINTER(_P)]),
     "velox_hip_mla_destroy": (None, [_P]),
     "velox_hip_mla_buffers": (_I, [_P, C.POINTER(MlaBuffers)]),

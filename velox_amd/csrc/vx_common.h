@@ -100,7 +100,7 @@ struct VxMat {
 struct VxGemvArgs {
     const uint4* codes;
     const uint16_t* scales;
-    uint32_t n, k, n_tiles, n_iter, contig;
+    uint32_t n, k, n_tiles, n_iter;
     const float* x;
     const float* gain;
     float eps;
@@ -196,8 +196,9 @@ uint64_t vx_mmat_code_bytes(const VxMMat& m);
 uint64_t vx_mmat_scale_bytes(const VxMMat& m);
 uint32_t vx_mgemm_grid(uint32_t n_tiles);  // workgroups of one grid row (also the ARGMAX candidate count)
 hipError_t vx_launch_mlayout(const VxMat& src, const VxMMat& dst, hipStream_t st);
-// Same arguments and epilogues as vx_launch_bgemm (codes/scales/n/k from `w`); ksplit > 1 is also
-// allowed for STORE, whose partials vx_launch_msum then sums (+ bias) into y.
+// The batched Q4_0 GEMM over an MFMA-layout copy (codes/scales/n/k from `w`), epilogues as the
+// GEMV's; ksplit > 1 (STORE or RESID) stores K-split partials, which vx_launch_msum (STORE, + bias)
+// or the next batched RMSNorm (RESID) sums in split order.
 hipError_t vx_launch_mgemm(const VxMMat& w, const VxBGemmArgs& a, int epi, hipStream_t st);
 hipError_t vx_launch_msum(const float* part, uint32_t nparts, uint64_t pstride, const float* bias, float* y,
                           uint32_t n, uint32_t ldy, uint32_t batch, uint32_t accumulate, uint64_t mask,
@@ -234,8 +235,6 @@ enum { VX_EPI_STORE = 0, VX_EPI_RESID = 1, VX_EPI_SWIGLU = 2, VX_EPI_ARGMAX = 3 
 hipError_t vx_launch_gemv(const VxMat& m, const VxGemvArgs& a, int epi, uint32_t max_wgs, hipStream_t st);
 hipError_t vx_launch_attention(const VxAttnArgs& a, uint32_t d, hipStream_t st);
 // vx_batch.hip
-hipError_t vx_launch_bgemm(const VxMat& m, const VxBGemmArgs& a, int epi, hipStream_t st);
-uint32_t vx_bgemm_grid(uint32_t n_tiles, uint32_t s);
 // Batched prefill (vx_batch.hip): row r of a chunk is position p0 + r of the one sequence.
 hipError_t vx_launch_prefill_rows(VeloxDecodeState* rows, uint32_t n_rows, uint64_t p0, const uint32_t* prompt,
                                   uint64_t mask, hipStream_t st);

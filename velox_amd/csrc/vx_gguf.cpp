@@ -10,6 +10,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -262,7 +263,7 @@ int velox_hip_gguf_config(const VeloxHipGguf* g, uint32_t max_seq_len, VeloxHipM
 }
 
 int velox_hip_gguf_load(VeloxHipArena* arena, const VeloxHipGguf* g, hipStream_t st) {
-    if (!arena || !arena->model || !g) return VELOX_HIP_EINVAL;
+    if (!arena || !velox_hip_arena_model(arena) || !g) return VELOX_HIP_EINVAL;
     VeloxHipModelConfig c;
     int rc = velox_hip_gguf_config(g, 0, &c);
     if (rc) return rc;
@@ -311,11 +312,13 @@ int velox_hip_gguf_load(VeloxHipArena* arena, const VeloxHipGguf* g, hipStream_t
     const uint64_t H = c.hidden_dim, F = c.intermediate_dim, D = c.head_dim;
     const uint64_t qd = (uint64_t)c.num_heads * D, kvd = (uint64_t)c.num_kv_heads * D;
     VeloxHipModelConfig mc;
-    rc = velox_hip_model_config(arena->model, &mc);
+    rc = velox_hip_model_config(velox_hip_arena_model(arena), &mc);
     if (rc) return rc;
     if (mc.hidden_dim != c.hidden_dim || mc.num_layers != c.num_layers || mc.intermediate_dim != c.intermediate_dim ||
         mc.num_heads != c.num_heads || mc.num_kv_heads != c.num_kv_heads || mc.vocab_size != c.vocab_size ||
-        mc.qkv_bias != c.qkv_bias || mc.tied_lm_head != c.tied_lm_head)
+        mc.qkv_bias != c.qkv_bias || mc.tied_lm_head != c.tied_lm_head || mc.head_dim != c.head_dim ||
+        std::fabs(mc.rms_norm_eps - c.rms_norm_eps) > 1e-3f * c.rms_norm_eps ||
+        std::fabs(mc.rope_theta - c.rope_theta) > 1e-6f * c.rope_theta)
         return VELOX_HIP_ESHAPE;
     rc = matrix("token_embd.weight", VELOX_T_EMBED, 0, c.vocab_size, H, 0);
     for (uint32_t l = 0; l < c.num_layers && !rc; ++l) {

@@ -11,13 +11,15 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "vx_common.h"
 
 namespace {
 
-int g_last_error = 0;
+// first error of the calling thread (each host thread drives its own streams)
+thread_local int g_last_error = 0;
 
 inline int vx_record(hipError_t e) {
     if (e != hipSuccess && g_last_error == 0) g_last_error = (int)e;
@@ -47,31 +49,12 @@ struct VxLayerPlan {
     uint64_t attn_norm = 0, mlp_norm = 0, bias = 0;
 };
 
-// K splits of a batched residual GEMM: enough workgroup rows over its 64-row groups to give
-// about 512 workgroups (the GEMMs of hidden-sized outputs have only hidden / 64 row groups), at
-// most 8 (the partials the batched RMSNorm folds in) and at most one item per split.
-uint32_t vx_bgemm_ksplit(const VxMatPlan& m) {
-    uint32_t ks = 0;
-    if (const char* env = std::getenv("VELOX_HIP_BGEMM_KSPLIT")) ks = (uint32_t)std::strtoul(env, nullptr, 10);  // tuning
-    if (ks == 0) {
-        const uint32_t wgs = vx_bgemm_grid(m.n_tiles, m.s);
-        ks = (512u + wgs - 1u) / wgs;
-    }
-    if (ks > 8u) ks = 8u;
-    if (ks > m.n_iter) ks = m.n_iter;
-    return ks ? ks : 1u;
-}
-
 // K splits of a batched GEMM over the MFMA layout: enough grid rows for about 1024 workgroups (two
 // 16-row tiles each, its 4 waves splitting K again), at most 8 (the partials a batched RMSNorm or
 // the partial sum folds in) and at most one group of 4 blocks per split.
 uint32_t vx_mgemm_ksplit(const VxMatPlan& m) {
-    uint32_t ks = 0;
-    if (const char* env = std::getenv("VELOX_HIP_MGEMM_KSPLIT")) ks = (uint32_t)std::strtoul(env, nullptr, 10);  // tuning
-    if (ks == 0) {
-        const uint32_t wgs = vx_mgemm_grid(m.m_tiles);
-        ks = (1024u + wgs - 1u) / wgs;
-    }
+    const uint32_t wgs = vx_mgemm_grid(m.m_tiles);
+    uint32_t ks = (1024u + wgs - 1u) / wgs;
     if (ks > 8u) ks = 8u;
     if (ks > m.m_grp) ks = m.m_grp;
     return ks ? ks : 1u;
@@ -102,14 +85,41 @@ struct VeloxHipModel {
     // K-split partials of the residual GEMMs (o_proj, down): [ksplit][batch][hidden]
     uint64_t a_bpart_r = 0;
     uint32_t ksplit_o = 1, ksplit_down = 1, ksplit_qkv = 1;
-    bool mgemm = false;  // batched GEMMs over the MFMA-layout copies (else the LDS-staged tiled GEMM)
-    // fp16 activation operands: element k of row m at m * x_ld + (k / 32) * x_bs + k % 32 -- block-major
-    // [k / 32][16-row-padded rows][32] for the MFMA-layout GEMM (one operand load = 1 KiB contiguous),
-    // row-major [rows][xw] for the tiled GEMM
+    // fp16 activation operands of the batched GEMMs (over the MFMA-layout copies): element k of row m
+    // at m * x_ld + (k / 32) * x_bs + k % 32, block-major [k / 32][16-row-padded rows][32] (one operand
+    // load = 1 KiB contiguous)
     uint32_t x_ld = 0, x_bs = 32;
 };
 
 namespace {
+
+// The plan of every live arena, keyed by its weight_arena pointer: VeloxHipArena keeps the
+// reference's eight fields (VeloxCudaArena, src/codegen.rs:1032-1041) and nothing else, so the plan
+// cannot travel inside it. Arenas enter through velox_hip_arena_create (library-owned buffers) or
+// velox_hip_arena_bind (caller-owned buffers, the reference runner's cudaMalloc pattern).
+struct VxArenaRec {
+    const uint8_t* key = nullptr;   // weight_arena
+    const VeloxHipModel* model = nullptr;
+    uint8_t* base = nullptr;        // the one device allocation (owned arenas), else nullptr
+    uint32_t* ring = nullptr;       // the mapped host ring (owned arenas), else nullptr
+    uint32_t staged_plen = 0;       // prompt length of the last velox_hip_set_prompt
+};
+std::mutex g_arena_mu;
+std::vector<VxArenaRec> g_arenas;
+
+VxArenaRec* vx_rec_locked(const uint8_t* key) {
+    for (VxArenaRec& r : g_arenas)
+        if (r.key == key) return &r;
+    return nullptr;
+}
+
+// The plan `a` was created or bound with; nullptr for an unknown arena.
+const VeloxHipModel* vx_model(const VeloxHipArena* a) {
+    if (!a || !a->weight_arena) return nullptr;
+    std::lock_guard<std::mutex> lock(g_arena_mu);
+    const VxArenaRec* r = vx_rec_locked(a->weight_arena);
+    return r ? r->model : nullptr;
+}
 
 // Lanes per row S: the largest of {32, 16, 8, 4} wasting at most 1/32 of a row's blocks, else the
 // one wasting least. Padded blocks are zero and are streamed with the rest, so waste costs
@@ -194,7 +204,7 @@ hipError_t vx_build_m(const VeloxHipArena* a, const VxMatPlan& p, hipStream_t st
 
 // KV cache of (layer, sequence): [layer][sequence][K | V][kv head][position][dim] bf16
 uint16_t* vx_kv(const VeloxHipArena* a, uint32_t layer, uint32_t seq) {
-    const VeloxHipModel* M = a->model;
+    const VeloxHipModel* M = vx_model(a);
     return (uint16_t*)(a->kv_cache_pool + M->kv_layer_bytes * ((uint64_t)layer * M->batch + seq));
 }
 
@@ -236,32 +246,6 @@ int velox_hip_last_error(void) {
     const int e = g_last_error;
     g_last_error = 0;
     return e;
-}
-
-int velox_hip_builtin_config(const char* which, uint32_t max_seq_len, VeloxHipModelConfig* out) {
-    if (!which || !out) return VELOX_HIP_EINVAL;
-    VeloxHipModelConfig c;
-    std::memset(&c, 0, sizeof(c));
-    c.quant_mode = VELOX_QUANT_GGML_Q4_0;
-    if (!std::strcmp(which, "smollm_135m")) {  // examples/tinystories_smollm.vlx; src/runtime.rs:1175-1189
-        c = VeloxHipModelConfig{{0}, 49152, 576, 1536, 30, 9, 3, 64, 2048, 1e-5f, 10000.0f, 0, 1,
-                                VELOX_QUANT_GGML_Q4_0, 0, 0};
-    } else if (!std::strcmp(which, "llama3_8b")) {  // examples/llama3_8b.vlx
-        c = VeloxHipModelConfig{{0}, 128256, 4096, 14336, 32, 32, 8, 128, 8192, 1e-5f, 500000.0f, 0, 0,
-                                VELOX_QUANT_GGML_Q4_0, 0, 0};
-    } else if (!std::strcmp(which, "qwen2_5_7b")) {  // examples/qwen2_5_7b.vlx (tied head, QKV bias)
-        c = VeloxHipModelConfig{{0}, 152064, 3584, 18944, 28, 28, 4, 128, 4096, 1e-6f, 1000000.0f, 1, 1,
-                                VELOX_QUANT_GGML_Q4_0, 0, 0};
-    } else if (!std::strcmp(which, "qwen2_72b")) {  // examples/qwen2_72b.vlx
-        c = VeloxHipModelConfig{{0}, 152064, 8192, 29568, 80, 64, 8, 128, 8448, 1e-6f, 1000000.0f, 1, 0,
-                                VELOX_QUANT_GGML_Q4_0, 0, 0};
-    } else {
-        return VELOX_HIP_EINVAL;
-    }
-    std::snprintf(c.name, sizeof(c.name), "%s", which);
-    if (max_seq_len) c.max_seq_len = max_seq_len;
-    *out = c;
-    return VELOX_HIP_OK;
 }
 
 int velox_hip_q4_layout(uint32_t n, uint32_t k, uint32_t s_lanes, uint32_t paired, VeloxHipQ4Matrix* m,
@@ -355,11 +339,6 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
     // MFMA attention, measured: 1 split 702.6 tok/s, 2: 712.7, 4: 707.4, 8: 690.3.)
     uint32_t splits = c.attn_splits;
     if (!splits) {
-        const char* env = std::getenv("VELOX_HIP_ATTN_SPLITS");  // tuning override
-        if (env) splits = (uint32_t)std::strtoul(env, nullptr, 10);
-        if (splits > 64) splits = 64;
-    }
-    if (!splits) {
         if (c.max_seq_len <= 1024) {
             const uint32_t want = (c.max_seq_len + 255) / 256;
             splits = 2;
@@ -405,21 +384,15 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
         uint32_t xw = H > qd ? H : qd;
         if (F > xw) xw = F;
         M->xw = (xw + 7u) & ~7u;
-        const char* tiled = std::getenv("VELOX_HIP_BGEMM_TILED");  // A/B switch: the LDS-staged tiled GEMM
-        M->mgemm = M->head.has_m && !(tiled && tiled[0] == '1');
-        if (!M->mgemm && B > 32) {  // the tiled GEMM takes at most 32 rows
-            delete M;
-            return VELOX_HIP_EINVAL;
-        }
-        M->head_bwgs = M->mgemm ? vx_mgemm_grid(M->head.m_tiles) : vx_bgemm_grid(M->head.n_tiles, M->head.s);
+        M->head_bwgs = vx_mgemm_grid(M->head.m_tiles);
         const uint64_t S = M->batch;  // per-sequence state, prompt length and prompt
         M->a_bstate = take(S * sizeof(VeloxDecodeState));
         M->a_bplen = take(S * 4);
         M->a_bprompt = take(S * c.max_seq_len * 4);
         M->a_bh = take(B * H * 4);
         const uint64_t R16 = (B + 15u) / 16u * 16u;
-        M->x_ld = M->mgemm ? 32u : M->xw;
-        M->x_bs = M->mgemm ? (uint32_t)(32u * R16) : 32u;
+        M->x_ld = 32u;
+        M->x_bs = (uint32_t)(32u * R16);
         M->a_bxa = take(R16 * M->xw * 2);
         M->a_bxb = take(R16 * M->xw * 2);
         M->a_bqkv = take(B * (qd + 2 * kvd) * 4);
@@ -431,14 +404,9 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
         // K-split partials: [8][rows][max(hidden, q/k/v width)]
         M->a_bpart_r = take(8 * B * (H > qd + 2 * kvd ? H : qd + 2 * kvd) * 4);
         M->a_prows = take(B * sizeof(VeloxDecodeState));
-        if (M->mgemm) {
-            M->ksplit_qkv = vx_mgemm_ksplit(M->layers[0].qkv);
-            M->ksplit_o = vx_mgemm_ksplit(M->layers[0].o);
-            M->ksplit_down = vx_mgemm_ksplit(M->layers[0].down);
-        } else {
-            M->ksplit_o = vx_bgemm_ksplit(M->layers[0].o);
-            M->ksplit_down = vx_bgemm_ksplit(M->layers[0].down);
-        }
+        M->ksplit_qkv = vx_mgemm_ksplit(M->layers[0].qkv);
+        M->ksplit_o = vx_mgemm_ksplit(M->layers[0].o);
+        M->ksplit_down = vx_mgemm_ksplit(M->layers[0].down);
     }
     M->act_bytes = ac;
 
@@ -496,30 +464,19 @@ uint64_t velox_hip_model_hidden_offset(const VeloxHipModel* m) { return m ? m->a
 // ---------------------------------------------------------------------------------------------
 // Arena
 // ---------------------------------------------------------------------------------------------
-int velox_hip_arena_create(const VeloxHipModel* m, VeloxHipArena* out) {
-    if (!m || !out) return VELOX_HIP_EINVAL;
-    std::memset(out, 0, sizeof(*out));
-    uint8_t *w = nullptr, *kv = nullptr, *act = nullptr, *nrm = nullptr;
-    uint32_t* ring = nullptr;
-    hipError_t e = hipMalloc((void**)&w, m->code_bytes + m->scale_bytes);
-    if (e == hipSuccess) e = hipMalloc((void**)&nrm, m->norm_bytes);
-    if (e == hipSuccess) e = hipMalloc((void**)&kv, m->kv_bytes);
-    if (e == hipSuccess) e = hipMalloc((void**)&act, m->act_bytes);
-    // one ring of VELOX_HIP_RING_SIZE tokens per sequence (sequence 0 is the single-sequence ring)
-    const size_t ring_bytes = (size_t)VELOX_HIP_RING_SIZE * 4u * m->batch;
-    if (e == hipSuccess) e = hipHostMalloc((void**)&ring, ring_bytes, hipHostMallocMapped);
-    if (e == hipSuccess) e = hipMemset(w, 0, m->code_bytes + m->scale_bytes);  // tile padding = 0
-    if (e == hipSuccess) e = hipMemset(nrm, 0, m->norm_bytes);
-    if (e == hipSuccess) e = hipMemset(kv, 0, m->kv_bytes);
-    if (e == hipSuccess) e = hipMemset(act, 0, m->act_bytes);  // state, counters, prompt_len = 0
-    if (e != hipSuccess) {
-        hipFree(w); hipFree(nrm); hipFree(kv); hipFree(act);
-        if (ring) hipHostFree(ring);
-        return (int)e;
-    }
-    std::memset(ring, 0, ring_bytes);
-    // RoPE table: cos/sin of pos * theta^(-2j/D) evaluated exactly as src/runtime.rs:756-760
-    // (fp32 powf, product and sin/cos), once at startup instead of per token.
+namespace {
+
+// Clears every region of a planned arena (tile padding, KV pool, state, counters, prompt length)
+// and uploads the RoPE table: cos/sin of pos * theta^(-2j/D) evaluated exactly as
+// src/runtime.rs:756-760 (fp32 powf, product and sin/cos), once at startup instead of per token.
+hipError_t vx_arena_init(const VeloxHipModel* m, const VeloxHipArena* a) {
+    hipError_t e = hipMemset((void*)a->weight_arena, 0, m->code_bytes);
+    if (e == hipSuccess) e = hipMemset((void*)a->weight_scales, 0, m->scale_bytes);
+    if (e == hipSuccess) e = hipMemset((void*)a->norm_weight_arena, 0, m->norm_bytes);
+    if (e == hipSuccess) e = hipMemset(a->kv_cache_pool, 0, m->kv_bytes);
+    if (e == hipSuccess) e = hipMemset(a->activation_arena, 0, m->act_bytes);
+    if (e != hipSuccess) return e;
+    std::memset(a->host_pinned_ring, 0, (size_t)VELOX_HIP_RING_SIZE * 4u * m->batch);
     const VeloxHipModelConfig& c = m->cfg;
     const uint32_t half = c.head_dim / 2;
     std::vector<float> rope((size_t)c.max_seq_len * half * 2);
@@ -530,27 +487,86 @@ int velox_hip_arena_create(const VeloxHipModel* m, VeloxHipArena* out) {
             rope[((size_t)p * half + j) * 2] = cosf(angle);
             rope[((size_t)p * half + j) * 2 + 1] = sinf(angle);
         }
-    e = hipMemcpy(nrm + m->rope, rope.data(), rope.size() * 4, hipMemcpyHostToDevice);
-    if (e != hipSuccess) return (int)e;
-    out->weight_arena = w;
-    out->weight_scales = w + m->code_bytes;
-    out->norm_weight_arena = nrm;
-    out->kv_cache_pool = kv;
-    out->activation_arena = act;
-    out->host_pinned_ring = ring;
-    out->quant_mode = c.quant_mode;
-    out->tied_lm_head = c.tied_lm_head;
-    out->model = m;
+    return hipMemcpy((void*)(a->norm_weight_arena + m->rope), rope.data(), rope.size() * 4, hipMemcpyHostToDevice);
+}
+
+int vx_register(const VeloxHipModel* m, const VeloxHipArena* a, uint8_t* base, uint32_t* ring) {
+    std::lock_guard<std::mutex> lock(g_arena_mu);
+    if (vx_rec_locked(a->weight_arena)) return VELOX_HIP_EINVAL;  // already an arena
+    VxArenaRec r;
+    r.key = a->weight_arena;
+    r.model = m;
+    r.base = base;
+    r.ring = ring;
+    g_arenas.push_back(r);
     return VELOX_HIP_OK;
 }
 
+}  // namespace
+
+// One device allocation split into the reference's regions (weights, scales, norms + RoPE table,
+// KV pool, activations, each 256-byte aligned) plus the mapped host ring.
+int velox_hip_arena_create(const VeloxHipModel* m, VeloxHipArena* out) {
+    if (!m || !out) return VELOX_HIP_EINVAL;
+    std::memset(out, 0, sizeof(*out));
+    const uint64_t o_scale = vx_align(m->code_bytes), o_norm = o_scale + vx_align(m->scale_bytes);
+    const uint64_t o_kv = o_norm + vx_align(m->norm_bytes), o_act = o_kv + vx_align(m->kv_bytes);
+    const uint64_t total = o_act + vx_align(m->act_bytes);
+    uint8_t* base = nullptr;
+    uint32_t* ring = nullptr;
+    hipError_t e = hipMalloc((void**)&base, total);
+    // one ring of VELOX_HIP_RING_SIZE tokens per sequence (sequence 0 is the single-sequence ring)
+    const size_t ring_bytes = (size_t)VELOX_HIP_RING_SIZE * 4u * m->batch;
+    if (e == hipSuccess) e = hipHostMalloc((void**)&ring, ring_bytes, hipHostMallocMapped);
+    VeloxHipArena a;
+    std::memset(&a, 0, sizeof(a));
+    if (e == hipSuccess) {
+        a.weight_arena = base;
+        a.weight_scales = base + o_scale;
+        a.norm_weight_arena = base + o_norm;
+        a.kv_cache_pool = base + o_kv;
+        a.activation_arena = base + o_act;
+        a.host_pinned_ring = ring;
+        a.quant_mode = m->cfg.quant_mode;
+        a.tied_lm_head = m->cfg.tied_lm_head;
+        e = vx_arena_init(m, &a);
+    }
+    int rc = (int)e;
+    if (rc == VELOX_HIP_OK) rc = vx_register(m, &a, base, ring);
+    if (rc != VELOX_HIP_OK) {
+        hipFree(base);
+        if (ring) hipHostFree(ring);
+        return rc;
+    }
+    *out = a;
+    return VELOX_HIP_OK;
+}
+
+int velox_hip_arena_bind(const VeloxHipModel* m, VeloxHipArena* a) {
+    if (!m || !a || !a->weight_arena || !a->weight_scales || !a->norm_weight_arena || !a->kv_cache_pool ||
+        !a->activation_arena || !a->host_pinned_ring)
+        return VELOX_HIP_EINVAL;
+    if (a->quant_mode != m->cfg.quant_mode || a->tied_lm_head != m->cfg.tied_lm_head) return VELOX_HIP_EINVAL;
+    const hipError_t e = vx_arena_init(m, a);
+    if (e != hipSuccess) return (int)e;
+    return vx_register(m, a, nullptr, nullptr);
+}
+
+const VeloxHipModel* velox_hip_arena_model(const VeloxHipArena* a) { return vx_model(a); }
+
 int velox_hip_arena_destroy(VeloxHipArena* a) {
-    if (!a) return VELOX_HIP_EINVAL;
-    hipFree((void*)a->weight_arena);
-    hipFree((void*)a->norm_weight_arena);
-    hipFree(a->kv_cache_pool);
-    hipFree(a->activation_arena);
-    if (a->host_pinned_ring) hipHostFree(a->host_pinned_ring);
+    if (!a || !a->weight_arena) return VELOX_HIP_EINVAL;
+    VxArenaRec r;
+    {
+        std::lock_guard<std::mutex> lock(g_arena_mu);
+        VxArenaRec* p = vx_rec_locked(a->weight_arena);
+        if (!p) return VELOX_HIP_EINVAL;
+        r = *p;
+        g_arenas.erase(g_arenas.begin() + (p - g_arenas.data()));
+    }
+    // caller-owned buffers (velox_hip_arena_bind) stay with the caller
+    if (r.base) hipFree(r.base);
+    if (r.ring) hipHostFree(r.ring);
     std::memset(a, 0, sizeof(*a));
     return VELOX_HIP_OK;
 }
@@ -605,11 +621,11 @@ bool vx_vec_target(const VeloxHipModel* M, int kind, uint32_t layer, uint64_t* o
 }  // namespace
 
 int velox_hip_arena_matrix(const VeloxHipArena* a, int kind, uint32_t layer, VeloxHipQ4Matrix* out, uint32_t* row0) {
-    if (!a || !a->model || !out) return VELOX_HIP_EINVAL;
+    if (!a || !vx_model(a) || !out) return VELOX_HIP_EINVAL;
     const VxMatPlan* mp;
     uint32_t r0, pair, rows, cols;
-    if (kind == VELOX_T_HEAD && a->model->cfg.tied_lm_head) kind = VELOX_T_EMBED;
-    if (!vx_target(a->model, kind, layer, &mp, &r0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
+    if (kind == VELOX_T_HEAD && vx_model(a)->cfg.tied_lm_head) kind = VELOX_T_EMBED;
+    if (!vx_target(vx_model(a), kind, layer, &mp, &r0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
     out->codes = (void*)(a->weight_arena + mp->code_off);
     out->scales = (void*)(a->weight_scales + mp->scale_off);
     out->n = mp->n;
@@ -624,9 +640,9 @@ int velox_hip_arena_matrix(const VeloxHipArena* a, int kind, uint32_t layer, Vel
 }
 
 int velox_hip_arena_vector(const VeloxHipArena* a, int kind, uint32_t layer, const float** out, uint64_t* count) {
-    if (!a || !a->model || !out) return VELOX_HIP_EINVAL;
+    if (!a || !vx_model(a) || !out) return VELOX_HIP_EINVAL;
     uint64_t off, n;
-    if (!vx_vec_target(a->model, kind, layer, &off, &n)) return VELOX_HIP_EINVAL;
+    if (!vx_vec_target(vx_model(a), kind, layer, &off, &n)) return VELOX_HIP_EINVAL;
     *out = (const float*)(a->norm_weight_arena + off);
     if (count) *count = n;
     return VELOX_HIP_OK;
@@ -634,17 +650,17 @@ int velox_hip_arena_vector(const VeloxHipArena* a, int kind, uint32_t layer, con
 
 int velox_hip_load_q4_0(VeloxHipArena* a, int kind, uint32_t layer, const void* blocks, uint64_t nbytes,
                         hipStream_t stream) {
-    if (!a || !a->model || !blocks) return VELOX_HIP_EINVAL;
+    if (!a || !vx_model(a) || !blocks) return VELOX_HIP_EINVAL;
     const VxMatPlan* mp;
     uint32_t row0, pair, rows, cols;
-    if (!vx_target(a->model, kind, layer, &mp, &row0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
+    if (!vx_target(vx_model(a), kind, layer, &mp, &row0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
     if (nbytes != (uint64_t)rows * (cols / 32) * 18) return VELOX_HIP_ESHAPE;
     void* staging = nullptr;
     hipError_t e = hipMalloc(&staging, nbytes);
     if (e == hipSuccess) e = hipMemcpyAsync(staging, blocks, nbytes, hipMemcpyHostToDevice, stream);
     if (e == hipSuccess) e = vx_launch_repack(staging, rows, row0, pair, vx_view(a, *mp), stream);
     if (e == hipSuccess) e = vx_build_m(a, *mp, stream);
-    if (e == hipSuccess && kind == VELOX_T_EMBED && a->model->cfg.tied_lm_head) e = vx_build_m(a, a->model->head, stream);
+    if (e == hipSuccess && kind == VELOX_T_EMBED && vx_model(a)->cfg.tied_lm_head) e = vx_build_m(a, vx_model(a)->head, stream);
     if (e == hipSuccess) e = hipStreamSynchronize(stream);
     hipFree(staging);
     return (int)e;
@@ -652,9 +668,9 @@ int velox_hip_load_q4_0(VeloxHipArena* a, int kind, uint32_t layer, const void* 
 
 int velox_hip_load_f32(VeloxHipArena* a, int kind, uint32_t layer, const float* data, uint64_t count,
                        hipStream_t stream) {
-    if (!a || !a->model || !data) return VELOX_HIP_EINVAL;
+    if (!a || !vx_model(a) || !data) return VELOX_HIP_EINVAL;
     uint64_t off, n;
-    if (!vx_vec_target(a->model, kind, layer, &off, &n)) return VELOX_HIP_EINVAL;
+    if (!vx_vec_target(vx_model(a), kind, layer, &off, &n)) return VELOX_HIP_EINVAL;
     if (count != n) return VELOX_HIP_ESHAPE;
     hipError_t e = hipMemcpyAsync((void*)(a->norm_weight_arena + off), data, n * 4, hipMemcpyHostToDevice, stream);
     if (e == hipSuccess) e = hipStreamSynchronize(stream);
@@ -662,8 +678,8 @@ int velox_hip_load_f32(VeloxHipArena* a, int kind, uint32_t layer, const float* 
 }
 
 int velox_hip_synthesize_model(VeloxHipArena* a, uint64_t seed, float sigma, float norm_sigma, hipStream_t st) {
-    if (!a || !a->model) return VELOX_HIP_EINVAL;
-    const VeloxHipModel* M = a->model;
+    if (!a || !vx_model(a)) return VELOX_HIP_EINVAL;
+    const VeloxHipModel* M = vx_model(a);
     const VeloxHipModelConfig& c = M->cfg;
     const float coef = vx_normal_coef(sigma), ncoef = norm_sigma == 0.0f ? 0.0f : vx_normal_coef(norm_sigma);
     hipError_t e = hipSuccess;
@@ -703,11 +719,11 @@ int velox_hip_synthesize_model(VeloxHipArena* a, uint64_t seed, float sigma, flo
 }
 
 int velox_hip_fill_kv(VeloxHipArena* a, uint32_t layer, uint32_t n_pos, uint64_t seed, float sigma, hipStream_t st) {
-    if (!a || !a->model) return VELOX_HIP_EINVAL;
-    const VeloxHipModelConfig& c = a->model->cfg;
+    if (!a || !vx_model(a)) return VELOX_HIP_EINVAL;
+    const VeloxHipModelConfig& c = vx_model(a)->cfg;
     if (layer >= c.num_layers || n_pos > c.max_seq_len) return VELOX_HIP_EINVAL;
     uint16_t* base = vx_kv(a, layer, 0);
-    hipError_t e = vx_launch_fill_kv(base, c.num_kv_heads, a->model->s_cap, c.head_dim, n_pos,
+    hipError_t e = vx_launch_fill_kv(base, c.num_kv_heads, vx_model(a)->s_cap, c.head_dim, n_pos,
                                      vx_stream(seed, vx_tag(layer, VX_TAG_KV_K)),
                                      vx_stream(seed, vx_tag(layer, VX_TAG_KV_V)), vx_normal_coef(sigma), st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
@@ -718,24 +734,28 @@ int velox_hip_fill_kv(VeloxHipArena* a, uint32_t layer, uint32_t n_pos, uint64_t
 // Decode state / prompt
 // ---------------------------------------------------------------------------------------------
 int velox_hip_set_prompt(VeloxHipArena* a, const uint32_t* tokens, uint32_t n, hipStream_t st) {
-    if (!a || !a->model || (n && !tokens)) return VELOX_HIP_EINVAL;
-    if (n > a->model->cfg.max_seq_len) return VELOX_HIP_EINVAL;
+    if (!a || !vx_model(a) || (n && !tokens)) return VELOX_HIP_EINVAL;
+    if (n > vx_model(a)->cfg.max_seq_len) return VELOX_HIP_EINVAL;
     hipError_t e = hipSuccess;
-    if (n) e = hipMemcpyAsync(a->activation_arena + a->model->a_prompt, tokens, (size_t)n * 4, hipMemcpyHostToDevice, st);
+    if (n) e = hipMemcpyAsync(a->activation_arena + vx_model(a)->a_prompt, tokens, (size_t)n * 4, hipMemcpyHostToDevice, st);
     if (e == hipSuccess)
-        e = hipMemcpyAsync(a->activation_arena + a->model->a_plen, &n, 4, hipMemcpyHostToDevice, st);
+        e = hipMemcpyAsync(a->activation_arena + vx_model(a)->a_plen, &n, 4, hipMemcpyHostToDevice, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e == hipSuccess) {
+        std::lock_guard<std::mutex> lock(g_arena_mu);
+        if (VxArenaRec* r = vx_rec_locked(a->weight_arena)) r->staged_plen = n;
+    }
     return (int)e;
 }
 
 int velox_hip_set_state(VeloxHipArena* a, uint64_t step, uint32_t token, hipStream_t st) {
-    if (!a || !a->model) return VELOX_HIP_EINVAL;
-    return (int)vx_launch_set_state((VeloxDecodeState*)(a->activation_arena + a->model->a_state), step, token, st);
+    if (!a || !vx_model(a)) return VELOX_HIP_EINVAL;
+    return (int)vx_launch_set_state((VeloxDecodeState*)(a->activation_arena + vx_model(a)->a_state), step, token, st);
 }
 
 int velox_hip_get_state(const VeloxHipArena* a, VeloxDecodeState* out, hipStream_t st) {
-    if (!a || !a->model || !out) return VELOX_HIP_EINVAL;
-    hipError_t e = hipMemcpyAsync(out, a->activation_arena + a->model->a_state, sizeof(*out), hipMemcpyDeviceToHost, st);
+    if (!a || !vx_model(a) || !out) return VELOX_HIP_EINVAL;
+    hipError_t e = hipMemcpyAsync(out, a->activation_arena + vx_model(a)->a_state, sizeof(*out), hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     return (int)e;
 }
@@ -744,8 +764,8 @@ int velox_hip_get_state(const VeloxHipArena* a, VeloxDecodeState* out, hipStream
 // Batched decode of independent sequences (arena planned with max_batch > 1)
 // ---------------------------------------------------------------------------------------------
 int velox_hip_batch_set_prompt(VeloxHipArena* a, uint32_t seq, const uint32_t* tokens, uint32_t n, hipStream_t st) {
-    if (!a || !a->model || a->model->batch < 2 || seq >= a->model->batch || (n && !tokens)) return VELOX_HIP_EINVAL;
-    const VeloxHipModel* M = a->model;
+    if (!a || !vx_model(a) || vx_model(a)->batch < 2 || seq >= vx_model(a)->batch || (n && !tokens)) return VELOX_HIP_EINVAL;
+    const VeloxHipModel* M = vx_model(a);
     if (n > M->cfg.max_seq_len) return VELOX_HIP_EINVAL;
     hipError_t e = hipSuccess;
     if (n)
@@ -758,14 +778,14 @@ int velox_hip_batch_set_prompt(VeloxHipArena* a, uint32_t seq, const uint32_t* t
 }
 
 int velox_hip_batch_set_state(VeloxHipArena* a, uint32_t seq, uint64_t step, uint32_t token, hipStream_t st) {
-    if (!a || !a->model || a->model->batch < 2 || seq >= a->model->batch) return VELOX_HIP_EINVAL;
-    VeloxDecodeState* s = (VeloxDecodeState*)(a->activation_arena + a->model->a_bstate) + seq;
+    if (!a || !vx_model(a) || vx_model(a)->batch < 2 || seq >= vx_model(a)->batch) return VELOX_HIP_EINVAL;
+    VeloxDecodeState* s = (VeloxDecodeState*)(a->activation_arena + vx_model(a)->a_bstate) + seq;
     return (int)vx_launch_set_state(s, step, token, st);
 }
 
 int velox_hip_batch_get_state(const VeloxHipArena* a, uint32_t seq, VeloxDecodeState* out, hipStream_t st) {
-    if (!a || !a->model || a->model->batch < 2 || seq >= a->model->batch || !out) return VELOX_HIP_EINVAL;
-    hipError_t e = hipMemcpyAsync(out, a->activation_arena + a->model->a_bstate + (size_t)seq * sizeof(*out),
+    if (!a || !vx_model(a) || vx_model(a)->batch < 2 || seq >= vx_model(a)->batch || !out) return VELOX_HIP_EINVAL;
+    hipError_t e = hipMemcpyAsync(out, a->activation_arena + vx_model(a)->a_bstate + (size_t)seq * sizeof(*out),
                                   sizeof(*out), hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     return (int)e;
@@ -773,12 +793,12 @@ int velox_hip_batch_get_state(const VeloxHipArena* a, uint32_t seq, VeloxDecodeS
 
 int velox_hip_fill_kv_seq(VeloxHipArena* a, uint32_t layer, uint32_t seq, uint32_t n_pos, uint64_t seed, float sigma,
                           hipStream_t st) {
-    if (!a || !a->model || seq >= a->model->batch) return VELOX_HIP_EINVAL;
-    const VeloxHipModelConfig& c = a->model->cfg;
+    if (!a || !vx_model(a) || seq >= vx_model(a)->batch) return VELOX_HIP_EINVAL;
+    const VeloxHipModelConfig& c = vx_model(a)->cfg;
     if (layer >= c.num_layers || n_pos > c.max_seq_len) return VELOX_HIP_EINVAL;
     // sequence 0 is velox_hip_fill_kv's context; others draw from streams of a sequence-tagged seed
     const uint64_t sseed = seed + (uint64_t)seq * 0x9E3779B97F4A7C15ULL;
-    hipError_t e = vx_launch_fill_kv(vx_kv(a, layer, seq), c.num_kv_heads, a->model->s_cap, c.head_dim, n_pos,
+    hipError_t e = vx_launch_fill_kv(vx_kv(a, layer, seq), c.num_kv_heads, vx_model(a)->s_cap, c.head_dim, n_pos,
                                      vx_stream(sseed, vx_tag(layer, VX_TAG_KV_K)),
                                      vx_stream(sseed, vx_tag(layer, VX_TAG_KV_V)), vx_normal_coef(sigma), st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
@@ -815,7 +835,7 @@ namespace {
 // LM head.
 void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n, uint64_t mask, bool prefill,
                      uint32_t max_len, hipStream_t st) {
-    const VeloxHipModel* M = A->model;
+    const VeloxHipModel* M = vx_model(A);
     const VeloxHipModelConfig& c = M->cfg;
     uint8_t* act = A->activation_arena;
     const uint32_t H = c.hidden_dim, D = c.head_dim, qd = c.num_heads * D, kvd = c.num_kv_heads * D;
@@ -828,7 +848,7 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
     float* part_r = (float*)(act + M->a_bpart_r);
     const uint64_t pstride = (uint64_t)M->rows * H;
     auto gemm = [&](const VxMatPlan& p, const VxBGemmArgs& ga, int epi) {
-        return M->mgemm ? vx_launch_mgemm(vx_mview(A, p), ga, epi, st) : vx_launch_bgemm(vx_view(A, p), ga, epi, st);
+        return vx_launch_mgemm(vx_mview(A, p), ga, epi, st);
     };
 
     vx_record(vx_launch_bembed(vx_view(A, M->embed), rows, n, h, H, mask, st));
@@ -847,7 +867,6 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
     // Qwen2.5-7B ctx 2048: B = 32 best at 2, B = 8 at 8), at most the planned count the partial
     // buffers hold
     uint32_t bsplits = (256u + n * c.num_kv_heads / 2u) / (n * c.num_kv_heads);
-    if (const char* env = std::getenv("VELOX_HIP_BATCH_ATTN_SPLITS")) bsplits = (uint32_t)std::strtoul(env, nullptr, 10);
     bsplits = bsplits < 1u ? 1u : bsplits > M->splits ? M->splits : bsplits;
     at.splits = bsplits;
     at.scale = 1.0f / sqrtf((float)D);
@@ -874,7 +893,7 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
         g.bias = c.qkv_bias ? vecp(L.bias) : nullptr;
         g.y = qkv;
         g.ldy = qd + 2 * kvd;
-        if (M->mgemm && M->ksplit_qkv > 1) {  // K-split partials, then their sum + bias
+        if (M->ksplit_qkv > 1) {  // K-split partials, then their sum + bias
             g.ksplit = M->ksplit_qkv;
             g.part = part_r;
             g.pstride = (uint64_t)M->rows * g.ldy;
@@ -949,11 +968,11 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
 // One decode step of sequences 0 .. batch-1, each at its own state (step, token): the weights are
 // read once per step for all of them; then the argmax of every sequence.
 void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_t mask, hipStream_t st) {
-    if (!A || !A->model || A->model->batch < 2 || batch == 0 || batch > A->model->batch) {
+    if (!A || !vx_model(A) || vx_model(A)->batch < 2 || batch == 0 || batch > vx_model(A)->batch) {
         if (!g_last_error) g_last_error = VELOX_HIP_EINVAL;
         return;
     }
-    const VeloxHipModel* M = A->model;
+    const VeloxHipModel* M = vx_model(A);
     uint8_t* act = A->activation_arena;
     VeloxDecodeState* states = (VeloxDecodeState*)(act + M->a_bstate);
     vx_rows_forward(A, states, batch, mask, false, 0u, st);
@@ -964,14 +983,23 @@ void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_
 
 // Prompt positions [pos0, pos0 + n_tokens) of sequence 0 in chunks of up to prefill_chunk rows.
 int velox_hip_prefill_batch(VeloxHipArena* A, uint64_t pos0, uint32_t n_tokens, uint64_t mask, hipStream_t st) {
-    if (!A || !A->model) return VELOX_HIP_EINVAL;
-    const VeloxHipModel* M = A->model;
+    const VeloxHipModel* M = vx_model(A);
+    if (!M) return VELOX_HIP_EINVAL;
     const uint32_t chunk = M->cfg.prefill_chunk;
-    if (chunk < 2 || n_tokens == 0 || pos0 + n_tokens > M->cfg.max_seq_len) return VELOX_HIP_EINVAL;
+    uint32_t plen = 0;
+    {
+        std::lock_guard<std::mutex> lock(g_arena_mu);
+        if (const VxArenaRec* r = vx_rec_locked(A->weight_arena)) plen = r->staged_plen;
+    }
+    // every row reads its token from the staged prompt: positions must lie inside it
+    if (chunk < 2 || n_tokens == 0 || pos0 + n_tokens > M->cfg.max_seq_len || pos0 + n_tokens > plen)
+        return VELOX_HIP_EINVAL;
     uint8_t* act = A->activation_arena;
     VeloxDecodeState* rows = (VeloxDecodeState*)(act + M->a_prows);
     const uint32_t* prompt = (const uint32_t*)(act + M->a_prompt);
+    // this call's first launch error, whatever an earlier unread one was (restored afterwards)
     const int before = g_last_error;
+    g_last_error = 0;
     for (uint32_t done = 0; done < n_tokens;) {
         const uint32_t n = n_tokens - done < chunk ? n_tokens - done : chunk;
         vx_record(vx_launch_prefill_rows(rows, n, pos0 + done, prompt, mask, st));
@@ -982,12 +1010,9 @@ int velox_hip_prefill_batch(VeloxHipArena* A, uint64_t pos0, uint32_t n_tokens, 
                                              (const uint32_t*)(act + M->a_plen), mask, st));
         done += n;
     }
-    if (!before && g_last_error) {
-        const int e = g_last_error;
-        g_last_error = 0;
-        return e;
-    }
-    return VELOX_HIP_OK;
+    const int mine = g_last_error;
+    g_last_error = before;
+    return mine;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -995,8 +1020,8 @@ int velox_hip_prefill_batch(VeloxHipArena* A, uint64_t pos0, uint32_t n_tokens, 
 // down+res] -> norm + LM head + argmax (+ ring + state advance). 2 + 5L launches.
 // ---------------------------------------------------------------------------------------------
 void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st) {
-    if (!A || !A->model) { if (!g_last_error) g_last_error = VELOX_HIP_EINVAL; return; }
-    const VeloxHipModel* M = A->model;
+    if (!A || !vx_model(A)) { if (!g_last_error) g_last_error = VELOX_HIP_EINVAL; return; }
+    const VeloxHipModel* M = vx_model(A);
     const VeloxHipModelConfig& c = M->cfg;
     uint8_t* act = A->activation_arena;
     const float* nrm = (const float*)A->norm_weight_arena;
@@ -1084,8 +1109,8 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
 }
 
 void velox_hip_decode(VeloxHipArena* A, uint32_t token_in, size_t step, uint64_t mask, hipStream_t st) {
-    if (!A || !A->model) { if (!g_last_error) g_last_error = VELOX_HIP_EINVAL; return; }
-    vx_record(vx_launch_set_state((VeloxDecodeState*)(A->activation_arena + A->model->a_state), step, token_in, st));
+    if (!A || !vx_model(A)) { if (!g_last_error) g_last_error = VELOX_HIP_EINVAL; return; }
+    vx_record(vx_launch_set_state((VeloxDecodeState*)(A->activation_arena + vx_model(A)->a_state), step, token_in, st));
     velox_hip_decode_graph_step(A, mask, st);
 }
 
@@ -1100,7 +1125,8 @@ void velox_hip_prefill(VeloxHipArena* A, uint32_t token_in, size_t step, uint64_
 
 #define VX_MODEL_ENTRY(NAME, KEY)                                                                   \
     static bool vx_is_##NAME(const VeloxHipArena* a) {                                              \
-        if (a && a->model && !std::strcmp(a->model->cfg.name, KEY)) return true;                    \
+        const VeloxHipModel* m_ = vx_model(a);                                                      \
+        if (m_ && (!std::strcmp(m_->cfg.name, KEY) || !std::strcmp(m_->cfg.name, #NAME))) return true; \
         if (!g_last_error) g_last_error = VELOX_HIP_EINVAL;                                         \
         return false;                                                                               \
     }                                                                                               \
@@ -1127,6 +1153,18 @@ void velox_Llama3_8B_prefill_graph_step_hip(VeloxHipArena* ctx, uint64_t m, hipS
 }
 void velox_Llama3_8B_prefill_hip(VeloxHipArena* ctx, uint32_t t, size_t st, uint64_t m, hipStream_t s) {
     if (vx_is_Llama3_8B(ctx)) velox_hip_prefill(ctx, t, st, m, s);
+}
+void velox_Qwen2_5_7B_prefill_graph_step_hip(VeloxHipArena* ctx, uint64_t m, hipStream_t s) {
+    if (vx_is_Qwen2_5_7B(ctx)) velox_hip_prefill_graph_step(ctx, m, s);
+}
+void velox_Qwen2_5_7B_prefill_hip(VeloxHipArena* ctx, uint32_t t, size_t st, uint64_t m, hipStream_t s) {
+    if (vx_is_Qwen2_5_7B(ctx)) velox_hip_prefill(ctx, t, st, m, s);
+}
+void velox_Qwen2_72B_prefill_graph_step_hip(VeloxHipArena* ctx, uint64_t m, hipStream_t s) {
+    if (vx_is_Qwen2_72B(ctx)) velox_hip_prefill_graph_step(ctx, m, s);
+}
+void velox_Qwen2_72B_prefill_hip(VeloxHipArena* ctx, uint32_t t, size_t st, uint64_t m, hipStream_t s) {
+    if (vx_is_Qwen2_72B(ctx)) velox_hip_prefill(ctx, t, st, m, s);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1178,9 +1216,22 @@ int velox_hip_gemv_q4_0(const VeloxHipQ4Matrix* m, const float* d_x, const float
 int velox_hip_gemm_q4_0_batch(const VeloxHipQ4Matrix* m, const uint16_t* d_x16, uint32_t batch, uint32_t ldx,
                               const float* d_bias, float* d_y, uint32_t ldy, uint16_t* d_out16, uint32_t ldo,
                               int mode, hipStream_t st) {
-    if (!m || !d_x16 || batch == 0 || batch > 32 || ldx < m->k || mode < 0 || mode > 2) return VELOX_HIP_EINVAL;
+    if (!m || !d_x16 || batch == 0 || batch > 32 || ldx < m->k || (ldx & 7u) || mode < 0 || mode > 2)
+        return VELOX_HIP_EINVAL;
     if ((mode == VELOX_GEMV_SWIGLU) != (m->paired != 0)) return VELOX_HIP_EINVAL;
-    if (mode == VELOX_GEMV_SWIGLU ? (!d_out16 || ldo < m->n) : (!d_y || ldy < m->n)) return VELOX_HIP_EINVAL;
+    if (mode == VELOX_GEMV_SWIGLU ? (!d_out16 || ldo < m->n) : (!d_y || ldy < m->n))
+        return VELOX_HIP_EINVAL;
+    // the batched steps' GEMM over a per-call MFMA-layout copy of the tiled matrix (built on the
+    // device, released after a stream synchronization)
+    VxMMat mm;
+    vx_mmat_shape(m->n, m->k, m->paired, mm);
+    const uint64_t cb = vx_mmat_code_bytes(mm), sb = vx_mmat_scale_bytes(mm);
+    uint8_t* buf = nullptr;
+    hipError_t e = hipMalloc((void**)&buf, cb + sb);
+    if (e != hipSuccess) return (int)e;
+    mm.codes = (const uint4*)buf;
+    mm.scales = (const uint2*)(buf + cb);
+    e = vx_launch_mlayout(vx_view_public(m), mm, st);
     VxBGemmArgs g;
     std::memset(&g, 0, sizeof(g));
     g.batch = batch;
@@ -1194,8 +1245,13 @@ int velox_hip_gemm_q4_0_batch(const VeloxHipQ4Matrix* m, const uint16_t* d_x16, 
     g.ldo = ldo;
     g.obs = 32;
     g.active_mask = 1;
+    g.ksplit = 1;
     const int epi = mode == VELOX_GEMV_STORE ? VX_EPI_STORE : mode == VELOX_GEMV_RESIDUAL ? VX_EPI_RESID : VX_EPI_SWIGLU;
-    return (int)vx_launch_bgemm(vx_view_public(m), g, epi, st);
+    if (e == hipSuccess) e = vx_launch_mgemm(mm, g, epi, st);
+    const hipError_t es = hipStreamSynchronize(st);
+    if (e == hipSuccess) e = es;
+    hipFree(buf);
+    return (int)e;
 }
 
 namespace {
@@ -1351,7 +1407,8 @@ int velox_hip_attention_decode(const float* d_qkv, uint16_t* d_kv_layer, uint32_
 // graph capture (:474-481), prefill (:493-512), timed decode replays (:535-563).
 // ---------------------------------------------------------------------------------------------
 int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_tokens, VeloxHipRunReport* rep) {
-    if (!opt || !rep || (!opt->model && !opt->weights_path) || opt->prompt_len == 0) return VELOX_HIP_EINVAL;
+    if (!opt || !rep || (!opt->model && !opt->weights_path && !opt->model_file) || opt->prompt_len == 0)
+        return VELOX_HIP_EINVAL;
     if (opt->context_len && opt->prompt_len != 1) return VELOX_HIP_EINVAL;  // context + one seed token
     std::memset(rep, 0, sizeof(*rep));
     const uint32_t base = opt->context_len;  // first decoded position
@@ -1363,6 +1420,9 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
         rc = velox_hip_gguf_open(opt->weights_path, &gguf);
         if (!rc) rc = velox_hip_gguf_config(gguf, opt->max_seq_len ? opt->max_seq_len : total + 1, &cfg);
         if (rc) { velox_hip_gguf_close(gguf); return rc; }
+    } else if (opt->model_file) {
+        rc = velox_hip_vlx_load(opt->model_file, opt->max_seq_len ? opt->max_seq_len : total + 1, &cfg, nullptr);
+        if (rc) return rc;
     } else {
         rc = velox_hip_builtin_config(opt->model, opt->max_seq_len ? opt->max_seq_len : total + 1, &cfg);
         if (rc) return rc;
@@ -1437,15 +1497,43 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
         }
         rc = velox_hip_last_error();
     }
+    // ring[pos & 1023] holds the argmax after position pos (velox_cuda_runner.cu:541-546). The host
+    // copies entries out before the device can overwrite them: whenever 1024 positions have run
+    // since the last copy (a stream synchronization per 1024 steps), and at the end.
+    uint32_t drained = base, next_pos = base, n_out = 0;
+    bool first_seen = false;
+    auto drain = [&](uint32_t upto) {
+        if (upto <= drained) return;
+        const int e = (int)hipStreamSynchronize(st);
+        if (!rc) rc = e;
+        for (uint32_t p = drained; p < upto; ++p) {
+            const uint32_t t = A.host_pinned_ring[p & (VELOX_HIP_RING_SIZE - 1)];
+            if (p == base + opt->prompt_len - 1) { rep->first_token = t; first_seen = true; }
+            if (tokens && n_out < max_tokens) tokens[n_out++] = t;
+        }
+        drained = upto;
+    };
     auto one_step = [&]() {
+        if (next_pos - drained >= VELOX_HIP_RING_SIZE) drain(next_pos);
         if (exec) vx_record(hipGraphLaunch(exec, st));
         else launch_step();
+        ++next_pos;
     };
     if (!rc) {
         hipEventRecord(e0, st);
-        if (batched_prefill) rc = velox_hip_prefill_batch(&A, base, opt->prompt_len, 1ULL, st);
-        else
+        if (batched_prefill) {
+            // pieces of at most one ring of positions, drained in between
+            for (uint32_t done = 0; done < opt->prompt_len && !rc;) {
+                const uint32_t n = opt->prompt_len - done < VELOX_HIP_RING_SIZE ? opt->prompt_len - done
+                                                                                : VELOX_HIP_RING_SIZE;
+                drain(next_pos);
+                rc = velox_hip_prefill_batch(&A, next_pos, n, 1ULL, st);
+                next_pos += n;
+                done += n;
+            }
+        } else {
             for (uint32_t p = 0; p < opt->prompt_len; ++p) one_step();
+        }
         hipEventRecord(e1, st);
         for (uint32_t w = 0; w < opt->warmup && !rc; ++w) one_step();
         const int e = (int)hipStreamSynchronize(st);
@@ -1462,6 +1550,7 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
         if (!rc) rc = velox_hip_last_error();
     }
     if (!rc) {
+        drain(next_pos);
         float ms_p = 0.f, ms_d = 0.f;
         hipEventElapsedTime(&ms_p, e0, e1);
         hipEventElapsedTime(&ms_d, e2, e3);
@@ -1475,14 +1564,9 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
                                     : velox_hip_model_step_bytes(M, first + s));
         rep->bytes_per_step = opt->steps ? bytes / opt->steps : 0.0;
         rep->hbm_gbps = rep->bytes_per_step * rep->tok_per_s / B / 1e9;
-        // ring[pos & 1023] holds the argmax after position pos (velox_cuda_runner.cu:541-546)
-        uint32_t n = 0;
-        uint32_t lo = total > VELOX_HIP_RING_SIZE ? total - VELOX_HIP_RING_SIZE : 0;
-        if (lo < base) lo = base;
-        for (uint32_t p = lo; p < total && n < max_tokens; ++p)
-            if (tokens) tokens[n++] = A.host_pinned_ring[p & (VELOX_HIP_RING_SIZE - 1)];
-        rep->n_tokens = n;
-        rep->first_token = A.host_pinned_ring[(base + opt->prompt_len - 1) & (VELOX_HIP_RING_SIZE - 1)];
+        rep->n_tokens = n_out;
+        rep->first_position = base;
+        if (!first_seen) rep->first_token = 0;
     }
     if (!rc && opt->kernel_passes) {
         // The dominant kernel alone: the fused RMSNorm + gate/up + SwiGLU GEMV of every layer in
@@ -1509,8 +1593,7 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
             for (uint32_t l = 0; l < cfg.num_layers; ++l) {
                 if (B > 1) {
                     const VxMatPlan& gu = M->layers[l].gate_up;
-                    vx_record(M->mgemm ? vx_launch_mgemm(vx_mview(&A, gu), bg, VX_EPI_SWIGLU, st)
-                                       : vx_launch_bgemm(vx_view(&A, gu), bg, VX_EPI_SWIGLU, st));
+                    vx_record(vx_launch_mgemm(vx_mview(&A, gu), bg, VX_EPI_SWIGLU, st));
                 } else {
                     g.gain = (const float*)(A.norm_weight_arena + M->layers[l].mlp_norm);
                     vx_record(vx_launch_gemv(vx_view(&A, M->layers[l].gate_up), g, VX_EPI_SWIGLU, M->max_wgs, st));

@@ -172,8 +172,8 @@ __device__ __forceinline__ float vx_normal_value(uint64_t stream, uint64_t idx, 
 // first, then the first kU weight items, so staging x in LDS overlaps the weight fetch. Every
 // load outside the last 2*kU items is issued unconditionally: vector memory completes in issue
 // order, and with no load under a branch the compiler's s_waitcnt for item u waits for that item
-// only, keeping kU items in flight instead of draining the queue once per iteration. Tiles go to
-// waves round-robin over the grid (a.contig == 0) or in contiguous runs (a.contig == 1).
+// only, keeping kU items in flight instead of draining the queue once per iteration. Each workgroup
+// owns a contiguous block of tiles, dealt to its waves round-robin.
 // No workgroup waits on another: the LM head's argmax leaves one candidate per workgroup for
 // vx_argmax_finalize_kernel (a release fence per workgroup costs a full L2 write-back on gfx950).
 constexpr int kGemvWaves = 8, kGemvU = 4;
@@ -190,26 +190,12 @@ __global__ __launch_bounds__(64 * kGemvWaves) void vx_gemv_q4_kernel(VxGemvArgs 
     // the wave index is uniform: readfirstlane lets every per-wave quantity live in SGPRs
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane / S, s = lane % S;
-    const uint32_t waves_total = gridDim.x * W, gw = blockIdx.x * W + wave;
-    uint32_t first, step, my_tiles;
-    if (a.contig == 2u) {
-        // workgroup blocks: workgroup b owns tiles [b n / grid, (b + 1) n / grid), dealt to its W
-        // waves round-robin, so every workgroup (every CU) streams the same number of tiles
-        const uint32_t b0 = (uint32_t)(((uint64_t)blockIdx.x * a.n_tiles) / gridDim.x);
-        const uint32_t b1 = (uint32_t)(((uint64_t)(blockIdx.x + 1u) * a.n_tiles) / gridDim.x);
-        first = b0 + (uint32_t)wave;
-        step = (uint32_t)W;
-        my_tiles = first < b1 ? (b1 - 1u - first) / (uint32_t)W + 1u : 0u;
-    } else if (a.contig) {
-        const uint32_t per = (a.n_tiles + waves_total - 1u) / waves_total;
-        first = gw * per;
-        step = 1u;
-        my_tiles = first < a.n_tiles ? min(per, a.n_tiles - first) : 0u;
-    } else {
-        first = gw;
-        step = waves_total;
-        my_tiles = first < a.n_tiles ? (a.n_tiles - 1u - first) / waves_total + 1u : 0u;
-    }
+    // workgroup blocks: workgroup b owns tiles [b n / grid, (b + 1) n / grid), dealt to its W waves
+    // round-robin, so every workgroup (every CU) streams the same number of tiles
+    const uint32_t b0 = (uint32_t)(((uint64_t)blockIdx.x * a.n_tiles) / gridDim.x);
+    const uint32_t b1 = (uint32_t)(((uint64_t)(blockIdx.x + 1u) * a.n_tiles) / gridDim.x);
+    const uint32_t first = b0 + (uint32_t)wave, step = (uint32_t)W;
+    const uint32_t my_tiles = first < b1 ? (b1 - 1u - first) / (uint32_t)W + 1u : 0u;
     const uint32_t total = my_tiles * n_iter;
 
     auto row_of = [&](uint32_t t) -> uint32_t {
@@ -994,36 +980,16 @@ __global__ __launch_bounds__(kWG) void vx_argmax_kernel(const float* x, uint32_t
 // Launch helpers
 // =============================================================================================
 namespace {
-int vx_env_int(const char* name, int dflt) {
-    const char* e = getenv(name);
-    return e ? (int)strtol(e, nullptr, 10) : dflt;
-}
-
-// GEMV grid for n_tiles wave tiles. The tile schedule (VELOX_HIP_GEMV_SCHED, for tuning):
-//   3 (default) workgroup blocks: min(ceil(n_tiles / W), 512, max_wgs) workgroups, each owning an
-//     equal contiguous block of tiles dealt to its waves round-robin, so every CU streams the
-//     same share however the workgroups are placed;
-//   2 the same over <= 256 workgroups;
-//   1 tiles round-robin over all waves, min(ceil(n_tiles / W), max_wgs) workgroups;
-//   0 round-robin on the fewest waves that keep the largest per-wave tile count.
-// Llama-3-8B decode: 714 / 708 / 708 / 700 tok/s for 3 / 2 / 1 / 0.
+// GEMV grid for n_tiles wave tiles: min(ceil(n_tiles / W), 512, max_wgs) workgroups, each owning an
+// equal contiguous block of tiles dealt to its waves round-robin, so every CU streams the same share
+// however the workgroups are placed. (Llama-3-8B decode, measured against the alternatives: 714
+// tok/s; the same blocks over <= 256 workgroups 708, tiles round-robin over all waves 708, over the
+// fewest waves with the largest per-wave tile count 700.)
 uint32_t vx_gemv_wgs(uint32_t n_tiles, uint32_t max_wgs) {
     if (n_tiles == 0 || max_wgs == 0) return 1u;
-    const int sched = vx_env_int("VELOX_HIP_GEMV_SCHED", 3);
-    if (sched == 1) {  // round-robin, plain cap
-        const uint32_t w = (n_tiles + kGemvWaves - 1u) / kGemvWaves;
-        return w > max_wgs ? max_wgs : (w ? w : 1u);
-    }
-    if (sched == 2 || sched == 3) {  // workgroup blocks over <= 256 (2) or <= 512 (3) workgroups
-        const uint32_t cap = min(sched == 2 ? 256u : 512u, max_wgs);
-        const uint32_t w = (n_tiles + kGemvWaves - 1u) / kGemvWaves;
-        return w > cap ? cap : (w ? w : 1u);
-    }
-    const uint32_t max_waves = max_wgs * (uint32_t)kGemvWaves;
-    const uint32_t per_wave = (n_tiles + max_waves - 1u) / max_waves;
-    const uint32_t waves = (n_tiles + per_wave - 1u) / per_wave;
-    const uint32_t wgs = (waves + kGemvWaves - 1u) / kGemvWaves;
-    return wgs < 1u ? 1u : (wgs > max_wgs ? max_wgs : wgs);
+    const uint32_t cap = min(512u, max_wgs);
+    const uint32_t w = (n_tiles + kGemvWaves - 1u) / kGemvWaves;
+    return w > cap ? cap : (w ? w : 1u);
 }
 
 template <int S, int EPI, bool NORM, int GX, int SPL>
@@ -1140,10 +1106,7 @@ hipError_t vx_attn_launch_t(const VxAttnArgs& a, hipStream_t st) {
 
 // Upper bound on GEMV workgroups (waves loop over the remaining tiles); VELOX_HIP_GEMV_MAX_WGS
 // overrides it for tuning sweeps.
-uint32_t vx_gemv_max_wgs_default() {
-    const int v = vx_env_int("VELOX_HIP_GEMV_MAX_WGS", 0);
-    return (v > 0 && v <= 65536) ? (uint32_t)v : 512u;
-}
+uint32_t vx_gemv_max_wgs_default() { return 512u; }
 
 hipError_t vx_launch_gemv(const VxMat& m, const VxGemvArgs& a0, int epi, uint32_t max_wgs, hipStream_t st) {
     VxGemvArgs a = a0;
@@ -1153,11 +1116,6 @@ hipError_t vx_launch_gemv(const VxMat& m, const VxGemvArgs& a0, int epi, uint32_
     a.k = m.k;
     a.n_tiles = m.n_tiles;
     a.n_iter = m.n_iter;
-    a.contig = (uint32_t)vx_env_int("VELOX_HIP_GEMV_CONTIG", 0);
-    {
-        const int sched = vx_env_int("VELOX_HIP_GEMV_SCHED", 3);
-        if (sched == 2 || sched == 3) a.contig = 2u;
-    }
     if (m.k == 0 || (m.k & 31u) != 0) return hipErrorInvalidValue;
     if ((epi == VX_EPI_SWIGLU) != (m.paired != 0)) return hipErrorInvalidValue;
     switch (epi) {

@@ -245,9 +245,6 @@ int velox_hip_mla_create(const VeloxHipMlaConfig* cfg, VeloxHipMla** out) {
     if (m->ks_o > m->nh * m->dv / 64) m->ks_o = m->nh * m->dv / 64;
     uint32_t splits = c.attn_splits;
     if (!splits) {
-        if (const char* env = std::getenv("VELOX_HIP_MLA_SPLITS")) splits = (uint32_t)std::strtoul(env, nullptr, 10);
-    }
-    if (!splits) {
         const uint32_t hg = m->lr == 512 ? m->nh / 64 : m->nh / 16;
         splits = (256 + m->B * hg - 1) / (m->B * hg);
         const uint32_t by_len = (c.max_seq_len + 63) / 64;  // at least two 32-position chunks per split

@@ -3,10 +3,14 @@
 // (src/cli.rs:640-770, "[Step N] Token: id" parsing at :706-733) and the benchmark regexes
 // (benchmarks/run_sota_roofline_benchmarks.py:278-292) keep working.
 //
-//   velox_hip_runner [--model llama3_8b] [--weights synthetic|FILE.gguf] [--tokens 1,2,3 | --prompt-len N]
+//   velox_hip_runner [--model llama3_8b | --model-file MODEL.vlx] [--weights synthetic|FILE.gguf]
+//                    [--tokens 1,2,3 | --prompt-len N]
 //                    [--context-len N] [--steps N] [--warmup N] [--seed S] [--layers L]
 //                    [--prefill-chunk N] [--no-cuda-graph] [--verbose]
 //
+// --model-file MODEL.vlx reads the model from its .vlx source (the `model` header, weight
+// declarations and `target hardware` budget; what `velox build MODEL.vlx` compiles into the
+// reference's emitted runner) instead of a builtin configuration.
 // --prefill-chunk N (2..64) prefills the prompt N positions per batched step (one weight pass per
 // chunk) instead of the reference's one decode step per prompt token; TTFT reports either.
 //
@@ -22,7 +26,7 @@
 #include "velox_hip.h"
 
 int main(int argc, char** argv) {
-    std::string model = "llama3_8b", weights;
+    std::string model = "llama3_8b", weights, model_file;
     std::vector<uint32_t> tokens;
     uint32_t prompt_len = 128, steps = 32, warmup = 0, layers = 0, context_len = 0, prefill_chunk = 0;
     uint64_t seed = 1234;
@@ -34,6 +38,7 @@ int main(int argc, char** argv) {
             return argv[++i];
         };
         if (!std::strcmp(a, "--model")) model = next();
+        else if (!std::strcmp(a, "--model-file")) model_file = next();
         else if (!std::strcmp(a, "--tokens")) {
             std::string s = next();
             size_t p = 0;
@@ -98,6 +103,7 @@ int main(int argc, char** argv) {
     VeloxHipRunOptions opt;
     std::memset(&opt, 0, sizeof(opt));
     opt.model = model.c_str();
+    opt.model_file = model_file.empty() ? nullptr : model_file.c_str();
     opt.prompt_len = prompt_len;
     opt.warmup = warmup;
     // the first generated token comes from the prefill; steps-1 decode steps are timed
@@ -127,7 +133,8 @@ int main(int argc, char** argv) {
     std::printf("VELOX MI355X HIP RUNTIME EXECUTION REPORT\n");
     std::printf("================================================================================\n");
     if (weights.empty()) {
-        std::printf("Model                  : %s (synthetic Q4_0, seed %llu)\n", model.c_str(), (unsigned long long)seed);
+        std::printf("Model                  : %s (synthetic Q4_0, seed %llu)\n",
+                    model_file.empty() ? model.c_str() : model_file.c_str(), (unsigned long long)seed);
         std::printf("Weight Synthesis       : %.2f ms\n", rep.load_ms);
     } else {
         std::printf("Model                  : %s (GGUF Q4_0)\n", weights.c_str());

@@ -29,12 +29,22 @@ def gguf_config(path: str, max_seq_len: int = 0) -> L.ModelConfig:
     return cfg
 
 
+def vlx_config(path: str, max_seq_len: int = 0) -> tuple[L.ModelConfig, L.VlxTarget]:
+    """The model configuration and target a .vlx model source declares (velox_hip_vlx_load)."""
+    lib = L.load()
+    cfg, tgt = L.ModelConfig(), L.VlxTarget()
+    L.check(lib.velox_hip_vlx_load(path.encode(), max_seq_len, C.byref(cfg), C.byref(tgt)), f"vlx_load {path}")
+    return cfg, tgt
+
+
 def make_config(model, max_seq_len: int = 0, num_layers: int = 0, attn_splits: int = 0,
                 max_batch: int = 0, prefill_chunk: int = 0) -> L.ModelConfig:
-    """A builtin config by name, a GGUF file (path ending in .gguf), or a dict of ModelConfig
-    fields (custom shapes for tests)."""
+    """A builtin config by name, a GGUF file (path ending in .gguf), a .vlx model source (path ending
+    in .vlx, read by velox_hip_vlx_load), or a dict of ModelConfig fields (custom shapes for tests)."""
     if isinstance(model, str) and model.endswith(".gguf"):
         cfg = gguf_config(model, max_seq_len)
+    elif isinstance(model, str) and model.endswith(".vlx"):
+        cfg = vlx_config(model, max_seq_len)[0]
     elif isinstance(model, str):
         cfg = L.builtin_config(model, max_seq_len)
     else:
@@ -243,12 +253,13 @@ def run(model: str = "llama3_8b", prompt_len: int = 128, warmup: int = 5, steps:
         sigma: float = 0.02, norm_sigma: float = 0.0, use_graph: bool = True, num_layers: int = 0,
         max_seq_len: int = 0, max_tokens: int = 1024, kernel_passes: int = 0,
         prompt: list[int] | None = None, context_len: int = 0, batch: int = 1,
-        prefill_chunk: int = 0) -> tuple[dict, list[int]]:
+        prefill_chunk: int = 0, model_file: str | None = None) -> tuple[dict, list[int]]:
     """The C++ runner flow (velox_hip_run): synthesize, capture, prefill, timed decode. `prompt`
     replaces the seeded random prompt of `prompt_len` ids; `context_len` > 0 starts from a seeded
     context of that many positions already in the KV cache (then prompt_len must be 1). Returned
     tokens are ring entries, ring[p] = argmax after position p, for the last positions run.
-    `prefill_chunk` > 1 prefills the prompt as batched chunks of that many positions."""
+    `prefill_chunk` > 1 prefills the prompt as batched chunks of that many positions. `model_file`
+    reads the model from a .vlx source instead of the builtin `model`."""
     lib = L.load()
     ptoks = None
     if prompt is not None:
@@ -256,7 +267,7 @@ def run(model: str = "llama3_8b", prompt_len: int = 128, warmup: int = 5, steps:
         ptoks = (C.c_uint32 * prompt_len)(*prompt)
     opt = L.RunOptions(model.encode(), max_seq_len, prompt_len, warmup, steps, seed, sigma, norm_sigma,
                        int(use_graph), num_layers, kernel_passes, 0, ptoks, context_len, batch, None,
-                       prefill_chunk)
+                       prefill_chunk, model_file.encode() if model_file else None)
     rep = L.RunReport()
     toks = (C.c_uint32 * max_tokens)()
     rc = lib.velox_hip_run(C.byref(opt), toks, max_tokens, C.byref(rep))
