@@ -262,7 +262,8 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 x f16 -> f32 (bf16 KV)",
+        "dtype": ("q4_0 x 22-bit block-scaled integer activations -> exact int32 block dots, f32 sums (bf16 KV)"
+                  if args.batch == 1 else "q4_0 x f16 -> f32 (bf16 KV)"),
         "data": "synthetic",
         "config": {
             "workload": workload,
@@ -280,7 +281,7 @@ def main() -> int:
         "roofline": {
             "kernel": (f"vx_gemv_q4_kernel<S,SWIGLU> (RMSNorm + gate/up Q4_0 GEMV + SwiGLU), "
                        f"{cfg.intermediate_dim}x2 x {cfg.hidden_dim}") if args.batch == 1 else
-                      (f"vx_bgemm_q4_kernel<S,SWIGLU,MT> (gate/up Q4_0 MFMA GEMM + SwiGLU, {args.batch} sequences), "
+                      (f"vx_mgemm_kernel<SWIGLU,MT,NT> (gate/up Q4_0 MFMA GEMM + SwiGLU, {args.batch} sequences), "
                        f"{cfg.intermediate_dim}x2 x {cfg.hidden_dim}"),
             "bound": "hbm",
             "achieved": round(kernel_gbps, 1),

@@ -118,6 +118,7 @@ def lib() -> C.CDLL:
         L.vxo_engine_k_cache.argtypes = [C.c_void_p]
         L.vxo_engine_v_cache.restype = fp
         L.vxo_engine_v_cache.argtypes = [C.c_void_p]
+        L.vxo_engine_force_kv.argtypes = [C.c_void_p, fp, fp, fp, fp]
         _lib = L
     return _lib
 
@@ -290,6 +291,18 @@ class Engine:
             base = np.ctypeslib.as_array(fn(self.h), shape=(self.cfg["num_layers"] * n,))
             views.append(base[layer * n:(layer + 1) * n].reshape(self.cfg["max_seq_len"], kvd))
         return views[0], views[1]
+
+    def forward_forced(self, token: int, pos: int, k_rows: np.ndarray, v_rows: np.ndarray):
+        """One step that attends with the given K/V rows ([layers][kv_heads * head_dim] fp32) at `pos`
+        in place of its own; returns (token, the K rows, the V rows it computed)."""
+        k_rows = np.ascontiguousarray(k_rows, np.float32)
+        v_rows = np.ascontiguousarray(v_rows, np.float32)
+        kvd = self.cfg["num_kv_heads"] * self.cfg["head_dim"]
+        assert k_rows.shape == v_rows.shape == (self.layers, kvd)
+        seen_k, seen_v = np.zeros_like(k_rows), np.zeros_like(v_rows)
+        lib().vxo_engine_force_kv(self.h, fptr(k_rows), fptr(v_rows), fptr(seen_k), fptr(seen_v))
+        t = int(lib().vxo_engine_forward(self.h, token, pos, fptr(self.logits)))
+        return t, seen_k, seen_v
 
     def close(self):
         if self.h:

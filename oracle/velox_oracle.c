@@ -607,6 +607,10 @@ struct VxoEngine {
     VxoTensor embed, final_norm, head;
     VxoTensor* layer; /* [built_layers][16] indexed by kind */
     float *k_cache, *v_cache;
+    /* one-step K/V forcing (vxo_engine_force_kv): rows to attend with at the next forward's position,
+     * and where the rows it computed itself go */
+    const float *force_k, *force_v;
+    float *seen_k, *seen_v;
     float *hidden, *norm_x, *q_buf, *attn_out, *o_buf, *gate, *up, *down, *scores;
 };
 
@@ -736,6 +740,13 @@ void vxo_engine_set_threads(VxoEngine* e, int threads) { e->threads = threads > 
 float* vxo_engine_k_cache(VxoEngine* e) { return e->k_cache; }
 float* vxo_engine_v_cache(VxoEngine* e) { return e->v_cache; }
 
+void vxo_engine_force_kv(VxoEngine* e, const float* k_rows, const float* v_rows, float* seen_k, float* seen_v) {
+    e->force_k = k_rows;
+    e->force_v = v_rows;
+    e->seen_k = seen_k;
+    e->seen_v = seen_v;
+}
+
 static void vxo_linear(const VxoEngine* e, float* dst, const float* x, const VxoTensor* w, uint64_t in_dim,
                        uint64_t out_dim) {
     if (e->cfg.q4_0) vxo_matmul_q4_0(dst, x, (const uint8_t*)w->data, in_dim, out_dim, e->threads);
@@ -780,6 +791,12 @@ uint32_t vxo_engine_forward_layers(VxoEngine* e, uint32_t token, uint64_t pos, u
                 v_slot[i] = vxo_bf16_to_f32(vxo_f32_to_bf16(v_slot[i]));
             }
         }
+        if (e->force_k) {
+            memcpy(e->seen_k + (uint64_t)l * kvd, k_slot, kvd * sizeof(float));
+            memcpy(e->seen_v + (uint64_t)l * kvd, v_slot, kvd * sizeof(float));
+            memcpy(k_slot, e->force_k + (uint64_t)l * kvd, kvd * sizeof(float));
+            memcpy(v_slot, e->force_v + (uint64_t)l * kvd, kvd * sizeof(float));
+        }
         vxo_gqa_attention_step(e->attn_out, e->scores, e->q_buf, e->k_cache + (uint64_t)l * layer_kv,
                                e->v_cache + (uint64_t)l * layer_kv, c->num_heads, c->num_kv_heads, D, pos);
         vxo_linear(e, e->o_buf, e->attn_out, &L[VXO_T_O], qd, H);
@@ -793,6 +810,7 @@ uint32_t vxo_engine_forward_layers(VxoEngine* e, uint32_t token, uint64_t pos, u
         for (uint64_t i = 0; i < H; ++i) e->hidden[i] += e->down[i];
     }
 
+    e->force_k = e->force_v = NULL;
     vxo_rmsnorm(e->norm_x, e->hidden, (const float*)e->final_norm.data, H, c->rms_norm_eps);
     const VxoTensor* head = c->tied_lm_head ? &e->embed : &e->head;
     vxo_linear(e, logits, e->norm_x, head, H, c->vocab_size);

@@ -138,6 +138,11 @@ const float* vxo_engine_hidden(const VxoEngine* e);
 /* Emulated hand-off used by tests to fill KV caches for context configs. */
 float* vxo_engine_k_cache(VxoEngine* e);
 float* vxo_engine_v_cache(VxoEngine* e);
+/* Test harness, not part of the reference's algorithm: for the next forward only, every layer writes
+ * its own (bf16-rounded) K and V rows of that position to seen_k / seen_v ([layers][kv_heads * D]) and
+ * attends with k_rows / v_rows in their place, so a step can be recomputed on another engine's cache
+ * rows, the current position's included. */
+void vxo_engine_force_kv(VxoEngine* e, const float* k_rows, const float* v_rows, float* seen_k, float* seen_v);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,182 @@
+"""The benchmark configurations at their stated sizes against the CPU oracle (teacher forcing, logits
+within the bf16 bar of 2e-2, every GPU token the exact argmax of the GPU's own logits):
+
+  * config 2, Llama-3-8B: the full 32-layer model (untied 128256-row head) over a 128-token prompt and
+    256 greedy steps, each sampled step recomputed by the oracle on the GPU's K/V rows;
+  * config 3, Qwen2.5-7B layer shapes (QKV bias, 28/4 heads, FFN 18944), batched decode of B = 8 and
+    B = 32 sequences, each over its own seeded 2048-position context (ragged by sequence);
+  * config 4, the DeepSeek-V3 MLA layer at 4096 latent positions: B = 1 (64 splits, the 32-wide
+    merge) and B = 16 (8 splits);
+  * config 5, the Qwen2-72B layer shape after an 8192-position context: the planner's 32 splits of
+    288 positions and the separate merge kernel.
+Contexts are the device's seeded bf16 fill, copied into the oracle's caches, so both sides attend over
+the same values."""
+import numpy as np
+import pytest
+
+from velox_amd import _lib as L
+from velox_amd.engine import HipBatchEngine, HipDecodeEngine
+
+from test_gpu_kernels import kv_from_device
+from test_gpu_mla import _check_layer
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 2e-2
+GOLDEN = 0x9E3779B97F4A7C15
+LLAMA = dict(vocab_size=128256, hidden_dim=4096, intermediate_dim=14336, num_layers=32, num_heads=32, num_kv_heads=8,
+             head_dim=128, rms_norm_eps=1e-5, rope_theta=500000.0, qkv_bias=0, tied_lm_head=0)
+QWEN7_SMALL_VOCAB = dict(vocab_size=4096, hidden_dim=3584, intermediate_dim=18944, num_heads=28, num_kv_heads=4,
+                         head_dim=128, rms_norm_eps=1e-6, rope_theta=1000000.0, qkv_bias=1, tied_lm_head=1)
+QWEN72_SMALL_VOCAB = dict(vocab_size=4096, hidden_dim=8192, intermediate_dim=29568, num_heads=64, num_kv_heads=8,
+                          head_dim=128, rms_norm_eps=1e-6, rope_theta=1000000.0, qkv_bias=1, tied_lm_head=0)
+
+
+def _device_kv(arena, layer_index: int, hkv: int, max_seq: int, d: int, n_pos: int) -> np.ndarray:
+    """K/V rows [0, n_pos) of one (layer, sequence) cache slot as fp32 [2][n_pos][hkv * d]."""
+    cap = (max_seq + 31) // 32 * 32
+    layer_bytes = (2 * hkv * cap * d * 2 + 255) // 256 * 256
+    raw = np.zeros(2 * hkv * cap * d, np.uint16)
+    L.memcpy_dtoh(raw.ctypes.data, arena.kv_cache_pool + layer_index * layer_bytes, raw.nbytes)
+    kv = (kv_from_device(raw, hkv, max_seq, d).astype(np.uint32) << 16).view(np.float32)[:, :, :n_pos]
+    return kv.transpose(0, 2, 1, 3).reshape(2, n_pos, hkv * d)
+
+
+def test_config2_llama3_8b_full_depth_vs_oracle(oracle):
+    """All 32 layers and the untied head: the GPU decodes a 128-token prompt and 256 greedy steps in
+    its own state. At sampled positions the oracle recomputes that one step on the GPU's bf16 K/V
+    rows of every layer, [0, pos] (the step's own row included, so that no layer attends over a
+    value the two sides rounded to bf16 differently): its logits must be within the bf16 bar of the
+    GPU's, and the K/V rows it computed itself (RoPE'd K and V, bf16-rounded) must equal the GPU's to
+    a bf16 rounding step plus 1e-4 of the row's largest magnitude (each GEMV keeps its input to
+    2^-22 of each 32-value block's largest magnitude; 32 layers carry that to about 2e-5). Run
+    free instead, the two sides' bf16 roundings part wherever a value sits
+    at a rounding boundary, and a one-ulp step (2^-8 relative) in an early layer's V row moves every
+    later layer's input by about 1e-3 of its scale."""
+    seed, P, steps = 71, 128, 256
+    n = P + steps
+    max_seq = n + 1
+    hkv, d, nl = LLAMA["num_kv_heads"], LLAMA["head_dim"], LLAMA["num_layers"]
+    toks = [int(t) for t in oracle.prompt_tokens(seed, P, LLAMA["vocab_size"])]
+    gpu = HipDecodeEngine("llama3_8b", seed=seed, max_seq_len=max_seq)
+    got = []
+    for pos in range(n):
+        tg = gpu.forward_step(toks[pos], pos)
+        assert tg == oracle.argmax(gpu.logits), pos
+        got.append(gpu.logits.copy())
+        if pos + 1 >= P:
+            toks.append(tg)  # greedy decode after the prompt
+    kv = [_device_kv(gpu.arena, layer, hkv, max_seq, d, n) for layer in range(nl)]
+    gpu.close()
+    ref = oracle.Engine(dict(LLAMA, max_seq_len=max_seq), seed=seed, sigma=0.02, norm_sigma=0.0, q4_0=True,
+                        kv_bf16=True, threads=16)
+    caches = [ref.kv_cache(layer) for layer in range(nl)]
+    worst, worst_kv = 0.0, 0.0
+    for pos in (0, 1, 2, 31, 64, 127, 128, 129, 200, 255, 320, 383):
+        for layer, (kr, vr) in enumerate(caches):
+            kr[:pos], vr[:pos] = kv[layer][0][:pos], kv[layer][1][:pos]
+        t_ref, seen_k, seen_v = ref.forward_forced(toks[pos], pos, np.stack([kv[layer][0][pos] for layer in range(nl)]),
+                                                   np.stack([kv[layer][1][pos] for layer in range(nl)]))
+        dl = float(np.max(np.abs(got[pos] - ref.logits)))
+        worst = max(worst, dl)
+        for layer in range(nl):
+            for kind, mine, theirs in (("K", seen_k[layer], kv[layer][0][pos]), ("V", seen_v[layer], kv[layer][1][pos])):
+                scale = float(np.max(np.abs(theirs)))
+                beyond = np.maximum(np.abs(mine - theirs) - 2 ** -7 * np.abs(theirs), 0.0) / scale
+                i = int(np.argmax(beyond))
+                worst_kv = max(worst_kv, float(beyond[i]))
+                assert beyond[i] <= 1e-4, (pos, layer, kind, i, float(mine[i]), float(theirs[i]))
+        print(f"[llama3_8b 32 layers] pos={pos} gpu={int(np.argmax(got[pos]))} ref={t_ref} maxabs={dl:.3e} "
+              f"K/V rows beyond a bf16 step: {worst_kv:.2e} of the row's scale", flush=True)
+        srt = np.sort(ref.logits)
+        if srt[-1] - srt[-2] > 2 * LOGIT_TOL:
+            assert int(np.argmax(got[pos])) == t_ref, pos
+        # within the bf16 bar, and within the fp32-accumulation bar of 1e-3 as well
+        assert dl < LOGIT_TOL and dl < 1e-3, (pos, dl)
+    print(f"[llama3_8b 32 layers] worst logits maxabs with the K/V rows shared: {worst:.3e}", flush=True)
+    ref.close()
+
+
+@pytest.mark.parametrize("batch", [8, 32])
+def test_config3_qwen_batched_2048_context_vs_oracle(oracle, batch):
+    """Each sequence b attends over its own seeded context of 2048 - 3b positions (so sequences end in
+    different 32-position chunks), 2 layers, two batched steps per sequence."""
+    seed, layers, steps, ctx0 = 81, 2, 2, 2048
+    cfg = QWEN7_SMALL_VOCAB
+    max_seq = ctx0 + steps + 1
+    hkv, D, V = cfg["num_kv_heads"], cfg["head_dim"], cfg["vocab_size"]
+    gpu = HipBatchEngine(cfg, max_batch=batch, seed=seed, norm_sigma=0.1, max_seq_len=max_seq, num_layers=layers)
+    ctxs = [ctx0 - 3 * b for b in range(batch)]
+    prompts = [[int(t) for t in oracle.prompt_tokens(seed + 100 + b, max_seq, V)] for b in range(batch)]
+    for b in range(batch):
+        for layer in range(layers):
+            gpu.fill_kv_seq(layer, b, ctxs[b], seed=seed + 7)
+        gpu.set_prompt_seq(b, prompts[b])
+        gpu.set_state_seq(b, ctxs[b], prompts[b][ctxs[b]])
+    contexts = [[_device_kv(gpu.arena, layer * batch + b, hkv, max_seq, D, ctxs[b]) for layer in range(layers)]
+                for b in range(batch)]
+    got = [[] for _ in range(batch)]
+    for _ in range(steps):
+        gpu.batch_step(batch)
+        gpu.sync()
+        for b in range(batch):
+            got[b].append(gpu.logits_seq(b))
+    ref = oracle.Engine(dict(cfg, num_layers=layers, max_seq_len=max_seq), seed=seed, sigma=0.02, norm_sigma=0.1,
+                        q4_0=True, kv_bf16=True, threads=16)
+    worst = 0.0
+    for b in range(batch):
+        ref.reset()
+        for layer in range(layers):
+            kr, vr = ref.kv_cache(layer)
+            kr[:ctxs[b]] = contexts[b][layer][0]
+            vr[:ctxs[b]] = contexts[b][layer][1]
+        for t in range(steps):
+            pos = ctxs[b] + t
+            ref.forward(prompts[b][pos], pos)
+            d = float(np.max(np.abs(got[b][t] - ref.logits)))
+            worst = max(worst, d)
+            assert gpu.ring_seq(b, pos) == oracle.argmax(got[b][t]), (b, pos)
+            assert d < LOGIT_TOL, (b, pos, d)
+        assert gpu.state_seq(b) == (ctxs[b] + steps, prompts[b][ctxs[b] + steps])
+    print(f"[qwen2.5-7b batch {batch} ctx ~2048] worst logits maxabs {worst:.3e}", flush=True)
+    gpu.close()
+    ref.close()
+
+
+def test_config4_mla_4096_batch1_vs_oracle(oracle):
+    """B = 1 at 4096 latent positions: 64 position splits, merged 32 loads at a time."""
+    _check_layer(oracle, "deepseek_v3_mla", batch=1, ctxs=[4096], steps=2, max_seq=4104, norm_sigma=0.0)
+
+
+def test_config4_mla_4096_batch16_vs_oracle(oracle):
+    """B = 16 sequences near 4096 latent positions (ragged): 8 splits x 2 head groups per sequence."""
+    _check_layer(oracle, "deepseek_v3_mla", batch=16, ctxs=[4096 - 5 * i for i in range(16)], steps=1,
+                 max_seq=4104, norm_sigma=0.0)
+
+
+def test_config5_qwen72_8192_context_vs_oracle(oracle):
+    """A Qwen2-72B-shaped layer (64/8 heads, hidden 8192, FFN 29568, QKV bias, untied head) after an
+    8192-position seeded context: the planner's 32 splits (of 288 positions) and the merge kernel."""
+    seed, ctx = 91, 8192
+    max_seq = ctx + 16
+    cfg = QWEN72_SMALL_VOCAB
+    gpu = HipDecodeEngine(dict(cfg, num_layers=1), seed=seed, norm_sigma=0.1, max_seq_len=max_seq)
+    c = L.ModelConfig()
+    L.check(gpu.lib.velox_hip_model_config(gpu._model, __import__("ctypes").byref(c)))
+    assert c.attn_splits == 32
+    gpu.fill_kv(0, ctx, seed=13, sigma=1.0)
+    kv = _device_kv(gpu.arena, 0, cfg["num_kv_heads"], max_seq, cfg["head_dim"], ctx)
+    ref = oracle.Engine(dict(cfg, num_layers=1, max_seq_len=max_seq), seed=seed, sigma=0.02, norm_sigma=0.1,
+                        q4_0=True, kv_bf16=True, threads=16)
+    kr, vr = ref.kv_cache(0)
+    kr[:ctx], vr[:ctx] = kv[0], kv[1]
+    for i, tok in enumerate(oracle.prompt_tokens(seed, 3, cfg["vocab_size"])):
+        pos = ctx + i
+        t_ref = ref.forward(int(tok), pos)
+        t_gpu = gpu.forward_step(int(tok), pos)
+        d = float(np.max(np.abs(gpu.logits - ref.logits)))
+        print(f"[qwen2-72b ctx 8192] pos={pos} gpu={t_gpu} ref={t_ref} maxabs={d:.3e}", flush=True)
+        assert t_gpu == oracle.argmax(gpu.logits)
+        assert d < LOGIT_TOL, (pos, d)
+    gpu.close()
+    ref.close()

@@ -2,7 +2,7 @@
 
 Teacher forcing: both paths consume the same token sequence, so one argmax
 flip on a near-tie cannot desynchronise the comparison. Bars: logits max-abs <= 2e-2 against
-the oracle with bf16 KV (the bf16 parity bar; activations enter each GEMV as fp16), and the
+the oracle with bf16 KV (the bf16 parity bar), and the
 GPU argmax equal to the exact argmax of the GPU's own logits.
 """
 import numpy as np

@@ -176,10 +176,11 @@ def test_prefill_chunking_invariance(oracle):
     d = float(np.max(np.abs(la - lb)))
     print(f"[prefill chunking] logits maxabs {d:.3e}, identical {np.array_equal(la, lb)}", flush=True)
     assert d < 1e-3
-    # one bf16 ulp of each value, plus the fp32 rounding of the RoPE's cancellations near zero
+    # the batched GEMMs round their inputs to fp16 (2^-12 relative), the decode GEMV keeps them to
+    # 2^-22: one bf16 step of each value plus 2e-3 of the largest, where rows cancel towards zero
     kt = _device_kv(a, 0, P)
     for k in (ka, kb):
-        assert np.all(np.abs(k - kt) <= 2 ** -7 * np.abs(kt) + 1e-5 * np.max(np.abs(kt)))
+        assert np.all(np.abs(k - kt) <= 2 ** -7 * np.abs(kt) + 2e-3 * np.max(np.abs(kt)))
     a.close()
 
 

@@ -364,3 +364,46 @@ def test_qkv_bias_added_before_rope_closed_form(oracle):
                 g = h // (hq // hkv)
                 np.testing.assert_allclose(attn[h * d:(h + 1) * d], want_v[g * d:(g + 1) * d], atol=5e-5)
     eng.close()
+
+
+def test_forced_kv_step_attends_with_the_given_rows(oracle):
+    """The one-step K/V forcing of the oracle (the harness of the full-depth GPU comparison, which
+    recomputes a step on the GPU's cache rows): forcing the rows an engine computes itself changes
+    nothing, bit for bit, and reports those rows; and the forced rows are the ones attended: one
+    layer with O = identity and a zero FFN at position 0 (a single position, so each head's attention
+    output is its group's V row) leaves hidden - embedding equal to the forced V rows."""
+    cfg = dict(vocab_size=64, hidden_dim=64, intermediate_dim=96, num_layers=2, num_heads=4, num_kv_heads=2,
+               head_dim=16, max_seq_len=8, rms_norm_eps=1e-5, rope_theta=10000.0, qkv_bias=0, tied_lm_head=1)
+    a = oracle.Engine(cfg, seed=5, sigma=0.2, q4_0=False, kv_bf16=True, threads=1)
+    b = oracle.Engine(cfg, seed=5, sigma=0.2, q4_0=False, kv_bf16=True, threads=1)
+    for pos, tok in enumerate((7, 19)):
+        a.forward(tok, pos)
+    rows = [np.stack([a.kv_cache(layer)[i][1] for layer in range(2)]) for i in (0, 1)]
+    b.forward(7, 0)
+    t, seen_k, seen_v = b.forward_forced(19, 1, rows[0], rows[1])
+    assert t == oracle.argmax(a.logits) and np.array_equal(b.logits, a.logits)
+    assert np.array_equal(seen_k, rows[0]) and np.array_equal(seen_v, rows[1])
+    a.forward(33, 2)
+    b.forward(33, 2)  # the forcing lasts one step
+    assert np.array_equal(b.logits, a.logits)
+    a.close()
+    b.close()
+
+    H, hq, hkv, d = 64, 4, 2, 16
+    one = dict(cfg, num_layers=1)
+    eng = oracle.Engine(one, seed=6, q4_0=False, kv_bf16=False, threads=1)
+    f32 = lambda kind: eng.tensor_view(kind, 0).view(np.float32)  # noqa: E731
+    f32(oracle.T_O)[:] = np.eye(H, hq * d, dtype=np.float32).ravel()
+    for k in (oracle.T_GATE, oracle.T_UP, oracle.T_DOWN):
+        f32(k)[:] = 0.0
+    rng = np.random.default_rng(4)
+    fk = rng.standard_normal((1, hkv * d)).astype(np.float32)
+    fv = rng.standard_normal((1, hkv * d)).astype(np.float32)
+    _, seen_k, seen_v = eng.forward_forced(9, 0, fk, fv)
+    assert not np.array_equal(seen_v, fv)
+    x = f32(oracle.T_EMBED).reshape(64, H)[9].astype(np.float64)
+    want = np.concatenate([fv[0, (h // (hq // hkv)) * d:(h // (hq // hkv) + 1) * d] for h in range(hq)])
+    np.testing.assert_allclose(eng.hidden().astype(np.float64) - x, want, rtol=0, atol=1e-6)
+    kc, vc = eng.kv_cache(0)
+    assert np.array_equal(kc[0], fk[0]) and np.array_equal(vc[0], fv[0])
+    eng.close()

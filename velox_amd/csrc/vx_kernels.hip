@@ -5,10 +5,11 @@
 // with an MI355X design:
 //   * Q4_0 GEMV: wave64 tiles of R = 64/S rows x S lanes per row; every lane streams one
 //     16-byte code word (one 32-weight block) per iteration with fully coalesced 1 KiB wave loads
-//     of a layout repacked at load time; x lives in LDS as fp16; nibbles are unpacked with the
-//     0x6400 magic-exponent trick and consumed by v_dot2c_f32_f16 with fp32 accumulation; the
-//     Q4_0 offset -8 is folded into one per-block correction. RMSNorm runs in the prologue,
-//     residual / SwiGLU / argmax in the epilogue.
+//     of a layout repacked at load time; x lives in LDS as 22-bit integers per power-of-two-scaled
+//     32-element block, stored as six planes of signed base-16 digits, and each code word meets
+//     them in v_dot8_i32_i4 (q - 8 is the code nibble xor 8): the block's dot product is exact
+//     integer arithmetic, so x keeps 2^-22 of each block's largest magnitude (fp32-class).
+//     RMSNorm runs in the prologue, residual / SwiGLU / argmax in the epilogue.
 //   * Decode attention: split-K over the sequence, RoPE + bf16 KV append in the prologue,
 //     online softmax per split, LSE merge by the last workgroup of each KV head.
 #include <hip/hip_fp16.h>
@@ -36,19 +37,25 @@ __device__ __forceinline__ float vx_h2f(uint32_t h) { return __half2float(__usho
 // matching fp16 activation pair; the -1032 offset is folded into the block correction.
 __device__ __forceinline__ uint32_t vx_code_nibble(uint32_t dw, int e) { return (dw >> (8 * (e & 3) + 4 * (e >> 2))) & 15u; }
 
-__device__ __forceinline__ float vx_dot8(uint32_t q, uint4 xq, float acc) {
-    const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
-    const uint32_t c64 = 0x64646464u;
-    const uint32_t h0 = __builtin_amdgcn_perm(c64, lo, 0x04010400u);  // elements 0, 1
-    const uint32_t h1 = __builtin_amdgcn_perm(c64, lo, 0x04030402u);  // elements 2, 3
-    const uint32_t h2 = __builtin_amdgcn_perm(c64, hi, 0x04010400u);  // elements 4, 5
-    const uint32_t h3 = __builtin_amdgcn_perm(c64, hi, 0x04030402u);  // elements 6, 7
-    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, h0), __builtin_bit_cast(vx_h2, xq.x), acc, false);
-    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, h1), __builtin_bit_cast(vx_h2, xq.y), acc, false);
-    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, h2), __builtin_bit_cast(vx_h2, xq.z), acc, false);
-    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, h3), __builtin_bit_cast(vx_h2, xq.w), acc, false);
-    return acc;
+// Activations of the GEMV: block b of 32 values u is scaled by 2^e (e from its largest magnitude
+// m: m 2^e in [2^(B - 1), 2^B), B = kXBits) and rounded to integers X (|X| <= 2^B), written as
+// kXDigits balanced base-16 digits c_d in [-8, 7] (X = sum c_d 16^d; c_d + 8 is digit d of
+// X + kXOffset, the number with 8 in each digit). Digit d of the 8 values of code dword w sits at
+// the same nibble positions as their codes (value j at bit 8 (j & 3) + 4 (j >> 2)), so
+// v_dot8_i32_i4 of the code dword xor 0x88888888 (q - 8 as a signed nibble) and the digit dword
+// is sum (q - 8) c_d over 8 values, exactly. Zero, NaN and inf blocks keep e = 0.
+constexpr int kXDigits = 6;
+constexpr int kXBits = 4 * kXDigits - 2;  // balanced digits reach 8 (16^D - 1) / 15 > 2^B
+constexpr uint32_t kXOffset = 0x888888u >> (4 * (6 - kXDigits));
+static_assert(kXDigits == 5 || kXDigits == 6, "five or six digits: 18 or 22 bits");
+
+__device__ __forceinline__ int vx_xblock_exp(float m) {
+    if (!(m > 0.0f) || m > 3.0e38f) return 0;
+    const int e = (kXBits - 1) - ((int)((__float_as_uint(m) >> 23) & 255u) - 127);  // B - 1 - floor(log2 m)
+    return e < -100 ? -100 : (e > 120 ? 120 : e);
 }
+
+__device__ __forceinline__ float vx_pow2f(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
 
 template <int CTRL>
 __device__ __forceinline__ float vx_dpp(float x) {
@@ -184,9 +191,11 @@ __global__ __launch_bounds__(64 * kGemvWaves) void vx_gemv_q4_kernel(VxGemvArgs 
     if ((a.active_mask & 1ULL) == 0ULL) return;
     constexpr int W = kGemvWaves, kU = kGemvU, R = 64 / S, NT = 64 * W;
     const uint32_t K = a.k, nb = K >> 5, n_iter = a.n_iter;
-    uint4* xs4 = (uint4*)vx_smem;  // fp16 activations: 4 planes of nb 16-byte chunks
-    float* corr = (float*)(vx_smem + (size_t)K * 2u);
-    float* red = corr + nb;
+    // activations: kXDigits planes of nb 16-byte chunks (the 4 digit dwords of one block), then the
+    // blocks' unscale factors 2^-e
+    uint4* xs4 = (uint4*)vx_smem;
+    float* unscale = (float*)(xs4 + (size_t)kXDigits * nb);
+    float* red = unscale + nb;
     // the wave index is uniform: readfirstlane lets every per-wave quantity live in SGPRs
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane / S, s = lane % S;
@@ -313,33 +322,56 @@ __global__ __launch_bounds__(64 * kGemvWaves) void vx_gemv_q4_kernel(VxGemvArgs 
         ss = vx_block_sum<W>(ss, red);
         inv_rms = 1.0f / sqrtf(ss / (float)K + a.eps);
     }
-    // x -> fp16 in LDS, plane-major [w][b]: the S lanes of a row read blocks b..b+S-1 of one plane
-    // at consecutive 16-byte addresses (no LDS bank conflicts); corr[b] = -1032 * sum of block b
+    // x -> LDS digit planes [d][b] (16 bytes: the digit dwords of the block's 4 code dwords): the S
+    // lanes of a row read blocks b..b+S-1 of one plane at consecutive 16-byte addresses (no LDS
+    // bank conflicts). Group g = values 8g..8g+7 = code dword g & 3 of block g >> 2.
     auto stage = [&](uint32_t g, float4 v0, float4 v1, float4 g0, float4 g1) {
+        float u[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         if constexpr (NORM) {
-            v0 = make_float4((v0.x * inv_rms) * g0.x, (v0.y * inv_rms) * g0.y, (v0.z * inv_rms) * g0.z,
-                             (v0.w * inv_rms) * g0.w);
-            v1 = make_float4((v1.x * inv_rms) * g1.x, (v1.y * inv_rms) * g1.y, (v1.z * inv_rms) * g1.z,
-                             (v1.w * inv_rms) * g1.w);
+            const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) u[e] = (u[e] * inv_rms) * gg[e];
         }
-        const __half h[8] = {__float2half(v0.x), __float2half(v0.y), __float2half(v0.z), __float2half(v0.w),
-                             __float2half(v1.x), __float2half(v1.y), __float2half(v1.z), __float2half(v1.w)};
-        const uint4 hp = *(const uint4*)h;
-        xs4[(g & 3u) * nb + (g >> 2)] = hp;
-        // corr must see exactly the fp16 values stored above. The compiler may fuse the product
-        // and the conversion (v_fma_mix, one rounding) for one use of h and not for another (two
-        // roundings), so the sum is taken from the stored bits with v_dot2 against (1, 1):
-        // a one-ulp disagreement would cost 1024 ulp in the block's dot product.
-        const vx_h2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
-        float sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, hp.x), one2, 0.0f, false);
-        sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, hp.y), one2, sum, false);
-        sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, hp.z), one2, sum, false);
-        sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(vx_h2, hp.w), one2, sum, false);
         // the four 8-element groups of one 32-block sit in four consecutive lanes, which are all
-        // in range or all out of range (ng is a multiple of 4)
-        sum += __shfl_xor(sum, 1);
-        sum += __shfl_xor(sum, 2);
-        if ((g & 3u) == 0u) corr[g >> 2] = -1032.0f * sum;
+        // in range or all out of range (ng is a multiple of 4); nan is NaN when any value is NaN
+        // or infinite (the block's result is then NaN, as the fp32 dot product's would be)
+        float m = 0.0f, nan = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            m = fmaxf(m, fabsf(u[e]));
+            nan += u[e] * 0.0f;
+        }
+        m = fmaxf(m, __shfl_xor(m, 1));
+        m = fmaxf(m, __shfl_xor(m, 2));
+        nan += __shfl_xor(nan, 1);
+        nan += __shfl_xor(nan, 2);
+        const int ex = vx_xblock_exp(m);
+        const float sc = vx_pow2f(ex);
+        // Y = X + kXOffset (so that its plain base-16 digits are c_d + 8): adding 1.5 * 2^23 to the
+        // exactly scaled value rounds it to an integer (to nearest even, |X| <= 2^B <= 2^22) held in
+        // the low mantissa bits
+        uint32_t Y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) Y[e] = __float_as_uint(u[e] * sc + 12582912.0f) - (0x4B400000u - kXOffset);
+        // byte k of Y holds digits 2k (low nibble) and 2k + 1 (high nibble): gather byte k of
+        // values 0-3 and of values 4-7, then split the nibbles into the two digit dwords (values
+        // 0-3 in the low nibbles, 4-7 in the high ones); xor 8 turns c_d + 8 into c_d's signed nibble
+        uint32_t* dst = (uint32_t*)xs4 + (size_t)(g >> 2) * 4u + (g & 3u);
+#pragma unroll
+        for (int k = 0; k < (kXDigits + 1) / 2; ++k) {
+            const uint32_t sel = 0x0C0C0000u | ((4u + (uint32_t)k) << 8) | (uint32_t)k;
+            const uint32_t lw = __builtin_amdgcn_perm(__builtin_amdgcn_perm(Y[3], Y[2], sel),
+                                                      __builtin_amdgcn_perm(Y[1], Y[0], sel), 0x05040100u);
+            const uint32_t hw = __builtin_amdgcn_perm(__builtin_amdgcn_perm(Y[7], Y[6], sel),
+                                                      __builtin_amdgcn_perm(Y[5], Y[4], sel), 0x05040100u);
+            const uint32_t d0 = (lw & 0x0F0F0F0Fu) | ((hw << 4) & 0xF0F0F0F0u);
+            dst[(size_t)(2 * k) * nb * 4u] = d0 ^ 0x88888888u;
+            if (2 * k + 1 < kXDigits) {
+                const uint32_t d1 = ((lw >> 4) & 0x0F0F0F0Fu) | (hw & 0xF0F0F0F0u);
+                dst[(size_t)(2 * k + 1) * nb * 4u] = d1 ^ 0x88888888u;
+            }
+        }
+        if ((g & 3u) == 0u) unscale[g >> 2] = vx_pow2f(-ex) + nan;
     };
 #pragma unroll
     for (int i = 0; i < GX; ++i) {
@@ -365,13 +397,21 @@ __global__ __launch_bounds__(64 * kGemvWaves) void vx_gemv_q4_kernel(VxGemvArgs 
     auto consume = [&](int u) {
         // padded blocks (b >= nb, zero scale) read a valid activation chunk instead
         const uint32_t b = min(ci * S + s, nb - 1u);
-        const vx_u32x4 c = buf[u];
-        float dot = corr[b];
-        dot = vx_dot8(c.x, xs4[b], dot);
-        dot = vx_dot8(c.y, xs4[nb + b], dot);
-        dot = vx_dot8(c.z, xs4[2u * nb + b], dot);
-        dot = vx_dot8(c.w, xs4[3u * nb + b], dot);
-        acc = fmaf(vx_h2f(sbuf[u]), dot, acc);
+        const vx_u32x4 c = buf[u] ^ 0x88888888u;  // q - 8 as signed nibbles
+        int dg[kXDigits];
+#pragma unroll
+        for (int d = 0; d < kXDigits; ++d) {
+            const uint4 xd = xs4[(uint32_t)d * nb + b];
+            int t = __builtin_amdgcn_sdot8((int)c.x, (int)xd.x, 0, false);
+            t = __builtin_amdgcn_sdot8((int)c.y, (int)xd.y, t, false);
+            t = __builtin_amdgcn_sdot8((int)c.z, (int)xd.z, t, false);
+            dg[d] = __builtin_amdgcn_sdot8((int)c.w, (int)xd.w, t, false);  // |.| <= 2048
+        }
+        // sum (q - 8) X = lo + 4096 hi, both below 2^20 in magnitude: exact in fp32, one rounding
+        const int lo = dg[0] + dg[1] * 16 + dg[2] * 256;
+        const int hi = kXDigits == 6 ? dg[3] + dg[4] * 16 + dg[kXDigits - 1] * 256 : dg[3] + dg[4] * 16;
+        const float dot = fmaf((float)hi, 4096.0f, (float)lo);
+        acc = fmaf(vx_h2f(sbuf[u]) * unscale[b], dot, acc);
         if (++ci == n_iter) {
             acc = vx_group_sum<S>(acc);
             const uint32_t row = row_of(first + ct * step);
@@ -996,7 +1036,7 @@ template <int S, int EPI, bool NORM, int GX, int SPL>
 hipError_t vx_gemv_launch_t(const VxGemvArgs& a, uint32_t max_wgs, hipStream_t st) {
     constexpr int W = kGemvWaves;
     const uint32_t nb = a.k >> 5;
-    const size_t lds = (size_t)a.k * 2u + (size_t)nb * 4u + 64u;
+    const size_t lds = (size_t)nb * (16u * kXDigits + 4u) + 64u;  // K <= 32768: at most 102,464 bytes
     static size_t attr_lds = 64u * 1024u;
     if (lds > attr_lds) {
         if (hipFuncSetAttribute((const void*)vx_gemv_q4_kernel<S, EPI, NORM, GX, SPL>,
@@ -1104,8 +1144,7 @@ hipError_t vx_attn_launch_t(const VxAttnArgs& a, hipStream_t st) {
 
 }  // namespace
 
-// Upper bound on GEMV workgroups (waves loop over the remaining tiles); VELOX_HIP_GEMV_MAX_WGS
-// overrides it for tuning sweeps.
+// Upper bound on GEMV workgroups (waves loop over the remaining tiles).
 uint32_t vx_gemv_max_wgs_default() { return 512u; }
 
 hipError_t vx_launch_gemv(const VxMat& m, const VxGemvArgs& a0, int epi, uint32_t max_wgs, hipStream_t st) {
