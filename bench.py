@@ -107,6 +107,44 @@ def cpu_baseline(seed: int, tokens: int = 3) -> dict:
     }
 
 
+# The other BASELINE configurations, timed beside the headline on the same box (hipGraph replays of
+# the same runner flow): (key, builtin model, seeded context, batch, warmup, timed steps).
+OTHER_CONFIGS = (
+    ("config3_qwen2_5_7b_ctx2048_b1", "qwen2_5_7b", 2048, 1, 3, 30),
+    ("config3_qwen2_5_7b_ctx2048_b8", "qwen2_5_7b", 2048, 8, 3, 20),
+    ("config3_qwen2_5_7b_ctx2048_b32", "qwen2_5_7b", 2048, 32, 3, 20),
+    ("config5_qwen2_72b_ctx8192_b1", "qwen2_72b", 8192, 1, 3, 15),
+)
+MLA_CONFIGS = (("config4_deepseek_v3_mla_ctx4096_b1", 1), ("config4_deepseek_v3_mla_ctx4096_b16", 16))
+
+
+def other_configs(seed: int) -> dict:
+    """Benchmark configurations 3-5 at their stated shapes: decode tokens/s over all sequences (MLA:
+    device microseconds per layer step) and the achieved HBM bytes per second of the whole step
+    (weights once per step, every sequence's K/V or latent rows)."""
+    from velox_amd.engine import mla_run, run
+
+    out = {}
+    for key, model, ctx, batch, warmup, steps in OTHER_CONFIGS:
+        t0 = time.perf_counter()
+        rep, _ = run(model, prompt_len=1, warmup=warmup, steps=steps, seed=seed, use_graph=True, kernel_passes=0,
+                     context_len=ctx, batch=batch)
+        out[key] = {"value": round(rep["tok_per_s"], 2), "unit": "tok/s", "batch": batch, "context_tokens": ctx,
+                    "timed_positions": [ctx + 1 + warmup, ctx + warmup + steps],
+                    "hbm_gbps": round(rep["hbm_gbps"], 1), "hbm_frac": round(rep["hbm_gbps"] / HBM_PEAK_GBPS, 4),
+                    "bytes_per_step": int(rep["bytes_per_step"]), "ms_per_step": round(rep["decode_ms"] / steps, 5)}
+        print(f"[bench] {key}: {rep['tok_per_s']:.1f} tok/s, {rep['hbm_gbps']:.0f} GB/s "
+              f"({time.perf_counter() - t0:.1f} s)", file=sys.stderr, flush=True)
+    for key, batch in MLA_CONFIGS:
+        r = mla_run(batch=batch, context_len=4096, warmup=5, steps=50, seed=seed)
+        out[key] = {"value": round(r["us_per_layer"], 3), "unit": "us/layer", "higher_is_better": False,
+                    "batch": batch, "context_tokens": 4096, "hbm_gbps": round(r["hbm_gbps"], 1),
+                    "hbm_frac": round(r["hbm_gbps"] / HBM_PEAK_GBPS, 4), "bytes_per_step": int(r["bytes_per_layer"]),
+                    "attention_us": round(r["attn_us"], 3)}
+        print(f"[bench] {key}: {r['us_per_layer']:.2f} us/layer", file=sys.stderr, flush=True)
+    return out
+
+
 def bench_mla(args) -> int:
     """Benchmark configuration 4: one DeepSeek-V3 absorbed-MLA layer (fp8 e4m3 weights with 128x128 block
     scales, bf16 latent cache of `context_len` seeded positions per sequence), timed as hipGraph
@@ -195,6 +233,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--kernel-passes", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip benchmark configurations 3-5, timed beside the headline as other_configs")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--prompt-len", type=int, default=PROMPT_LEN)
     ap.add_argument("--model", default="llama3_8b",
@@ -296,6 +336,8 @@ def main() -> int:
     }
     if prefill:
         out["prefill"] = prefill
+    if not args.no_other_configs and headline:
+        out["other_configs"] = other_configs(args.seed)
     if not args.no_cpu_baseline and headline:
         print("[bench] cpu baseline (oracle, bounded sample)...", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(args.seed)
