@@ -110,6 +110,7 @@ def cpu_baseline(seed: int, tokens: int = 3) -> dict:
 # The other BASELINE configurations, timed beside the headline on the same box (hipGraph replays of
 # the same runner flow): (key, builtin model, seeded context, batch, warmup, timed steps).
 OTHER_CONFIGS = (
+    ("config1_smollm_135m_fp32_b1", "smollm_135m", 0, 1, 5, 64),
     ("config3_qwen2_5_7b_ctx2048_b1", "qwen2_5_7b", 2048, 1, 3, 30),
     ("config3_qwen2_5_7b_ctx2048_b8", "qwen2_5_7b", 2048, 8, 3, 20),
     ("config3_qwen2_5_7b_ctx2048_b32", "qwen2_5_7b", 2048, 32, 3, 20),
@@ -119,7 +120,7 @@ MLA_CONFIGS = (("config4_deepseek_v3_mla_ctx4096_b1", 1), ("config4_deepseek_v3_
 
 
 def other_configs(seed: int) -> dict:
-    """Benchmark configurations 3-5 at their stated shapes: decode tokens/s over all sequences (MLA:
+    """Benchmark configurations 1 and 3-5 at their stated shapes: decode tokens/s over all sequences (MLA:
     device microseconds per layer step) and the achieved HBM bytes per second of the whole step
     (weights once per step, every sequence's K/V or latent rows)."""
     from velox_amd.engine import mla_run, run
@@ -127,10 +128,12 @@ def other_configs(seed: int) -> dict:
     out = {}
     for key, model, ctx, batch, warmup, steps in OTHER_CONFIGS:
         t0 = time.perf_counter()
-        rep, _ = run(model, prompt_len=1, warmup=warmup, steps=steps, seed=seed, use_graph=True, kernel_passes=0,
-                     context_len=ctx, batch=batch)
+        fp32 = "fp32" in key  # configuration 1: the reference's fp32 rows, a 32-token prompt
+        rep, _ = run(model, prompt_len=32 if fp32 else 1, warmup=warmup, steps=steps, seed=seed, use_graph=True,
+                     kernel_passes=0, context_len=ctx, batch=batch, unquantized=1 if fp32 else 0)
         out[key] = {"value": round(rep["tok_per_s"], 2), "unit": "tok/s", "batch": batch, "context_tokens": ctx,
-                    "timed_positions": [ctx + 1 + warmup, ctx + warmup + steps],
+                    "timed_positions": ([32 + warmup, 31 + warmup + steps] if fp32 else
+                                        [ctx + 1 + warmup, ctx + warmup + steps]),
                     "hbm_gbps": round(rep["hbm_gbps"], 1), "hbm_frac": round(rep["hbm_gbps"] / HBM_PEAK_GBPS, 4),
                     "bytes_per_step": int(rep["bytes_per_step"]), "ms_per_step": round(rep["decode_ms"] / steps, 5)}
         print(f"[bench] {key}: {rep['tok_per_s']:.1f} tok/s, {rep['hbm_gbps']:.0f} GB/s "
@@ -234,7 +237,7 @@ def main() -> int:
     ap.add_argument("--kernel-passes", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-other-configs", action="store_true",
-                    help="skip benchmark configurations 3-5, timed beside the headline as other_configs")
+                    help="skip benchmark configurations 1 and 3-5, timed beside the headline as other_configs")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--prompt-len", type=int, default=PROMPT_LEN)
     ap.add_argument("--model", default="llama3_8b",

@@ -54,7 +54,8 @@ typedef struct VeloxHipModelConfig {
     float rms_norm_eps, rope_theta;
     uint32_t qkv_bias;          /* 1: q/k/v biases (Qwen) */
     uint32_t tied_lm_head;      /* 1: LM head reads the embedding table */
-    uint32_t quant_mode;        /* VELOX_QUANT_GGML_Q4_0 */
+    uint32_t quant_mode;        /* VELOX_QUANT_GGML_Q4_0; or VELOX_QUANT_F32 / _F16 rows (single-sequence
+                                   decode only: max_batch and prefill_chunk <= 1; widths <= 16384) */
     uint32_t attn_splits;       /* split-K partitions over the sequence (<= 64); 0 = automatic */
     uint64_t vram_budget_bytes; /* 0 = 288 GB of HBM3E */
     uint32_t max_batch;         /* sequences of the batched decode step (<= 32; 0 or 1 = single);
@@ -153,13 +154,19 @@ const VeloxHipModel* velox_hip_arena_model(const VeloxHipArena* a);
 
 /* ---- loaders (velox_cuda_runner.cu:154-199 stream_tensor_converted) ----
  * q4_0: host GGML Q4_0 blocks, row-major [rows][in/32] x 18 B, for a matrix kind of `layer`.
- * f32: host fp32 vector (norm gains, biases). Both upload and repack on `stream`. */
+ * rows: host fp32 (quant_mode VELOX_QUANT_F32) or fp16 (VELOX_QUANT_F16) rows [rows][in] of a
+ *   matrix kind, stored as the reference's weight arena holds them (src/codegen.rs:1024-1028);
+ *   EINVAL on a Q4_0 arena, as q4_0 is on a row arena.
+ * f32: host fp32 vector (norm gains, biases). All upload (and repack) on `stream`. */
 int velox_hip_load_q4_0(VeloxHipArena* a, int kind, uint32_t layer, const void* blocks, uint64_t nbytes,
+                        hipStream_t stream);
+int velox_hip_load_rows(VeloxHipArena* a, int kind, uint32_t layer, const void* rows, uint64_t nbytes,
                         hipStream_t stream);
 int velox_hip_load_f32(VeloxHipArena* a, int kind, uint32_t layer, const float* data, uint64_t count,
                        hipStream_t stream);
 /* Synthesizes the whole seeded model on the device (linear weights N(0,sigma) quantized to Q4_0,
- * norm gains 1 or N(1,norm_sigma), biases N(0,sigma)), bit-identical to the oracle's recipe. */
+ * or as fp32 / fp16 rows for those quant_modes; norm gains 1 or N(1,norm_sigma), biases
+ * N(0,sigma)), bit-identical to the oracle's recipe. */
 int velox_hip_synthesize_model(VeloxHipArena* a, uint64_t seed, float sigma, float norm_sigma,
                                hipStream_t stream);
 /* Fills layer `layer`'s KV cache positions [0, n_pos) with bf16 values seed-generated N(0, sigma). */
@@ -375,6 +382,8 @@ typedef struct VeloxHipRunOptions {
                                 instead of one decode step each */
     const char* model_file;  /* non-NULL: the model is read from this .vlx source (velox_hip_vlx_load),
                                 its target block setting the VRAM budget; `model` is then ignored */
+    uint32_t unquantized;    /* 0: GGML Q4_0 weights; 1 / 2: fp32 / fp16 rows (quant_mode 0 / 1, a build
+                                without --quantize, src/cli.rs:1214-1388), single sequence only */
 } VeloxHipRunOptions;
 
 typedef struct VeloxHipRunReport {

@@ -27,7 +27,7 @@ class VxoConfig(C.Structure):
         ("num_layers", C.c_uint32), ("num_heads", C.c_uint32), ("num_kv_heads", C.c_uint32),
         ("head_dim", C.c_uint32), ("max_seq_len", C.c_uint32), ("rms_norm_eps", C.c_float),
         ("rope_theta", C.c_float), ("qkv_bias", C.c_uint32), ("tied_lm_head", C.c_uint32),
-        ("q4_0", C.c_uint32), ("kv_bf16", C.c_uint32),
+        ("q4_0", C.c_uint32), ("kv_bf16", C.c_uint32), ("w_f16", C.c_uint32),
     ]
 
 
@@ -228,7 +228,7 @@ class Engine:
 
     def __init__(self, cfg: dict, seed: int, sigma: float = 0.02, norm_sigma: float = 0.0,
                  q4_0: bool = True, kv_bf16: bool = True, layers_to_build: int | None = None,
-                 threads: int = 1):
+                 threads: int = 1, w_f16: bool = False):
         self.cfg = dict(cfg)
         c = VxoConfig()
         c.vocab_size = cfg["vocab_size"]
@@ -245,6 +245,7 @@ class Engine:
         c.tied_lm_head = int(cfg.get("tied_lm_head", 0))
         c.q4_0 = int(q4_0)
         c.kv_bf16 = int(kv_bf16)
+        c.w_f16 = int(w_f16)
         self._c = c
         nl = cfg["num_layers"] if layers_to_build is None else layers_to_build
         self.layers = min(nl, cfg["num_layers"])

@@ -645,7 +645,11 @@ static void vxo_make_matrix(VxoTensor* t, const VxoConfig* c, uint64_t seed, uin
 #pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
 #endif
         for (long r = 0; r < (long)rows; ++r)
-            for (uint64_t k = 0; k < cols; ++k) dst[(uint64_t)r * cols + k] = vxo_normal(st, (uint64_t)r * cols + k, coef);
+            for (uint64_t k = 0; k < cols; ++k) {
+                const float v = vxo_normal(st, (uint64_t)r * cols + k, coef);
+                /* fp16 weights (the reference's quant_mode 1): the value rounded to fp16, exact in fp32 */
+                dst[(uint64_t)r * cols + k] = c->w_f16 ? vxo_f16_to_f32(vxo_f32_to_f16(v)) : v;
+            }
     }
     (void)threads;
 }

@@ -82,8 +82,31 @@ def test_arena_plan_sizes_and_budget():
     assert rc == -2
 
 
+def test_float_row_plan_sizes():
+    """quant_mode 0 / 1: every matrix as fp32 / fp16 rows (gate and up as one 2F-row matrix), no
+    scales; the single-sequence decode only."""
+    lib = L.load()
+    smollm = dict(vocab_size=49152, hidden_dim=576, intermediate_dim=1536, num_layers=30, num_heads=9,
+                  num_kv_heads=3, head_dim=64, max_seq_len=64, rms_norm_eps=1e-5, rope_theta=10000.0, qkv_bias=0,
+                  tied_lm_head=1)
+    weights = 30 * ((576 + 2 * 192) * 576 + 576 * 576 + 2 * 1536 * 576 + 576 * 1536) + 49152 * 576
+    for quant, elt in ((L.QUANT_F32, 4), (L.QUANT_F16, 2)):
+        rc, m = _plan(make_config(dict(smollm, quant_mode=quant)))
+        assert rc == 0
+        v = [C.c_uint64() for _ in range(5)]
+        lib.velox_hip_model_arena_bytes(m, *[C.byref(x) for x in v])
+        assert v[1].value == 0
+        # each matrix starts 256-aligned: at most 255 padding bytes per matrix
+        assert weights * elt <= v[0].value < weights * elt + 256 * (4 * 30 + 1)
+        assert lib.velox_hip_model_step_bytes(m, 0) >= weights * elt
+        lib.velox_hip_model_destroy(m)
+        for field, value in (("max_batch", 8), ("prefill_chunk", 16), ("intermediate_dim", 18944)):
+            rc, _ = _plan(make_config(dict(smollm, quant_mode=quant, **{field: value})))
+            assert rc == -1, field
+
+
 @pytest.mark.parametrize("field,value", [("head_dim", 96), ("num_kv_heads", 5), ("hidden_dim", 4100),
-                                         ("quant_mode", 0), ("num_layers", 0)])
+                                         ("quant_mode", 2), ("num_layers", 0)])
 def test_plan_rejects_unsupported_shapes(field, value):
     cfg = make_config("llama3_8b", max_seq_len=64)
     setattr(cfg, field, value)

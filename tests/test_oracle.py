@@ -407,3 +407,18 @@ def test_forced_kv_step_attends_with_the_given_rows(oracle):
     kc, vc = eng.kv_cache(0)
     assert np.array_equal(kc[0], fk[0]) and np.array_equal(vc[0], fv[0])
     eng.close()
+
+
+def test_fp16_weight_mode_rounds_the_fp32_weights(oracle):
+    """w_f16 (the reference's quant_mode 1): every linear weight and embedding value is the fp32
+    engine's value rounded to fp16 (numpy's round-to-nearest-even cast); vectors stay fp32."""
+    cfg = dict(vocab_size=64, hidden_dim=64, intermediate_dim=96, num_layers=1, num_heads=4, num_kv_heads=2,
+               head_dim=16, max_seq_len=8, rms_norm_eps=1e-5, rope_theta=10000.0, qkv_bias=0, tied_lm_head=1)
+    a = oracle.Engine(cfg, seed=4, sigma=0.5, norm_sigma=0.1, q4_0=False, threads=1)
+    b = oracle.Engine(cfg, seed=4, sigma=0.5, norm_sigma=0.1, q4_0=False, w_f16=True, threads=1)
+    for kind in (oracle.T_EMBED, oracle.T_Q, oracle.T_GATE, oracle.T_DOWN):
+        wa, wb = a.tensor(kind, 0).view(np.float32), b.tensor(kind, 0).view(np.float32)
+        assert np.array_equal(wb, wa.astype(np.float16).astype(np.float32)) and not np.array_equal(wa, wb)
+    assert np.array_equal(a.tensor(oracle.T_ATTN_NORM, 0), b.tensor(oracle.T_ATTN_NORM, 0))
+    a.close()
+    b.close()

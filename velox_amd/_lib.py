@@ -13,7 +13,7 @@ ROOT = os.path.dirname(PKG)
 LIB_PATH = os.path.join(PKG, "lib", "libvelox_hip.so")
 HEADER = os.path.join(ROOT, "include", "velox_hip.h")
 
-QUANT_GGML_Q4_0 = 5
+QUANT_F32, QUANT_F16, QUANT_GGML_Q4_0 = 0, 1, 5  # quant_mode: the reference's fp32 / fp16 rows, GGML Q4_0
 GEMV_STORE, GEMV_RESIDUAL, GEMV_SWIGLU = 0, 1, 2
 EINVAL, ENOMEM, ESHAPE, ENOTLOADED = -1, -2, -3, -4
 T_EMBED, T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN = 1, 2, 3, 4, 5, 6, 7, 8
@@ -66,7 +66,7 @@ class RunOptions(C.Structure):
         ("norm_sigma", C.c_float), ("use_graph", C.c_uint32), ("num_layers", C.c_uint32),
         ("kernel_passes", C.c_uint32), ("verbose", C.c_uint32), ("prompt_tokens", C.POINTER(C.c_uint32)),
         ("context_len", C.c_uint32), ("batch", C.c_uint32), ("weights_path", C.c_char_p),
-        ("prefill_chunk", C.c_uint32), ("model_file", C.c_char_p),
+        ("prefill_chunk", C.c_uint32), ("model_file", C.c_char_p), ("unquantized", C.c_uint32),
     ]
 
 
@@ -137,6 +137,7 @@ _SIGS = {
     "velox_hip_arena_bind": (_I, [_P, C.POINTER(Arena)]),
     "velox_hip_arena_model": (_P, [C.POINTER(Arena)]),
     "velox_hip_load_q4_0": (_I, [C.POINTER(Arena), _I, _U32, _P, _U64, _P]),
+    "velox_hip_load_rows": (_I, [C.POINTER(Arena), _I, _U32, _P, _U64, _P]),
     "velox_hip_load_f32": (_I, [C.POINTER(Arena), _I, _U32, _P, _U64, _P]),
     "velox_hip_synthesize_model": (_I, [C.POINTER(Arena), _U64, _F, _F, _P]),
     "velox_hip_fill_kv": (_I, [C.POINTER(Arena), _U32, _U32, _U64, _F, _P]),

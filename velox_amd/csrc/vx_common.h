@@ -91,10 +91,17 @@ VX_HD uint32_t vx_vslot(uint32_t r) { return 8u * ((r & 15u) >> 2) + 4u * (r >> 
 // ---------------------------------------------------------------------------------------------
 // Device-side views
 // ---------------------------------------------------------------------------------------------
+// Weight formats of a VxMat: GGML Q4_0 in the tiled layout, or the reference's unquantized rows
+// (quant_mode 0 fp32, 1 fp16), row-major [rows][k] (paired: n gate rows, then n up rows), n_tiles
+// = ceil(n / 4) tiles of 4 logical rows, no scales.
+enum { VX_FMT_Q4 = 0, VX_FMT_F32 = 1, VX_FMT_F16 = 2 };
+constexpr uint32_t kVxFloatMaxK = 16384;  // fp32 activations of a float-row GEMV in LDS
+
 struct VxMat {
     const uint4* codes;
     const uint16_t* scales;
     uint32_t n, k, s, n_tiles, n_iter, paired;
+    uint32_t fmt;
 };
 
 struct VxGemvArgs {
@@ -233,6 +240,9 @@ int vx_record_error(hipError_t e);  // vx_host.cpp: the first error of a step, r
 // Launch helpers implemented in vx_kernels.hip, used by vx_host.cpp.
 enum { VX_EPI_STORE = 0, VX_EPI_RESID = 1, VX_EPI_SWIGLU = 2, VX_EPI_ARGMAX = 3 };
 hipError_t vx_launch_gemv(const VxMat& m, const VxGemvArgs& a, int epi, uint32_t max_wgs, hipStream_t st);
+// The float-row GEMV (vx_gemv_f.hip) that vx_launch_gemv runs for VX_FMT_F32 / VX_FMT_F16 matrices,
+// on `wgs` workgroups (vx_gemv_grid of the matrix's tiles).
+hipError_t vx_launch_gemv_f(const VxMat& m, const VxGemvArgs& a, int epi, uint32_t wgs, hipStream_t st);
 hipError_t vx_launch_attention(const VxAttnArgs& a, uint32_t d, hipStream_t st);
 // vx_batch.hip
 // Batched prefill (vx_batch.hip): row r of a chunk is position p0 + r of the one sequence.
@@ -267,6 +277,7 @@ hipError_t vx_launch_repack(const void* blocks, uint32_t rows, uint32_t row0, ui
 hipError_t vx_launch_synth_q4(const VxMat& m, uint32_t rows, uint32_t row0, uint32_t pair_part, uint64_t stream,
                               float coef, hipStream_t st);
 hipError_t vx_launch_fill_normal(float* out, uint64_t n, uint64_t stream, float coef, float mean, hipStream_t st);
+hipError_t vx_launch_fill_normal_f16(uint16_t* out, uint64_t n, uint64_t stream, float coef, float mean, hipStream_t st);
 // Fills K/V of one layer, positions [0, n_pos): element (t, g, d) draws index (t*hkv + g)*D + d,
 // the [S][hkv*D] order of the reference's cache (src/runtime.rs:1358-1361).
 hipError_t vx_launch_fill_kv(uint16_t* layer_base, uint32_t hkv, uint32_t s_cap, uint32_t d, uint32_t n_pos,

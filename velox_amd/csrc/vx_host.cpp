@@ -38,6 +38,7 @@ namespace {
 struct VxMatPlan {
     uint64_t code_off = 0, scale_off = 0, code_bytes = 0, scale_bytes = 0;
     uint32_t n = 0, k = 0, s = 0, n_tiles = 0, n_iter = 0, paired = 0;
+    uint32_t fmt = VX_FMT_Q4;
     // second copy in the MFMA operand layout of the batched GEMM (arenas planned for more than one row)
     bool has_m = false;
     uint64_t mcode_off = 0, mscale_off = 0;
@@ -139,8 +140,26 @@ uint32_t vx_choose_s(uint32_t nb) {
     return best;
 }
 
-void vx_mat_layout(uint32_t n, uint32_t k, uint32_t s, uint32_t paired, VxMatPlan& p) {
+// The weight format of a quant_mode (GGML Q4_0 in the tiled layout, or the reference's fp32 / fp16
+// rows).
+uint32_t vx_fmt_of(uint32_t quant_mode) {
+    return quant_mode == VELOX_QUANT_F32 ? VX_FMT_F32 : quant_mode == VELOX_QUANT_F16 ? VX_FMT_F16 : VX_FMT_Q4;
+}
+
+void vx_mat_layout(uint32_t n, uint32_t k, uint32_t s, uint32_t paired, VxMatPlan& p, uint32_t fmt = VX_FMT_Q4) {
     const uint32_t nb = k / 32;
+    p.fmt = fmt;
+    if (fmt != VX_FMT_Q4) {  // row-major [rows][k] (paired: n gate rows, then n up rows), tiles of 4 rows
+        p.n = n;
+        p.k = k;
+        p.s = 0;
+        p.paired = paired;
+        p.n_tiles = (n + 3) / 4;
+        p.n_iter = 0;
+        p.code_bytes = (uint64_t)(paired ? 2 * n : n) * k * (fmt == VX_FMT_F32 ? 4 : 2);
+        p.scale_bytes = 0;
+        return;
+    }
     p.n = n;
     p.k = k;
     p.s = s ? s : vx_choose_s(nb);
@@ -181,6 +200,7 @@ VxMat vx_view(const VeloxHipArena* a, const VxMatPlan& p) {
     m.n_tiles = p.n_tiles;
     m.n_iter = p.n_iter;
     m.paired = p.paired;
+    m.fmt = p.fmt;
     return m;
 }
 
@@ -218,6 +238,7 @@ VxMat vx_view_public(const VeloxHipQ4Matrix* q) {
     m.n_tiles = q->n_tiles;
     m.n_iter = q->n_iter;
     m.paired = q->paired;
+    m.fmt = VX_FMT_Q4;
     return m;
 }
 
@@ -230,7 +251,16 @@ bool vx_shape_ok(const VeloxHipModelConfig& c) {
     if (c.head_dim == 64 && !(G == 1 || G == 2 || G == 3 || G == 4 || G == 8)) return false;
     if (c.head_dim == 128 && !(G == 1 || G == 2 || G == 4 || G == 7 || G == 8)) return false;
     if (((uint64_t)c.num_heads * c.head_dim) % 32) return false;
-    if (c.quant_mode != VELOX_QUANT_GGML_Q4_0) return false;
+    if (c.quant_mode != VELOX_QUANT_GGML_Q4_0 && c.quant_mode != VELOX_QUANT_F32 && c.quant_mode != VELOX_QUANT_F16)
+        return false;
+    if (c.quant_mode != VELOX_QUANT_GGML_Q4_0) {
+        // fp32 / fp16 rows: the single-sequence decode only (the batched GEMMs read Q4_0), and
+        // fp32 activations of a row in LDS
+        if (c.max_batch > 1 || c.prefill_chunk > 1) return false;
+        if (c.hidden_dim > kVxFloatMaxK || c.intermediate_dim > kVxFloatMaxK ||
+            (uint64_t)c.num_heads * c.head_dim > kVxFloatMaxK)
+            return false;
+    }
     if (c.num_kv_heads > 64 || c.attn_splits > 64 || c.max_batch > 32 || c.prefill_chunk > 64) return false;
     // batched RMSNorm: float4 rows of at most 8192
     if ((c.max_batch > 1 || c.prefill_chunk > 1) && ((c.hidden_dim & 3u) || c.hidden_dim > 8192)) return false;
@@ -281,13 +311,14 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
     const uint32_t H = c.hidden_dim, F = c.intermediate_dim, D = c.head_dim;
     const uint32_t qd = c.num_heads * D, kvd = c.num_kv_heads * D;
     uint64_t cc = 0, sc = 0, nc = 0;
+    const uint32_t fmt = vx_fmt_of(c.quant_mode);
     M->layers.resize(c.num_layers);
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         VxLayerPlan& L = M->layers[l];
-        vx_mat_layout(qd + 2 * kvd, H, 0, 0, L.qkv);
-        vx_mat_layout(H, qd, 0, 0, L.o);
-        vx_mat_layout(F, H, 0, 1, L.gate_up);
-        vx_mat_layout(H, F, 0, 0, L.down);
+        vx_mat_layout(qd + 2 * kvd, H, 0, 0, L.qkv, fmt);
+        vx_mat_layout(H, qd, 0, 0, L.o, fmt);
+        vx_mat_layout(F, H, 0, 1, L.gate_up, fmt);
+        vx_mat_layout(H, F, 0, 0, L.down, fmt);
         vx_place(L.qkv, cc, sc);
         vx_place(L.o, cc, sc);
         vx_place(L.gate_up, cc, sc);
@@ -301,12 +332,12 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
             nc = vx_align(nc + (uint64_t)(qd + 2 * kvd) * 4);
         }
     }
-    vx_mat_layout(c.vocab_size, H, 0, 0, M->embed);
+    vx_mat_layout(c.vocab_size, H, 0, 0, M->embed, fmt);
     vx_place(M->embed, cc, sc);
     if (c.tied_lm_head) {
         M->head = M->embed;
     } else {
-        vx_mat_layout(c.vocab_size, H, 0, 0, M->head);
+        vx_mat_layout(c.vocab_size, H, 0, 0, M->head, fmt);
         vx_place(M->head, cc, sc);
     }
     // batched rows (sequences of a batched step, or positions of a prefill chunk): every matrix
@@ -448,8 +479,11 @@ uint64_t velox_hip_model_step_bytes(const VeloxHipModel* m, uint64_t pos) {
     const uint64_t H = c.hidden_dim, F = c.intermediate_dim, D = c.head_dim;
     const uint64_t qd = (uint64_t)c.num_heads * D, kvd = (uint64_t)c.num_kv_heads * D;
     const uint64_t per_layer_w = (qd + 2 * kvd) * H + H * qd + 2 * F * H + H * F;
-    uint64_t bytes = (per_layer_w * c.num_layers + (uint64_t)c.vocab_size * H) / 32 * 18;
-    bytes += H / 32 * 18;                                   // embedding row
+    // bytes per weight read: Q4_0 18 per 32, fp32 4, fp16 2
+    const uint64_t wnum = c.quant_mode == VELOX_QUANT_F32 ? 4 : c.quant_mode == VELOX_QUANT_F16 ? 2 : 18;
+    const uint64_t wden = c.quant_mode == VELOX_QUANT_F32 || c.quant_mode == VELOX_QUANT_F16 ? 1 : 32;
+    uint64_t bytes = (per_layer_w * c.num_layers + (uint64_t)c.vocab_size * H) / wden * wnum;
+    bytes += H / wden * wnum;                               // embedding row
     bytes += (2 * (uint64_t)c.num_layers + 1) * H * 4;      // norm gains
     if (c.qkv_bias) bytes += (uint64_t)c.num_layers * (qd + 2 * kvd) * 4;
     const uint64_t p = pos < c.max_seq_len ? pos : c.max_seq_len - 1;
@@ -626,6 +660,7 @@ int velox_hip_arena_matrix(const VeloxHipArena* a, int kind, uint32_t layer, Vel
     uint32_t r0, pair, rows, cols;
     if (kind == VELOX_T_HEAD && vx_model(a)->cfg.tied_lm_head) kind = VELOX_T_EMBED;
     if (!vx_target(vx_model(a), kind, layer, &mp, &r0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
+    if (mp->fmt != VX_FMT_Q4) return VELOX_HIP_EINVAL;  // a Q4_0 view; fp32 / fp16 rows have none
     out->codes = (void*)(a->weight_arena + mp->code_off);
     out->scales = (void*)(a->weight_scales + mp->scale_off);
     out->n = mp->n;
@@ -654,6 +689,7 @@ int velox_hip_load_q4_0(VeloxHipArena* a, int kind, uint32_t layer, const void* 
     const VxMatPlan* mp;
     uint32_t row0, pair, rows, cols;
     if (!vx_target(vx_model(a), kind, layer, &mp, &row0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
+    if (mp->fmt != VX_FMT_Q4) return VELOX_HIP_EINVAL;  // the arena holds fp32 / fp16 rows
     if (nbytes != (uint64_t)rows * (cols / 32) * 18) return VELOX_HIP_ESHAPE;
     void* staging = nullptr;
     hipError_t e = hipMalloc(&staging, nbytes);
@@ -663,6 +699,22 @@ int velox_hip_load_q4_0(VeloxHipArena* a, int kind, uint32_t layer, const void* 
     if (e == hipSuccess && kind == VELOX_T_EMBED && vx_model(a)->cfg.tied_lm_head) e = vx_build_m(a, vx_model(a)->head, stream);
     if (e == hipSuccess) e = hipStreamSynchronize(stream);
     hipFree(staging);
+    return (int)e;
+}
+
+int velox_hip_load_rows(VeloxHipArena* a, int kind, uint32_t layer, const void* rows_data, uint64_t nbytes,
+                        hipStream_t stream) {
+    if (!a || !vx_model(a) || !rows_data) return VELOX_HIP_EINVAL;
+    const VxMatPlan* mp;
+    uint32_t row0, pair, rows, cols;
+    if (!vx_target(vx_model(a), kind, layer, &mp, &row0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
+    if (mp->fmt == VX_FMT_Q4) return VELOX_HIP_EINVAL;  // Q4_0 arenas load blocks (velox_hip_load_q4_0)
+    const uint64_t elt = mp->fmt == VX_FMT_F32 ? 4 : 2;
+    if (nbytes != (uint64_t)rows * cols * elt) return VELOX_HIP_ESHAPE;
+    const uint64_t first = (uint64_t)(pair ? mp->n : 0) + row0;  // paired: up rows follow the n gate rows
+    hipError_t e = hipMemcpyAsync((void*)(a->weight_arena + mp->code_off + first * cols * elt), rows_data, nbytes,
+                                  hipMemcpyHostToDevice, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
     return (int)e;
 }
 
@@ -688,7 +740,17 @@ int velox_hip_synthesize_model(VeloxHipArena* a, uint64_t seed, float sigma, flo
         const VxMatPlan* mp;
         uint32_t row0, pair, rows, cols;
         if (!vx_target(M, kind, layer, &mp, &row0, &pair, &rows, &cols)) return;
-        e = vx_launch_synth_q4(vx_view(a, *mp), rows, row0, pair, vx_stream(seed, vx_tag(layer, kind)), coef, st);
+        const uint64_t stream = vx_stream(seed, vx_tag(layer, kind));
+        if (mp->fmt == VX_FMT_Q4) {
+            e = vx_launch_synth_q4(vx_view(a, *mp), rows, row0, pair, stream, coef, st);
+            return;
+        }
+        // fp32 / fp16 rows: the seeded values themselves (rounded to fp16), row-major
+        const uint64_t first = (uint64_t)(pair ? mp->n : 0) + row0, count = (uint64_t)rows * cols;
+        uint8_t* dst = (uint8_t*)a->weight_arena + mp->code_off;
+        e = mp->fmt == VX_FMT_F32
+                ? vx_launch_fill_normal((float*)dst + first * cols, count, stream, coef, 0.0f, st)
+                : vx_launch_fill_normal_f16((uint16_t*)dst + first * cols, count, stream, coef, 0.0f, st);
     };
     auto vec = [&](int kind, uint32_t layer, float cf, float mean) {
         if (e != hipSuccess) return;
@@ -1430,6 +1492,8 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
     // the arena's model stays alive until the end of the run; the file is closed once loaded
     struct GgufCloser { VeloxHipGguf*& g; ~GgufCloser() { velox_hip_gguf_close(g); } } gguf_closer{gguf};
     if (opt->num_layers && !gguf) cfg.num_layers = opt->num_layers;
+    if (opt->unquantized > 2 || (opt->unquantized && gguf)) return VELOX_HIP_EINVAL;
+    if (opt->unquantized) cfg.quant_mode = opt->unquantized == 1 ? VELOX_QUANT_F32 : VELOX_QUANT_F16;
     const uint32_t B = opt->batch > 1 ? opt->batch : 1u;
     if (B > 32 || (B > 1 && opt->prompt_tokens)) return VELOX_HIP_EINVAL;
     if (B > 1) cfg.max_batch = B;

@@ -880,6 +880,15 @@ __global__ __launch_bounds__(kWG) void vx_embed_kernel(VxMat m, const VeloxDecod
     const uint32_t token = state ? state->token : fixed_token;
     const uint32_t b = blockIdx.x * kWG + threadIdx.x, nb = m.k >> 5;
     if (b >= nb || token >= m.n) return;  // src/codegen.rs:2386-2390 guard
+    if (m.fmt != VX_FMT_Q4) {  // unquantized rows (src/codegen.rs:1108-1117 and its fp16 twin)
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const size_t i = (size_t)token * m.k + b * 32u + (uint32_t)e;
+            h[b * 32 + e] = m.fmt == VX_FMT_F32 ? ((const float*)m.codes)[i]
+                                                : __half2float(__ushort_as_half(((const uint16_t*)m.codes)[i]));
+        }
+        return;
+    }
     const uint32_t phys = vx_phys_row(m, token, 0);
     const uint32_t R = 64u / m.s;
     const size_t off = ((size_t)(phys / R) * m.n_iter + b / m.s) * 64u + (phys % R) * m.s + b % m.s;
@@ -931,6 +940,13 @@ __global__ __launch_bounds__(kWG) void vx_fill_normal_kernel(float* out, uint64_
                                                              float mean) {
     for (uint64_t i = (uint64_t)blockIdx.x * kWG + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kWG)
         out[i] = vx_normal_value(stream, i, coef, mean);
+}
+
+// The same values rounded to fp16 (to nearest even): the synthetic weights of an fp16-row model.
+__global__ __launch_bounds__(kWG) void vx_fill_normal_f16_kernel(uint16_t* out, uint64_t n, uint64_t stream, float coef,
+                                                                 float mean) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kWG + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kWG)
+        out[i] = vx_f32_to_f16_bits(vx_normal_value(stream, i, coef, mean));
 }
 
 __global__ __launch_bounds__(kWG) void vx_fill_kv_kernel(uint16_t* base, uint32_t hkv, uint32_t s_cap, uint32_t d,
@@ -1148,6 +1164,7 @@ hipError_t vx_attn_launch_t(const VxAttnArgs& a, hipStream_t st) {
 uint32_t vx_gemv_max_wgs_default() { return 512u; }
 
 hipError_t vx_launch_gemv(const VxMat& m, const VxGemvArgs& a0, int epi, uint32_t max_wgs, hipStream_t st) {
+    if (m.fmt != VX_FMT_Q4) return vx_launch_gemv_f(m, a0, epi, vx_gemv_wgs(m.n_tiles, max_wgs), st);
     VxGemvArgs a = a0;
     a.codes = m.codes;
     a.scales = m.scales;
@@ -1239,6 +1256,14 @@ hipError_t vx_launch_fill_normal(float* out, uint64_t n, uint64_t stream, float 
     if (n == 0) return hipSuccess;
     const size_t g = (n + kWG - 1) / kWG;
     hipLaunchKernelGGL(vx_fill_normal_kernel, dim3((unsigned)(g < 65536 ? g : 65536)), dim3(kWG), 0, st, out, n,
+                       stream, coef, mean);
+    return hipGetLastError();
+}
+
+hipError_t vx_launch_fill_normal_f16(uint16_t* out, uint64_t n, uint64_t stream, float coef, float mean, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    const size_t g = (n + kWG - 1) / kWG;
+    hipLaunchKernelGGL(vx_fill_normal_f16_kernel, dim3((unsigned)(g < 65536 ? g : 65536)), dim3(kWG), 0, st, out, n,
                        stream, coef, mean);
     return hipGetLastError();
 }

@@ -6,13 +6,15 @@
 //   velox_hip_runner [--model llama3_8b | --model-file MODEL.vlx] [--weights synthetic|FILE.gguf]
 //                    [--tokens 1,2,3 | --prompt-len N]
 //                    [--context-len N] [--steps N] [--warmup N] [--seed S] [--layers L]
-//                    [--prefill-chunk N] [--no-cuda-graph] [--verbose]
+//                    [--prefill-chunk N] [--unquantized f32|f16] [--no-cuda-graph] [--verbose]
 //
 // --model-file MODEL.vlx reads the model from its .vlx source (the `model` header, weight
 // declarations and `target hardware` budget; what `velox build MODEL.vlx` compiles into the
 // reference's emitted runner) instead of a builtin configuration.
 // --prefill-chunk N (2..64) prefills the prompt N positions per batched step (one weight pass per
 // chunk) instead of the reference's one decode step per prompt token; TTFT reports either.
+// --unquantized f32|f16 keeps the synthetic weights as fp32 / fp16 rows (the reference's quant_mode
+// 0 / 1, a build without --quantize) instead of Q4_0.
 //
 // Weights are the seeded synthetic Q4_0 model (`--weights synthetic`, what src/cli.rs:654 passes
 // through) or a GGUF Q4_0 checkpoint (`--weights FILE.gguf`, whose metadata then defines the model,
@@ -27,6 +29,7 @@
 
 int main(int argc, char** argv) {
     std::string model = "llama3_8b", weights, model_file;
+    uint32_t unquantized = 0;
     std::vector<uint32_t> tokens;
     uint32_t prompt_len = 128, steps = 32, warmup = 0, layers = 0, context_len = 0, prefill_chunk = 0;
     uint64_t seed = 1234;
@@ -39,6 +42,12 @@ int main(int argc, char** argv) {
         };
         if (!std::strcmp(a, "--model")) model = next();
         else if (!std::strcmp(a, "--model-file")) model_file = next();
+        else if (!std::strcmp(a, "--unquantized")) {
+            const char* f = next();
+            if (!std::strcmp(f, "f32")) unquantized = 1;
+            else if (!std::strcmp(f, "f16")) unquantized = 2;
+            else { std::fprintf(stderr, "Error: --unquantized takes f32 or f16\n"); return 1; }
+        }
         else if (!std::strcmp(a, "--tokens")) {
             std::string s = next();
             size_t p = 0;
@@ -104,6 +113,7 @@ int main(int argc, char** argv) {
     std::memset(&opt, 0, sizeof(opt));
     opt.model = model.c_str();
     opt.model_file = model_file.empty() ? nullptr : model_file.c_str();
+    opt.unquantized = unquantized;
     opt.prompt_len = prompt_len;
     opt.warmup = warmup;
     // the first generated token comes from the prefill; steps-1 decode steps are timed

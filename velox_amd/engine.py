@@ -38,9 +38,10 @@ def vlx_config(path: str, max_seq_len: int = 0) -> tuple[L.ModelConfig, L.VlxTar
 
 
 def make_config(model, max_seq_len: int = 0, num_layers: int = 0, attn_splits: int = 0,
-                max_batch: int = 0, prefill_chunk: int = 0) -> L.ModelConfig:
+                max_batch: int = 0, prefill_chunk: int = 0, quant_mode: int | None = None) -> L.ModelConfig:
     """A builtin config by name, a GGUF file (path ending in .gguf), a .vlx model source (path ending
-    in .vlx, read by velox_hip_vlx_load), or a dict of ModelConfig fields (custom shapes for tests)."""
+    in .vlx, read by velox_hip_vlx_load), or a dict of ModelConfig fields (custom shapes for tests).
+    `quant_mode` overrides the weight format (L.QUANT_F32 / L.QUANT_F16 rows, L.QUANT_GGML_Q4_0)."""
     if isinstance(model, str) and model.endswith(".gguf"):
         cfg = gguf_config(model, max_seq_len)
     elif isinstance(model, str) and model.endswith(".vlx"):
@@ -64,15 +65,17 @@ def make_config(model, max_seq_len: int = 0, num_layers: int = 0, attn_splits: i
         cfg.max_batch = max_batch
     if prefill_chunk:
         cfg.prefill_chunk = prefill_chunk
+    if quant_mode is not None:
+        cfg.quant_mode = quant_mode
     return cfg
 
 
 class HipDecodeEngine:
     def __init__(self, model, seed: int = 0, sigma: float = 0.02, norm_sigma: float = 0.0,
                  max_seq_len: int = 0, num_layers: int = 0, attn_splits: int = 0, synthesize: bool = True,
-                 max_batch: int = 0, prefill_chunk: int = 0):
+                 max_batch: int = 0, prefill_chunk: int = 0, quant_mode: int | None = None):
         self.lib = L.load()
-        self.cfg = make_config(model, max_seq_len, num_layers, attn_splits, max_batch, prefill_chunk)
+        self.cfg = make_config(model, max_seq_len, num_layers, attn_splits, max_batch, prefill_chunk, quant_mode)
         self._model = C.c_void_p()
         L.check(self.lib.velox_hip_model_create(C.byref(self.cfg), C.byref(self._model)), "model_create")
         self.arena = L.Arena()
@@ -253,13 +256,14 @@ def run(model: str = "llama3_8b", prompt_len: int = 128, warmup: int = 5, steps:
         sigma: float = 0.02, norm_sigma: float = 0.0, use_graph: bool = True, num_layers: int = 0,
         max_seq_len: int = 0, max_tokens: int = 1024, kernel_passes: int = 0,
         prompt: list[int] | None = None, context_len: int = 0, batch: int = 1,
-        prefill_chunk: int = 0, model_file: str | None = None) -> tuple[dict, list[int]]:
+        prefill_chunk: int = 0, model_file: str | None = None, unquantized: int = 0) -> tuple[dict, list[int]]:
     """The C++ runner flow (velox_hip_run): synthesize, capture, prefill, timed decode. `prompt`
     replaces the seeded random prompt of `prompt_len` ids; `context_len` > 0 starts from a seeded
     context of that many positions already in the KV cache (then prompt_len must be 1). Returned
     tokens are ring entries, ring[p] = argmax after position p, for the last positions run.
     `prefill_chunk` > 1 prefills the prompt as batched chunks of that many positions. `model_file`
-    reads the model from a .vlx source instead of the builtin `model`."""
+    reads the model from a .vlx source instead of the builtin `model`. `unquantized` 1 / 2 keeps the
+    weights as fp32 / fp16 rows (the reference's quant_mode 0 / 1) instead of GGML Q4_0."""
     lib = L.load()
     ptoks = None
     if prompt is not None:
@@ -267,7 +271,7 @@ def run(model: str = "llama3_8b", prompt_len: int = 128, warmup: int = 5, steps:
         ptoks = (C.c_uint32 * prompt_len)(*prompt)
     opt = L.RunOptions(model.encode(), max_seq_len, prompt_len, warmup, steps, seed, sigma, norm_sigma,
                        int(use_graph), num_layers, kernel_passes, 0, ptoks, context_len, batch, None,
-                       prefill_chunk, model_file.encode() if model_file else None)
+                       prefill_chunk, model_file.encode() if model_file else None, unquantized)
     rep = L.RunReport()
     toks = (C.c_uint32 * max_tokens)()
     rc = lib.velox_hip_run(C.byref(opt), toks, max_tokens, C.byref(rep))
