@@ -407,27 +407,33 @@ __global__ __launch_bounds__(1024) void vx_mla_prep_kernel(VxMlaPrepArgs a) {
     }
 }
 
-template <int LR, int DR, int W>
-constexpr size_t vx_mla_attn_lds() {
-    return (size_t)32 * (LR + DR + 8) * 2 + (size_t)LR * 40 * 2 + (size_t)(LR / 8) * 32;
+template <int LR, int DR, int W, int LS>
+constexpr size_t vx_mla_attn_lds() {  // K rows, dimension-major V, the W head groups' q operands
+    return (size_t)32 * (LR + DR + 8) * 2 + (size_t)LR * 40 * 2 + (size_t)(LR / 8) * 32 +
+           (size_t)W * ((LR + DR) / 32) * 64 * 16;
 }
 
 // Absorbed MLA attention of one (split, sequence, group of 16 W heads). The split's positions go
 // through LDS in chunks of 32: the bf16 latent rows are converted to fp16 once, as rows for the
-// scores and dimension-major for P.V. Each wave owns 16 heads: scores S^T[pos][head] = [c | kr] .
-// [q_abs | rope(q_rope)] on v_mfma_f32_16x16x32_f16 (the q operands stay in registers), a log2-
-// domain online softmax per head, O[head][latent] += P c on MFMA. Writes the split's (m, l, o).
-template <int LR, int DR, int W>
-__global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a) {
+// scores and dimension-major for P.V. LS waves share each 16 heads: every one of them computes the
+// heads' scores S^T[pos][head] = [c | kr] . [q_abs | rope(q_rope)] on v_mfma_f32_16x16x32_f16 (the q
+// operands, built once, wait in LDS) and the log2-domain online softmax, and accumulates its 1 / LS
+// of the latent dimensions of O[head][latent] += P c on MFMA (fewer registers: two waves per SIMD).
+// Writes the split's (m, l, o).
+template <int LR, int DR, int W, int LS>
+__global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a) {
     if ((a.active_mask & 1ULL) == 0ULL) return;
-    constexpr int R = LR + DR, NCK = R / 32, NB = LR / 16, KP = R + 8, VP = 40, NT = 64 * W;
+    constexpr int R = LR + DR, NCK = R / 32, NB = LR / 16, NBW = NB / LS, KP = R + 8, VP = 40, NT = 64 * W * LS;
+    static_assert(NB % LS == 0, "whole 16-dimension blocks per wave");
     extern __shared__ __align__(16) unsigned char vm_smem[];
     _Float16* k_s = (_Float16*)vm_smem;        // [32][KP]: rows [c | kr]
     _Float16* v_s = k_s + 32 * KP;             // latent dim r at voff(r); slot 8j + e holds vrow(j, e)
+    vm_h8* q_s = (vm_h8*)(vm_smem + (size_t)32 * KP * 2 + (size_t)LR * 40 * 2 + (size_t)(LR / 8) * 32);  // [W][NCK][64]
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hg = wave / LS, ls = wave % LS;  // head group of the workgroup, latent part
     const int col = lane & 15, grp = lane >> 4;
     const uint32_t sp = blockIdx.x, b = blockIdx.y;
-    const uint32_t head = (blockIdx.z * W + (uint32_t)wave) * 16u + (uint32_t)col;
+    const uint32_t head = (blockIdx.z * W + (uint32_t)hg) * 16u + (uint32_t)col;
     const uint64_t step = a.states[b].step;
     const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;
     const uint32_t len = pos + 1u;
@@ -440,8 +446,9 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
     // units: slot group j (positions 4j..4j+3 and 16+4j..16+4j+3) x 8 dimensions, 8 row loads each;
     // RoPE units: one row x 8 dimensions (the unit -> (j, db) map is below) ----
     constexpr int NVU = (4 * (LR / 8) + NT - 1) / NT, NRU = (32 * (DR / 8) + NT - 1) / NT;
-    // two register sets: chunk i + 2 is loaded while chunk i is computed
-    uint4 kv[2][NVU][8], kq[2][NRU];
+    // one register set: chunk i + 1 is loaded while chunk i is computed (a second set, two chunks
+    // ahead, needs 255 registers and measured slower: 73.9 against 70.3 us at 16 sequences)
+    uint4 kv[NVU][8], kq[NRU];
     auto vrow = [](int j, int e) { return (uint32_t)(e < 4 ? 4 * j + e : 16 + 4 * j + (e - 4)); };
     // unit un -> (slot group j, 8-dimension block db): 8 consecutive lanes take 2 slot groups x 4
     // blocks, so their 16-byte stores into k_s hit 8 different 16-byte bank groups; voff shifts
@@ -450,57 +457,68 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
     auto unit_j = [](int un) { return (un & 1) | (((un >> 3) & 1) << 1); };
     auto unit_db = [](int un) { return ((un >> 1) & 3) | ((un >> 4) << 2); };
     auto voff = [](int r) { return r * VP + 16 * (r >> 3); };
-    auto load_chunk = [&](auto SET, uint32_t cb) {
-        constexpr int S = decltype(SET)::value;
+    auto load_chunk = [&](uint32_t cb) {
 #pragma unroll
         for (int u = 0; u < NVU; ++u) {
             const int un = min(tid + u * NT, 4 * (LR / 8) - 1), j = unit_j(un), db = unit_db(un);
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                kv[S][u][e] = *(const uint4*)(cb_base + (size_t)min(cb + vrow(j, e), pos) * R + 8 * db);
+                kv[u][e] = *(const uint4*)(cb_base + (size_t)min(cb + vrow(j, e), pos) * R + 8 * db);
         }
 #pragma unroll
         for (int u = 0; u < NRU; ++u) {
             const int un = min(tid + u * NT, 32 * (DR / 8) - 1), r = un / (DR / 8), db = LR / 8 + un % (DR / 8);
-            kq[S][u] = *(const uint4*)(cb_base + (size_t)min(cb + (uint32_t)r, pos) * R + 8 * db);
+            kq[u] = *(const uint4*)(cb_base + (size_t)min(cb + (uint32_t)r, pos) * R + 8 * db);
         }
     };
-    using Set0 = std::integral_constant<int, 0>;
-    using Set1 = std::integral_constant<int, 1>;
-    load_chunk(Set0{}, t0 < len ? t0 : pos & ~31u);
-    load_chunk(Set1{}, t0 + 32u < len ? t0 + 32u : pos & ~31u);
+    load_chunk(t0 < len ? t0 : pos & ~31u);
 
-    // ---- q operands of head col: latent dims scaled, the RoPE part rotated, as fp16 ----
-    vm_h8 qop[NCK];
+    // ---- q operands of head col: latent dims scaled, the RoPE part rotated, as fp16; each lane's 8
+    // consecutive dimensions of a 32-dimension chunk come as vector loads (the RoPE part's 8 stay
+    // within one half of the rotation). The head group's latent part ls builds chunks ls, ls + LS,
+    // ... into LDS (visible after the first chunk's barrier) ----
     {
         const float* qa = a.qabs + ((size_t)b * a.nh + head) * LR;
         const float* qr = a.q32 + (size_t)b * a.nh * a.dq + (size_t)head * a.dq + a.dn;
         const float2* rp = a.rope + (size_t)pos * (DR / 2);
 #pragma unroll
-        for (int c = 0; c < NCK; ++c) {
+        for (int c = ls; c < NCK; c += LS) {
+            const int d0 = 32 * c + 8 * grp;
+            float v[8];
+            if (d0 < LR) {
+                const float4 x0 = *(const float4*)(qa + d0), x1 = *(const float4*)(qa + d0 + 4);
+                v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+                v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+            } else {
+                constexpr int h2 = DR / 2;
+                const int r0 = d0 - LR, i0 = r0 % h2;
+                float x1[8], x2[8];
+                float2 cs[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int d = 32 * c + 8 * grp + e;
-                float v;
-                if (d < LR) {
-                    v = qa[d];
-                } else {
-                    const int r = d - LR, h2 = DR / 2;
-                    const float2 o = vm_rope_pair(qr[r % h2], qr[r % h2 + h2], rp[r % h2]);
-                    v = r < h2 ? o.x : o.y;
+                for (int e = 0; e < 8; ++e) {
+                    x1[e] = qr[i0 + e];
+                    x2[e] = qr[i0 + e + h2];
+                    cs[e] = rp[i0 + e];
                 }
-                qop[c][e] = (_Float16)(v * a.qscale);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float2 o = vm_rope_pair(x1[e], x2[e], cs[e]);
+                    v[e] = r0 < h2 ? o.x : o.y;
+                }
             }
+            vm_h8 q;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) q[e] = (_Float16)(v[e] * a.qscale);
+            q_s[(hg * NCK + c) * 64 + lane] = q;
         }
     }
 
     float m_run = -INFINITY, l_run = 0.0f;
-    vm_f4 o_acc[NB];
+    vm_f4 o_acc[NBW];  // latent blocks ls NBW .. + NBW - 1
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) o_acc[nb] = vm_f4{0.f, 0.f, 0.f, 0.f};
+    for (int nb = 0; nb < NBW; ++nb) o_acc[nb] = vm_f4{0.f, 0.f, 0.f, 0.f};
 
-    auto chunk_step = [&](auto SET, uint32_t ci) {
-        constexpr int S = decltype(SET)::value;
+    auto chunk_step = [&](uint32_t ci) {
         const uint32_t cb = t0 + 32u * ci;
         __syncthreads();  // the previous chunk is consumed
         auto to_h8 = [](const uint4& q) {
@@ -521,7 +539,7 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
                 vm_h8 hv[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    hv[e] = to_h8(kv[S][u][e]);
+                    hv[e] = to_h8(kv[u][e]);
                     *(vm_h8*)(k_s + vrow(j, e) * KP + 8 * db) = hv[e];
                 }
 #pragma unroll
@@ -538,20 +556,20 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
             const int un = tid + u * NT;
             if (un < 32 * (DR / 8)) {
                 const int r = un / (DR / 8), db = LR / 8 + un % (DR / 8);
-                *(vm_h8*)(k_s + r * KP + 8 * db) = to_h8(kq[S][u]);
+                *(vm_h8*)(k_s + r * KP + 8 * db) = to_h8(kq[u]);
             }
         }
         __syncthreads();
-        if (ci + 2u < n_chunks) load_chunk(SET, cb + 64u);
+        if (ci + 1u < n_chunks) load_chunk(cb + 32u);
         // scores: sc[bb][i] = S[position cb + 16 bb + 4 grp + i][head col]
-        vm_f4 sc[2];
+        vm_f4 sc[2] = {vm_f4{0.f, 0.f, 0.f, 0.f}, vm_f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-        for (int bb = 0; bb < 2; ++bb) {
-            sc[bb] = vm_f4{0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < NCK; ++c) {
+            const vm_h8 qop = q_s[(hg * NCK + c) * 64 + lane];
 #pragma unroll
-            for (int c = 0; c < NCK; ++c) {
+            for (int bb = 0; bb < 2; ++bb) {
                 const vm_h8 kop = *(const vm_h8*)(k_s + (16 * bb + col) * KP + 32 * c + 8 * grp);
-                sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[c], sc[bb], 0, 0, 0);
+                sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop, sc[bb], 0, 0, 0);
             }
         }
         float pr[8];
@@ -568,6 +586,9 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float m_new = fmaxf(m_run, mx);
         const float alpha = m_run == -INFINITY ? 0.0f : vm_exp2(m_run - m_new);
+        // the accumulators change only where a running maximum grew (alpha < 1); before the first
+        // finite maximum they are still zero
+        const bool grew = m_run != -INFINITY && m_new != m_run;
         float lt = 0.0f;
         vm_h8 pop;
 #pragma unroll
@@ -578,37 +599,37 @@ __global__ __launch_bounds__(64 * W, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a)
         }
         l_run = l_run * alpha + lt;
         m_run = m_new;
+        if (__any(grew)) {  // wave-uniform
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float ai = __shfl(alpha, 4 * grp + i);
+            for (int i = 0; i < 4; ++i) {
+                const float ai = __shfl(alpha, 4 * grp + i);
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) o_acc[nb][i] *= ai;
+                for (int nb = 0; nb < NBW; ++nb) o_acc[nb][i] *= ai;
+            }
         }
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const vm_h8 vop = *(const vm_h8*)(v_s + voff(16 * nb + col) + 8 * grp);
+        for (int nb = 0; nb < NBW; ++nb) {
+            const vm_h8 vop = *(const vm_h8*)(v_s + voff(16 * (ls * NBW + nb) + col) + 8 * grp);
             o_acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, vop, o_acc[nb], 0, 0, 0);
         }
     };
-    for (uint32_t ci = 0; ci < n_chunks; ci += 2u) {
-        chunk_step(Set0{}, ci);
-        if (ci + 1u < n_chunks) chunk_step(Set1{}, ci + 1u);
-    }
+    for (uint32_t ci = 0; ci < n_chunks; ++ci) chunk_step(ci);
 
-    // ---- the split's partial: o_acc[nb][i] is head 4 grp + i of the wave, latent dim 16 nb + col ----
+    // ---- the split's partial: o_acc[nb][i] is head 4 grp + i of the wave, latent dim
+    // 16 (ls NBW + nb) + col ----
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
-    const uint32_t hbase = (blockIdx.z * W + (uint32_t)wave) * 16u;
+    const uint32_t hbase = (blockIdx.z * W + (uint32_t)hg) * 16u;
     const size_t bh = (size_t)b * a.nh;
-    if (lane < 16) {
+    if (lane < 16 && ls == 0) {
         a.part_ml[((bh + hbase + lane) * a.splits + sp) * 2] = m_run;
         a.part_ml[((bh + hbase + lane) * a.splits + sp) * 2 + 1] = l_run;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        float* po = a.part_o + ((bh + hbase + 4u * grp + i) * a.splits + sp) * LR + col;
+        float* po = a.part_o + ((bh + hbase + 4u * grp + i) * a.splits + sp) * LR + 16 * ls * NBW + col;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) po[16 * nb] = o_acc[nb][i];
+        for (int nb = 0; nb < NBW; ++nb) po[16 * nb] = o_acc[nb][i];
     }
 }
 
@@ -669,28 +690,28 @@ hipError_t vx_launch_mla_prep(const VxMlaPrepArgs& a, uint32_t batch, hipStream_
     return hipGetLastError();
 }
 
-template <int LR, int DR, int W>
+template <int LR, int DR, int W, int LS>
 hipError_t vx_mla_attn_launch_t(const VxMlaAttnArgs& a, uint32_t batch, hipStream_t st) {
-    constexpr size_t lds = vx_mla_attn_lds<LR, DR, W>();
+    constexpr size_t lds = vx_mla_attn_lds<LR, DR, W, LS>();
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)vx_mla_attn_kernel<LR, DR, W>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds) != hipSuccess) {
+        if (hipFuncSetAttribute((const void*)vx_mla_attn_kernel<LR, DR, W, LS>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
             (void)hipGetLastError();
             return hipErrorInvalidValue;
         }
         attr_set = true;
     }
-    hipLaunchKernelGGL((vx_mla_attn_kernel<LR, DR, W>), dim3(a.splits, batch, a.nh / (16u * W)), dim3(64 * W), lds, st,
-                       a);
+    hipLaunchKernelGGL((vx_mla_attn_kernel<LR, DR, W, LS>), dim3(a.splits, batch, a.nh / (16u * W)),
+                       dim3(64 * W * LS), lds, st, a);
     return hipGetLastError();
 }
 
 hipError_t vx_launch_mla_attn(const VxMlaAttnArgs& a, uint32_t lr, uint32_t dr, uint32_t batch, hipStream_t st) {
     if (a.splits == 0 || a.splits > 64 || (a.s_cap & 31u) || a.s_cap < a.s_max || a.nh % 16u || dr != 64u)
         return hipErrorInvalidValue;
-    if (lr == 512 && a.nh % 64u == 0) return vx_mla_attn_launch_t<512, 64, 4>(a, batch, st);
-    if (lr == 128 && a.nh % 16u == 0) return vx_mla_attn_launch_t<128, 64, 1>(a, batch, st);
+    if (lr == 512 && a.nh % 64u == 0) return vx_mla_attn_launch_t<512, 64, 4, 2>(a, batch, st);
+    if (lr == 128 && a.nh % 16u == 0) return vx_mla_attn_launch_t<128, 64, 1, 2>(a, batch, st);
     return hipErrorInvalidValue;
 }
 
