@@ -111,6 +111,7 @@ def cpu_baseline(seed: int, tokens: int = 3) -> dict:
 # the same runner flow): (key, builtin model, seeded context, batch, warmup, timed steps).
 OTHER_CONFIGS = (
     ("config1_smollm_135m_fp32_b1", "smollm_135m", 0, 1, 5, 64),
+    ("config1_smollm_135m_group64_b1", "smollm_135m", 0, 1, 5, 64),
     ("config3_qwen2_5_7b_ctx2048_b1", "qwen2_5_7b", 2048, 1, 3, 30),
     ("config3_qwen2_5_7b_ctx2048_b8", "qwen2_5_7b", 2048, 8, 3, 20),
     ("config3_qwen2_5_7b_ctx2048_b32", "qwen2_5_7b", 2048, 32, 3, 20),
@@ -128,11 +129,14 @@ def other_configs(seed: int) -> dict:
     out = {}
     for key, model, ctx, batch, warmup, steps in OTHER_CONFIGS:
         t0 = time.perf_counter()
-        fp32 = "fp32" in key  # configuration 1: the reference's fp32 rows, a 32-token prompt
-        rep, _ = run(model, prompt_len=32 if fp32 else 1, warmup=warmup, steps=steps, seed=seed, use_graph=True,
-                     kernel_passes=0, context_len=ctx, batch=batch, unquantized=1 if fp32 else 0)
+        # configuration 1: the reference's fp32 weights, as fp32 rows or converted to its group-64
+        # format (its runner's --quantize q4_0), after a 32-token prompt
+        unq = 1 if "fp32" in key else 3 if "group64" in key else 0
+        cfg1 = unq != 0
+        rep, _ = run(model, prompt_len=32 if cfg1 else 1, warmup=warmup, steps=steps, seed=seed, use_graph=True,
+                     kernel_passes=0, context_len=ctx, batch=batch, unquantized=unq)
         out[key] = {"value": round(rep["tok_per_s"], 2), "unit": "tok/s", "batch": batch, "context_tokens": ctx,
-                    "timed_positions": ([32 + warmup, 31 + warmup + steps] if fp32 else
+                    "timed_positions": ([32 + warmup, 31 + warmup + steps] if cfg1 else
                                         [ctx + 1 + warmup, ctx + warmup + steps]),
                     "hbm_gbps": round(rep["hbm_gbps"], 1), "hbm_frac": round(rep["hbm_gbps"] / HBM_PEAK_GBPS, 4),
                     "bytes_per_step": int(rep["bytes_per_step"]), "ms_per_step": round(rep["decode_ms"] / steps, 5)}

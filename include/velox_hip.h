@@ -54,8 +54,9 @@ typedef struct VeloxHipModelConfig {
     float rms_norm_eps, rope_theta;
     uint32_t qkv_bias;          /* 1: q/k/v biases (Qwen) */
     uint32_t tied_lm_head;      /* 1: LM head reads the embedding table */
-    uint32_t quant_mode;        /* VELOX_QUANT_GGML_Q4_0; or VELOX_QUANT_F32 / _F16 rows (single-sequence
-                                   decode only: max_batch and prefill_chunk <= 1; widths <= 16384) */
+    uint32_t quant_mode;        /* VELOX_QUANT_GGML_Q4_0; or the reference's formats (single-sequence decode
+                                   only: max_batch and prefill_chunk <= 1): VELOX_QUANT_F32 / _F16 rows
+                                   (widths <= 16384), VELOX_QUANT_Q4_GROUP64 (widths multiples of 64) */
     uint32_t attn_splits;       /* split-K partitions over the sequence (<= 64); 0 = automatic */
     uint64_t vram_budget_bytes; /* 0 = 288 GB of HBM3E */
     uint32_t max_batch;         /* sequences of the batched decode step (<= 32; 0 or 1 = single);
@@ -155,8 +156,10 @@ const VeloxHipModel* velox_hip_arena_model(const VeloxHipArena* a);
 /* ---- loaders (velox_cuda_runner.cu:154-199 stream_tensor_converted) ----
  * q4_0: host GGML Q4_0 blocks, row-major [rows][in/32] x 18 B, for a matrix kind of `layer`.
  * rows: host fp32 (quant_mode VELOX_QUANT_F32) or fp16 (VELOX_QUANT_F16) rows [rows][in] of a
- *   matrix kind, stored as the reference's weight arena holds them (src/codegen.rs:1024-1028);
- *   EINVAL on a Q4_0 arena, as q4_0 is on a row arena.
+ *   matrix kind, stored as the reference's weight arena holds them (src/codegen.rs:1024-1028); or
+ *   host fp32 rows of a VELOX_QUANT_Q4_GROUP64 arena, quantized on the device by the reference's
+ *   group-64 rule (velox_cuda_runner.cu:174-197, src/codegen.rs:2337-2370) into the tiled layout;
+ *   EINVAL on a Q4_0 arena, as q4_0 is on any other arena.
  * f32: host fp32 vector (norm gains, biases). All upload (and repack) on `stream`. */
 int velox_hip_load_q4_0(VeloxHipArena* a, int kind, uint32_t layer, const void* blocks, uint64_t nbytes,
                         hipStream_t stream);
@@ -165,7 +168,7 @@ int velox_hip_load_rows(VeloxHipArena* a, int kind, uint32_t layer, const void* 
 int velox_hip_load_f32(VeloxHipArena* a, int kind, uint32_t layer, const float* data, uint64_t count,
                        hipStream_t stream);
 /* Synthesizes the whole seeded model on the device (linear weights N(0,sigma) quantized to Q4_0,
- * or as fp32 / fp16 rows for those quant_modes; norm gains 1 or N(1,norm_sigma), biases
+ * as fp32 / fp16 rows, or quantized to group-64, per quant_mode; norm gains 1 or N(1,norm_sigma), biases
  * N(0,sigma)), bit-identical to the oracle's recipe. */
 int velox_hip_synthesize_model(VeloxHipArena* a, uint64_t seed, float sigma, float norm_sigma,
                                hipStream_t stream);
@@ -268,7 +271,9 @@ typedef struct VeloxHipQ4Matrix {
     uint32_t s_lanes;      /* lanes per row: 4, 8, 16, 32 or 64 */
     uint32_t n_tiles, n_iter;
     uint32_t paired;       /* 1: tiles interleave gate/up rows for the fused SwiGLU epilogue */
-    uint32_t reserved;
+    uint32_t format;       /* 0: GGML Q4_0 (slot = fp16 d, w = d (q - 8)); VELOX_QUANT_Q4_GROUP64: the
+                              reference's group-64 format (k % 64 == 0; the slot of block 2g holds the
+                              group's fp16 scale s, of block 2g + 1 its fp16 minimum m; w = fmaf(q, s, m)) */
 } VeloxHipQ4Matrix;
 
 /* Descriptor of a weight matrix inside an arena (kind VELOX_T_Q/K/V return the fused QKV matrix
@@ -285,10 +290,21 @@ int velox_hip_q4_layout(uint32_t n, uint32_t k, uint32_t s_lanes, uint32_t paire
  * 0 = gate rows, 1 = up rows). Zero padding is the caller's (the arena loaders clear it). */
 int velox_hip_q4_0_repack(const void* d_blocks, uint32_t rows, uint32_t row0, uint32_t pair_part,
                           const VeloxHipQ4Matrix* m, hipStream_t stream);
-/* Tiled layout -> dense fp32 [n][k] (paired: logical rows gate 0..n/2-1 then up). Bit-exact d*(q-8). */
+/* Tiled layout -> dense fp32 [n][k] (paired: logical rows gate 0..n/2-1 then up). Bit-exact d*(q-8)
+ * (format 0) or fmaf(q, s, m) (group-64). */
 int velox_hip_q4_0_dequant(const VeloxHipQ4Matrix* m, float* d_out, hipStream_t stream);
 /* fp32 [rows][k] -> GGML Q4_0 blocks, the GGML rounding rule restated (bit-exact with the oracle). */
 int velox_hip_q4_0_quantize(const float* d_x, uint32_t rows, uint32_t k, void* d_blocks, hipStream_t stream);
+/* The reference's group-64 quantizer, velox_cuda_quantize_q4_group64_kernel (src/codegen.rs:2337-2370):
+ * fp32 [n_groups][64] -> d_packed [n_groups][8] words (q0|q2<<4|q4<<8|q6<<12|q1<<16|q3<<20|q5<<24|q7<<28
+ * of elements 8w..8w+7) and d_scale_min [n_groups][2] fp16 (s, m), in the reference's own layout. */
+int velox_hip_g64_quantize(const float* d_x, uint64_t n_groups, uint32_t* d_packed, uint16_t* d_scale_min,
+                           hipStream_t stream);
+/* fp32 rows [rows][k] (device) -> group-64 codes of a tiled matrix (format VELOX_QUANT_Q4_GROUP64) at
+ * logical rows [row0, row0+rows) (paired: pair_part 0 = gate rows, 1 = up rows); the same codes and
+ * scales as velox_hip_g64_quantize. */
+int velox_hip_g64_pack(const float* d_rows, uint32_t rows, uint32_t row0, uint32_t pair_part,
+                       const VeloxHipQ4Matrix* m, hipStream_t stream);
 /* Seeded N(mean, sigma) fill identical to the oracle's vxo_fill_normal. */
 int velox_hip_fill_normal(float* d_out, uint64_t n, uint64_t seed, uint64_t tag, float sigma, float mean,
                           hipStream_t stream);
@@ -382,8 +398,10 @@ typedef struct VeloxHipRunOptions {
                                 instead of one decode step each */
     const char* model_file;  /* non-NULL: the model is read from this .vlx source (velox_hip_vlx_load),
                                 its target block setting the VRAM budget; `model` is then ignored */
-    uint32_t unquantized;    /* 0: GGML Q4_0 weights; 1 / 2: fp32 / fp16 rows (quant_mode 0 / 1, a build
-                                without --quantize, src/cli.rs:1214-1388), single sequence only */
+    uint32_t unquantized;    /* 0: GGML Q4_0 weights; else the reference's fp32 weights (single sequence
+                                only): 1 as fp32 rows (a build without --quantize, src/cli.rs:1214-1388),
+                                2 converted to fp16 rows (--quantize f16), 3 quantized to group-64
+                                (--quantize q4_0, velox_cuda_runner.cu:356-372) */
 } VeloxHipRunOptions;
 
 typedef struct VeloxHipRunReport {

@@ -27,7 +27,7 @@ class VxoConfig(C.Structure):
         ("num_layers", C.c_uint32), ("num_heads", C.c_uint32), ("num_kv_heads", C.c_uint32),
         ("head_dim", C.c_uint32), ("max_seq_len", C.c_uint32), ("rms_norm_eps", C.c_float),
         ("rope_theta", C.c_float), ("qkv_bias", C.c_uint32), ("tied_lm_head", C.c_uint32),
-        ("q4_0", C.c_uint32), ("kv_bf16", C.c_uint32), ("w_f16", C.c_uint32),
+        ("q4_0", C.c_uint32), ("kv_bf16", C.c_uint32), ("w_f16", C.c_uint32), ("w_g64", C.c_uint32),
     ]
 
 
@@ -170,6 +170,27 @@ def q4_0_dequant(blocks: np.ndarray, k: int) -> np.ndarray:
     return out
 
 
+def g64_quantize(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """The reference's group-64 codec over consecutive groups of 64 values: packed words
+    [n_groups][8] uint32 and (s, m) fp16 bits [n_groups][2]."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    ng = x.size // 64
+    packed = np.empty((ng, 8), np.uint32)
+    sm = np.empty((ng, 2), np.uint16)
+    lib().vxo_g64_quantize(fptr(x), ng, packed.ctypes.data_as(C.POINTER(C.c_uint32)),
+                           sm.ctypes.data_as(C.POINTER(C.c_uint16)))
+    return packed, sm
+
+
+def g64_dequant(packed: np.ndarray, sm: np.ndarray) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, np.uint32)
+    sm = np.ascontiguousarray(sm, np.uint16)
+    out = np.empty(packed.size * 8, np.float32)
+    lib().vxo_g64_dequant(packed.ctypes.data_as(C.POINTER(C.c_uint32)), sm.ctypes.data_as(C.POINTER(C.c_uint16)),
+                          packed.size // 8, fptr(out))
+    return out
+
+
 def rmsnorm(x, w, eps):
     x = np.ascontiguousarray(x, np.float32)
     w = np.ascontiguousarray(w, np.float32)
@@ -228,7 +249,7 @@ class Engine:
 
     def __init__(self, cfg: dict, seed: int, sigma: float = 0.02, norm_sigma: float = 0.0,
                  q4_0: bool = True, kv_bf16: bool = True, layers_to_build: int | None = None,
-                 threads: int = 1, w_f16: bool = False):
+                 threads: int = 1, w_f16: bool = False, w_g64: bool = False):
         self.cfg = dict(cfg)
         c = VxoConfig()
         c.vocab_size = cfg["vocab_size"]
@@ -246,6 +267,7 @@ class Engine:
         c.q4_0 = int(q4_0)
         c.kv_bf16 = int(kv_bf16)
         c.w_f16 = int(w_f16)
+        c.w_g64 = int(w_g64)
         self._c = c
         nl = cfg["num_layers"] if layers_to_build is None else layers_to_build
         self.layers = min(nl, cfg["num_layers"])

@@ -644,12 +644,24 @@ static void vxo_make_matrix(VxoTensor* t, const VxoConfig* c, uint64_t seed, uin
 #if defined(_OPENMP)
 #pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
 #endif
-        for (long r = 0; r < (long)rows; ++r)
+        for (long r = 0; r < (long)rows; ++r) {
+            float* row = dst + (uint64_t)r * cols;
             for (uint64_t k = 0; k < cols; ++k) {
                 const float v = vxo_normal(st, (uint64_t)r * cols + k, coef);
                 /* fp16 weights (the reference's quant_mode 1): the value rounded to fp16, exact in fp32 */
-                dst[(uint64_t)r * cols + k] = c->w_f16 ? vxo_f16_to_f32(vxo_f32_to_f16(v)) : v;
+                row[k] = c->w_f16 ? vxo_f16_to_f32(vxo_f32_to_f16(v)) : v;
             }
+            if (c->w_g64) {
+                /* group-64 weights (quant_mode 2): the values the reference's GEMV dequantizes,
+                 * fmaf(q, s, m), from its load-time quantizer */
+                uint32_t packed[8];
+                uint16_t sm[2];
+                for (uint64_t g = 0; g < cols / 64; ++g) {
+                    vxo_g64_quantize(row + g * 64, 1, packed, sm);
+                    vxo_g64_dequant(packed, sm, 1, row + g * 64);
+                }
+            }
+        }
     }
     (void)threads;
 }

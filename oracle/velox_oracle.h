@@ -115,6 +115,8 @@ typedef struct VxoConfig {
     uint32_t q4_0;         /* 1: linear weights + embedding are Q4_0 blocks; 0: fp32 */
     uint32_t kv_bf16;      /* 1: round K/V to bf16 when written to the cache */
     uint32_t w_f16;        /* 1 (with q4_0 = 0): linear weights and embedding rounded to fp16 (quant_mode 1) */
+    uint32_t w_g64;        /* 1 (with q4_0 = 0): linear weights and embedding through the reference's
+                              group-64 codec, quantized and dequantized (quant_mode 2) */
 } VxoConfig;
 
 typedef struct VxoEngine VxoEngine;

@@ -105,8 +105,34 @@ def test_float_row_plan_sizes():
             assert rc == -1, field
 
 
+def test_group64_plan_sizes():
+    """quant_mode 2 (the reference's group-64 format): the tiled layout of GGML Q4_0, the same bytes
+    per weight (16-byte codes and a 16-bit slot per 32 weights); single-sequence decode only, and
+    whole 64-weight groups along every row."""
+    lib = L.load()
+    base = make_config("smollm_135m", max_seq_len=64)
+    sizes = {}
+    for quant in (L.QUANT_GGML_Q4_0, L.QUANT_G64):
+        cfg = make_config("smollm_135m", max_seq_len=64)
+        cfg.quant_mode = quant
+        rc, m = _plan(cfg)
+        assert rc == 0
+        v = [C.c_uint64() for _ in range(5)]
+        lib.velox_hip_model_arena_bytes(m, *[C.byref(x) for x in v])
+        sizes[quant] = (v[0].value, v[1].value, lib.velox_hip_model_step_bytes(m, 0))
+        lib.velox_hip_model_destroy(m)
+    assert sizes[L.QUANT_GGML_Q4_0] == sizes[L.QUANT_G64]
+    for field, value in (("max_batch", 8), ("prefill_chunk", 16), ("intermediate_dim", 1568)):
+        cfg = make_config("smollm_135m", max_seq_len=64)
+        cfg.quant_mode = L.QUANT_G64
+        setattr(cfg, field, value)
+        rc, _ = _plan(cfg)
+        assert rc == -1, field
+    assert base.quant_mode == L.QUANT_GGML_Q4_0
+
+
 @pytest.mark.parametrize("field,value", [("head_dim", 96), ("num_kv_heads", 5), ("hidden_dim", 4100),
-                                         ("quant_mode", 2), ("num_layers", 0)])
+                                         ("quant_mode", 3), ("num_layers", 0)])
 def test_plan_rejects_unsupported_shapes(field, value):
     cfg = make_config("llama3_8b", max_seq_len=64)
     setattr(cfg, field, value)

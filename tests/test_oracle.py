@@ -258,6 +258,29 @@ def test_g64_reference_codec(oracle):
     np.testing.assert_allclose(out, x, atol=1e-4)  # the reference test's tolerance
 
 
+def test_g64_codec_picks_the_nearest_level(oracle):
+    """Random groups of every sign and scale: each value decodes to the level q s + m (q in 0..15)
+    nearest to it, brute-forced over all 16 levels in float64 (ties and fp32 rounding of the
+    quantizer's own arithmetic within 1e-5 s); a constant group has scale 0 and decodes exactly to
+    its value rounded to fp16."""
+    rng = np.random.default_rng(64)
+    groups = [rng.standard_normal(64) * sc + off for sc, off in ((0.02, 0.0), (1.0, 3.0), (1e-3, -0.5), (40.0, 0.0))]
+    x = np.concatenate(groups).astype(np.float32)
+    packed, sm = oracle.g64_quantize(x)
+    got = oracle.g64_dequant(packed, sm).astype(np.float64)
+    s = sm[:, 0].view(np.float16).astype(np.float64).repeat(64)
+    m = sm[:, 1].view(np.float16).astype(np.float64).repeat(64)
+    levels = m[:, None] + s[:, None] * np.arange(16)[None, :]
+    best = np.min(np.abs(levels - x[:, None]), axis=1)
+    assert np.all(np.abs(got - x) <= best + 1e-5 * s + 1e-12)
+    # the decoded values are the levels themselves (fmaf(q, s, m) within one fp32 rounding)
+    q = np.rint((got - m) / s)
+    assert np.all((q >= 0) & (q <= 15)) and np.allclose(got, m + q * s, rtol=2 ** -23, atol=0)
+    c = np.full(64, 0.3, np.float32)
+    packed, sm = oracle.g64_quantize(c)
+    assert sm[0, 0] == 0 and np.all(oracle.g64_dequant(packed, sm) == np.float32(np.float16(0.3)))
+
+
 # ---- synthetic recipe ---------------------------------------------------------------------------
 def test_rng_statistics_and_determinism(oracle):
     a = oracle.fill_normal(400000, 1, 2, 0.02)

@@ -13,7 +13,8 @@ ROOT = os.path.dirname(PKG)
 LIB_PATH = os.path.join(PKG, "lib", "libvelox_hip.so")
 HEADER = os.path.join(ROOT, "include", "velox_hip.h")
 
-QUANT_F32, QUANT_F16, QUANT_GGML_Q4_0 = 0, 1, 5  # quant_mode: the reference's fp32 / fp16 rows, GGML Q4_0
+# quant_mode: the reference's fp32 / fp16 rows and group-64 format, GGML Q4_0
+QUANT_F32, QUANT_F16, QUANT_G64, QUANT_GGML_Q4_0 = 0, 1, 2, 5
 GEMV_STORE, GEMV_RESIDUAL, GEMV_SWIGLU = 0, 1, 2
 EINVAL, ENOMEM, ESHAPE, ENOTLOADED = -1, -2, -3, -4
 T_EMBED, T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN = 1, 2, 3, 4, 5, 6, 7, 8
@@ -55,7 +56,7 @@ class Q4Matrix(C.Structure):
     _fields_ = [
         ("codes", C.c_void_p), ("scales", C.c_void_p), ("n", C.c_uint32), ("k", C.c_uint32),
         ("s_lanes", C.c_uint32), ("n_tiles", C.c_uint32), ("n_iter", C.c_uint32),
-        ("paired", C.c_uint32), ("reserved", C.c_uint32),
+        ("paired", C.c_uint32), ("format", C.c_uint32),
     ]
 
 
@@ -162,6 +163,8 @@ _SIGS = {
     "velox_hip_q4_0_repack": (_I, [_P, _U32, _U32, _U32, C.POINTER(Q4Matrix), _P]),
     "velox_hip_q4_0_dequant": (_I, [C.POINTER(Q4Matrix), _P, _P]),
     "velox_hip_q4_0_quantize": (_I, [_P, _U32, _U32, _P, _P]),
+    "velox_hip_g64_quantize": (_I, [_P, _U64, _P, _P, _P]),
+    "velox_hip_g64_pack": (_I, [_P, _U32, _U32, _U32, C.POINTER(Q4Matrix), _P]),
     "velox_hip_fill_normal": (_I, [_P, _U64, _U64, _U64, _F, _F, _P]),
     "velox_hip_gemv_q4_0": (_I, [C.POINTER(Q4Matrix), _P, _P, _F, _P, _P, _P, _I, _P]),
     "velox_hip_gemm_q4_0_batch": (_I, [C.POINTER(Q4Matrix), _P, _U32, _U32, _P, _P, _U32, _P, _U32, _I, _P]),

@@ -33,6 +33,11 @@ VX_HD uint32_t vx_uniform_u32(uint64_t stream, uint64_t idx, uint32_t n) {
     return (uint32_t)(((vx_hash(stream, idx) >> 32) * (uint64_t)n) >> 32);
 }
 inline float vx_normal_coef(float sigma) { return (float)((double)sigma / (131072.0 * 0.81649658092772603)); }
+// Value idx of a seeded N(mean, sigma) stream (coef = vx_normal_coef(sigma)), unfused.
+VX_HD float vx_normal_value(uint64_t stream, uint64_t idx, float coef, float mean) {
+#pragma clang fp contract(off)
+    return mean + (float)vx_normal_int(stream, idx) * coef;
+}
 VX_HD uint64_t vx_tag(uint32_t layer, uint32_t kind) { return (uint64_t)layer * 256ULL + kind; }
 #define VX_TAG_PROMPT 16u
 #define VX_TAG_KV_K 17u
@@ -91,10 +96,11 @@ VX_HD uint32_t vx_vslot(uint32_t r) { return 8u * ((r & 15u) >> 2) + 4u * (r >> 
 // ---------------------------------------------------------------------------------------------
 // Device-side views
 // ---------------------------------------------------------------------------------------------
-// Weight formats of a VxMat: GGML Q4_0 in the tiled layout, or the reference's unquantized rows
-// (quant_mode 0 fp32, 1 fp16), row-major [rows][k] (paired: n gate rows, then n up rows), n_tiles
-// = ceil(n / 4) tiles of 4 logical rows, no scales.
-enum { VX_FMT_Q4 = 0, VX_FMT_F32 = 1, VX_FMT_F16 = 2 };
+// Weight formats of a VxMat: GGML Q4_0 or the reference's group-64 format (quant_mode 2) in the
+// tiled layout, or the reference's unquantized rows (quant_mode 0 fp32, 1 fp16), row-major
+// [rows][k] (paired: n gate rows, then n up rows), n_tiles = ceil(n / 4) tiles of 4 logical rows,
+// no scales.
+enum { VX_FMT_Q4 = 0, VX_FMT_F32 = 1, VX_FMT_F16 = 2, VX_FMT_G64 = 3 };
 constexpr uint32_t kVxFloatMaxK = 16384;  // fp32 activations of a float-row GEMV in LDS
 
 struct VxMat {
@@ -244,6 +250,16 @@ hipError_t vx_launch_gemv(const VxMat& m, const VxGemvArgs& a, int epi, uint32_t
 // on `wgs` workgroups (vx_gemv_grid of the matrix's tiles).
 hipError_t vx_launch_gemv_f(const VxMat& m, const VxGemvArgs& a, int epi, uint32_t wgs, hipStream_t st);
 hipError_t vx_launch_attention(const VxAttnArgs& a, uint32_t d, hipStream_t st);
+// vx_gemv_g64.hip: the reference's group-64 format (quant_mode 2) in the tiled layout -- the GEMV
+// that vx_launch_gemv runs for VX_FMT_G64 matrices, fp32 rows (device) or seeded weights converted
+// into rows [row0, row0 + rows) of part pair_part, and the reference's own packed output layout
+hipError_t vx_launch_gemv_g64(const VxMat& m, const VxGemvArgs& a, int epi, uint32_t max_wgs, hipStream_t st);
+hipError_t vx_launch_g64_from_rows(const float* rows_dev, uint32_t rows, uint32_t row0, uint32_t pair_part,
+                                   const VxMat& m, hipStream_t st);
+hipError_t vx_launch_synth_g64(const VxMat& m, uint32_t rows, uint32_t row0, uint32_t pair_part, uint64_t stream,
+                               float coef, hipStream_t st);
+hipError_t vx_launch_g64_quantize_ref(const float* src, uint64_t n_groups, uint32_t* packed, uint16_t* scale_min,
+                                      hipStream_t st);
 // vx_batch.hip
 // Batched prefill (vx_batch.hip): row r of a chunk is position p0 + r of the one sequence.
 hipError_t vx_launch_prefill_rows(VeloxDecodeState* rows, uint32_t n_rows, uint64_t p0, const uint32_t* prompt,

@@ -140,16 +140,23 @@ uint32_t vx_choose_s(uint32_t nb) {
     return best;
 }
 
-// The weight format of a quant_mode (GGML Q4_0 in the tiled layout, or the reference's fp32 / fp16
-// rows).
+// The weight format of a quant_mode (GGML Q4_0 or the reference's group-64 format in the tiled
+// layout, or the reference's fp32 / fp16 rows).
 uint32_t vx_fmt_of(uint32_t quant_mode) {
-    return quant_mode == VELOX_QUANT_F32 ? VX_FMT_F32 : quant_mode == VELOX_QUANT_F16 ? VX_FMT_F16 : VX_FMT_Q4;
+    switch (quant_mode) {
+        case VELOX_QUANT_F32: return VX_FMT_F32;
+        case VELOX_QUANT_F16: return VX_FMT_F16;
+        case VELOX_QUANT_Q4_GROUP64: return VX_FMT_G64;
+        default: return VX_FMT_Q4;
+    }
 }
+
+bool vx_fmt_tiled(uint32_t fmt) { return fmt == VX_FMT_Q4 || fmt == VX_FMT_G64; }
 
 void vx_mat_layout(uint32_t n, uint32_t k, uint32_t s, uint32_t paired, VxMatPlan& p, uint32_t fmt = VX_FMT_Q4) {
     const uint32_t nb = k / 32;
     p.fmt = fmt;
-    if (fmt != VX_FMT_Q4) {  // row-major [rows][k] (paired: n gate rows, then n up rows), tiles of 4 rows
+    if (!vx_fmt_tiled(fmt)) {  // row-major [rows][k] (paired: n gate rows, then n up rows), tiles of 4 rows
         p.n = n;
         p.k = k;
         p.s = 0;
@@ -238,7 +245,9 @@ VxMat vx_view_public(const VeloxHipQ4Matrix* q) {
     m.n_tiles = q->n_tiles;
     m.n_iter = q->n_iter;
     m.paired = q->paired;
-    m.fmt = VX_FMT_Q4;
+    // format 0: GGML Q4_0 blocks; VELOX_QUANT_Q4_GROUP64: group-64 pairs (anything else is refused
+    // by the launchers as an unknown format)
+    m.fmt = q->format == 0 ? VX_FMT_Q4 : q->format == VELOX_QUANT_Q4_GROUP64 ? VX_FMT_G64 : 0xFFFFFFFFu;
     return m;
 }
 
@@ -251,16 +260,20 @@ bool vx_shape_ok(const VeloxHipModelConfig& c) {
     if (c.head_dim == 64 && !(G == 1 || G == 2 || G == 3 || G == 4 || G == 8)) return false;
     if (c.head_dim == 128 && !(G == 1 || G == 2 || G == 4 || G == 7 || G == 8)) return false;
     if (((uint64_t)c.num_heads * c.head_dim) % 32) return false;
-    if (c.quant_mode != VELOX_QUANT_GGML_Q4_0 && c.quant_mode != VELOX_QUANT_F32 && c.quant_mode != VELOX_QUANT_F16)
+    if (c.quant_mode != VELOX_QUANT_GGML_Q4_0 && c.quant_mode != VELOX_QUANT_F32 && c.quant_mode != VELOX_QUANT_F16 &&
+        c.quant_mode != VELOX_QUANT_Q4_GROUP64)
         return false;
-    if (c.quant_mode != VELOX_QUANT_GGML_Q4_0) {
-        // fp32 / fp16 rows: the single-sequence decode only (the batched GEMMs read Q4_0), and
+    // the reference's formats run the single-sequence decode only (the batched GEMMs read Q4_0)
+    if (c.quant_mode != VELOX_QUANT_GGML_Q4_0 && (c.max_batch > 1 || c.prefill_chunk > 1)) return false;
+    if (c.quant_mode == VELOX_QUANT_F32 || c.quant_mode == VELOX_QUANT_F16) {
         // fp32 activations of a row in LDS
-        if (c.max_batch > 1 || c.prefill_chunk > 1) return false;
         if (c.hidden_dim > kVxFloatMaxK || c.intermediate_dim > kVxFloatMaxK ||
             (uint64_t)c.num_heads * c.head_dim > kVxFloatMaxK)
             return false;
     }
+    if (c.quant_mode == VELOX_QUANT_Q4_GROUP64 &&
+        (c.hidden_dim % 64 || c.intermediate_dim % 64 || ((uint64_t)c.num_heads * c.head_dim) % 64))
+        return false;  // whole 64-weight groups along every row
     if (c.num_kv_heads > 64 || c.attn_splits > 64 || c.max_batch > 32 || c.prefill_chunk > 64) return false;
     // batched RMSNorm: float4 rows of at most 8192
     if ((c.max_batch > 1 || c.prefill_chunk > 1) && ((c.hidden_dim & 3u) || c.hidden_dim > 8192)) return false;
@@ -292,7 +305,7 @@ int velox_hip_q4_layout(uint32_t n, uint32_t k, uint32_t s_lanes, uint32_t paire
     m->n_tiles = p.n_tiles;
     m->n_iter = p.n_iter;
     m->paired = paired;
-    m->reserved = 0;
+    m->format = 0;
     if (code_bytes) *code_bytes = p.code_bytes;
     if (scale_bytes) *scale_bytes = p.scale_bytes;
     return VELOX_HIP_OK;
@@ -660,7 +673,7 @@ int velox_hip_arena_matrix(const VeloxHipArena* a, int kind, uint32_t layer, Vel
     uint32_t r0, pair, rows, cols;
     if (kind == VELOX_T_HEAD && vx_model(a)->cfg.tied_lm_head) kind = VELOX_T_EMBED;
     if (!vx_target(vx_model(a), kind, layer, &mp, &r0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
-    if (mp->fmt != VX_FMT_Q4) return VELOX_HIP_EINVAL;  // a Q4_0 view; fp32 / fp16 rows have none
+    if (!vx_fmt_tiled(mp->fmt)) return VELOX_HIP_EINVAL;  // a tiled view; fp32 / fp16 rows have none
     out->codes = (void*)(a->weight_arena + mp->code_off);
     out->scales = (void*)(a->weight_scales + mp->scale_off);
     out->n = mp->n;
@@ -669,7 +682,7 @@ int velox_hip_arena_matrix(const VeloxHipArena* a, int kind, uint32_t layer, Vel
     out->n_tiles = mp->n_tiles;
     out->n_iter = mp->n_iter;
     out->paired = mp->paired;
-    out->reserved = 0;
+    out->format = mp->fmt == VX_FMT_G64 ? VELOX_QUANT_Q4_GROUP64 : 0u;
     if (row0) *row0 = pair ? mp->n : r0;  // paired: up rows follow the n gate rows when dequantized
     return VELOX_HIP_OK;
 }
@@ -689,7 +702,7 @@ int velox_hip_load_q4_0(VeloxHipArena* a, int kind, uint32_t layer, const void* 
     const VxMatPlan* mp;
     uint32_t row0, pair, rows, cols;
     if (!vx_target(vx_model(a), kind, layer, &mp, &row0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
-    if (mp->fmt != VX_FMT_Q4) return VELOX_HIP_EINVAL;  // the arena holds fp32 / fp16 rows
+    if (mp->fmt != VX_FMT_Q4) return VELOX_HIP_EINVAL;  // GGML blocks load into GGML Q4_0 arenas only
     if (nbytes != (uint64_t)rows * (cols / 32) * 18) return VELOX_HIP_ESHAPE;
     void* staging = nullptr;
     hipError_t e = hipMalloc(&staging, nbytes);
@@ -709,8 +722,19 @@ int velox_hip_load_rows(VeloxHipArena* a, int kind, uint32_t layer, const void* 
     uint32_t row0, pair, rows, cols;
     if (!vx_target(vx_model(a), kind, layer, &mp, &row0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
     if (mp->fmt == VX_FMT_Q4) return VELOX_HIP_EINVAL;  // Q4_0 arenas load blocks (velox_hip_load_q4_0)
-    const uint64_t elt = mp->fmt == VX_FMT_F32 ? 4 : 2;
+    const uint64_t elt = mp->fmt == VX_FMT_F16 ? 2 : 4;
     if (nbytes != (uint64_t)rows * cols * elt) return VELOX_HIP_ESHAPE;
+    if (mp->fmt == VX_FMT_G64) {
+        // fp32 rows converted on the device, as the reference runner's stream_tensor_converted
+        // does for quant_mode 2 (velox_cuda_runner.cu:174-197)
+        void* staging = nullptr;
+        hipError_t e = hipMalloc(&staging, nbytes);
+        if (e == hipSuccess) e = hipMemcpyAsync(staging, rows_data, nbytes, hipMemcpyHostToDevice, stream);
+        if (e == hipSuccess) e = vx_launch_g64_from_rows((const float*)staging, rows, row0, pair, vx_view(a, *mp), stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(stream);
+        hipFree(staging);
+        return (int)e;
+    }
     const uint64_t first = (uint64_t)(pair ? mp->n : 0) + row0;  // paired: up rows follow the n gate rows
     hipError_t e = hipMemcpyAsync((void*)(a->weight_arena + mp->code_off + first * cols * elt), rows_data, nbytes,
                                   hipMemcpyHostToDevice, stream);
@@ -743,6 +767,10 @@ int velox_hip_synthesize_model(VeloxHipArena* a, uint64_t seed, float sigma, flo
         const uint64_t stream = vx_stream(seed, vx_tag(layer, kind));
         if (mp->fmt == VX_FMT_Q4) {
             e = vx_launch_synth_q4(vx_view(a, *mp), rows, row0, pair, stream, coef, st);
+            return;
+        }
+        if (mp->fmt == VX_FMT_G64) {  // the fp32 model's seeded values, quantized to group-64
+            e = vx_launch_synth_g64(vx_view(a, *mp), rows, row0, pair, stream, coef, st);
             return;
         }
         // fp32 / fp16 rows: the seeded values themselves (rounded to fp16), row-major
@@ -1234,20 +1262,33 @@ void velox_Qwen2_72B_prefill_hip(VeloxHipArena* ctx, uint32_t t, size_t st, uint
 // ---------------------------------------------------------------------------------------------
 int velox_hip_q4_0_repack(const void* d_blocks, uint32_t rows, uint32_t row0, uint32_t pair_part,
                           const VeloxHipQ4Matrix* m, hipStream_t st) {
-    if (!d_blocks || !m) return VELOX_HIP_EINVAL;
+    if (!d_blocks || !m || m->format != 0) return VELOX_HIP_EINVAL;  // GGML Q4_0 blocks only
     const uint32_t logical = m->n;
     if (row0 + rows > logical || pair_part > (m->paired ? 1u : 0u)) return VELOX_HIP_EINVAL;
     return (int)vx_launch_repack(d_blocks, rows, row0, pair_part, vx_view_public(m), st);
 }
 
 int velox_hip_q4_0_dequant(const VeloxHipQ4Matrix* m, float* d_out, hipStream_t st) {
-    if (!m || !d_out) return VELOX_HIP_EINVAL;
+    if (!m || !d_out || (m->format != 0 && m->format != VELOX_QUANT_Q4_GROUP64)) return VELOX_HIP_EINVAL;
     return (int)vx_launch_dequant(vx_view_public(m), d_out, st);
 }
 
 int velox_hip_q4_0_quantize(const float* d_x, uint32_t rows, uint32_t k, void* d_blocks, hipStream_t st) {
     if (!d_x || !d_blocks || k % 32) return VELOX_HIP_EINVAL;
     return (int)vx_launch_quantize(d_x, rows, k, d_blocks, st);
+}
+
+int velox_hip_g64_quantize(const float* d_x, uint64_t n_groups, uint32_t* d_packed, uint16_t* d_scale_min,
+                           hipStream_t st) {
+    if (!d_x || !d_packed || !d_scale_min) return VELOX_HIP_EINVAL;
+    return (int)vx_launch_g64_quantize_ref(d_x, n_groups, d_packed, d_scale_min, st);
+}
+
+int velox_hip_g64_pack(const float* d_rows, uint32_t rows, uint32_t row0, uint32_t pair_part,
+                       const VeloxHipQ4Matrix* m, hipStream_t st) {
+    if (!d_rows || !m || m->format != VELOX_QUANT_Q4_GROUP64 || m->k % 64 || (m->s_lanes & 1u)) return VELOX_HIP_EINVAL;
+    if (row0 + rows > m->n || pair_part > (m->paired ? 1u : 0u)) return VELOX_HIP_EINVAL;
+    return (int)vx_launch_g64_from_rows(d_rows, rows, row0, pair_part, vx_view_public(m), st);
 }
 
 int velox_hip_fill_normal(float* d_out, uint64_t n, uint64_t seed, uint64_t tag, float sigma, float mean,
@@ -1278,7 +1319,8 @@ int velox_hip_gemv_q4_0(const VeloxHipQ4Matrix* m, const float* d_x, const float
 int velox_hip_gemm_q4_0_batch(const VeloxHipQ4Matrix* m, const uint16_t* d_x16, uint32_t batch, uint32_t ldx,
                               const float* d_bias, float* d_y, uint32_t ldy, uint16_t* d_out16, uint32_t ldo,
                               int mode, hipStream_t st) {
-    if (!m || !d_x16 || batch == 0 || batch > 32 || ldx < m->k || (ldx & 7u) || mode < 0 || mode > 2)
+    if (!m || m->format != 0 || !d_x16 || batch == 0 || batch > 32 || ldx < m->k || (ldx & 7u) || mode < 0 ||
+        mode > 2)
         return VELOX_HIP_EINVAL;
     if ((mode == VELOX_GEMV_SWIGLU) != (m->paired != 0)) return VELOX_HIP_EINVAL;
     if (mode == VELOX_GEMV_SWIGLU ? (!d_out16 || ldo < m->n) : (!d_y || ldy < m->n))
@@ -1318,7 +1360,7 @@ int velox_hip_gemm_q4_0_batch(const VeloxHipQ4Matrix* m, const uint16_t* d_x16, 
 
 namespace {
 bool vx_mmat_public(const VeloxHipQ4Matrix* m, const void* codes, const void* scales, VxMMat& out) {
-    if (!m || m->k == 0 || (m->k & 31u) || m->n == 0) return false;
+    if (!m || m->format != 0 || m->k == 0 || (m->k & 31u) || m->n == 0) return false;  // GGML Q4_0 only
     vx_mmat_shape(m->n, m->k, m->paired, out);
     out.codes = (const uint4*)codes;
     out.scales = (const uint2*)scales;
@@ -1492,8 +1534,11 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
     // the arena's model stays alive until the end of the run; the file is closed once loaded
     struct GgufCloser { VeloxHipGguf*& g; ~GgufCloser() { velox_hip_gguf_close(g); } } gguf_closer{gguf};
     if (opt->num_layers && !gguf) cfg.num_layers = opt->num_layers;
-    if (opt->unquantized > 2 || (opt->unquantized && gguf)) return VELOX_HIP_EINVAL;
-    if (opt->unquantized) cfg.quant_mode = opt->unquantized == 1 ? VELOX_QUANT_F32 : VELOX_QUANT_F16;
+    if (opt->unquantized > 3 || (opt->unquantized && gguf)) return VELOX_HIP_EINVAL;
+    if (opt->unquantized)
+        cfg.quant_mode = opt->unquantized == 1   ? VELOX_QUANT_F32
+                         : opt->unquantized == 2 ? VELOX_QUANT_F16
+                                                 : VELOX_QUANT_Q4_GROUP64;
     const uint32_t B = opt->batch > 1 ? opt->batch : 1u;
     if (B > 32 || (B > 1 && opt->prompt_tokens)) return VELOX_HIP_EINVAL;
     if (B > 1) cfg.max_batch = B;

@@ -62,6 +62,9 @@ extern "C" int velox_hip_lm_head_argmax_noalloc(const VeloxHipQ4Matrix* m, const
     w.n_tiles = m->n_tiles;
     w.n_iter = m->n_iter;
     w.paired = 0;
+    // format 0: GGML Q4_0 blocks; VELOX_QUANT_Q4_GROUP64: group-64 pairs; others are refused
+    if (m->format != 0 && m->format != VELOX_QUANT_Q4_GROUP64) return VELOX_HIP_EINVAL;
+    w.fmt = m->format == 0 ? VX_FMT_Q4 : VX_FMT_G64;
     VxGemvArgs g = {};
     g.x = d_x;
     g.gain = d_gain;

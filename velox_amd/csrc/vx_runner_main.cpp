@@ -6,7 +6,8 @@
 //   velox_hip_runner [--model llama3_8b | --model-file MODEL.vlx] [--weights synthetic|FILE.gguf]
 //                    [--tokens 1,2,3 | --prompt-len N]
 //                    [--context-len N] [--steps N] [--warmup N] [--seed S] [--layers L]
-//                    [--prefill-chunk N] [--unquantized f32|f16] [--no-cuda-graph] [--verbose]
+//                    [--prefill-chunk N] [--unquantized f32|f16] [--quantize MODE] [--no-cuda-graph]
+//                    [--verbose]
 //
 // --model-file MODEL.vlx reads the model from its .vlx source (the `model` header, weight
 // declarations and `target hardware` budget; what `velox build MODEL.vlx` compiles into the
@@ -15,6 +16,9 @@
 // chunk) instead of the reference's one decode step per prompt token; TTFT reports either.
 // --unquantized f32|f16 keeps the synthetic weights as fp32 / fp16 rows (the reference's quant_mode
 // 0 / 1, a build without --quantize) instead of Q4_0.
+// --quantize MODE (or --quantize=MODE) takes the reference runner's fp32 model and converts it at
+// load as that runner does (velox_cuda_runner.cu:356-372): f16 / fp16 to fp16 rows, q4_0 / int4 /
+// w4a16 to its group-64 format, any other value keeps fp32 rows.
 //
 // Weights are the seeded synthetic Q4_0 model (`--weights synthetic`, what src/cli.rs:654 passes
 // through) or a GGUF Q4_0 checkpoint (`--weights FILE.gguf`, whose metadata then defines the model,
@@ -47,6 +51,12 @@ int main(int argc, char** argv) {
             if (!std::strcmp(f, "f32")) unquantized = 1;
             else if (!std::strcmp(f, "f16")) unquantized = 2;
             else { std::fprintf(stderr, "Error: --unquantized takes f32 or f16\n"); return 1; }
+        }
+        else if (!std::strcmp(a, "--quantize") || !std::strncmp(a, "--quantize=", 11)) {
+            const char* f = a[10] == '=' ? a + 11 : next();
+            if (!std::strcmp(f, "f16") || !std::strcmp(f, "fp16")) unquantized = 2;
+            else if (!std::strcmp(f, "q4_0") || !std::strcmp(f, "int4") || !std::strcmp(f, "w4a16")) unquantized = 3;
+            else unquantized = 1;
         }
         else if (!std::strcmp(a, "--tokens")) {
             std::string s = next();
@@ -90,7 +100,7 @@ int main(int argc, char** argv) {
             }
         } else if (!std::strcmp(a, "--context-len")) {
             context_len = (uint32_t)std::atoi(next());
-        } else if (!std::strcmp(a, "--quantize") || !std::strcmp(a, "--speculative") ||
+        } else if (!std::strcmp(a, "--speculative") ||
                    !std::strcmp(a, "--draft-len") || !std::strcmp(a, "--spec-ema")) {
             std::fprintf(stderr, "Error: %s is not supported by this runner\n", a);
             return 1;

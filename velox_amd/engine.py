@@ -262,8 +262,9 @@ def run(model: str = "llama3_8b", prompt_len: int = 128, warmup: int = 5, steps:
     context of that many positions already in the KV cache (then prompt_len must be 1). Returned
     tokens are ring entries, ring[p] = argmax after position p, for the last positions run.
     `prefill_chunk` > 1 prefills the prompt as batched chunks of that many positions. `model_file`
-    reads the model from a .vlx source instead of the builtin `model`. `unquantized` 1 / 2 keeps the
-    weights as fp32 / fp16 rows (the reference's quant_mode 0 / 1) instead of GGML Q4_0."""
+    reads the model from a .vlx source instead of the builtin `model`. `unquantized` 1 / 2 / 3 runs the
+    reference's fp32 weights as fp32 rows, fp16 rows or quantized to group-64 (quant_mode 0 / 1 / 2)
+    instead of GGML Q4_0."""
     lib = L.load()
     ptoks = None
     if prompt is not None:
