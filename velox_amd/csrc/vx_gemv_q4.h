@@ -258,36 +258,22 @@ __device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a) {
         }
     }
 
-    // ---- RMSNorm scale (src/runtime.rs:588-601) from the registers, plus groups beyond them ----
-    float inv_rms = 1.0f;
-    if constexpr (NORM) {
-        float ss = 0.0f;
-#pragma unroll
-        for (int i = 0; i < GX; ++i) {
-            if ((uint32_t)tid + (uint32_t)i * NT < ng) {
-                const float4 v0 = xv[2 * i], v1 = xv[2 * i + 1];
-                ss += v0.x * v0.x + v0.y * v0.y + v0.z * v0.z + v0.w * v0.w;
-                ss += v1.x * v1.x + v1.y * v1.y + v1.z * v1.z + v1.w * v1.w;
-            }
-        }
-        for (uint32_t g = (uint32_t)tid + GX * NT; g < ng; g += NT) {
-            const float4 v0 = *(const float4*)(a.x + 8u * g);
-            const float4 v1 = *(const float4*)(a.x + 8u * g + 4u);
-            ss += v0.x * v0.x + v0.y * v0.y + v0.z * v0.z + v0.w * v0.w;
-            ss += v1.x * v1.x + v1.y * v1.y + v1.z * v1.z + v1.w * v1.w;
-        }
-        ss = vx_block_sum<W>(ss, red);
-        inv_rms = 1.0f / sqrtf(ss / (float)K + a.eps);
-    }
     // x -> LDS digit planes [d][b] (16 bytes: the digit dwords of the block's 4 code dwords): the S
     // lanes of a row read blocks b..b+S-1 of one plane at consecutive 16-byte addresses (no LDS
     // bank conflicts). Group g = values 8g..8g+7 = code dword g & 3 of block g >> 2.
+    // RMSNorm (src/runtime.rs:588-601): the block-scaled integers hold x * gain at any magnitude, so
+    // the stage does not wait for the sum of squares; each thread sums its values' squares while
+    // staging, the staging barrier also publishes the waves' sums, and the row results take
+    // 1 / rms in the epilogue (sum_k w_k x_k g_k / rms = sum_k w_k (x_k / rms) g_k).
+    float ss = 0.0f;
     auto stage = [&](uint32_t g, float4 v0, float4 v1, float4 g0, float4 g1) {
         float u[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         if constexpr (NORM) {
+            ss += v0.x * v0.x + v0.y * v0.y + v0.z * v0.z + v0.w * v0.w;
+            ss += v1.x * v1.x + v1.y * v1.y + v1.z * v1.z + v1.w * v1.w;
             const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) u[e] = (u[e] * inv_rms) * gg[e];
+            for (int e = 0; e < 8; ++e) u[e] = u[e] * gg[e];
         }
         // the four 8-element groups of one 32-block sit in four consecutive lanes, which are all
         // in range or all out of range (ng is a multiple of 4); nan is NaN when any value is NaN
@@ -353,7 +339,18 @@ __device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a) {
         }
         stage(g, v0, v1, g0, g1);
     }
+    if constexpr (NORM) {
+        ss = vx_wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+    }
     __syncthreads();
+    float inv_rms = 1.0f;
+    if constexpr (NORM) {
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) t += red[w];
+        inv_rms = 1.0f / sqrtf(t / (float)K + a.eps);
+    }
 
     // ---- stream: consume slot u, refill it with the item kU ahead, finish tiles on the fly ----
     float best_v = -INFINITY;
@@ -389,6 +386,7 @@ __device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a) {
         }
         if (++ci == n_iter) {
             acc = vx_group_sum<S>(acc);
+            if constexpr (NORM) acc *= inv_rms;
             const uint32_t row = row_of(first + ct * step);
             const bool row_ok = row < a.n;
             if constexpr (EPI == VX_EPI_STORE) {

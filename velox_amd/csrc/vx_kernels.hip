@@ -9,7 +9,8 @@
 //     32-element block, stored as six planes of signed base-16 digits, and each code word meets
 //     them in v_dot8_i32_i4 (q - 8 is the code nibble xor 8): the block's dot product is exact
 //     integer arithmetic, so x keeps 2^-22 of each block's largest magnitude (fp32-class).
-//     RMSNorm runs in the prologue, residual / SwiGLU / argmax in the epilogue.
+//     RMSNorm's gain is applied while staging x and its 1/rms in the epilogue, with residual /
+//     SwiGLU / argmax.
 //   * Decode attention: split-K over the sequence, RoPE + bf16 KV append in the prologue,
 //     online softmax per split, LSE merge by the last workgroup of each KV head.
 #include <hip/hip_fp16.h>

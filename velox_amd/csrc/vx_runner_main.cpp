@@ -153,8 +153,12 @@ int main(int argc, char** argv) {
     std::printf("VELOX MI355X HIP RUNTIME EXECUTION REPORT\n");
     std::printf("================================================================================\n");
     if (weights.empty()) {
-        std::printf("Model                  : %s (synthetic Q4_0, seed %llu)\n",
-                    model_file.empty() ? model.c_str() : model_file.c_str(), (unsigned long long)seed);
+        const char* fmt = unquantized == 1   ? "fp32 rows"
+                          : unquantized == 2 ? "fp16 rows"
+                          : unquantized == 3 ? "group-64 4-bit"
+                                             : "Q4_0";
+        std::printf("Model                  : %s (synthetic %s, seed %llu)\n",
+                    model_file.empty() ? model.c_str() : model_file.c_str(), fmt, (unsigned long long)seed);
         std::printf("Weight Synthesis       : %.2f ms\n", rep.load_ms);
     } else {
         std::printf("Model                  : %s (GGUF Q4_0)\n", weights.c_str());
