@@ -118,6 +118,10 @@ OTHER_CONFIGS = (
     ("config5_qwen2_72b_ctx8192_b1", "qwen2_72b", 8192, 1, 3, 15),
 )
 MLA_CONFIGS = (("config4_deepseek_v3_mla_ctx4096_b1", 1), ("config4_deepseek_v3_mla_ctx4096_b16", 16))
+# configuration 4 runs DeepSeek-V3's own stack of attention layers (NUM_LAYERS of
+# examples/deepseek_v3_mla.vlx): every layer's 187 MB of fp8 weights stream from HBM once per step,
+# where one replayed layer would leave most of them in the 256 MB memory-side cache between replays
+MLA_LAYERS = 61
 
 
 def other_configs(seed: int) -> dict:
@@ -143,19 +147,20 @@ def other_configs(seed: int) -> dict:
         print(f"[bench] {key}: {rep['tok_per_s']:.1f} tok/s, {rep['hbm_gbps']:.0f} GB/s "
               f"({time.perf_counter() - t0:.1f} s)", file=sys.stderr, flush=True)
     for key, batch in MLA_CONFIGS:
-        r = mla_run(batch=batch, context_len=4096, warmup=5, steps=50, seed=seed)
+        r = mla_run(batch=batch, context_len=4096, warmup=3, steps=10, seed=seed, layers=MLA_LAYERS)
         out[key] = {"value": round(r["us_per_layer"], 3), "unit": "us/layer", "higher_is_better": False,
                     "batch": batch, "context_tokens": 4096, "hbm_gbps": round(r["hbm_gbps"], 1),
                     "hbm_frac": round(r["hbm_gbps"] / HBM_PEAK_GBPS, 4), "bytes_per_step": int(r["bytes_per_layer"]),
-                    "attention_us": round(r["attn_us"], 3)}
+                    "attention_us": round(r["attn_us"], 3), "layers": MLA_LAYERS}
         print(f"[bench] {key}: {r['us_per_layer']:.2f} us/layer", file=sys.stderr, flush=True)
     return out
 
 
 def bench_mla(args) -> int:
-    """Benchmark configuration 4: one DeepSeek-V3 absorbed-MLA layer (fp8 e4m3 weights with 128x128 block
-    scales, bf16 latent cache of `context_len` seeded positions per sequence), timed as hipGraph
-    replays of the layer step; value = device microseconds per layer (lower is better)."""
+    """Benchmark configuration 4: the DeepSeek-V3 absorbed-MLA layer (fp8 e4m3 weights with 128x128 block
+    scales, bf16 latent cache of `context_len` seeded positions per sequence and layer), timed as
+    hipGraph replays of the decode step over `--mla-layers` layers; value = device microseconds per
+    layer (lower is better)."""
     from velox_amd.engine import mla_run
 
     ctx = args.context_len or 4096
@@ -163,7 +168,8 @@ def bench_mla(args) -> int:
           f"steps {args.steps}", file=sys.stderr, flush=True)
     if args.no_graph:
         return bench_mla_eager(args, ctx)
-    r = mla_run(batch=args.batch, context_len=ctx, warmup=args.warmup, steps=args.steps, seed=args.seed)
+    r = mla_run(batch=args.batch, context_len=ctx, warmup=args.warmup, steps=args.steps, seed=args.seed,
+                layers=args.mla_layers)
     attn_gbps = r["attn_bytes"] / (r["attn_us"] * 1e3) if r["attn_us"] > 0 else 0.0
     print(f"[bench] mla done: {r['us_per_layer']:.2f} us/layer, {r['hbm_gbps']:.0f} GB/s; attention "
           f"{r['attn_us']:.2f} us", file=sys.stderr, flush=True)
@@ -181,13 +187,13 @@ def bench_mla(args) -> int:
         "dtype": "fp8 e4m3 x f16 -> f32 (bf16 latent cache)",
         "data": "synthetic",
         "config": {"workload": f"deepseek_v3_mla_fp8_layer_bs{args.batch}_ctx{ctx}", "batch": args.batch,
-                   "context_tokens": ctx, "hipgraph": True},
+                   "context_tokens": ctx, "layers": args.mla_layers, "hipgraph": True},
         "hbm_gbps": round(r["hbm_gbps"], 1),
         "hbm_frac": round(r["hbm_gbps"] / HBM_PEAK_GBPS, 4),
         "bytes_per_step": int(r["bytes_per_layer"]),
         "wall_ms": round(r["wall_ms"], 3),
         "roofline": {
-            "kernel": "vx_mla_attn_kernel<512,64,4> (absorbed MLA attention over the bf16 latent cache, MFMA)",
+            "kernel": "vx_mla_attn_kernel<512,64,4,2> (absorbed MLA attention over the bf16 latent cache, MFMA)",
             "bound": "hbm",
             "achieved": round(attn_gbps, 1),
             "peak": HBM_PEAK_GBPS,
@@ -203,7 +209,7 @@ def bench_mla(args) -> int:
 
 
 def bench_mla_eager(args, ctx: int) -> int:
-    """The same layer step launched eagerly (one synchronized step per call), for per-kernel traces:
+    """The same step launched eagerly (one synchronized step per call), for per-kernel traces:
     rocprofv3's kernel trace of replayed hipGraphs is not usable here. Its wall time includes host
     launch and synchronization, so it is reported beside, never as, the graph figure."""
     import numpy as np
@@ -211,19 +217,24 @@ def bench_mla_eager(args, ctx: int) -> int:
     from velox_amd.engine import MlaEngine
 
     n = args.warmup + args.steps
-    e = MlaEngine("deepseek_v3_mla", max_seq_len=ctx + n + 1, max_batch=args.batch, seed=args.seed)
+    layers = max(args.mla_layers, 1)
+    e = MlaEngine("deepseek_v3_mla", max_seq_len=ctx + n + 1, max_batch=args.batch, seed=args.seed,
+                  num_layers=layers)
     for b in range(args.batch):
-        e.fill_cache(0, b, ctx, seed=args.seed + b)
+        for layer in range(layers):
+            e.fill_cache(layer, b, ctx, seed=args.seed + b)
         e.set_position(b, ctx)
     e.set_hidden(np.random.default_rng(args.seed).standard_normal((args.batch, e.cfg.hidden_dim)).astype(np.float32))
+    step = (lambda: e.decode_step(args.batch)) if layers > 1 else (lambda: e.step(0, args.batch))
     for _ in range(args.warmup):
-        e.step(0, args.batch)
+        step()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        e.step(0, args.batch)
-    wall_us = (time.perf_counter() - t0) * 1e6 / max(args.steps, 1)
+        step()
+    wall_us = (time.perf_counter() - t0) * 1e6 / max(args.steps, 1) / layers
     e.close()
-    print(f"[bench] mla eager: {args.steps} synchronized steps, {wall_us:.1f} us wall each", file=sys.stderr, flush=True)
+    print(f"[bench] mla eager: {args.steps} synchronized steps of {layers} layers, {wall_us:.1f} us wall per layer",
+          file=sys.stderr, flush=True)
     print(json.dumps({"metric": f"MLA layer eager wall us, DeepSeek-V3 MLA fp8 bs={args.batch} ctx {ctx}, 1 GPU",
                       "value": round(wall_us, 3), "unit": "us/layer (eager, host-synchronized)", "n_gpus": 1,
                       "steps": args.steps, "warmup": args.warmup, "higher_is_better": False, "data": "synthetic",
@@ -243,6 +254,8 @@ def main() -> int:
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip benchmark configurations 1 and 3-5, timed beside the headline as other_configs")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--mla-layers", type=int, default=MLA_LAYERS,
+                    help="--model deepseek_v3_mla: layers of the timed decode step (1: one replayed layer)")
     ap.add_argument("--prompt-len", type=int, default=PROMPT_LEN)
     ap.add_argument("--model", default="llama3_8b",
                     choices=["llama3_8b", "qwen2_5_7b", "qwen2_72b", "smollm_135m", "deepseek_v3_mla"],

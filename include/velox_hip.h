@@ -513,21 +513,30 @@ int velox_hip_mla_set_position(VeloxHipMla* m, uint32_t seq, uint64_t pos, hipSt
  * Capturable; errors through velox_hip_last_error(). */
 void velox_hip_mla_layer_step(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t active_mask,
                               hipStream_t stream);
+/* The attention stack of a decode step: the layer step of layers 0 .. num_layers - 1 in order, as the
+ * reference's graph step launches its MLA kernel per layer (src/codegen.rs:2980-3003), with each
+ * layer's W_o partials folded into the next layer's RMSNorm instead of a residual launch (hidden
+ * ends equal to num_layers successive layer steps, bit for bit). The MoE FFN the reference model
+ * places between the attention layers is outside this backend (not in the benchmark configurations).
+ * Capturable; errors through velox_hip_last_error(). */
+void velox_hip_mla_decode_step(VeloxHipMla* m, uint32_t batch, uint64_t active_mask, hipStream_t stream);
 /* Algorithmic HBM bytes of one layer step (weights + scales + latent rows 0..pos + activations). */
 double velox_hip_mla_step_bytes(const VeloxHipMla* m, uint32_t batch, uint64_t pos);
 
 typedef struct VeloxHipMlaRunReport {
-    double us_per_layer;     /* mean device time of one layer step (hipGraph replays) */
+    double us_per_layer;     /* mean device time per layer (hipGraph replays of the step / layers) */
     double bytes_per_layer, hbm_gbps;
     double attn_us;          /* mean attention-kernel time (event-timed passes) */
     double attn_bytes;       /* its algorithmic bytes (latent rows read) */
     double wall_ms;
     int status;
 } VeloxHipMlaRunReport;
-/* Synthesize `which`, seed a context_len-position latent context per sequence, time `steps` layer
- * steps of `batch` sequences at position context_len after `warmup` untimed ones. */
-int velox_hip_mla_run(const char* which, uint32_t batch, uint32_t context_len, uint32_t warmup, uint32_t steps,
-                      uint64_t seed, VeloxHipMlaRunReport* rep);
+/* Synthesize `which` with num_layers layers, seed a context_len-position latent context per
+ * sequence and layer, time `steps` steps of `batch` sequences at position context_len after
+ * `warmup` untimed ones: velox_hip_mla_decode_step over the stack (num_layers > 1; every layer's
+ * weights then stream from HBM once per step) or one layer step (num_layers 0 or 1). */
+int velox_hip_mla_run(const char* which, uint32_t batch, uint32_t context_len, uint32_t num_layers, uint32_t warmup,
+                      uint32_t steps, uint64_t seed, VeloxHipMlaRunReport* rep);
 
 #ifdef __cplusplus
 }

@@ -127,6 +127,37 @@ def test_mla_synthesized_weights_equal_loaded_codes(oracle):
     b.close()
 
 
+@pytest.mark.parametrize("batch", [1, 16])
+def test_mla_decode_step_equals_layer_steps(batch):
+    """velox_hip_mla_decode_step over a 3-layer DeepSeek-V3-shaped stack (each layer's W_o partials
+    folded into the next layer's RMSNorm: 5 of them at B=1, 19 at B=16) ends with the hidden state
+    and appended latent rows of three successive layer steps, bit for bit; the layers' own weights
+    and contexts differ, so a wrong layer index or a dropped partial changes the result."""
+    layers, max_seq = 3, 96
+    eng = [MlaEngine("deepseek_v3_mla", max_seq_len=max_seq, max_batch=batch, num_layers=layers, seed=9,
+                     norm_sigma=0.1) for _ in range(2)]
+    h = np.random.default_rng(batch).standard_normal((batch, eng[0].cfg.hidden_dim)).astype(np.float32)
+    ctx = [40 + 3 * s for s in range(batch)]
+    for e in eng:
+        for layer in range(layers):
+            for s in range(batch):
+                e.fill_cache(layer, s, ctx[s], seed=3 + layer)
+        for s in range(batch):
+            e.set_position(s, ctx[s])
+        e.set_hidden(h)
+    eng[0].decode_step(batch)
+    for layer in range(layers):
+        eng[1].step(layer, batch)
+    got, want = eng[0].hidden(batch), eng[1].hidden(batch)
+    assert np.all(np.isfinite(got)) and not np.array_equal(got, h)
+    assert np.array_equal(got, want)
+    for layer in range(layers):
+        for s in range(batch):
+            assert np.array_equal(eng[0].cache(layer, s, ctx[s] + 1), eng[1].cache(layer, s, ctx[s] + 1)), (layer, s)
+    for e in eng:
+        e.close()
+
+
 def test_mla_bad_arguments():
     lib = L.load()
     c = L.MlaConfig()

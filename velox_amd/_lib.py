@@ -196,8 +196,9 @@ _SIGS = {
     "velox_hip_mla_fill_cache": (_I, [_P, _U32, _U32, _U32, _U64, _F, _P]),
     "velox_hip_mla_set_position": (_I, [_P, _U32, _U64, _P]),
     "velox_hip_mla_layer_step": (None, [_P, _U32, _U32, _U64, _P]),
+    "velox_hip_mla_decode_step": (None, [_P, _U32, _U64, _P]),
     "velox_hip_mla_step_bytes": (C.c_double, [_P, _U32, _U64]),
-    "velox_hip_mla_run": (_I, [C.c_char_p, _U32, _U32, _U32, _U32, _U64, C.POINTER(MlaRunReport)]),
+    "velox_hip_mla_run": (_I, [C.c_char_p, _U32, _U32, _U32, _U32, _U32, _U64, C.POINTER(MlaRunReport)]),
 }
 
 

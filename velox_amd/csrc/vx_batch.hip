@@ -11,7 +11,8 @@ namespace {
 
 typedef _Float16 vx_bh2 __attribute__((ext_vector_type(2)));
 
-constexpr uint32_t kBNormMaxParts = 8;  // K splits of a RESID GEMM that one batched RMSNorm folds in
+// K splits of a RESID GEMM that one batched RMSNorm folds in, loaded kBNormPartGroup at a time
+constexpr uint32_t kBNormMaxParts = 32, kBNormPartGroup = 8;
 
 __device__ __forceinline__ float vx_bh2f(uint32_t h) { return __half2float(__ushort_as_half((unsigned short)h)); }
 
@@ -84,26 +85,28 @@ __global__ __launch_bounds__(1024) void vx_bnorm_kernel(float* h, uint32_t ldh, 
         v[j] = x[i];
     }
     if (parts) {
-        // every partial of every element loaded before the first add (split index clamped; the
-        // adds past nparts are skipped)
-        float4 p[kBNormMaxParts][NV];
+        // partials added in split order; each group of kBNormPartGroup is loaded before its first
+        // add (split index clamped; the adds past nparts are skipped)
+        for (uint32_t s0 = 0; s0 < nparts; s0 += kBNormPartGroup) {
+            float4 p[kBNormPartGroup][NV];
 #pragma unroll
-        for (uint32_t s = 0; s < kBNormMaxParts; ++s)
-#pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const uint32_t i = min(threadIdx.x + 1024u * j, k4 - 1u);
-                p[s][j] = ((const float4*)(parts + min(s, nparts - 1u) * pstride + (size_t)b * ldh))[i];
-            }
-#pragma unroll
-        for (uint32_t s = 0; s < kBNormMaxParts; ++s)
-            if (s < nparts)
+            for (uint32_t s = 0; s < kBNormPartGroup; ++s)
 #pragma unroll
                 for (int j = 0; j < NV; ++j) {
-                    v[j].x += p[s][j].x;
-                    v[j].y += p[s][j].y;
-                    v[j].z += p[s][j].z;
-                    v[j].w += p[s][j].w;
+                    const uint32_t i = min(threadIdx.x + 1024u * j, k4 - 1u);
+                    p[s][j] = ((const float4*)(parts + min(s0 + s, nparts - 1u) * pstride + (size_t)b * ldh))[i];
                 }
+#pragma unroll
+            for (uint32_t s = 0; s < kBNormPartGroup; ++s)
+                if (s0 + s < nparts)
+#pragma unroll
+                    for (int j = 0; j < NV; ++j) {
+                        v[j].x += p[s][j].x;
+                        v[j].y += p[s][j].y;
+                        v[j].z += p[s][j].z;
+                        v[j].w += p[s][j].w;
+                    }
+        }
 #pragma unroll
         for (int j = 0; j < NV; ++j)
             if (threadIdx.x + 1024u * j < k4) x[threadIdx.x + 1024u * j] = v[j];

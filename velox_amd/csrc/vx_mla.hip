@@ -217,7 +217,104 @@ __global__ __launch_bounds__(64 * kFWaves) void vx_f8gemm_kernel(VxF8GemmArgs a)
     }
 }
 
+// =============================================================================================
+// fp8 block-scaled GEMV (one sequence): the same tiled weights without the matrix cores
+// =============================================================================================
+// With one sequence the MFMA form computes 16 columns of which one is used and loads the activation
+// fragment twice per weight word. Here lane (row c = lane & 15, group q = lane >> 4) of a wave takes
+// the 16 weights of its row at k-elements 64 kt + 16 q + 0..15 (its bytes of tile kt's word),
+// converts them exactly to fp16 and dots them against x staged once per workgroup in LDS (fp16,
+// the rounding the MFMA form applies) with v_dot2_f32_f16, one block-scale FMA per k-tile. KW waves
+// share a row tile, splitting its k-tiles; their sums meet in LDS and the first of them writes the
+// 16 rows. Waves stream D words ahead, unconditionally (a clamped re-read past the end): 8 where
+// eight waves share a tile (long k-ranges), else 4 (the re-reads past a short range cost more than
+// the deeper queue gains).
+constexpr int kFGWaves = 8;
+
+template <int KW, bool XF32>
+__global__ __launch_bounds__(64 * kFGWaves) void vx_f8gemv_kernel(VxF8GemmArgs a) {
+    extern __shared__ __align__(16) unsigned char vm_smem[];
+    if ((a.active_mask & 1ULL) == 0ULL) return;
+    constexpr int TPW = kFGWaves / KW;  // row tiles per workgroup
+    constexpr int D = KW == 8 ? 8 : 4;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, grp = lane >> 4;
+    const uint32_t g = blockIdx.z, ks = blockIdx.y, kw = (uint32_t)wave % KW, tw = (uint32_t)wave / KW;
+    const uint32_t rt = blockIdx.x * TPW + tw, rtc = min(rt, a.n_rt - 1u);
+    // the workgroup's k-tiles (its split), then this wave's share of them
+    const uint32_t kt0 = ks * a.n_kt / gridDim.y, kt1 = (ks + 1u) * a.n_kt / gridDim.y;
+    const uint32_t w0 = kt0 + kw * (kt1 - kt0) / KW, w1 = kt0 + (kw + 1u) * (kt1 - kt0) / KW;
+    const uint4* W = a.codes + g * a.w_gstride + (size_t)rtc * a.n_kt * 64u + lane;
+    const float* S = a.scales + g * a.s_gstride + (size_t)rtc * a.n_kb;
+    const uint32_t wl = w1 > w0 ? w1 - 1u : w0;
+    uint4 wr[D];
+#pragma unroll
+    for (int u = 0; u < D; ++u) wr[u] = W[(size_t)min(w0 + (uint32_t)u, wl) * 64u];
+    // x over the split's k-range -> LDS as fp16 (8 elements per thread and pass)
+    uint4* xs = (uint4*)vm_smem;
+    const uint32_t n8 = (kt1 - kt0) * 8u;
+    for (uint32_t i = (uint32_t)tid; i < n8; i += 64u * kFGWaves) {
+        const size_t e = g * a.x_gstride + (size_t)kt0 * 64u + 8u * i;
+        if constexpr (XF32) {
+            const float4 lo = *(const float4*)((const float*)a.x + e), hi = *(const float4*)((const float*)a.x + e + 4);
+            xs[i] = __builtin_bit_cast(uint4, vm_f32x8_to_h8(lo, hi));
+        } else {
+            xs[i] = *(const uint4*)((const uint16_t*)a.x + e);
+        }
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    for (uint32_t base = w0; base < w1; base += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            const uint32_t kt = base + (uint32_t)u;
+            if (kt < w1) {
+                const uint32_t xi = (kt - kt0) * 8u + 2u * (uint32_t)grp;
+                const vm_h8 x0 = __builtin_bit_cast(vm_h8, xs[xi]), x1 = __builtin_bit_cast(vm_h8, xs[xi + 1u]);
+                const vm_h8 f0 = vm_fp8x8(wr[u].x, wr[u].y), f1 = vm_fp8x8(wr[u].z, wr[u].w);
+                float d = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    d = __builtin_amdgcn_fdot2(vm_h2{f0[2 * j], f0[2 * j + 1]}, vm_h2{x0[2 * j], x0[2 * j + 1]}, d, false);
+                    d = __builtin_amdgcn_fdot2(vm_h2{f1[2 * j], f1[2 * j + 1]}, vm_h2{x1[2 * j], x1[2 * j + 1]}, d, false);
+                }
+                acc = fmaf(S[kt >> 1], d, acc);
+            }
+            wr[u] = W[(size_t)min(kt + (uint32_t)D, wl) * 64u];
+        }
+    }
+    // the row's four k-groups, then the KW waves of the tile
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    float* red = (float*)vm_smem;  // x is no longer read: every wave passed its last LDS read below
+    if constexpr (KW > 1) {
+        __syncthreads();
+        if (lane < 16) red[(tw * KW + kw) * 16u + (uint32_t)lane] = acc;
+        __syncthreads();
+        if (kw != 0) return;
+        acc = 0.0f;
+#pragma unroll
+        for (int w = 0; w < KW; ++w) acc += red[(tw * KW + (uint32_t)w) * 16u + (uint32_t)lane % 16u];
+    }
+    if (lane >= 16 || rt >= a.n_rt) return;
+    const size_t o = g * a.y_gstride + 16u * rt + (uint32_t)col;
+    if (a.y16) {
+        a.y16[o] = __builtin_bit_cast(uint16_t, (_Float16)acc);
+    } else {
+        float* y = a.y + o + (gridDim.y > 1u ? ks * a.pstride : 0u);
+        *y = a.add_y ? *y + acc : acc;
+    }
+}
+
 namespace {
+
+template <int KW>
+void vx_f8gemv_launch_t(const VxF8GemmArgs& a, uint32_t groups, size_t lds, hipStream_t st) {
+    constexpr int TPW = kFGWaves / KW;
+    const dim3 grid((a.n_rt + TPW - 1) / TPW, a.ksplit, groups), block(64 * kFGWaves);
+    if (a.x_f32) hipLaunchKernelGGL((vx_f8gemv_kernel<KW, true>), grid, block, lds, st, a);
+    else hipLaunchKernelGGL((vx_f8gemv_kernel<KW, false>), grid, block, lds, st, a);
+}
 
 template <int MT, int MR>
 void vx_f8gemm_launch_t(const VxF8GemmArgs& a, uint32_t groups, hipStream_t st) {
@@ -238,6 +335,27 @@ hipError_t vx_launch_f8gemm(const VxF8GemmArgs& a, uint32_t groups, hipStream_t 
         return hipErrorInvalidValue;
     if (a.ksplit > 1u && a.pstride < (uint64_t)a.batch * a.ldy) return hipErrorInvalidValue;
     if ((a.y16 != nullptr) == (a.y != nullptr) || (a.y16 && a.ksplit != 1u)) return hipErrorInvalidValue;
+    if (a.add_y && (a.batch != 1u || a.ksplit != 1u || a.y16)) return hipErrorInvalidValue;
+    if (a.batch == 1u) {
+        // one sequence: the GEMV. Waves per row tile: the fewest giving >= 256 workgroups, as long
+        // as each wave keeps >= 2 k-tiles.
+        const uint32_t kts = a.n_kt / a.ksplit;  // k-tiles of the shortest split
+        auto wgs = [&](uint32_t kw) { return (a.n_rt + kFGWaves / kw - 1u) / (kFGWaves / kw) * a.ksplit * groups; };
+        uint32_t kw = 1u;
+        while (kw < (uint32_t)kFGWaves && wgs(kw) < 256u && kts / (2u * kw) >= 2u) kw *= 2u;
+        // fp16 x of the longest split; at least the waves' 16-row sums that reuse it
+        size_t lds = (size_t)((a.n_kt + a.ksplit - 1u) / a.ksplit) * 128u;
+        if (lds < (size_t)kFGWaves * 16u * 4u) lds = (size_t)kFGWaves * 16u * 4u;
+        if (lds > 64u * 1024u) return hipErrorInvalidValue;
+        switch (kw) {
+            case 1: vx_f8gemv_launch_t<1>(a, groups, lds, st); break;
+            case 2: vx_f8gemv_launch_t<2>(a, groups, lds, st); break;
+            case 4: vx_f8gemv_launch_t<4>(a, groups, lds, st); break;
+            default: vx_f8gemv_launch_t<8>(a, groups, lds, st); break;
+        }
+        return hipGetLastError();
+    }
+    if (a.add_y) return hipErrorInvalidValue;
     // fewer row tiles per wave while the grid would leave CUs idle (< 256 workgroups): a wave's row
     // tiles only share its activation loads, the per-row arithmetic is the same
     uint32_t mr = vx_f8gemm_rows_per_wave(a.batch);

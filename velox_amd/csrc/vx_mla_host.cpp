@@ -242,6 +242,7 @@ int velox_hip_mla_create(const VeloxHipMlaConfig* cfg, VeloxHipMla** out) {
     if (m->ks_a > 16) m->ks_a = 16;  // the prep kernel folds at most 16 partials
     if (m->ks_a > m->H / 64) m->ks_a = m->H / 64;
     m->ks_o = (512 + wg_o - 1) / wg_o;
+    if (m->ks_o > 32) m->ks_o = 32;  // the next layer's RMSNorm folds at most 32 partials
     if (m->ks_o > m->nh * m->dv / 64) m->ks_o = m->nh * m->dv / 64;
     uint32_t splits = c.attn_splits;
     if (!splits) {
@@ -413,12 +414,20 @@ int velox_hip_mla_set_position(VeloxHipMla* m, uint32_t seq, uint64_t pos, hipSt
     return (int)e;
 }
 
-void velox_hip_mla_layer_step(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, hipStream_t st) {
-    if (!m || layer >= m->cfg.num_layers || batch == 0 || batch > m->B) {
-        vx_record_error(hipErrorInvalidValue);
-        return;
-    }
+}  // extern "C"
+
+namespace {
+
+// One layer's absorbed-MLA sub-block. With one sequence W_o is a GEMV over the whole K that adds
+// its rows to h itself. Otherwise W_o leaves K-split partials: fold_prev -- the previous layer's
+// partials are still to be added to h, which this layer's RMSNorm does (same split order as the
+// residual kernel) before normalizing; finish -- this layer adds its own with the residual kernel.
+void vm_layer(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, bool fold_prev, bool finish,
+              hipStream_t st) {
     const VmLayer& L = m->layers[layer];
+    const bool direct = batch == 1;  // W_o GEMV with the residual epilogue
+    fold_prev = fold_prev && !direct;
+    finish = finish && !direct;
     const VeloxHipMlaConfig& c = m->cfg;
     const uint4* codes = (const uint4*)(m->base + m->o_codes);
     const float* scales = (const float*)(m->base + m->o_scales);
@@ -428,7 +437,8 @@ void velox_hip_mla_layer_step(VeloxHipMla* m, uint32_t layer, uint32_t batch, ui
     uint16_t* x16 = (uint16_t*)vm_act(m, m->a_x16);
     uint16_t* cache = (uint16_t*)(m->base + m->o_cache + m->cache_layer_bytes * layer);
     auto gemm = [&](const VmF8Plan& p, const void* x, uint32_t ldx, uint64_t x_gstride, uint32_t x_f32, float* y,
-                    uint32_t ldy, uint64_t y_gstride, uint32_t ksplit, uint64_t pstride, uint16_t* y16 = nullptr) {
+                    uint32_t ldy, uint64_t y_gstride, uint32_t ksplit, uint64_t pstride, uint16_t* y16 = nullptr,
+                    uint32_t add_y = 0) {
         VxF8GemmArgs g;
         std::memset(&g, 0, sizeof(g));
         g.codes = codes + p.code_off / 16;
@@ -449,11 +459,15 @@ void velox_hip_mla_layer_step(VeloxHipMla* m, uint32_t layer, uint32_t batch, ui
         g.x_gstride = x_gstride;
         g.y_gstride = y_gstride;
         g.pstride = pstride;
+        g.add_y = add_y;
         g.active_mask = mask;
         vx_record_error(vx_launch_f8gemm(g, p.groups, st));
     };
-    // 1. x = rmsnorm(h) as fp16
-    vx_record_error(vx_launch_bnorm(h, m->H, nullptr, 0, 0, (const float*)((const uint8_t*)norms + L.norm), m->H,
+    float* parts_o = vm_act(m, m->a_parts_o);
+    const uint64_t pstride_o = (uint64_t)m->B * m->H;
+    // 1. x = rmsnorm(h) as fp16 (h first takes the previous layer's W_o partials when they are pending)
+    vx_record_error(vx_launch_bnorm(h, m->H, fold_prev ? parts_o : nullptr, fold_prev ? m->ks_o : 0u,
+                                    fold_prev ? pstride_o : 0u, (const float*)((const uint8_t*)norms + L.norm), m->H,
                                     c.rms_norm_eps, x16, m->ldx16, 32u, batch, mask, st));
     // 2. [W_qa; W_kva] x, split over K
     float* parts_a = vm_act(m, m->a_parts_a);
@@ -522,10 +536,33 @@ void velox_hip_mla_layer_step(VeloxHipMla* m, uint32_t layer, uint32_t batch, ui
     // o_h goes to W_o as fp16, the rounding the GEMM applies to fp32 activations: half the bytes
     uint16_t* oh16 = (uint16_t*)vm_act(m, m->a_oh);
     gemm(L.uv, ctx, m->nh * m->lr, m->lr, 1, nullptr, m->nh * m->dv, m->dv, 1, 0, oh16);
-    float* parts_o = vm_act(m, m->a_parts_o);
-    const uint64_t pstride_o = (uint64_t)m->B * m->H;
+    if (direct) {
+        gemm(L.o, oh16, m->nh * m->dv, 0, 0, h, m->H, 0, 1, 0, nullptr, 1);
+        return;
+    }
     gemm(L.o, oh16, m->nh * m->dv, 0, 0, parts_o, m->H, 0, m->ks_o, pstride_o);
-    vx_record_error(vx_launch_mla_resid(h, parts_o, m->ks_o, pstride_o, m->H, batch, mask, st));
+    if (finish) vx_record_error(vx_launch_mla_resid(h, parts_o, m->ks_o, pstride_o, m->H, batch, mask, st));
+}
+
+}  // namespace
+
+extern "C" {
+
+void velox_hip_mla_layer_step(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, hipStream_t st) {
+    if (!m || layer >= m->cfg.num_layers || batch == 0 || batch > m->B) {
+        vx_record_error(hipErrorInvalidValue);
+        return;
+    }
+    vm_layer(m, layer, batch, mask, false, true, st);
+}
+
+void velox_hip_mla_decode_step(VeloxHipMla* m, uint32_t batch, uint64_t mask, hipStream_t st) {
+    if (!m || batch == 0 || batch > m->B) {
+        vx_record_error(hipErrorInvalidValue);
+        return;
+    }
+    const uint32_t n = m->cfg.num_layers;
+    for (uint32_t l = 0; l < n; ++l) vm_layer(m, l, batch, mask, l > 0, l + 1 == n, st);
 }
 
 double velox_hip_mla_step_bytes(const VeloxHipMla* m, uint32_t batch, uint64_t pos) {
@@ -537,13 +574,15 @@ double velox_hip_mla_step_bytes(const VeloxHipMla* m, uint32_t batch, uint64_t p
     return (double)per_layer_w + latent + act;
 }
 
-int velox_hip_mla_run(const char* which, uint32_t batch, uint32_t context_len, uint32_t warmup, uint32_t steps,
-                      uint64_t seed, VeloxHipMlaRunReport* rep) {
+int velox_hip_mla_run(const char* which, uint32_t batch, uint32_t context_len, uint32_t num_layers, uint32_t warmup,
+                      uint32_t steps, uint64_t seed, VeloxHipMlaRunReport* rep) {
     if (!rep || batch == 0 || steps == 0) return VELOX_HIP_EINVAL;
     std::memset(rep, 0, sizeof(*rep));
     VeloxHipMlaConfig cfg;
     int rc = velox_hip_mla_builtin_config(which, context_len + 1, batch, &cfg);
     if (rc) return rc;
+    const bool stack = num_layers > 1;  // the decode step over a stack of layers, else one layer step
+    if (stack) cfg.num_layers = num_layers;
     VeloxHipMla* m = nullptr;
     rc = velox_hip_mla_create(&cfg, &m);
     if (rc) return rc;
@@ -554,7 +593,8 @@ int velox_hip_mla_run(const char* which, uint32_t batch, uint32_t context_len, u
     hipEventCreate(&e1);
     rc = velox_hip_mla_synthesize(m, seed, 0.02f, 0.0f, st);
     for (uint32_t b = 0; b < batch && !rc; ++b) {
-        rc = velox_hip_mla_fill_cache(m, 0, b, context_len, seed, 1.0f, st);
+        for (uint32_t l = 0; l < cfg.num_layers && !rc; ++l)
+            rc = velox_hip_mla_fill_cache(m, l, b, context_len, seed, 1.0f, st);
         if (!rc) rc = velox_hip_mla_set_position(m, b, context_len, st);
     }
     VeloxHipMlaBuffers buf;
@@ -569,7 +609,8 @@ int velox_hip_mla_run(const char* which, uint32_t batch, uint32_t context_len, u
     if (!rc) {
         hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
         if (e == hipSuccess) {
-            velox_hip_mla_layer_step(m, 0, batch, 1ULL, st);
+            if (stack) velox_hip_mla_decode_step(m, batch, 1ULL, st);
+            else velox_hip_mla_layer_step(m, 0, batch, 1ULL, st);
             e = hipStreamEndCapture(st, &graph);
         }
         if (e == hipSuccess) e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
@@ -588,7 +629,7 @@ int velox_hip_mla_run(const char* which, uint32_t batch, uint32_t context_len, u
         rep->wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - w0).count();
         float ms = 0.0f;
         hipEventElapsedTime(&ms, e0, e1);
-        rep->us_per_layer = 1000.0 * ms / steps;
+        rep->us_per_layer = 1000.0 * ms / steps / cfg.num_layers;
         rep->bytes_per_layer = velox_hip_mla_step_bytes(m, batch, context_len);
         rep->hbm_gbps = rep->us_per_layer > 0 ? rep->bytes_per_layer / (rep->us_per_layer * 1e3) : 0.0;
     }

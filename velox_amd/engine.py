@@ -349,6 +349,12 @@ class MlaEngine:
         L.check(L.hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
         L.check(self.lib.velox_hip_last_error(), "mla_layer_step")
 
+    def decode_step(self, batch: int = 1) -> None:
+        """Every layer in order (velox_hip_mla_decode_step)."""
+        self.lib.velox_hip_mla_decode_step(self._m, batch, 1, None)
+        L.check(L.hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
+        L.check(self.lib.velox_hip_last_error(), "mla_decode_step")
+
     def step_bytes(self, batch: int, pos: int) -> float:
         return float(self.lib.velox_hip_mla_step_bytes(self._m, batch, pos))
 
@@ -365,9 +371,10 @@ class MlaEngine:
 
 
 def mla_run(which: str = "deepseek_v3_mla", batch: int = 1, context_len: int = 4096, warmup: int = 5,
-            steps: int = 50, seed: int = 1234) -> dict:
-    """velox_hip_mla_run: synthesize, seed the latent context, time graph-replayed layer steps."""
+            steps: int = 50, seed: int = 1234, layers: int = 1) -> dict:
+    """velox_hip_mla_run: synthesize `layers` layers, seed the latent contexts, time graph-replayed
+    steps (the decode step over the stack when layers > 1); us_per_layer = step time / layers."""
     rep = L.MlaRunReport()
-    L.check(L.load().velox_hip_mla_run(which.encode(), batch, context_len, warmup, steps, seed, C.byref(rep)),
-            "velox_hip_mla_run")
+    L.check(L.load().velox_hip_mla_run(which.encode(), batch, context_len, layers, warmup, steps, seed,
+                                       C.byref(rep)), "velox_hip_mla_run")
     return {f: getattr(rep, f) for f, _ in rep._fields_}
