@@ -54,7 +54,7 @@ struct VxMlaAttnArgs {
     float qscale;               // softmax scale * log2(e)
     const uint16_t* cache;      // bf16 [batch][s_cap][LR + DR]
     uint64_t cache_bstride;
-    float* part_o;              // [batch][nh][splits][LR]
+    uint16_t* part_o;           // fp16 [batch][nh][splits][LR]: each split's output divided by its l
     float* part_ml;             // [batch][nh][splits][2]
     uint64_t active_mask;
 };
@@ -64,7 +64,7 @@ hipError_t vx_launch_f8_synth_scales(float* scales, uint32_t rows, uint32_t cols
 hipError_t vx_launch_f8_pack(const VxF8Dest& d, hipStream_t st);
 hipError_t vx_launch_mla_prep(const VxMlaPrepArgs& a, uint32_t batch, hipStream_t st);
 hipError_t vx_launch_mla_attn(const VxMlaAttnArgs& a, uint32_t lr, uint32_t dr, uint32_t batch, hipStream_t st);
-hipError_t vx_launch_mla_merge(const float* part_o, const float* part_ml, uint32_t nh, uint32_t splits, uint32_t lr,
+hipError_t vx_launch_mla_merge(const uint16_t* part_o, const float* part_ml, uint32_t nh, uint32_t splits, uint32_t lr,
                                float* ctx, uint32_t batch, uint64_t mask, hipStream_t st);
 hipError_t vx_launch_mla_resid(float* h, const float* parts, uint32_t nparts, uint64_t pstride, uint32_t n,
                                uint32_t batch, uint64_t mask, hipStream_t st);

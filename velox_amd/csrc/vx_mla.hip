@@ -734,7 +734,8 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
     for (uint32_t ci = 0; ci < n_chunks; ++ci) chunk_step(ci);
 
     // ---- the split's partial: o_acc[nb][i] is head 4 grp + i of the wave, latent dim
-    // 16 (ls NBW + nb) + col ----
+    // 16 (ls NBW + nb) + col; stored as o / l in fp16 (a convex combination of latent rows, so
+    // within their range; an empty split stores 0) ----
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
     const uint32_t hbase = (blockIdx.z * W + (uint32_t)hg) * 16u;
@@ -745,20 +746,34 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        float* po = a.part_o + ((bh + hbase + 4u * grp + i) * a.splits + sp) * LR + 16 * ls * NBW + col;
+        const float lh = __shfl(l_run, 4 * grp + i);  // l of head 4 grp + i (lanes 0..15 hold heads 0..15)
+        const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
+        uint16_t* po = a.part_o + ((bh + hbase + 4u * grp + i) * a.splits + sp) * LR + 16 * ls * NBW + col;
 #pragma unroll
-        for (int nb = 0; nb < NBW; ++nb) po[16 * nb] = o_acc[nb][i];
+        for (int nb = 0; nb < NBW; ++nb) po[16 * nb] = __builtin_bit_cast(uint16_t, (_Float16)(o_acc[nb][i] * inv));
     }
 }
 
 // LSE merge of the split partials of one (head, sequence) -> ctx[b][h][LR] fp32. A workgroup covers
-// 128 latent dimensions of its (head, sequence) (grid z), one per thread, with 32 splits' loads in
-// flight ahead of their adds (the adds stay in split order).
-__global__ __launch_bounds__(128) void vx_mla_merge_kernel(const float* part_o, const float* part_ml, uint32_t nh,
+// 128 latent dimensions of its (head, sequence) (grid z), one per thread. The first NL splits'
+// loads are issued before the split weights are computed (they do not depend on them), then NL at
+// a time ahead of their adds (the adds stay in split order); NL = 8 for at most 8 splits, so no
+// load repeats a clamped split.
+template <int NL>
+__global__ __launch_bounds__(128) void vx_mla_merge_kernel(const uint16_t* part_o, const float* part_ml, uint32_t nh,
                                                            uint32_t splits, uint32_t lr, float* ctx, uint64_t mask) {
     if ((mask & 1ULL) == 0ULL) return;
     __shared__ float s_w[64];
     const size_t bh = (size_t)blockIdx.y * nh + blockIdx.x;
+    const uint16_t* po = part_o + bh * splits * lr;
+    const uint32_t d = blockIdx.z * 128u + threadIdx.x, dc = min(d, lr - 1u);
+    float v[NL];
+    auto load = [&](uint32_t j0) {
+#pragma unroll
+        for (uint32_t u = 0; u < (uint32_t)NL; ++u)
+            v[u] = (float)__builtin_bit_cast(_Float16, po[(size_t)min(j0 + u, splits - 1u) * lr + dc]);
+    };
+    load(0u);
     const float* pml = part_ml + bh * splits * 2u;
     if (threadIdx.x < 64) {
         const int j = threadIdx.x;
@@ -771,22 +786,17 @@ __global__ __launch_bounds__(128) void vx_mla_merge_kernel(const float* part_o, 
         float Ls = lj * wj;
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) Ls += __shfl_xor(Ls, off);
-        s_w[j] = Ls > 0.0f ? wj / Ls : 0.0f;
+        s_w[j] = Ls > 0.0f ? wj * lj / Ls : 0.0f;  // the partials are o_j / l_j
     }
     __syncthreads();
-    const float* po = part_o + bh * splits * lr;
-    const uint32_t d = blockIdx.z * 128u + threadIdx.x;
-    if (d >= lr) return;
     float acc = 0.0f;
-    for (uint32_t j0 = 0; j0 < splits; j0 += 32u) {
-        float v[32];
+    for (uint32_t j0 = 0; j0 < splits; j0 += (uint32_t)NL) {
+        if (j0) load(j0);
 #pragma unroll
-        for (uint32_t u = 0; u < 32; ++u) v[u] = po[(size_t)min(j0 + u, splits - 1u) * lr + d];
-#pragma unroll
-        for (uint32_t u = 0; u < 32; ++u)
+        for (uint32_t u = 0; u < (uint32_t)NL; ++u)
             if (j0 + u < splits) acc += s_w[j0 + u] * v[u];
     }
-    ctx[bh * lr + d] = acc;
+    if (d < lr) ctx[bh * lr + d] = acc;
 }
 
 // h[b] += the K-split partials of W_o, in split order.
@@ -833,11 +843,14 @@ hipError_t vx_launch_mla_attn(const VxMlaAttnArgs& a, uint32_t lr, uint32_t dr, 
     return hipErrorInvalidValue;
 }
 
-hipError_t vx_launch_mla_merge(const float* part_o, const float* part_ml, uint32_t nh, uint32_t splits, uint32_t lr,
+hipError_t vx_launch_mla_merge(const uint16_t* part_o, const float* part_ml, uint32_t nh, uint32_t splits, uint32_t lr,
                                float* ctx, uint32_t batch, uint64_t mask, hipStream_t st) {
     if (splits == 0 || splits > 64 || lr == 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(vx_mla_merge_kernel, dim3(nh, batch, (lr + 127u) / 128u), dim3(128), 0, st, part_o, part_ml, nh,
-                       splits, lr, ctx, mask);
+    const dim3 grid(nh, batch, (lr + 127u) / 128u);
+    if (splits <= 8u)
+        hipLaunchKernelGGL(vx_mla_merge_kernel<8>, grid, dim3(128), 0, st, part_o, part_ml, nh, splits, lr, ctx, mask);
+    else
+        hipLaunchKernelGGL(vx_mla_merge_kernel<32>, grid, dim3(128), 0, st, part_o, part_ml, nh, splits, lr, ctx, mask);
     return hipGetLastError();
 }
 

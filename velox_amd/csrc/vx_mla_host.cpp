@@ -264,7 +264,7 @@ int velox_hip_mla_create(const VeloxHipMlaConfig* cfg, VeloxHipMla** out) {
     m->a_parts_a = take((uint64_t)m->ks_a * B * m->na * 4);
     m->a_q32 = take(B * m->nh * m->dq * 4);
     m->a_qabs = take(B * m->nh * m->lr * 4);
-    m->a_po = take(B * m->nh * splits * m->lr * 4);
+    m->a_po = take(B * m->nh * splits * m->lr * 2);
     m->a_pml = take(B * m->nh * splits * 2 * 4);
     m->a_ctx = take(B * m->nh * m->lr * 4);
     m->a_oh = take(B * m->nh * m->dv * 4);
@@ -507,7 +507,7 @@ void vm_layer(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, boo
     float* qabs = vm_act(m, m->a_qabs);
     gemm(L.ukt, q32, m->nh * m->dq, m->dq, 1, qabs, m->nh * m->lr, m->lr, 1, 0);
     // 6. attention over the latent cache, split over positions; 7. merge
-    float* po = vm_act(m, m->a_po);
+    uint16_t* po = (uint16_t*)vm_act(m, m->a_po);
     float* pml = vm_act(m, m->a_pml);
     float* ctx = vm_act(m, m->a_ctx);
     {
@@ -650,7 +650,7 @@ int velox_hip_mla_run(const char* which, uint32_t batch, uint32_t context_len, u
         a.qscale = m->scale * 1.4426950408889634f;
         a.cache = buf.latent_cache;
         a.cache_bstride = (uint64_t)m->s_cap * m->R;
-        a.part_o = vm_act(m, m->a_po);
+        a.part_o = (uint16_t*)vm_act(m, m->a_po);
         a.part_ml = vm_act(m, m->a_pml);
         a.active_mask = 1;
         const int reps = 20;
