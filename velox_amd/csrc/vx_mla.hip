@@ -526,14 +526,23 @@ __global__ __launch_bounds__(1024) void vx_mla_prep_kernel(VxMlaPrepArgs a) {
 }
 
 template <int LR, int DR, int W, int LS>
-constexpr size_t vx_mla_attn_lds() {  // K rows, dimension-major V, the W head groups' q operands
-    return (size_t)32 * (LR + DR + 8) * 2 + (size_t)LR * 40 * 2 + (size_t)(LR / 8) * 32 +
-           (size_t)W * ((LR + DR) / 32) * 64 * 16;
+constexpr size_t vx_mla_attn_lds() {  // the chunk's rows [c | kr], the W head groups' q operands
+    return (size_t)32 * (LR + DR + 8) * 2 + (size_t)W * ((LR + DR) / 32) * 64 * 16;
+}
+
+typedef short vm_s4 __attribute__((ext_vector_type(4)));
+
+// Four 16-bit values per lane from LDS, transposed within each 16-lane group: lane i of a group
+// receives element i % 4 of the words that lanes 4 e + i / 4 (e = 0..3) address (ds_read_b64_tr_b16).
+__device__ __forceinline__ vm_s4 vm_lds_tr4(const _Float16* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) vm_s4*)p);
 }
 
 // Absorbed MLA attention of one (split, sequence, group of 16 W heads). The split's positions go
-// through LDS in chunks of 32: the bf16 latent rows are converted to fp16 once, as rows for the
-// scores and dimension-major for P.V. LS waves share each 16 heads: every one of them computes the
+// through LDS in chunks of 32: the bf16 latent rows are converted to fp16 once, as rows; the scores
+// read them as rows and P.V reads the latent part transposed (ds_read_b64_tr_b16: the 8 positions
+// of one dimension that a lane's MFMA operand takes, from the row layout, with no transposed copy).
+// LS waves share each 16 heads: every one of them computes the
 // heads' scores S^T[pos][head] = [c | kr] . [q_abs | rope(q_rope)] on v_mfma_f32_16x16x32_f16 (the q
 // operands, built once, wait in LDS) and the log2-domain online softmax, and accumulates its 1 / LS
 // of the latent dimensions of O[head][latent] += P c on MFMA (fewer registers: two waves per SIMD).
@@ -541,12 +550,11 @@ constexpr size_t vx_mla_attn_lds() {  // K rows, dimension-major V, the W head g
 template <int LR, int DR, int W, int LS>
 __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a) {
     if ((a.active_mask & 1ULL) == 0ULL) return;
-    constexpr int R = LR + DR, NCK = R / 32, NB = LR / 16, NBW = NB / LS, KP = R + 8, VP = 40, NT = 64 * W * LS;
+    constexpr int R = LR + DR, NCK = R / 32, NB = LR / 16, NBW = NB / LS, KP = R + 8, NT = 64 * W * LS;
     static_assert(NB % LS == 0, "whole 16-dimension blocks per wave");
     extern __shared__ __align__(16) unsigned char vm_smem[];
-    _Float16* k_s = (_Float16*)vm_smem;        // [32][KP]: rows [c | kr]
-    _Float16* v_s = k_s + 32 * KP;             // latent dim r at voff(r); slot 8j + e holds vrow(j, e)
-    vm_h8* q_s = (vm_h8*)(vm_smem + (size_t)32 * KP * 2 + (size_t)LR * 40 * 2 + (size_t)(LR / 8) * 32);  // [W][NCK][64]
+    _Float16* k_s = (_Float16*)vm_smem;                      // [32][KP]: rows [c | kr]
+    vm_h8* q_s = (vm_h8*)(vm_smem + (size_t)32 * KP * 2);  // [W][NCK][64]
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hg = wave / LS, ls = wave % LS;  // head group of the workgroup, latent part
     const int col = lane & 15, grp = lane >> 4;
@@ -560,33 +568,16 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
     const uint32_t n_chunks = t1 > t0 ? (t1 - t0 + 31u) >> 5 : 0u;
     const uint16_t* cb_base = a.cache + (size_t)b * a.cache_bstride;
 
-    // ---- the chunk's rows into registers (rows clamped to pos: past t1 they are masked). Latent
-    // units: slot group j (positions 4j..4j+3 and 16+4j..16+4j+3) x 8 dimensions, 8 row loads each;
-    // RoPE units: one row x 8 dimensions (the unit -> (j, db) map is below) ----
-    constexpr int NVU = (4 * (LR / 8) + NT - 1) / NT, NRU = (32 * (DR / 8) + NT - 1) / NT;
-    // one register set: chunk i + 1 is loaded while chunk i is computed (a second set, two chunks
-    // ahead, needs 255 registers and measured slower: 73.9 against 70.3 us at 16 sequences)
-    uint4 kv[NVU][8], kq[NRU];
-    auto vrow = [](int j, int e) { return (uint32_t)(e < 4 ? 4 * j + e : 16 + 4 * j + (e - 4)); };
-    // unit un -> (slot group j, 8-dimension block db): 8 consecutive lanes take 2 slot groups x 4
-    // blocks, so their 16-byte stores into k_s hit 8 different 16-byte bank groups; voff shifts
-    // every 8 latent rows by 32 more bytes, which does the same for the transposed stores into v_s
-    // and keeps the P.V operand reads (16 consecutive rows) conflict-free
-    auto unit_j = [](int un) { return (un & 1) | (((un >> 3) & 1) << 1); };
-    auto unit_db = [](int un) { return ((un >> 1) & 3) | ((un >> 4) << 2); };
-    auto voff = [](int r) { return r * VP + 16 * (r >> 3); };
+    // ---- the chunk's rows into registers (rows clamped to pos: past t1 they are masked), one
+    // register set: chunk i + 1 is loaded while chunk i is computed. Unit un = 16-byte block un % (R / 8)
+    // of row un / (R / 8): consecutive lanes read and write consecutive 16 bytes of a row ----
+    constexpr int RB = R / 8, NU = (32 * RB + NT - 1) / NT;
+    uint4 kr[NU];
     auto load_chunk = [&](uint32_t cb) {
 #pragma unroll
-        for (int u = 0; u < NVU; ++u) {
-            const int un = min(tid + u * NT, 4 * (LR / 8) - 1), j = unit_j(un), db = unit_db(un);
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                kv[u][e] = *(const uint4*)(cb_base + (size_t)min(cb + vrow(j, e), pos) * R + 8 * db);
-        }
-#pragma unroll
-        for (int u = 0; u < NRU; ++u) {
-            const int un = min(tid + u * NT, 32 * (DR / 8) - 1), r = un / (DR / 8), db = LR / 8 + un % (DR / 8);
-            kq[u] = *(const uint4*)(cb_base + (size_t)min(cb + (uint32_t)r, pos) * R + 8 * db);
+        for (int u = 0; u < NU; ++u) {
+            const int un = min(tid + u * NT, 32 * RB - 1), r = un / RB, db = un % RB;
+            kr[u] = *(const uint4*)(cb_base + (size_t)min(cb + (uint32_t)r, pos) * R + 8 * db);
         }
     };
     load_chunk(t0 < len ? t0 : pos & ~31u);
@@ -650,32 +641,9 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
             return h;
         };
 #pragma unroll
-        for (int u = 0; u < NVU; ++u) {
+        for (int u = 0; u < NU; ++u) {
             const int un = tid + u * NT;
-            if (un < 4 * (LR / 8)) {
-                const int j = unit_j(un), db = unit_db(un);
-                vm_h8 hv[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    hv[e] = to_h8(kv[u][e]);
-                    *(vm_h8*)(k_s + vrow(j, e) * KP + 8 * db) = hv[e];
-                }
-#pragma unroll
-                for (int d = 0; d < 8; ++d) {
-                    vm_h8 t;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) t[e] = hv[e][d];
-                    *(vm_h8*)(v_s + voff(8 * db + d) + 8 * j) = t;
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < NRU; ++u) {
-            const int un = tid + u * NT;
-            if (un < 32 * (DR / 8)) {
-                const int r = un / (DR / 8), db = LR / 8 + un % (DR / 8);
-                *(vm_h8*)(k_s + r * KP + 8 * db) = to_h8(kq[u]);
-            }
+            if (un < 32 * RB) *(vm_h8*)(k_s + (un / RB) * KP + 8 * (un % RB)) = to_h8(kr[u]);
         }
         __syncthreads();
         if (ci + 1u < n_chunks) load_chunk(cb + 32u);
@@ -725,9 +693,14 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
                 for (int nb = 0; nb < NBW; ++nb) o_acc[nb][i] *= ai;
             }
         }
+        // B operand of latent block nb: lane (dimension col, group grp) takes positions 4 grp + e and
+        // 16 + 4 grp + e (e = 0..3), the positions of pop's elements; lane j of the group addresses
+        // row 4 grp + j / 4 (+ 16), dimensions 4 (j % 4) .. + 3 of the block
+        const _Float16* vb = k_s + (4 * grp + (col >> 2)) * KP + 16 * ls * NBW + 4 * (col & 3);
 #pragma unroll
         for (int nb = 0; nb < NBW; ++nb) {
-            const vm_h8 vop = *(const vm_h8*)(v_s + voff(16 * (ls * NBW + nb) + col) + 8 * grp);
+            const vm_s4 lo = vm_lds_tr4(vb + 16 * nb), hi = vm_lds_tr4(vb + 16 * KP + 16 * nb);
+            const vm_h8 vop = __builtin_bit_cast(vm_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
             o_acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, vop, o_acc[nb], 0, 0, 0);
         }
     };
