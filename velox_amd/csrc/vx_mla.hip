@@ -532,6 +532,8 @@ constexpr size_t vx_mla_attn_lds() {  // the chunk's rows [c | kr], the W head g
 
 typedef short vm_s4 __attribute__((ext_vector_type(4)));
 
+constexpr float kMlaLazy = 8.0f;  // log2 headroom of the attention's stale running maximum
+
 // Four 16-bit values per lane from LDS, transposed within each 16-lane group: lane i of a group
 // receives element i % 4 of the words that lanes 4 e + i / 4 (e = 0..3) address (ds_read_b64_tr_b16).
 __device__ __forceinline__ vm_s4 vm_lds_tr4(const _Float16* p) {
@@ -670,10 +672,12 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
             }
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
+        // lazy rescale: the reference maximum m_run moves only when a score exceeds it by more than
+        // 2^kMlaLazy (log2 units), so p = 2^(s - m_run) <= 2^kMlaLazy stays well inside fp16 and
+        // the accumulators are rescaled only on such a jump; before the first finite maximum they
+        // are still zero
+        const float m_new = (m_run == -INFINITY || mx > m_run + kMlaLazy) ? mx : m_run;
         const float alpha = m_run == -INFINITY ? 0.0f : vm_exp2(m_run - m_new);
-        // the accumulators change only where a running maximum grew (alpha < 1); before the first
-        // finite maximum they are still zero
         const bool grew = m_run != -INFINITY && m_new != m_run;
         float lt = 0.0f;
         vm_h8 pop;
