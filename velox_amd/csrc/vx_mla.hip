@@ -525,11 +525,14 @@ __global__ __launch_bounds__(1024) void vx_mla_prep_kernel(VxMlaPrepArgs a) {
     }
 }
 
-// QR: the q operands stay in each wave's registers (built by every wave; for splits of many chunks),
-// else in LDS (each of the LS waves of a head group builds 1 / LS of them; for few chunks)
+// QR (splits of many chunks): the LS waves of a head group split the scores' dimensions, each keeping
+// its share of the q operands in registers, and add their partial scores through LDS. Otherwise
+// (few chunks) every wave computes the full scores from q operands in LDS, of which each of the LS
+// waves builds 1 / LS.
 template <int LR, int DR, int W, int LS, bool QR>
-constexpr size_t vx_mla_attn_lds() {  // the chunk's rows [c | kr], the W head groups' q operands
-    return (size_t)32 * (LR + DR + 8) * 2 + (QR ? 0 : (size_t)W * ((LR + DR) / 32) * 64 * 16);
+constexpr size_t vx_mla_attn_lds() {  // the chunk's rows [c | kr]; partial scores or q operands
+    return (size_t)32 * (LR + DR + 8) * 2 +
+           (QR ? (size_t)W * LS * 2 * 64 * 16 : (size_t)W * ((LR + DR) / 32) * 64 * 16);
 }
 
 typedef short vm_s4 __attribute__((ext_vector_type(4)));
@@ -559,6 +562,9 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
     extern __shared__ __align__(16) unsigned char vm_smem[];
     _Float16* k_s = (_Float16*)vm_smem;                      // [32][KP]: rows [c | kr]
     vm_h8* q_s = (vm_h8*)(vm_smem + (size_t)32 * KP * 2);  // !QR: [W][NCK][64]
+    vm_f4* ps_s = (vm_f4*)(vm_smem + (size_t)32 * KP * 2);  // QR: partial scores [W LS][2][64]
+    constexpr int NCH = QR ? NCK / LS : NCK;                 // 32-dimension chunks of a wave's scores
+    static_assert(!QR || NCK % LS == 0, "whole 32-dimension chunks per wave");
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hg = wave / LS, ls = wave % LS;  // head group of the workgroup, latent part
     const int col = lane & 15, grp = lane >> 4;
@@ -590,13 +596,15 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
     // consecutive dimensions of a 32-dimension chunk come as vector loads (the RoPE part's 8 stay
     // within one half of the rotation). In registers (QR) they stop being a quarter of the chunk
     // loop's LDS traffic; in LDS (visible after the first chunk's barrier) each wave builds 1 / LS ----
-    vm_h8 qreg[QR ? NCK : 1];
+    vm_h8 qreg[QR ? NCH : 1];
     {
         const float* qa = a.qabs + ((size_t)b * a.nh + head) * LR;
         const float* qr = a.q32 + (size_t)b * a.nh * a.dq + (size_t)head * a.dq + a.dn;
         const float2* rp = a.rope + (size_t)pos * (DR / 2);
 #pragma unroll
-        for (int c = QR ? 0 : ls; c < NCK; c += QR ? 1 : LS) {
+        for (int cc = 0; cc < (QR ? NCH : NCK); cc += QR ? 1 : LS) {  // compile-time register index
+            const int c = QR ? ls * NCH + cc : cc + ls;
+            if (!QR && c >= NCK) break;
             const int d0 = 32 * c + 8 * grp;
             float v[8];
             if (d0 < LR) {
@@ -623,7 +631,7 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
             vm_h8 q;
 #pragma unroll
             for (int e = 0; e < 8; ++e) q[e] = (_Float16)(v[e] * a.qscale);
-            if constexpr (QR) qreg[c] = q;
+            if constexpr (QR) qreg[cc] = q;
             else q_s[(hg * NCK + c) * 64 + lane] = q;
         }
     }
@@ -656,12 +664,26 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
         // scores: sc[bb][i] = S[position cb + 16 bb + 4 grp + i][head col]
         vm_f4 sc[2] = {vm_f4{0.f, 0.f, 0.f, 0.f}, vm_f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-        for (int c = 0; c < NCK; ++c) {
-            const vm_h8 qop = QR ? qreg[QR ? c : 0] : q_s[(hg * NCK + c) * 64 + lane];
+        for (int cc = 0; cc < NCH; ++cc) {
+            const int c = QR ? ls * NCH + cc : cc;
+            const vm_h8 qop = QR ? qreg[QR ? cc : 0] : q_s[(hg * NCK + c) * 64 + lane];
 #pragma unroll
             for (int bb = 0; bb < 2; ++bb) {
                 const vm_h8 kop = *(const vm_h8*)(k_s + (16 * bb + col) * KP + 32 * c + 8 * grp);
                 sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop, sc[bb], 0, 0, 0);
+            }
+        }
+        if constexpr (QR) {
+            // the head group's LS partial scores, added in ls order by every wave (the same sums)
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb) ps_s[(wave * 2 + bb) * 64 + lane] = sc[bb];
+            __syncthreads();
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb) {
+                vm_f4 t = vm_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int l = 0; l < LS; ++l) t += ps_s[((hg * LS + l) * 2 + bb) * 64 + lane];
+                sc[bb] = t;
             }
         }
         float pr[8];
