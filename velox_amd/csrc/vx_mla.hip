@@ -525,14 +525,9 @@ __global__ __launch_bounds__(1024) void vx_mla_prep_kernel(VxMlaPrepArgs a) {
     }
 }
 
-// QR (splits of many chunks): the LS waves of a head group split the scores' dimensions, each keeping
-// its share of the q operands in registers, and add their partial scores through LDS. Otherwise
-// (few chunks) every wave computes the full scores from q operands in LDS, of which each of the LS
-// waves builds 1 / LS.
-template <int LR, int DR, int W, int LS, bool QR>
-constexpr size_t vx_mla_attn_lds() {  // the chunk's rows [c | kr]; partial scores or q operands
-    return (size_t)32 * (LR + DR + 8) * 2 +
-           (QR ? (size_t)W * LS * 2 * 64 * 16 : (size_t)W * ((LR + DR) / 32) * 64 * 16);
+template <int LR, int DR, int W, int LS>
+constexpr size_t vx_mla_attn_lds() {  // the chunk's rows [c | kr], the waves' partial scores
+    return (size_t)32 * (LR + DR + 8) * 2 + (size_t)W * LS * 2 * 64 * 16;
 }
 
 typedef short vm_s4 __attribute__((ext_vector_type(4)));
@@ -549,22 +544,21 @@ __device__ __forceinline__ vm_s4 vm_lds_tr4(const _Float16* p) {
 // through LDS in chunks of 32: the bf16 latent rows are converted to fp16 once, as rows; the scores
 // read them as rows and P.V reads the latent part transposed (ds_read_b64_tr_b16: the 8 positions
 // of one dimension that a lane's MFMA operand takes, from the row layout, with no transposed copy).
-// LS waves share each 16 heads: every one of them computes the
-// heads' scores S^T[pos][head] = [c | kr] . [q_abs | rope(q_rope)] on v_mfma_f32_16x16x32_f16 (the q
-// operands, built once, stay in registers) and the log2-domain online softmax, and accumulates its 1 / LS
-// of the latent dimensions of O[head][latent] += P c on MFMA (fewer registers: two waves per SIMD).
-// Writes the split's (m, l, o).
-template <int LR, int DR, int W, int LS, bool QR>
+// LS waves share each 16 heads: each computes the heads' partial scores S^T[pos][head] = [c | kr] .
+// [q_abs | rope(q_rope)] over 1 / LS of the dimensions on v_mfma_f32_16x16x32_f16 (its q operands,
+// built once, stay in registers), the partials meet in LDS, every wave runs the log2-domain online
+// softmax on the same sums and accumulates its 1 / LS of the latent dimensions of
+// O[head][latent] += P c on MFMA (fewer registers: two waves per SIMD). Writes the split's (m, l, o).
+template <int LR, int DR, int W, int LS>
 __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnArgs a) {
     if ((a.active_mask & 1ULL) == 0ULL) return;
     constexpr int R = LR + DR, NCK = R / 32, NB = LR / 16, NBW = NB / LS, KP = R + 8, NT = 64 * W * LS;
     static_assert(NB % LS == 0, "whole 16-dimension blocks per wave");
     extern __shared__ __align__(16) unsigned char vm_smem[];
     _Float16* k_s = (_Float16*)vm_smem;                      // [32][KP]: rows [c | kr]
-    vm_h8* q_s = (vm_h8*)(vm_smem + (size_t)32 * KP * 2);  // !QR: [W][NCK][64]
-    vm_f4* ps_s = (vm_f4*)(vm_smem + (size_t)32 * KP * 2);  // QR: partial scores [W LS][2][64]
-    constexpr int NCH = QR ? NCK / LS : NCK;                 // 32-dimension chunks of a wave's scores
-    static_assert(!QR || NCK % LS == 0, "whole 32-dimension chunks per wave");
+    vm_f4* ps_s = (vm_f4*)(vm_smem + (size_t)32 * KP * 2);  // partial scores [W LS][2][64]
+    constexpr int NCH = NCK / LS;                            // 32-dimension chunks of a wave's scores
+    static_assert(NCK % LS == 0, "whole 32-dimension chunks per wave");
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hg = wave / LS, ls = wave % LS;  // head group of the workgroup, latent part
     const int col = lane & 15, grp = lane >> 4;
@@ -594,17 +588,16 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
 
     // ---- q operands of head col: latent dims scaled, the RoPE part rotated, as fp16; each lane's 8
     // consecutive dimensions of a 32-dimension chunk come as vector loads (the RoPE part's 8 stay
-    // within one half of the rotation). In registers (QR) they stop being a quarter of the chunk
-    // loop's LDS traffic; in LDS (visible after the first chunk's barrier) each wave builds 1 / LS ----
-    vm_h8 qreg[QR ? NCH : 1];
+    // within one half of the rotation). Wave ls of a head group keeps the q chunks of its share of
+    // the score dimensions in registers ----
+    vm_h8 qreg[NCH];
     {
         const float* qa = a.qabs + ((size_t)b * a.nh + head) * LR;
         const float* qr = a.q32 + (size_t)b * a.nh * a.dq + (size_t)head * a.dq + a.dn;
         const float2* rp = a.rope + (size_t)pos * (DR / 2);
 #pragma unroll
-        for (int cc = 0; cc < (QR ? NCH : NCK); cc += QR ? 1 : LS) {  // compile-time register index
-            const int c = QR ? ls * NCH + cc : cc + ls;
-            if (!QR && c >= NCK) break;
+        for (int cc = 0; cc < NCH; ++cc) {  // compile-time register index
+            const int c = ls * NCH + cc;
             const int d0 = 32 * c + 8 * grp;
             float v[8];
             if (d0 < LR) {
@@ -631,8 +624,7 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
             vm_h8 q;
 #pragma unroll
             for (int e = 0; e < 8; ++e) q[e] = (_Float16)(v[e] * a.qscale);
-            if constexpr (QR) qreg[cc] = q;
-            else q_s[(hg * NCK + c) * 64 + lane] = q;
+            qreg[cc] = q;
         }
     }
 
@@ -665,15 +657,15 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
         vm_f4 sc[2] = {vm_f4{0.f, 0.f, 0.f, 0.f}, vm_f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int cc = 0; cc < NCH; ++cc) {
-            const int c = QR ? ls * NCH + cc : cc;
-            const vm_h8 qop = QR ? qreg[QR ? cc : 0] : q_s[(hg * NCK + c) * 64 + lane];
+            const int c = ls * NCH + cc;
+            const vm_h8 qop = qreg[cc];
 #pragma unroll
             for (int bb = 0; bb < 2; ++bb) {
                 const vm_h8 kop = *(const vm_h8*)(k_s + (16 * bb + col) * KP + 32 * c + 8 * grp);
                 sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop, sc[bb], 0, 0, 0);
             }
         }
-        if constexpr (QR) {
+        {
             // the head group's LS partial scores, added in ls order by every wave (the same sums)
 #pragma unroll
             for (int bb = 0; bb < 2; ++bb) ps_s[(wave * 2 + bb) * 64 + lane] = sc[bb];
@@ -821,31 +813,21 @@ hipError_t vx_launch_mla_prep(const VxMlaPrepArgs& a, uint32_t batch, hipStream_
     return hipGetLastError();
 }
 
-template <int LR, int DR, int W, int LS, bool QR>
-hipError_t vx_mla_attn_launch_q(const VxMlaAttnArgs& a, uint32_t batch, hipStream_t st) {
-    constexpr size_t lds = vx_mla_attn_lds<LR, DR, W, LS, QR>();
+template <int LR, int DR, int W, int LS>
+hipError_t vx_mla_attn_launch_t(const VxMlaAttnArgs& a, uint32_t batch, hipStream_t st) {
+    constexpr size_t lds = vx_mla_attn_lds<LR, DR, W, LS>();
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)vx_mla_attn_kernel<LR, DR, W, LS, QR>,
+        if (hipFuncSetAttribute((const void*)vx_mla_attn_kernel<LR, DR, W, LS>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
             (void)hipGetLastError();
             return hipErrorInvalidValue;
         }
         attr_set = true;
     }
-    hipLaunchKernelGGL((vx_mla_attn_kernel<LR, DR, W, LS, QR>), dim3(a.splits, batch, a.nh / (16u * W)),
+    hipLaunchKernelGGL((vx_mla_attn_kernel<LR, DR, W, LS>), dim3(a.splits, batch, a.nh / (16u * W)),
                        dim3(64 * W * LS), lds, st, a);
     return hipGetLastError();
-}
-
-// q operands in registers once a split spans 8 or more 32-position chunks (B=16 at 4096 positions:
-// 16 chunks, 56.3 -> 53.9 us); with 2-3 chunks (B=1: 64 splits) building all of them in every wave
-// costs more than it saves (18.2 -> 20.2 us)
-template <int LR, int DR, int W, int LS>
-hipError_t vx_mla_attn_launch_t(const VxMlaAttnArgs& a, uint32_t batch, hipStream_t st) {
-    const uint32_t chunks = ((a.s_max + a.splits - 1u) / a.splits + 31u) / 32u;
-    return chunks >= 8u ? vx_mla_attn_launch_q<LR, DR, W, LS, true>(a, batch, st)
-                        : vx_mla_attn_launch_q<LR, DR, W, LS, false>(a, batch, st);
 }
 
 hipError_t vx_launch_mla_attn(const VxMlaAttnArgs& a, uint32_t lr, uint32_t dr, uint32_t batch, hipStream_t st) {
