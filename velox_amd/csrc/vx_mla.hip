@@ -306,7 +306,93 @@ __global__ __launch_bounds__(64 * kFGWaves) void vx_f8gemv_kernel(VxF8GemmArgs a
     }
 }
 
+// The same structure for 2..16 sequences on the matrix cores: the workgroup stages its split's
+// activations of all 16 rows (zero past the batch) in LDS, fp16 [16][XR]; per k-tile a wave takes
+// the A operands of its two MFMAs (row col, k-elements 16 grp + 0..7 and + 8..15) from LDS and the B
+// operands from its weight word, then acc += block scale * the tile's product. KW waves per row tile
+// meet in LDS; the first writes 16 rows x the batch's sequences.
+template <int KW, bool XF32>
+__global__ __launch_bounds__(64 * kFGWaves) void vx_f8gemm_x_kernel(VxF8GemmArgs a) {
+    extern __shared__ __align__(16) unsigned char vm_smem[];
+    if ((a.active_mask & 1ULL) == 0ULL) return;
+    constexpr int TPW = kFGWaves / KW, D = KW == 8 ? 8 : 4;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, grp = lane >> 4;
+    const uint32_t g = blockIdx.z, ks = blockIdx.y, kw = (uint32_t)wave % KW, tw = (uint32_t)wave / KW;
+    const uint32_t rt = blockIdx.x * TPW + tw, rtc = min(rt, a.n_rt - 1u);
+    const uint32_t kt0 = ks * a.n_kt / gridDim.y, kt1 = (ks + 1u) * a.n_kt / gridDim.y;
+    const uint32_t w0 = kt0 + kw * (kt1 - kt0) / KW, w1 = kt0 + (kw + 1u) * (kt1 - kt0) / KW;
+    const uint4* W = a.codes + g * a.w_gstride + (size_t)rtc * a.n_kt * 64u + lane;
+    const float* S = a.scales + g * a.s_gstride + (size_t)rtc * a.n_kb;
+    const uint32_t wl = w1 > w0 ? w1 - 1u : w0;
+    uint4 wr[D];
+#pragma unroll
+    for (int u = 0; u < D; ++u) wr[u] = W[(size_t)min(w0 + (uint32_t)u, wl) * 64u];
+    // x rows 0..15 over the split's k-range -> LDS fp16, rows XR elements apart (16 bytes of padding
+    // per row: the 16 rows' operand reads fall in different banks)
+    uint4* xs = (uint4*)vm_smem;
+    const uint32_t n8 = (kt1 - kt0) * 8u, xr8 = n8 + 1u;  // 8-element units per row, row pitch
+    for (uint32_t i = (uint32_t)tid; i < 16u * n8; i += 64u * kFGWaves) {
+        const uint32_t m = i / n8, u = i % n8;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (m < a.batch) {
+            const size_t e = g * a.x_gstride + (size_t)m * a.ldx + (size_t)kt0 * 64u + 8u * u;
+            if constexpr (XF32) {
+                const float4 lo = *(const float4*)((const float*)a.x + e), hi = *(const float4*)((const float*)a.x + e + 4);
+                v = __builtin_bit_cast(uint4, vm_f32x8_to_h8(lo, hi));
+            } else {
+                v = *(const uint4*)((const uint16_t*)a.x + e);
+            }
+        }
+        xs[m * xr8 + u] = v;
+    }
+    __syncthreads();
+    vm_f4 acc = vm_f4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t base = w0; base < w1; base += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            const uint32_t kt = base + (uint32_t)u;
+            if (kt < w1) {
+                const uint32_t xi = (uint32_t)col * xr8 + (kt - kt0) * 8u + 2u * (uint32_t)grp;
+                const vm_h8 x0 = __builtin_bit_cast(vm_h8, xs[xi]), x1 = __builtin_bit_cast(vm_h8, xs[xi + 1u]);
+                const vm_h8 f0 = vm_fp8x8(wr[u].x, wr[u].y), f1 = vm_fp8x8(wr[u].z, wr[u].w);
+                vm_f4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, f0, vm_f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, f1, t, 0, 0, 0);
+                acc += S[kt >> 1] * t;
+            }
+            wr[u] = W[(size_t)min(kt + (uint32_t)D, wl) * 64u];
+        }
+    }
+    vm_f4* red = (vm_f4*)vm_smem;  // reuses x: every wave passed its last LDS read at the barrier below
+    if constexpr (KW > 1) {
+        __syncthreads();
+        red[(tw * KW + kw) * 64u + (uint32_t)lane] = acc;
+        __syncthreads();
+        if (kw != 0) return;
+        acc = vm_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < KW; ++w) acc += red[(tw * KW + (uint32_t)w) * 64u + (uint32_t)lane];
+    }
+    if (rt >= a.n_rt) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t m = 4u * (uint32_t)grp + (uint32_t)i;
+        if (m >= a.batch) continue;
+        const size_t o = g * a.y_gstride + (size_t)m * a.ldy + 16u * rt + (uint32_t)col;
+        if (a.y16) a.y16[o] = __builtin_bit_cast(uint16_t, (_Float16)acc[i]);
+        else a.y[o + (gridDim.y > 1u ? ks * a.pstride : 0u)] = acc[i];
+    }
+}
+
 namespace {
+
+template <int KW>
+void vx_f8gemm_x_launch_t(const VxF8GemmArgs& a, uint32_t groups, size_t lds, hipStream_t st) {
+    constexpr int TPW = kFGWaves / KW;
+    const dim3 grid((a.n_rt + TPW - 1) / TPW, a.ksplit, groups), block(64 * kFGWaves);
+    if (a.x_f32) hipLaunchKernelGGL((vx_f8gemm_x_kernel<KW, true>), grid, block, lds, st, a);
+    else hipLaunchKernelGGL((vx_f8gemm_x_kernel<KW, false>), grid, block, lds, st, a);
+}
 
 template <int KW>
 void vx_f8gemv_launch_t(const VxF8GemmArgs& a, uint32_t groups, size_t lds, hipStream_t st) {
@@ -336,22 +422,34 @@ hipError_t vx_launch_f8gemm(const VxF8GemmArgs& a, uint32_t groups, hipStream_t 
     if (a.ksplit > 1u && a.pstride < (uint64_t)a.batch * a.ldy) return hipErrorInvalidValue;
     if ((a.y16 != nullptr) == (a.y != nullptr) || (a.y16 && a.ksplit != 1u)) return hipErrorInvalidValue;
     if (a.add_y && (a.batch != 1u || a.ksplit != 1u || a.y16)) return hipErrorInvalidValue;
-    if (a.batch == 1u) {
-        // one sequence: the GEMV. Waves per row tile: the fewest giving >= 256 workgroups, as long
-        // as each wave keeps >= 2 k-tiles.
+    // up to 16 sequences: activations staged in LDS (one sequence: the GEMV, else the MFMA form), if
+    // the longest split's fp16 activations fit 64 KB (16 padded rows for the MFMA form; at least the
+    // waves' sums that reuse the space). Waves per row tile: the fewest giving >= 256 workgroups, as
+    // long as each wave keeps >= 2 k-tiles.
+    const size_t kspan = (a.n_kt + a.ksplit - 1u) / a.ksplit;  // k-tiles of the longest split
+    size_t lds = a.batch == 1u ? kspan * 128u : 16u * (kspan * 128u + 16u);
+    const size_t red = a.batch == 1u ? (size_t)kFGWaves * 16u * 4u : (size_t)kFGWaves * 64u * 16u;
+    if (lds < red) lds = red;
+    if (a.batch == 1u && lds > 64u * 1024u) return hipErrorInvalidValue;
+    if (a.batch <= 16u && lds <= 64u * 1024u) {
         const uint32_t kts = a.n_kt / a.ksplit;  // k-tiles of the shortest split
         auto wgs = [&](uint32_t kw) { return (a.n_rt + kFGWaves / kw - 1u) / (kFGWaves / kw) * a.ksplit * groups; };
         uint32_t kw = 1u;
         while (kw < (uint32_t)kFGWaves && wgs(kw) < 256u && kts / (2u * kw) >= 2u) kw *= 2u;
-        // fp16 x of the longest split; at least the waves' 16-row sums that reuse it
-        size_t lds = (size_t)((a.n_kt + a.ksplit - 1u) / a.ksplit) * 128u;
-        if (lds < (size_t)kFGWaves * 16u * 4u) lds = (size_t)kFGWaves * 16u * 4u;
-        if (lds > 64u * 1024u) return hipErrorInvalidValue;
-        switch (kw) {
-            case 1: vx_f8gemv_launch_t<1>(a, groups, lds, st); break;
-            case 2: vx_f8gemv_launch_t<2>(a, groups, lds, st); break;
-            case 4: vx_f8gemv_launch_t<4>(a, groups, lds, st); break;
-            default: vx_f8gemv_launch_t<8>(a, groups, lds, st); break;
+        if (a.batch == 1u) {
+            switch (kw) {
+                case 1: vx_f8gemv_launch_t<1>(a, groups, lds, st); break;
+                case 2: vx_f8gemv_launch_t<2>(a, groups, lds, st); break;
+                case 4: vx_f8gemv_launch_t<4>(a, groups, lds, st); break;
+                default: vx_f8gemv_launch_t<8>(a, groups, lds, st); break;
+            }
+        } else {
+            switch (kw) {
+                case 1: vx_f8gemm_x_launch_t<1>(a, groups, lds, st); break;
+                case 2: vx_f8gemm_x_launch_t<2>(a, groups, lds, st); break;
+                case 4: vx_f8gemm_x_launch_t<4>(a, groups, lds, st); break;
+                default: vx_f8gemm_x_launch_t<8>(a, groups, lds, st); break;
+            }
         }
         return hipGetLastError();
     }
