@@ -236,7 +236,9 @@ int velox_hip_mla_create(const VeloxHipMlaConfig* cfg, VeloxHipMla** out) {
 
     // split counts: ~512 workgroups for the two skinny GEMMs; attention ~256 workgroups with at
     // least 64 positions per split
-    const uint32_t tpw = 4 * vx_f8gemm_rows_per_wave(m->B);  // row tiles per GEMM workgroup
+    // row tiles per GEMM workgroup: 8 for the LDS-activation forms (up to 16 sequences), else the
+    // register form's 4 waves x rows per wave
+    const uint32_t tpw = m->B <= 16 ? 8u : 4 * vx_f8gemm_rows_per_wave(m->B);
     const uint32_t wg_a = (m->na / 16 + tpw - 1) / tpw, wg_o = (m->H / 16 + tpw - 1) / tpw;
     m->ks_a = (512 + wg_a - 1) / wg_a;
     if (m->ks_a > 16) m->ks_a = 16;  // the prep kernel folds at most 16 partials
