@@ -234,16 +234,17 @@ int velox_hip_mla_create(const VeloxHipMlaConfig* cfg, VeloxHipMla** out) {
     m->cache_layer_bytes = (uint64_t)m->B * m->s_cap * m->R * 2;
     m->cache_bytes = vm_align(m->cache_layer_bytes * c.num_layers);
 
-    // split counts: ~512 workgroups for the two skinny GEMMs; attention ~256 workgroups with at
+    // split counts: at most 512 workgroups for the two skinny GEMMs; attention ~256 workgroups with at
     // least 64 positions per split
     // row tiles per GEMM workgroup: 8 for the LDS-activation forms (up to 16 sequences), else the
     // register form's 4 waves x rows per wave
     const uint32_t tpw = m->B <= 16 ? 8u : 4 * vx_f8gemm_rows_per_wave(m->B);
     const uint32_t wg_a = (m->na / 16 + tpw - 1) / tpw, wg_o = (m->H / 16 + tpw - 1) / tpw;
-    m->ks_a = (512 + wg_a - 1) / wg_a;
+    // (at most 512 workgroups: one round of two per CU)
+    m->ks_a = wg_a >= 512 ? 1u : 512 / wg_a;
     if (m->ks_a > 16) m->ks_a = 16;  // the prep kernel folds at most 16 partials
     if (m->ks_a > m->H / 64) m->ks_a = m->H / 64;
-    m->ks_o = (512 + wg_o - 1) / wg_o;
+    m->ks_o = wg_o >= 512 ? 1u : 512 / wg_o;
     if (m->ks_o > 32) m->ks_o = 32;  // the next layer's RMSNorm folds at most 32 partials
     if (m->ks_o > m->nh * m->dv / 64) m->ks_o = m->nh * m->dv / 64;
     uint32_t splits = c.attn_splits;
