@@ -232,6 +232,8 @@ struct VxF8GemmArgs {
     uint16_t* y16;          // != nullptr (ksplit 1): fp16 output [batch][ldy] in place of y
     uint32_t ldy, ksplit;
     uint32_t add_y;         // 1 (batch 1, ksplit 1, fp32 y): y += the product (a residual epilogue)
+    const float* gain;      // != nullptr (batch 1, fp32 x): x := RMSNorm(x) * gain over its whole row first
+    float eps;
     uint64_t w_gstride, s_gstride, x_gstride, y_gstride, pstride;
     uint64_t active_mask;
 };

@@ -250,13 +250,43 @@ __global__ __launch_bounds__(64 * kFGWaves) void vx_f8gemv_kernel(VxF8GemmArgs a
     uint4 wr[D];
 #pragma unroll
     for (int u = 0; u < D; ++u) wr[u] = W[(size_t)min(w0 + (uint32_t)u, wl) * 64u];
-    // x over the split's k-range -> LDS as fp16 (8 elements per thread and pass)
+    // x over the split's k-range -> LDS as fp16 (8 elements per thread and pass); with a gain, x is
+    // first RMSNorm'd over its whole row (every workgroup sums the row's squares itself), in the
+    // operation order of the batched RMSNorm kernel: (x * inv_rms) * gain, rounded to fp16
     uint4* xs = (uint4*)vm_smem;
+    float inv = 1.0f;
+    if constexpr (XF32) {
+        if (a.gain) {
+            __shared__ float red_n[kFGWaves];
+            const uint32_t K = a.n_kt * 64u;
+            const float4* xr = (const float4*)((const float*)a.x + g * a.x_gstride);
+            float ss = 0.0f;
+            for (uint32_t i = (uint32_t)tid; i < K / 4u; i += 64u * kFGWaves) {
+                const float4 v = xr[i];
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+            if (lane == 0) red_n[wave] = ss;
+            __syncthreads();
+            float t = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kFGWaves; ++w) t += red_n[w];
+            inv = 1.0f / sqrtf(t / (float)K + a.eps);
+        }
+    }
     const uint32_t n8 = (kt1 - kt0) * 8u;
     for (uint32_t i = (uint32_t)tid; i < n8; i += 64u * kFGWaves) {
         const size_t e = g * a.x_gstride + (size_t)kt0 * 64u + 8u * i;
         if constexpr (XF32) {
-            const float4 lo = *(const float4*)((const float*)a.x + e), hi = *(const float4*)((const float*)a.x + e + 4);
+            float4 lo = *(const float4*)((const float*)a.x + e), hi = *(const float4*)((const float*)a.x + e + 4);
+            if (a.gain) {
+#pragma clang fp contract(off)
+                const size_t ge = (size_t)kt0 * 64u + 8u * i;
+                const float4 g0 = *(const float4*)(a.gain + ge), g1 = *(const float4*)(a.gain + ge + 4);
+                lo = make_float4((lo.x * inv) * g0.x, (lo.y * inv) * g0.y, (lo.z * inv) * g0.z, (lo.w * inv) * g0.w);
+                hi = make_float4((hi.x * inv) * g1.x, (hi.y * inv) * g1.y, (hi.z * inv) * g1.z, (hi.w * inv) * g1.w);
+            }
             xs[i] = __builtin_bit_cast(uint4, vm_f32x8_to_h8(lo, hi));
         } else {
             xs[i] = *(const uint4*)((const uint16_t*)a.x + e);
@@ -422,6 +452,7 @@ hipError_t vx_launch_f8gemm(const VxF8GemmArgs& a, uint32_t groups, hipStream_t 
     if (a.ksplit > 1u && a.pstride < (uint64_t)a.batch * a.ldy) return hipErrorInvalidValue;
     if ((a.y16 != nullptr) == (a.y != nullptr) || (a.y16 && a.ksplit != 1u)) return hipErrorInvalidValue;
     if (a.add_y && (a.batch != 1u || a.ksplit != 1u || a.y16)) return hipErrorInvalidValue;
+    if (a.gain && (a.batch != 1u || !a.x_f32 || a.x_gstride)) return hipErrorInvalidValue;
     // up to 16 sequences: activations staged in LDS (one sequence: the GEMV, else the MFMA form), if
     // the longest split's fp16 activations fit 64 KB (16 padded rows for the MFMA form; at least the
     // waves' sums that reuse the space). Waves per row tile: the fewest giving >= 256 workgroups, as

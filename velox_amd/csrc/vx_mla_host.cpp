@@ -441,7 +441,7 @@ void vm_layer(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, boo
     uint16_t* cache = (uint16_t*)(m->base + m->o_cache + m->cache_layer_bytes * layer);
     auto gemm = [&](const VmF8Plan& p, const void* x, uint32_t ldx, uint64_t x_gstride, uint32_t x_f32, float* y,
                     uint32_t ldy, uint64_t y_gstride, uint32_t ksplit, uint64_t pstride, uint16_t* y16 = nullptr,
-                    uint32_t add_y = 0) {
+                    uint32_t add_y = 0, const float* gain = nullptr) {
         VxF8GemmArgs g;
         std::memset(&g, 0, sizeof(g));
         g.codes = codes + p.code_off / 16;
@@ -463,19 +463,26 @@ void vm_layer(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, boo
         g.y_gstride = y_gstride;
         g.pstride = pstride;
         g.add_y = add_y;
+        g.gain = gain;
+        g.eps = c.rms_norm_eps;
         g.active_mask = mask;
         vx_record_error(vx_launch_f8gemm(g, p.groups, st));
     };
     float* parts_o = vm_act(m, m->a_parts_o);
     const uint64_t pstride_o = (uint64_t)m->B * m->H;
-    // 1. x = rmsnorm(h) as fp16 (h first takes the previous layer's W_o partials when they are pending)
-    vx_record_error(vx_launch_bnorm(h, m->H, fold_prev ? parts_o : nullptr, fold_prev ? m->ks_o : 0u,
-                                    fold_prev ? pstride_o : 0u, (const float*)((const uint8_t*)norms + L.norm), m->H,
-                                    c.rms_norm_eps, x16, m->ldx16, 32u, batch, mask, st));
-    // 2. [W_qa; W_kva] x, split over K
+    // 1. x = rmsnorm(h) as fp16 (h first takes the previous layer's W_o partials when they are pending);
+    // 2. [W_qa; W_kva] x, split over K. One sequence: the GEMV normalizes h itself.
+    const float* g_norm = (const float*)((const uint8_t*)norms + L.norm);
     float* parts_a = vm_act(m, m->a_parts_a);
     const uint64_t pstride_a = (uint64_t)m->B * m->na;
-    gemm(L.a, x16, m->ldx16, 0, 0, parts_a, m->na, 0, m->ks_a, pstride_a);
+    if (direct) {
+        gemm(L.a, h, m->H, 0, 1, parts_a, m->na, 0, m->ks_a, pstride_a, nullptr, 0, g_norm);
+    } else {
+        vx_record_error(vx_launch_bnorm(h, m->H, fold_prev ? parts_o : nullptr, fold_prev ? m->ks_o : 0u,
+                                        fold_prev ? pstride_o : 0u, g_norm, m->H, c.rms_norm_eps, x16, m->ldx16, 32u,
+                                        batch, mask, st));
+        gemm(L.a, x16, m->ldx16, 0, 0, parts_a, m->na, 0, m->ks_a, pstride_a);
+    }
     // 3. q latent RMSNorm (fp16) or q; latent RMSNorm + RoPE(k_rope) appended to the cache
     float* q32 = vm_act(m, m->a_q32);
     {
