@@ -316,9 +316,272 @@ __global__ __launch_bounds__(kMThreads) void vx_mgemm_kernel(VxMMat w, VxBGemmAr
     }
 }
 
+// ---- the GEMM for 33-64 activation rows (prefill chunks) ----
+// A workgroup owns 8 tiles over all MT row tiles and its grid row's K range, which its two halves
+// of 4 waves split (the first half takes the first ceil(n / 2) groups); in each half wave w owns
+// tiles 2w, 2w + 1 (a gate/up pair for SWIGLU). Per group of 4 blocks a half stages the group's
+// 4 x MT activation tiles (1 KiB each) once in LDS, in the lane order of the MFMA A operand, and
+// its 4 waves read them from there for both their tiles: a quarter of the activation loads of the
+// kernel above, whose waves split K and each load their own. Stages are double-buffered, one
+// barrier per group; the weights are loaded 4 groups ahead and the activations 2 ahead. The two
+// halves put two waves on every SIMD, so one wave's VALU work partly overlaps the other's MFMAs
+// (with one 4-wave half, Llama's gate/up at 64 rows kept the matrix cores busy a third of its
+// 42 us); their sums meet in LDS at the end. The arithmetic is the kernel above's: exact block
+// products, the block scale applied in fp32 (4 VALU per MFMA). Splitting each weight d (q - 8)
+// exactly into two fp16 MFMA operands instead (hi = fp16(d (q - 8)), lo = the fused residual) needs
+// no scale multiply-adds but twice the MFMAs, and measured slower: on gfx950 a wave's MFMAs and
+// another wave's VALU instructions on the same SIMD take about the MFMA time plus half the VALU
+// time (timed with MFMA-only and VALU-only waves sharing the SIMDs).
+constexpr int kPNT = 2, kPTiles = kPNT * kMWaves;  // tiles per wave, per workgroup
+constexpr int kPRing = 4;                           // weight register sets: groups loaded ahead
+
+template <int P>
+struct vx_ic {
+    static constexpr int value = P;
+};
+
+template <int EPI, int MT, int KH>
+__global__ __launch_bounds__(kMThreads * KH) void vx_pgemm_kernel(VxMMat w, VxBGemmArgs a) {
+    if ((a.active_mask & 1ULL) == 0ULL) return;
+    constexpr int NT = kPNT, SU = 4 * MT, UPW = SU / kMWaves;  // 1 KiB units per group, per wave
+    static_assert(SU % kMWaves == 0, "whole units per wave");
+    static_assert(KH == 1 || KH == 2, "one or two K halves");
+    static_assert(sizeof(vx_mh8) * 2 * 2 * SU * 64 >= sizeof(vx_mf4) * kMWaves * NT * MT * 64, "reduction fits");
+    __shared__ vx_mh8 xs[KH][2][SU][64];  // [half][stage][block * MT + row tile][lane]
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kh = KH == 1 ? 0 : wv / kMWaves, wave = wv % kMWaves;  // K half, wave within the half
+    const int row = lane & 15, g = lane >> 4;
+    const uint32_t T0 = blockIdx.x * (uint32_t)kPTiles + 2u * (uint32_t)wave;  // this wave's first tile
+    const uint32_t ng = w.n_grp;
+    const uint32_t jg0 = blockIdx.y * ng / gridDim.y, j1 = (blockIdx.y + 1u) * ng / gridDim.y;
+    const uint32_t jl = j1 - 1u;  // j1 > jg0: the launcher keeps ksplit <= n_grp
+    // both halves run ns steps (the barriers are the workgroup's); the second half's last step has
+    // no group when the count is odd
+    const uint32_t ns = (j1 - jg0 + (uint32_t)KH - 1u) / (uint32_t)KH;
+    const uint32_t j0 = jg0 + (uint32_t)kh * ns, nj = kh ? (j1 - jg0) - ns : ns;
+
+    // tiles past the matrix re-read its last tile, rows past the batch the last row, blocks past k
+    // (zero codes and scales) the last real block: every load is in bounds and unconditional
+    const vx_mu4* cp[NT];
+    const vx_mu2* sp[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t t = min(T0 + (uint32_t)nt, w.n_tiles - 1u);
+        cp[nt] = (const vx_mu4*)w.codes + (size_t)t * ng * 64u + lane;
+        sp[nt] = (const vx_mu2*)w.scales + (size_t)t * ng * 16u + row;
+    }
+    // the wave stages units wave, wave + 4, ...: unit u is block u / MT, row tile u % MT; lane
+    // (row, g) moves elements 8 g .. 8 g + 7 of the tile's row, the A operand it later reads
+    const uint16_t* xsrc[UPW];
+    uint32_t xblk[UPW];
+#pragma unroll
+    for (int i = 0; i < UPW; ++i) {
+        const int u = wave + kMWaves * i;
+        xblk[i] = (uint32_t)(u / MT);
+        xsrc[i] = a.x16 + (size_t)min((uint32_t)(16 * (u % MT) + row), a.batch - 1u) * a.ldx + 8 * g;
+    }
+    const uint32_t xbs = a.xbs, b_last = (w.k >> 5) - 1u;
+
+    vx_mf4 acc[NT][MT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = vx_mf4{0.f, 0.f, 0.f, 0.f};
+
+    const uint32_t e6400 = __builtin_amdgcn_readfirstlane(0x64006400u) + (uint32_t)lane * 0u;  // held in a VGPR
+    // Weights: a ring of kPRing register sets, set i % kPRing holding group j0 + i, refilled with
+    // group i + kPRing right after its MFMAs. Activations: two register sets; group i + 1 goes from
+    // set i & 1 into LDS stage (i + 1) & 1 after group i's MFMAs, and set i & 1 then loads group
+    // i + 3. Every set index is a compile-time constant (the loop is unrolled by the ring size).
+    vx_mu4 cw[kPRing][NT];
+    vx_mu2 sw[kPRing][NT];
+    vx_mh8 xr[2][UPW];
+    auto load_w = [&](auto pc, uint32_t j) {
+        constexpr int p = decltype(pc)::value;
+        const uint32_t jc = min(j, jl);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            cw[p][nt] = cp[nt][(size_t)jc * 64u];
+            sw[p][nt] = sp[nt][(size_t)jc * 16u];
+        }
+    };
+    auto load_x = [&](auto pc, uint32_t j) {
+        constexpr int p = decltype(pc)::value;
+        const uint32_t jc = min(j, jl);
+#pragma unroll
+        for (int i = 0; i < UPW; ++i)
+            xr[p][i] = *(const vx_mh8*)(xsrc[i] + (size_t)min(4u * jc + xblk[i], b_last) * xbs);
+    };
+    auto store_x = [&](auto pc, int s) {
+        constexpr int p = decltype(pc)::value;
+#pragma unroll
+        for (int i = 0; i < UPW; ++i) xs[kh][s][wave + kMWaves * i][lane] = xr[p][i];
+    };
+    // block b of the group: c = mfma(x, q - 8, 0), acc += d_b c -- the arithmetic of the kernel above
+    auto compute = [&](auto pc, int s) {
+        constexpr int p = decltype(pc)::value;
+        // the group's A operands are all read from LDS first
+        vx_mh8 xa[4][MT];
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) xa[b][mt] = xs[kh][s][b * MT + mt][lane];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const vx_mh8 q = vx_munpack8(cw[p][nt][b], e6400);
+                const float d = (float)__builtin_bit_cast(vx_mh2, b < 2 ? sw[p][nt].x : sw[p][nt].y)[b & 1];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const vx_mf4 cb = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[b][mt], q, vx_mf4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    acc[nt][mt] += d * cb;
+                }
+            }
+    };
+    // group j0 + i (set i % kPRing, stage i & 1), then the loads it frees; a stage is rewritten
+    // only after the barrier that follows every wave's reads of it. Past the range the loads are
+    // clamped to its last group (in bounds, unused). The scheduling barriers keep each step's
+    // loads in one order, so the waits the compiler places count the same loads on every path.
+    auto step = [&](auto pc, uint32_t i) {
+        constexpr int p = decltype(pc)::value;
+        if (i < nj) compute(pc, p & 1);  // wave-uniform
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(pc, j0 + i + (uint32_t)kPRing);
+        store_x(vx_ic<p & 1>{}, (p + 1) & 1);
+        load_x(vx_ic<p & 1>{}, j0 + i + 3u);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+    };
+    static_assert(kPRing == 4, "the loop below is unrolled by 4");
+    load_x(vx_ic<0>{}, j0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(vx_ic<0>{}, j0);
+    load_w(vx_ic<1>{}, j0 + 1u);
+    load_w(vx_ic<2>{}, j0 + 2u);
+    load_w(vx_ic<3>{}, j0 + 3u);
+    __builtin_amdgcn_sched_barrier(0);
+    store_x(vx_ic<0>{}, 0);
+    load_x(vx_ic<0>{}, j0 + 1u);
+    load_x(vx_ic<1>{}, j0 + 2u);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    uint32_t i = 0;
+    for (; i + 4u <= ns; i += 4u) {
+        step(vx_ic<0>{}, i);
+        step(vx_ic<1>{}, i + 1u);
+        step(vx_ic<2>{}, i + 2u);
+        step(vx_ic<3>{}, i + 3u);
+    }
+    if (i < ns) step(vx_ic<0>{}, i);  // the last 1..3 steps (workgroup-uniform branches)
+    if (i + 1u < ns) step(vx_ic<1>{}, i + 1u);
+    if (i + 2u < ns) step(vx_ic<2>{}, i + 2u);
+
+    // the second half's sums into LDS (the stages are free after the last step's barrier), added
+    // to the first half's in that order
+    if constexpr (KH == 2) {
+        vx_mf4(*red)[NT * MT][64] = (vx_mf4(*)[NT * MT][64])&xs[0][0][0][0];
+        if (kh) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) red[wave][nt * MT + mt][lane] = acc[nt][mt];
+        }
+        __syncthreads();
+        if (kh) return;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[nt][mt] += red[wave][nt * MT + mt][lane];
+    }
+
+    // ---- epilogues (every wave, its two tiles): lane holds acc[nt][mt][i] for activation row
+    // m = 16 mt + 4 g + i of tile T0 + nt's row 16 t + row ----
+    if constexpr (EPI == VX_EPI_SWIGLU) {
+        const uint32_t jrow = 16u * (T0 >> 1) + (uint32_t)row;  // T0 the gate tile, T0 + 1 its up tile
+        if (T0 < w.n_tiles && jrow < w.n) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t m = (uint32_t)(16 * mt + 4 * g + i);
+                    if (m >= a.batch) continue;
+                    const float gt = acc[0][mt][i], up = acc[1][mt][i];
+                    a.out16[(size_t)m * a.ldo + (size_t)(jrow >> 5) * a.obs + (jrow & 31u)] =
+                        __half_as_ushort(__float2half((gt / (1.0f + expf(-gt))) * up));
+                }
+        }
+    } else if constexpr (EPI == VX_EPI_ARGMAX) {
+        // one candidate slot per tile pair, as the kernel above (its workgroups hold one pair)
+        const uint32_t slot = T0 >> 1, nslots = (w.n_tiles + 1u) >> 1;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t m = (uint32_t)(16 * mt + 4 * g + i);
+                float bv = -INFINITY;
+                uint32_t bi = 0xFFFFFFFFu;
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const uint32_t t = T0 + (uint32_t)nt, n = 16u * t + (uint32_t)row;
+                    if (t < w.n_tiles && n < w.n) {
+                        if (m < a.batch) a.y[(size_t)m * a.ldy + n] = acc[nt][mt][i];
+                        if (vx_mbetter(acc[nt][mt][i], n, bv, bi)) { bv = acc[nt][mt][i]; bi = n; }
+                    }
+                }
+#pragma unroll
+                for (int off = 1; off < 16; off <<= 1) {
+                    const float ov = __shfl_xor(bv, off);
+                    const uint32_t oi = __shfl_xor(bi, off);
+                    if (vx_mbetter(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+                }
+                if (row == 0 && m < a.batch && slot < nslots) {
+                    a.cand_v[(size_t)m * nslots + slot] = bv;
+                    a.cand_i[(size_t)m * nslots + slot] = bi;
+                }
+            }
+    } else {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const uint32_t t = T0 + (uint32_t)nt, n = 16u * t + (uint32_t)row;
+            if (t >= w.n_tiles || n >= w.n) continue;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t m = (uint32_t)(16 * mt + 4 * g + i);
+                    if (m >= a.batch) continue;
+                    const float v = acc[nt][mt][i];
+                    if (gridDim.y > 1u) {
+                        a.part[blockIdx.y * a.pstride + (size_t)m * a.ldy + n] = v;
+                    } else {
+                        float* yp = a.y + (size_t)m * a.ldy + n;
+                        if constexpr (EPI == VX_EPI_STORE) *yp = a.bias ? v + a.bias[n] : v;
+                        else *yp += v;
+                    }
+                }
+        }
+    }
+}
+
 namespace {
 
 constexpr int kMNT = 2;  // tiles per wave (a gate/up pair for SWIGLU)
+
+// Two K halves per workgroup where the grid is at most one round of workgroups and each has 8 or
+// more groups (Llama-3-8B at 64 rows: gate/up 47.5 -> 36.2 us, down); one where the grid already
+// fills the CUs or the groups are few (QKV and o_proj split 6 and 8 ways over K, the LM head).
+template <int EPI, int MT>
+hipError_t vx_pgemm_launch_t(const VxMMat& w, const VxBGemmArgs& a, hipStream_t st) {
+    const uint32_t ks = a.ksplit > 1u ? a.ksplit : 1u;
+    const dim3 grid((w.n_tiles + kPTiles - 1u) / kPTiles, ks);
+    if ((uint64_t)grid.x * ks <= 256u && w.n_grp / ks >= 8u)
+        hipLaunchKernelGGL((vx_pgemm_kernel<EPI, MT, 2>), grid, dim3(2 * kMThreads), 0, st, w, a);
+    else
+        hipLaunchKernelGGL((vx_pgemm_kernel<EPI, MT, 1>), grid, dim3(kMThreads), 0, st, w, a);
+    return hipGetLastError();
+}
 
 template <int EPI, int MT>
 hipError_t vx_mgemm_launch_t(const VxMMat& w, const VxBGemmArgs& a, hipStream_t st) {
@@ -332,8 +595,8 @@ hipError_t vx_mgemm_dispatch_mt(const VxMMat& w, const VxBGemmArgs& a, hipStream
     if (a.batch == 0 || a.batch > 64) return hipErrorInvalidValue;
     if (a.batch <= 16) return vx_mgemm_launch_t<EPI, 1>(w, a, st);
     if (a.batch <= 32) return vx_mgemm_launch_t<EPI, 2>(w, a, st);
-    if (a.batch <= 48) return vx_mgemm_launch_t<EPI, 3>(w, a, st);
-    return vx_mgemm_launch_t<EPI, 4>(w, a, st);
+    if (a.batch <= 48) return vx_pgemm_launch_t<EPI, 3>(w, a, st);
+    return vx_pgemm_launch_t<EPI, 4>(w, a, st);
 }
 
 }  // namespace
