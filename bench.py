@@ -267,7 +267,7 @@ def main() -> int:
                     help="decode B <= 32 independent sequences per step (batched MFMA GEMMs); value = all tokens/s")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="afterwards run a device-to-device copy of MIB MiB (byte-counter yardstick)")
-    ap.add_argument("--prefill-chunk", type=int, default=64,
+    ap.add_argument("--prefill-chunk", type=int, default=128,
                     help="beside the headline, time the prompt's batched prefill in chunks of N positions "
                          "(velox_hip_prefill_batch; 0 skips it)")
     args = ap.parse_args()

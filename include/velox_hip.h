@@ -62,7 +62,7 @@ typedef struct VeloxHipModelConfig {
     uint32_t max_batch;         /* sequences of the batched decode step (<= 32; 0 or 1 = single);
                                    sizes the KV pool like B_MAX in src/memory_planner.rs:282-488 */
     uint32_t prefill_chunk;     /* >1: positions of one prompt that velox_hip_prefill_batch runs as the
-                                   rows of one batched step (<= 64); 0 or 1 = token-by-token only */
+                                   rows of one batched step (<= 128); 0 or 1 = token-by-token only */
 } VeloxHipModelConfig;
 
 typedef struct VeloxHipModel VeloxHipModel; /* opaque: the static memory plan */
@@ -350,7 +350,7 @@ int velox_hip_q4_mlayout(const VeloxHipQ4Matrix* m, void* d_codes, void* d_scale
  * Activations: element k of row m at d_x16[m * ldx + (k / 32) * xbs + k % 32] -- row-major with
  * xbs = 32 (0 means 32), or block-major [k / 32][rows][32] with ldx = 32, xbs = 32 * rows, the layout
  * the batched steps use (one operand load is 1 KiB contiguous); d_out16 (SWIGLU) likewise with
- * (ldo, obs). batch <= 64; ksplit 1..8 splits K over workgroup rows (STORE and RESIDUAL), the
+ * (ldo, obs). batch <= 128; ksplit 1..8 splits K over workgroup rows (STORE and RESIDUAL), the
  * partials going through d_part [ksplit][batch][ldy] and summed in split order (+ bias for STORE)
  * into y. */
 int velox_hip_gemm_q4_0_batch_m(const VeloxHipQ4Matrix* m, const void* d_mcodes, const void* d_mscales,
@@ -394,7 +394,7 @@ typedef struct VeloxHipRunOptions {
     const char* weights_path;/* NULL: synthetic weights of `model`; else a GGUF Q4_0 checkpoint whose
                                 metadata defines the model (the runner's --weights file.gguf) */
     uint32_t prefill_chunk;  /* >1 (single sequence, no context_len): the prompt runs through
-                                velox_hip_prefill_batch in chunks of this many positions (<= 64)
+                                velox_hip_prefill_batch in chunks of this many positions (<= 128)
                                 instead of one decode step each */
     const char* model_file;  /* non-NULL: the model is read from this .vlx source (velox_hip_vlx_load),
                                 its target block setting the VRAM budget; `model` is then ignored */

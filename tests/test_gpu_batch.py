@@ -236,7 +236,8 @@ def _block_major(x: np.ndarray, k: int) -> np.ndarray:
 @pytest.mark.parametrize("n,k,batch,ks,bm", [(4608, 3584, 8, 1, 1), (4608, 3584, 32, 4, 1), (960, 576, 5, 1, 0),
                                              (123, 4096, 17, 3, 1), (4096, 14336, 32, 8, 0), (64, 4096, 1, 2, 1),
                                              (200, 1536, 16, 1, 0), (1000, 4096, 40, 2, 1), (6144, 4096, 64, 1, 1),
-                                             (96, 576, 64, 5, 0)])
+                                             (96, 576, 64, 5, 0), (6144, 4096, 128, 6, 1), (1000, 4096, 100, 2, 0),
+                                             (4096, 14336, 128, 8, 1)])
 def test_gemm_m_store_and_residual(hiplib, oracle, dev, n, k, batch, ks, bm):
     """Row-major (bm 0) and block-major (bm 1) activations; 1..8 K splits."""
     rng = np.random.default_rng(n + k + batch + ks)
@@ -274,7 +275,8 @@ def test_gemm_m_store_and_residual(hiplib, oracle, dev, n, k, batch, ks, bm):
 
 
 @pytest.mark.parametrize("F,H,batch,bm", [(1536, 576, 3, 0), (2048, 3584, 32, 1), (100, 576, 9, 0), (18944, 3584, 20, 1),
-                                          (96, 576, 16, 1), (14336, 4096, 64, 1), (160, 576, 47, 0)])
+                                          (96, 576, 16, 1), (14336, 4096, 64, 1), (160, 576, 47, 0),
+                                          (14336, 4096, 128, 1), (160, 576, 77, 0)])
 def test_gemm_m_swiglu(hiplib, oracle, dev, F, H, batch, bm):
     rng = np.random.default_rng(F + batch + 1)
     g = _weights(oracle, F, H, 41)
@@ -308,8 +310,8 @@ def test_gemm_m_rejects_bad_arguments(hiplib, oracle, dev):
     blocks = _weights(oracle, 64, 576, 9)
     t = TiledQ4(hiplib, dev, blocks, 64, 576)
     mq = MQ4(hiplib, dev, t)
-    dx, dy, part = dev.empty(65 * 576, np.uint16), dev.empty(65 * 64), dev.empty(9 * 65 * 64)
-    cases = [(0, 576, 1, part), (65, 576, 1, part), (4, 500, 1, part), (4, 576, 9, part), (4, 576, 2, None),
+    dx, dy, part = dev.empty(129 * 576, np.uint16), dev.empty(129 * 64), dev.empty(9 * 129 * 64)
+    cases = [(0, 576, 1, part), (129, 576, 1, part), (4, 500, 1, part), (4, 576, 9, part), (4, 576, 2, None),
              (4, 576, 6, part)]  # 576 = 18 blocks = 5 groups: at most 5 splits
     for batch, ldx, ks, p in cases:
         assert hiplib.velox_hip_gemm_q4_0_batch_m(C.byref(t.m), mq.codes.data_ptr(), mq.scales.data_ptr(),

@@ -129,6 +129,13 @@ def test_prefill_64_and_48_row_chunks_vs_oracle(oracle):
     _prefill_vs_oracle(oracle, SMOLLM, 2, 48, 60, [(0, 60)], 64, seed=80, decode_steps=1)
 
 
+def test_prefill_128_and_100_row_chunks_vs_oracle(oracle):
+    """Chunks of 128 rows (eight MFMA row tiles: a 128-token prompt reads the weights once) and a
+    100-row tail; Llama-shaped layers, then SmolLM layers in 100-row chunks."""
+    _prefill_vs_oracle(oracle, LLAMA_SMALL_VOCAB, 2, 128, 228, [(0, 228)], 256, seed=81, decode_steps=2)
+    _prefill_vs_oracle(oracle, SMOLLM, 2, 100, 130, [(0, 130)], 160, seed=82, decode_steps=1)
+
+
 def test_prefill_four_and_eight_wave_attention_agree(oracle):
     """Llama-3-8B layer shapes (8 KV heads), a 100-token prompt: 64-row chunks run the prefill
     attention on 4-wave workgroups (64 x 8 = 512 workgroups, rows attending <= 128 positions), 16-row
@@ -215,7 +222,7 @@ def test_prefill_rejects_bad_arguments():
     b.close()
     c = L.ModelConfig()
     L.check(lib.velox_hip_builtin_config(b"smollm_135m", 32, C.byref(c)))
-    c.prefill_chunk = 65
+    c.prefill_chunk = 129
     m = C.c_void_p()
     assert lib.velox_hip_model_create(C.byref(c), C.byref(m)) == L.EINVAL
 

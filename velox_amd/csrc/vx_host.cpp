@@ -274,7 +274,7 @@ bool vx_shape_ok(const VeloxHipModelConfig& c) {
     if (c.quant_mode == VELOX_QUANT_Q4_GROUP64 &&
         (c.hidden_dim % 64 || c.intermediate_dim % 64 || ((uint64_t)c.num_heads * c.head_dim) % 64))
         return false;  // whole 64-weight groups along every row
-    if (c.num_kv_heads > 64 || c.attn_splits > 64 || c.max_batch > 32 || c.prefill_chunk > 64) return false;
+    if (c.num_kv_heads > 64 || c.attn_splits > 64 || c.max_batch > 32 || c.prefill_chunk > 128) return false;
     // batched RMSNorm: float4 rows of at most 8192
     if ((c.max_batch > 1 || c.prefill_chunk > 1) && ((c.hidden_dim & 3u) || c.hidden_dim > 8192)) return false;
     if (c.hidden_dim > 32768 || c.intermediate_dim > 32768 || (uint64_t)c.num_heads * c.head_dim > 32768) return false;
@@ -1390,7 +1390,7 @@ int velox_hip_gemm_q4_0_batch_m(const VeloxHipQ4Matrix* m, const void* d_mcodes,
     if (!d_mcodes || !d_mscales || !vx_mmat_public(m, d_mcodes, d_mscales, mm)) return VELOX_HIP_EINVAL;
     if (xbs == 0) xbs = 32;
     if (obs == 0) obs = 32;
-    if (!d_x16 || batch == 0 || batch > 64 || (ldx & 7u) || (xbs & 7u) || !vx_x_layout_ok(m->k, ldx, xbs, batch) ||
+    if (!d_x16 || batch == 0 || batch > 128 || (ldx & 7u) || (xbs & 7u) || !vx_x_layout_ok(m->k, ldx, xbs, batch) ||
         mode < 0 || mode > 2)
         return VELOX_HIP_EINVAL;
     if ((mode == VELOX_GEMV_SWIGLU) != (m->paired != 0)) return VELOX_HIP_EINVAL;
@@ -1544,7 +1544,7 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
     if (B > 1) cfg.max_batch = B;
     const bool batched_prefill = opt->prefill_chunk > 1;
     // (the batched prefill reads its tokens from the staged prompt at their positions: no context)
-    if (batched_prefill && (B > 1 || opt->prefill_chunk > 64 || base)) return VELOX_HIP_EINVAL;
+    if (batched_prefill && (B > 1 || opt->prefill_chunk > 128 || base)) return VELOX_HIP_EINVAL;
     if (batched_prefill) cfg.prefill_chunk = opt->prefill_chunk;
     if (cfg.max_seq_len < total) return VELOX_HIP_EINVAL;
     VeloxHipModel* M = nullptr;

@@ -347,7 +347,8 @@ __global__ __launch_bounds__(kMThreads * KH) void vx_pgemm_kernel(VxMMat w, VxBG
     static_assert(SU % kMWaves == 0, "whole units per wave");
     static_assert(KH == 1 || KH == 2, "one or two K halves");
     static_assert(sizeof(vx_mh8) * 2 * 2 * SU * 64 >= sizeof(vx_mf4) * kMWaves * NT * MT * 64, "reduction fits");
-    __shared__ vx_mh8 xs[KH][2][SU][64];  // [half][stage][block * MT + row tile][lane]
+    extern __shared__ __align__(16) unsigned char vx_psmem[];
+    vx_mh8(*xs)[2][SU][64] = (vx_mh8(*)[2][SU][64])vx_psmem;  // [half][stage][block * MT + row tile][lane]
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kh = KH == 1 ? 0 : wv / kMWaves, wave = wv % kMWaves;  // K half, wave within the half
     const int row = lane & 15, g = lane >> 4;
@@ -390,12 +391,13 @@ __global__ __launch_bounds__(kMThreads * KH) void vx_pgemm_kernel(VxMMat w, VxBG
 
     const uint32_t e6400 = __builtin_amdgcn_readfirstlane(0x64006400u) + (uint32_t)lane * 0u;  // held in a VGPR
     // Weights: a ring of kPRing register sets, set i % kPRing holding group j0 + i, refilled with
-    // group i + kPRing right after its MFMAs. Activations: two register sets; group i + 1 goes from
-    // set i & 1 into LDS stage (i + 1) & 1 after group i's MFMAs, and set i & 1 then loads group
-    // i + 3. Every set index is a compile-time constant (the loop is unrolled by the ring size).
+    // group i + kPRing right after its MFMAs. Activations: XS register sets; group i + 1 goes from
+    // set i % XS into LDS stage (i + 1) & 1 after group i's MFMAs, and that set then loads group
+    // i + 1 + XS. Every set index is a compile-time constant (the loop is unrolled by the ring size).
     vx_mu4 cw[kPRing][NT];
     vx_mu2 sw[kPRing][NT];
-    vx_mh8 xr[2][UPW];
+    constexpr int XS = MT <= 4 ? 2 : 1;  // activation register sets (one at 8 row tiles: registers)
+    vx_mh8 xr[XS][UPW];
     auto load_w = [&](auto pc, uint32_t j) {
         constexpr int p = decltype(pc)::value;
         const uint32_t jc = min(j, jl);
@@ -420,25 +422,22 @@ __global__ __launch_bounds__(kMThreads * KH) void vx_pgemm_kernel(VxMMat w, VxBG
     // block b of the group: c = mfma(x, q - 8, 0), acc += d_b c -- the arithmetic of the kernel above
     auto compute = [&](auto pc, int s) {
         constexpr int p = decltype(pc)::value;
-        // the group's A operands are all read from LDS first
-        vx_mh8 xa[4][MT];
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int b = 0; b < 4; ++b) {
+            vx_mh8 xa[MT];
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) xa[b][mt] = xs[kh][s][b * MT + mt][lane];
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
+            for (int mt = 0; mt < MT; ++mt) xa[mt] = xs[kh][s][b * MT + mt][lane];
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 const vx_mh8 q = vx_munpack8(cw[p][nt][b], e6400);
                 const float d = (float)__builtin_bit_cast(vx_mh2, b < 2 ? sw[p][nt].x : sw[p][nt].y)[b & 1];
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
-                    const vx_mf4 cb = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[b][mt], q, vx_mf4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    const vx_mf4 cb = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt], q, vx_mf4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                     acc[nt][mt] += d * cb;
                 }
             }
+        }
     };
     // group j0 + i (set i % kPRing, stage i & 1), then the loads it frees; a stage is rewritten
     // only after the barrier that follows every wave's reads of it. Past the range the loads are
@@ -449,8 +448,8 @@ __global__ __launch_bounds__(kMThreads * KH) void vx_pgemm_kernel(VxMMat w, VxBG
         if (i < nj) compute(pc, p & 1);  // wave-uniform
         __builtin_amdgcn_sched_barrier(0);
         load_w(pc, j0 + i + (uint32_t)kPRing);
-        store_x(vx_ic<p & 1>{}, (p + 1) & 1);
-        load_x(vx_ic<p & 1>{}, j0 + i + 3u);
+        store_x(vx_ic<p % XS>{}, (p + 1) & 1);
+        load_x(vx_ic<p % XS>{}, j0 + i + 1u + (uint32_t)XS);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
     };
@@ -464,7 +463,7 @@ __global__ __launch_bounds__(kMThreads * KH) void vx_pgemm_kernel(VxMMat w, VxBG
     __builtin_amdgcn_sched_barrier(0);
     store_x(vx_ic<0>{}, 0);
     load_x(vx_ic<0>{}, j0 + 1u);
-    load_x(vx_ic<1>{}, j0 + 2u);
+    if constexpr (XS == 2) load_x(vx_ic<1 % XS>{}, j0 + 2u);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     uint32_t i = 0;
@@ -573,15 +572,28 @@ constexpr int kMNT = 2;  // tiles per wave (a gate/up pair for SWIGLU)
 // Two K halves per workgroup where the grid is at most one round of workgroups and each has 8 or
 // more groups (Llama-3-8B at 64 rows: gate/up 47.5 -> 36.2 us, down); one where the grid already
 // fills the CUs or the groups are few (QKV and o_proj split 6 and 8 ways over K, the LM head).
+template <int EPI, int MT, int KH>
+hipError_t vx_pgemm_launch_kh(const VxMMat& w, const VxBGemmArgs& a, dim3 grid, hipStream_t st) {
+    constexpr size_t lds = (size_t)KH * 2 * 4 * MT * 1024;  // [half][stage][4 MT activation tiles of 1 KiB]
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void*)vx_pgemm_kernel<EPI, MT, KH>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds) != hipSuccess) {
+            (void)hipGetLastError();
+            return hipErrorInvalidValue;
+        }
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((vx_pgemm_kernel<EPI, MT, KH>), grid, dim3(KH * kMThreads), lds, st, w, a);
+    return hipGetLastError();
+}
+
 template <int EPI, int MT>
 hipError_t vx_pgemm_launch_t(const VxMMat& w, const VxBGemmArgs& a, hipStream_t st) {
     const uint32_t ks = a.ksplit > 1u ? a.ksplit : 1u;
     const dim3 grid((w.n_tiles + kPTiles - 1u) / kPTiles, ks);
-    if ((uint64_t)grid.x * ks <= 256u && w.n_grp / ks >= 8u)
-        hipLaunchKernelGGL((vx_pgemm_kernel<EPI, MT, 2>), grid, dim3(2 * kMThreads), 0, st, w, a);
-    else
-        hipLaunchKernelGGL((vx_pgemm_kernel<EPI, MT, 1>), grid, dim3(kMThreads), 0, st, w, a);
-    return hipGetLastError();
+    if ((uint64_t)grid.x * ks <= 256u && w.n_grp / ks >= 8u) return vx_pgemm_launch_kh<EPI, MT, 2>(w, a, grid, st);
+    return vx_pgemm_launch_kh<EPI, MT, 1>(w, a, grid, st);
 }
 
 template <int EPI, int MT>
@@ -593,11 +605,12 @@ hipError_t vx_mgemm_launch_t(const VxMMat& w, const VxBGemmArgs& a, hipStream_t 
 
 template <int EPI>
 hipError_t vx_mgemm_dispatch_mt(const VxMMat& w, const VxBGemmArgs& a, hipStream_t st) {
-    if (a.batch == 0 || a.batch > 64) return hipErrorInvalidValue;
+    if (a.batch == 0 || a.batch > 128) return hipErrorInvalidValue;
     if (a.batch <= 16) return vx_mgemm_launch_t<EPI, 1>(w, a, st);
     if (a.batch <= 32) return vx_pgemm_launch_t<EPI, 2>(w, a, st);
     if (a.batch <= 48) return vx_pgemm_launch_t<EPI, 3>(w, a, st);
-    return vx_pgemm_launch_t<EPI, 4>(w, a, st);
+    if (a.batch <= 64) return vx_pgemm_launch_t<EPI, 4>(w, a, st);
+    return vx_pgemm_launch_t<EPI, 8>(w, a, st);
 }
 
 }  // namespace

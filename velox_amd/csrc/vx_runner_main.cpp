@@ -12,7 +12,7 @@
 // --model-file MODEL.vlx reads the model from its .vlx source (the `model` header, weight
 // declarations and `target hardware` budget; what `velox build MODEL.vlx` compiles into the
 // reference's emitted runner) instead of a builtin configuration.
-// --prefill-chunk N (2..64) prefills the prompt N positions per batched step (one weight pass per
+// --prefill-chunk N (2..128) prefills the prompt N positions per batched step (one weight pass per
 // chunk) instead of the reference's one decode step per prompt token; TTFT reports either.
 // --unquantized f32|f16 keeps the synthetic weights as fp32 / fp16 rows (the reference's quant_mode
 // 0 / 1, a build without --quantize) instead of Q4_0.
@@ -82,8 +82,8 @@ int main(int argc, char** argv) {
         else if (!std::strcmp(a, "--layers")) layers = (uint32_t)std::atoi(next());
         else if (!std::strcmp(a, "--prefill-chunk")) {
             prefill_chunk = (uint32_t)std::atoi(next());
-            if (prefill_chunk < 2 || prefill_chunk > 64) {
-                std::fprintf(stderr, "Error: --prefill-chunk takes 2..64 positions\n");
+            if (prefill_chunk < 2 || prefill_chunk > 128) {
+                std::fprintf(stderr, "Error: --prefill-chunk takes 2..128 positions\n");
                 return 1;
             }
         }
