@@ -419,25 +419,44 @@ __global__ __launch_bounds__(kMThreads * KH) void vx_pgemm_kernel(VxMMat w, VxBG
 #pragma unroll
         for (int i = 0; i < UPW; ++i) xs[kh][s][wave + kMWaves * i][lane] = xr[p][i];
     };
-    // block b of the group: c = mfma(x, q - 8, 0), acc += d_b c -- the arithmetic of the kernel above
+    // block b of the group: c = mfma(x, q - 8, 0), acc += d_b c -- the arithmetic of the kernel above.
+    // Software-pipelined over (block, row tile): the MFMAs of one (b, mt) are issued before the
+    // scale multiply-adds of the previous one, so each product has two MFMAs' time to complete
+    // before a VALU instruction reads it (written plainly, the compiler gave every MFMA the same
+    // result registers and waited out each one with s_nop before its multiply-adds).
     auto compute = [&](auto pc, int s) {
         constexpr int p = decltype(pc)::value;
+        vx_mh8 q[NT];
+        float d[NT], dprev[NT];
+        vx_mf4 cprev[NT];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-            vx_mh8 xa[MT];
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) xa[mt] = xs[kh][s][b * MT + mt][lane];
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
-                const vx_mh8 q = vx_munpack8(cw[p][nt][b], e6400);
-                const float d = (float)__builtin_bit_cast(vx_mh2, b < 2 ? sw[p][nt].x : sw[p][nt].y)[b & 1];
+                q[nt] = vx_munpack8(cw[p][nt][b], e6400);
+                d[nt] = (float)__builtin_bit_cast(vx_mh2, b < 2 ? sw[p][nt].x : sw[p][nt].y)[b & 1];
+            }
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const vx_mf4 cb = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt], q, vx_mf4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    acc[nt][mt] += d * cb;
+            for (int mt = 0; mt < MT; ++mt) {
+                const vx_mh8 xa = xs[kh][s][b * MT + mt][lane];
+                vx_mf4 cnew[NT];
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    cnew[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, q[nt], vx_mf4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                if (b | mt) {  // compile-time: the previous (block, row tile)'s products
+                    const int pm = mt ? mt - 1 : MT - 1;
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) acc[nt][pm] += dprev[nt] * cprev[nt];
+                }
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    cprev[nt] = cnew[nt];
+                    dprev[nt] = d[nt];
                 }
             }
         }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[nt][MT - 1] += dprev[nt] * cprev[nt];
     };
     // group j0 + i (set i % kPRing, stage i & 1), then the loads it frees; a stage is rewritten
     // only after the barrier that follows every wave's reads of it. Past the range the loads are
