@@ -625,7 +625,7 @@ hipError_t vx_mgemm_launch_t(const VxMMat& w, const VxBGemmArgs& a, hipStream_t 
 template <int EPI>
 hipError_t vx_mgemm_dispatch_mt(const VxMMat& w, const VxBGemmArgs& a, hipStream_t st) {
     if (a.batch == 0 || a.batch > 128) return hipErrorInvalidValue;
-    if (a.batch <= 16) return vx_mgemm_launch_t<EPI, 1>(w, a, st);
+    if (a.batch <= 16) return vx_mgemm_launch_t<EPI, 1>(w, a, st);  // (the LDS-shared kernel: B=8 3857 -> 3640 tok/s)
     if (a.batch <= 32) return vx_pgemm_launch_t<EPI, 2>(w, a, st);
     if (a.batch <= 48) return vx_pgemm_launch_t<EPI, 3>(w, a, st);
     if (a.batch <= 64) return vx_pgemm_launch_t<EPI, 4>(w, a, st);
