@@ -174,19 +174,26 @@ __device__ __forceinline__ void vx_split_bf16(const float (&x)[8], vx_bf8 (&out)
 // merges its waves' (m, l, O) into the split's partial (o unnormalized). The o_proj GEMV or
 // vx_attn_merge_kernel merges the partials; with one split and no consumer merge, the output is
 // normalized here.
-template <int D, int G>
-constexpr int vx_attn_hrows() { return G <= 4 ? 4 : 8; }  // head rows of the per-wave O in LDS
+// head rows of the per-wave O in LDS: the used MFMA columns (G heads of each of R rows) rounded up
+template <int D, int G, int R>
+constexpr int vx_attn_hrows() { return G * R <= 4 ? 4 : G * R <= 8 ? 8 : 16; }
 
-template <int D, int G, int W>
+template <int D, int G, int W, int R>
 constexpr size_t vx_attn_lds_bytes() {
     return (size_t)3 * 16 * (D + 8) * 2 + (size_t)2 * D * 2 + (size_t)W * 16 * 2 * 4 + 16 * 4 +
-           (size_t)W * vx_attn_hrows<D, G>() * D * 4;
+           (size_t)W * vx_attn_hrows<D, G, R>() * D * 4;
 }
 
-template <int D, int G, int W, bool PS>
+// R > 1 (prefill chunks only: the rows' K/V are in the cache, no append, no new position): the
+// workgroup takes R consecutive rows of the chunk, the MFMA columns r G + h holding head h of row
+// r, each column masked at its own row's position, so R rows share every K/V chunk load and the
+// q operand's 16 columns are used 16 / G times as fully (Llama-3-8B at 128 rows: 4 rows of 4 heads).
+template <int D, int G, int W, bool PS, int R = 1>
 __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     if ((a.active_mask & 1ULL) == 0ULL) return;
-    constexpr int HALF = D / 2, NT = 64 * W, NC = D / 32, NB = D / 16, HR = vx_attn_hrows<D, G>();
+    constexpr int HALF = D / 2, NT = 64 * W, NC = D / 32, NB = D / 16, HR = vx_attn_hrows<D, G, R>();
+    constexpr int GC = G * R;  // used MFMA columns
+    static_assert(GC <= 16 && (R == 1 || PS), "R rows of G heads in 16 columns; several rows only in prefill");
     constexpr int QP = D + 8;  // padded q row: the 16 rows one operand read touches sit 4 banks apart
     constexpr float kLog2e = 1.4426950408889634f;
     static_assert(G >= 1 && G <= 8, "q heads of a group: MFMA columns 0..G-1, O rows 4 grp + i < 8");
@@ -199,31 +206,45 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     float* o_s = sn_s + 16;                                // [W][HR][D]: per wave O
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, grp = lane >> 4;            // MFMA column (head / dimension), K group
-    const uint32_t g = blockIdx.y, sp = blockIdx.x, bq = blockIdx.z;  // bq: sequence of a batch
+    const uint32_t g = blockIdx.y, sp = blockIdx.x, bq = blockIdx.z * (uint32_t)R;  // bq: sequence / first row
     const uint32_t chunk = ((a.s_max + a.splits - 1u) / a.splits + 31u) & ~31u;
     const uint32_t t0 = sp * chunk;
     uint16_t* kvb = a.kv + (size_t)bq * a.kv_bstride;
     uint16_t* Kc = kvb + (size_t)g * a.s_cap * D;
     uint16_t* Vc = kvb + ((size_t)a.hkv + g) * a.s_cap * D;
 
-    constexpr int NP = (G + 1) * HALF, RP = (NP + NT - 1) / NT;  // RoPE pairs, pairs per thread
+    // RoPE pairs (q heads and the new k; R > 1: the q heads of R rows), pairs per thread
+    constexpr int NP = R == 1 ? (G + 1) * HALF : GC * HALF, RP = (NP + NT - 1) / NT;
     // ---- the decode position first, as a vector load, then the RoPE row it selects; vector loads
     // return in order, so both arrive ahead of the q/k/v and K/V chunk loads issued after them (a
     // scalar state load issued after those waited behind every workgroup's whole burst: ~4 us at 256
     // workgroups) ----
-    uint64_t step = (uint64_t)a.fixed_pos;
-    if (a.state) step = __hip_atomic_load((uint64_t*)&a.state[bq].step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    step = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(step >> 32)) << 32) |
-           (uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)step);
-    const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;  // safe_step clamp
+    const uint32_t nrow = a.batch ? a.batch : 1u;
+    // row bq + r's position (rows past the chunk repeat its last row; safe_step clamp)
+    auto row_pos = [&](uint32_t r) {
+        uint64_t step = (uint64_t)a.fixed_pos;
+        if (a.state)
+            step = __hip_atomic_load((uint64_t*)&a.state[min(bq + r, nrow - 1u)].step, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        return step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;
+    };
+    auto uniform = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane(v); };
+    const uint32_t pos = uniform(row_pos(0u));
+    uint32_t posmax = pos;
+#pragma unroll
+    for (int r = 1; r < R; ++r) posmax = max(posmax, uniform(row_pos((uint32_t)r)));
     // cached positions [t0, t1): below pos, or up to pos when a prefill chunk appended its rows
-    const uint32_t t1 = min(a.prefill ? pos + 1u : pos, t0 + chunk);
+    const uint32_t t1 = min(a.prefill ? posmax + 1u : pos, t0 + chunk);
     const uint32_t n_chunks = t1 > t0 ? (t1 - t0 + 31u) >> 5 : 0u;
     const bool has_new = !a.prefill && t0 <= pos && pos < t0 + chunk;  // this split folds in the new position
-    const float2* rp = a.rope + (size_t)pos * HALF;
+    // the row (of R) a RoPE pair belongs to
+    auto pair_row = [&](int p) { return R == 1 ? 0 : p / (G * HALF); };
     float2 rcs[RP];
 #pragma unroll
-    for (int i = 0; i < RP; ++i) rcs[i] = rp[min(tid + i * NT, NP - 1) % HALF];
+    for (int i = 0; i < RP; ++i) {
+        const int p = min(tid + i * NT, NP - 1);
+        rcs[i] = a.rope[(size_t)(R == 1 ? pos : row_pos((uint32_t)pair_row(p))) * HALF + p % HALF];
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- q, the new k/v into registers (clamped: no load under a branch) ----
@@ -245,9 +266,9 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
         const uint32_t vcol = (a.hq + a.hkv + g) * (uint32_t)D + (uint32_t)min(tid, D - 1);
         // K-split partials of the batched QKV GEMM: every partial of an element loaded before the
         // adds, summed in split order, then the bias
-        const float* base = a.qkv_part + (size_t)bq * a.qkv_bstride;
         const uint32_t np = a.qkv_nparts;
-        auto qkv_at = [&](uint32_t c) {
+        auto qkv_at = [&](uint32_t row, uint32_t c) {
+            const float* base = a.qkv_part + (size_t)row * a.qkv_bstride;
             float t[8];
 #pragma unroll
             for (uint32_t s = 0; s < 8; ++s) t[s] = base[min(s, np - 1u) * a.qkv_pstride + c];
@@ -260,12 +281,13 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
 #pragma unroll
         for (int i = 0; i < RP; ++i) {
             const int p = min(tid + i * NT, NP - 1);
-            const int hh = p / HALF, j = p % HALF;
+            const int r = pair_row(p), hh = (p / HALF) % (R == 1 ? G + 1 : G), j = p % HALF;
             const uint32_t c0 = (hh < G ? (g * G + hh) : (a.hq + g)) * (uint32_t)D + (uint32_t)j;
-            r1[i] = qkv_at(c0);
-            r2[i] = qkv_at(c0 + HALF);
+            const uint32_t row = min(bq + (uint32_t)r, nrow - 1u);
+            r1[i] = qkv_at(row, c0);
+            r2[i] = qkv_at(row, c0 + HALF);
         }
-        vnew = qkv_at(vcol);
+        vnew = R == 1 ? qkv_at(bq, vcol) : 0.0f;
     }
 
     // ---- one 32-position chunk into registers: K rows cb + 16 b + col, dimensions 32 c + 8 grp;
@@ -288,17 +310,17 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
 
     // ---- RoPE on this group's q heads and the new k; bf16 K/V row ----
     const float qscale = a.scale * kLog2e;  // scores in the log2 domain
-    for (int i = tid; i < 3 * (16 - G) * QP / 2; i += NT) {  // q rows G..15 of every term: zero
-        const int t = i / ((16 - G) * QP / 2), r = i % ((16 - G) * QP / 2);
-        ((uint32_t*)(qt_s + (t * 16 + G) * QP))[r] = 0u;
+    for (int i = tid; i < 3 * (16 - GC) * QP / 2; i += NT) {  // q rows GC..15 of every term: zero
+        const int t = i / ((16 - GC) * QP / 2), r = i % ((16 - GC) * QP / 2);
+        ((uint32_t*)(qt_s + (t * 16 + GC) * QP))[r] = 0u;
     }
 #pragma unroll
     for (int i = 0; i < RP; ++i) {
         const int p = tid + i * NT;
         const float2 o = vx_rope_pair(r1[i], r2[i], rcs[i]);
         if (p < NP) {
-            const int hh = p / HALF, j = p % HALF;
-            if (hh < G) {
+            const int hh = p / HALF, j = p % HALF;  // q column r G + h (R == 1: head h, or G for k)
+            if (hh < GC) {
                 // the pre-scaled q as three bf16 terms (truncations of the exact remainders)
                 float x0 = o.x * qscale, x1 = o.y * qscale;
 #pragma unroll
@@ -351,6 +373,9 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) o_acc[nb] = vx_af4{0.f, 0.f, 0.f, 0.f};
 
+    // positions this lane's column attends below: its row's (R > 1; columns past GC none)
+    uint32_t t1c = t1;
+    if constexpr (R > 1) t1c = col < GC ? min(row_pos((uint32_t)(col / G)) + 1u, t0 + chunk) : 0u;
     for (; ci < n_chunks; ci += W) {
         const uint32_t cb = t0 + 32u * ci;
         // scores: sc[b][i] = S[position cb + 16 b + 4 grp + i][head col]
@@ -370,7 +395,7 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t p = cb + 16u * b + 4u * grp + i;
-                pr[4 * b + i] = p < t1 ? sc[b][i] : -INFINITY;
+                pr[4 * b + i] = p < t1c ? sc[b][i] : -INFINITY;
                 mx = fmaxf(mx, pr[4 * b + i]);
             }
         mx = fmaxf(mx, __shfl_xor(mx, 16));
@@ -415,8 +440,10 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
             for (int i = 0; i < 4; ++i) o_s[(wave * HR + 4 * grp + i) * D + 16 * nb + col] = o_acc[nb][i];
     }
     __syncthreads();
-    for (int idx = tid; idx < G * D; idx += NT) {
-        const int h = idx / D, d = idx % D;
+    for (int idx = tid; idx < GC * D; idx += NT) {
+        const int h = idx / D, d = idx % D;  // column: head h % G of row h / G
+        const uint32_t row = bq + (uint32_t)(h / G);
+        if (R > 1 && row >= nrow) continue;  // past the chunk's last row
         const float sn = has_new ? sn_s[h] : -INFINITY;
         float M = sn;
 #pragma unroll
@@ -434,7 +461,7 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
             o += wt * o_s[(w * HR + h) * D + d];
             l += wt * ml_s[w * 32 + 16 + h];
         }
-        const size_t hq_idx = (size_t)bq * a.hq + (size_t)g * G + h;  // (sequence, q head)
+        const size_t hq_idx = (size_t)row * a.hq + (size_t)g * G + (size_t)(h % G);  // (sequence or row, q head)
         if (a.splits == 1 && !a.partials_only) {
             a.out[hq_idx * D + d] = l > 0.0f ? o / l : 0.0f;
         } else {
@@ -643,19 +670,20 @@ __global__ __launch_bounds__(kWG) void vx_argmax_kernel(const float* x, uint32_t
 // =============================================================================================
 namespace {
 
-template <int D, int G, bool PS, int W>
+template <int D, int G, bool PS, int W, int R = 1>
 hipError_t vx_attn_launch_w(const VxAttnArgs& a, hipStream_t st) {
-    constexpr size_t lds = vx_attn_lds_bytes<D, G, W>();
+    constexpr size_t lds = vx_attn_lds_bytes<D, G, W, R>();
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)vx_attn_kernel<D, G, W, PS>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        if (hipFuncSetAttribute((const void*)vx_attn_kernel<D, G, W, PS, R>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds) != hipSuccess) {
             (void)hipGetLastError();
             return hipErrorInvalidValue;
         }
         attr_set = true;
     }
-    hipLaunchKernelGGL((vx_attn_kernel<D, G, W, PS>), dim3(a.splits, a.hkv, a.batch ? a.batch : 1u), dim3(64 * W), lds,
+    const uint32_t rows = a.batch ? a.batch : 1u;
+    hipLaunchKernelGGL((vx_attn_kernel<D, G, W, PS, R>), dim3(a.splits, a.hkv, (rows + R - 1u) / R), dim3(64 * W), lds,
                        st, a);
     return hipGetLastError();
 }
@@ -663,6 +691,10 @@ hipError_t vx_attn_launch_w(const VxAttnArgs& a, hipStream_t st) {
 template <int D, int G, bool PS>
 hipError_t vx_attn_launch_ps(const VxAttnArgs& a, hipStream_t st) {
     if constexpr (PS) {
+        // prefill chunks: 16 / G rows per workgroup (4-wave workgroups)
+        constexpr int R = 16 / G;
+        if constexpr (R > 1)
+            if (a.prefill) return vx_attn_launch_w<D, G, PS, 4, R>(a, st);
         // 4 waves, two workgroups per CU, where 8-wave workgroups (one per CU) would need a second
         // round and 4 waves still take every 32-position chunk a split can attend in one pass (the
         // prefill chunks of short prompts: 64 rows x 8 KV heads = 512 workgroups, <= 128 positions)
