@@ -167,6 +167,11 @@ struct VxAttnArgs {
     uint64_t qkv_pstride;
     uint32_t qkv_nparts;
     uint32_t max_len;        // > 0: no row attends past this many positions (a prefill chunk's end); 0 unknown
+    // one split and x16 set (batched steps): the normalized output goes straight to the fp16 operand
+    // of the o_proj GEMM, element c of row b at x16[b * x_ld + (c / 32) * x_bs + c % 32] (the
+    // batched merge kernel's output: fp16((1 / l) o)), and no partials are written
+    uint16_t* x16;
+    uint32_t x_ld, x_bs;
 };
 
 // Batched (B <= 32 sequences) Q4_0 GEMM: Y[m][n] = sum_k X[m][k] W[n][k] for fp16 activations

@@ -968,6 +968,11 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
     // decode: consecutive sequences of one layer; prefill: every row reads sequence 0's cache
     at.kv_bstride = prefill ? 0 : M->kv_layer_bytes / 2;
     at.qkv_bstride = qd + 2 * kvd;
+    if (bsplits == 1) {
+        at.x16 = xa;
+        at.x_ld = M->x_ld;
+        at.x_bs = M->x_bs;
+    }
     VxBGemmArgs g;
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         const VxLayerPlan& L = M->layers[l];
@@ -1000,7 +1005,8 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
                                                g.bias, c.num_heads, c.num_kv_heads, D, rows, n, at.rope,
                                                c.max_seq_len, M->s_cap, at.kv, mask, st));
         vx_record(vx_launch_attention(at, D, st));
-        vx_record(vx_launch_bmerge(at.part_o, at.part_ml, c.num_heads, D, bsplits, xa, M->x_ld, M->x_bs, n, mask, st));
+        if (bsplits > 1)  // (one split: the attention wrote the o_proj operand itself)
+            vx_record(vx_launch_bmerge(at.part_o, at.part_ml, c.num_heads, D, bsplits, xa, M->x_ld, M->x_bs, n, mask, st));
         std::memset(&g, 0, sizeof(g));
         g.batch = n;
         g.active_mask = mask;

@@ -464,6 +464,10 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
         const size_t hq_idx = (size_t)row * a.hq + (size_t)g * G + (size_t)(h % G);  // (sequence or row, q head)
         if (a.splits == 1 && !a.partials_only) {
             a.out[hq_idx * D + d] = l > 0.0f ? o / l : 0.0f;
+        } else if (a.splits == 1 && a.x16) {
+            const float w = l > 0.0f ? 1.0f / l : 0.0f;
+            const size_t e = (size_t)(g * G + (uint32_t)(h % G)) * D + d;
+            a.x16[(size_t)row * a.x_ld + (e >> 5) * a.x_bs + (e & 31u)] = __half_as_ushort(__float2half(w * o));
         } else {
             a.part_o[(hq_idx * a.splits + sp) * D + d] = o;
             if (d == 0) {
