@@ -377,22 +377,44 @@ __global__ __launch_bounds__(64 * kFGWaves) void vx_f8gemm_x_kernel(VxF8GemmArgs
         xs[m * xr8 + u] = v;
     }
     __syncthreads();
-    vm_f4 acc = vm_f4{0.f, 0.f, 0.f, 0.f};
+    // The block scales come as vector loads in a ring beside the weight words (in order with them:
+    // a scalar load per k-tile waited on with the LDS reads, one memory round trip per tile), and
+    // each tile's scale multiply-add waits one tile: the next tile's MFMAs are issued first, so the
+    // product has completed when the VALU reads it. Past the wave's range a tile re-reads the last
+    // one and adds with scale 0 (no branch in the loop); the sums keep the k order.
+    uint32_t vzero;  // 0 in a VGPR the compiler cannot see through: the scale loads stay vector loads
+    asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
+    const float* Sv = S + vzero;
+    float sr[D];
+#pragma unroll
+    for (int u = 0; u < D; ++u) sr[u] = Sv[min(w0 + (uint32_t)u, wl) >> 1];
+    vm_f4 acc = vm_f4{0.f, 0.f, 0.f, 0.f}, tprev = vm_f4{0.f, 0.f, 0.f, 0.f};
+    float sprev = 0.0f;
+    // a tile's A operands are read from LDS one tile ahead (read just before its MFMAs, every tile
+    // waited out an LDS round trip)
+    auto xidx = [&](uint32_t kt) { return (uint32_t)col * xr8 + (min(kt, wl) - kt0) * 8u + 2u * (uint32_t)grp; };
+    uint4 xc0 = xs[xidx(w0)], xc1 = xs[xidx(w0) + 1u];
     for (uint32_t base = w0; base < w1; base += D) {
 #pragma unroll
         for (int u = 0; u < D; ++u) {
             const uint32_t kt = base + (uint32_t)u;
-            if (kt < w1) {
-                const uint32_t xi = (uint32_t)col * xr8 + (kt - kt0) * 8u + 2u * (uint32_t)grp;
-                const vm_h8 x0 = __builtin_bit_cast(vm_h8, xs[xi]), x1 = __builtin_bit_cast(vm_h8, xs[xi + 1u]);
-                const vm_h8 f0 = vm_fp8x8(wr[u].x, wr[u].y), f1 = vm_fp8x8(wr[u].z, wr[u].w);
-                vm_f4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, f0, vm_f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, f1, t, 0, 0, 0);
-                acc += S[kt >> 1] * t;
-            }
+            const uint32_t xn = xidx(kt + 1u);
+            const uint4 xn0 = xs[xn], xn1 = xs[xn + 1u];
+            __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of this tile's MFMAs
+            const vm_h8 x0 = __builtin_bit_cast(vm_h8, xc0), x1 = __builtin_bit_cast(vm_h8, xc1);
+            xc0 = xn0;
+            xc1 = xn1;
+            const vm_h8 f0 = vm_fp8x8(wr[u].x, wr[u].y), f1 = vm_fp8x8(wr[u].z, wr[u].w);
+            vm_f4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, f0, vm_f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, f1, t, 0, 0, 0);
+            acc += sprev * tprev;
+            tprev = t;
+            sprev = kt < w1 ? sr[u] : 0.0f;
             wr[u] = W[(size_t)min(kt + (uint32_t)D, wl) * 64u];
+            sr[u] = Sv[min(kt + (uint32_t)D, wl) >> 1];
         }
     }
+    acc += sprev * tprev;
     vm_f4* red = (vm_f4*)vm_smem;  // reuses x: every wave passed its last LDS read at the barrier below
     if constexpr (KW > 1) {
         __syncthreads();
