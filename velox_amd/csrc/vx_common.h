@@ -213,6 +213,7 @@ void vx_mmat_shape(uint32_t n, uint32_t k, uint32_t paired, VxMMat& m);  // fill
 uint64_t vx_mmat_code_bytes(const VxMMat& m);
 uint64_t vx_mmat_scale_bytes(const VxMMat& m);
 uint32_t vx_mgemm_grid(uint32_t n_tiles);  // workgroups of one grid row (also the ARGMAX candidate count)
+uint32_t vx_pgemm_grid(uint32_t n_tiles);  // the same for the 17-128-row GEMM (8 tiles per workgroup)
 hipError_t vx_launch_mlayout(const VxMat& src, const VxMMat& dst, hipStream_t st);
 // The batched Q4_0 GEMM over an MFMA-layout copy (codes/scales/n/k from `w`), epilogues as the
 // GEMV's; ksplit > 1 (STORE or RESID) stores K-split partials, which vx_launch_msum (STORE, + bias)

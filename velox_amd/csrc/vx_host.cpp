@@ -61,6 +61,17 @@ uint32_t vx_mgemm_ksplit(const VxMatPlan& m) {
     return ks ? ks : 1u;
 }
 
+// K splits of the QKV GEMM over more than 64 rows (MFMA-bound): as many as keep the grid within one
+// round of 256 workgroups, where a partial second round would add a whole workgroup's time (Llama-3-8B
+// QKV at 128 rows: 48 x 6 workgroups 26.6 us, 48 x 5 21.9 us).
+uint32_t vx_pgemm_ksplit(const VxMatPlan& m) {
+    const uint32_t wgs = vx_pgemm_grid(m.m_tiles);
+    uint32_t ks = wgs ? 256u / wgs : 1u;
+    if (ks > 8u) ks = 8u;
+    if (ks > m.m_grp) ks = m.m_grp;
+    return ks ? ks : 1u;
+}
+
 }  // namespace
 
 struct VeloxHipModel {
@@ -86,6 +97,7 @@ struct VeloxHipModel {
     // K-split partials of the residual GEMMs (o_proj, down): [ksplit][batch][hidden]
     uint64_t a_bpart_r = 0;
     uint32_t ksplit_o = 1, ksplit_down = 1, ksplit_qkv = 1;
+    uint32_t ksplit_qkv_wide = 1;  // QKV over chunks of more than 64 rows
     // fp16 activation operands of the batched GEMMs (over the MFMA-layout copies): element k of row m
     // at m * x_ld + (k / 32) * x_bs + k % 32, block-major [k / 32][16-row-padded rows][32] (one operand
     // load = 1 KiB contiguous)
@@ -449,6 +461,7 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
         M->a_bpart_r = take(8 * B * (H > qd + 2 * kvd ? H : qd + 2 * kvd) * 4);
         M->a_prows = take(B * sizeof(VeloxDecodeState));
         M->ksplit_qkv = vx_mgemm_ksplit(M->layers[0].qkv);
+        M->ksplit_qkv_wide = vx_pgemm_ksplit(M->layers[0].qkv);
         M->ksplit_o = vx_mgemm_ksplit(M->layers[0].o);
         M->ksplit_down = vx_mgemm_ksplit(M->layers[0].down);
     }
@@ -988,8 +1001,9 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
         g.bias = c.qkv_bias ? vecp(L.bias) : nullptr;
         g.y = qkv;
         g.ldy = qd + 2 * kvd;
-        if (M->ksplit_qkv > 1) {  // K-split partials, then their sum + bias
-            g.ksplit = M->ksplit_qkv;
+        const uint32_t ks_qkv = n > 64u ? M->ksplit_qkv_wide : M->ksplit_qkv;
+        if (ks_qkv > 1) {  // K-split partials, then their sum + bias
+            g.ksplit = ks_qkv;
             g.part = part_r;
             g.pstride = (uint64_t)M->rows * g.ldy;
         }

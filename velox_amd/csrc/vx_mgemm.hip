@@ -635,6 +635,7 @@ hipError_t vx_mgemm_dispatch_mt(const VxMMat& w, const VxBGemmArgs& a, hipStream
 }  // namespace
 
 uint32_t vx_mgemm_grid(uint32_t n_tiles) { return (n_tiles + kMNT - 1u) / kMNT; }
+uint32_t vx_pgemm_grid(uint32_t n_tiles) { return (n_tiles + kPTiles - 1u) / kPTiles; }
 
 void vx_mmat_shape(uint32_t n, uint32_t k, uint32_t paired, VxMMat& m) {
     m.n = n;
