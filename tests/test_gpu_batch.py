@@ -276,7 +276,7 @@ def test_gemm_m_store_and_residual(hiplib, oracle, dev, n, k, batch, ks, bm):
 
 @pytest.mark.parametrize("F,H,batch,bm", [(1536, 576, 3, 0), (2048, 3584, 32, 1), (100, 576, 9, 0), (18944, 3584, 20, 1),
                                           (96, 576, 16, 1), (14336, 4096, 64, 1), (160, 576, 47, 0),
-                                          (14336, 4096, 128, 1), (160, 576, 77, 0)])
+                                          (14336, 4096, 128, 1), (160, 576, 77, 0), (18944, 3584, 100, 1)])
 def test_gemm_m_swiglu(hiplib, oracle, dev, F, H, batch, bm):
     rng = np.random.default_rng(F + batch + 1)
     g = _weights(oracle, F, H, 41)

@@ -353,6 +353,7 @@ __global__ __launch_bounds__(kMThreads * KH) void vx_pgemm_kernel(VxMMat w, VxBG
     const int kh = KH == 1 ? 0 : wv / kMWaves, wave = wv % kMWaves;  // K half, wave within the half
     const int row = lane & 15, g = lane >> 4;
     const uint32_t T0 = blockIdx.x * (uint32_t)kPTiles + 2u * (uint32_t)wave;  // this wave's first tile
+    const uint32_t r0 = blockIdx.z * (uint32_t)(16 * MT);  // the workgroup's first activation row
     const uint32_t ng = w.n_grp;
     const uint32_t jg0 = blockIdx.y * ng / gridDim.y, j1 = (blockIdx.y + 1u) * ng / gridDim.y;
     const uint32_t jl = j1 - 1u;  // j1 > jg0: the launcher keeps ksplit <= n_grp
@@ -379,7 +380,7 @@ __global__ __launch_bounds__(kMThreads * KH) void vx_pgemm_kernel(VxMMat w, VxBG
     for (int i = 0; i < UPW; ++i) {
         const int u = wave + kMWaves * i;
         xblk[i] = (uint32_t)(u / MT);
-        xsrc[i] = a.x16 + (size_t)min((uint32_t)(16 * (u % MT) + row), a.batch - 1u) * a.ldx + 8 * g;
+        xsrc[i] = a.x16 + (size_t)min(r0 + (uint32_t)(16 * (u % MT) + row), a.batch - 1u) * a.ldx + 8 * g;
     }
     const uint32_t xbs = a.xbs, b_last = (w.k >> 5) - 1u;
 
@@ -460,29 +461,43 @@ __global__ __launch_bounds__(kMThreads * KH) void vx_pgemm_kernel(VxMMat w, VxBG
     };
     // group j0 + i (set i % kPRing, stage i & 1), then the loads it frees; a stage is rewritten
     // only after the barrier that follows every wave's reads of it. Past the range the loads are
-    // clamped to its last group (in bounds, unused). The scheduling barriers keep each step's
-    // loads in one order, so the waits the compiler places count the same loads on every path.
+    // clamped to its last group (in bounds, unused). Vector loads retire in issue order, so the
+    // wait before an activation store also waits for every load issued before that activation
+    // group: each step issues its activation group before its weight group, and the wait for
+    // group i + 1's activations then reaches only the weights of group i + 1 (XS = 2) or i + 2
+    // (XS = 1), loaded 3 or 2 steps earlier (issued the other way round, it reached the weights of
+    // group i + 2 or i + 3, loaded 2 steps or 1 step earlier). The scheduling barriers keep each
+    // step's loads in this order, and the prologue leaves the same loads outstanding as a step
+    // does, so the waits the compiler places count the same loads on every path.
     auto step = [&](auto pc, uint32_t i) {
         constexpr int p = decltype(pc)::value;
         if (i < nj) compute(pc, p & 1);  // wave-uniform
         __builtin_amdgcn_sched_barrier(0);
-        load_w(pc, j0 + i + (uint32_t)kPRing);
         store_x(vx_ic<p % XS>{}, (p + 1) & 1);
         load_x(vx_ic<p % XS>{}, j0 + i + 1u + (uint32_t)XS);
+        load_w(pc, j0 + i + (uint32_t)kPRing);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
     };
     static_assert(kPRing == 4, "the loop below is unrolled by 4");
-    load_x(vx_ic<0>{}, j0);
-    __builtin_amdgcn_sched_barrier(0);
+    // outstanding after the prologue, oldest first: XS = 2: w1 x1 w2 x2 w3; XS = 1: w2 x1 w3 (as
+    // after a step of the loop)
     load_w(vx_ic<0>{}, j0);
-    load_w(vx_ic<1>{}, j0 + 1u);
-    load_w(vx_ic<2>{}, j0 + 2u);
-    load_w(vx_ic<3>{}, j0 + 3u);
+    if constexpr (XS == 1) load_w(vx_ic<1>{}, j0 + 1u);
+    load_x(vx_ic<0>{}, j0);
+    if constexpr (XS == 2) load_w(vx_ic<1>{}, j0 + 1u);
     __builtin_amdgcn_sched_barrier(0);
     store_x(vx_ic<0>{}, 0);
-    load_x(vx_ic<0>{}, j0 + 1u);
-    if constexpr (XS == 2) load_x(vx_ic<1 % XS>{}, j0 + 2u);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (XS == 2) {
+        load_x(vx_ic<0>{}, j0 + 1u);
+        load_w(vx_ic<2>{}, j0 + 2u);
+        load_x(vx_ic<1>{}, j0 + 2u);
+    } else {
+        load_w(vx_ic<2>{}, j0 + 2u);
+        load_x(vx_ic<0>{}, j0 + 1u);
+    }
+    load_w(vx_ic<3>{}, j0 + 3u);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     uint32_t i = 0;
@@ -523,7 +538,7 @@ __global__ __launch_bounds__(kMThreads * KH) void vx_pgemm_kernel(VxMMat w, VxBG
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const uint32_t m = (uint32_t)(16 * mt + 4 * g + i);
+                    const uint32_t m = r0 + (uint32_t)(16 * mt + 4 * g + i);
                     if (m >= a.batch) continue;
                     const float gt = acc[0][mt][i], up = acc[1][mt][i];
                     a.out16[(size_t)m * a.ldo + (size_t)(jrow >> 5) * a.obs + (jrow & 31u)] =
@@ -537,7 +552,7 @@ __global__ __launch_bounds__(kMThreads * KH) void vx_pgemm_kernel(VxMMat w, VxBG
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t m = (uint32_t)(16 * mt + 4 * g + i);
+                const uint32_t m = r0 + (uint32_t)(16 * mt + 4 * g + i);
                 float bv = -INFINITY;
                 uint32_t bi = 0xFFFFFFFFu;
 #pragma unroll
@@ -568,7 +583,7 @@ __global__ __launch_bounds__(kMThreads * KH) void vx_pgemm_kernel(VxMMat w, VxBG
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const uint32_t m = (uint32_t)(16 * mt + 4 * g + i);
+                    const uint32_t m = r0 + (uint32_t)(16 * mt + 4 * g + i);
                     if (m >= a.batch) continue;
                     const float v = acc[nt][mt][i];
                     if (gridDim.y > 1u) {
@@ -603,6 +618,7 @@ hipError_t vx_pgemm_launch_kh(const VxMMat& w, const VxBGemmArgs& a, dim3 grid, 
         }
         attr_set = true;
     }
+    grid.z = (a.batch + 16u * MT - 1u) / (16u * MT);  // blocks of 16 MT activation rows
     hipLaunchKernelGGL((vx_pgemm_kernel<EPI, MT, KH>), grid, dim3(KH * kMThreads), lds, st, w, a);
     return hipGetLastError();
 }
@@ -611,7 +627,8 @@ template <int EPI, int MT>
 hipError_t vx_pgemm_launch_t(const VxMMat& w, const VxBGemmArgs& a, hipStream_t st) {
     const uint32_t ks = a.ksplit > 1u ? a.ksplit : 1u;
     const dim3 grid((w.n_tiles + kPTiles - 1u) / kPTiles, ks);
-    if ((uint64_t)grid.x * ks <= 256u && w.n_grp / ks >= 8u) return vx_pgemm_launch_kh<EPI, MT, 2>(w, a, grid, st);
+    const uint64_t wgs = (uint64_t)grid.x * ks * ((a.batch + 16u * MT - 1u) / (16u * MT));
+    if (wgs <= 256u && w.n_grp / ks >= 8u) return vx_pgemm_launch_kh<EPI, MT, 2>(w, a, grid, st);
     return vx_pgemm_launch_kh<EPI, MT, 1>(w, a, grid, st);
 }
 
@@ -629,6 +646,11 @@ hipError_t vx_mgemm_dispatch_mt(const VxMMat& w, const VxBGemmArgs& a, hipStream
     if (a.batch <= 32) return vx_pgemm_launch_t<EPI, 2>(w, a, st);
     if (a.batch <= 48) return vx_pgemm_launch_t<EPI, 3>(w, a, st);
     if (a.batch <= 64) return vx_pgemm_launch_t<EPI, 4>(w, a, st);
+    // 65-128 rows: one block of 8 row tiles, or two blocks of 4 where workgroups over all 8 would
+    // come to more than one round of 256 but not two (Qwen2.5-7B gate/up: 296 workgroups, 40 CUs
+    // holding two): the 592 smaller ones spread more evenly
+    const uint64_t wgs8 = (uint64_t)((w.n_tiles + kPTiles - 1u) / kPTiles) * (a.ksplit > 1u ? a.ksplit : 1u);
+    if (wgs8 > 256u && wgs8 <= 512u) return vx_pgemm_launch_t<EPI, 4>(w, a, st);
     return vx_pgemm_launch_t<EPI, 8>(w, a, st);
 }
 
