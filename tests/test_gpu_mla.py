@@ -2,7 +2,8 @@
 against the oracle's vxo_mla_layer_step on the same seeded fp8 weights and latent context.
 
 Tolerance: the device computes every projection with fp16 activations against exactly converted
-fp8 weights and the attention on fp16 MFMA operands (fp32 accumulation), the oracle in fp32; the
+fp8 weights and the attention on bf16 MFMA operands (the cached latent rows, q and P rounded to
+bf16; fp32 accumulation), the oracle in fp32; the
 layer's update (h_out - h) must agree to 2e-2 of its largest magnitude (the bf16 bound), and the
 appended latent row to bf16 rounding of the same value."""
 import ctypes as C

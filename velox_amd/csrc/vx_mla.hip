@@ -682,22 +682,25 @@ constexpr size_t vx_mla_attn_lds() {  // the chunk's rows [c | kr], the waves' p
 }
 
 typedef short vm_s4 __attribute__((ext_vector_type(4)));
+typedef __bf16 vm_b8 __attribute__((ext_vector_type(8)));
 
 constexpr float kMlaLazy = 8.0f;  // log2 headroom of the attention's stale running maximum
 
 // Four 16-bit values per lane from LDS, transposed within each 16-lane group: lane i of a group
 // receives element i % 4 of the words that lanes 4 e + i / 4 (e = 0..3) address (ds_read_b64_tr_b16).
-__device__ __forceinline__ vm_s4 vm_lds_tr4(const _Float16* p) {
+__device__ __forceinline__ vm_s4 vm_lds_tr4(const __bf16* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) vm_s4*)p);
 }
 
 // Absorbed MLA attention of one (split, sequence, group of 16 W heads). The split's positions go
-// through LDS in chunks of 32: the bf16 latent rows are converted to fp16 once, as rows; the scores
-// read them as rows and P.V reads the latent part transposed (ds_read_b64_tr_b16: the 8 positions
-// of one dimension that a lane's MFMA operand takes, from the row layout, with no transposed copy).
+// through LDS in chunks of 32, as the cache holds them (bf16 rows, copied with no conversion); the
+// scores read them as rows and P.V reads the latent part transposed (ds_read_b64_tr_b16: the 8
+// positions of one dimension that a lane's MFMA operand takes, from the row layout, with no
+// transposed copy). Both products run on v_mfma_f32_16x16x32_bf16 with q and P rounded to bf16 (an
+// fp16 copy of each chunk cost about a third of the kernel's VALU instructions).
 // LS waves share each 16 heads: each computes the heads' partial scores S^T[pos][head] = [c | kr] .
-// [q_abs | rope(q_rope)] over 1 / LS of the dimensions on v_mfma_f32_16x16x32_f16 (its q operands,
-// built once, stay in registers), the partials meet in LDS, every wave runs the log2-domain online
+// [q_abs | rope(q_rope)] over 1 / LS of the dimensions (its q operands, built once, stay in
+// registers), the partials meet in LDS, every wave runs the log2-domain online
 // softmax on the same sums and accumulates its 1 / LS of the latent dimensions of
 // O[head][latent] += P c on MFMA (fewer registers: two waves per SIMD). Writes the split's (m, l, o).
 template <int LR, int DR, int W, int LS>
@@ -706,7 +709,7 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
     constexpr int R = LR + DR, NCK = R / 32, NB = LR / 16, NBW = NB / LS, KP = R + 8, NT = 64 * W * LS;
     static_assert(NB % LS == 0, "whole 16-dimension blocks per wave");
     extern __shared__ __align__(16) unsigned char vm_smem[];
-    _Float16* k_s = (_Float16*)vm_smem;                      // [32][KP]: rows [c | kr]
+    __bf16* k_s = (__bf16*)vm_smem;                          // [32][KP]: rows [c | kr], bf16 as cached
     vm_f4* ps_s = (vm_f4*)(vm_smem + (size_t)32 * KP * 2);  // partial scores [W LS][2][64]
     constexpr int NCH = NCK / LS;                            // 32-dimension chunks of a wave's scores
     static_assert(NCK % LS == 0, "whole 32-dimension chunks per wave");
@@ -741,7 +744,7 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
     // consecutive dimensions of a 32-dimension chunk come as vector loads (the RoPE part's 8 stay
     // within one half of the rotation). Wave ls of a head group keeps the q chunks of its share of
     // the score dimensions in registers ----
-    vm_h8 qreg[NCH];
+    vm_b8 qreg[NCH];
     {
         const float* qa = a.qabs + ((size_t)b * a.nh + head) * LR;
         const float* qr = a.q32 + (size_t)b * a.nh * a.dq + (size_t)head * a.dq + a.dn;
@@ -772,9 +775,9 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
                     v[e] = r0 < h2 ? o.x : o.y;
                 }
             }
-            vm_h8 q;
+            vm_b8 q;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) q[e] = (_Float16)(v[e] * a.qscale);
+            for (int e = 0; e < 8; ++e) q[e] = (__bf16)(v[e] * a.qscale);
             qreg[cc] = q;
         }
     }
@@ -787,20 +790,10 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
     auto chunk_step = [&](uint32_t ci) {
         const uint32_t cb = t0 + 32u * ci;
         __syncthreads();  // the previous chunk is consumed
-        auto to_h8 = [](const uint4& q) {
-            const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
-            vm_h8 h;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                h[2 * e] = (_Float16)__uint_as_float(w4[e] << 16);
-                h[2 * e + 1] = (_Float16)__uint_as_float(w4[e] & 0xFFFF0000u);
-            }
-            return h;
-        };
 #pragma unroll
         for (int u = 0; u < NU; ++u) {
             const int un = tid + u * NT;
-            if (un < 32 * RB) *(vm_h8*)(k_s + (un / RB) * KP + 8 * (un % RB)) = to_h8(kr[u]);
+            if (un < 32 * RB) *(vm_b8*)(k_s + (un / RB) * KP + 8 * (un % RB)) = __builtin_bit_cast(vm_b8, kr[u]);
         }
         __syncthreads();
         if (ci + 1u < n_chunks) load_chunk(cb + 32u);
@@ -809,11 +802,11 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
 #pragma unroll
         for (int cc = 0; cc < NCH; ++cc) {
             const int c = ls * NCH + cc;
-            const vm_h8 qop = qreg[cc];
+            const vm_b8 qop = qreg[cc];
 #pragma unroll
             for (int bb = 0; bb < 2; ++bb) {
-                const vm_h8 kop = *(const vm_h8*)(k_s + (16 * bb + col) * KP + 32 * c + 8 * grp);
-                sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop, sc[bb], 0, 0, 0);
+                const vm_b8 kop = *(const vm_b8*)(k_s + (16 * bb + col) * KP + 32 * c + 8 * grp);
+                sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop, sc[bb], 0, 0, 0);
             }
         }
         {
@@ -842,19 +835,19 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         // lazy rescale: the reference maximum m_run moves only when a score exceeds it by more than
-        // 2^kMlaLazy (log2 units), so p = 2^(s - m_run) <= 2^kMlaLazy stays well inside fp16 and
+        // 2^kMlaLazy (log2 units), so p = 2^(s - m_run) <= 2^kMlaLazy stays small and
         // the accumulators are rescaled only on such a jump; before the first finite maximum they
         // are still zero
         const float m_new = (m_run == -INFINITY || mx > m_run + kMlaLazy) ? mx : m_run;
         const float alpha = m_run == -INFINITY ? 0.0f : vm_exp2(m_run - m_new);
         const bool grew = m_run != -INFINITY && m_new != m_run;
         float lt = 0.0f;
-        vm_h8 pop;
+        vm_b8 pop;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const float p = pr[e] == -INFINITY ? 0.0f : vm_exp2(pr[e] - m_new);
             lt += p;
-            pop[e] = (_Float16)p;
+            pop[e] = (__bf16)p;
         }
         l_run = l_run * alpha + lt;
         m_run = m_new;
@@ -869,12 +862,12 @@ __global__ __launch_bounds__(64 * W * LS, 1) void vx_mla_attn_kernel(VxMlaAttnAr
         // B operand of latent block nb: lane (dimension col, group grp) takes positions 4 grp + e and
         // 16 + 4 grp + e (e = 0..3), the positions of pop's elements; lane j of the group addresses
         // row 4 grp + j / 4 (+ 16), dimensions 4 (j % 4) .. + 3 of the block
-        const _Float16* vb = k_s + (4 * grp + (col >> 2)) * KP + 16 * ls * NBW + 4 * (col & 3);
+        const __bf16* vb = k_s + (4 * grp + (col >> 2)) * KP + 16 * ls * NBW + 4 * (col & 3);
 #pragma unroll
         for (int nb = 0; nb < NBW; ++nb) {
             const vm_s4 lo = vm_lds_tr4(vb + 16 * nb), hi = vm_lds_tr4(vb + 16 * KP + 16 * nb);
-            const vm_h8 vop = __builtin_bit_cast(vm_h8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-            o_acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, vop, o_acc[nb], 0, 0, 0);
+            const vm_b8 vop = __builtin_bit_cast(vm_b8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            o_acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop, vop, o_acc[nb], 0, 0, 0);
         }
     };
     for (uint32_t ci = 0; ci < n_chunks; ++ci) chunk_step(ci);
