@@ -602,10 +602,10 @@ namespace {
 
 constexpr int kMNT = 2;  // tiles per wave (a gate/up pair for SWIGLU)
 
-// Used for 17-64 rows (Qwen2.5-7B decode at 32 sequences: 9797-9850 -> 9972-10164 tok/s).
+// Used for 17-128 rows (Qwen2.5-7B decode at 32 sequences: 9797-9850 -> 9972-10164 tok/s).
 // Two K halves per workgroup where the grid is at most one round of workgroups and each has 8 or
 // more groups (Llama-3-8B at 64 rows: gate/up 47.5 -> 36.2 us, down); one where the grid already
-// fills the CUs or the groups are few (QKV and o_proj split 6 and 8 ways over K, the LM head).
+// fills the CUs or the groups are few (QKV and o_proj split 5-8 ways over K, the LM head).
 template <int EPI, int MT, int KH>
 hipError_t vx_pgemm_launch_kh(const VxMMat& w, const VxBGemmArgs& a, dim3 grid, hipStream_t st) {
     constexpr size_t lds = (size_t)KH * 2 * 4 * MT * 1024;  // [half][stage][4 MT activation tiles of 1 KiB]
