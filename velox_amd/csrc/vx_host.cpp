@@ -61,9 +61,10 @@ uint32_t vx_mgemm_ksplit(const VxMatPlan& m) {
     return ks ? ks : 1u;
 }
 
-// K splits of the QKV GEMM over more than 64 rows (MFMA-bound): as many as keep the grid within one
-// round of 256 workgroups, where a partial second round would add a whole workgroup's time (Llama-3-8B
-// QKV at 128 rows: 48 x 6 workgroups 26.6 us, 48 x 5 21.9 us).
+// K splits of the QKV GEMM over more than 16 rows (the LDS-shared GEMM, 8 tiles per workgroup): as
+// many as keep the grid within one round of 256 workgroups, where a partial second round would add
+// a whole workgroup's time (Llama-3-8B QKV at 128 rows: 48 x 6 workgroups 26.6 us, 48 x 5 21.9 us;
+// Qwen2.5-7B at 32 sequences: 36 x 8 9.7 us, 36 x 7 8.3 us).
 uint32_t vx_pgemm_ksplit(const VxMatPlan& m) {
     const uint32_t wgs = vx_pgemm_grid(m.m_tiles);
     uint32_t ks = wgs ? 256u / wgs : 1u;
@@ -97,7 +98,7 @@ struct VeloxHipModel {
     // K-split partials of the residual GEMMs (o_proj, down): [ksplit][batch][hidden]
     uint64_t a_bpart_r = 0;
     uint32_t ksplit_o = 1, ksplit_down = 1, ksplit_qkv = 1;
-    uint32_t ksplit_qkv_wide = 1;  // QKV over chunks of more than 64 rows
+    uint32_t ksplit_qkv_wide = 1;  // QKV over more than 16 rows
     // fp16 activation operands of the batched GEMMs (over the MFMA-layout copies): element k of row m
     // at m * x_ld + (k / 32) * x_bs + k % 32, block-major [k / 32][16-row-padded rows][32] (one operand
     // load = 1 KiB contiguous)
@@ -1001,7 +1002,7 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
         g.bias = c.qkv_bias ? vecp(L.bias) : nullptr;
         g.y = qkv;
         g.ldy = qd + 2 * kvd;
-        const uint32_t ks_qkv = n > 64u ? M->ksplit_qkv_wide : M->ksplit_qkv;
+        const uint32_t ks_qkv = n > 16u ? M->ksplit_qkv_wide : M->ksplit_qkv;
         if (ks_qkv > 1) {  // K-split partials, then their sum + bias
             g.ksplit = ks_qkv;
             g.part = part_r;
