@@ -27,6 +27,9 @@ extern "C" {
 #define VELOX_HIP_ENOMEM (-2)    /* plan exceeds the VRAM budget (reference diagnostic E002) */
 #define VELOX_HIP_ESHAPE (-3)    /* tensor size does not match the plan */
 #define VELOX_HIP_ENOTLOADED (-4)
+#define VELOX_HIP_ETENSOR (-5)   /* checkpoint tensor missing, or its data_offsets outside the file
+                                    (reference diagnostic E013, src/runtime.rs:260-330) */
+#define VELOX_HIP_EDTYPE (-6)    /* checkpoint tensor of a dtype the load cannot take (E014) */
 
 /* ---- quant_mode values (src/codegen.rs:1024-1028 defines 0 fp32, 1 fp16, 2 group-64 "Q4",
  *      3/4 fp8). GGML Q4_0 is new to this backend and gets its own value. ---- */
@@ -56,7 +59,7 @@ typedef struct VeloxHipModelConfig {
     uint32_t tied_lm_head;      /* 1: LM head reads the embedding table */
     uint32_t quant_mode;        /* VELOX_QUANT_GGML_Q4_0; or the reference's formats (single-sequence decode
                                    only: max_batch and prefill_chunk <= 1): VELOX_QUANT_F32 / _F16 rows
-                                   (widths <= 16384), VELOX_QUANT_Q4_GROUP64 (widths multiples of 64) */
+                                   (widths <= 32768), VELOX_QUANT_Q4_GROUP64 (widths multiples of 64) */
     uint32_t attn_splits;       /* split-K partitions over the sequence (<= 64); 0 = automatic */
     uint64_t vram_budget_bytes; /* 0 = 288 GB of HBM3E */
     uint32_t max_batch;         /* sequences of the batched decode step (<= 32; 0 or 1 = single);
@@ -98,8 +101,9 @@ typedef struct VeloxDecodeState {
  * The model the decode step runs is read from the source's `model Name< const ... >` header
  * (VOCAB, HIDDEN_DIM, INTERMEDIATE_DIM, NUM_LAYERS, NUM_HEADS, NUM_KV_HEADS, HEAD_DIM, S_MAX, B_MAX,
  * ROPE_THETA), its weight declarations (b_q/b_k/b_v: QKV bias; no w_head/w_lm_head: tied head) and
- * its first rmsnorm eps; theta and eps fall back on the reference's name rules
- * (src/codegen.rs:962-975, src/ir.rs:549-553). The `target hardware` block gives the planner's
+ * its first weight binding's file; eps follows the model name as the reference's lowering sets it
+ * (src/ir.rs:549-553), theta falls back on its name rule (src/codegen.rs:962-975). Header
+ * constants must be whole numbers in 0..2^32-1. The `target hardware` block gives the planner's
  * budget: floor(vram_capacity * safety_factor) less the driver reserve (src/memory_planner.rs:372-
  * 488) -> vram_budget_bytes (0 without a target block: the default 288 GB). max_seq_len 0 takes
  * S_MAX. The config's max_batch and prefill_chunk stay 0: B_MAX is reported in the target info and
@@ -113,6 +117,8 @@ typedef struct VeloxHipVlxTarget {
     uint64_t safe_budget_bytes;     /* floor(vram_capacity * safety_factor) */
     uint64_t system_reserve_bytes;  /* driver + stream ring reserve */
     uint32_t b_max, s_max;          /* the model header's B_MAX and S_MAX (0 if absent) */
+    char weights_file[256];         /* the first safetensors("file", ...) binding ("" if none): the
+                                       checkpoint the CLI runs the model on (src/cli.rs:1400-1414) */
 } VeloxHipVlxTarget;
 int velox_hip_vlx_config(const char* source, uint32_t max_seq_len, VeloxHipModelConfig* out,
                          VeloxHipVlxTarget* target);
@@ -167,6 +173,19 @@ int velox_hip_load_rows(VeloxHipArena* a, int kind, uint32_t layer, const void* 
                         hipStream_t stream);
 int velox_hip_load_f32(VeloxHipArena* a, int kind, uint32_t layer, const float* data, uint64_t count,
                        hipStream_t stream);
+/* Element types of checkpoint tensors (safetensors "F32", "F16", "BF16"). */
+#define VELOX_DT_F32 0u
+#define VELOX_DT_F16 1u
+#define VELOX_DT_BF16 2u
+/* Any tensor kind from host data as a checkpoint stores it (row-major [rows][in] fp32, fp16 or bf16;
+ * vectors [n]), converted on the device into the arena's format, as the reference runner's
+ * stream_tensor_converted does (velox_cuda_runner.cu:154-199): fp32 or fp16 rows (fp16 rounded to
+ * nearest even), the reference's group-64 format, or GGML Q4_0 (quantized on the device, bit-exact
+ * with velox_hip_q4_0_quantize). Matrices go through the device in chunks of at most 64 MiB of
+ * fp32; norm gains and biases are widened to fp32. ESHAPE when nbytes is not the kind's size,
+ * EDTYPE for another dtype; the tied head takes no separate load (EINVAL). */
+int velox_hip_load_tensor(VeloxHipArena* a, int kind, uint32_t layer, const void* data, uint64_t nbytes,
+                          uint32_t dtype, hipStream_t stream);
 /* Synthesizes the whole seeded model on the device (linear weights N(0,sigma) quantized to Q4_0,
  * as fp32 / fp16 rows, or quantized to group-64, per quant_mode; norm gains 1 or N(1,norm_sigma), biases
  * N(0,sigma)), bit-identical to the oracle's recipe. */
@@ -391,8 +410,12 @@ typedef struct VeloxHipRunOptions {
                                 (src/runners/velox_cuda_runner_k2.cu:1789 --context-len) */
     uint32_t batch;          /* >1: decode `batch` independent sequences per step (own seeded prompt and
                                 context each); tokens/report cover sequence 0, tok_per_s all of them */
-    const char* weights_path;/* NULL: synthetic weights of `model`; else a GGUF Q4_0 checkpoint whose
-                                metadata defines the model (the runner's --weights file.gguf) */
+    const char* weights_path;/* NULL: synthetic weights of `model`; else a checkpoint (the runner's
+                                --weights): a GGUF Q4_0 file (by its magic), whose metadata defines
+                                the model, or a safetensors file, run on model_file's or model's
+                                configuration, or with both NULL on the builtin one its tensor shapes
+                                match (velox_hip_st_config), converted to the quant_mode
+                                `unquantized` selects */
     uint32_t prefill_chunk;  /* >1 (single sequence, no context_len): the prompt runs through
                                 velox_hip_prefill_batch in chunks of this many positions (<= 128)
                                 instead of one decode step each */
@@ -401,7 +424,9 @@ typedef struct VeloxHipRunOptions {
     uint32_t unquantized;    /* 0: GGML Q4_0 weights; else the reference's fp32 weights (single sequence
                                 only): 1 as fp32 rows (a build without --quantize, src/cli.rs:1214-1388),
                                 2 converted to fp16 rows (--quantize f16), 3 quantized to group-64
-                                (--quantize q4_0, velox_cuda_runner.cu:356-372) */
+                                (--quantize q4_0, velox_cuda_runner.cu:356-372). A safetensors
+                                checkpoint is converted on the device to the format chosen (0:
+                                quantized to GGML Q4_0 there) */
 } VeloxHipRunOptions;
 
 typedef struct VeloxHipRunReport {
@@ -441,6 +466,39 @@ int velox_hip_gguf_tensor_info(const VeloxHipGguf* g, uint64_t i, char* name, ui
                                uint32_t* n_dims, uint64_t* dims, uint64_t* nbytes);
 int velox_hip_gguf_config(const VeloxHipGguf* g, uint32_t max_seq_len, VeloxHipModelConfig* out);
 int velox_hip_gguf_load(VeloxHipArena* arena, const VeloxHipGguf* g, hipStream_t stream);
+
+/* ---- safetensors checkpoints (the reference runner's --weights file: velox_cuda_runner.cu:60-199,
+ * 390-393; its CPU engine's MmapSafetensors, src/runtime.rs:200-520; Hugging Face tensor names as
+ * load_safetensors resolves them, src/runtime.rs:1258-1300) ----
+ * open: memory-maps the file and parses the 8-byte header length and the UTF-8 JSON header;
+ *   ENOTLOADED when the file cannot be opened, EINVAL for a file under 8 bytes, a header length
+ *   past the end of the file, invalid UTF-8 or JSON that is not an object of {dtype, shape,
+ *   data_offsets} entries ("__metadata__" is skipped).
+ * find / tensor_data: "lm_head.weight" falls back on "model.embed_tokens.weight" when absent (the
+ *   tied head); ETENSOR (E013) for a missing name or data_offsets inverted or past the end of the
+ *   file, EDTYPE (E014) when the stored dtype is not `dtype`, ESHAPE when the byte count is not the
+ *   shape's.
+ * config: the model of a file (vocabulary, depth, QKV bias and head tying from its tensors; head
+ *   count and size from the builtin configuration with the same layer shapes, which also gives eps
+ *   and theta); EINVAL when none matches. quant_mode is VELOX_QUANT_F32, the reference runner's
+ *   default.
+ * check: every tensor the configuration needs is present, F32/F16/BF16, in the file and shaped
+ *   [out][in] ([n] for vectors).
+ * load: check, then every tensor through velox_hip_load_tensor into an arena planned with the
+ *   configuration (converted to its quant_mode on the device). */
+typedef struct VeloxHipSafetensors VeloxHipSafetensors;
+int velox_hip_st_open(const char* path, VeloxHipSafetensors** out);
+void velox_hip_st_close(VeloxHipSafetensors* st);
+uint64_t velox_hip_st_tensor_count(const VeloxHipSafetensors* st);
+/* dtype: 16 bytes; shape: up to 8 entries; begin/end: data_offsets as written */
+int velox_hip_st_tensor_info(const VeloxHipSafetensors* st, uint64_t i, char* name, uint32_t name_cap, char* dtype,
+                             uint64_t* shape, uint32_t* n_dims, uint64_t* begin, uint64_t* end);
+int velox_hip_st_find(const VeloxHipSafetensors* st, const char* name, uint64_t* index);
+int velox_hip_st_tensor_data(const VeloxHipSafetensors* st, const char* name, const char* dtype, const void** data,
+                             uint64_t* nbytes);
+int velox_hip_st_config(const VeloxHipSafetensors* st, uint32_t max_seq_len, VeloxHipModelConfig* out);
+int velox_hip_st_check(const VeloxHipSafetensors* st, const VeloxHipModelConfig* cfg);
+int velox_hip_st_load(VeloxHipArena* arena, const VeloxHipSafetensors* st, hipStream_t stream);
 
 /* ---- Absorbed multi-head latent attention layer (benchmark configuration 4, DeepSeek-V3 form) ----
  * Replaces the reference's MLA step: the emitted velox_cuda_fused_mla_absorbed_attn

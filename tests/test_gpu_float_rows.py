@@ -183,3 +183,28 @@ def test_runner_unquantized_fp32_matches_the_engine(oracle):
     if srt[-1] - srt[-2] > 2 * BF16_TOL:
         assert steps[0] == t_ref
     ref.close()
+
+
+@pytest.mark.parametrize("quant", [L.QUANT_F32, L.QUANT_F16])
+@pytest.mark.parametrize("ffn", [16384, 29568])
+def test_wide_rows_past_64k_of_lds(oracle, quant, ffn):
+    """The float-row GEMV holds a row's fp32 activations in LDS: the down projection's 16384-wide rows
+    take 65,600 bytes and Qwen2-72B's 29568-wide ones 118,336, past the 64 KiB default the launch
+    raises. One layer of that width decodes within the fp32-accumulation bar of the oracle on the
+    GPU's own K/V rows."""
+    cfg = dict(vocab_size=512, hidden_dim=256, intermediate_dim=ffn, num_layers=1, num_heads=4, num_kv_heads=2,
+               head_dim=64, rms_norm_eps=1e-5, rope_theta=10000.0, qkv_bias=0, tied_lm_head=1)
+    gpu = HipDecodeEngine(dict(cfg, quant_mode=quant), seed=9, norm_sigma=0.1, max_seq_len=8)
+    ref = oracle.Engine(dict(cfg, max_seq_len=8), seed=9, sigma=0.02, norm_sigma=0.1, q4_0=False, kv_bf16=True,
+                        w_f16=quant == L.QUANT_F16, threads=8)
+    for pos, tok in enumerate((3, 500, 17)):
+        tg = gpu.forward_step(tok, pos)
+        kv = _device_kv(gpu.arena, 0, 2, 8, 64, pos + 1)
+        kr, vr = ref.kv_cache(0)
+        kr[:pos], vr[:pos] = kv[0][:pos], kv[1][:pos]
+        ref.forward_forced(tok, pos, kv[0][pos][None], kv[1][pos][None])
+        d = float(np.max(np.abs(gpu.logits - ref.logits)))
+        print(f"[float rows K={ffn} quant={quant}] pos={pos} max-abs {d:.2e}", flush=True)
+        assert tg == oracle.argmax(gpu.logits) and d < F32_TOL, (pos, d)
+    gpu.close()
+    ref.close()

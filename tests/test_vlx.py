@@ -64,7 +64,10 @@ def test_reader_on_a_source_of_its_own():
     assert _shape(c) == (1000, 256, 512, 2, 4, 2, 64)  # HEAD_DIM defaults to HIDDEN_DIM / NUM_HEADS
     assert c.max_seq_len == 1024 and c.qkv_bias == 0 and c.tied_lm_head == 0
     assert c.rope_theta == 500000.0  # "llama" in the name (src/codegen.rs:962-975)
-    assert abs(c.rms_norm_eps - 2.5e-6) < 1e-12  # the file's own eps
+    # eps by the model's name, as the reference's lowering sets it (src/ir.rs:549-553), not the
+    # source's `eps = 2.5e-6`, which its emitted kernels do not receive either
+    assert abs(c.rms_norm_eps - 1e-5) < 1e-12
+    assert t.weights_file.decode() == "x"  # the first safetensors("x", ...) binding
     assert t.device.decode() == "amd_mi355x" and t.vram_capacity_bytes == 288 * 10 ** 9
     assert t.safe_budget_bytes == 144 * 10 ** 9 and t.b_max == 4 and t.s_max == 1024
     assert c.vram_budget_bytes == _budget(288 * 10 ** 9, 0.5)
@@ -81,6 +84,22 @@ def test_reader_on_a_source_of_its_own():
 ])
 def test_reader_rejects_malformed_sources(bad):
     assert _cfg(bad)[0] == L.EINVAL
+
+
+@pytest.mark.parametrize("bad", [
+    MINI.replace("const NUM_LAYERS: usize = 2,", "const NUM_LAYERS: usize = 0 - 2,"),     # negative
+    MINI.replace("const NUM_LAYERS: usize = 2,", "const NUM_LAYERS: usize = 2.5,"),       # fractional
+    MINI.replace("const B_MAX: usize = 4,", "const B_MAX: usize = 9000000000,"),           # past 2^32
+    MINI.replace("const S_MAX: usize = 0x400,", "const S_MAX: usize = 0 - 1,"),
+])
+def test_reader_rejects_constants_out_of_range(bad):
+    assert _cfg(bad)[0] == L.EINVAL
+
+
+def test_eps_follows_the_model_name():
+    for name, want in (("Qwen_Tiny", 1e-6), ("Tiny_K2", 1e-6), ("Horizon_X", 1e-6), ("Mistral_Tiny", 1e-5)):
+        rc, c, _ = _cfg(MINI.replace("model Tiny_Llama<", f"model {name}<"))
+        assert rc == 0 and abs(c.rms_norm_eps - want) < 1e-12, name
 
 
 def test_missing_file_is_not_loaded():

@@ -16,7 +16,8 @@ HEADER = os.path.join(ROOT, "include", "velox_hip.h")
 # quant_mode: the reference's fp32 / fp16 rows and group-64 format, GGML Q4_0
 QUANT_F32, QUANT_F16, QUANT_G64, QUANT_GGML_Q4_0 = 0, 1, 2, 5
 GEMV_STORE, GEMV_RESIDUAL, GEMV_SWIGLU = 0, 1, 2
-EINVAL, ENOMEM, ESHAPE, ENOTLOADED = -1, -2, -3, -4
+EINVAL, ENOMEM, ESHAPE, ENOTLOADED, ETENSOR, EDTYPE = -1, -2, -3, -4, -5, -6
+DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 T_EMBED, T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN = 1, 2, 3, 4, 5, 6, 7, 8
 T_ATTN_NORM, T_MLP_NORM, T_FINAL_NORM, T_HEAD, T_BQ, T_BK, T_BV = 9, 10, 11, 12, 13, 14, 15
 RING_SIZE = 1024
@@ -84,7 +85,7 @@ class RunReport(C.Structure):
 class VlxTarget(C.Structure):
     _fields_ = [("device", C.c_char * 64), ("vram_capacity_bytes", C.c_uint64), ("safety_factor", C.c_double),
                 ("safe_budget_bytes", C.c_uint64), ("system_reserve_bytes", C.c_uint64), ("b_max", C.c_uint32),
-                ("s_max", C.c_uint32)]
+                ("s_max", C.c_uint32), ("weights_file", C.c_char * 256)]
 
 
 class MlaConfig(C.Structure):
@@ -140,6 +141,17 @@ _SIGS = {
     "velox_hip_load_q4_0": (_I, [C.POINTER(Arena), _I, _U32, _P, _U64, _P]),
     "velox_hip_load_rows": (_I, [C.POINTER(Arena), _I, _U32, _P, _U64, _P]),
     "velox_hip_load_f32": (_I, [C.POINTER(Arena), _I, _U32, _P, _U64, _P]),
+    "velox_hip_load_tensor": (_I, [C.POINTER(Arena), _I, _U32, _P, _U64, _U32, _P]),
+    "velox_hip_st_open": (_I, [C.c_char_p, C.POINTER(_P)]),
+    "velox_hip_st_close": (None, [_P]),
+    "velox_hip_st_tensor_count": (_U64, [_P]),
+    "velox_hip_st_tensor_info": (_I, [_P, _U64, C.c_char_p, _U32, C.c_char_p, C.POINTER(_U64), C.POINTER(_U32),
+                                      C.POINTER(_U64), C.POINTER(_U64)]),
+    "velox_hip_st_find": (_I, [_P, C.c_char_p, C.POINTER(_U64)]),
+    "velox_hip_st_tensor_data": (_I, [_P, C.c_char_p, C.c_char_p, C.POINTER(_P), C.POINTER(_U64)]),
+    "velox_hip_st_config": (_I, [_P, _U32, C.POINTER(ModelConfig)]),
+    "velox_hip_st_check": (_I, [_P, C.POINTER(ModelConfig)]),
+    "velox_hip_st_load": (_I, [C.POINTER(Arena), _P, _P]),
     "velox_hip_synthesize_model": (_I, [C.POINTER(Arena), _U64, _F, _F, _P]),
     "velox_hip_fill_kv": (_I, [C.POINTER(Arena), _U32, _U32, _U64, _F, _P]),
     "velox_hip_set_prompt": (_I, [C.POINTER(Arena), C.POINTER(_U32), _U32, _P]),

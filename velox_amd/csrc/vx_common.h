@@ -101,7 +101,7 @@ VX_HD uint32_t vx_vslot(uint32_t r) { return 8u * ((r & 15u) >> 2) + 4u * (r >> 
 // [rows][k] (paired: n gate rows, then n up rows), n_tiles = ceil(n / 4) tiles of 4 logical rows,
 // no scales.
 enum { VX_FMT_Q4 = 0, VX_FMT_F32 = 1, VX_FMT_F16 = 2, VX_FMT_G64 = 3 };
-constexpr uint32_t kVxFloatMaxK = 16384;  // fp32 activations of a float-row GEMV in LDS
+constexpr uint32_t kVxFloatMaxK = 32768;  // fp32 activations of a float-row GEMV in LDS (128 KiB)
 
 struct VxMat {
     const uint4* codes;
@@ -309,6 +309,9 @@ hipError_t vx_launch_fill_kv(uint16_t* layer_base, uint32_t hkv, uint32_t s_cap,
                              uint64_t stream_k, uint64_t stream_v, float coef, hipStream_t st);
 hipError_t vx_launch_dequant(const VxMat& m, float* out, hipStream_t st);
 hipError_t vx_launch_quantize(const float* x, uint32_t rows, uint32_t k, void* blocks, hipStream_t st);
+// Element types of checkpoint tensors (safetensors F32 / F16 / BF16) for vx_launch_convert.
+enum { VX_DT_F32 = 0, VX_DT_F16 = 1, VX_DT_BF16 = 2 };
+hipError_t vx_launch_convert(const void* src, uint32_t src_dt, void* dst, uint32_t dst_dt, uint64_t n, hipStream_t st);
 hipError_t vx_launch_rmsnorm(const float* x, const float* w, uint32_t n, float eps, float* y, hipStream_t st);
 hipError_t vx_launch_argmax(const float* x, uint32_t n, uint32_t* out, hipStream_t st);
 uint32_t vx_gemv_max_wgs_default();

@@ -188,6 +188,18 @@ __global__ __launch_bounds__(kFThreads) void vx_gemv_f_kernel(VxMat m, VxGemvArg
 template <typename T, int EPI, bool NORM, int SPL>
 hipError_t vx_gemv_f_launch_t(const VxMat& m, const VxGemvArgs& a, uint32_t wgs, hipStream_t st) {
     const size_t lds = (size_t)m.k * 4u + 2u * kFWaves * 4u;
+    // rows wider than 16376 need more than the default 64 KiB of dynamic LDS (up to 128 KiB + 64 B
+    // at kVxFloatMaxK, of the 160 KiB a CU has): raised once per instantiation to the widest row
+    static bool attr_set = false;
+    if (lds > 65536u && !attr_set) {
+        if (hipFuncSetAttribute((const void*)vx_gemv_f_kernel<T, EPI, NORM, SPL>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)((size_t)kVxFloatMaxK * 4u + 2u * kFWaves * 4u)) != hipSuccess) {
+            (void)hipGetLastError();
+            return hipErrorInvalidValue;
+        }
+        attr_set = true;
+    }
     hipLaunchKernelGGL((vx_gemv_f_kernel<T, EPI, NORM, SPL>), dim3(wgs), dim3(kFThreads), lds, st, m, a);
     return hipGetLastError();
 }

@@ -6,6 +6,7 @@
 // the C ABI of include/velox_hip.h.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -753,6 +754,88 @@ int velox_hip_load_rows(VeloxHipArena* a, int kind, uint32_t layer, const void* 
     hipError_t e = hipMemcpyAsync((void*)(a->weight_arena + mp->code_off + first * cols * elt), rows_data, nbytes,
                                   hipMemcpyHostToDevice, stream);
     if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    return (int)e;
+}
+
+int velox_hip_load_tensor(VeloxHipArena* a, int kind, uint32_t layer, const void* data, uint64_t nbytes,
+                          uint32_t dtype, hipStream_t stream) {
+    const VeloxHipModel* M = a ? vx_model(a) : nullptr;
+    if (!M || !data) return VELOX_HIP_EINVAL;
+    if (dtype > VELOX_DT_BF16) return VELOX_HIP_EDTYPE;
+    const uint64_t elt = dtype == VELOX_DT_F32 ? 4 : 2;
+    uint64_t voff, vn;
+    if (vx_vec_target(M, kind, layer, &voff, &vn)) {
+        if (nbytes != vn * elt) return VELOX_HIP_ESHAPE;
+        float* dst = (float*)(a->norm_weight_arena + voff);
+        hipError_t e = hipSuccess;
+        if (dtype == VELOX_DT_F32) {
+            e = hipMemcpyAsync(dst, data, nbytes, hipMemcpyHostToDevice, stream);
+        } else {
+            void* staging = nullptr;
+            e = hipMalloc(&staging, nbytes);
+            if (e == hipSuccess) e = hipMemcpyAsync(staging, data, nbytes, hipMemcpyHostToDevice, stream);
+            if (e == hipSuccess) e = vx_launch_convert(staging, dtype, dst, VX_DT_F32, vn, stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(stream);
+            hipFree(staging);
+        }
+        if (e == hipSuccess) e = hipStreamSynchronize(stream);
+        return (int)e;
+    }
+    const VxMatPlan* mp;
+    uint32_t row0, pair, rows, cols;
+    if (kind == VELOX_T_HEAD && M->cfg.tied_lm_head) return VELOX_HIP_EINVAL;  // the head is the embedding
+    if (!vx_target(M, kind, layer, &mp, &row0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
+    if (nbytes != (uint64_t)rows * cols * elt) return VELOX_HIP_ESHAPE;
+    // Rows go through the device in chunks of at most 64 MiB of fp32 (the reference stages 64 MiB
+    // chunks too, velox_cuda_runner.cu:172-197): upload as stored, widen or narrow on the device,
+    // and for the 4-bit formats quantize there into the tiled layout.
+    const uint64_t row_f32 = (uint64_t)cols * 4;
+    const uint32_t chunk = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(rows, (64ull << 20) / row_f32));
+    const bool quant = mp->fmt == VX_FMT_Q4 || mp->fmt == VX_FMT_G64;
+    const bool direct = mp->fmt == VX_FMT_F32 && dtype == VELOX_DT_F32;
+    void *src_st = nullptr, *f32_st = nullptr, *blk_st = nullptr;
+    hipError_t e = hipSuccess;
+    if (!direct) e = hipMalloc(&src_st, (uint64_t)chunk * cols * elt);
+    if (e == hipSuccess && quant && dtype != VELOX_DT_F32) e = hipMalloc(&f32_st, (uint64_t)chunk * row_f32);
+    if (e == hipSuccess && mp->fmt == VX_FMT_Q4) e = hipMalloc(&blk_st, (uint64_t)chunk * (cols / 32) * 18);
+    const uint64_t first = (uint64_t)(pair ? mp->n : 0) + row0;  // row-major formats: up rows follow the gate rows
+    uint8_t* rows_dst = (uint8_t*)a->weight_arena + mp->code_off;
+    for (uint32_t r = 0; r < rows && e == hipSuccess; r += chunk) {
+        const uint32_t n = std::min(chunk, rows - r);
+        const uint64_t cnt = (uint64_t)n * cols;
+        const uint8_t* src = (const uint8_t*)data + (uint64_t)r * cols * elt;
+        if (direct) {
+            e = hipMemcpyAsync(rows_dst + (first + r) * row_f32, src, cnt * 4, hipMemcpyHostToDevice, stream);
+            continue;
+        }
+        e = hipMemcpyAsync(src_st, src, cnt * elt, hipMemcpyHostToDevice, stream);
+        if (e != hipSuccess) break;
+        if (mp->fmt == VX_FMT_F32 || mp->fmt == VX_FMT_F16) {
+            const uint64_t out_elt = mp->fmt == VX_FMT_F32 ? 4 : 2;
+            e = vx_launch_convert(src_st, dtype, rows_dst + (first + r) * cols * out_elt,
+                                  mp->fmt == VX_FMT_F32 ? VX_DT_F32 : VX_DT_F16, cnt, stream);
+        } else {
+            const float* x = (const float*)src_st;
+            if (dtype != VELOX_DT_F32) {
+                e = vx_launch_convert(src_st, dtype, f32_st, VX_DT_F32, cnt, stream);
+                x = (const float*)f32_st;
+            }
+            if (e == hipSuccess && mp->fmt == VX_FMT_G64)
+                e = vx_launch_g64_from_rows(x, n, row0 + r, pair, vx_view(a, *mp), stream);
+            if (e == hipSuccess && mp->fmt == VX_FMT_Q4) {
+                e = vx_launch_quantize(x, n, cols, blk_st, stream);
+                if (e == hipSuccess) e = vx_launch_repack(blk_st, n, row0 + r, pair, vx_view(a, *mp), stream);
+            }
+        }
+        // the staging buffers are reused by the next chunk
+        if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    }
+    if (e == hipSuccess && mp->fmt == VX_FMT_Q4) e = vx_build_m(a, *mp, stream);
+    if (e == hipSuccess && mp->fmt == VX_FMT_Q4 && kind == VELOX_T_EMBED && M->cfg.tied_lm_head) e = vx_build_m(a, M->head, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    hipFree(src_st);
+    hipFree(f32_st);
+    hipFree(blk_st);
     return (int)e;
 }
 
@@ -1531,6 +1614,16 @@ int velox_hip_attention_decode(const float* d_qkv, uint16_t* d_kv_layer, uint32_
 // Runner: the flow of velox_cuda_runner.cu main (:327-726) -- plan, alloc, load (synthesize),
 // graph capture (:474-481), prefill (:493-512), timed decode replays (:535-563).
 // ---------------------------------------------------------------------------------------------
+// GGUF files start with the magic "GGUF"; any other checkpoint is read as safetensors.
+static bool vx_is_gguf(const char* path) {
+    FILE* f = std::fopen(path, "rb");
+    if (!f) return false;
+    char m[4] = {0, 0, 0, 0};
+    const size_t n = std::fread(m, 1, 4, f);
+    std::fclose(f);
+    return n == 4 && !std::memcmp(m, "GGUF", 4);
+}
+
 int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_tokens, VeloxHipRunReport* rep) {
     if (!opt || !rep || (!opt->model && !opt->weights_path && !opt->model_file) || opt->prompt_len == 0)
         return VELOX_HIP_EINVAL;
@@ -1540,20 +1633,31 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
     const uint32_t total = base + opt->prompt_len + opt->warmup + opt->steps;
     VeloxHipModelConfig cfg;
     VeloxHipGguf* gguf = nullptr;
+    VeloxHipSafetensors* stf = nullptr;
     int rc;
-    if (opt->weights_path) {
+    const uint32_t msl = opt->max_seq_len ? opt->max_seq_len : total + 1;
+    if (opt->weights_path && vx_is_gguf(opt->weights_path)) {
         rc = velox_hip_gguf_open(opt->weights_path, &gguf);
-        if (!rc) rc = velox_hip_gguf_config(gguf, opt->max_seq_len ? opt->max_seq_len : total + 1, &cfg);
+        if (!rc) rc = velox_hip_gguf_config(gguf, msl, &cfg);
         if (rc) { velox_hip_gguf_close(gguf); return rc; }
-    } else if (opt->model_file) {
-        rc = velox_hip_vlx_load(opt->model_file, opt->max_seq_len ? opt->max_seq_len : total + 1, &cfg, nullptr);
-        if (rc) return rc;
     } else {
-        rc = velox_hip_builtin_config(opt->model, opt->max_seq_len ? opt->max_seq_len : total + 1, &cfg);
-        if (rc) return rc;
+        // a safetensors checkpoint (the reference runner's --weights) runs on the model the caller
+        // names, or on the builtin configuration its tensor shapes match
+        if (opt->weights_path) {
+            rc = velox_hip_st_open(opt->weights_path, &stf);
+            if (rc) return rc;
+        }
+        if (opt->model_file) rc = velox_hip_vlx_load(opt->model_file, msl, &cfg, nullptr);
+        else if (opt->model) rc = velox_hip_builtin_config(opt->model, msl, &cfg);
+        else rc = velox_hip_st_config(stf, msl, &cfg);
+        if (rc) { velox_hip_st_close(stf); return rc; }
     }
     // the arena's model stays alive until the end of the run; the file is closed once loaded
-    struct GgufCloser { VeloxHipGguf*& g; ~GgufCloser() { velox_hip_gguf_close(g); } } gguf_closer{gguf};
+    struct Closer {
+        VeloxHipGguf*& g;
+        VeloxHipSafetensors*& s;
+        ~Closer() { velox_hip_gguf_close(g); velox_hip_st_close(s); }
+    } closer{gguf, stf};
     if (opt->num_layers && !gguf) cfg.num_layers = opt->num_layers;
     if (opt->unquantized > 3 || (opt->unquantized && gguf)) return VELOX_HIP_EINVAL;
     if (opt->unquantized)
@@ -1568,6 +1672,7 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
     if (batched_prefill && (B > 1 || opt->prefill_chunk > 128 || base)) return VELOX_HIP_EINVAL;
     if (batched_prefill) cfg.prefill_chunk = opt->prefill_chunk;
     if (cfg.max_seq_len < total) return VELOX_HIP_EINVAL;
+    if (stf && (rc = velox_hip_st_check(stf, &cfg)) != 0) return rc;  // before any device allocation
     VeloxHipModel* M = nullptr;
     rc = velox_hip_model_create(&cfg, &M);
     if (rc) return rc;
@@ -1582,7 +1687,9 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
     hipGraphExec_t exec = nullptr;
 
     const auto t_load = std::chrono::steady_clock::now();
-    rc = gguf ? velox_hip_gguf_load(&A, gguf, st) : velox_hip_synthesize_model(&A, opt->seed, opt->sigma, opt->norm_sigma, st);
+    rc = gguf  ? velox_hip_gguf_load(&A, gguf, st)
+         : stf ? velox_hip_st_load(&A, stf, st)
+               : velox_hip_synthesize_model(&A, opt->seed, opt->sigma, opt->norm_sigma, st);
     rep->load_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_load).count();
 
     // sequence b's prompt: seeded ids (sequence 0: the single-sequence prompt) or explicit ones

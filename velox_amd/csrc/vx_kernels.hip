@@ -637,6 +637,21 @@ __global__ __launch_bounds__(kWG) void vx_quantize_kernel(const float* x, uint32
     for (int j = 0; j < 16; ++j) o[2 + j] = qs[j];
 }
 
+// Checkpoint elements as stored (fp32, fp16 or bf16: VX_DT_*) widened to fp32, or rounded to fp16
+// (nearest even), for the loaders (the reference converts on the device at load as well,
+// velox_cuda_f32_to_f16_kernel in src/runners/velox_cuda_runner.cu:174-197).
+__global__ __launch_bounds__(kWG) void vx_convert_kernel(const void* src, uint32_t src_dt, void* dst, uint32_t dst_dt,
+                                                         uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kWG + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kWG) {
+        float v;
+        if (src_dt == VX_DT_F32) v = ((const float*)src)[i];
+        else if (src_dt == VX_DT_F16) v = vx_f16_bits_to_f32(((const uint16_t*)src)[i]);
+        else v = vx_bf16_bits_to_f32(((const uint16_t*)src)[i]);
+        if (dst_dt == VX_DT_F32) ((float*)dst)[i] = v;
+        else ((uint16_t*)dst)[i] = vx_f32_to_f16_bits(v);
+    }
+}
+
 __global__ __launch_bounds__(kWG) void vx_rmsnorm_kernel(const float* x, const float* w, uint32_t n, float eps, float* y) {
     __shared__ float red[4];
     float ss = 0.0f;
@@ -845,6 +860,14 @@ hipError_t vx_launch_quantize(const float* x, uint32_t rows, uint32_t k, void* b
     const size_t n = (size_t)rows * (k >> 5);
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(vx_quantize_kernel, vx_grid_for(n), dim3(kWG), 0, st, x, rows, k, (uint8_t*)blocks);
+    return hipGetLastError();
+}
+
+hipError_t vx_launch_convert(const void* src, uint32_t src_dt, void* dst, uint32_t dst_dt, uint64_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    const size_t g = (n + kWG - 1) / kWG;
+    hipLaunchKernelGGL(vx_convert_kernel, dim3((unsigned)(g < 65536 ? g : 65536)), dim3(kWG), 0, st, src, src_dt, dst,
+                       dst_dt, n);
     return hipGetLastError();
 }
 

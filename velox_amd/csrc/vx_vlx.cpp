@@ -12,10 +12,12 @@
 //     NUM_LAYERS, NUM_HEADS, NUM_KV_HEADS, HEAD_DIM, S_MAX, B_MAX, and ROPE_THETA where given;
 //   * the weight declarations: q/k/v biases (`b_q`, `b_k`, `b_v`) and an LM head (`w_head` or
 //     `w_lm_head`, src/codegen.rs:1063; without one the head is tied to the embedding);
-//   * the RMSNorm epsilon of the first `rmsnorm(..., eps = X)`.
-// Where the file does not say, the reference's own fallbacks apply: theta by model name
-// (src/codegen.rs:962-975: llama 5e5, qwen 1e6, else 1e4), epsilon by model name
-// (src/ir.rs:549-553: Qwen/K2/Horizon 1e-6, else 1e-5).
+//   * the first weight binding's file, `safetensors("file", "key")`, which the CLI hands the runner
+//     as its --weights (src/cli.rs:1400-1414).
+// The RMSNorm epsilon follows the model's name as the reference's lowering sets it
+// (src/ir.rs:549-553: Qwen/K2/Horizon 1e-6, else 1e-5), whatever `eps =` the source writes; theta
+// is ROPE_THETA or, where the file does not say, the name rule of src/codegen.rs:962-975 (llama
+// 5e5, qwen 1e6, else 1e4).
 // MLA models (LATENT_KV_DIM, src examples/deepseek_v3_mla.vlx) map to the MLA layer's
 // configuration instead.
 #include <cctype>
@@ -189,7 +191,7 @@ struct VxVlx {
     bool has_target = false;
     std::map<std::string, double> consts;
     std::vector<std::string> weights;
-    double eps = 0.0;  // 0: not given
+    std::string weights_file;  // the first `safetensors("file", "key")` binding's file
 };
 
 bool vx_parse(const std::string& src, VxVlx& v) {
@@ -241,19 +243,11 @@ bool vx_parse(const std::string& src, VxVlx& v) {
         } else if (P.is("weight") && P.peek(1).kind == VxTok::Ident) {
             v.weights.push_back(P.peek(1).text);
             P.p += 2;
-        } else if (P.is("rmsnorm") && P.is("(", 1) && v.eps == 0.0) {
-            // the first rmsnorm call's `eps = X` argument, if any, before its closing parenthesis
-            size_t q = P.p + 2;
-            int depth = 1;
-            while (q < toks.size() && depth > 0 && toks[q].kind != VxTok::End) {
-                if (toks[q].text == "(" && toks[q].kind == VxTok::Punct) ++depth;
-                else if (toks[q].text == ")" && toks[q].kind == VxTok::Punct) --depth;
-                else if (depth == 1 && toks[q].kind == VxTok::Ident && toks[q].text == "eps" && q + 2 < toks.size() &&
-                         toks[q + 1].text == "=" && toks[q + 2].kind == VxTok::Number)
-                    v.eps = toks[q + 2].num;
-                ++q;
-            }
-            P.p += 2;
+        } else if (P.is("safetensors") && P.is("(", 1) && P.peek(2).kind == VxTok::String) {
+            // a weight binding (src/ast.rs:1084); the CLI runs the model on the first one's file
+            // (src/cli.rs:1400-1414)
+            if (v.weights_file.empty()) v.weights_file = P.peek(2).text;
+            P.p += 3;
         } else {
             ++P.p;
         }
@@ -293,20 +287,32 @@ uint64_t vx_system_reserve(uint64_t vram) {
     return vram / 32;
 }
 
-void vx_fill_target(const VxVlx& v, VeloxHipVlxTarget* t) {
-    if (!t) return;
+// A header constant as a 32-bit count: `dflt` when absent, false when negative, fractional or
+// beyond 2^32 - 1 (a malformed source).
+bool vx_const_u32(const VxVlx& v, const char* k, uint32_t dflt, uint32_t* out) {
+    const auto it = v.consts.find(k);
+    if (it == v.consts.end()) { *out = dflt; return true; }
+    const double x = it->second;
+    if (!(x >= 0.0 && x <= 4294967295.0) || x != std::floor(x)) return false;
+    *out = (uint32_t)x;
+    return true;
+}
+
+bool vx_fill_target(const VxVlx& v, VeloxHipVlxTarget* t) {
+    uint32_t b_max, s_max;
+    if (!vx_const_u32(v, "B_MAX", 0, &b_max) || !vx_const_u32(v, "S_MAX", 0, &s_max)) return false;
+    if (!(v.vram >= 0.0 && v.vram < 1.8e19) || !(v.safety >= 0.0 && v.safety <= 1.0e3)) return false;
+    if (!t) return true;
     std::memset(t, 0, sizeof(*t));
     std::snprintf(t->device, sizeof(t->device), "%s", v.device.c_str());
     t->vram_capacity_bytes = (uint64_t)v.vram;
     t->safety_factor = v.safety;
     t->system_reserve_bytes = vx_system_reserve(t->vram_capacity_bytes);
     t->safe_budget_bytes = (uint64_t)std::floor((double)t->vram_capacity_bytes * v.safety);
-    auto get = [&](const char* k) -> uint32_t {
-        const auto it = v.consts.find(k);
-        return it == v.consts.end() ? 0u : (uint32_t)it->second;
-    };
-    t->b_max = get("B_MAX");
-    t->s_max = get("S_MAX");
+    t->b_max = b_max;
+    t->s_max = s_max;
+    std::snprintf(t->weights_file, sizeof(t->weights_file), "%s", v.weights_file.c_str());
+    return true;
 }
 
 // The planner's budget for this backend's own regions: the safe budget less the driver reserve
@@ -319,10 +325,11 @@ uint64_t vx_budget(const VxVlx& v) {
 }
 
 int vx_config_from(const VxVlx& v, uint32_t max_seq_len, VeloxHipModelConfig* out, VeloxHipVlxTarget* target) {
+    bool in_range = true;
     auto get = [&](const char* k, uint32_t dflt) -> uint32_t {
-        const auto it = v.consts.find(k);
-        if (it == v.consts.end()) return dflt;
-        return it->second >= 0.0 && it->second <= 4294967295.0 ? (uint32_t)it->second : 0u;
+        uint32_t x = 0;
+        if (!vx_const_u32(v, k, dflt, &x)) in_range = false;
+        return x;
     };
     if (v.consts.count("LATENT_KV_DIM")) return VELOX_HIP_EINVAL;  // an MLA model: velox_hip_vlx_mla_config
     VeloxHipModelConfig c;
@@ -336,21 +343,22 @@ int vx_config_from(const VxVlx& v, uint32_t max_seq_len, VeloxHipModelConfig* ou
     c.num_kv_heads = get("NUM_KV_HEADS", c.num_heads);
     c.head_dim = get("HEAD_DIM", c.num_heads ? c.hidden_dim / c.num_heads : 0);
     c.max_seq_len = max_seq_len ? max_seq_len : get("S_MAX", 2048);  // src/codegen.rs:955 default
-    if (!c.vocab_size || !c.hidden_dim || !c.intermediate_dim || !c.num_layers || !c.num_heads || !c.head_dim)
+    if (!in_range || !c.vocab_size || !c.hidden_dim || !c.intermediate_dim || !c.num_layers || !c.num_heads || !c.head_dim)
         return VELOX_HIP_EINVAL;
     const auto th = v.consts.find("ROPE_THETA");
     if (th != v.consts.end()) c.rope_theta = (float)th->second;
     else c.rope_theta = vx_contains_ci(v.model, "llama") ? 500000.0f : vx_contains_ci(v.model, "qwen") ? 1000000.0f
                                                                                                      : 10000.0f;
-    if (v.eps > 0.0) c.rms_norm_eps = (float)v.eps;
-    else c.rms_norm_eps = (v.model.find("Qwen") != std::string::npos || v.model.find("K2") != std::string::npos ||
-                           v.model.find("Horizon") != std::string::npos) ? 1e-6f : 1e-5f;
+    // epsilon by the model's name, as the reference lowers every rmsnorm (src/ir.rs:549-553): an
+    // `eps =` argument in the source does not reach its emitted kernels either
+    c.rms_norm_eps = (v.model.find("Qwen") != std::string::npos || v.model.find("K2") != std::string::npos ||
+                      v.model.find("Horizon") != std::string::npos) ? 1e-6f : 1e-5f;
     c.qkv_bias = vx_has_weight(v, "b_q") && vx_has_weight(v, "b_k") && vx_has_weight(v, "b_v") ? 1u : 0u;
     c.tied_lm_head = vx_has_weight(v, "w_head", "w_lm_head") ? 0u : 1u;
     c.quant_mode = VELOX_QUANT_GGML_Q4_0;
     c.vram_budget_bytes = vx_budget(v);
+    if (!vx_fill_target(v, target)) return VELOX_HIP_EINVAL;
     *out = c;
-    vx_fill_target(v, target);
     return VELOX_HIP_OK;
 }
 
@@ -419,10 +427,13 @@ int velox_hip_vlx_mla_config(const char* source, uint32_t max_seq_len, uint32_t 
     if (!source || !out) return VELOX_HIP_EINVAL;
     VxVlx v;
     if (!vx_parse(source, v)) return VELOX_HIP_EINVAL;
+    bool in_range = true;
     auto get = [&](const char* k) -> uint32_t {
-        const auto it = v.consts.find(k);
-        return it == v.consts.end() ? 0u : (uint32_t)it->second;
+        uint32_t x = 0;
+        if (!vx_const_u32(v, k, 0, &x)) in_range = false;
+        return x;
     };
+    if (!in_range) return VELOX_HIP_EINVAL;
     if (!get("LATENT_KV_DIM") || !get("HIDDEN_DIM") || !get("NUM_HEADS") || !get("HEAD_DIM")) return VELOX_HIP_EINVAL;
     VeloxHipMlaConfig c;
     std::memset(&c, 0, sizeof(c));
@@ -438,12 +449,12 @@ int velox_hip_vlx_mla_config(const char* source, uint32_t max_seq_len, uint32_t 
     const uint32_t bm = max_batch ? max_batch : (get("B_MAX") ? get("B_MAX") : 1u);
     c.max_batch = bm > 32 ? 32 : bm;
     c.kv_norm = 1;  // DeepSeek-V3's kv_a_layernorm
-    c.rms_norm_eps = v.eps > 0.0 ? (float)v.eps : 1e-6f;
+    c.rms_norm_eps = 1e-6f;  // DeepSeek-V3's
     c.rope_theta = get("ROPE_THETA") ? (float)get("ROPE_THETA") : 10000.0f;
     c.softmax_scale = 0.0f;  // 1/sqrt(nope + rope)
     c.vram_budget_bytes = vx_budget(v);
+    if (!in_range || !vx_fill_target(v, target)) return VELOX_HIP_EINVAL;
     *out = c;
-    vx_fill_target(v, target);
     return VELOX_HIP_OK;
 }
 

@@ -29,6 +29,45 @@ def gguf_config(path: str, max_seq_len: int = 0) -> L.ModelConfig:
     return cfg
 
 
+class Safetensors:
+    """A memory-mapped safetensors checkpoint (velox_hip_st_*): the reference runner's --weights format."""
+
+    def __init__(self, path: str):
+        self.lib = L.load()
+        self.handle = C.c_void_p()
+        L.check(self.lib.velox_hip_st_open(path.encode(), C.byref(self.handle)), f"st_open {path}")
+
+    def config(self, max_seq_len: int = 0) -> L.ModelConfig:
+        cfg = L.ModelConfig()
+        L.check(self.lib.velox_hip_st_config(self.handle, max_seq_len, C.byref(cfg)), "st_config")
+        return cfg
+
+    def names(self) -> list[str]:
+        out = []
+        buf = C.create_string_buffer(256)
+        for i in range(int(self.lib.velox_hip_st_tensor_count(self.handle))):
+            L.check(self.lib.velox_hip_st_tensor_info(self.handle, i, buf, 256, None, None, None, None, None))
+            out.append(buf.value.decode())
+        return out
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.velox_hip_st_close(self.handle)
+            self.handle = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+def safetensors_config(path: str, max_seq_len: int = 0) -> L.ModelConfig:
+    """The model a safetensors checkpoint holds (velox_hip_st_config)."""
+    with Safetensors(path) as st:
+        return st.config(max_seq_len)
+
+
 def vlx_config(path: str, max_seq_len: int = 0) -> tuple[L.ModelConfig, L.VlxTarget]:
     """The model configuration and target a .vlx model source declares (velox_hip_vlx_load)."""
     lib = L.load()
@@ -39,11 +78,14 @@ def vlx_config(path: str, max_seq_len: int = 0) -> tuple[L.ModelConfig, L.VlxTar
 
 def make_config(model, max_seq_len: int = 0, num_layers: int = 0, attn_splits: int = 0,
                 max_batch: int = 0, prefill_chunk: int = 0, quant_mode: int | None = None) -> L.ModelConfig:
-    """A builtin config by name, a GGUF file (path ending in .gguf), a .vlx model source (path ending
-    in .vlx, read by velox_hip_vlx_load), or a dict of ModelConfig fields (custom shapes for tests).
+    """A builtin config by name, a GGUF file (path ending in .gguf), a safetensors checkpoint (path
+    ending in .safetensors), a .vlx model source (path ending in .vlx, read by velox_hip_vlx_load), or a
+    dict of ModelConfig fields (custom shapes for tests).
     `quant_mode` overrides the weight format (L.QUANT_F32 / L.QUANT_F16 rows, L.QUANT_GGML_Q4_0)."""
     if isinstance(model, str) and model.endswith(".gguf"):
         cfg = gguf_config(model, max_seq_len)
+    elif isinstance(model, str) and model.endswith(".safetensors"):
+        cfg = safetensors_config(model, max_seq_len)
     elif isinstance(model, str) and model.endswith(".vlx"):
         cfg = vlx_config(model, max_seq_len)[0]
     elif isinstance(model, str):
@@ -92,6 +134,8 @@ class HipDecodeEngine:
                 L.check(self.lib.velox_hip_gguf_load(C.byref(self.arena), g, None), "gguf_load")
             finally:
                 self.lib.velox_hip_gguf_close(g)
+        elif isinstance(model, str) and model.endswith(".safetensors"):
+            self.load_safetensors(model)
         elif synthesize:
             L.check(self.lib.velox_hip_synthesize_model(C.byref(self.arena), seed, sigma, norm_sigma, None),
                     "synthesize_model")
@@ -110,6 +154,11 @@ class HipDecodeEngine:
         blocks = np.ascontiguousarray(blocks, np.uint8)
         L.check(self.lib.velox_hip_load_q4_0(C.byref(self.arena), kind, layer, blocks.ctypes.data, blocks.nbytes,
                                              None), "load_q4_0")
+
+    def load_safetensors(self, path: str) -> None:
+        """Every tensor of a safetensors checkpoint, converted on the device to this arena's format."""
+        with Safetensors(path) as st:
+            L.check(self.lib.velox_hip_st_load(C.byref(self.arena), st.handle, None), f"st_load {path}")
 
     def load_f32(self, kind: int, layer: int, data: np.ndarray) -> None:
         data = np.ascontiguousarray(data, np.float32)
