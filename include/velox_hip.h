@@ -36,6 +36,7 @@ extern "C" {
 #define VELOX_QUANT_F32 0u
 #define VELOX_QUANT_F16 1u
 #define VELOX_QUANT_Q4_GROUP64 2u
+#define VELOX_QUANT_FP8_E4M3 3u  /* the MLA arena's fp8 weights (the reference's value) */
 #define VELOX_QUANT_GGML_Q4_0 5u
 
 /* Tensor kinds for the loaders (one per HF safetensors name the reference resolves,
@@ -215,8 +216,15 @@ void velox_hip_prefill(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint6
                        hipStream_t stream);
 int velox_hip_last_error(void);
 
+/* 0 when the arena's plan has `want`'s dimensions -- vocabulary, hidden, FFN, heads, KV heads, head
+ * size, QKV bias, head tying, eps, theta, and depth unless want->num_layers is 0 -- else EINVAL
+ * (the plan's name, context, batch rows and weight format are not compared). */
+int velox_hip_arena_check(const VeloxHipArena* a, const VeloxHipModelConfig* want);
+
 /* Per-model entry points with the reference's names (src/runners/tinystories_smollm.cu:1520,
- * 2383, 2388, 3251); each checks that ctx was planned for that model. */
+ * 2383, 2388, 3251) for the builtin configurations; each runs only on an arena whose plan has that
+ * model's dimensions (velox_hip_arena_check, at any depth), else records EINVAL. `velox_amd.build
+ * --model X.vlx` generates the same four for the model any source declares. */
 void velox_SmolLM_135M_decode_graph_step_hip(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
 void velox_SmolLM_135M_decode_hip(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t active_mask,
                                   hipStream_t stream);
@@ -427,6 +435,12 @@ typedef struct VeloxHipRunOptions {
                                 (--quantize q4_0, velox_cuda_runner.cu:356-372). A safetensors
                                 checkpoint is converted on the device to the format chosen (0:
                                 quantized to GGML Q4_0 there) */
+    const VeloxHipModelConfig* model_config; /* non-NULL: run this configuration (a generated runner's
+                                model) instead of model_file / model; a checkpoint must fit it */
+    void (*decode_step)(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
+                             /* non-NULL: the single-sequence step the run captures and replays (a
+                                generated runner's velox_<Model>_decode_graph_step_hip); NULL:
+                                velox_hip_decode_graph_step */
 } VeloxHipRunOptions;
 
 typedef struct VeloxHipRunReport {
@@ -449,6 +463,16 @@ typedef struct VeloxHipRunReport {
  * argmax after every position (prompt-forced positions included), drained from the 1024-entry ring
  * at least once per 1024 positions. */
 int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_tokens, VeloxHipRunReport* rep);
+
+/* The runner program (argv and stdout report of the reference's runner, velox_cuda_runner.cu:327-726,
+ * parsed by src/cli.rs:706-733): the generic velox_hip_runner passes NULL, NULL; a runner generated
+ * for one model (velox_amd.build --model X.vlx) passes its configuration and its named graph step.
+ * Returns the process exit code (0, or 1 with a message on stderr). */
+int velox_hip_runner_main(int argc, char** argv, const VeloxHipModelConfig* model,
+                          void (*decode_step)(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream));
+/* Records `status` as the step error velox_hip_last_error() returns, unless one is recorded already
+ * (generated entry points report an arena of another model through it). */
+void velox_hip_record_error(int status);
 
 /* ---- GGUF checkpoints (GGML's container, read by the reference's K2 runner,
  * src/runners/velox_cuda_runner_k2.cu:48-196; llama.cpp tensor names as at :1918-1963) ----
@@ -552,7 +576,10 @@ typedef struct VeloxHipMlaBuffers {
 /* "deepseek_v3_mla": hidden 7168, 128 heads, q LoRA 1536, kv LoRA 512, nope 128 + rope 64, v 128. */
 int velox_hip_mla_builtin_config(const char* which, uint32_t max_seq_len, uint32_t max_batch,
                                  VeloxHipMlaConfig* out);
-int velox_hip_mla_create(const VeloxHipMlaConfig* cfg, VeloxHipMla** out);  /* plan + one hipMalloc */
+/* plan: the static memory plan only (no device memory; ENOMEM past the budget, E002); create: plan
+ * plus one hipMalloc holding every region, initialized. destroy forgets its arenas too. */
+int velox_hip_mla_plan(const VeloxHipMlaConfig* cfg, VeloxHipMla** out);
+int velox_hip_mla_create(const VeloxHipMlaConfig* cfg, VeloxHipMla** out);
 void velox_hip_mla_destroy(VeloxHipMla* m);
 int velox_hip_mla_buffers(const VeloxHipMla* m, VeloxHipMlaBuffers* out);
 /* fp8 matrix of `kind` for `layer`: codes [rows][cols], scales [ceil(rows/128)][ceil(cols/128)]. */
@@ -580,6 +607,44 @@ void velox_hip_mla_layer_step(VeloxHipMla* m, uint32_t layer, uint32_t batch, ui
 void velox_hip_mla_decode_step(VeloxHipMla* m, uint32_t batch, uint64_t active_mask, hipStream_t stream);
 /* Algorithmic HBM bytes of one layer step (weights + scales + latent rows 0..pos + activations). */
 double velox_hip_mla_step_bytes(const VeloxHipMla* m, uint32_t batch, uint64_t pos);
+
+/* ---- the MLA model on the emitted-runner arena (src/codegen.rs:2980-3003: the MLA kernel reads its
+ * weights from weight_arena and its latent cache from kv_cache_pool) ----
+ * The regions of a plan as the eight VeloxHipArena fields: weight_arena = fp8 codes (tiled),
+ * weight_scales = fp32 block scales, norm_weight_arena = fp32 gains then the RoPE table,
+ * kv_cache_pool = the bf16 latent cache [layer][sequence][s_cap][kv_lora_rank + rope],
+ * activation_arena = the sequences' VeloxDecodeState, then activations; host_pinned_ring NULL (the
+ * attention stack emits no token), quant_mode VELOX_QUANT_FP8_E4M3, tied_lm_head 0.
+ * arena_bytes: the region sizes of a plan (for caller-owned buffers, as the reference runner
+ *   cudaMallocs its own, velox_cuda_runner.cu:417-431).
+ * arena: fills the fields over a created handle's buffers and records the arena.
+ * arena_bind: a planned handle (velox_hip_mla_plan) takes the caller's buffers from the fields
+ *   (each at least its arena_bytes size, quant_mode VELOX_QUANT_FP8_E4M3), initializes them as
+ *   create does and records the arena; EINVAL for a handle with buffers or a recorded weight_arena.
+ * arena_mla: the handle an arena was recorded with (NULL if none).
+ * arena_check: 0 when the arena's plan has `want`'s per-layer dimensions, norm, eps, theta and
+ *   softmax scale (depth, context and batch are the plan's own), else EINVAL.
+ * graph_step: velox_hip_mla_decode_step over all max_batch sequences, then every active sequence's
+ *   position advances by one (capturable; one graph replays every step). decode: sets sequence 0's
+ *   state to (step, token_in) first. Errors through velox_hip_last_error(). */
+int velox_hip_mla_arena_bytes(const VeloxHipMla* m, uint64_t* weight_bytes, uint64_t* scale_bytes,
+                              uint64_t* norm_bytes, uint64_t* kv_bytes, uint64_t* act_bytes);
+int velox_hip_mla_arena(VeloxHipMla* m, VeloxHipArena* out);
+int velox_hip_mla_arena_bind(VeloxHipMla* m, VeloxHipArena* a);
+VeloxHipMla* velox_hip_mla_arena_mla(const VeloxHipArena* a);
+int velox_hip_mla_arena_check(const VeloxHipArena* a, const VeloxHipMlaConfig* want);
+void velox_hip_mla_graph_step(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
+void velox_hip_mla_decode(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t active_mask,
+                          hipStream_t stream);
+/* DeepSeek-V3's MLA model (examples/deepseek_v3_mla.vlx) under the reference's emitted names, for an
+ * arena whose plan has DeepSeek-V3's dimensions (velox_hip_mla_arena_check against
+ * velox_hip_mla_builtin_config("deepseek_v3_mla")); prefill is the same single-token step. */
+void velox_DeepSeek_V3_MLA_decode_graph_step_hip(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
+void velox_DeepSeek_V3_MLA_decode_hip(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t active_mask,
+                                      hipStream_t stream);
+void velox_DeepSeek_V3_MLA_prefill_graph_step_hip(VeloxHipArena* ctx, uint64_t active_mask, hipStream_t stream);
+void velox_DeepSeek_V3_MLA_prefill_hip(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t active_mask,
+                                       hipStream_t stream);
 
 typedef struct VeloxHipMlaRunReport {
     double us_per_layer;     /* mean device time per layer (hipGraph replays of the step / layers) */

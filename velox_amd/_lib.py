@@ -69,6 +69,7 @@ class RunOptions(C.Structure):
         ("kernel_passes", C.c_uint32), ("verbose", C.c_uint32), ("prompt_tokens", C.POINTER(C.c_uint32)),
         ("context_len", C.c_uint32), ("batch", C.c_uint32), ("weights_path", C.c_char_p),
         ("prefill_chunk", C.c_uint32), ("model_file", C.c_char_p), ("unquantized", C.c_uint32),
+        ("model_config", C.POINTER(ModelConfig)), ("decode_step", C.c_void_p),
     ]
 
 
@@ -211,7 +212,29 @@ _SIGS = {
     "velox_hip_mla_decode_step": (None, [_P, _U32, _U64, _P]),
     "velox_hip_mla_step_bytes": (C.c_double, [_P, _U32, _U64]),
     "velox_hip_mla_run": (_I, [C.c_char_p, _U32, _U32, _U32, _U32, _U32, _U64, C.POINTER(MlaRunReport)]),
+    "velox_hip_mla_plan": (_I, [C.POINTER(MlaConfig), C.POINTER(_P)]),
+    "velox_hip_mla_arena_bytes": (_I, [_P] + [C.POINTER(_U64)] * 5),
+    "velox_hip_mla_arena": (_I, [_P, C.POINTER(Arena)]),
+    "velox_hip_mla_arena_bind": (_I, [_P, C.POINTER(Arena)]),
+    "velox_hip_mla_arena_mla": (_P, [C.POINTER(Arena)]),
+    "velox_hip_mla_arena_check": (_I, [C.POINTER(Arena), C.POINTER(MlaConfig)]),
+    "velox_hip_mla_graph_step": (None, [C.POINTER(Arena), _U64, _P]),
+    "velox_hip_mla_decode": (None, [C.POINTER(Arena), _U32, C.c_size_t, _U64, _P]),
+    "velox_hip_arena_check": (_I, [C.POINTER(Arena), C.POINTER(ModelConfig)]),
+    "velox_hip_record_error": (None, [_I]),
+    "velox_hip_decode": (None, [C.POINTER(Arena), _U32, C.c_size_t, _U64, _P]),
+    "velox_hip_decode_graph_step": (None, [C.POINTER(Arena), _U64, _P]),
 }
+
+
+def bind_entry_points(lib: C.CDLL, model: str) -> None:
+    """Argument types of a model's four named entry points (velox_<model>_{decode,prefill}
+    {_graph_step,}_hip) in `lib` (the HIP library, or a module velox_amd.build generated)."""
+    for phase in ("decode", "prefill"):
+        g = getattr(lib, f"velox_{model}_{phase}_graph_step_hip")
+        g.restype, g.argtypes = None, [C.POINTER(Arena), _U64, _P]
+        f = getattr(lib, f"velox_{model}_{phase}_hip")
+        f.restype, f.argtypes = None, [C.POINTER(Arena), _U32, C.c_size_t, _U64, _P]
 
 
 def load() -> C.CDLL:
@@ -226,6 +249,8 @@ def load() -> C.CDLL:
         fn = getattr(L, name)
         fn.restype = res
         fn.argtypes = args
+    for model in ("SmolLM_135M", "Llama3_8B", "Qwen2_5_7B", "Qwen2_72B", "DeepSeek_V3_MLA"):
+        bind_entry_points(L, model)
     _lib = L
     return L
 

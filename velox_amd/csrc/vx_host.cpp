@@ -244,8 +244,7 @@ hipError_t vx_build_m(const VeloxHipArena* a, const VxMatPlan& p, hipStream_t st
 }
 
 // KV cache of (layer, sequence): [layer][sequence][K | V][kv head][position][dim] bf16
-uint16_t* vx_kv(const VeloxHipArena* a, uint32_t layer, uint32_t seq) {
-    const VeloxHipModel* M = vx_model(a);
+uint16_t* vx_kv(const VeloxHipModel* M, const VeloxHipArena* a, uint32_t layer, uint32_t seq) {
     return (uint16_t*)(a->kv_cache_pool + M->kv_layer_bytes * ((uint64_t)layer * M->batch + seq));
 }
 
@@ -298,6 +297,10 @@ bool vx_shape_ok(const VeloxHipModelConfig& c) {
 }  // namespace
 
 extern "C" {
+
+void velox_hip_record_error(int status) {
+    if (!g_last_error) g_last_error = status;
+}
 
 int velox_hip_last_error(void) {
     const int e = g_last_error;
@@ -683,11 +686,12 @@ bool vx_vec_target(const VeloxHipModel* M, int kind, uint32_t layer, uint64_t* o
 }  // namespace
 
 int velox_hip_arena_matrix(const VeloxHipArena* a, int kind, uint32_t layer, VeloxHipQ4Matrix* out, uint32_t* row0) {
-    if (!a || !vx_model(a) || !out) return VELOX_HIP_EINVAL;
+    const VeloxHipModel* M = vx_model(a);
+    if (!M || !out) return VELOX_HIP_EINVAL;
     const VxMatPlan* mp;
     uint32_t r0, pair, rows, cols;
-    if (kind == VELOX_T_HEAD && vx_model(a)->cfg.tied_lm_head) kind = VELOX_T_EMBED;
-    if (!vx_target(vx_model(a), kind, layer, &mp, &r0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
+    if (kind == VELOX_T_HEAD && M->cfg.tied_lm_head) kind = VELOX_T_EMBED;
+    if (!vx_target(M, kind, layer, &mp, &r0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
     if (!vx_fmt_tiled(mp->fmt)) return VELOX_HIP_EINVAL;  // a tiled view; fp32 / fp16 rows have none
     out->codes = (void*)(a->weight_arena + mp->code_off);
     out->scales = (void*)(a->weight_scales + mp->scale_off);
@@ -703,9 +707,10 @@ int velox_hip_arena_matrix(const VeloxHipArena* a, int kind, uint32_t layer, Vel
 }
 
 int velox_hip_arena_vector(const VeloxHipArena* a, int kind, uint32_t layer, const float** out, uint64_t* count) {
-    if (!a || !vx_model(a) || !out) return VELOX_HIP_EINVAL;
+    const VeloxHipModel* M = vx_model(a);
+    if (!M || !out) return VELOX_HIP_EINVAL;
     uint64_t off, n;
-    if (!vx_vec_target(vx_model(a), kind, layer, &off, &n)) return VELOX_HIP_EINVAL;
+    if (!vx_vec_target(M, kind, layer, &off, &n)) return VELOX_HIP_EINVAL;
     *out = (const float*)(a->norm_weight_arena + off);
     if (count) *count = n;
     return VELOX_HIP_OK;
@@ -713,10 +718,11 @@ int velox_hip_arena_vector(const VeloxHipArena* a, int kind, uint32_t layer, con
 
 int velox_hip_load_q4_0(VeloxHipArena* a, int kind, uint32_t layer, const void* blocks, uint64_t nbytes,
                         hipStream_t stream) {
-    if (!a || !vx_model(a) || !blocks) return VELOX_HIP_EINVAL;
+    const VeloxHipModel* M = vx_model(a);
+    if (!M || !blocks) return VELOX_HIP_EINVAL;
     const VxMatPlan* mp;
     uint32_t row0, pair, rows, cols;
-    if (!vx_target(vx_model(a), kind, layer, &mp, &row0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
+    if (!vx_target(M, kind, layer, &mp, &row0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
     if (mp->fmt != VX_FMT_Q4) return VELOX_HIP_EINVAL;  // GGML blocks load into GGML Q4_0 arenas only
     if (nbytes != (uint64_t)rows * (cols / 32) * 18) return VELOX_HIP_ESHAPE;
     void* staging = nullptr;
@@ -724,7 +730,7 @@ int velox_hip_load_q4_0(VeloxHipArena* a, int kind, uint32_t layer, const void* 
     if (e == hipSuccess) e = hipMemcpyAsync(staging, blocks, nbytes, hipMemcpyHostToDevice, stream);
     if (e == hipSuccess) e = vx_launch_repack(staging, rows, row0, pair, vx_view(a, *mp), stream);
     if (e == hipSuccess) e = vx_build_m(a, *mp, stream);
-    if (e == hipSuccess && kind == VELOX_T_EMBED && vx_model(a)->cfg.tied_lm_head) e = vx_build_m(a, vx_model(a)->head, stream);
+    if (e == hipSuccess && kind == VELOX_T_EMBED && M->cfg.tied_lm_head) e = vx_build_m(a, M->head, stream);
     if (e == hipSuccess) e = hipStreamSynchronize(stream);
     hipFree(staging);
     return (int)e;
@@ -732,10 +738,11 @@ int velox_hip_load_q4_0(VeloxHipArena* a, int kind, uint32_t layer, const void* 
 
 int velox_hip_load_rows(VeloxHipArena* a, int kind, uint32_t layer, const void* rows_data, uint64_t nbytes,
                         hipStream_t stream) {
-    if (!a || !vx_model(a) || !rows_data) return VELOX_HIP_EINVAL;
+    const VeloxHipModel* M = vx_model(a);
+    if (!M || !rows_data) return VELOX_HIP_EINVAL;
     const VxMatPlan* mp;
     uint32_t row0, pair, rows, cols;
-    if (!vx_target(vx_model(a), kind, layer, &mp, &row0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
+    if (!vx_target(M, kind, layer, &mp, &row0, &pair, &rows, &cols)) return VELOX_HIP_EINVAL;
     if (mp->fmt == VX_FMT_Q4) return VELOX_HIP_EINVAL;  // Q4_0 arenas load blocks (velox_hip_load_q4_0)
     const uint64_t elt = mp->fmt == VX_FMT_F16 ? 2 : 4;
     if (nbytes != (uint64_t)rows * cols * elt) return VELOX_HIP_ESHAPE;
@@ -841,9 +848,10 @@ int velox_hip_load_tensor(VeloxHipArena* a, int kind, uint32_t layer, const void
 
 int velox_hip_load_f32(VeloxHipArena* a, int kind, uint32_t layer, const float* data, uint64_t count,
                        hipStream_t stream) {
-    if (!a || !vx_model(a) || !data) return VELOX_HIP_EINVAL;
+    const VeloxHipModel* M = vx_model(a);
+    if (!M || !data) return VELOX_HIP_EINVAL;
     uint64_t off, n;
-    if (!vx_vec_target(vx_model(a), kind, layer, &off, &n)) return VELOX_HIP_EINVAL;
+    if (!vx_vec_target(M, kind, layer, &off, &n)) return VELOX_HIP_EINVAL;
     if (count != n) return VELOX_HIP_ESHAPE;
     hipError_t e = hipMemcpyAsync((void*)(a->norm_weight_arena + off), data, n * 4, hipMemcpyHostToDevice, stream);
     if (e == hipSuccess) e = hipStreamSynchronize(stream);
@@ -851,8 +859,8 @@ int velox_hip_load_f32(VeloxHipArena* a, int kind, uint32_t layer, const float* 
 }
 
 int velox_hip_synthesize_model(VeloxHipArena* a, uint64_t seed, float sigma, float norm_sigma, hipStream_t st) {
-    if (!a || !vx_model(a)) return VELOX_HIP_EINVAL;
     const VeloxHipModel* M = vx_model(a);
+    if (!M) return VELOX_HIP_EINVAL;
     const VeloxHipModelConfig& c = M->cfg;
     const float coef = vx_normal_coef(sigma), ncoef = norm_sigma == 0.0f ? 0.0f : vx_normal_coef(norm_sigma);
     hipError_t e = hipSuccess;
@@ -906,11 +914,12 @@ int velox_hip_synthesize_model(VeloxHipArena* a, uint64_t seed, float sigma, flo
 }
 
 int velox_hip_fill_kv(VeloxHipArena* a, uint32_t layer, uint32_t n_pos, uint64_t seed, float sigma, hipStream_t st) {
-    if (!a || !vx_model(a)) return VELOX_HIP_EINVAL;
-    const VeloxHipModelConfig& c = vx_model(a)->cfg;
+    const VeloxHipModel* M = vx_model(a);
+    if (!M) return VELOX_HIP_EINVAL;
+    const VeloxHipModelConfig& c = M->cfg;
     if (layer >= c.num_layers || n_pos > c.max_seq_len) return VELOX_HIP_EINVAL;
-    uint16_t* base = vx_kv(a, layer, 0);
-    hipError_t e = vx_launch_fill_kv(base, c.num_kv_heads, vx_model(a)->s_cap, c.head_dim, n_pos,
+    uint16_t* base = vx_kv(M, a, layer, 0);
+    hipError_t e = vx_launch_fill_kv(base, c.num_kv_heads, M->s_cap, c.head_dim, n_pos,
                                      vx_stream(seed, vx_tag(layer, VX_TAG_KV_K)),
                                      vx_stream(seed, vx_tag(layer, VX_TAG_KV_V)), vx_normal_coef(sigma), st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
@@ -921,12 +930,13 @@ int velox_hip_fill_kv(VeloxHipArena* a, uint32_t layer, uint32_t n_pos, uint64_t
 // Decode state / prompt
 // ---------------------------------------------------------------------------------------------
 int velox_hip_set_prompt(VeloxHipArena* a, const uint32_t* tokens, uint32_t n, hipStream_t st) {
-    if (!a || !vx_model(a) || (n && !tokens)) return VELOX_HIP_EINVAL;
-    if (n > vx_model(a)->cfg.max_seq_len) return VELOX_HIP_EINVAL;
+    const VeloxHipModel* M = vx_model(a);
+    if (!M || (n && !tokens)) return VELOX_HIP_EINVAL;
+    if (n > M->cfg.max_seq_len) return VELOX_HIP_EINVAL;
     hipError_t e = hipSuccess;
-    if (n) e = hipMemcpyAsync(a->activation_arena + vx_model(a)->a_prompt, tokens, (size_t)n * 4, hipMemcpyHostToDevice, st);
+    if (n) e = hipMemcpyAsync(a->activation_arena + M->a_prompt, tokens, (size_t)n * 4, hipMemcpyHostToDevice, st);
     if (e == hipSuccess)
-        e = hipMemcpyAsync(a->activation_arena + vx_model(a)->a_plen, &n, 4, hipMemcpyHostToDevice, st);
+        e = hipMemcpyAsync(a->activation_arena + M->a_plen, &n, 4, hipMemcpyHostToDevice, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     if (e == hipSuccess) {
         std::lock_guard<std::mutex> lock(g_arena_mu);
@@ -936,13 +946,15 @@ int velox_hip_set_prompt(VeloxHipArena* a, const uint32_t* tokens, uint32_t n, h
 }
 
 int velox_hip_set_state(VeloxHipArena* a, uint64_t step, uint32_t token, hipStream_t st) {
-    if (!a || !vx_model(a)) return VELOX_HIP_EINVAL;
-    return (int)vx_launch_set_state((VeloxDecodeState*)(a->activation_arena + vx_model(a)->a_state), step, token, st);
+    const VeloxHipModel* M = vx_model(a);
+    if (!M) return VELOX_HIP_EINVAL;
+    return (int)vx_launch_set_state((VeloxDecodeState*)(a->activation_arena + M->a_state), step, token, st);
 }
 
 int velox_hip_get_state(const VeloxHipArena* a, VeloxDecodeState* out, hipStream_t st) {
-    if (!a || !vx_model(a) || !out) return VELOX_HIP_EINVAL;
-    hipError_t e = hipMemcpyAsync(out, a->activation_arena + vx_model(a)->a_state, sizeof(*out), hipMemcpyDeviceToHost, st);
+    const VeloxHipModel* M = vx_model(a);
+    if (!M || !out) return VELOX_HIP_EINVAL;
+    hipError_t e = hipMemcpyAsync(out, a->activation_arena + M->a_state, sizeof(*out), hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     return (int)e;
 }
@@ -951,8 +963,8 @@ int velox_hip_get_state(const VeloxHipArena* a, VeloxDecodeState* out, hipStream
 // Batched decode of independent sequences (arena planned with max_batch > 1)
 // ---------------------------------------------------------------------------------------------
 int velox_hip_batch_set_prompt(VeloxHipArena* a, uint32_t seq, const uint32_t* tokens, uint32_t n, hipStream_t st) {
-    if (!a || !vx_model(a) || vx_model(a)->batch < 2 || seq >= vx_model(a)->batch || (n && !tokens)) return VELOX_HIP_EINVAL;
     const VeloxHipModel* M = vx_model(a);
+    if (!M || M->batch < 2 || seq >= M->batch || (n && !tokens)) return VELOX_HIP_EINVAL;
     if (n > M->cfg.max_seq_len) return VELOX_HIP_EINVAL;
     hipError_t e = hipSuccess;
     if (n)
@@ -965,14 +977,16 @@ int velox_hip_batch_set_prompt(VeloxHipArena* a, uint32_t seq, const uint32_t* t
 }
 
 int velox_hip_batch_set_state(VeloxHipArena* a, uint32_t seq, uint64_t step, uint32_t token, hipStream_t st) {
-    if (!a || !vx_model(a) || vx_model(a)->batch < 2 || seq >= vx_model(a)->batch) return VELOX_HIP_EINVAL;
-    VeloxDecodeState* s = (VeloxDecodeState*)(a->activation_arena + vx_model(a)->a_bstate) + seq;
+    const VeloxHipModel* M = vx_model(a);
+    if (!M || M->batch < 2 || seq >= M->batch) return VELOX_HIP_EINVAL;
+    VeloxDecodeState* s = (VeloxDecodeState*)(a->activation_arena + M->a_bstate) + seq;
     return (int)vx_launch_set_state(s, step, token, st);
 }
 
 int velox_hip_batch_get_state(const VeloxHipArena* a, uint32_t seq, VeloxDecodeState* out, hipStream_t st) {
-    if (!a || !vx_model(a) || vx_model(a)->batch < 2 || seq >= vx_model(a)->batch || !out) return VELOX_HIP_EINVAL;
-    hipError_t e = hipMemcpyAsync(out, a->activation_arena + vx_model(a)->a_bstate + (size_t)seq * sizeof(*out),
+    const VeloxHipModel* M = vx_model(a);
+    if (!M || M->batch < 2 || seq >= M->batch || !out) return VELOX_HIP_EINVAL;
+    hipError_t e = hipMemcpyAsync(out, a->activation_arena + M->a_bstate + (size_t)seq * sizeof(*out),
                                   sizeof(*out), hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     return (int)e;
@@ -980,12 +994,13 @@ int velox_hip_batch_get_state(const VeloxHipArena* a, uint32_t seq, VeloxDecodeS
 
 int velox_hip_fill_kv_seq(VeloxHipArena* a, uint32_t layer, uint32_t seq, uint32_t n_pos, uint64_t seed, float sigma,
                           hipStream_t st) {
-    if (!a || !vx_model(a) || seq >= vx_model(a)->batch) return VELOX_HIP_EINVAL;
-    const VeloxHipModelConfig& c = vx_model(a)->cfg;
+    const VeloxHipModel* M = vx_model(a);
+    if (!M || seq >= M->batch) return VELOX_HIP_EINVAL;
+    const VeloxHipModelConfig& c = M->cfg;
     if (layer >= c.num_layers || n_pos > c.max_seq_len) return VELOX_HIP_EINVAL;
     // sequence 0 is velox_hip_fill_kv's context; others draw from streams of a sequence-tagged seed
     const uint64_t sseed = seed + (uint64_t)seq * 0x9E3779B97F4A7C15ULL;
-    hipError_t e = vx_launch_fill_kv(vx_kv(a, layer, seq), c.num_kv_heads, vx_model(a)->s_cap, c.head_dim, n_pos,
+    hipError_t e = vx_launch_fill_kv(vx_kv(M, a, layer, seq), c.num_kv_heads, M->s_cap, c.head_dim, n_pos,
                                      vx_stream(sseed, vx_tag(layer, VX_TAG_KV_K)),
                                      vx_stream(sseed, vx_tag(layer, VX_TAG_KV_V)), vx_normal_coef(sigma), st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
@@ -1020,9 +1035,8 @@ namespace {
 // which then attends over [0, position] of every row. Launches: embed, L x [norm, QKV, (prefill:
 // K/V rows,) attention, merge, o_proj + residual, norm, gate/up + SwiGLU, down + residual], norm,
 // LM head.
-void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n, uint64_t mask, bool prefill,
-                     uint32_t max_len, hipStream_t st) {
-    const VeloxHipModel* M = vx_model(A);
+void vx_rows_forward(const VeloxHipModel* M, VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n, uint64_t mask,
+                     bool prefill, uint32_t max_len, hipStream_t st) {
     const VeloxHipModelConfig& c = M->cfg;
     uint8_t* act = A->activation_arena;
     const uint32_t H = c.hidden_dim, D = c.head_dim, qd = c.num_heads * D, kvd = c.num_kv_heads * D;
@@ -1097,7 +1111,7 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
         at.qkv_part = part_r;
         at.qkv_pstride = g.pstride;
         at.qkv_bias = g.bias;
-        at.kv = vx_kv(A, l, 0);
+        at.kv = vx_kv(M, A, l, 0);
         if (prefill)
             vx_record(vx_launch_kv_append_rows(at.qkv_nparts ? part_r : qkv, qd + 2 * kvd, at.qkv_nparts, g.pstride,
                                                g.bias, c.num_heads, c.num_kv_heads, D, rows, n, at.rope,
@@ -1162,14 +1176,14 @@ void vx_rows_forward(VeloxHipArena* A, const VeloxDecodeState* rows, uint32_t n,
 // One decode step of sequences 0 .. batch-1, each at its own state (step, token): the weights are
 // read once per step for all of them; then the argmax of every sequence.
 void velox_hip_decode_batch_graph_step(VeloxHipArena* A, uint32_t batch, uint64_t mask, hipStream_t st) {
-    if (!A || !vx_model(A) || vx_model(A)->batch < 2 || batch == 0 || batch > vx_model(A)->batch) {
+    const VeloxHipModel* M = vx_model(A);
+    if (!M || M->batch < 2 || batch == 0 || batch > M->batch) {
         if (!g_last_error) g_last_error = VELOX_HIP_EINVAL;
         return;
     }
-    const VeloxHipModel* M = vx_model(A);
     uint8_t* act = A->activation_arena;
     VeloxDecodeState* states = (VeloxDecodeState*)(act + M->a_bstate);
-    vx_rows_forward(A, states, batch, mask, false, 0u, st);
+    vx_rows_forward(M, A, states, batch, mask, false, 0u, st);
     vx_record(vx_launch_bfinalize((const float*)(act + M->a_bcand_v), (const uint32_t*)(act + M->a_bcand_i),
                                   M->head_bwgs, states, A->host_pinned_ring, (const uint32_t*)(act + M->a_bprompt),
                                   (const uint32_t*)(act + M->a_bplen), M->cfg.max_seq_len, batch, mask, st));
@@ -1197,7 +1211,7 @@ int velox_hip_prefill_batch(VeloxHipArena* A, uint64_t pos0, uint32_t n_tokens, 
     for (uint32_t done = 0; done < n_tokens;) {
         const uint32_t n = n_tokens - done < chunk ? n_tokens - done : chunk;
         vx_record(vx_launch_prefill_rows(rows, n, pos0 + done, prompt, mask, st));
-        vx_rows_forward(A, rows, n, mask, true, (uint32_t)(pos0 + done + n), st);
+        vx_rows_forward(M, A, rows, n, mask, true, (uint32_t)(pos0 + done + n), st);
         vx_record(vx_launch_prefill_finalize((const float*)(act + M->a_bcand_v), (const uint32_t*)(act + M->a_bcand_i),
                                              M->head_bwgs, rows, n, A->host_pinned_ring,
                                              (VeloxDecodeState*)(act + M->a_state), prompt,
@@ -1214,8 +1228,8 @@ int velox_hip_prefill_batch(VeloxHipArena* A, uint64_t pos0, uint32_t n_tokens, 
 // down+res] -> norm + LM head + argmax (+ ring + state advance). 2 + 5L launches.
 // ---------------------------------------------------------------------------------------------
 void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st) {
-    if (!A || !vx_model(A)) { if (!g_last_error) g_last_error = VELOX_HIP_EINVAL; return; }
     const VeloxHipModel* M = vx_model(A);
+    if (!M) { if (!g_last_error) g_last_error = VELOX_HIP_EINVAL; return; }
     const VeloxHipModelConfig& c = M->cfg;
     uint8_t* act = A->activation_arena;
     const float* nrm = (const float*)A->norm_weight_arena;
@@ -1256,7 +1270,7 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
         g.y = qkv;
         vx_record(vx_launch_gemv(vx_view(A, L.qkv), g, VX_EPI_STORE, M->max_wgs, st));
 
-        at.kv = vx_kv(A, l, 0);
+        at.kv = vx_kv(M, A, l, 0);
         vx_record(vx_launch_attention(at, c.head_dim, st));
 
         std::memset(&g, 0, sizeof(g));
@@ -1303,8 +1317,9 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
 }
 
 void velox_hip_decode(VeloxHipArena* A, uint32_t token_in, size_t step, uint64_t mask, hipStream_t st) {
-    if (!A || !vx_model(A)) { if (!g_last_error) g_last_error = VELOX_HIP_EINVAL; return; }
-    vx_record(vx_launch_set_state((VeloxDecodeState*)(A->activation_arena + vx_model(A)->a_state), step, token_in, st));
+    const VeloxHipModel* M = vx_model(A);
+    if (!M) { if (!g_last_error) g_last_error = VELOX_HIP_EINVAL; return; }
+    vx_record(vx_launch_set_state((VeloxDecodeState*)(A->activation_arena + M->a_state), step, token_in, st));
     velox_hip_decode_graph_step(A, mask, st);
 }
 
@@ -1317,10 +1332,28 @@ void velox_hip_prefill(VeloxHipArena* A, uint32_t token_in, size_t step, uint64_
     velox_hip_decode(A, token_in, step, mask, st);
 }
 
+int velox_hip_arena_check(const VeloxHipArena* a, const VeloxHipModelConfig* want) {
+    const VeloxHipModel* M = vx_model(a);
+    if (!M || !want) return VELOX_HIP_EINVAL;
+    const VeloxHipModelConfig& c = M->cfg;
+    const bool same = c.vocab_size == want->vocab_size && c.hidden_dim == want->hidden_dim &&
+                      c.intermediate_dim == want->intermediate_dim && c.num_heads == want->num_heads &&
+                      c.num_kv_heads == want->num_kv_heads && c.head_dim == want->head_dim &&
+                      c.qkv_bias == want->qkv_bias && c.tied_lm_head == want->tied_lm_head &&
+                      c.rms_norm_eps == want->rms_norm_eps && c.rope_theta == want->rope_theta &&
+                      (want->num_layers == 0 || c.num_layers == want->num_layers);
+    return same ? VELOX_HIP_OK : VELOX_HIP_EINVAL;
+}
+
+// The builtin models' entry points take an arena whose plan has the model's dimensions (any depth:
+// the parity tests run them on fewer layers), whatever the plan is named.
 #define VX_MODEL_ENTRY(NAME, KEY)                                                                   \
     static bool vx_is_##NAME(const VeloxHipArena* a) {                                              \
-        const VeloxHipModel* m_ = vx_model(a);                                                      \
-        if (m_ && (!std::strcmp(m_->cfg.name, KEY) || !std::strcmp(m_->cfg.name, #NAME))) return true; \
+        VeloxHipModelConfig want;                                                                   \
+        if (velox_hip_builtin_config(KEY, 0, &want) == VELOX_HIP_OK) {                              \
+            want.num_layers = 0;                                                                    \
+            if (velox_hip_arena_check(a, &want) == VELOX_HIP_OK) return true;                      \
+        }                                                                                           \
         if (!g_last_error) g_last_error = VELOX_HIP_EINVAL;                                         \
         return false;                                                                               \
     }                                                                                               \
@@ -1625,7 +1658,8 @@ static bool vx_is_gguf(const char* path) {
 }
 
 int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_tokens, VeloxHipRunReport* rep) {
-    if (!opt || !rep || (!opt->model && !opt->weights_path && !opt->model_file) || opt->prompt_len == 0)
+    if (!opt || !rep || (!opt->model && !opt->weights_path && !opt->model_file && !opt->model_config) ||
+        opt->prompt_len == 0)
         return VELOX_HIP_EINVAL;
     if (opt->context_len && opt->prompt_len != 1) return VELOX_HIP_EINVAL;  // context + one seed token
     std::memset(rep, 0, sizeof(*rep));
@@ -1647,7 +1681,11 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
             rc = velox_hip_st_open(opt->weights_path, &stf);
             if (rc) return rc;
         }
-        if (opt->model_file) rc = velox_hip_vlx_load(opt->model_file, msl, &cfg, nullptr);
+        if (opt->model_config) {
+            cfg = *opt->model_config;
+            cfg.max_seq_len = msl;
+            rc = VELOX_HIP_OK;
+        } else if (opt->model_file) rc = velox_hip_vlx_load(opt->model_file, msl, &cfg, nullptr);
         else if (opt->model) rc = velox_hip_builtin_config(opt->model, msl, &cfg);
         else rc = velox_hip_st_config(stf, msl, &cfg);
         if (rc) { velox_hip_st_close(stf); return rc; }
@@ -1718,6 +1756,7 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
     velox_hip_last_error();
     auto launch_step = [&]() {
         if (B > 1) velox_hip_decode_batch_graph_step(&A, B, 1ULL, st);
+        else if (opt->decode_step) opt->decode_step(&A, 1ULL, st);
         else velox_hip_decode_graph_step(&A, 1ULL, st);
     };
     if (!rc && opt->use_graph) {

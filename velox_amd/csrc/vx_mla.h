@@ -69,3 +69,4 @@ hipError_t vx_launch_mla_merge(const uint16_t* part_o, const float* part_ml, uin
 hipError_t vx_launch_mla_resid(float* h, const float* parts, uint32_t nparts, uint64_t pstride, uint32_t n,
                                uint32_t batch, uint64_t mask, hipStream_t st);
 hipError_t vx_launch_mla_fill_cache(uint16_t* dst, uint64_t n, uint64_t stream, float coef, hipStream_t st);
+hipError_t vx_launch_mla_advance(VeloxDecodeState* states, uint32_t batch, uint64_t mask, hipStream_t st);

@@ -1018,3 +1018,17 @@ hipError_t vx_launch_mla_fill_cache(uint16_t* dst, uint64_t n, uint64_t stream, 
                        stream, coef);
     return hipGetLastError();
 }
+
+// End of an MLA decode step: every active sequence's position moves to the next one (the reference's
+// graph step advances its state in its final kernel, src/codegen.rs:1590-1677).
+__global__ __launch_bounds__(64) void vx_mla_advance_kernel(VeloxDecodeState* states, uint32_t batch, uint64_t mask) {
+    if (!(mask & 1ULL)) return;
+    const uint32_t b = threadIdx.x;
+    if (b < batch) states[b].step += 1u;
+}
+
+hipError_t vx_launch_mla_advance(VeloxDecodeState* states, uint32_t batch, uint64_t mask, hipStream_t st) {
+    if (batch == 0 || batch > 64) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(vx_mla_advance_kernel, dim3(1), dim3(64), 0, st, states, batch, mask);
+    return hipGetLastError();
+}

@@ -7,6 +7,8 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
+#include <utility>
 #include <vector>
 
 #include "vx_common.h"
@@ -61,19 +63,24 @@ struct VeloxHipMla {
     std::vector<VmLayer> layers;
     uint64_t code_bytes = 0, scale_bytes = 0, norm_bytes = 0, rope_bytes = 0, cache_bytes = 0, act_bytes = 0;
     uint64_t cache_layer_bytes = 0;
-    // arena regions (bytes from base)
-    uint64_t o_codes = 0, o_scales = 0, o_norms = 0, o_rope = 0, o_cache = 0, o_act = 0;
-    // activation offsets (bytes from base + o_act)
+    uint64_t o_rope = 0;  // the RoPE table's offset in the norm region (after the gains)
+    // activation offsets (bytes from the activation region)
     uint64_t a_state = 0, a_h = 0, a_x16 = 0, a_parts_a = 0, a_q32 = 0, a_qabs = 0, a_po = 0, a_pml = 0, a_ctx = 0,
              a_oh = 0, a_parts_o = 0;
+    // device regions, the fields of a VeloxHipArena: fp8 codes (weight_arena), block scales
+    // (weight_scales), gains + RoPE table (norm_weight_arena), latent cache (kv_cache_pool),
+    // states + activations (activation_arena). `base` is the one allocation of velox_hip_mla_create;
+    // a planned handle bound to caller-owned buffers has none.
+    uint8_t *w_codes = nullptr, *w_scales = nullptr, *w_norms = nullptr, *kv = nullptr, *act = nullptr;
     uint8_t* base = nullptr;
 };
 
 namespace {
 
-template <typename T>
-T* vm_at(const VeloxHipMla* m, uint64_t off) { return (T*)(m->base + off); }
-float* vm_act(const VeloxHipMla* m, uint64_t off) { return (float*)(m->base + m->o_act + off); }
+float* vm_act(const VeloxHipMla* m, uint64_t off) { return (float*)(m->act + off); }
+const float2* vm_rope(const VeloxHipMla* m) { return (const float2*)(m->w_norms + m->o_rope); }
+VeloxDecodeState* vm_states(const VeloxHipMla* m) { return (VeloxDecodeState*)(m->act + m->a_state); }
+uint16_t* vm_cache(const VeloxHipMla* m, uint32_t layer) { return (uint16_t*)(m->kv + m->cache_layer_bytes * layer); }
 
 bool vm_valid(const VeloxHipMlaConfig& c) {
     if (c.hidden_dim == 0 || c.num_heads == 0 || c.num_layers == 0 || c.max_seq_len == 0) return false;
@@ -89,8 +96,8 @@ bool vm_valid(const VeloxHipMlaConfig& c) {
 hipError_t vm_pack_source(VeloxHipMla* m, uint32_t layer, int kind, const uint8_t* d_src_codes,
                           const float* d_src_scales, uint64_t stream, float coef, hipStream_t st) {
     VmLayer& L = m->layers[layer];
-    uint8_t* codes = m->base + m->o_codes;
-    float* scales = (float*)(m->base + m->o_scales);
+    uint8_t* codes = m->w_codes;
+    float* scales = (float*)m->w_scales;
     auto dest = [&](const VmF8Plan& p, uint32_t map, uint32_t rows, uint32_t row_tile0, uint32_t row_off,
                     uint32_t src_rows, uint32_t src_cols) {
         VxF8Dest d;
@@ -187,7 +194,7 @@ int velox_hip_mla_builtin_config(const char* which, uint32_t max_seq_len, uint32
     return VELOX_HIP_OK;
 }
 
-int velox_hip_mla_create(const VeloxHipMlaConfig* cfg, VeloxHipMla** out) {
+int velox_hip_mla_plan(const VeloxHipMlaConfig* cfg, VeloxHipMla** out) {
     if (!cfg || !out) return VELOX_HIP_EINVAL;
     *out = nullptr;
     if (!vm_valid(*cfg)) return VELOX_HIP_ESHAPE;
@@ -274,32 +281,75 @@ int velox_hip_mla_create(const VeloxHipMlaConfig* cfg, VeloxHipMla** out) {
     m->a_parts_o = take((uint64_t)m->ks_o * B * m->H * 4);
     m->act_bytes = ac;
 
-    m->o_codes = 0;
-    m->o_scales = vm_align(m->code_bytes);
-    m->o_norms = m->o_scales + vm_align(m->scale_bytes);
-    m->o_rope = m->o_norms + vm_align(m->norm_bytes);
-    m->o_cache = m->o_rope + m->rope_bytes;
-    m->o_act = m->o_cache + m->cache_bytes;
-    const uint64_t total = m->o_act + m->act_bytes;
+    m->o_rope = vm_align(m->norm_bytes);
+    const uint64_t total = vm_align(m->code_bytes) + vm_align(m->scale_bytes) + m->o_rope + m->rope_bytes +
+                           m->cache_bytes + m->act_bytes;
     const uint64_t budget = c.vram_budget_bytes ? c.vram_budget_bytes : 288ULL * 1000 * 1000 * 1000;
     if (total > budget) {  // reference diagnostic E002 (src/memory_planner.rs:398-420)
         delete m;
         return VELOX_HIP_ENOMEM;
     }
-    hipError_t e = hipMalloc((void**)&m->base, total);
-    if (e == hipSuccess) e = hipMemset(m->base, 0, total);
+    *out = m;
+    return VELOX_HIP_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Zeroes the regions and writes the RoPE table of the rope part (src/runtime.rs:754-760: fp32 powf,
+// product, sin/cos) into the norm region after the gains.
+hipError_t vm_init_regions(VeloxHipMla* m) {
+    const VeloxHipMlaConfig& c = m->cfg;
+    hipError_t e = hipMemset(m->w_codes, 0, m->code_bytes);
+    if (e == hipSuccess) e = hipMemset(m->w_scales, 0, m->scale_bytes);
+    if (e == hipSuccess) e = hipMemset(m->w_norms, 0, m->o_rope + m->rope_bytes);
+    if (e == hipSuccess) e = hipMemset(m->kv, 0, m->cache_bytes);
+    if (e == hipSuccess) e = hipMemset(m->act, 0, m->act_bytes);
+    if (e != hipSuccess) return e;
+    const uint32_t half = m->dr / 2;
+    std::vector<float> rope((size_t)c.max_seq_len * half * 2);
+    for (uint32_t p = 0; p < c.max_seq_len; ++p)
+        for (uint32_t j = 0; j < half; ++j) {
+            const float freq = 1.0f / powf(c.rope_theta, (float)(2 * j) / (float)m->dr);
+            const float angle = (float)p * freq;
+            rope[((size_t)p * half + j) * 2] = cosf(angle);
+            rope[((size_t)p * half + j) * 2 + 1] = sinf(angle);
+        }
+    return hipMemcpy(m->w_norms + m->o_rope, rope.data(), rope.size() * 4, hipMemcpyHostToDevice);
+}
+
+bool vm_has_buffers(const VeloxHipMla* m) { return m && m->w_codes && m->w_scales && m->w_norms && m->kv && m->act; }
+
+// Arenas over MLA handles (velox_hip_mla_arena / _arena_bind), found by weight_arena.
+std::mutex g_mla_mu;
+std::vector<std::pair<const uint8_t*, VeloxHipMla*>> g_mla_arenas;
+
+void vm_forget(const VeloxHipMla* m) {
+    std::lock_guard<std::mutex> lk(g_mla_mu);
+    for (size_t i = 0; i < g_mla_arenas.size();)
+        if (g_mla_arenas[i].second == m) g_mla_arenas.erase(g_mla_arenas.begin() + (long)i);
+        else ++i;
+}
+
+}  // namespace
+
+extern "C" {
+
+int velox_hip_mla_create(const VeloxHipMlaConfig* cfg, VeloxHipMla** out) {
+    VeloxHipMla* m = nullptr;
+    int rc = velox_hip_mla_plan(cfg, &m);
+    if (rc) return rc;
+    const uint64_t o_scales = vm_align(m->code_bytes), o_norms = o_scales + vm_align(m->scale_bytes);
+    const uint64_t o_cache = o_norms + m->o_rope + m->rope_bytes, o_act = o_cache + m->cache_bytes;
+    hipError_t e = hipMalloc((void**)&m->base, o_act + m->act_bytes);
     if (e == hipSuccess) {
-        // RoPE table of the rope part (src/runtime.rs:754-760: fp32 powf, product, sin/cos)
-        const uint32_t half = m->dr / 2;
-        std::vector<float> rope((size_t)c.max_seq_len * half * 2);
-        for (uint32_t p = 0; p < c.max_seq_len; ++p)
-            for (uint32_t j = 0; j < half; ++j) {
-                const float freq = 1.0f / powf(c.rope_theta, (float)(2 * j) / (float)m->dr);
-                const float angle = (float)p * freq;
-                rope[((size_t)p * half + j) * 2] = cosf(angle);
-                rope[((size_t)p * half + j) * 2 + 1] = sinf(angle);
-            }
-        e = hipMemcpy(m->base + m->o_rope, rope.data(), rope.size() * 4, hipMemcpyHostToDevice);
+        m->w_codes = m->base;
+        m->w_scales = m->base + o_scales;
+        m->w_norms = m->base + o_norms;
+        m->kv = m->base + o_cache;
+        m->act = m->base + o_act;
+        e = vm_init_regions(m);
     }
     if (e != hipSuccess) {
         if (m->base) hipFree(m->base);
@@ -312,6 +362,7 @@ int velox_hip_mla_create(const VeloxHipMlaConfig* cfg, VeloxHipMla** out) {
 
 void velox_hip_mla_destroy(VeloxHipMla* m) {
     if (!m) return;
+    vm_forget(m);
     if (m->base) hipFree(m->base);
     delete m;
 }
@@ -319,8 +370,9 @@ void velox_hip_mla_destroy(VeloxHipMla* m) {
 int velox_hip_mla_buffers(const VeloxHipMla* m, VeloxHipMlaBuffers* out) {
     if (!m || !out) return VELOX_HIP_EINVAL;
     out->hidden = vm_act(m, m->a_h);
-    out->latent_cache = vm_at<uint16_t>(m, m->o_cache);
-    out->states = (VeloxDecodeState*)(m->base + m->o_act + m->a_state);
+    if (!vm_has_buffers(m)) return VELOX_HIP_ENOTLOADED;
+    out->latent_cache = vm_cache(m, 0);
+    out->states = vm_states(m);
     out->s_cap = m->s_cap;
     out->splits = m->splits;
     out->weight_bytes = m->code_bytes + m->scale_bytes + m->norm_bytes;
@@ -331,7 +383,7 @@ int velox_hip_mla_buffers(const VeloxHipMla* m, VeloxHipMlaBuffers* out) {
 
 int velox_hip_mla_load_fp8(VeloxHipMla* m, int kind, uint32_t layer, const uint8_t* codes, const float* scales,
                            hipStream_t st) {
-    if (!m || !codes || !scales || layer >= m->cfg.num_layers) return VELOX_HIP_EINVAL;
+    if (!vm_has_buffers(m) || !codes || !scales || layer >= m->cfg.num_layers) return VELOX_HIP_EINVAL;
     uint32_t rows, cols;
     vm_source_dims(m, kind, rows, cols);
     if (!rows) return VELOX_HIP_EINVAL;
@@ -349,17 +401,17 @@ int velox_hip_mla_load_fp8(VeloxHipMla* m, int kind, uint32_t layer, const uint8
 
 int velox_hip_mla_load_f32(VeloxHipMla* m, int kind, uint32_t layer, const float* data, uint64_t count,
                            hipStream_t st) {
-    if (!m || !data || layer >= m->cfg.num_layers) return VELOX_HIP_EINVAL;
+    if (!vm_has_buffers(m) || !data || layer >= m->cfg.num_layers) return VELOX_HIP_EINVAL;
     uint32_t n;
     const uint64_t off = vm_norm_off(m, layer, kind, n);
     if (!n || count != n) return VELOX_HIP_EINVAL;
-    hipError_t e = hipMemcpyAsync(m->base + m->o_norms + off, data, count * 4, hipMemcpyHostToDevice, st);
+    hipError_t e = hipMemcpyAsync(m->w_norms + off, data, count * 4, hipMemcpyHostToDevice, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     return (int)e;
 }
 
 int velox_hip_mla_synthesize(VeloxHipMla* m, uint64_t seed, float sigma, float norm_sigma, hipStream_t st) {
-    if (!m) return VELOX_HIP_EINVAL;
+    if (!vm_has_buffers(m)) return VELOX_HIP_EINVAL;
     // source block scales of the largest matrix
     uint64_t max_blocks = 0;
     for (int kind = VELOX_MLA_Q_A; kind <= VELOX_MLA_O; ++kind) {
@@ -389,7 +441,7 @@ int velox_hip_mla_synthesize(VeloxHipMla* m, uint64_t seed, float sigma, float n
             uint32_t n;
             const uint64_t off = vm_norm_off(m, l, vk[i], n);
             if (!n) continue;
-            e = vx_launch_fill_normal((float*)(m->base + m->o_norms + off), n, vx_stream(seed, vx_tag(l, vt[i])),
+            e = vx_launch_fill_normal((float*)(m->w_norms + off), n, vx_stream(seed, vx_tag(l, vt[i])),
                                       norm_sigma > 0.0f ? vx_normal_coef(norm_sigma) : 0.0f, 1.0f, st);
         }
     }
@@ -400,9 +452,10 @@ int velox_hip_mla_synthesize(VeloxHipMla* m, uint64_t seed, float sigma, float n
 
 int velox_hip_mla_fill_cache(VeloxHipMla* m, uint32_t layer, uint32_t seq, uint32_t n_pos, uint64_t seed, float sigma,
                              hipStream_t st) {
-    if (!m || layer >= m->cfg.num_layers || seq >= m->B || n_pos > m->cfg.max_seq_len) return VELOX_HIP_EINVAL;
+    if (!vm_has_buffers(m) || layer >= m->cfg.num_layers || seq >= m->B || n_pos > m->cfg.max_seq_len)
+        return VELOX_HIP_EINVAL;
     const uint64_t sseed = seed + (uint64_t)seq * 0x9E3779B97F4A7C15ULL;
-    uint16_t* dst = (uint16_t*)(m->base + m->o_cache + m->cache_layer_bytes * layer) + (uint64_t)seq * m->s_cap * m->R;
+    uint16_t* dst = vm_cache(m, layer) + (uint64_t)seq * m->s_cap * m->R;
     hipError_t e = vx_launch_mla_fill_cache(dst, (uint64_t)n_pos * m->R, vx_stream(sseed, vx_tag(layer, VM_T_CACHE)),
                                             vx_normal_coef(sigma), st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
@@ -410,8 +463,8 @@ int velox_hip_mla_fill_cache(VeloxHipMla* m, uint32_t layer, uint32_t seq, uint3
 }
 
 int velox_hip_mla_set_position(VeloxHipMla* m, uint32_t seq, uint64_t pos, hipStream_t st) {
-    if (!m || seq >= m->B || pos >= m->cfg.max_seq_len) return VELOX_HIP_EINVAL;
-    VeloxDecodeState* s = (VeloxDecodeState*)(m->base + m->o_act + m->a_state) + seq;
+    if (!vm_has_buffers(m) || seq >= m->B || pos >= m->cfg.max_seq_len) return VELOX_HIP_EINVAL;
+    VeloxDecodeState* s = vm_states(m) + seq;
     hipError_t e = vx_launch_set_state(s, pos, 0u, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     return (int)e;
@@ -432,13 +485,13 @@ void vm_layer(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, boo
     fold_prev = fold_prev && !direct;
     finish = finish && !direct;
     const VeloxHipMlaConfig& c = m->cfg;
-    const uint4* codes = (const uint4*)(m->base + m->o_codes);
-    const float* scales = (const float*)(m->base + m->o_scales);
-    const float* norms = (const float*)(m->base + m->o_norms);
-    VeloxDecodeState* states = (VeloxDecodeState*)(m->base + m->o_act + m->a_state);
+    const uint4* codes = (const uint4*)m->w_codes;
+    const float* scales = (const float*)m->w_scales;
+    const float* norms = (const float*)m->w_norms;
+    VeloxDecodeState* states = vm_states(m);
     float* h = vm_act(m, m->a_h);
     uint16_t* x16 = (uint16_t*)vm_act(m, m->a_x16);
-    uint16_t* cache = (uint16_t*)(m->base + m->o_cache + m->cache_layer_bytes * layer);
+    uint16_t* cache = vm_cache(m, layer);
     auto gemm = [&](const VmF8Plan& p, const void* x, uint32_t ldx, uint64_t x_gstride, uint32_t x_f32, float* y,
                     uint32_t ldy, uint64_t y_gstride, uint32_t ksplit, uint64_t pstride, uint16_t* y16 = nullptr,
                     uint32_t add_y = 0, const float* gain = nullptr) {
@@ -502,7 +555,7 @@ void vm_layer(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, boo
         a.eps = c.rms_norm_eps;
         a.states = states;
         a.s_max = c.max_seq_len;
-        a.rope = (const float2*)(m->base + m->o_rope);
+        a.rope = vm_rope(m);
         a.cache = cache;
         a.cache_bstride = (uint64_t)m->s_cap * m->R;
         a.q16 = x16;
@@ -532,7 +585,7 @@ void vm_layer(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, boo
         a.s_max = c.max_seq_len;
         a.s_cap = m->s_cap;
         a.splits = m->splits;
-        a.rope = (const float2*)(m->base + m->o_rope);
+        a.rope = vm_rope(m);
         a.qscale = m->scale * 1.4426950408889634f;
         a.cache = cache;
         a.cache_bstride = (uint64_t)m->s_cap * m->R;
@@ -559,7 +612,7 @@ void vm_layer(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, boo
 extern "C" {
 
 void velox_hip_mla_layer_step(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, hipStream_t st) {
-    if (!m || layer >= m->cfg.num_layers || batch == 0 || batch > m->B) {
+    if (!vm_has_buffers(m) || layer >= m->cfg.num_layers || batch == 0 || batch > m->B) {
         vx_record_error(hipErrorInvalidValue);
         return;
     }
@@ -567,12 +620,129 @@ void velox_hip_mla_layer_step(VeloxHipMla* m, uint32_t layer, uint32_t batch, ui
 }
 
 void velox_hip_mla_decode_step(VeloxHipMla* m, uint32_t batch, uint64_t mask, hipStream_t st) {
-    if (!m || batch == 0 || batch > m->B) {
+    if (!vm_has_buffers(m) || batch == 0 || batch > m->B) {
         vx_record_error(hipErrorInvalidValue);
         return;
     }
     const uint32_t n = m->cfg.num_layers;
     for (uint32_t l = 0; l < n; ++l) vm_layer(m, l, batch, mask, l > 0, l + 1 == n, st);
+}
+
+int velox_hip_mla_arena_bytes(const VeloxHipMla* m, uint64_t* weight_bytes, uint64_t* scale_bytes,
+                              uint64_t* norm_bytes, uint64_t* kv_bytes, uint64_t* act_bytes) {
+    if (!m) return VELOX_HIP_EINVAL;
+    if (weight_bytes) *weight_bytes = m->code_bytes;
+    if (scale_bytes) *scale_bytes = m->scale_bytes;
+    if (norm_bytes) *norm_bytes = m->o_rope + m->rope_bytes;
+    if (kv_bytes) *kv_bytes = m->cache_bytes;
+    if (act_bytes) *act_bytes = m->act_bytes;
+    return VELOX_HIP_OK;
+}
+
+int velox_hip_mla_arena(VeloxHipMla* m, VeloxHipArena* out) {
+    if (!vm_has_buffers(m) || !out) return VELOX_HIP_EINVAL;
+    out->weight_arena = m->w_codes;
+    out->weight_scales = m->w_scales;
+    out->norm_weight_arena = m->w_norms;
+    out->kv_cache_pool = m->kv;
+    out->activation_arena = m->act;
+    out->host_pinned_ring = nullptr;  // the attention stack emits no token
+    out->quant_mode = VELOX_QUANT_FP8_E4M3;
+    out->tied_lm_head = 0;
+    std::lock_guard<std::mutex> lk(g_mla_mu);
+    for (const auto& r : g_mla_arenas)
+        if (r.first == out->weight_arena) return VELOX_HIP_OK;
+    g_mla_arenas.emplace_back(out->weight_arena, m);
+    return VELOX_HIP_OK;
+}
+
+int velox_hip_mla_arena_bind(VeloxHipMla* m, VeloxHipArena* a) {
+    if (!m || !a || m->base || vm_has_buffers(m)) return VELOX_HIP_EINVAL;  // a planned handle, bound once
+    if (!a->weight_arena || !a->weight_scales || !a->norm_weight_arena || !a->kv_cache_pool || !a->activation_arena ||
+        a->quant_mode != VELOX_QUANT_FP8_E4M3)
+        return VELOX_HIP_EINVAL;
+    {
+        std::lock_guard<std::mutex> lk(g_mla_mu);
+        for (const auto& r : g_mla_arenas)
+            if (r.first == a->weight_arena) return VELOX_HIP_EINVAL;
+    }
+    m->w_codes = (uint8_t*)a->weight_arena;
+    m->w_scales = (uint8_t*)a->weight_scales;
+    m->w_norms = (uint8_t*)a->norm_weight_arena;
+    m->kv = a->kv_cache_pool;
+    m->act = a->activation_arena;
+    const hipError_t e = vm_init_regions(m);
+    if (e != hipSuccess) {
+        m->w_codes = m->w_scales = m->w_norms = m->kv = m->act = nullptr;
+        return (int)e;
+    }
+    std::lock_guard<std::mutex> lk(g_mla_mu);
+    g_mla_arenas.emplace_back(a->weight_arena, m);
+    return VELOX_HIP_OK;
+}
+
+VeloxHipMla* velox_hip_mla_arena_mla(const VeloxHipArena* a) {
+    if (!a) return nullptr;
+    std::lock_guard<std::mutex> lk(g_mla_mu);
+    for (const auto& r : g_mla_arenas)
+        if (r.first == a->weight_arena) return r.second;
+    return nullptr;
+}
+
+int velox_hip_mla_arena_check(const VeloxHipArena* a, const VeloxHipMlaConfig* want) {
+    const VeloxHipMla* m = velox_hip_mla_arena_mla(a);
+    if (!m || !want) return VELOX_HIP_EINVAL;
+    const VeloxHipMlaConfig& c = m->cfg;
+    const bool same = c.hidden_dim == want->hidden_dim && c.num_heads == want->num_heads &&
+                      c.q_lora_rank == want->q_lora_rank && c.kv_lora_rank == want->kv_lora_rank &&
+                      c.qk_nope_dim == want->qk_nope_dim && c.qk_rope_dim == want->qk_rope_dim &&
+                      c.v_head_dim == want->v_head_dim && c.kv_norm == want->kv_norm &&
+                      c.rms_norm_eps == want->rms_norm_eps && c.rope_theta == want->rope_theta &&
+                      c.softmax_scale == want->softmax_scale;
+    return same ? VELOX_HIP_OK : VELOX_HIP_EINVAL;
+}
+
+void velox_hip_mla_graph_step(VeloxHipArena* ctx, uint64_t mask, hipStream_t st) {
+    VeloxHipMla* m = velox_hip_mla_arena_mla(ctx);
+    if (!vm_has_buffers(m)) {
+        vx_record_error(hipErrorInvalidValue);
+        return;
+    }
+    velox_hip_mla_decode_step(m, m->B, mask, st);
+    vx_record_error(vx_launch_mla_advance(vm_states(m), m->B, mask, st));
+}
+
+void velox_hip_mla_decode(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint64_t mask, hipStream_t st) {
+    VeloxHipMla* m = velox_hip_mla_arena_mla(ctx);
+    if (!vm_has_buffers(m)) {
+        vx_record_error(hipErrorInvalidValue);
+        return;
+    }
+    vx_record_error(vx_launch_set_state(vm_states(m), step, token_in, st));
+    velox_hip_mla_graph_step(ctx, mask, st);
+}
+
+// DeepSeek-V3's MLA model with the reference's emitted names (examples/deepseek_v3_mla.vlx; the
+// graph step launches its MLA kernel per layer, src/codegen.rs:2980-3003): the attention stack of
+// the arena's plan, checked against DeepSeek-V3's dimensions.
+static bool vm_is_deepseek(const VeloxHipArena* a) {
+    VeloxHipMlaConfig want;
+    if (velox_hip_mla_builtin_config("deepseek_v3_mla", 0, 0, &want) == 0 && velox_hip_mla_arena_check(a, &want) == 0)
+        return true;
+    velox_hip_record_error(VELOX_HIP_EINVAL);  // an arena of another model, as the dense entry points
+    return false;
+}
+void velox_DeepSeek_V3_MLA_decode_graph_step_hip(VeloxHipArena* ctx, uint64_t mask, hipStream_t s) {
+    if (vm_is_deepseek(ctx)) velox_hip_mla_graph_step(ctx, mask, s);
+}
+void velox_DeepSeek_V3_MLA_decode_hip(VeloxHipArena* ctx, uint32_t t, size_t step, uint64_t mask, hipStream_t s) {
+    if (vm_is_deepseek(ctx)) velox_hip_mla_decode(ctx, t, step, mask, s);
+}
+void velox_DeepSeek_V3_MLA_prefill_graph_step_hip(VeloxHipArena* ctx, uint64_t mask, hipStream_t s) {
+    if (vm_is_deepseek(ctx)) velox_hip_mla_graph_step(ctx, mask, s);
+}
+void velox_DeepSeek_V3_MLA_prefill_hip(VeloxHipArena* ctx, uint32_t t, size_t step, uint64_t mask, hipStream_t s) {
+    if (vm_is_deepseek(ctx)) velox_hip_mla_decode(ctx, t, step, mask, s);
 }
 
 double velox_hip_mla_step_bytes(const VeloxHipMla* m, uint32_t batch, uint64_t pos) {
@@ -656,7 +826,7 @@ int velox_hip_mla_run(const char* which, uint32_t batch, uint32_t context_len, u
         a.s_max = cfg.max_seq_len;
         a.s_cap = m->s_cap;
         a.splits = m->splits;
-        a.rope = (const float2*)(m->base + m->o_rope);
+        a.rope = vm_rope(m);
         a.qscale = m->scale * 1.4426950408889634f;
         a.cache = buf.latent_cache;
         a.cache_bstride = (uint64_t)m->s_cap * m->R;

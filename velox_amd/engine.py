@@ -355,6 +355,8 @@ class MlaEngine:
         self.cfg = c
         self._m = C.c_void_p()
         L.check(self.lib.velox_hip_mla_create(C.byref(c), C.byref(self._m)), "mla_create")
+        self.arena = L.Arena()  # the plan's regions as the emitted-runner arena (velox_hip_mla_arena)
+        L.check(self.lib.velox_hip_mla_arena(self._m, C.byref(self.arena)), "mla_arena")
         self.buf = L.MlaBuffers()
         L.check(self.lib.velox_hip_mla_buffers(self._m, C.byref(self.buf)), "mla_buffers")
         self.R = c.kv_lora_rank + c.qk_rope_dim
