@@ -180,3 +180,88 @@ def test_config5_qwen72_8192_context_vs_oracle(oracle):
         assert d < LOGIT_TOL, (pos, d)
     gpu.close()
     ref.close()
+
+
+def test_config3_qwen_batch1_2048_context_full_vocab_vs_oracle(oracle):
+    """Configuration 3 at B = 1 as the bench runs it: Qwen2.5-7B (full 152064-word tied head, QKV
+    bias), the planner's split choice for a 2048-token context (9 splits at S_MAX 2082), 2 layers, a
+    seeded 2048-position context. Each step is recomputed by the oracle on the GPU's K/V rows of every
+    layer (its own row included): logits within the fp32-accumulation bar of 1e-3."""
+    seed, layers, ctx, steps = 93, 2, 2048, 3
+    max_seq = 2082
+    gpu = HipDecodeEngine("qwen2_5_7b", seed=seed, norm_sigma=0.1, max_seq_len=max_seq, num_layers=layers)
+    c = L.ModelConfig()
+    L.check(gpu.lib.velox_hip_model_config(gpu._model, __import__("ctypes").byref(c)))
+    assert c.attn_splits == 9 and c.vocab_size == 152064 and c.tied_lm_head == 1
+    hkv, D = c.num_kv_heads, c.head_dim
+    for layer in range(layers):
+        gpu.fill_kv(layer, ctx, seed=seed + 1, sigma=1.0)
+    ref = oracle.Engine(dict(gpu.cfg.as_dict(), max_seq_len=max_seq), seed=seed, sigma=0.02, norm_sigma=0.1,
+                        q4_0=True, kv_bf16=True, threads=16)
+    toks = [int(t) for t in oracle.prompt_tokens(seed, steps, c.vocab_size)]
+    worst = 0.0
+    for i, tok in enumerate(toks):
+        pos = ctx + i
+        t_gpu = gpu.forward_step(tok, pos)
+        assert t_gpu == oracle.argmax(gpu.logits), pos
+        kv = [_device_kv(gpu.arena, layer, hkv, max_seq, D, pos + 1) for layer in range(layers)]
+        for layer in range(layers):
+            kr, vr = ref.kv_cache(layer)
+            kr[:pos], vr[:pos] = kv[layer][0][:pos], kv[layer][1][:pos]
+        t_ref, _, _ = ref.forward_forced(tok, pos, np.stack([kv[layer][0][pos] for layer in range(layers)]),
+                                         np.stack([kv[layer][1][pos] for layer in range(layers)]))
+        d = float(np.max(np.abs(gpu.logits - ref.logits)))
+        worst = max(worst, d)
+        print(f"[qwen2.5-7b B=1 ctx 2048, 9 splits] pos={pos} gpu={t_gpu} ref={t_ref} maxabs={d:.3e}", flush=True)
+        srt = np.sort(ref.logits)
+        if srt[-1] - srt[-2] > 2 * LOGIT_TOL:
+            assert t_gpu == t_ref, pos
+        assert d < 1e-3, (pos, d)
+    gpu.close()
+    ref.close()
+
+
+def test_config3_qwen_batch32_full_vocab_lm_head_vs_oracle(oracle):
+    """One batched step at B = 32 with Qwen2.5-7B's full 152064-row tied LM head (the bench's
+    152064 x 3584 batched head GEMM and per-sequence argmax), 2 layers, every sequence over its own
+    seeded context near 2048 positions."""
+    seed, layers, batch, ctx0 = 95, 2, 32, 2048
+    max_seq = ctx0 + 3
+    gpu = HipBatchEngine("qwen2_5_7b", max_batch=batch, seed=seed, norm_sigma=0.1, max_seq_len=max_seq,
+                         num_layers=layers)
+    c = gpu.cfg
+    assert c.vocab_size == 152064
+    hkv, D, V = c.num_kv_heads, c.head_dim, c.vocab_size
+    ctxs = [ctx0 - 3 * b for b in range(batch)]
+    prompts = [[int(t) for t in oracle.prompt_tokens(seed + 100 + b, max_seq, V)] for b in range(batch)]
+    for b in range(batch):
+        for layer in range(layers):
+            gpu.fill_kv_seq(layer, b, ctxs[b], seed=seed + 7)
+        gpu.set_prompt_seq(b, prompts[b])
+        gpu.set_state_seq(b, ctxs[b], prompts[b][ctxs[b]])
+    contexts = [[_device_kv(gpu.arena, layer * batch + b, hkv, max_seq, D, ctxs[b]) for layer in range(layers)]
+                for b in range(batch)]
+    gpu.batch_step(batch)
+    gpu.sync()
+    got = [gpu.logits_seq(b) for b in range(batch)]
+    ref = oracle.Engine(dict(c.as_dict(), max_seq_len=max_seq), seed=seed, sigma=0.02, norm_sigma=0.1,
+                        q4_0=True, kv_bf16=True, threads=16)
+    worst = 0.0
+    for b in range(batch):
+        ref.reset()
+        for layer in range(layers):
+            kr, vr = ref.kv_cache(layer)
+            kr[:ctxs[b]] = contexts[b][layer][0]
+            vr[:ctxs[b]] = contexts[b][layer][1]
+        pos = ctxs[b]
+        t_ref = ref.forward(prompts[b][pos], pos)
+        d = float(np.max(np.abs(got[b] - ref.logits)))
+        worst = max(worst, d)
+        assert gpu.ring_seq(b, pos) == oracle.argmax(got[b]), (b, pos)
+        srt = np.sort(ref.logits)
+        if srt[-1] - srt[-2] > 2 * LOGIT_TOL:
+            assert gpu.ring_seq(b, pos) == t_ref, (b, pos)
+        assert d < LOGIT_TOL, (b, pos, d)
+    print(f"[qwen2.5-7b batch 32, full vocab] worst logits maxabs {worst:.3e}", flush=True)
+    gpu.close()
+    ref.close()

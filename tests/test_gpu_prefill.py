@@ -258,3 +258,44 @@ def test_prefill_rejects_positions_past_the_staged_prompt():
     assert lib.velox_hip_prefill_batch(C.byref(b.arena), 3, 2, 1, None) == L.EINVAL
     b.prefill_batch(0, 4)
     b.close()
+
+
+def test_prefill_llama3_8b_full_depth_128_rows_vs_oracle(oracle):
+    """The bench's TTFT path at full size: Llama-3-8B (32 layers, untied 128256-row head) prefills a
+    128-token prompt as one 128-row chunk of velox_hip_prefill_batch. At sampled rows the oracle
+    recomputes that position on the GPU's K/V rows of every layer (its own row included), so the
+    two sides attend over the same values; the chunk's logits rows must be within the bf16 bar."""
+    from test_gpu_configs import _device_kv as kv_rows
+
+    seed, P = 97, 128
+    max_seq = P + 8
+    gpu = HipDecodeEngine("llama3_8b", seed=seed, max_seq_len=max_seq, prefill_chunk=128)
+    c = gpu.cfg
+    nl, hkv, D = c.num_layers, c.num_kv_heads, c.head_dim
+    prompt = [int(t) for t in oracle.prompt_tokens(seed, P, c.vocab_size)]
+    gpu.set_prompt(prompt)
+    gpu.prefill_batch(0, P)
+    rows = gpu.chunk_logits(P)
+    kv = [kv_rows(gpu.arena, layer, hkv, max_seq, D, P) for layer in range(nl)]
+    for pos in range(P):
+        assert gpu.ring(pos) == oracle.argmax(rows[pos]), pos
+    assert gpu.state() == (P, oracle.argmax(rows[-1]))
+    gpu.close()
+    ref = oracle.Engine(dict(c.as_dict(), max_seq_len=max_seq), seed=seed, sigma=0.02, norm_sigma=0.0, q4_0=True,
+                        kv_bf16=True, threads=16)
+    caches = [ref.kv_cache(layer) for layer in range(nl)]
+    worst = 0.0
+    for pos in (0, 1, 63, 126, 127):
+        for layer, (kr, vr) in enumerate(caches):
+            kr[:pos], vr[:pos] = kv[layer][0][:pos], kv[layer][1][:pos]
+        t_ref, _, _ = ref.forward_forced(prompt[pos], pos, np.stack([kv[layer][0][pos] for layer in range(nl)]),
+                                         np.stack([kv[layer][1][pos] for layer in range(nl)]))
+        d = float(np.max(np.abs(rows[pos] - ref.logits)))
+        worst = max(worst, d)
+        print(f"[llama3_8b prefill 128 rows, 32 layers] pos={pos} gpu={oracle.argmax(rows[pos])} ref={t_ref} "
+              f"maxabs={d:.3e}", flush=True)
+        if _margin(ref.logits) > 2 * LOGIT_TOL:
+            assert oracle.argmax(rows[pos]) == t_ref, pos
+        assert d < LOGIT_TOL, (pos, d)
+    print(f"[llama3_8b prefill 128 rows, 32 layers] worst logits maxabs {worst:.3e}", flush=True)
+    ref.close()
