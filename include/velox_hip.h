@@ -441,6 +441,8 @@ typedef struct VeloxHipRunOptions {
                              /* non-NULL: the single-sequence step the run captures and replays (a
                                 generated runner's velox_<Model>_decode_graph_step_hip); NULL:
                                 velox_hip_decode_graph_step */
+    uint32_t attn_splits;    /* >0: the configuration's attn_splits (split-K attention with that many
+                                splits, never the fused QKV + attention launch); 0: the planner's */
 } VeloxHipRunOptions;
 
 typedef struct VeloxHipRunReport {

@@ -69,7 +69,7 @@ class RunOptions(C.Structure):
         ("kernel_passes", C.c_uint32), ("verbose", C.c_uint32), ("prompt_tokens", C.POINTER(C.c_uint32)),
         ("context_len", C.c_uint32), ("batch", C.c_uint32), ("weights_path", C.c_char_p),
         ("prefill_chunk", C.c_uint32), ("model_file", C.c_char_p), ("unquantized", C.c_uint32),
-        ("model_config", C.POINTER(ModelConfig)), ("decode_step", C.c_void_p),
+        ("model_config", C.POINTER(ModelConfig)), ("decode_step", C.c_void_p), ("attn_splits", C.c_uint32),
     ]
 
 

@@ -1697,6 +1697,7 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
         ~Closer() { velox_hip_gguf_close(g); velox_hip_st_close(s); }
     } closer{gguf, stf};
     if (opt->num_layers && !gguf) cfg.num_layers = opt->num_layers;
+    if (opt->attn_splits) cfg.attn_splits = opt->attn_splits;
     if (opt->unquantized > 3 || (opt->unquantized && gguf)) return VELOX_HIP_EINVAL;
     if (opt->unquantized)
         cfg.quant_mode = opt->unquantized == 1   ? VELOX_QUANT_F32

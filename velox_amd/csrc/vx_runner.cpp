@@ -8,7 +8,7 @@
 //                    [--tokens 1,2,3 | --prompt-len N]
 //                    [--context-len N] [--steps N] [--warmup N] [--seed S] [--layers L]
 //                    [--prefill-chunk N] [--unquantized f32|f16] [--quantize MODE] [--no-cuda-graph]
-//                    [--verbose]
+//                    [--attn-splits N] [--verbose]
 //
 // --weights FILE is what src/cli.rs:653-654 passes on every run: the checkpoint the model's source
 // binds (src/cli.rs:1400-1414). A safetensors file (the reference runner's format,
@@ -61,7 +61,7 @@ extern "C" int velox_hip_runner_main(int argc, char** argv, const VeloxHipModelC
     bool model_given = false;
     int qsel = -1;  // weight format: -1 the default of the weight source, else VeloxHipRunOptions.unquantized
     std::vector<uint32_t> tokens;
-    uint32_t prompt_len = 128, steps = 32, warmup = 0, layers = 0, context_len = 0, prefill_chunk = 0;
+    uint32_t prompt_len = 128, steps = 32, warmup = 0, layers = 0, context_len = 0, prefill_chunk = 0, attn_splits = 0;
     uint64_t seed = 1234;
     bool graph = true, verbose = false;
     for (int i = 1; i < argc; ++i) {
@@ -111,6 +111,7 @@ extern "C" int velox_hip_runner_main(int argc, char** argv, const VeloxHipModelC
         else if (!std::strcmp(a, "--warmup")) warmup = (uint32_t)std::atoi(next());
         else if (!std::strcmp(a, "--seed")) seed = std::strtoull(next(), nullptr, 10);
         else if (!std::strcmp(a, "--layers")) layers = (uint32_t)std::atoi(next());
+        else if (!std::strcmp(a, "--attn-splits")) attn_splits = (uint32_t)std::atoi(next());
         else if (!std::strcmp(a, "--prefill-chunk")) {
             prefill_chunk = (uint32_t)std::atoi(next());
             if (prefill_chunk < 2 || prefill_chunk > 128) {
@@ -167,6 +168,7 @@ extern "C" int velox_hip_runner_main(int argc, char** argv, const VeloxHipModelC
     std::memset(&opt, 0, sizeof(opt));
     opt.model = st_file && !model_given ? nullptr : model.c_str();
     opt.model_config = baked;
+    opt.attn_splits = attn_splits;
     opt.decode_step = step;
     opt.model_file = model_file.empty() ? nullptr : model_file.c_str();
     opt.unquantized = unquantized;

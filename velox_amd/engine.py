@@ -305,7 +305,8 @@ def run(model: str = "llama3_8b", prompt_len: int = 128, warmup: int = 5, steps:
         sigma: float = 0.02, norm_sigma: float = 0.0, use_graph: bool = True, num_layers: int = 0,
         max_seq_len: int = 0, max_tokens: int = 1024, kernel_passes: int = 0,
         prompt: list[int] | None = None, context_len: int = 0, batch: int = 1,
-        prefill_chunk: int = 0, model_file: str | None = None, unquantized: int = 0) -> tuple[dict, list[int]]:
+        prefill_chunk: int = 0, model_file: str | None = None, unquantized: int = 0,
+        attn_splits: int = 0) -> tuple[dict, list[int]]:
     """The C++ runner flow (velox_hip_run): synthesize, capture, prefill, timed decode. `prompt`
     replaces the seeded random prompt of `prompt_len` ids; `context_len` > 0 starts from a seeded
     context of that many positions already in the KV cache (then prompt_len must be 1). Returned
@@ -321,7 +322,8 @@ def run(model: str = "llama3_8b", prompt_len: int = 128, warmup: int = 5, steps:
         ptoks = (C.c_uint32 * prompt_len)(*prompt)
     opt = L.RunOptions(model.encode(), max_seq_len, prompt_len, warmup, steps, seed, sigma, norm_sigma,
                        int(use_graph), num_layers, kernel_passes, 0, ptoks, context_len, batch, None,
-                       prefill_chunk, model_file.encode() if model_file else None, unquantized)
+                       prefill_chunk, model_file.encode() if model_file else None, unquantized, None, None,
+                       attn_splits)
     rep = L.RunReport()
     toks = (C.c_uint32 * max_tokens)()
     rc = lib.velox_hip_run(C.byref(opt), toks, max_tokens, C.byref(rep))
