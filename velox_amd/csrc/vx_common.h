@@ -114,6 +114,8 @@ struct VxGemvArgs {
     const uint4* codes;
     const uint16_t* scales;
     uint32_t n, k, n_tiles, n_iter;
+    // tiled GEMV grid (set by the launcher): workgroup b owns tiles [b q + min(b, r), + q + (b < r))
+    uint32_t wg_q, wg_r;
     const float* x;
     const float* gain;
     float eps;
@@ -172,6 +174,10 @@ struct VxAttnArgs {
     // batched merge kernel's output: fp16((1 / l) o)), and no partials are written
     uint16_t* x16;
     uint32_t x_ld, x_bs;
+    // single-sequence decode (batch <= 1, state set): the RoPE row of the state's position, which the
+    // step's embedding kernel copied there; the kernel then issues every load before it waits for the
+    // position. NULL: the row is read from `rope` at the position.
+    const float2* rope_cur;
 };
 
 // Batched (B <= 32 sequences) Q4_0 GEMM: Y[m][n] = sum_k X[m][k] W[n][k] for fp16 activations
@@ -295,7 +301,8 @@ hipError_t vx_launch_bfinalize(const float* cand_v, const uint32_t* cand_i, uint
                                uint32_t* rings, const uint32_t* prompts, const uint32_t* plens, uint32_t prompt_stride,
                                uint32_t batch, uint64_t mask, hipStream_t st);
 hipError_t vx_launch_embed(const VxMat& m, const VeloxDecodeState* state, uint32_t fixed_token, float* h,
-                           uint64_t mask, hipStream_t st);
+                           uint64_t mask, hipStream_t st, const float2* rope = nullptr, float2* rope_cur = nullptr,
+                           uint32_t half = 0, uint32_t s_max = 0);
 hipError_t vx_launch_set_state(VeloxDecodeState* state, uint64_t step, uint32_t token, hipStream_t st);
 hipError_t vx_launch_repack(const void* blocks, uint32_t rows, uint32_t row0, uint32_t pair_part, const VxMat& m,
                             hipStream_t st);

@@ -144,7 +144,9 @@ __device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a) {
     static_assert(FMT != VX_FMT_G64 || S % 2 == 0, "a group-64 pair of blocks shares one row's lanes");
     constexpr bool G64 = FMT == VX_FMT_G64;
     extern __shared__ __align__(16) unsigned char vx_smem[];
-    if ((a.active_mask & 1ULL) == 0ULL) return;
+    // (the active-mask test comes after the first loads are issued: a branch here would wait for the
+    // kernel arguments once for the mask and again for everything else)
+    const bool active = (a.active_mask & 1ULL) != 0ULL;
     constexpr int W = kGemvWaves, kU = kGemvU, R = 64 / S, NT = 64 * W;
     const uint32_t K = a.k, nb = K >> 5, n_iter = a.n_iter;
     // activations: kXDigits planes of nb 16-byte chunks (the 4 digit dwords of one block), then the
@@ -156,10 +158,12 @@ __device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a) {
     // the wave index is uniform: readfirstlane lets every per-wave quantity live in SGPRs
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane / S, s = lane % S;
-    // workgroup blocks: workgroup b owns tiles [b n / grid, (b + 1) n / grid), dealt to its W waves
-    // round-robin, so every workgroup (every CU) streams the same number of tiles
-    const uint32_t b0 = (uint32_t)(((uint64_t)blockIdx.x * a.n_tiles) / gridDim.x);
-    const uint32_t b1 = (uint32_t)(((uint64_t)(blockIdx.x + 1u) * a.n_tiles) / gridDim.x);
+    // workgroup blocks: workgroup b owns q or q + 1 consecutive tiles (the launcher's split of n_tiles
+    // over the grid, no device division), dealt to its W waves round-robin, so every workgroup (every
+    // CU) streams the same number of tiles to within one
+    const uint32_t bid = blockIdx.x;
+    const uint32_t b0 = bid * a.wg_q + min(bid, a.wg_r);
+    const uint32_t b1 = b0 + a.wg_q + (bid < a.wg_r ? 1u : 0u);
     const uint32_t first = b0 + (uint32_t)wave, step = (uint32_t)W;
     const uint32_t my_tiles = first < b1 ? (b1 - 1u - first) / (uint32_t)W + 1u : 0u;
     const uint32_t total = my_tiles * n_iter;
@@ -227,6 +231,7 @@ __device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a) {
     };
 #pragma unroll
     for (int u = 0; u < kU; ++u) issue(u);
+    if (!active) return;  // uniform: the whole workgroup leaves before the staging barrier
 
     if constexpr (SPL > 0) {
         // LSE merge of the splits (m, l in the log2 domain; an empty split has m = -inf, l = 0):
@@ -284,10 +289,11 @@ __device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a) {
             m = fmaxf(m, fabsf(u[e]));
             nan += u[e] * 0.0f;
         }
-        m = fmaxf(m, __shfl_xor(m, 1));
-        m = fmaxf(m, __shfl_xor(m, 2));
-        nan += __shfl_xor(nan, 1);
-        nan += __shfl_xor(nan, 2);
+        // across the block's four lanes by DPP quad permutations (no LDS round trip)
+        m = fmaxf(m, vx_dpp<0xB1>(m));
+        m = fmaxf(m, vx_dpp<0x4E>(m));
+        nan += vx_dpp<0xB1>(nan);
+        nan += vx_dpp<0x4E>(nan);
         const int ex = vx_xblock_exp(m);
         const float sc = vx_pow2f(ex);
         // Y = X + kXOffset (so that its plain base-16 digits are c_d + 8): adding 1.5 * 2^23 to the
@@ -319,8 +325,8 @@ __device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a) {
             int xsum = 0;
 #pragma unroll
             for (int e = 0; e < 8; ++e) xsum += (int)Y[e] - (int)kXOffset;
-            xsum += __shfl_xor(xsum, 1);
-            xsum += __shfl_xor(xsum, 2);
+            xsum += __builtin_amdgcn_update_dpp(0, xsum, 0xB1, 0xF, 0xF, true);
+            xsum += __builtin_amdgcn_update_dpp(0, xsum, 0x4E, 0xF, 0xF, true);
             if ((g & 3u) == 0u) tsum[g >> 2] = (float)xsum * vx_pow2f(-ex) + nan;
         }
         if ((g & 3u) == 0u) unscale[g >> 2] = vx_pow2f(-ex) + nan;
@@ -340,7 +346,7 @@ __device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a) {
         stage(g, v0, v1, g0, g1);
     }
     if constexpr (NORM) {
-        ss = vx_wave_sum(ss);
+        ss = vx_group_sum<64>(ss);
         if (lane == 0) red[wave] = ss;
     }
     __syncthreads();
@@ -500,7 +506,10 @@ hipError_t vx_gemv_launch_t(const VxGemvArgs& a, uint32_t max_wgs, hipStream_t s
         attr_lds = lds;
     }
     const uint32_t wgs = vx_gemv_wgs(a.n_tiles, max_wgs);
-    hipLaunchKernelGGL(kern, dim3(wgs), dim3(64 * W), lds, st, a);
+    VxGemvArgs ag = a;
+    ag.wg_q = a.n_tiles / wgs;
+    ag.wg_r = a.n_tiles % wgs;
+    hipLaunchKernelGGL(kern, dim3(wgs), dim3(64 * W), lds, st, ag);
     return hipGetLastError();
 }
 

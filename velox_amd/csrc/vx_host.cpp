@@ -84,7 +84,7 @@ struct VeloxHipModel {
     uint64_t code_bytes = 0, scale_bytes = 0, norm_bytes = 0, kv_bytes = 0, act_bytes = 0, kv_layer_bytes = 0;
     // activation arena offsets (bytes)
     uint64_t a_state = 0, a_plen = 0, a_argmax_counter = 0, a_counters = 0, a_token = 0, a_prompt = 0;
-    uint64_t a_h = 0, a_qkv = 0, a_attn = 0, a_act = 0, a_logits = 0, a_part_o = 0, a_part_ml = 0;
+    uint64_t a_h = 0, a_qkv = 0, a_attn = 0, a_act = 0, a_logits = 0, a_part_o = 0, a_part_ml = 0, a_rope_cur = 0;
     uint64_t a_cand_v = 0, a_cand_i = 0;
     uint32_t splits = 1, max_wgs = 2048, s_cap = 0;
     bool fused_merge = false;  // o_proj merges the attention partials
@@ -432,6 +432,7 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
     M->a_h = take((uint64_t)H * 4);
     M->a_qkv = take((uint64_t)(qd + 2 * kvd) * 4);
     M->a_attn = take((uint64_t)qd * 4);
+    M->a_rope_cur = take((uint64_t)D / 2 * 8);
     M->a_act = take((uint64_t)F * 4);
     M->a_logits = take((uint64_t)c.vocab_size * 4);
     M->a_part_o = take((uint64_t)c.num_heads * splits * D * 4);
@@ -1240,11 +1241,14 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
     float* ffn = (float*)(act + M->a_act);
     auto vecp = [&](uint64_t off) { return (const float*)((const uint8_t*)nrm + off); };
 
-    vx_record(vx_launch_embed(vx_view(A, M->embed), state, 0, h, mask, st));
+    float2* rope_cur = (float2*)(act + M->a_rope_cur);
+    vx_record(vx_launch_embed(vx_view(A, M->embed), state, 0, h, mask, st, (const float2*)vecp(M->rope), rope_cur,
+                              c.head_dim / 2, c.max_seq_len));
     VxAttnArgs at;
     std::memset(&at, 0, sizeof(at));
     at.qkv = qkv;
     at.rope = (const float2*)vecp(M->rope);
+    at.rope_cur = rope_cur;
     at.state = state;
     at.part_o = (float*)(act + M->a_part_o);
     at.part_ml = (float*)(act + M->a_part_ml);

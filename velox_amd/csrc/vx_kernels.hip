@@ -188,9 +188,12 @@ constexpr size_t vx_attn_lds_bytes() {
 // workgroup takes R consecutive rows of the chunk, the MFMA columns r G + h holding head h of row
 // r, each column masked at its own row's position, so R rows share every K/V chunk load and the
 // q operand's 16 columns are used 16 / G times as fully (Llama-3-8B at 128 rows: 4 rows of 4 heads).
-template <int D, int G, int W, bool PS, int R = 1>
+template <int D, int G, int W, bool PS, int R = 1, bool RC = false>
 __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
-    if ((a.active_mask & 1ULL) == 0ULL) return;
+    static_assert(!RC || (R == 1 && !PS), "the copied RoPE row serves the single-sequence decode step");
+    // (the active-mask test follows the first loads: a branch here would wait for the kernel
+    // arguments once for the mask and again for everything else)
+    const bool active = (a.active_mask & 1ULL) != 0ULL;
     constexpr int HALF = D / 2, NT = 64 * W, NC = D / 32, NB = D / 16, HR = vx_attn_hrows<D, G, R>();
     constexpr int GC = G * R;  // used MFMA columns
     static_assert(GC <= 16 && (R == 1 || PS), "R rows of G heads in 16 columns; several rows only in prefill");
@@ -229,21 +232,27 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
         return step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;
     };
     auto uniform = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane(v); };
-    const uint32_t pos = uniform(row_pos(0u));
-    uint32_t posmax = pos;
-#pragma unroll
-    for (int r = 1; r < R; ++r) posmax = max(posmax, uniform(row_pos((uint32_t)r)));
-    // cached positions [t0, t1): below pos, or up to pos when a prefill chunk appended its rows
-    const uint32_t t1 = min(a.prefill ? posmax + 1u : pos, t0 + chunk);
-    const uint32_t n_chunks = t1 > t0 ? (t1 - t0 + 31u) >> 5 : 0u;
-    const bool has_new = !a.prefill && t0 <= pos && pos < t0 + chunk;  // this split folds in the new position
     // the row (of R) a RoPE pair belongs to
     auto pair_row = [&](int p) { return R == 1 ? 0 : p / (G * HALF); };
     float2 rcs[RP];
+    uint32_t pos = 0, posmax = 0;
+    uint64_t step0 = (uint64_t)a.fixed_pos;
+    if constexpr (RC) {
+        // the step's RoPE row was copied to rope_cur: nothing waits for the position until the masks
+        // below, so its load goes first and the RoPE row, q/k/v and first K/V chunk loads follow at once
+        step0 = __hip_atomic_load((uint64_t*)&a.state[0].step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
-    for (int i = 0; i < RP; ++i) {
-        const int p = min(tid + i * NT, NP - 1);
-        rcs[i] = a.rope[(size_t)(R == 1 ? pos : row_pos((uint32_t)pair_row(p))) * HALF + p % HALF];
+        for (int i = 0; i < RP; ++i) rcs[i] = a.rope_cur[min(tid + i * NT, NP - 1) % HALF];
+    } else {
+        pos = uniform(row_pos(0u));
+        posmax = pos;
+#pragma unroll
+        for (int r = 1; r < R; ++r) posmax = max(posmax, uniform(row_pos((uint32_t)r)));
+#pragma unroll
+        for (int i = 0; i < RP; ++i) {
+            const int p = min(tid + i * NT, NP - 1);
+            rcs[i] = a.rope[(size_t)(R == 1 ? pos : row_pos((uint32_t)pair_row(p))) * HALF + p % HALF];
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -307,6 +316,16 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     };
     uint32_t ci = (uint32_t)wave;
     load_chunk(t0 + 32u * min(ci, chunk / 32u - 1u));
+    if (!active) return;  // uniform, before any LDS use
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (RC) {  // the position: its load, issued first, has returned first
+        pos = uniform(step0 < (uint64_t)a.s_max ? (uint32_t)step0 : a.s_max - 1u);
+        posmax = pos;
+    }
+    // cached positions [t0, t1): below pos, or up to pos when a prefill chunk appended its rows
+    const uint32_t t1 = min(a.prefill ? posmax + 1u : pos, t0 + chunk);
+    const uint32_t n_chunks = t1 > t0 ? (t1 - t0 + 31u) >> 5 : 0u;
+    const bool has_new = !a.prefill && t0 <= pos && pos < t0 + chunk;  // this split folds in the new position
 
     // ---- RoPE on this group's q heads and the new k; bf16 K/V row ----
     const float qscale = a.scale * kLog2e;  // scores in the log2 domain
@@ -503,9 +522,17 @@ __global__ __launch_bounds__(D) void vx_attn_merge_kernel(VxAttnArgs a) {
 // =============================================================================================
 // Small kernels: embedding gather, decode state, loaders, parity helpers
 // =============================================================================================
+// rope_cur (single-sequence step): the RoPE row of the state's position, copied here for the step's
+// attention kernels, which then issue every load before they wait for the position.
 __global__ __launch_bounds__(kWG) void vx_embed_kernel(VxMat m, const VeloxDecodeState* state, uint32_t fixed_token,
-                                                       float* h, uint64_t mask) {
+                                                       float* h, uint64_t mask, const float2* rope, float2* rope_cur,
+                                                       uint32_t half, uint32_t s_max) {
     if ((mask & 1ULL) == 0ULL) return;
+    if (rope_cur && state && blockIdx.x == 0 && threadIdx.x < half) {
+        const uint64_t step = state->step;
+        const uint32_t pos = step < (uint64_t)s_max ? (uint32_t)step : s_max - 1u;  // the attention's clamp
+        rope_cur[threadIdx.x] = rope[(size_t)pos * half + threadIdx.x];
+    }
     const uint32_t token = state ? state->token : fixed_token;
     const uint32_t b = blockIdx.x * kWG + threadIdx.x, nb = m.k >> 5;
     if (b >= nb || token >= m.n) return;  // src/codegen.rs:2386-2390 guard
@@ -689,12 +716,12 @@ __global__ __launch_bounds__(kWG) void vx_argmax_kernel(const float* x, uint32_t
 // =============================================================================================
 namespace {
 
-template <int D, int G, bool PS, int W, int R = 1>
+template <int D, int G, bool PS, int W, int R = 1, bool RC = false>
 hipError_t vx_attn_launch_w(const VxAttnArgs& a, hipStream_t st) {
     constexpr size_t lds = vx_attn_lds_bytes<D, G, W, R>();
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)vx_attn_kernel<D, G, W, PS, R>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        if (hipFuncSetAttribute((const void*)vx_attn_kernel<D, G, W, PS, R, RC>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds) != hipSuccess) {
             (void)hipGetLastError();
             return hipErrorInvalidValue;
@@ -702,7 +729,7 @@ hipError_t vx_attn_launch_w(const VxAttnArgs& a, hipStream_t st) {
         attr_set = true;
     }
     const uint32_t rows = a.batch ? a.batch : 1u;
-    hipLaunchKernelGGL((vx_attn_kernel<D, G, W, PS, R>), dim3(a.splits, a.hkv, (rows + R - 1u) / R), dim3(64 * W), lds,
+    hipLaunchKernelGGL((vx_attn_kernel<D, G, W, PS, R, RC>), dim3(a.splits, a.hkv, (rows + R - 1u) / R), dim3(64 * W), lds,
                        st, a);
     return hipGetLastError();
 }
@@ -722,6 +749,8 @@ hipError_t vx_attn_launch_ps(const VxAttnArgs& a, hipStream_t st) {
         const uint64_t wgs = (uint64_t)a.splits * a.hkv * (a.batch ? a.batch : 1u);
         if (wgs > 256u && span <= 4u * 32u) return vx_attn_launch_w<D, G, PS, 4>(a, st);
     }
+    if constexpr (!PS)
+        if (a.rope_cur && a.state && a.batch <= 1u && !a.prefill) return vx_attn_launch_w<D, G, PS, 8, 1, true>(a, st);
     return vx_attn_launch_w<D, G, PS, 8>(a, st);
 }
 
@@ -793,9 +822,12 @@ hipError_t vx_launch_attention(const VxAttnArgs& a, uint32_t d, hipStream_t st) 
 }
 
 hipError_t vx_launch_embed(const VxMat& m, const VeloxDecodeState* state, uint32_t fixed_token, float* h,
-                           uint64_t mask, hipStream_t st) {
+                           uint64_t mask, hipStream_t st, const float2* rope, float2* rope_cur, uint32_t half,
+                           uint32_t s_max) {
     const uint32_t nb = m.k >> 5;
-    hipLaunchKernelGGL(vx_embed_kernel, dim3((nb + kWG - 1) / kWG), dim3(kWG), 0, st, m, state, fixed_token, h, mask);
+    if (rope_cur && (!rope || half == 0 || half > kWG || s_max == 0)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(vx_embed_kernel, dim3((nb + kWG - 1) / kWG), dim3(kWG), 0, st, m, state, fixed_token, h, mask,
+                       rope, rope_cur, half, s_max);
     return hipGetLastError();
 }
 
