@@ -178,6 +178,7 @@ struct VxAttnArgs {
     // step's embedding kernel copied there; the kernel then issues every load before it waits for the
     // position. NULL: the row is read from `rope` at the position.
     const float2* rope_cur;
+    uint32_t chunk;  // set by vx_launch_attention: positions per split, ceil(s_max / splits) rounded up to 32
 };
 
 // Batched (B <= 32 sequences) Q4_0 GEMM: Y[m][n] = sum_k X[m][k] W[n][k] for fp16 activations

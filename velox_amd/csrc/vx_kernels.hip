@@ -191,7 +191,7 @@ constexpr size_t vx_attn_lds_bytes() {
 template <int D, int G, int W, bool PS, int R = 1, bool RC = false>
 __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     static_assert(!RC || (R == 1 && !PS), "the copied RoPE row serves the single-sequence decode step");
-    // (the active-mask test follows the first loads: a branch here would wait for the kernel
+    // (the active-mask test follows the first barrier: a branch here would wait for the kernel
     // arguments once for the mask and again for everything else)
     const bool active = (a.active_mask & 1ULL) != 0ULL;
     constexpr int HALF = D / 2, NT = 64 * W, NC = D / 32, NB = D / 16, HR = vx_attn_hrows<D, G, R>();
@@ -210,7 +210,7 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, grp = lane >> 4;            // MFMA column (head / dimension), K group
     const uint32_t g = blockIdx.y, sp = blockIdx.x, bq = blockIdx.z * (uint32_t)R;  // bq: sequence / first row
-    const uint32_t chunk = ((a.s_max + a.splits - 1u) / a.splits + 31u) & ~31u;
+    const uint32_t chunk = a.chunk;
     const uint32_t t0 = sp * chunk;
     uint16_t* kvb = a.kv + (size_t)bq * a.kv_bstride;
     uint16_t* Kc = kvb + (size_t)g * a.s_cap * D;
@@ -253,8 +253,8 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
             const int p = min(tid + i * NT, NP - 1);
             rcs[i] = a.rope[(size_t)(R == 1 ? pos : row_pos((uint32_t)pair_row(p))) * HALF + p % HALF];
         }
+        __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
 
     // ---- q, the new k/v into registers (clamped: no load under a branch) ----
     float r1[RP], r2[RP], vnew;
@@ -316,7 +316,6 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     };
     uint32_t ci = (uint32_t)wave;
     load_chunk(t0 + 32u * min(ci, chunk / 32u - 1u));
-    if (!active) return;  // uniform, before any LDS use
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (RC) {  // the position: its load, issued first, has returned first
         pos = uniform(step0 < (uint64_t)a.s_max ? (uint32_t)step0 : a.s_max - 1u);
@@ -358,6 +357,9 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     }
     if (tid < D) vn_s[tid] = vx_f32_to_bf16_bits(vnew);
     __syncthreads();
+    // the step's mask (uniform) after the barrier: loads are not moved across it, so the kernel
+    // arguments come in one batch and every load above is issued before the test
+    if (!active) return;
     if (sp == 0 && !a.prefill) {
         const uint16_t* vblk = Vc + (size_t)(pos >> 5) * D * 32 + vx_vslot(pos & 31u);
         for (int d = tid; d < D; d += NT) {
@@ -797,24 +799,26 @@ hipError_t vx_launch_attention(const VxAttnArgs& a, uint32_t d, hipStream_t st) 
     if (a.hkv == 0 || a.hq % a.hkv != 0 || a.splits == 0 || a.splits > 64 || a.s_max == 0 || (a.s_cap & 31u) ||
         a.s_cap < a.s_max)
         return hipErrorInvalidValue;
+    VxAttnArgs b = a;
+    b.chunk = ((a.s_max + a.splits - 1u) / a.splits + 31u) & ~31u;
     const uint32_t G = a.hq / a.hkv;
     if (d == 64) {
         switch (G) {
-            case 1: return vx_attn_launch_t<64, 1>(a, st);
-            case 2: return vx_attn_launch_t<64, 2>(a, st);
-            case 3: return vx_attn_launch_t<64, 3>(a, st);
-            case 4: return vx_attn_launch_t<64, 4>(a, st);
-            case 8: return vx_attn_launch_t<64, 8>(a, st);
+            case 1: return vx_attn_launch_t<64, 1>(b, st);
+            case 2: return vx_attn_launch_t<64, 2>(b, st);
+            case 3: return vx_attn_launch_t<64, 3>(b, st);
+            case 4: return vx_attn_launch_t<64, 4>(b, st);
+            case 8: return vx_attn_launch_t<64, 8>(b, st);
             default: return hipErrorInvalidValue;
         }
     }
     if (d == 128) {
         switch (G) {
-            case 1: return vx_attn_launch_t<128, 1>(a, st);
-            case 2: return vx_attn_launch_t<128, 2>(a, st);
-            case 4: return vx_attn_launch_t<128, 4>(a, st);
-            case 7: return vx_attn_launch_t<128, 7>(a, st);
-            case 8: return vx_attn_launch_t<128, 8>(a, st);
+            case 1: return vx_attn_launch_t<128, 1>(b, st);
+            case 2: return vx_attn_launch_t<128, 2>(b, st);
+            case 4: return vx_attn_launch_t<128, 4>(b, st);
+            case 7: return vx_attn_launch_t<128, 7>(b, st);
+            case 8: return vx_attn_launch_t<128, 8>(b, st);
             default: return hipErrorInvalidValue;
         }
     }
