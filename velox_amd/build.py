@@ -49,16 +49,17 @@ _VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 FILE_FLAGS = {"vx_mgemm.hip": _VGPR_MFMA, "vx_mla.hip": _VGPR_MFMA}
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(LIBDIR, exist_ok=True)
+def _compile_library(lib: str, extra: list[str], verbose: bool) -> None:
+    """Every HIP_SOURCES unit (common flags + extra) linked into the shared library `lib`."""
+    os.makedirs(os.path.dirname(lib), exist_ok=True)
     hipcc = _hipcc()
-    tmp = LIB + ".tmp"
+    tmp = lib + ".tmp"
     with tempfile.TemporaryDirectory(prefix="velox_hip_build_") as objdir:
         cmds, objs = [], []
         for s in HIP_SOURCES:
             obj = os.path.join(objdir, s + ".o")
             objs.append(obj)
-            cmds.append([hipcc, *common_flags(), *FILE_FLAGS.get(s, []), "-c", "-o", obj, os.path.join(CSRC, s)])
+            cmds.append([hipcc, *common_flags(), *extra, *FILE_FLAGS.get(s, []), "-c", "-o", obj, os.path.join(CSRC, s)])
         with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(cmds))) as pool:
             for cmd in cmds:
                 if verbose:
@@ -72,16 +73,40 @@ def build(verbose: bool = False) -> str:
         if verbose:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True)
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def _link_program(src: str, exe: str, extra: list[str], verbose: bool) -> None:
+    """A program on the library beside it (rpath $ORIGIN)."""
+    cmd = [_hipcc(), *common_flags(), *extra, "-o", exe + ".tmp", src, f"-L{os.path.dirname(exe)}", "-lvelox_hip",
+           "-Wl,-rpath,$ORIGIN"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(exe + ".tmp", exe)
+
+
+def build(verbose: bool = False) -> str:
+    _compile_library(LIB, [], verbose)
     runner_src = os.path.join(CSRC, "vx_runner_main.cpp")
     if os.path.exists(runner_src):
-        cmd = [hipcc, *common_flags(), "-o", RUNNER + ".tmp", runner_src, f"-L{LIBDIR}", "-lvelox_hip",
-               f"-Wl,-rpath,$ORIGIN"]
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        subprocess.run(cmd, check=True)
-        os.replace(RUNNER + ".tmp", RUNNER)
+        _link_program(runner_src, RUNNER, [], verbose)
     return LIB
+
+
+TIMELINE_DIR = os.path.join(LIBDIR, "timeline")
+
+
+def build_timeline(verbose: bool = False) -> str:
+    """The timeline build (-DVX_TIMELINE) of the library and its velox_hip_timeline program under
+    velox_amd/lib/timeline/: the single-sequence decode step's GEMV and attention workgroups stamp
+    s_memrealtime at their start, staging / first barrier and end. A measuring tool only: the
+    product library (build()) holds no stamps. Returns the program's path."""
+    lib = os.path.join(TIMELINE_DIR, "libvelox_hip.so")
+    _compile_library(lib, ["-DVX_TIMELINE"], verbose)
+    exe = os.path.join(TIMELINE_DIR, "velox_hip_timeline")
+    _link_program(os.path.join(CSRC, "vx_timeline_main.cpp"), exe, ["-DVX_TIMELINE"], verbose)
+    return exe
 
 
 # ---------------------------------------------------------------------------------------------
@@ -256,9 +281,13 @@ if __name__ == "__main__":
     ap.add_argument("--out", help="output directory (default velox_amd/lib/models/<Model>)")
     ap.add_argument("--max-seq-len", type=int, default=0)
     ap.add_argument("--no-runner", action="store_true")
+    ap.add_argument("--timeline", action="store_true",
+                    help="build the timeline build and velox_hip_timeline under velox_amd/lib/timeline/")
     ap.add_argument("-v", "--verbose", action="store_true")
     args = ap.parse_args()
-    if args.model:
+    if args.timeline:
+        print(build_timeline(verbose=args.verbose))
+    elif args.model:
         res = build_model(args.model, args.out, args.max_seq_len, not args.no_runner, args.verbose)
         for k in ("library", "runner"):
             if k in res:

@@ -103,6 +103,56 @@ VX_HD uint32_t vx_vslot(uint32_t r) { return 8u * ((r & 15u) >> 2) + 4u * (r >> 
 enum { VX_FMT_Q4 = 0, VX_FMT_F32 = 1, VX_FMT_F16 = 2, VX_FMT_G64 = 3 };
 constexpr uint32_t kVxFloatMaxK = 32768;  // fp32 activations of a float-row GEMV in LDS (128 KiB)
 
+// Timeline build (-DVX_TIMELINE; velox_amd.build --timeline): the decode step's GEMV and attention
+// launches stamp s_memrealtime (100 MHz) per workgroup into a host-set buffer, 8 words per workgroup
+// at tl + 8 (tl_slot + workgroup): [0] start, [1] activations staged (GEMV) or first barrier
+// (attention), [2] end, [3] attention's chunk loop done, [4] its merge barrier. The product build
+// has neither the fields nor the stamps.
+#ifdef VX_TIMELINE
+#define VX_TIMELINE_FIELDS \
+    unsigned long long* tl;  \
+    uint32_t tl_slot;
+#if defined(__HIP__)
+__device__ __forceinline__ unsigned long long& vx_tl_mark(int i) {
+    __shared__ unsigned long long m[5];
+    return m[i];
+}
+struct VxTimelineWg {
+    unsigned long long* e;
+    __device__ VxTimelineWg(unsigned long long* tl, uint32_t slot, uint32_t wg) : e(tl ? tl + 8ull * (slot + wg) : nullptr) {
+        if (threadIdx.x == 0) {
+            vx_tl_mark(0) = __builtin_amdgcn_s_memrealtime();
+            vx_tl_mark(1) = vx_tl_mark(3) = vx_tl_mark(4) = 0ull;
+        }
+    }
+    // every thread of the workgroup leaves through one (uniform) return
+    __device__ ~VxTimelineWg() {
+        __syncthreads();
+        if (e && threadIdx.x == 0) {
+            e[0] = vx_tl_mark(0);
+            e[1] = vx_tl_mark(1) ? vx_tl_mark(1) : vx_tl_mark(0);
+            e[2] = __builtin_amdgcn_s_memrealtime();
+            e[3] = vx_tl_mark(3);
+            e[4] = vx_tl_mark(4);
+        }
+    }
+};
+#define VX_TL_BEGIN(args, wg) VxTimelineWg vx_tl_wg_((args).tl, (args).tl_slot, (wg))
+#define VX_TL_MARK(i) \
+    do {                                                                    \
+        if (threadIdx.x == 0) vx_tl_mark(i) = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#endif
+#else
+#define VX_TIMELINE_FIELDS
+#define VX_TL_BEGIN(args, wg) \
+    do {                      \
+    } while (0)
+#define VX_TL_MARK(i) \
+    do {              \
+    } while (0)
+#endif
+
 struct VxMat {
     const uint4* codes;
     const uint16_t* scales;
@@ -137,6 +187,7 @@ struct VxGemvArgs {
     const float* part_o;
     const float* part_ml;
     uint32_t att_splits, att_d;
+    VX_TIMELINE_FIELDS
 };
 
 struct VxAttnArgs {
@@ -179,6 +230,7 @@ struct VxAttnArgs {
     // position. NULL: the row is read from `rope` at the position.
     const float2* rope_cur;
     uint32_t chunk;  // set by vx_launch_attention: positions per split, ceil(s_max / splits) rounded up to 32
+    VX_TIMELINE_FIELDS
 };
 
 // Batched (B <= 32 sequences) Q4_0 GEMM: Y[m][n] = sum_k X[m][k] W[n][k] for fp16 activations

@@ -357,6 +357,7 @@ __device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a) {
         for (int w = 0; w < W; ++w) t += red[w];
         inv_rms = 1.0f / sqrtf(t / (float)K + a.eps);
     }
+    VX_TL_MARK(1);
 
     // ---- stream: consume slot u, refill it with the item kU ahead, finish tiles on the fly ----
     float best_v = -INFINITY;
@@ -460,6 +461,7 @@ __device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a) {
 
 template <int S, int EPI, bool NORM, int GX, int SPL>
 __global__ __launch_bounds__(64 * kGemvWaves) void vx_gemv_q4_kernel(VxGemvArgs a) {
+    VX_TL_BEGIN(a, blockIdx.x);
     vx_gemv_tiled<VX_FMT_Q4, S, EPI, NORM, GX, SPL>(a);
 }
 

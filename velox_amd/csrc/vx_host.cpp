@@ -296,6 +296,21 @@ bool vx_shape_ok(const VeloxHipModelConfig& c) {
 
 }  // namespace
 
+#ifdef VX_TIMELINE
+// Timeline build: the buffer the single-sequence decode step's GEMV and attention launches stamp,
+// 1024 workgroup slots of 64 bytes per launch in launch order (see VX_TIMELINE_FIELDS).
+static unsigned long long* g_tl = nullptr;
+template <class T>
+void vx_tl_slot(T& args, uint32_t& n) {
+    args.tl = g_tl;
+    args.tl_slot = 1024u * n++;
+}
+extern "C" void velox_hip_timeline_set(unsigned long long* d_buf) { g_tl = d_buf; }
+#else
+template <class T>
+void vx_tl_slot(T&, uint32_t&) {}
+#endif
+
 extern "C" {
 
 void velox_hip_record_error(int status) {
@@ -1262,6 +1277,7 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
     at.scale = 1.0f / sqrtf((float)c.head_dim);
     at.active_mask = mask;
     at.partials_only = M->fused_merge ? 1u : 0u;
+    uint32_t tl_n = 0;
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         const VxLayerPlan& L = M->layers[l];
         VxGemvArgs g;
@@ -1272,9 +1288,11 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
         g.gain = vecp(L.attn_norm);
         g.bias = c.qkv_bias ? vecp(L.bias) : nullptr;
         g.y = qkv;
+        vx_tl_slot(g, tl_n);
         vx_record(vx_launch_gemv(vx_view(A, L.qkv), g, VX_EPI_STORE, M->max_wgs, st));
 
         at.kv = vx_kv(M, A, l, 0);
+        vx_tl_slot(at, tl_n);
         vx_record(vx_launch_attention(at, c.head_dim, st));
 
         std::memset(&g, 0, sizeof(g));
@@ -1288,6 +1306,7 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
         }
         g.res = h;
         g.y = h;
+        vx_tl_slot(g, tl_n);
         vx_record(vx_launch_gemv(vx_view(A, L.o), g, VX_EPI_RESID, M->max_wgs, st));
 
         std::memset(&g, 0, sizeof(g));
@@ -1296,6 +1315,7 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
         g.x = h;
         g.gain = vecp(L.mlp_norm);
         g.y = ffn;
+        vx_tl_slot(g, tl_n);
         vx_record(vx_launch_gemv(vx_view(A, L.gate_up), g, VX_EPI_SWIGLU, M->max_wgs, st));
 
         std::memset(&g, 0, sizeof(g));
@@ -1303,6 +1323,7 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
         g.x = ffn;
         g.res = h;
         g.y = h;
+        vx_tl_slot(g, tl_n);
         vx_record(vx_launch_gemv(vx_view(A, L.down), g, VX_EPI_RESID, M->max_wgs, st));
     }
     VxGemvArgs g;
@@ -1314,6 +1335,7 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
     g.y = (float*)(act + M->a_logits);
     g.cand_v = (float*)(act + M->a_cand_v);
     g.cand_i = (uint32_t*)(act + M->a_cand_i);
+    vx_tl_slot(g, tl_n);
     vx_record(vx_launch_gemv(vx_view(A, M->head), g, VX_EPI_ARGMAX, M->max_wgs, st));
     vx_record(vx_launch_argmax_finalize(g.cand_v, g.cand_i, vx_gemv_grid(M->head.n_tiles, M->max_wgs), state,
                                         A->host_pinned_ring, (const uint32_t*)(act + M->a_prompt),

@@ -191,6 +191,7 @@ constexpr size_t vx_attn_lds_bytes() {
 template <int D, int G, int W, bool PS, int R = 1, bool RC = false>
 __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     static_assert(!RC || (R == 1 && !PS), "the copied RoPE row serves the single-sequence decode step");
+    VX_TL_BEGIN(a, blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
     // (the active-mask test follows the first barrier: a branch here would wait for the kernel
     // arguments once for the mask and again for everything else)
     const bool active = (a.active_mask & 1ULL) != 0ULL;
@@ -357,6 +358,7 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
     }
     if (tid < D) vn_s[tid] = vx_f32_to_bf16_bits(vnew);
     __syncthreads();
+    VX_TL_MARK(1);
     // the step's mask (uniform) after the barrier: loads are not moved across it, so the kernel
     // arguments come in one batch and every load above is issued before the test
     if (!active) return;
@@ -447,6 +449,7 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
         if (ci + W < n_chunks) load_chunk(t0 + 32u * (ci + W));
     }
 
+    VX_TL_MARK(3);
     // ---- merge the waves (and the new position): per head the max m, weights 2^(m_w - m) ----
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
@@ -461,6 +464,7 @@ __global__ __launch_bounds__(64 * W) void vx_attn_kernel(VxAttnArgs a) {
             for (int i = 0; i < 4; ++i) o_s[(wave * HR + 4 * grp + i) * D + 16 * nb + col] = o_acc[nb][i];
     }
     __syncthreads();
+    VX_TL_MARK(4);
     for (int idx = tid; idx < GC * D; idx += NT) {
         const int h = idx / D, d = idx % D;  // column: head h % G of row h / G
         const uint32_t row = bq + (uint32_t)(h / G);
