@@ -353,7 +353,9 @@ int velox_hip_lm_head_argmax(const VeloxHipQ4Matrix* m, const float* d_x, const 
  * results as velox_hip_lm_head_argmax, but the per-workgroup candidates live in a fixed device
  * array of the library (512 candidates, 4 KiB per GPU, held until the process ends; EINVAL if a
  * matrix needed more), so the call allocates nothing and does not synchronize. Calls that overlap
- * on one GPU (concurrent streams or threads) share that array and race. */
+ * on one GPU (concurrent streams or threads) share that array and race. The first call on a device
+ * looks the array's address up (hipGetSymbolAddress, no stream work): make that first call eagerly,
+ * then the call can be captured into a HIP graph (it records kernel launches only) and replayed. */
 int velox_hip_lm_head_argmax_noalloc(const VeloxHipQ4Matrix* m, const float* d_x, const float* d_gain, float eps,
                                      float* d_logits, uint32_t* d_token, hipStream_t stream);
 /* Standalone two-stage argmax over n fp32 values (strict '>' lowest-index rule). */

@@ -1801,14 +1801,16 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
         rc = velox_hip_last_error();
     }
     // ring[pos & 1023] holds the argmax after position pos (velox_cuda_runner.cu:541-546). The host
-    // copies entries out before the device can overwrite them: whenever 1024 positions have run
-    // since the last copy (a stream synchronization per 1024 steps), and at the end.
+    // copies entries out before the device can overwrite them. Single steps: an event marks the end
+    // of every 512th position, and before launching the position that would overwrite an uncopied
+    // entry the host waits for the event 1024 positions back and copies those 512 entries: the
+    // stream keeps the ~512 steps queued behind it, so no drain stalls the device. Batched prefill
+    // pieces and the end synchronize the stream and copy what is left.
+    constexpr uint32_t kDrainChunk = VELOX_HIP_RING_SIZE / 2;
     uint32_t drained = base, next_pos = base, n_out = 0;
     bool first_seen = false;
-    auto drain = [&](uint32_t upto) {
-        if (upto <= drained) return;
-        const int e = (int)hipStreamSynchronize(st);
-        if (!rc) rc = e;
+    std::vector<std::pair<uint32_t, hipEvent_t>> marks;  // (position the event follows, event)
+    auto copy_out = [&](uint32_t upto) {
         for (uint32_t p = drained; p < upto; ++p) {
             const uint32_t t = A.host_pinned_ring[p & (VELOX_HIP_RING_SIZE - 1)];
             if (p == base + opt->prompt_len - 1) { rep->first_token = t; first_seen = true; }
@@ -1816,11 +1818,37 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
         }
         drained = upto;
     };
+    auto drain = [&](uint32_t upto) {
+        if (upto <= drained) return;
+        const int e = (int)hipStreamSynchronize(st);
+        if (!rc) rc = e;
+        copy_out(upto);
+    };
     auto one_step = [&]() {
-        if (next_pos - drained >= VELOX_HIP_RING_SIZE) drain(next_pos);
+        if (next_pos - drained >= VELOX_HIP_RING_SIZE) {
+            // positions [drained, drained + kDrainChunk) ended at the mark recorded after them
+            const uint32_t upto = drained + kDrainChunk;
+            auto it = std::find_if(marks.begin(), marks.end(), [&](const auto& m) { return m.first == upto; });
+            if (it == marks.end()) {
+                drain(next_pos);
+            } else {
+                const int e = (int)hipEventSynchronize(it->second);
+                if (!rc) rc = e;
+                copy_out(upto);
+                (void)hipEventDestroy(it->second);
+                marks.erase(it);
+            }
+        }
         if (exec) vx_record(hipGraphLaunch(exec, st));
         else launch_step();
         ++next_pos;
+        if ((next_pos - drained) % kDrainChunk == 0) {
+            hipEvent_t ev = nullptr;
+            if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) == hipSuccess) {
+                if (hipEventRecord(ev, st) == hipSuccess) marks.emplace_back(next_pos, ev);
+                else (void)hipEventDestroy(ev);
+            }
+        }
     };
     if (!rc) {
         hipEventRecord(e0, st);
@@ -1852,6 +1880,8 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
         rep->wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - w0).count();
         if (!rc) rc = velox_hip_last_error();
     }
+    for (auto& m : marks) (void)hipEventDestroy(m.second);
+    marks.clear();
     if (!rc) {
         drain(next_pos);
         float ms_p = 0.f, ms_d = 0.f;
