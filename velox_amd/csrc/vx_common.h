@@ -301,6 +301,13 @@ struct VxF8GemmArgs {
     float eps;
     uint64_t w_gstride, s_gstride, x_gstride, y_gstride, pstride;
     uint64_t active_mask;
+    // != nullptr (batch 1, fp32 x, ksplit 1, no gain): group g's activation row is the LSE merge of
+    // its m_splits split partials -- fp16 o_j / l_j at m_part_o[(g m_splits + j) n_kt 64 + c] and
+    // (m_j, l_j) at m_part_ml[2 (g m_splits + j)] -- in split order, as vx_mla_merge_kernel forms ctx;
+    // x is then unused
+    const uint16_t* m_part_o;
+    const float* m_part_ml;
+    uint32_t m_splits;
 };
 
 // vx_mla.hip launchers (absorbed MLA layer), used by vx_mla_host.cpp.

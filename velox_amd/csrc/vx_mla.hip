@@ -231,6 +231,51 @@ __global__ __launch_bounds__(64 * kFWaves) void vx_f8gemm_kernel(VxF8GemmArgs a)
 // the deeper queue gains).
 constexpr int kFGWaves = 8;
 
+// The activation row of group g as the LSE merge of its split partials (VxF8GemmArgs::m_part_o):
+// the group's splits x lr fp16 partials come into LDS with 16-byte loads (all in flight at once),
+// then thread c sums column c over the splits in split order with vx_mla_merge_kernel's weights and
+// operations, so the fp32 context before its fp16 rounding is the one that kernel writes; after a
+// barrier the fp16 row goes to the start of LDS, where the GEMV reads its activations. The
+// launcher admits lr <= the workgroup's threads and splits x lr x 2 bytes <= 64 KiB.
+__device__ __forceinline__ void vm_merge_stage(const VxF8GemmArgs& a, uint32_t g, unsigned char* smem) {
+    __shared__ float s_w[64];
+    const uint32_t lr = a.n_kt * 64u, splits = a.m_splits, tid = threadIdx.x, nt = blockDim.x;
+    const uint4* po = (const uint4*)(a.m_part_o + (size_t)g * splits * lr);
+    uint4* stage = (uint4*)smem;
+    const uint32_t n16 = splits * lr / 8u;  // 16-byte units
+    constexpr int U = 8;  // units per thread per pass: 64 KiB over 512 threads in one pass
+    for (uint32_t i0 = 0; i0 < n16; i0 += U * nt) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = po[min(i0 + (uint32_t)u * nt + tid, n16 - 1u)];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (i0 + (uint32_t)u * nt + tid < n16) stage[i0 + (uint32_t)u * nt + tid] = v[u];
+    }
+    if (tid < 64u) {
+        const float* pml = a.m_part_ml + (size_t)g * splits * 2u;
+        const uint32_t j = tid;
+        const float mj = j < splits ? pml[2 * j] : -INFINITY;
+        const float lj = j < splits ? pml[2 * j + 1] : 0.0f;
+        float M = mj;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+        const float wj = mj == -INFINITY ? 0.0f : vm_exp2(mj - M);
+        float Ls = lj * wj;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) Ls += __shfl_xor(Ls, off);
+        s_w[j] = Ls > 0.0f ? wj * lj / Ls : 0.0f;  // the partials are o_j / l_j
+    }
+    __syncthreads();
+    const uint16_t* st16 = (const uint16_t*)smem;
+    float acc = 0.0f;
+    if (tid < lr)
+        for (uint32_t j = 0; j < splits; ++j)
+            acc = fmaf(s_w[j], (float)__builtin_bit_cast(_Float16, st16[(size_t)j * lr + tid]), acc);
+    __syncthreads();  // every column read before the row overwrites the first split's
+    if (tid < lr) ((uint16_t*)smem)[tid] = __builtin_bit_cast(uint16_t, (_Float16)acc);
+}
+
 template <int KW, bool XF32>
 __global__ __launch_bounds__(64 * kFGWaves) void vx_f8gemv_kernel(VxF8GemmArgs a) {
     extern __shared__ __align__(16) unsigned char vm_smem[];
@@ -276,7 +321,13 @@ __global__ __launch_bounds__(64 * kFGWaves) void vx_f8gemv_kernel(VxF8GemmArgs a
         }
     }
     const uint32_t n8 = (kt1 - kt0) * 8u;
-    for (uint32_t i = (uint32_t)tid; i < n8; i += 64u * kFGWaves) {
+    if constexpr (XF32) {
+        if (a.m_part_o) {
+            vm_merge_stage(a, g, vm_smem);
+            __syncthreads();
+        }
+    }
+    for (uint32_t i = (uint32_t)tid; i < n8 && !(XF32 && a.m_part_o); i += 64u * kFGWaves) {
         const size_t e = g * a.x_gstride + (size_t)kt0 * 64u + 8u * i;
         if constexpr (XF32) {
             float4 lo = *(const float4*)((const float*)a.x + e), hi = *(const float4*)((const float*)a.x + e + 4);
@@ -475,12 +526,17 @@ hipError_t vx_launch_f8gemm(const VxF8GemmArgs& a, uint32_t groups, hipStream_t 
     if ((a.y16 != nullptr) == (a.y != nullptr) || (a.y16 && a.ksplit != 1u)) return hipErrorInvalidValue;
     if (a.add_y && (a.batch != 1u || a.ksplit != 1u || a.y16)) return hipErrorInvalidValue;
     if (a.gain && (a.batch != 1u || !a.x_f32 || a.x_gstride)) return hipErrorInvalidValue;
+    if (a.m_part_o && (a.batch != 1u || !a.x_f32 || a.ksplit != 1u || a.gain || !a.m_part_ml || a.m_splits == 0 ||
+                       a.m_splits > 64u || a.n_kt * 64u > 64u * kFGWaves ||
+                       (uint64_t)a.m_splits * a.n_kt * 128u > 64u * 1024u))
+        return hipErrorInvalidValue;
     // up to 16 sequences: activations staged in LDS (one sequence: the GEMV, else the MFMA form), if
     // the longest split's fp16 activations fit 64 KB (16 padded rows for the MFMA form; at least the
     // waves' sums that reuse the space). Waves per row tile: the fewest giving >= 256 workgroups, as
     // long as each wave keeps >= 2 k-tiles.
     const size_t kspan = (a.n_kt + a.ksplit - 1u) / a.ksplit;  // k-tiles of the longest split
     size_t lds = a.batch == 1u ? kspan * 128u : 16u * (kspan * 128u + 16u);
+    if (a.m_part_o) lds = (size_t)a.m_splits * a.n_kt * 128u;  // the staged partials (the row reuses them)
     const size_t red = a.batch == 1u ? (size_t)kFGWaves * 16u * 4u : (size_t)kFGWaves * 64u * 16u;
     if (lds < red) lds = red;
     if (a.batch == 1u && lds > 64u * 1024u) return hipErrorInvalidValue;
@@ -933,7 +989,7 @@ __global__ __launch_bounds__(128) void vx_mla_merge_kernel(const uint16_t* part_
         if (j0) load(j0);
 #pragma unroll
         for (uint32_t u = 0; u < (uint32_t)NL; ++u)
-            if (j0 + u < splits) acc += s_w[j0 + u] * v[u];
+            if (j0 + u < splits) acc = fmaf(s_w[j0 + u], v[u], acc);
     }
     if (d < lr) ctx[bh * lr + d] = acc;
 }

@@ -494,7 +494,8 @@ void vm_layer(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, boo
     uint16_t* cache = vm_cache(m, layer);
     auto gemm = [&](const VmF8Plan& p, const void* x, uint32_t ldx, uint64_t x_gstride, uint32_t x_f32, float* y,
                     uint32_t ldy, uint64_t y_gstride, uint32_t ksplit, uint64_t pstride, uint16_t* y16 = nullptr,
-                    uint32_t add_y = 0, const float* gain = nullptr) {
+                    uint32_t add_y = 0, const float* gain = nullptr, const uint16_t* m_part_o = nullptr,
+                    const float* m_part_ml = nullptr, uint32_t m_splits = 0) {
         VxF8GemmArgs g;
         std::memset(&g, 0, sizeof(g));
         g.codes = codes + p.code_off / 16;
@@ -519,6 +520,9 @@ void vm_layer(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, boo
         g.gain = gain;
         g.eps = c.rms_norm_eps;
         g.active_mask = mask;
+        g.m_part_o = m_part_o;
+        g.m_part_ml = m_part_ml;
+        g.m_splits = m_splits;
         vx_record_error(vx_launch_f8gemm(g, p.groups, st));
     };
     float* parts_o = vm_act(m, m->a_parts_o);
@@ -594,11 +598,18 @@ void vm_layer(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, boo
         a.active_mask = mask;
         vx_record_error(vx_launch_mla_attn(a, m->lr, m->dr, batch, st));
     }
-    vx_record_error(vx_launch_mla_merge(po, pml, m->nh, m->splits, m->lr, ctx, batch, mask, st));
     // 8. o_h = W_uv[h] ctx_h; 9. W_o [o_h], split over K; 10. residual
-    // o_h goes to W_o as fp16, the rounding the GEMM applies to fp32 activations: half the bytes
+    // o_h goes to W_o as fp16, the rounding the GEMM applies to fp32 activations: half the bytes.
+    // One sequence: the W_uv workgroups of head h merge its split partials into ctx_h themselves
+    // (one launch less); several: the merge kernel writes ctx first.
     uint16_t* oh16 = (uint16_t*)vm_act(m, m->a_oh);
-    gemm(L.uv, ctx, m->nh * m->lr, m->lr, 1, nullptr, m->nh * m->dv, m->dv, 1, 0, oh16);
+    if (direct) {
+        gemm(L.uv, ctx, m->nh * m->lr, m->lr, 1, nullptr, m->nh * m->dv, m->dv, 1, 0, oh16, 0, nullptr, po, pml,
+             m->splits);
+    } else {
+        vx_record_error(vx_launch_mla_merge(po, pml, m->nh, m->splits, m->lr, ctx, batch, mask, st));
+        gemm(L.uv, ctx, m->nh * m->lr, m->lr, 1, nullptr, m->nh * m->dv, m->dv, 1, 0, oh16);
+    }
     if (direct) {
         gemm(L.o, oh16, m->nh * m->dv, 0, 0, h, m->H, 0, 1, 0, nullptr, 1);
         return;
