@@ -216,6 +216,17 @@ void velox_hip_prefill(VeloxHipArena* ctx, uint32_t token_in, size_t step, uint6
                        hipStream_t stream);
 int velox_hip_last_error(void);
 
+/* The single-sequence step runs QKV and attention as one launch per layer where the plan allows it
+ * (Q4_0, head size 128, KV heads a multiple of 8, 4 or 8 q heads per KV head, up to 2048 positions,
+ * the planner's own split count) and the device deals workgroup b of a launch to XCD (b + o) % 8, o
+ * fixed per launch (checked when the arena is created or bound). No counterpart in the reference (whose step always launches
+ * the two apart): set_fused_attention(0) makes steps recorded afterwards use the two launches
+ * (process-wide; 1 restores the default). fused_attention_status reports the splits per KV head
+ * the arena's steps use fused (0: two launches) and the fused launches' error bits (1: a KV head's
+ * workgroups ran on two XCDs, 2: a wait expired; 0 after correct steps; synchronous). */
+void velox_hip_set_fused_attention(int enable);
+int velox_hip_fused_attention_status(const VeloxHipArena* a, uint32_t* splits_used, uint32_t* errors);
+
 /* 0 when the arena's plan has `want`'s dimensions -- vocabulary, hidden, FFN, heads, KV heads, head
  * size, QKV bias, head tying, eps, theta, and depth unless want->num_layers is 0 -- else EINVAL
  * (the plan's name, context, batch rows and weight format are not compared). */

@@ -125,6 +125,8 @@ _U32, _U64, _F, _I = C.c_uint32, C.c_uint64, C.c_float, C.c_int
 
 _SIGS = {
     "velox_hip_last_error": (_I, []),
+    "velox_hip_set_fused_attention": (None, [_I]),
+    "velox_hip_fused_attention_status": (_I, [C.POINTER(Arena), C.POINTER(_U32), C.POINTER(_U32)]),
     "velox_hip_builtin_config": (_I, [C.c_char_p, _U32, C.POINTER(ModelConfig)]),
     "velox_hip_vlx_config": (_I, [C.c_char_p, _U32, C.POINTER(ModelConfig), C.POINTER(VlxTarget)]),
     "velox_hip_vlx_load": (_I, [C.c_char_p, _U32, C.POINTER(ModelConfig), C.POINTER(VlxTarget)]),

@@ -23,7 +23,7 @@ LIB = os.path.join(LIBDIR, "libvelox_hip.so")
 RUNNER = os.path.join(LIBDIR, "velox_hip_runner")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["vx_kernels.hip", "vx_gemv_g64.hip", "vx_gemv_f.hip", "vx_batch.hip", "vx_mgemm.hip", "vx_mla.hip", "vx_noalloc.hip", "vx_host.cpp", "vx_mla_host.cpp", "vx_gguf.cpp", "vx_safetensors.cpp", "vx_vlx.cpp", "vx_runner.cpp"]
+HIP_SOURCES = ["vx_kernels.hip", "vx_gemv_g64.hip", "vx_gemv_f.hip", "vx_batch.hip", "vx_mgemm.hip", "vx_mla.hip", "vx_noalloc.hip", "vx_qkv_attn.hip", "vx_host.cpp", "vx_mla_host.cpp", "vx_gguf.cpp", "vx_safetensors.cpp", "vx_vlx.cpp", "vx_runner.cpp"]
 
 
 def _hipcc() -> str:

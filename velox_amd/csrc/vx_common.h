@@ -233,6 +233,21 @@ struct VxAttnArgs {
     VX_TIMELINE_FIELDS
 };
 
+// The single-sequence decode step's QKV GEMV and attention in one launch (vx_qkv_attn.hip): the
+// GEMV's arguments (its own grid fields set by the launcher), the attention's (splits = A splits
+// per KV head), and the synchronisation words: [g * 64] (64-bit) workgroups of head g counted in
+// (low 8 bits; 7 bits per XCD above), [(hkv + g) * 64] its splits past their wait, [2 hkv * 64]
+// error bits (1: a head's workgroups on two XCDs, 2: an expired wait), zero between launches.
+struct VxQkvAttnArgs {
+    VxGemvArgs g;
+    VxAttnArgs at;
+    uint32_t* sync;
+    uint32_t na, p;               // attention workgroups (hkv x A); GEMV workgroups per KV head
+    uint32_t tq, tk;              // row tiles of a KV head's q heads, and of its k (= of its v)
+    uint32_t k_base, v_base;      // first row tile of the k heads, of the v heads
+};
+constexpr uint32_t kVxQkvSyncWords(uint32_t hkv) { return (2u * hkv + 1u) * 64u; }
+
 // Batched (B <= 32 sequences) Q4_0 GEMM: Y[m][n] = sum_k X[m][k] W[n][k] for fp16 activations
 // X (row stride ldx elements), through MFMA, with the same epilogues as the GEMV.
 struct VxBGemmArgs {
@@ -325,6 +340,12 @@ hipError_t vx_launch_gemv(const VxMat& m, const VxGemvArgs& a, int epi, uint32_t
 // on `wgs` workgroups (vx_gemv_grid of the matrix's tiles).
 hipError_t vx_launch_gemv_f(const VxMat& m, const VxGemvArgs& a, int epi, uint32_t wgs, hipStream_t st);
 hipError_t vx_launch_attention(const VxAttnArgs& a, uint32_t d, hipStream_t st);
+// vx_qkv_attn.hip: whether matrix m (the fused [q; k; v] rows) and the head shape take the fused
+// QKV + attention launch; the launch with p GEMV workgroups per KV head; and the device check that
+// workgroup b of a launch runs on XCD b % 8 (synchronous, once per device).
+bool vx_qkv_attn_supported(const VxMat& m, uint32_t hq, uint32_t hkv, uint32_t d);
+hipError_t vx_launch_qkv_attn(const VxMat& m, const VxQkvAttnArgs& f, uint32_t p, hipStream_t st);
+bool vx_xcd_roundrobin_ok();
 // vx_gemv_g64.hip: the reference's group-64 format (quant_mode 2) in the tiled layout -- the GEMV
 // that vx_launch_gemv runs for VX_FMT_G64 matrices, fp32 rows (device) or seeded weights converted
 // into rows [row0, row0 + rows) of part pair_part, and the reference's own packed output layout

@@ -138,8 +138,16 @@ __device__ __forceinline__ float vx_tiled_weight(const uint32_t (&dw)[4], int e,
 // vx_argmax_finalize_kernel (a release fence per workgroup costs a full L2 write-back on gfx950).
 constexpr int kGemvWaves = 8, kGemvU = 4;
 
-template <int FMT, int S, int EPI, bool NORM, int GX, int SPL>
-__device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a) {
+// Wave tile t of a workgroup's block -> tile of the matrix (the plain GEMV: the same index).
+struct VxTileIdentity {
+    __device__ __forceinline__ uint32_t operator()(uint32_t t) const { return t; }
+};
+
+// bid: the workgroup's index in the GEMV's own grid (its block of tiles); tmap: the block's tile
+// numbering -> the matrix's row tiles (vx_qkv_attn.hip deals one KV head's q/k/v tiles to the
+// workgroups of one XCD)
+template <int FMT, int S, int EPI, bool NORM, int GX, int SPL, class TM = VxTileIdentity>
+__device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a, uint32_t bid = blockIdx.x, TM tmap = TM()) {
     static_assert(FMT == VX_FMT_Q4 || FMT == VX_FMT_G64, "tiled 4-bit formats");
     static_assert(FMT != VX_FMT_G64 || S % 2 == 0, "a group-64 pair of blocks shares one row's lanes");
     constexpr bool G64 = FMT == VX_FMT_G64;
@@ -161,7 +169,6 @@ __device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a) {
     // workgroup blocks: workgroup b owns q or q + 1 consecutive tiles (the launcher's split of n_tiles
     // over the grid, no device division), dealt to its W waves round-robin, so every workgroup (every
     // CU) streams the same number of tiles to within one
-    const uint32_t bid = blockIdx.x;
     const uint32_t b0 = bid * a.wg_q + min(bid, a.wg_r);
     const uint32_t b1 = b0 + a.wg_q + (bid < a.wg_r ? 1u : 0u);
     const uint32_t first = b0 + (uint32_t)wave, step = (uint32_t)W;
@@ -169,8 +176,8 @@ __device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a) {
     const uint32_t total = my_tiles * n_iter;
 
     auto row_of = [&](uint32_t t) -> uint32_t {
-        if constexpr (EPI == VX_EPI_SWIGLU) return t * (R / 2) + (r % (R / 2));  // logical j of gate/up
-        else return t * R + r;
+        if constexpr (EPI == VX_EPI_SWIGLU) return tmap(t) * (R / 2) + (r % (R / 2));  // logical j of gate/up
+        else return tmap(t) * R + r;
     };
 
     // ---- activations (and the RMSNorm gain) into registers, before any weight load ----
@@ -211,12 +218,12 @@ __device__ __forceinline__ void vx_gemv_tiled(const VxGemvArgs& a) {
     const uint32_t lane16 = (uint32_t)lane * 16u, lane2 = (uint32_t)lane * 2u;
     vx_u32x4 buf[kU];
     uint32_t sbuf[kU];
-    uint32_t nt = 0, ni = 0, nslot = first * n_iter;  // next item: tile index, iteration, 64-lane slot
+    uint32_t nt = 0, ni = 0, nslot = tmap(first) * n_iter;  // next item: tile index, iteration, 64-lane slot
     auto advance = [&]() {
         if (++ni == n_iter) {
             ni = 0;
             ++nt;
-            nslot = (first + nt * step) * n_iter;
+            nslot = tmap(first + nt * step) * n_iter;
         } else {
             ++nslot;
         }

@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -88,6 +89,11 @@ struct VeloxHipModel {
     uint64_t a_cand_v = 0, a_cand_i = 0;
     uint32_t splits = 1, max_wgs = 2048, s_cap = 0;
     bool fused_merge = false;  // o_proj merges the attention partials
+    // the single-sequence step's fused QKV + attention launch (vx_qkv_attn.hip), where the plan
+    // allows it: fused_splits > 0 attention splits per KV head, fused_p GEMV workgroups per KV head,
+    // and its synchronisation words at a_fsync
+    uint32_t fused_splits = 0, fused_p = 0;
+    uint64_t a_fsync = 0;
     // batched decode (max_batch > 1): per-sequence states, prompts, fp32 residuals, two fp16 GEMM
     // operands, q/k/v, attention partials, logits and LM-head candidates, sequence-major
     uint32_t batch = 1, xw = 0, head_bwgs = 0;
@@ -115,6 +121,7 @@ namespace {
 struct VxArenaRec {
     const uint8_t* key = nullptr;   // weight_arena
     const VeloxHipModel* model = nullptr;
+    bool xcd_rr = false;            // the device deals workgroup b to XCD b % 8 (fused QKV + attention)
     uint8_t* base = nullptr;        // the one device allocation (owned arenas), else nullptr
     uint32_t* ring = nullptr;       // the mapped host ring (owned arenas), else nullptr
     uint32_t staged_plen = 0;       // prompt length of the last velox_hip_set_prompt
@@ -128,13 +135,19 @@ VxArenaRec* vx_rec_locked(const uint8_t* key) {
     return nullptr;
 }
 
-// The plan `a` was created or bound with; nullptr for an unknown arena.
-const VeloxHipModel* vx_model(const VeloxHipArena* a) {
+// The plan `a` was created or bound with; nullptr for an unknown arena. xcd_rr (optional): whether
+// its device takes the fused QKV + attention launch.
+const VeloxHipModel* vx_model(const VeloxHipArena* a, bool* xcd_rr = nullptr) {
+    if (xcd_rr) *xcd_rr = false;
     if (!a || !a->weight_arena) return nullptr;
     std::lock_guard<std::mutex> lock(g_arena_mu);
     const VxArenaRec* r = vx_rec_locked(a->weight_arena);
+    if (r && xcd_rr) *xcd_rr = r->xcd_rr;
     return r ? r->model : nullptr;
 }
+
+// Process-wide switch of the fused QKV + attention launch (velox_hip_set_fused_attention).
+std::atomic<int> g_fused_attention{1};
 
 // Lanes per row S: the largest of {32, 16, 8, 4} wasting at most 1/32 of a row's blocks, else the
 // one wasting least. Padded blocks are zero and are streamed with the rest, so waste costs
@@ -317,6 +330,24 @@ void velox_hip_record_error(int status) {
     if (!g_last_error) g_last_error = status;
 }
 
+void velox_hip_set_fused_attention(int enable) { g_fused_attention.store(enable ? 1 : 0); }
+
+int velox_hip_fused_attention_status(const VeloxHipArena* a, uint32_t* used, uint32_t* errors) {
+    bool xcd_rr = false;
+    const VeloxHipModel* M = vx_model(a, &xcd_rr);
+    if (!M) return VELOX_HIP_EINVAL;
+    const bool on = M->fused_splits && xcd_rr && g_fused_attention.load();
+    if (used) *used = on ? M->fused_splits : 0u;
+    if (errors) {
+        *errors = 0;
+        if (M->fused_splits) {
+            const uint32_t* w = (const uint32_t*)(a->activation_arena + M->a_fsync) + 2u * M->cfg.num_kv_heads * 64u;
+            if (hipMemcpy(errors, w, 4, hipMemcpyDeviceToHost) != hipSuccess) return VELOX_HIP_EINVAL;
+        }
+    }
+    return VELOX_HIP_OK;
+}
+
 int velox_hip_last_error(void) {
     const int e = g_last_error;
     g_last_error = 0;
@@ -414,6 +445,7 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
     // longer contexts use 256-position splits and the merge kernel. (Llama-3-8B at 385 positions,
     // MFMA attention, measured: 1 split 702.6 tok/s, 2: 712.7, 4: 707.4, 8: 690.3.)
     uint32_t splits = c.attn_splits;
+    const bool auto_splits = splits == 0;
     if (!splits) {
         if (c.max_seq_len <= 1024) {
             const uint32_t want = (c.max_seq_len + 255) / 256;
@@ -434,6 +466,33 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
     M->cfg.attn_splits = splits;  // reported by velox_hip_model_config
     const uint32_t o_groups_per_thread = (qd / 8 + 511) / 512;
     M->fused_merge = (splits == 1 || splits == 2 || splits == 4 || splits == 8) && o_groups_per_thread <= 4;
+    // The fused QKV + attention launch: every KV head's q/k/v rows and its A attention splits on one
+    // XCD, the splits' partials merged by o_proj (A of 4 up to 512 positions: each wave pair takes one
+    // 32-position chunk at the 133-383 positions of the Llama-3-8B bench; 8 up to 2048). Only with the
+    // planner's own split count (an explicit attn_splits keeps the separate attention kernel).
+    if (auto_splits && c.max_seq_len <= 2048 && o_groups_per_thread <= 4) {
+        VxMat qm;
+        std::memset(&qm, 0, sizeof(qm));
+        const VxMatPlan& q0 = M->layers.empty() ? M->embed : M->layers[0].qkv;
+        qm.n = q0.n;
+        qm.k = q0.k;
+        qm.s = q0.s;
+        qm.n_tiles = q0.n_tiles;
+        qm.n_iter = q0.n_iter;
+        qm.paired = q0.paired;
+        qm.fmt = q0.fmt;
+        if (!M->layers.empty() && vx_qkv_attn_supported(qm, c.num_heads, c.num_kv_heads, D)) {
+            const uint32_t A = c.max_seq_len <= 512 ? 4u : 8u;
+            const uint32_t R = 64u / qm.s, th = (c.num_heads / c.num_kv_heads + 2u) * D / R;
+            // one 8-wave tile per GEMV wave, all workgroups within one round (two per CU)
+            uint32_t P = (th + 7u) / 8u;
+            const uint32_t cap = 512u / c.num_kv_heads - A;
+            if (P > cap) P = cap;
+            M->fused_splits = A;
+            M->fused_p = P;
+        }
+    }
+    const uint32_t part_splits = M->fused_splits > splits ? M->fused_splits : splits;
     M->max_wgs = vx_gemv_max_wgs_default();
 
     uint64_t ac = 0;
@@ -450,8 +509,9 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
     M->a_rope_cur = take((uint64_t)D / 2 * 8);
     M->a_act = take((uint64_t)F * 4);
     M->a_logits = take((uint64_t)c.vocab_size * 4);
-    M->a_part_o = take((uint64_t)c.num_heads * splits * D * 4);
-    M->a_part_ml = take((uint64_t)c.num_heads * splits * 2 * 4);
+    M->a_part_o = take((uint64_t)c.num_heads * part_splits * D * 4);
+    M->a_part_ml = take((uint64_t)c.num_heads * part_splits * 2 * 4);
+    if (M->fused_splits) M->a_fsync = take((uint64_t)kVxQkvSyncWords(c.num_kv_heads) * 4);
     M->a_cand_v = take((uint64_t)65536 * 4);
     M->a_cand_i = take((uint64_t)65536 * 4);
     M->rows = M->batch;
@@ -572,11 +632,14 @@ hipError_t vx_arena_init(const VeloxHipModel* m, const VeloxHipArena* a) {
 }
 
 int vx_register(const VeloxHipModel* m, const VeloxHipArena* a, uint8_t* base, uint32_t* ring) {
+    // (a device check with launches of its own: before the registry's lock)
+    const bool xcd_rr = m->fused_splits ? vx_xcd_roundrobin_ok() : false;
     std::lock_guard<std::mutex> lock(g_arena_mu);
     if (vx_rec_locked(a->weight_arena)) return VELOX_HIP_EINVAL;  // already an arena
     VxArenaRec r;
     r.key = a->weight_arena;
     r.model = m;
+    r.xcd_rr = xcd_rr;
     r.base = base;
     r.ring = ring;
     g_arenas.push_back(r);
@@ -1244,8 +1307,12 @@ int velox_hip_prefill_batch(VeloxHipArena* A, uint64_t pos0, uint32_t n_tokens, 
 // down+res] -> norm + LM head + argmax (+ ring + state advance). 2 + 5L launches.
 // ---------------------------------------------------------------------------------------------
 void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st) {
-    const VeloxHipModel* M = vx_model(A);
+    bool xcd_rr = false;
+    const VeloxHipModel* M = vx_model(A, &xcd_rr);
     if (!M) { if (!g_last_error) g_last_error = VELOX_HIP_EINVAL; return; }
+    // QKV and attention in one launch per layer (vx_qkv_attn.hip)
+    const bool fused = M->fused_splits && xcd_rr && g_fused_attention.load(std::memory_order_relaxed);
+    const uint32_t att_splits = fused ? M->fused_splits : M->splits;
     const VeloxHipModelConfig& c = M->cfg;
     uint8_t* act = A->activation_arena;
     const float* nrm = (const float*)A->norm_weight_arena;
@@ -1273,7 +1340,7 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
     at.hkv = c.num_kv_heads;
     at.s_max = c.max_seq_len;
     at.s_cap = M->s_cap;
-    at.splits = M->splits;
+    at.splits = att_splits;
     at.scale = 1.0f / sqrtf((float)c.head_dim);
     at.active_mask = mask;
     at.partials_only = M->fused_merge ? 1u : 0u;
@@ -1288,20 +1355,29 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
         g.gain = vecp(L.attn_norm);
         g.bias = c.qkv_bias ? vecp(L.bias) : nullptr;
         g.y = qkv;
-        vx_tl_slot(g, tl_n);
-        vx_record(vx_launch_gemv(vx_view(A, L.qkv), g, VX_EPI_STORE, M->max_wgs, st));
-
         at.kv = vx_kv(M, A, l, 0);
-        vx_tl_slot(at, tl_n);
-        vx_record(vx_launch_attention(at, c.head_dim, st));
+        if (fused) {
+            VxQkvAttnArgs f;
+            std::memset(&f, 0, sizeof(f));
+            f.g = g;
+            f.at = at;
+            f.sync = (uint32_t*)(act + M->a_fsync);
+            vx_tl_slot(f.g, tl_n);
+            vx_record(vx_launch_qkv_attn(vx_view(A, L.qkv), f, M->fused_p, st));
+        } else {
+            vx_tl_slot(g, tl_n);
+            vx_record(vx_launch_gemv(vx_view(A, L.qkv), g, VX_EPI_STORE, M->max_wgs, st));
+            vx_tl_slot(at, tl_n);
+            vx_record(vx_launch_attention(at, c.head_dim, st));
+        }
 
         std::memset(&g, 0, sizeof(g));
         g.active_mask = mask;
         g.x = attn;
-        if (M->fused_merge) {
+        if (fused || M->fused_merge) {
             g.part_o = at.part_o;
             g.part_ml = at.part_ml;
-            g.att_splits = M->splits;
+            g.att_splits = att_splits;
             g.att_d = c.head_dim;
         }
         g.res = h;

@@ -57,7 +57,12 @@ int main(int argc, char** argv) {
     velox_hip_synthesize_model(&A, 1234, 0.02f, 0.0f, st);
     for (uint32_t l = 0; l < cfg.num_layers; ++l) velox_hip_fill_kv(&A, l, pos, 7, 1.0f, st);
     velox_hip_set_state(&A, pos, 17, st);
-    const size_t per_layer = 5, nlaunch = per_layer * cfg.num_layers + 1, slots = nlaunch * 1024;
+    // the fused QKV + attention launch (one per layer) where the step uses it: its GEMV and attention
+    // workgroups are tabulated apart (the first na workgroups attend)
+    uint32_t fsplits = 0, ferr = 0;
+    if (velox_hip_fused_attention_status(&A, &fsplits, &ferr)) return fail("fused_attention_status");
+    const size_t na = (size_t)fsplits * cfg.num_kv_heads;
+    const size_t per_layer = fsplits ? 4 : 5, nlaunch = per_layer * cfg.num_layers + 1, slots = nlaunch * 1024;
     unsigned long long* tl = nullptr;
     if (hipMalloc(&tl, slots * 64) != hipSuccess || hipMemset(tl, 0, slots * 64) != hipSuccess) return 1;
     velox_hip_timeline_set(tl);
@@ -83,7 +88,14 @@ int main(int argc, char** argv) {
 
     std::printf("model %s, position %u: step %.1f us (event-timed mean of %d graph replays; the stamps are the last "
                 "replay's)\n", model.c_str(), pos, ms * 1000.0 / reps, reps);
+    // kinds: 0 qkv (GEMV workgroups of the fused launch), 1 attn (its attention workgroups), 2 o_proj,
+    // 3 gate_up, 4 down, 5 lm_head
     const char* names[6] = {"qkv", "attn", "o_proj", "gate_up", "down", "lm_head"};
+    if (fsplits) {
+        names[0] = "qkv|f";
+        names[1] = "attn|f";
+        std::printf("fused QKV + attention: %u splits per KV head (%zu attention workgroups per launch)\n", fsplits, na);
+    }
     unsigned long long base = ~0ull;
     for (size_t i = 0; i < slots; ++i)
         if (h[8 * i]) base = std::min(base, h[8 * i]);
@@ -95,11 +107,16 @@ int main(int argc, char** argv) {
     std::printf("\nlayer 0 and the head (us from the step's first stamp):\n");
     std::printf("%-8s %5s %8s %8s %6s %6s %9s %7s %7s %8s %8s\n", "launch", "wgs", "start", "end", "span", "gap",
                 "prologue", "rest", "wg", "1st_end", "last_st");
-    for (size_t L = 0; L < nlaunch; ++L) {
+    // (launch, part): part 1 of a fused launch is its attention workgroups
+    for (size_t LP = 0; LP < 2 * nlaunch; ++LP) {
+        const size_t L = LP / 2, part = LP % 2;
+        const bool fused_launch = fsplits && L < nlaunch - 1 && L % per_layer == 0;
+        if (part == 1 && !fused_launch) continue;
         std::vector<double> t0, t1, t2, t3, t4;
         for (size_t b = 0; b < 1024; ++b) {
             const unsigned long long* e = &h[8 * (L * 1024 + b)];
             if (!e[0]) continue;
+            if (fused_launch && (b < na) != (part == 1)) continue;
             t0.push_back((double)(e[0] - base) * 0.01);
             t1.push_back((double)(e[1] - base) * 0.01);
             t2.push_back((double)(e[2] - base) * 0.01);
@@ -107,7 +124,7 @@ int main(int argc, char** argv) {
             t4.push_back(e[4] ? (double)(e[4] - e[0]) * 0.01 : 0.0);
         }
         if (t0.empty()) continue;
-        const int kind = L == nlaunch - 1 ? 5 : (int)(L % per_layer);
+        const int kind = L == nlaunch - 1 ? 5 : fused_launch ? (int)part : (int)(L % per_layer) + (fsplits ? 1 : 0);
         std::vector<double> pro, rest, wg;
         for (size_t i = 0; i < t0.size(); ++i) {
             pro.push_back(t1[i] - t0[i]);
@@ -116,7 +133,7 @@ int main(int argc, char** argv) {
         }
         const double fs = *std::min_element(t0.begin(), t0.end()), le = *std::max_element(t2.begin(), t2.end());
         const double fe = *std::min_element(t2.begin(), t2.end()), ls = *std::max_element(t0.begin(), t0.end());
-        const double gap = prev_end < 0 ? 0.0 : fs - prev_end;
+        const double gap = prev_end < 0 || part == 1 ? 0.0 : fs - prev_end;
         if (L < per_layer || L == nlaunch - 1)
             std::printf("%-8s %5zu %8.2f %8.2f %6.2f %6.2f %9.2f %7.2f %7.2f %8.2f %8.2f\n", names[kind], t0.size(), fs,
                         le, le - fs, gap, median(pro), median(rest), median(wg), fe - fs, ls - fs);
@@ -125,8 +142,18 @@ int main(int argc, char** argv) {
             for (int k = 0; k < 9; ++k) sums[kind][k] += v[k];
             ++cnt[kind];
         }
-        prev_end = le;
-        last_end = le;
+        if (fused_launch && part == 0) {  // the launch ends with the later of its two parts
+            double le_all = le;
+            for (size_t b = 0; b < na; ++b) {
+                const unsigned long long* e = &h[8 * (L * 1024 + b)];
+                if (e[0]) le_all = std::max(le_all, (double)(e[2] - base) * 0.01);
+            }
+            prev_end = le_all;
+            last_end = le_all;
+        } else if (part == 0) {
+            prev_end = le;
+            last_end = le;
+        }
     }
     std::printf("\nmeans over layers 1..%u and the head (us): span, gap before, workgroup medians\n", cfg.num_layers - 1);
     std::printf("%-8s %6s %6s %9s %7s %7s %8s %8s %9s %7s\n", "kind", "span", "gap", "prologue", "rest", "wg", "1st_end",
@@ -136,7 +163,7 @@ int main(int argc, char** argv) {
         if (!cnt[k]) continue;
         double m[9];
         for (int j = 0; j < 9; ++j) m[j] = sums[k][j] / cnt[k];
-        if (k < 5) layer += m[0] + m[1];
+        if (k < 5 && !(fsplits && k == 1)) layer += m[0] + m[1];  // (fused: the attention part overlaps)
         std::printf("%-8s %6.2f %6.2f %9.2f %7.2f %7.2f %8.2f %8.2f %9.2f %7.2f\n", names[k], m[0], m[1], m[2], m[3], m[4],
                     m[5], m[6], m[7], m[8]);
     }

@@ -112,6 +112,12 @@ def make_config(model, max_seq_len: int = 0, num_layers: int = 0, attn_splits: i
     return cfg
 
 
+def set_fused_attention(enable: bool) -> None:
+    """Process-wide: steps recorded afterwards run QKV and attention as one launch per layer where
+    the plan allows it (the default), or always as two."""
+    L.load().velox_hip_set_fused_attention(1 if enable else 0)
+
+
 class HipDecodeEngine:
     def __init__(self, model, seed: int = 0, sigma: float = 0.02, norm_sigma: float = 0.0,
                  max_seq_len: int = 0, num_layers: int = 0, attn_splits: int = 0, synthesize: bool = True,
@@ -212,6 +218,14 @@ class HipDecodeEngine:
         out = np.empty((n_rows, self.vocab), np.float32)
         L.memcpy_dtoh(out.ctypes.data, self.arena.activation_arena + lo.value, out.nbytes)
         return out
+
+    def fused_status(self) -> tuple[int, int]:
+        """(attention splits per KV head of the fused QKV + attention launch, 0 when the step
+        launches the two apart; the fused launches' error bits, 0 after correct steps)."""
+        used, err = C.c_uint32(), C.c_uint32()
+        L.check(self.lib.velox_hip_fused_attention_status(C.byref(self.arena), C.byref(used), C.byref(err)),
+                "fused_attention_status")
+        return int(used.value), int(err.value)
 
     def graph_step(self) -> None:
         """One decode step driven by the device state (no host round trip)."""
