@@ -5,7 +5,9 @@
 // graph as the runner replays it. Prints, per launch kind, the launch span, the gap from the previous
 // launch's last workgroup end to this launch's first workgroup start, and workgroup medians.
 //
-//   velox_hip_timeline [--model llama3_8b] [--pos 133] [--reps 20]
+//   velox_hip_timeline [--model llama3_8b] [--pos 133] [--reps 20] [--dump FILE]
+// --dump writes every stamped workgroup of the last replay as CSV (launch, workgroup, start, staged,
+// end, mark3, mark4; us from the step's first stamp).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -38,12 +40,14 @@ int main(int argc, char** argv) {
     std::string model = "llama3_8b";
     uint32_t pos = 133;
     int reps = 20;
+    std::string dump;
     for (int i = 1; i < argc; ++i) {
         const std::string f = argv[i];
         if (i + 1 >= argc) { std::fprintf(stderr, "missing value for %s\n", f.c_str()); return 2; }
         if (f == "--model") model = argv[++i];
         else if (f == "--pos") pos = (uint32_t)std::strtoul(argv[++i], nullptr, 10);
         else if (f == "--reps") reps = std::max(1, std::atoi(argv[++i]));
+        else if (f == "--dump") dump = argv[++i];
         else { std::fprintf(stderr, "unknown flag %s\n", f.c_str()); return 2; }
     }
     VeloxHipModelConfig cfg;
@@ -99,6 +103,19 @@ int main(int argc, char** argv) {
     unsigned long long base = ~0ull;
     for (size_t i = 0; i < slots; ++i)
         if (h[8 * i]) base = std::min(base, h[8 * i]);
+    if (!dump.empty()) {
+        FILE* fd = std::fopen(dump.c_str(), "w");
+        if (!fd) return fail("--dump file");
+        std::fprintf(fd, "launch,wg,start,staged,end,mark3,mark4\n");
+        for (size_t i = 0; i < slots; ++i) {
+            const unsigned long long* e = &h[8 * i];
+            if (!e[0]) continue;
+            auto us = [&](unsigned long long t) { return t ? (double)(t - base) * 0.01 : -1.0; };
+            std::fprintf(fd, "%zu,%zu,%.2f,%.2f,%.2f,%.2f,%.2f\n", i / 1024, i % 1024, us(e[0]), us(e[1]), us(e[2]),
+                         us(e[3]), us(e[4]));
+        }
+        std::fclose(fd);
+    }
     // per kind: span, gap before, median prologue (start -> staged / first barrier), median rest,
     // median workgroup, first workgroup end, last workgroup start, attention: median loop end, merge
     double sums[6][9] = {{0}};
