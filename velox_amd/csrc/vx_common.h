@@ -323,6 +323,10 @@ struct VxF8GemmArgs {
     const uint16_t* m_part_o;
     const float* m_part_ml;
     uint32_t m_splits;
+    // x_nparts > 1 (batch 1, fp32 x, with gain): the activation row is the sum of x_nparts K-split
+    // partials x[s * x_pstride + k] (in split order), as the MLA prep kernel folded them
+    uint32_t x_nparts;
+    uint64_t x_pstride;
 };
 
 // vx_mla.hip launchers (absorbed MLA layer), used by vx_mla_host.cpp.

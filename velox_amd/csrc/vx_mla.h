@@ -63,6 +63,9 @@ hipError_t vx_launch_f8_synth_scales(float* scales, uint32_t rows, uint32_t cols
                                      hipStream_t st);
 hipError_t vx_launch_f8_pack(const VxF8Dest& d, hipStream_t st);
 hipError_t vx_launch_mla_prep(const VxMlaPrepArgs& a, uint32_t batch, hipStream_t st);
+// one sequence: W_qb's GEMV (x: the q-latent partials, with gain) and, in one more workgroup, the new
+// latent row of p (the prep kernel's latent half)
+hipError_t vx_launch_f8gemv_prep(const VxF8GemmArgs& a, const VxMlaPrepArgs& p, hipStream_t st);
 hipError_t vx_launch_mla_attn(const VxMlaAttnArgs& a, uint32_t lr, uint32_t dr, uint32_t batch, hipStream_t st);
 hipError_t vx_launch_mla_merge(const uint16_t* part_o, const float* part_ml, uint32_t nh, uint32_t splits, uint32_t lr,
                                float* ctx, uint32_t batch, uint64_t mask, hipStream_t st);

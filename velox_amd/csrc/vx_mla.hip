@@ -277,7 +277,7 @@ __device__ __forceinline__ void vm_merge_stage(const VxF8GemmArgs& a, uint32_t g
 }
 
 template <int KW, bool XF32>
-__global__ __launch_bounds__(64 * kFGWaves) void vx_f8gemv_kernel(VxF8GemmArgs a) {
+__device__ __forceinline__ void vm_f8gemv_body(const VxF8GemmArgs& a) {
     extern __shared__ __align__(16) unsigned char vm_smem[];
     if ((a.active_mask & 1ULL) == 0ULL) return;
     constexpr int TPW = kFGWaves / KW;  // row tiles per workgroup
@@ -300,15 +300,48 @@ __global__ __launch_bounds__(64 * kFGWaves) void vx_f8gemv_kernel(VxF8GemmArgs a
     // operation order of the batched RMSNorm kernel: (x * inv_rms) * gain, rounded to fp16
     uint4* xs = (uint4*)vm_smem;
     float inv = 1.0f;
+    // the activation row's 4 elements at e (fp32 x): x itself, or the sum of its K-split partials
+    const uint32_t nparts = a.x_nparts > 1u ? a.x_nparts : 1u;
+    auto x4 = [&](size_t e) {
+        const float* xb = (const float*)a.x + e;
+        float4 v = *(const float4*)xb;
+        for (uint32_t s = 1; s < nparts; ++s) {
+            const float4 w = *(const float4*)(xb + s * a.x_pstride);
+            v.x += w.x; v.y += w.y; v.z += w.z; v.w += w.w;
+        }
+        return v;
+    };
+    const uint32_t n8 = (kt1 - kt0) * 8u;
+    // one pass where the workgroup stages the whole row and a thread holds at most two 8-element units:
+    // the RMSNorm sum of squares comes from the registers the staging uses (one load round, not two)
+    constexpr uint32_t NT1 = 64u * kFGWaves;
+    const bool one_pass = XF32 && a.gain && gridDim.y == 1u && n8 <= 2u * NT1;
+    float4 xu[4];
     if constexpr (XF32) {
         if (a.gain) {
             __shared__ float red_n[kFGWaves];
             const uint32_t K = a.n_kt * 64u;
-            const float4* xr = (const float4*)((const float*)a.x + g * a.x_gstride);
             float ss = 0.0f;
-            for (uint32_t i = (uint32_t)tid; i < K / 4u; i += 64u * kFGWaves) {
-                const float4 v = xr[i];
-                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            if (one_pass) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const uint32_t i = min((uint32_t)tid + (uint32_t)u * NT1, n8 - 1u);
+                    const size_t e = g * a.x_gstride + 8u * i;
+                    xu[2 * u] = x4(e);
+                    xu[2 * u + 1] = x4(e + 4);
+                }
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+                    if ((uint32_t)tid + (uint32_t)u * NT1 < n8) {
+                        const float4 v0 = xu[2 * u], v1 = xu[2 * u + 1];
+                        ss += v0.x * v0.x + v0.y * v0.y + v0.z * v0.z + v0.w * v0.w;
+                        ss += v1.x * v1.x + v1.y * v1.y + v1.z * v1.z + v1.w * v1.w;
+                    }
+            } else {
+                for (uint32_t i = (uint32_t)tid; i < K / 4u; i += NT1) {
+                    const float4 v = x4(g * a.x_gstride + 4u * i);
+                    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                }
             }
 #pragma unroll
             for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
@@ -320,17 +353,24 @@ __global__ __launch_bounds__(64 * kFGWaves) void vx_f8gemv_kernel(VxF8GemmArgs a
             inv = 1.0f / sqrtf(t / (float)K + a.eps);
         }
     }
-    const uint32_t n8 = (kt1 - kt0) * 8u;
     if constexpr (XF32) {
         if (a.m_part_o) {
             vm_merge_stage(a, g, vm_smem);
             __syncthreads();
         }
     }
-    for (uint32_t i = (uint32_t)tid; i < n8 && !(XF32 && a.m_part_o); i += 64u * kFGWaves) {
+    for (uint32_t i = (uint32_t)tid; i < n8 && !(XF32 && a.m_part_o); i += NT1) {
         const size_t e = g * a.x_gstride + (size_t)kt0 * 64u + 8u * i;
         if constexpr (XF32) {
-            float4 lo = *(const float4*)((const float*)a.x + e), hi = *(const float4*)((const float*)a.x + e + 4);
+            float4 lo, hi;
+            if (one_pass) {
+                const bool second = i >= NT1;  // (a thread's second unit: i = tid + NT1)
+                lo = second ? xu[2] : xu[0];
+                hi = second ? xu[3] : xu[1];
+            } else {
+                lo = x4(e);
+                hi = x4(e + 4);
+            }
             if (a.gain) {
 #pragma clang fp contract(off)
                 const size_t ge = (size_t)kt0 * 64u + 8u * i;
@@ -385,6 +425,11 @@ __global__ __launch_bounds__(64 * kFGWaves) void vx_f8gemv_kernel(VxF8GemmArgs a
         float* y = a.y + o + (gridDim.y > 1u ? ks * a.pstride : 0u);
         *y = a.add_y ? *y + acc : acc;
     }
+}
+
+template <int KW, bool XF32>
+__global__ __launch_bounds__(64 * kFGWaves) void vx_f8gemv_kernel(VxF8GemmArgs a) {
+    vm_f8gemv_body<KW, XF32>(a);
 }
 
 // The same structure for 2..16 sequences on the matrix cores: the workgroup stages its split's
@@ -526,6 +571,7 @@ hipError_t vx_launch_f8gemm(const VxF8GemmArgs& a, uint32_t groups, hipStream_t 
     if ((a.y16 != nullptr) == (a.y != nullptr) || (a.y16 && a.ksplit != 1u)) return hipErrorInvalidValue;
     if (a.add_y && (a.batch != 1u || a.ksplit != 1u || a.y16)) return hipErrorInvalidValue;
     if (a.gain && (a.batch != 1u || !a.x_f32 || a.x_gstride)) return hipErrorInvalidValue;
+    if (a.x_nparts > 1u && (!a.gain || a.x_nparts > 16u || (a.x_pstride & 3u) || a.m_part_o)) return hipErrorInvalidValue;
     if (a.m_part_o && (a.batch != 1u || !a.x_f32 || a.ksplit != 1u || a.gain || !a.m_part_ml || a.m_splits == 0 ||
                        a.m_splits > 64u || a.n_kt * 64u > 64u * kFGWaves ||
                        (uint64_t)a.m_splits * a.n_kt * 128u > 64u * 1024u))
@@ -669,6 +715,62 @@ hipError_t vx_launch_f8_pack(const VxF8Dest& d, hipStream_t st) {
 // row pos (src/runtime.rs:588-601, 745-768).
 constexpr uint32_t kMlaMaxParts = 16;
 
+// The new position's latent row of sequence b: the K-split partials of outputs [q_part, na) summed,
+// latent RMSNorm (kv_norm), RoPE of the rope part, bf16 -> cache row pos (src/runtime.rs:588-601,
+// 745-768), by the NT threads of a workgroup; cs: LDS for lr + dr floats.
+template <int NT>
+__device__ __forceinline__ void vm_prep_latent(const VxMlaPrepArgs& a, uint32_t b, float* cs) {
+    __shared__ float red[NT / 64];
+    const uint32_t tid = threadIdx.x;
+    const uint64_t step = a.states[b].step;
+    const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;
+    const float* pb = a.parts + (size_t)b * a.na;
+    for (uint32_t i = a.q_part + tid; i < a.na; i += NT) {
+        float p[kMlaMaxParts];
+#pragma unroll
+        for (uint32_t s = 0; s < kMlaMaxParts; ++s) p[s] = pb[min(s, a.nparts - 1u) * a.pstride + i];
+        float v = 0.0f;
+#pragma unroll
+        for (uint32_t s = 0; s < kMlaMaxParts; ++s)
+            if (s < a.nparts) v += p[s];
+        cs[i - a.q_part] = v;
+    }
+    __syncthreads();
+    uint16_t* row = a.cache + (size_t)b * a.cache_bstride + (size_t)pos * (a.lr + a.dr);
+    float inv = 1.0f;
+    if (a.kv_norm) {
+        float ss = 0.0f;
+        for (uint32_t i = tid; i < a.lr; i += NT) ss += cs[i] * cs[i];
+        ss = vm_block_sum<NT>(ss, red);
+        inv = 1.0f / sqrtf(ss / (float)a.lr + a.eps);
+    }
+    for (uint32_t i = tid; i < a.lr; i += NT) {
+#pragma clang fp contract(off)
+        const float v = a.kv_norm ? (cs[i] * inv) * a.g_kva[i] : cs[i];
+        row[i] = vx_f32_to_bf16_bits(v);
+    }
+    const uint32_t half = a.dr / 2u;
+    for (uint32_t j = tid; j < half; j += NT) {
+        const float2 o = vm_rope_pair(cs[a.lr + j], cs[a.lr + j + half], a.rope[(size_t)pos * half + j]);
+        row[a.lr + j] = vx_f32_to_bf16_bits(o.x);
+        row[a.lr + j + half] = vx_f32_to_bf16_bits(o.y);
+    }
+}
+
+// One sequence: W_qb's GEMV (its prologue summing the q-latent partials and normalizing them) with
+// one more workgroup, the grid's last, that appends the new latent row (the prep kernel's other half,
+// off the GEMV's critical path).
+template <int KW>
+__global__ __launch_bounds__(64 * kFGWaves) void vx_f8gemv_prep_kernel(VxF8GemmArgs g, VxMlaPrepArgs p) {
+    if (blockIdx.x == gridDim.x - 1u) {
+        if ((p.active_mask & 1ULL) == 0ULL) return;
+        extern __shared__ __align__(16) unsigned char vm_smem[];
+        vm_prep_latent<64 * kFGWaves>(p, 0u, (float*)vm_smem);
+        return;
+    }
+    vm_f8gemv_body<KW, true>(g);
+}
+
 __global__ __launch_bounds__(1024) void vx_mla_prep_kernel(VxMlaPrepArgs a) {
     if ((a.active_mask & 1ULL) == 0ULL) return;
     extern __shared__ __align__(16) unsigned char vm_smem[];
@@ -677,11 +779,12 @@ __global__ __launch_bounds__(1024) void vx_mla_prep_kernel(VxMlaPrepArgs a) {
     __shared__ float red[16];
     // grid (batch, 2): workgroup y = 0 takes the q outputs, y = 1 the latent and rope outputs
     const uint32_t b = blockIdx.x, tid = threadIdx.x, part = blockIdx.y;
-    const uint64_t step = a.states[b].step;
-    const uint32_t pos = step < (uint64_t)a.s_max ? (uint32_t)step : a.s_max - 1u;
+    if (part == 1) {
+        vm_prep_latent<1024>(a, b, cs);
+        return;
+    }
     const float* pb = a.parts + (size_t)b * a.na;
-    const uint32_t i_lo = part ? a.q_part : 0u, i_hi = part ? a.na : a.q_part;
-    for (uint32_t i = i_lo + tid; i < i_hi; i += 1024u) {
+    for (uint32_t i = tid; i < a.q_part; i += 1024u) {
         float p[kMlaMaxParts];
 #pragma unroll
         for (uint32_t s = 0; s < kMlaMaxParts; ++s) p[s] = pb[min(s, a.nparts - 1u) * a.pstride + i];
@@ -689,46 +792,20 @@ __global__ __launch_bounds__(1024) void vx_mla_prep_kernel(VxMlaPrepArgs a) {
 #pragma unroll
         for (uint32_t s = 0; s < kMlaMaxParts; ++s)
             if (s < a.nparts) v += p[s];
-        if (i < a.q_part) {
-            if (a.q_lora) qs[i] = v;
-            else a.q32[(size_t)b * a.q_part + i] = v;
-        } else {
-            cs[i - a.q_part] = v;
-        }
+        if (a.q_lora) qs[i] = v;
+        else a.q32[(size_t)b * a.q_part + i] = v;
     }
     __syncthreads();
-    if (part == 0) {
-        if (a.q_lora) {
-            float ss = 0.0f;
-            for (uint32_t i = tid; i < a.q_lora; i += 1024u) ss += qs[i] * qs[i];
-            ss = vm_block_sum<1024>(ss, red);
-            const float inv = 1.0f / sqrtf(ss / (float)a.q_lora + a.eps);
-            for (uint32_t i = tid; i < a.q_lora; i += 1024u) {
-#pragma clang fp contract(off)
-                const float v = (qs[i] * inv) * a.g_qa[i];
-                a.q16[(size_t)b * a.ldq16 + i] = __half_as_ushort(__float2half(v));
-            }
-        }
-        return;
-    }
-    uint16_t* row = a.cache + (size_t)b * a.cache_bstride + (size_t)pos * (a.lr + a.dr);
-    float inv = 1.0f;
-    if (a.kv_norm) {
+    if (a.q_lora) {
         float ss = 0.0f;
-        for (uint32_t i = tid; i < a.lr; i += 1024u) ss += cs[i] * cs[i];
+        for (uint32_t i = tid; i < a.q_lora; i += 1024u) ss += qs[i] * qs[i];
         ss = vm_block_sum<1024>(ss, red);
-        inv = 1.0f / sqrtf(ss / (float)a.lr + a.eps);
-    }
-    for (uint32_t i = tid; i < a.lr; i += 1024u) {
+        const float inv = 1.0f / sqrtf(ss / (float)a.q_lora + a.eps);
+        for (uint32_t i = tid; i < a.q_lora; i += 1024u) {
 #pragma clang fp contract(off)
-        const float v = a.kv_norm ? (cs[i] * inv) * a.g_kva[i] : cs[i];
-        row[i] = vx_f32_to_bf16_bits(v);
-    }
-    const uint32_t half = a.dr / 2u;
-    for (uint32_t j = tid; j < half; j += 1024u) {
-        const float2 o = vm_rope_pair(cs[a.lr + j], cs[a.lr + j + half], a.rope[(size_t)pos * half + j]);
-        row[a.lr + j] = vx_f32_to_bf16_bits(o.x);
-        row[a.lr + j + half] = vx_f32_to_bf16_bits(o.y);
+            const float v = (qs[i] * inv) * a.g_qa[i];
+            a.q16[(size_t)b * a.ldq16 + i] = __half_as_ushort(__float2half(v));
+        }
     }
 }
 
@@ -1003,6 +1080,33 @@ __global__ __launch_bounds__(256) void vx_mla_resid_kernel(float* h, const float
     float v = h[(size_t)b * n + i];
     for (uint32_t s = 0; s < nparts; ++s) v += parts[s * pstride + (size_t)b * n + i];
     h[(size_t)b * n + i] = v;
+}
+
+// W_qb's one-sequence GEMV (x the q-latent partials, normalized in its prologue) plus the workgroup
+// that appends the new latent row (p: the prep kernel's arguments, sequence 0).
+hipError_t vx_launch_f8gemv_prep(const VxF8GemmArgs& a, const VxMlaPrepArgs& p, hipStream_t st) {
+    if (a.batch != 1u || !a.x_f32 || !a.gain || a.ksplit != 1u || a.m_part_o || !a.y || a.add_y || a.n_rt == 0 ||
+        a.n_kt == 0 || a.n_kb != (a.n_kt + 1u) / 2u || p.nparts == 0 || p.nparts > kMlaMaxParts ||
+        p.na != p.q_part + p.lr + p.dr || (p.dr & 1u) || !p.cache || !p.states)
+        return hipErrorInvalidValue;
+    if (a.x_nparts > 1u && (a.x_nparts > 16u || (a.x_pstride & 3u))) return hipErrorInvalidValue;
+    size_t lds = (size_t)a.n_kt * 128u;
+    const size_t red = (size_t)kFGWaves * 16u * 4u, lat = (size_t)(p.na - p.q_part) * 4u;
+    if (lds < red) lds = red;
+    if (lds < lat) lds = lat;
+    if (lds > 64u * 1024u) return hipErrorInvalidValue;
+    const uint32_t kts = a.n_kt;
+    auto wgs = [&](uint32_t kw) { return (a.n_rt + kFGWaves / kw - 1u) / (kFGWaves / kw); };
+    uint32_t kw = 1u;
+    while (kw < (uint32_t)kFGWaves && wgs(kw) < 256u && kts / (2u * kw) >= 2u) kw *= 2u;
+    const dim3 block(64 * kFGWaves);
+    switch (kw) {
+        case 1: hipLaunchKernelGGL(vx_f8gemv_prep_kernel<1>, dim3(wgs(1) + 1u), block, lds, st, a, p); break;
+        case 2: hipLaunchKernelGGL(vx_f8gemv_prep_kernel<2>, dim3(wgs(2) + 1u), block, lds, st, a, p); break;
+        case 4: hipLaunchKernelGGL(vx_f8gemv_prep_kernel<4>, dim3(wgs(4) + 1u), block, lds, st, a, p); break;
+        default: hipLaunchKernelGGL(vx_f8gemv_prep_kernel<8>, dim3(wgs(8) + 1u), block, lds, st, a, p); break;
+    }
+    return hipGetLastError();
 }
 
 hipError_t vx_launch_mla_prep(const VxMlaPrepArgs& a, uint32_t batch, hipStream_t st) {

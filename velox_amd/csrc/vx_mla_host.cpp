@@ -59,6 +59,9 @@ struct VeloxHipMla {
     VeloxHipMlaConfig cfg;
     uint32_t H = 0, nh = 0, ql = 0, lr = 0, dn = 0, dr = 0, dv = 0, R = 0, dq = 0, na = 0, q_part = 0;
     uint32_t s_cap = 0, splits = 1, ks_a = 1, ks_o = 1, B = 1, ldx16 = 0;
+    // one sequence: [W_qa; W_kva] over the whole K (8 waves per row tile split it), so W_qb normalizes
+    // its q latent itself and one extra W_qb workgroup writes the latent row: no prep launch
+    uint32_t ks_a1 = 1;
     float scale = 0.0f;
     std::vector<VmLayer> layers;
     uint64_t code_bytes = 0, scale_bytes = 0, norm_bytes = 0, rope_bytes = 0, cache_bytes = 0, act_bytes = 0;
@@ -271,7 +274,7 @@ int velox_hip_mla_plan(const VeloxHipMlaConfig* cfg, VeloxHipMla** out) {
     m->a_state = take(B * sizeof(VeloxDecodeState));
     m->a_h = take(B * m->H * 4);
     m->a_x16 = take(B * m->ldx16 * 2);
-    m->a_parts_a = take((uint64_t)m->ks_a * B * m->na * 4);
+    m->a_parts_a = take((uint64_t)(m->ks_a > m->ks_a1 ? m->ks_a : m->ks_a1) * B * m->na * 4);
     m->a_q32 = take(B * m->nh * m->dq * 4);
     m->a_qabs = take(B * m->nh * m->lr * 4);
     m->a_po = take(B * m->nh * splits * m->lr * 2);
@@ -492,10 +495,10 @@ void vm_layer(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, boo
     float* h = vm_act(m, m->a_h);
     uint16_t* x16 = (uint16_t*)vm_act(m, m->a_x16);
     uint16_t* cache = vm_cache(m, layer);
-    auto gemm = [&](const VmF8Plan& p, const void* x, uint32_t ldx, uint64_t x_gstride, uint32_t x_f32, float* y,
-                    uint32_t ldy, uint64_t y_gstride, uint32_t ksplit, uint64_t pstride, uint16_t* y16 = nullptr,
-                    uint32_t add_y = 0, const float* gain = nullptr, const uint16_t* m_part_o = nullptr,
-                    const float* m_part_ml = nullptr, uint32_t m_splits = 0) {
+    auto gemm_args = [&](const VmF8Plan& p, const void* x, uint32_t ldx, uint64_t x_gstride, uint32_t x_f32, float* y,
+                         uint32_t ldy, uint64_t y_gstride, uint32_t ksplit, uint64_t pstride, uint16_t* y16 = nullptr,
+                         uint32_t add_y = 0, const float* gain = nullptr, const uint16_t* m_part_o = nullptr,
+                         const float* m_part_ml = nullptr, uint32_t m_splits = 0) {
         VxF8GemmArgs g;
         std::memset(&g, 0, sizeof(g));
         g.codes = codes + p.code_off / 16;
@@ -523,7 +526,15 @@ void vm_layer(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, boo
         g.m_part_o = m_part_o;
         g.m_part_ml = m_part_ml;
         g.m_splits = m_splits;
-        vx_record_error(vx_launch_f8gemm(g, p.groups, st));
+        return g;
+    };
+    auto gemm = [&](const VmF8Plan& p, const void* x, uint32_t ldx, uint64_t x_gstride, uint32_t x_f32, float* y,
+                    uint32_t ldy, uint64_t y_gstride, uint32_t ksplit, uint64_t pstride, uint16_t* y16 = nullptr,
+                    uint32_t add_y = 0, const float* gain = nullptr, const uint16_t* m_part_o = nullptr,
+                    const float* m_part_ml = nullptr, uint32_t m_splits = 0) {
+        vx_record_error(vx_launch_f8gemm(gemm_args(p, x, ldx, x_gstride, x_f32, y, ldy, y_gstride, ksplit, pstride, y16,
+                                                   add_y, gain, m_part_o, m_part_ml, m_splits),
+                                         p.groups, st));
     };
     float* parts_o = vm_act(m, m->a_parts_o);
     const uint64_t pstride_o = (uint64_t)m->B * m->H;
@@ -532,8 +543,10 @@ void vm_layer(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, boo
     const float* g_norm = (const float*)((const uint8_t*)norms + L.norm);
     float* parts_a = vm_act(m, m->a_parts_a);
     const uint64_t pstride_a = (uint64_t)m->B * m->na;
+    // one sequence with a q LoRA: W_qb's prologue and the attention fold the partials (no prep)
+    const bool folded = direct && m->ql > 0;
     if (direct) {
-        gemm(L.a, h, m->H, 0, 1, parts_a, m->na, 0, m->ks_a, pstride_a, nullptr, 0, g_norm);
+        gemm(L.a, h, m->H, 0, 1, parts_a, m->na, 0, folded ? m->ks_a1 : m->ks_a, pstride_a, nullptr, 0, g_norm);
     } else {
         vx_record_error(vx_launch_bnorm(h, m->H, fold_prev ? parts_o : nullptr, fold_prev ? m->ks_o : 0u,
                                         fold_prev ? pstride_o : 0u, g_norm, m->H, c.rms_norm_eps, x16, m->ldx16, 32u,
@@ -566,10 +579,19 @@ void vm_layer(VeloxHipMla* m, uint32_t layer, uint32_t batch, uint64_t mask, boo
         a.ldq16 = m->ldx16;
         a.q32 = q32;
         a.active_mask = mask;
-        vx_record_error(vx_launch_mla_prep(a, batch, st));
+        if (folded) {
+            // 4. q = W_qb q_latent, normalized in W_qb's prologue; its extra workgroup appends the latent row
+            a.nparts = m->ks_a1;
+            VxF8GemmArgs g = gemm_args(L.qb, parts_a, m->ql, 0, 1, q32, m->nh * m->dq, 0, 1, 0, nullptr, 0, a.g_qa);
+            g.x_nparts = m->ks_a1;
+            g.x_pstride = pstride_a;
+            vx_record_error(vx_launch_f8gemv_prep(g, a, st));
+        } else {
+            vx_record_error(vx_launch_mla_prep(a, batch, st));
+        }
     }
     // 4. q = W_qb q_latent
-    if (m->ql) gemm(L.qb, x16, m->ldx16, 0, 0, q32, m->nh * m->dq, 0, 1, 0);
+    if (!folded && m->ql) gemm(L.qb, x16, m->ldx16, 0, 0, q32, m->nh * m->dq, 0, 1, 0);
     // 5. absorption: q_abs[h] = W_uk[h]^T q_nope[h]
     float* qabs = vm_act(m, m->a_qabs);
     gemm(L.ukt, q32, m->nh * m->dq, m->dq, 1, qabs, m->nh * m->lr, m->lr, 1, 0);
