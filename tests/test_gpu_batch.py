@@ -322,3 +322,29 @@ def test_gemm_m_rejects_bad_arguments(hiplib, oracle, dev):
     assert hiplib.velox_hip_gemm_q4_0_batch_m(C.byref(t.m), mq.codes.data_ptr(), mq.scales.data_ptr(), dx.data_ptr(),
                                               8, 32, 32 * 7, None, dy.data_ptr(), 64, None, 0, 0, L.GEMV_STORE, 1,
                                               None, None) == L.EINVAL
+
+
+@pytest.mark.parametrize("n,k,s,batch", [(96, 576, 4, 16), (100, 4096, 8, 16), (64, 4096, 16, 64), (70, 4096, 32, 128),
+                                         (40, 4096, 64, 3), (33, 29568, 0, 40)])
+def test_gemm_m_weights_enter_exactly(hiplib, oracle, dev, n, k, s, batch):
+    """One-hot activation rows: row m selects column k_m, so y[m][n] = d (q - 8) of the weight the
+    GEMM applied -- bit for bit the oracle's dequantized value (the block product is exact and the
+    scale is applied once in fp32). Pins the M-layout copy and the K order of both GEMM kernels
+    (1-16 rows, 17-128 rows) for every lanes-per-row layout of the source matrix."""
+    rng = np.random.default_rng(n + k + s)
+    blocks = _weights(oracle, n, k, 700 + s)
+    t = TiledQ4(hiplib, dev, blocks, n, k, s)
+    mq = MQ4(hiplib, dev, t)
+    deq = oracle.q4_0_dequant(blocks, k)
+    cols = rng.choice(k, size=batch, replace=batch > k)
+    edge = [0, 7, 8 * 5 + 3, k - 1]
+    cols[:min(4, batch)] = edge[:min(4, batch)]
+    x = np.zeros((batch, k), np.float16)
+    x[np.arange(batch), cols] = 1.0
+    dx = dev.put(x.view(np.int16))
+    dy = dev.put(np.zeros((batch, n), np.float32))
+    L.check(hiplib.velox_hip_gemm_q4_0_batch_m(C.byref(t.m), mq.codes.data_ptr(), mq.scales.data_ptr(), dx.data_ptr(),
+                                               batch, k, 32, None, dy.data_ptr(), n, None, 0, 0, L.GEMV_STORE, 1, None,
+                                               None))
+    got = dev.get(dy).reshape(batch, n)
+    assert np.array_equal(got, deq[:, cols].T)  # (a zero weight of a negative scale: -0 in the oracle)
