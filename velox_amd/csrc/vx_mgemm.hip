@@ -645,7 +645,7 @@ hipError_t vx_mgemm_dispatch_mt(const VxMMat& w, const VxBGemmArgs& a, hipStream
     if (a.batch <= 16) return vx_mgemm_launch_t<EPI, 1>(w, a, st);  // (the LDS-shared kernel: B=8 3857 -> 3640 tok/s)
     if (a.batch <= 32) return vx_pgemm_launch_t<EPI, 2>(w, a, st);
     if (a.batch <= 48) return vx_pgemm_launch_t<EPI, 3>(w, a, st);
-    // 33-128 rows: blocks of 4 row tiles from the grid's z dimension. At 65-128 rows each weight
+    // 49-128 rows: blocks of 4 row tiles from the grid's z dimension. At 65-128 rows each weight
     // tile is then read by two workgroups, but twice the workgroups (single K halves, two per CU)
     // run out of phase with each other, so one's loads and barrier overlap the other's MFMAs: TTFT
     // at 128 tokens 5.84-5.93 -> 5.70-5.78 ms (Llama-3-8B), 5.73-5.77 -> 5.49-5.55 ms (Qwen2.5-7B)
