@@ -28,6 +28,13 @@ sys.path.insert(0, ROOT)
 
 METRIC = "decode tok/s + achieved HBM GB/s (% of ~8 TB/s), Llama-3-8B Q4 bs=1, 1 GPU"
 HBM_PEAK_GBPS = 8000.0
+
+
+def _step_ms(rep: dict, steps: int) -> dict:
+    """Per-step device time of the timed graph replays (an event after every step): mean, median,
+    99th percentile (nearest rank) and maximum, in ms."""
+    return {"mean": round(rep["decode_ms"] / max(steps, 1), 5), "p50": round(rep["step_p50_ms"], 5),
+            "p99": round(rep["step_p99_ms"], 5), "max": round(rep["step_max_ms"], 5)}
 PROMPT_LEN = 128
 # HBM bytes per launch of the dominant kernel, measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 # and scaled by a copy kernel of known size; the file records the commands and the raw counters.
@@ -143,7 +150,8 @@ def other_configs(seed: int) -> dict:
                     "timed_positions": ([32 + warmup, 31 + warmup + steps] if cfg1 else
                                         [ctx + 1 + warmup, ctx + warmup + steps]),
                     "hbm_gbps": round(rep["hbm_gbps"], 1), "hbm_frac": round(rep["hbm_gbps"] / HBM_PEAK_GBPS, 4),
-                    "bytes_per_step": int(rep["bytes_per_step"]), "ms_per_step": round(rep["decode_ms"] / steps, 5)}
+                    "bytes_per_step": int(rep["bytes_per_step"]), "ms_per_step": round(rep["decode_ms"] / steps, 5),
+                    "step_ms": _step_ms(rep, steps)}
         print(f"[bench] {key}: {rep['tok_per_s']:.1f} tok/s, {rep['hbm_gbps']:.0f} GB/s "
               f"({time.perf_counter() - t0:.1f} s)", file=sys.stderr, flush=True)
     for key, batch in MLA_CONFIGS:
@@ -319,6 +327,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(rep["decode_ms"] / max(args.steps, 1), 5),
+        "step_ms": _step_ms(rep, args.steps),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -472,6 +472,9 @@ typedef struct VeloxHipRunReport {
     int status;
     uint32_t first_position;                /* position whose argmax is tokens[0] (the first decoded
                                                position: context_len) */
+    /* per-step device time of the timed steps (an event after every step on the step's stream):
+       median, 99th percentile (nearest rank) and maximum; the mean is decode_ms / steps */
+    double step_p50_ms, step_p99_ms, step_max_ms;
 } VeloxHipRunReport;
 
 /* Runs the whole flow; tokens (capacity max_tokens) receives, from position first_position on, the

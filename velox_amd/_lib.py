@@ -80,6 +80,7 @@ class RunReport(C.Structure):
         ("wall_ms", C.c_double), ("kernel_us", C.c_double), ("kernel_bytes", C.c_double),
         ("kernel_launches", C.c_uint32), ("n_tokens", C.c_uint32), ("first_token", C.c_uint32), ("status", C.c_int),
         ("first_position", C.c_uint32),
+        ("step_p50_ms", C.c_double), ("step_p99_ms", C.c_double), ("step_max_ms", C.c_double),
     ]
 
 

@@ -1946,11 +1946,25 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
         const int e = (int)hipStreamSynchronize(st);
         if (!rc) rc = e;
     }
+    // one timing event after every timed step, for the per-step distribution (created before the
+    // timed region; a record is one marker packet between two graph launches)
+    std::vector<hipEvent_t> step_ev;
+    if (!rc) {
+        step_ev.reserve(opt->steps);
+        for (uint32_t s = 0; s < opt->steps; ++s) {
+            hipEvent_t ev = nullptr;
+            if (hipEventCreate(&ev) != hipSuccess) break;
+            step_ev.push_back(ev);
+        }
+    }
     if (!rc) {
         // timed region: synchronized on both sides, device time from events on the same stream
         const auto w0 = std::chrono::steady_clock::now();
         hipEventRecord(e2, st);
-        for (uint32_t s = 0; s < opt->steps; ++s) one_step();
+        for (uint32_t s = 0; s < opt->steps; ++s) {
+            one_step();
+            if (s < step_ev.size()) hipEventRecord(step_ev[s], st);
+        }
         hipEventRecord(e3, st);
         rc = (int)hipStreamSynchronize(st);
         rep->wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - w0).count();
@@ -1965,6 +1979,19 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
         hipEventElapsedTime(&ms_d, e2, e3);
         rep->prefill_ms = ms_p;
         rep->decode_ms = ms_d;
+        if (!step_ev.empty() && step_ev.size() == opt->steps) {
+            std::vector<double> t(step_ev.size());
+            for (size_t s = 0; s < step_ev.size(); ++s) {
+                float ms = 0.f;
+                hipEventElapsedTime(&ms, s ? step_ev[s - 1] : e2, step_ev[s]);
+                t[s] = ms;
+            }
+            std::sort(t.begin(), t.end());
+            auto rank = [&](double q) { return t[std::min(t.size() - 1, (size_t)std::ceil(q * (double)t.size()) - 1)]; };
+            rep->step_p50_ms = rank(0.50);
+            rep->step_p99_ms = rank(0.99);
+            rep->step_max_ms = t.back();
+        }
         rep->tok_per_s = opt->steps && ms_d > 0 ? (double)B * opt->steps / (ms_d * 1e-3) : 0.0;
         double bytes = 0.0;
         const uint32_t first = base + opt->prompt_len + opt->warmup;
@@ -2026,6 +2053,7 @@ int velox_hip_run(const VeloxHipRunOptions* opt, uint32_t* tokens, uint32_t max_
     rep->status = rc;
     if (exec) hipGraphExecDestroy(exec);
     if (graph) hipGraphDestroy(graph);
+    for (hipEvent_t ev : step_ev) (void)hipEventDestroy(ev);
     hipEventDestroy(e0); hipEventDestroy(e1); hipEventDestroy(e2); hipEventDestroy(e3);
     hipStreamDestroy(st);
     velox_hip_arena_destroy(&A);
