@@ -1312,6 +1312,18 @@ int velox_hip_prefill_batch(VeloxHipArena* A, uint64_t pos0, uint32_t n_tokens, 
 // The decode step: embed -> L x [QKV(+norm), attention, o_proj+res, gate/up(+norm)+SwiGLU,
 // down+res] -> norm + LM head + argmax (+ ring + state advance). 2 + 5L launches.
 // ---------------------------------------------------------------------------------------------
+namespace {
+// Grid cap of a single-sequence GEMV: one workgroup per CU (M->head_wgs) for matrices of more than
+// 96 MB, as for the LM head, else the default 512. Qwen2-72B's gate/up (272 MB) and down (136 MB):
+// 48.3 -> 45.6 us and 31.1 -> 26.4 us per launch (kernel trace), 104.3-105.4 -> 108.2-111.2 tok/s
+// (three alternating runs each); lowering the bound to 60 MB (Llama-3-8B's and Qwen2.5-7B's gate/up)
+// lost: 773 -> 757 and 726 -> 712 tok/s.
+constexpr uint64_t kVxOneRoundBytes = 96000000ull;
+uint32_t vx_wgs_for(const VeloxHipModel* M, const VxMatPlan& p) {
+    return p.code_bytes + p.scale_bytes > kVxOneRoundBytes ? M->head_wgs : M->max_wgs;
+}
+}  // namespace
+
 void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st) {
     bool xcd_rr = false;
     const VeloxHipModel* M = vx_model(A, &xcd_rr);
@@ -1372,7 +1384,7 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
             vx_record(vx_launch_qkv_attn(vx_view(A, L.qkv), f, M->fused_p, st));
         } else {
             vx_tl_slot(g, tl_n);
-            vx_record(vx_launch_gemv(vx_view(A, L.qkv), g, VX_EPI_STORE, M->max_wgs, st));
+            vx_record(vx_launch_gemv(vx_view(A, L.qkv), g, VX_EPI_STORE, vx_wgs_for(M, L.qkv), st));
             vx_tl_slot(at, tl_n);
             vx_record(vx_launch_attention(at, c.head_dim, st));
         }
@@ -1389,7 +1401,7 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
         g.res = h;
         g.y = h;
         vx_tl_slot(g, tl_n);
-        vx_record(vx_launch_gemv(vx_view(A, L.o), g, VX_EPI_RESID, M->max_wgs, st));
+        vx_record(vx_launch_gemv(vx_view(A, L.o), g, VX_EPI_RESID, vx_wgs_for(M, L.o), st));
 
         std::memset(&g, 0, sizeof(g));
         g.active_mask = mask;
@@ -1398,7 +1410,7 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
         g.gain = vecp(L.mlp_norm);
         g.y = ffn;
         vx_tl_slot(g, tl_n);
-        vx_record(vx_launch_gemv(vx_view(A, L.gate_up), g, VX_EPI_SWIGLU, M->max_wgs, st));
+        vx_record(vx_launch_gemv(vx_view(A, L.gate_up), g, VX_EPI_SWIGLU, vx_wgs_for(M, L.gate_up), st));
 
         std::memset(&g, 0, sizeof(g));
         g.active_mask = mask;
@@ -1406,7 +1418,7 @@ void velox_hip_decode_graph_step(VeloxHipArena* A, uint64_t mask, hipStream_t st
         g.res = h;
         g.y = h;
         vx_tl_slot(g, tl_n);
-        vx_record(vx_launch_gemv(vx_view(A, L.down), g, VX_EPI_RESID, M->max_wgs, st));
+        vx_record(vx_launch_gemv(vx_view(A, L.down), g, VX_EPI_RESID, vx_wgs_for(M, L.down), st));
     }
     VxGemvArgs g;
     std::memset(&g, 0, sizeof(g));
