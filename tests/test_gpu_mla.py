@@ -98,6 +98,13 @@ def test_mla_deepseek_shape_many_splits_vs_oracle(oracle):
                  max_seq=520, norm_sigma=0.0)
 
 
+def test_mla_deepseek_shape_one_sequence_vs_oracle(oracle):
+    """Config 4's B=1 step: [W_qa; W_kva] over the whole K normalizing h itself, W_qb's GEMV normalizing
+    the q latent (its extra workgroup appending the latent row), W_uk^T, the W_uv GEMV merging the
+    attention splits, W_o adding to h -- two steps against the oracle."""
+    _check_layer(oracle, "deepseek_v3_mla", batch=1, ctxs=[100], steps=2, max_seq=160, norm_sigma=0.0)
+
+
 def test_mla_synthesized_weights_equal_loaded_codes(oracle):
     """The device quantizer and tile maps: loading the oracle's fp8 codes and block scales through the
     checkpoint entry point gives bit-identical layer outputs to the device-synthesized weights."""
