@@ -229,9 +229,9 @@ def test_caller_allocated_arena_bind(hiplib):
 
 
 def test_run_drains_the_ring_past_1024_positions(oracle):
-    """velox_hip_run over more positions than the 1024-entry ring (ADVICE: tokens were read only
-    at the end, shifted once positions wrapped): every position's token is the engine's own greedy
-    decode of the same prompt, from position 0 on."""
+    """velox_hip_run over more positions than the 1024-entry ring (a regression test: tokens read only
+    at the end of the run came out shifted once positions wrapped): every position's token is the
+    engine's own greedy decode of the same prompt, from position 0 on."""
     seed, P, steps = 29, 6, 1100
     prompt = [int(t) for t in oracle.prompt_tokens(seed, P, 49152)]
     rep, toks = run("smollm_135m", prompt=prompt, warmup=3, steps=steps, seed=seed, num_layers=1,
