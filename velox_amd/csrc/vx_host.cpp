@@ -1314,13 +1314,16 @@ int velox_hip_prefill_batch(VeloxHipArena* A, uint64_t pos0, uint32_t n_tokens, 
 // ---------------------------------------------------------------------------------------------
 namespace {
 // Grid cap of a single-sequence GEMV: one workgroup per CU (M->head_wgs) for matrices of more than
-// 96 MB, as for the LM head, else the default 512. Qwen2-72B's gate/up (272 MB) and down (136 MB):
-// 48.3 -> 45.6 us and 31.1 -> 26.4 us per launch (kernel trace), 104.3-105.4 -> 108.2-111.2 tok/s
-// (three alternating runs each); lowering the bound to 60 MB (Llama-3-8B's and Qwen2.5-7B's gate/up)
-// lost: 773 -> 757 and 726 -> 712 tok/s.
+// 96 MB, as for the LM head, and for rows of 8192 or more weights (256+ blocks: every wave tile a long
+// stream), else the default 512. Qwen2-72B's gate/up (272 MB) and down (136 MB): 48.3 -> 45.6 us and
+// 31.1 -> 26.4 us per launch (kernel trace), 104.3-105.4 -> 108.2-111.2 tok/s (three alternating runs
+// each); then its QKV and o_proj (K = 8192): 12.95 -> 12.23 and 9.77 -> 9.32 us, 107.1-110.0 ->
+// 109.9-112.8 tok/s. Lowering the size bound to 60 MB (Llama-3-8B's and Qwen2.5-7B's gate/up, K 4096
+// and 3584) lost: 773 -> 757 and 726 -> 712 tok/s. (Other grids of these models are already <= 256.)
 constexpr uint64_t kVxOneRoundBytes = 96000000ull;
+constexpr uint32_t kVxOneRoundK = 8192;
 uint32_t vx_wgs_for(const VeloxHipModel* M, const VxMatPlan& p) {
-    return p.code_bytes + p.scale_bytes > kVxOneRoundBytes ? M->head_wgs : M->max_wgs;
+    return p.code_bytes + p.scale_bytes > kVxOneRoundBytes || p.k >= kVxOneRoundK ? M->head_wgs : M->max_wgs;
 }
 }  // namespace
 
