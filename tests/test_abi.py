@@ -142,13 +142,13 @@ def test_plan_rejects_unsupported_shapes(field, value):
 
 def test_attention_split_choices():
     """The planner's split-K count over the sequence: up to 1024 positions a power of two >= 2 of
-    up to 256 positions (merged in the o_proj prologue); beyond, 256-position splits -- 8 longer ones
-    in place of 9 to 12, so that o_proj still merges them --, or 256 / KV heads longer ones when
+    up to 256 positions (merged in the o_proj prologue); beyond, 8 splits up to 3072 positions (o_proj
+    still merges them), then 256-position splits, or 256 / KV heads longer ones when
     splits x KV heads would exceed 256 workgroups (two rounds of the one-workgroup-per-CU attention
     kernel), as long as no split exceeds 512 positions."""
     lib = L.load()
     cases = [("llama3_8b", 130, 2), ("llama3_8b", 385, 2), ("llama3_8b", 512, 2), ("llama3_8b", 513, 4),
-             ("llama3_8b", 1024, 4), ("qwen2_5_7b", 2080, 8), ("qwen2_5_7b", 2304, 8),
+             ("llama3_8b", 1024, 4), ("llama3_8b", 1025, 8), ("qwen2_5_7b", 1535, 8), ("qwen2_5_7b", 2080, 8), ("qwen2_5_7b", 2304, 8),
              ("qwen2_5_7b", 3072, 8), ("qwen2_5_7b", 3073, 13), ("llama3_8b", 2048, 8), ("qwen2_72b", 8216, 32), ("qwen2_72b", 8192, 32),
              ("llama3_8b", 20000, 64)]
     for name, max_seq, want in cases:

@@ -443,7 +443,7 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
 
     // Split-K over the sequence: up to 1024 positions, a power of two (2, 4) of up to 256
     // positions whose (m, l, o) partials the o_proj GEMV merges in its prologue (no extra launch);
-    // longer contexts use 256-position splits (8 up to 3072 positions) and beyond 8 the merge
+    // longer contexts use 8 splits up to 3072 positions, then 256-position splits and the merge
     // kernel. (Llama-3-8B at 385 positions,
     // MFMA attention, measured: 1 split 702.6 tok/s, 2: 712.7, 4: 707.4, 8: 690.3.)
     uint32_t splits = c.attn_splits;
@@ -462,10 +462,10 @@ int velox_hip_model_create(const VeloxHipModelConfig* cfg, VeloxHipModel** out) 
             const uint32_t one_round = 256u / c.num_kv_heads, min_splits = (c.max_seq_len + 511) / 512;
             if (splits * c.num_kv_heads > 256u && one_round >= min_splits) splits = one_round;
             if (splits > 64) splits = 64;
-            // 9-12 splits of 256 (2049-3072 positions): 8 longer ones instead, which o_proj merges
-            // in its prologue, no merge launch (Qwen2.5-7B at 2083 positions: 722-724 -> 734-735
-            // tok/s, three alternating runs each)
-            if (splits > 8 && splits <= 12) splits = 8;
+            // 5-12 splits of 256 (1025-3072 positions): 8 instead, which o_proj merges in its
+            // prologue, no merge launch (Qwen2.5-7B, three alternating runs each: 2083 positions
+            // 722-724 -> 734-735 tok/s, 1135: 709-712 -> 745-746, 1535: 691 -> 740-741)
+            if (splits >= 5 && splits <= 12) splits = 8;
         }
     }
     M->splits = splits;
