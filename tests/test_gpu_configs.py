@@ -5,8 +5,8 @@ within the bf16 bar of 2e-2, every GPU token the exact argmax of the GPU's own l
     256 greedy steps, each sampled step recomputed by the oracle on the GPU's K/V rows;
   * config 3, Qwen2.5-7B layer shapes (QKV bias, 28/4 heads, FFN 18944), batched decode of B = 8 and
     B = 32 sequences, each over its own seeded 2048-position context (ragged by sequence);
-  * config 4, the DeepSeek-V3 MLA layer at 4096 latent positions: B = 1 (64 splits, the 32-wide
-    merge) and B = 16 (8 splits);
+  * config 4, the DeepSeek-V3 MLA layer at 4096 latent positions: B = 1 (43 splits of 96 positions,
+    the 32-wide merge) and B = 16 (8 splits);
   * config 5, the Qwen2-72B layer shape after an 8192-position context: the planner's 32 splits of
     288 positions and the separate merge kernel.
 Contexts are the device's seeded bf16 fill, copied into the oracle's caches, so both sides attend over
@@ -144,7 +144,8 @@ def test_config3_qwen_batched_2048_context_vs_oracle(oracle, batch):
 
 
 def test_config4_mla_4096_batch1_vs_oracle(oracle):
-    """B = 1 at 4096 latent positions: 64 position splits, merged 32 loads at a time."""
+    """B = 1 at 4096 latent positions: 43 position splits of 96 (the planner drops the splits its 4104
+    positions leave empty), merged 32 loads at a time."""
     _check_layer(oracle, "deepseek_v3_mla", batch=1, ctxs=[4096], steps=2, max_seq=4104, norm_sigma=0.0)
 
 
